@@ -1,0 +1,347 @@
+/*
+ * tt_oracle.c -- CPU restatement of ThinTensor's decode-path operators.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the checker for the HIP kernels: only
+ * tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it.  The
+ * product never links or calls it.
+ *
+ * Each operator restates the reference semantics (file:line cited per function)
+ * and evaluates it in binary32 in the documented reduction order of the kernels,
+ * so every output can be compared bit for bit.  Compile with -ffp-contract=off:
+ * every fused multiply-add below is an explicit fmaf().
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define TTO_F16 0
+#define TTO_BF16 1
+#define TTO_F32 2
+
+/* ------------------------------------------------------------ conversions */
+
+static float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+static uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+
+float tto_f16_to_f32(uint16_t h) {
+  uint32_t s = (uint32_t)(h >> 15) << 31, e = (h >> 10) & 31u, m = h & 1023u;
+  if (e == 0) {
+    float v = ldexpf((float)m, -24);
+    return s ? -v : v;
+  }
+  if (e == 31) return u2f(s | 0x7f800000u | (m << 13));
+  return u2f(s | ((e + 112u) << 23) | (m << 13));
+}
+
+/* round to nearest even, IEEE binary16 (subnormals, overflow to inf, NaN kept quiet) */
+uint16_t tto_f32_to_f16(float f) {
+  uint32_t x = f2u(f);
+  uint32_t sign = (x >> 16) & 0x8000u;
+  uint32_t ax = x & 0x7fffffffu;
+  if (ax > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((ax >> 13) & 0x3ffu));
+  if (ax >= 0x47800000u) {           /* >= 65536: inf (values in [65520, 65536) handled below) */
+    return (uint16_t)(sign | 0x7c00u);
+  }
+  int e = (int)(ax >> 23) - 127;
+  uint32_t m = (ax & 0x7fffffu) | 0x800000u;
+  if (ax < 0x38800000u) {            /* below 2^-14: subnormal half or zero */
+    if (ax == 0) return (uint16_t)sign;
+    int sh = -14 - e + 13;             /* shift of the 24-bit significand */
+    if (sh > 24) return (uint16_t)sign;
+    uint32_t q = m >> sh, r = m & ((1u << sh) - 1u), half = 1u << (sh - 1);
+    if (r > half || (r == half && (q & 1u))) q++;
+    return (uint16_t)(sign | q);
+  }
+  uint32_t q = m >> 13, r = m & 0x1fffu;
+  if (r > 0x1000u || (r == 0x1000u && (q & 1u))) q++;
+  uint32_t h = ((uint32_t)(e + 15) << 10) + (q - 1024u);   /* carry into exponent is fine */
+  if (h >= 0x7c00u) return (uint16_t)(sign | 0x7c00u);
+  return (uint16_t)(sign | h);
+}
+
+float tto_bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); }
+
+uint16_t tto_f32_to_bf16(float f) {
+  uint32_t u = f2u(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+float tto_round_bf16(float f) { return tto_bf16_to_f32(tto_f32_to_bf16(f)); }
+float tto_round_f16(float f) { return tto_f16_to_f32(tto_f32_to_f16(f)); }
+
+static float act_get(const void* p, int dtype, int64_t i) {
+  if (dtype == TTO_F16) return tto_f16_to_f32(((const uint16_t*)p)[i]);
+  if (dtype == TTO_BF16) return tto_bf16_to_f32(((const uint16_t*)p)[i]);
+  return ((const float*)p)[i];
+}
+
+static void act_put(void* p, int dtype, int64_t i, float v) {
+  if (dtype == TTO_F16) ((uint16_t*)p)[i] = tto_f32_to_f16(v);
+  else if (dtype == TTO_BF16) ((uint16_t*)p)[i] = tto_f32_to_bf16(v);
+  else ((float*)p)[i] = v;
+}
+
+static float round_to(int dtype, float v) {
+  if (dtype == TTO_F16) return tto_round_f16(v);
+  if (dtype == TTO_BF16) return tto_round_bf16(v);
+  return v;
+}
+
+/* 2^e as binary32 for e in [-149, 128] */
+static float pow2i(int e) {
+  if (e >= -126) return u2f((uint32_t)(e + 127) << 23);
+  return u2f(1u << (e + 149));
+}
+
+/* Device exp_f32 (tt_common.h): Cody-Waite reduction + degree-7 Taylor/Horner. */
+float tto_exp_f32(float x) {
+  if (x != x) return x;
+  if (x < -0x1.5d589ep+6f) return 0.0f;
+  if (x > 0x1.62e42ep+6f) return u2f(0x7f800000u);
+  const float log2e = 0x1.715476p+0f;
+  float n = rintf(x * log2e);
+  float r = fmaf(n, -0x1.62e4p-1f, x);
+  r = fmaf(n, -0x1.7f7d1cp-20f, r);
+  float p = 0x1.a01a02p-13f;
+  p = fmaf(p, r, 0x1.6c16c2p-10f);
+  p = fmaf(p, r, 0x1.111112p-7f);
+  p = fmaf(p, r, 0x1.555556p-5f);
+  p = fmaf(p, r, 0x1.555556p-3f);
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  int ni = (int)n;
+  int n1 = ni / 2, n2 = ni - n1;
+  p = p * u2f((uint32_t)(n1 + 127) << 23);
+  p = p * u2f((uint32_t)(n2 + 127) << 23);
+  return p;
+}
+
+/* ------------------------------------------------------------ weight formats */
+
+enum {
+  FMT_INT4_SYM = 0, FMT_INT4_AFF = 1, FMT_FP8 = 2, FMT_F16W = 3, FMT_BF16W = 4,
+  FMT_MXFP4 = 5, FMT_Q2E8 = 6, FMT_Q1E8 = 7, FMT_Q2AFF = 8, FMT_Q1AFF = 9
+};
+enum { SM_NONE = 0, SM_ROW = 1, SM_GROUP = 2, SM_GROUP_AFF = 3, SM_BLOCK_E8 = 4 };
+
+static int fmt_bytes(int fmt) {
+  switch (fmt) {
+    case FMT_INT4_SYM: case FMT_INT4_AFF: case FMT_MXFP4: return 16;
+    case FMT_FP8: return 32;
+    case FMT_F16W: case FMT_BF16W: return 64;
+    case FMT_Q2E8: case FMT_Q2AFF: return 8;
+    default: return 4;
+  }
+}
+
+/* float8_e4m3fn -> binary32, exact (reference weights are torch.float8_e4m3fn). */
+float tto_fp8e4m3_to_f32(uint8_t b) {
+  int s = b >> 7, e = (b >> 3) & 15, m = b & 7;
+  float v;
+  if (e == 15 && m == 7) return NAN;
+  if (e == 0) v = ldexpf((float)m, -9);
+  else v = ldexpf((float)(8 + m), e - 10);
+  return s ? -v : v;
+}
+
+/* e2m1 code -> value (triton_kernels.py:249-276, gpu_runtime.py:12876-12897). */
+float tto_e2m1(int code) {
+  static const float mag[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
+  float v = mag[code & 7];
+  return (code & 8) ? -v : v;
+}
+
+/* Value of element e (0..31) of one chunk as the kernel feeds it to the fma.
+ * MXFP4 values carry an extra 2^-14 that the block scale removes again. */
+static float chunk_weight(int fmt, const uint8_t* c, int e) {
+  switch (fmt) {
+    case FMT_INT4_SYM: return (float)(((c[e >> 1] >> ((e & 1) * 4)) & 15) - 8);
+    case FMT_INT4_AFF: return (float)((c[e >> 1] >> ((e & 1) * 4)) & 15);
+    case FMT_FP8: return tto_fp8e4m3_to_f32(c[e]);
+    case FMT_F16W: return tto_f16_to_f32(((const uint16_t*)c)[e]);
+    case FMT_BF16W: return tto_bf16_to_f32(((const uint16_t*)c)[e]);
+    case FMT_MXFP4: return ldexpf(tto_e2m1((c[e >> 1] >> ((e & 1) * 4)) & 15), -14);
+    case FMT_Q2E8: return (float)((c[e >> 2] >> ((e & 3) * 2)) & 3) - 1.5f;
+    case FMT_Q1E8: return ((c[e >> 3] >> (e & 7)) & 1) ? 1.0f : -1.0f;
+    case FMT_Q2AFF: return (float)((c[e >> 2] >> ((e & 3) * 2)) & 3);
+    case FMT_Q1AFF: return (float)((c[e >> 3] >> (e & 7)) & 1);
+  }
+  return 0.0f;
+}
+
+/* Butterfly over lane bits [m0, m1): v[i] <- v[i] + v[i ^ m] for m = m0, 2*m0, ... */
+static void xor_sum(float* v, int lanes, int m0, int m1) {
+  float t[64];
+  for (int m = m0; m < m1; m <<= 1) {
+    for (int i = 0; i < lanes; i++) t[i] = v[i] + v[i ^ m];
+    memcpy(v, t, sizeof(float) * (size_t)lanes);
+  }
+}
+
+static float scale_get(const void* s, int sdtype, int64_t i) {
+  if (sdtype == TTO_F16) return tto_f16_to_f32(((const uint16_t*)s)[i]);
+  if (sdtype == TTO_BF16) return tto_bf16_to_f32(((const uint16_t*)s)[i]);
+  return ((const float*)s)[i];
+}
+
+/*
+ * One output row in the kernels' reduction order (thintensor_amd/csrc/tt_gemv.h):
+ * chunks of 32, chunk j -> lane j % lpr, round j / lpr; fma chain per chunk; group
+ * butterfly and scale; sequential accumulation over rounds; final butterfly.
+ */
+float tto_gemv_row(int fmt, int smode, const uint8_t* wrow, const void* srow, int sdtype, int64_t s_grp,
+                   int64_t s_pair, int aff_zero, int e8_extra, const void* x, int xdtype, int cols, int L,
+                   int lpr) {
+  const int B = fmt_bytes(fmt);
+  const int nchunks = cols / 32;
+  const int rounds = (nchunks + lpr - 1) / lpr;
+  float A[64], p[64], xs[64];
+  for (int l = 0; l < lpr; l++) A[l] = 0.0f;
+  for (int r = 0; r < rounds; r++) {
+    for (int l = 0; l < lpr; l++) {
+      const int j = r * lpr + l;
+      p[l] = 0.0f;
+      xs[l] = 0.0f;
+      if (j < nchunks) {
+        const uint8_t* c = wrow + (int64_t)j * B;
+        float acc = 0.0f;
+        for (int e = 0; e < 32; e++) acc = fmaf(chunk_weight(fmt, c, e), act_get(x, xdtype, 32 * j + e), acc);
+        p[l] = acc;
+        if (smode == SM_GROUP_AFF) {
+          float s = 0.0f;
+          for (int e = 0; e < 32; e++) s = s + act_get(x, xdtype, 32 * j + e);
+          xs[l] = s;
+        }
+      }
+    }
+    if (smode == SM_NONE || smode == SM_ROW) {
+      for (int l = 0; l < lpr; l++) A[l] = A[l] + p[l];
+    } else if (smode == SM_BLOCK_E8) {
+      for (int l = 0; l < lpr; l++) {
+        const int j = r * lpr + l;
+        float t = 0.0f;
+        if (j < nchunks) {
+          const int e = ((const uint8_t*)srow)[j];
+          float q = p[l];
+          if (e8_extra) q = q * pow2i(e8_extra);
+          t = q * pow2i(e - 127);
+        }
+        A[l] = A[l] + t;
+      }
+    } else {
+      xor_sum(p, lpr, 1, L);
+      if (smode == SM_GROUP_AFF) xor_sum(xs, lpr, 1, L);
+      for (int l = 0; l < lpr; l++) {
+        const int j = r * lpr + l;
+        float t = 0.0f;
+        if (j < nchunks) {
+          const int g = j / L;
+          const float s = scale_get(srow, sdtype, (int64_t)g * s_grp);
+          if (smode == SM_GROUP_AFF) {
+            float m = scale_get(srow, sdtype, (int64_t)g * s_grp + s_pair);
+            if (aff_zero) m = -(m * s);
+            t = fmaf(xs[l], m, p[l] * s);
+          } else {
+            t = p[l] * s;
+          }
+        }
+        A[l] = A[l] + t;
+      }
+    }
+  }
+  if (smode == SM_GROUP || smode == SM_GROUP_AFF) xor_sum(A, lpr, L, lpr);
+  else xor_sum(A, lpr, 1, lpr);
+  float v = A[0];
+  if (smode == SM_ROW) v = v * scale_get(srow, sdtype, 0);
+  return v;
+}
+
+/*
+ * Generic GEMV over `rows` rows (optionally a selected expert and a per-slot
+ * activation row).  w points at the first row of the chosen matrix/expert.
+ */
+int tto_gemv(int fmt, int smode, const uint8_t* w, int64_t w_row_bytes, const void* s, int sdtype, int64_t s_row,
+             int64_t s_grp, int64_t s_pair, int aff_zero, int e8_extra, const void* x, int xdtype, void* out,
+             int odtype, int64_t rows, int cols, int L, int lpr) {
+  if (cols % 32 || lpr < 1 || lpr > 64) return -1;
+  for (int64_t n = 0; n < rows; n++) {
+    const void* srow = NULL;
+    if (s) {
+      const size_t es = smode == SM_BLOCK_E8 ? 1 : (sdtype == TTO_F32 ? 4 : 2);
+      srow = (const uint8_t*)s + (size_t)(n * s_row) * es;
+    }
+    const float v = tto_gemv_row(fmt, smode, w + n * w_row_bytes, srow, sdtype, s_grp, s_pair, aff_zero, e8_extra,
+                                 x, xdtype, cols, L, lpr);
+    act_put(out, odtype, n, v);
+  }
+  return 0;
+}
+
+/* ------------------------------------------------------------ fused MoE experts */
+
+static float round_rt(int rt, float v) { return round_to(rt, v); }
+
+/*
+ * Fused interleaved gate/up GEMV + gpt-oss SwiGLU for one launch
+ * (triton_kernels.py:1214-1343; MXFP4 chain gpu_runtime.py:9647-9704 + :2778-2793).
+ * fmt: FMT_Q2E8 / FMT_Q1E8 / FMT_MXFP4; rt: rounding dtype of dot results and
+ * bias sums (bf16 for q1/q2, activation dtype for MXFP4).
+ */
+int tto_swiglu(int fmt, int rt, const uint8_t* w, int64_t w_expert, int64_t w_row, const uint8_t* s,
+               int64_t s_expert, int64_t s_row, const void* x, int xdtype, int64_t x_slot, const int32_t* experts,
+               int selected, const void* bias, int bdtype, int64_t bias_expert, float alpha, float limit, void* out,
+               int odtype, int64_t out_slot, int act_rows, int cols, int lpr) {
+  const int extra = fmt == FMT_MXFP4 ? 14 : 0;
+  const size_t xes = xdtype == TTO_F32 ? 4 : 2;
+  for (int slot = 0; slot < selected; slot++) {
+    const int64_t e = experts[slot];
+    const void* xs = (const uint8_t*)x + (size_t)(slot * x_slot) * xes;
+    for (int a = 0; a < act_rows; a++) {
+      float g = tto_gemv_row(fmt, SM_BLOCK_E8, w + e * w_expert + (2 * (int64_t)a) * w_row,
+                             s + e * s_expert + (2 * (int64_t)a) * s_row, TTO_F32, 1, 0, 0, extra, xs, xdtype, cols, 1,
+                             lpr);
+      float u = tto_gemv_row(fmt, SM_BLOCK_E8, w + e * w_expert + (2 * (int64_t)a + 1) * w_row,
+                             s + e * s_expert + (2 * (int64_t)a + 1) * s_row, TTO_F32, 1, 0, 0, extra, xs, xdtype,
+                             cols, 1, lpr);
+      g = round_rt(rt, g);
+      u = round_rt(rt, u);
+      if (bias) {
+        g = round_rt(rt, g + act_get(bias, bdtype, e * bias_expert + 2 * (int64_t)a));
+        u = round_rt(rt, u + act_get(bias, bdtype, e * bias_expert + 2 * (int64_t)a + 1));
+      }
+      g = fminf(g, limit);
+      u = fmaxf(fminf(u, limit), -limit);
+      const float num = (u + 1.0f) * g;
+      const float den = 1.0f + tto_exp_f32(-g * alpha);
+      act_put(out, odtype, slot * out_slot + a, num / den);
+    }
+  }
+  return 0;
+}
+
+/* Fused down GEMV + router-weighted sum in slot order (triton_kernels.py:1347-1435). */
+int tto_weighted_down(int fmt, int rt, const uint8_t* w, int64_t w_expert, int64_t w_row, const uint8_t* s,
+                      int64_t s_expert, int64_t s_row, const void* x, int xdtype, int64_t x_slot,
+                      const int32_t* experts, const void* scores, int sdtype, int selected, const void* bias,
+                      int bdtype, int64_t bias_expert, void* out, int odtype, int rows, int cols, int lpr) {
+  const int extra = fmt == FMT_MXFP4 ? 14 : 0;
+  const size_t xes = xdtype == TTO_F32 ? 4 : 2;
+  for (int n = 0; n < rows; n++) {
+    float combined = 0.0f;
+    for (int slot = 0; slot < selected; slot++) {
+      const int64_t e = experts[slot];
+      const void* xs = (const uint8_t*)x + (size_t)(slot * x_slot) * xes;
+      float v = tto_gemv_row(fmt, SM_BLOCK_E8, w + e * w_expert + (int64_t)n * w_row, s + e * s_expert + (int64_t)n * s_row,
+                             TTO_F32, 1, 0, 0, extra, xs, xdtype, cols, 1, lpr);
+      v = round_rt(rt, v);
+      if (bias) v = round_rt(rt, v + act_get(bias, bdtype, e * bias_expert + n));
+      combined = fmaf(v, act_get(scores, sdtype, slot), combined);
+    }
+    act_put(out, odtype, n, combined);
+  }
+  return 0;
+}

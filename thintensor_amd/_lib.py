@@ -1,0 +1,106 @@
+"""ctypes binding of ``libthintensor_hip.so`` (the C ABI in include/thintensor_hip.h).
+
+The shared library is the product: every operator of :class:`HipDecodeBackend`
+lands in one of these entry points.  Loading fails loudly when the library is
+missing or was built without an entry point; there is no fallback path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from pathlib import Path
+
+from . import build as _build
+
+F16, BF16, F32 = 0, 1, 2
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_L = ctypes.c_int64
+_F = ctypes.c_float
+_PP = ctypes.POINTER(ctypes.c_void_p)
+_LP = ctypes.POINTER(ctypes.c_int64)
+
+# name -> argtypes (restype is int unless listed in _RESTYPES)
+SIGNATURES: dict[str, list] = {
+    "tt_version": [],
+    "tt_last_error": [],
+    "tt_gemv_lanes_per_row": [_L, _L],
+    "tt_int4_scaled_matvec": [_P, _L, _P, _I, _L, _L, _L, _I, _P, _I, _P, _I, _L, _L, _L, _P],
+    "tt_multi_int4_scaled_matvec": [_I, _PP, _LP, _PP, _I, _LP, _LP, _L, _I, _LP, _P, _I, _P, _I, _L, _L, _P],
+    "tt_scaled_matvec": [_P, _L, _P, _I, _P, _I, _P, _I, _L, _L, _P],
+    "tt_matvec": [_P, _I, _L, _P, _I, _P, _I, _L, _L, _P],
+    "tt_multi_matvec": [_I, _PP, _I, _LP, _LP, _P, _I, _P, _I, _L, _P],
+    "tt_mxfp4_selected_matvec": [_P, _L, _L, _P, _L, _L, _P, _I, _L, _P, _L, _P, _I, _L, _L, _L, _P],
+    "tt_mxfp_lowbit_selected_matvec": [_P, _L, _L, _P, _L, _L, _I, _P, _I, _L, _P, _L, _P, _I, _L, _L, _L, _P],
+    "tt_mxfp_lowbit_selected_swiglu": [_P, _L, _L, _P, _L, _L, _I, _P, _I, _L, _P, _L, _P, _I, _L, _F, _F, _P, _I,
+                                       _L, _L, _L, _P],
+    "tt_mxfp_lowbit_weighted_down": [_P, _L, _L, _P, _L, _L, _I, _P, _I, _L, _P, _P, _I, _L, _P, _I, _L, _P, _I, _L,
+                                     _L, _P],
+    "tt_lowbit_affine_matvec": [_P, _L, _P, _L, _L, _I, _P, _I, _P, _I, _L, _L, _L, _P],
+    "tt_int4_selected_matvec": [_P, _L, _L, _P, _I, _L, _L, _L, _P, _I, _L, _P, _L, _P, _I, _L, _L, _L, _L, _P],
+}
+_RESTYPES = {"tt_last_error": ctypes.c_char_p}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+class KernelLibraryError(RuntimeError):
+    """The HIP kernel library is missing, stale or rejected a call."""
+
+
+def library_path() -> Path:
+    override = os.environ.get("THINTENSOR_HIP_LIB")
+    return Path(override) if override else _build.LIB_PATH
+
+
+def load(build_if_missing: bool = True) -> ctypes.CDLL:
+    """Load the kernel library (building it with hipcc only if no build exists)."""
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        path = library_path()
+        if not path.exists():
+            if not build_if_missing:
+                raise KernelLibraryError(f"HIP kernel library not built: {path}")
+            _build.build()
+        lib = ctypes.CDLL(str(path))
+        missing = []
+        for name, argtypes in SIGNATURES.items():
+            try:
+                fn = getattr(lib, name)
+            except AttributeError:
+                missing.append(name)
+                continue
+            fn.argtypes = argtypes
+            fn.restype = _RESTYPES.get(name, ctypes.c_int)
+        if missing:
+            raise KernelLibraryError(f"{path} lacks entry points {missing}; rebuild with thintensor_amd.build")
+        _lib = lib
+        return lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = load().tt_last_error().decode(errors="replace")
+        if rc == -1:
+            raise ValueError(f"{what}: {msg}")
+        raise KernelLibraryError(f"{what} failed ({rc}): {msg}")
+
+
+def ptr_array(values) -> ctypes.Array:
+    arr = (ctypes.c_void_p * len(values))()
+    for i, v in enumerate(values):
+        arr[i] = v
+    return arr
+
+
+def i64_array(values) -> ctypes.Array:
+    arr = (ctypes.c_int64 * len(values))()
+    for i, v in enumerate(values):
+        arr[i] = int(v)
+    return arr

@@ -1,0 +1,515 @@
+"""HipDecodeBackend: the MI355X drop-in for the reference's ``TritonDecodeBackend``.
+
+Method names, positional/keyword arguments, return values, shape contracts and
+their ``ValueError`` messages follow ``TritonDecodeBackend``
+(thinruntime/triton_kernels.py:3553-5893) so the reference runtime can construct
+this object where it constructs the Triton backend (gpu_runtime.py:5441-5457).
+Every operator is destination-passing, launches on torch's current stream through
+the C ABI of ``libthintensor_hip.so`` and never synchronises the host.
+
+Launch-tuning keywords of the Triton backend (``block_m``, ``num_warps``,
+``block_k``, ``config_name``) are accepted for signature compatibility and
+ignored: the HIP kernels choose their own launch shape, and their reduction order
+depends only on the tensor shapes.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Any
+
+import torch
+
+from . import _lib
+
+_DTYPE_CODE = {torch.float16: _lib.F16, torch.bfloat16: _lib.BF16, torch.float32: _lib.F32}
+
+
+def _code(t: torch.Tensor, what: str) -> int:
+    try:
+        return _DTYPE_CODE[t.dtype]
+    except KeyError:
+        raise ValueError(f"{what}: unsupported dtype {t.dtype}") from None
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _require_cuda(*tensors: torch.Tensor) -> None:
+    for t in tensors:
+        if t is not None and t.device.type != "cuda":
+            raise ValueError("HipDecodeBackend operates on device tensors only")
+
+
+@dataclass
+class DecodeBuffers:
+    """Persistent activation vectors, as ``TritonDecodeBuffers`` (triton_kernels.py:3516-3529)."""
+
+    hidden_a: torch.Tensor
+    hidden_b: torch.Tensor
+    normed: torch.Tensor
+    qkv: torch.Tensor
+    q_norm: torch.Tensor
+    k_norm: torch.Tensor
+    attn: torch.Tensor
+    attn_out: torch.Tensor
+    gate_up: torch.Tensor
+    mlp_act: torch.Tensor
+    mlp: torch.Tensor
+    final: torch.Tensor
+
+
+class HipDecodeBackend:
+    """HIP/gfx950 implementation of the decode operator set."""
+
+    def __init__(
+        self,
+        device: torch.device,
+        dtype: torch.dtype,
+        hidden_size: int,
+        q_dim: int,
+        kv_dim: int,
+        intermediate_size: int,
+        argmax_mode: str = "torch",
+    ) -> None:
+        self.lib = _lib.load()
+        self.device = torch.device(device)
+        self.dtype = dtype
+        self.hidden_size = hidden_size
+        self.q_dim = q_dim
+        self.kv_dim = kv_dim
+        self.intermediate_size = intermediate_size
+        self.argmax_mode = argmax_mode
+        empty = lambda n: torch.empty(n, device=self.device, dtype=dtype)  # noqa: E731
+        self.buffers = DecodeBuffers(
+            hidden_a=empty(hidden_size),
+            hidden_b=empty(hidden_size),
+            normed=empty(hidden_size),
+            qkv=empty(q_dim + 2 * kv_dim),
+            q_norm=empty(q_dim),
+            k_norm=empty(kv_dim),
+            attn=empty(q_dim),
+            attn_out=empty(hidden_size),
+            gate_up=empty(2 * intermediate_size),
+            mlp_act=empty(intermediate_size),
+            mlp=empty(hidden_size),
+            final=empty(hidden_size),
+        )
+        self._logits_buffer: torch.Tensor | None = None
+        # The argmax result is a reused buffer: later calls overwrite it
+        # (same ownership as triton_kernels.py:3595).
+        self._argmax_out_idx = torch.empty((), device=self.device, dtype=torch.int64)
+        self._argmax_out_val = torch.empty((), device=self.device, dtype=torch.float32)
+        self._argmax_partials: torch.Tensor | None = None
+        self._attention_partials: torch.Tensor | None = None
+
+    # ------------------------------------------------------------ helpers
+    @staticmethod
+    def _layout_key(tensor: torch.Tensor) -> tuple[Any, ...]:
+        return (str(tensor.device), str(tensor.dtype), tuple(tensor.shape), tuple(tensor.stride()))
+
+    def logits_buffer(self, rows: int, dtype: torch.dtype) -> torch.Tensor:
+        if self._logits_buffer is None or self._logits_buffer.numel() != rows or self._logits_buffer.dtype != dtype:
+            self._logits_buffer = torch.empty(rows, device=self.device, dtype=dtype)
+        return self._logits_buffer
+
+    # ------------------------------------------------------------ dense GEMV
+    def matvec(
+        self,
+        weight: torch.Tensor,
+        x: torch.Tensor,
+        out: torch.Tensor,
+        *,
+        block_m: int | None = None,
+        num_warps: int | None = None,
+        config_name: str | None = None,
+    ) -> torch.Tensor:
+        """out = weight @ x for fp16/bf16 weight [rows, cols] (triton_kernels.py:3701-3771)."""
+        _require_cuda(weight, x, out)
+        rows, cols = int(weight.shape[0]), int(weight.shape[1])
+        if weight.stride(1) != 1 or x.numel() != cols or out.numel() != rows or not out.is_contiguous():
+            raise ValueError(f"matvec shape mismatch: weight {tuple(weight.shape)}, x {tuple(x.shape)}, out {tuple(out.shape)}")
+        rc = self.lib.tt_matvec(
+            weight.data_ptr(), _code(weight, "matvec"), weight.stride(0), x.data_ptr(), _code(x, "matvec"),
+            out.data_ptr(), _code(out, "matvec"), rows, cols, _stream(out),
+        )
+        _lib.check(rc, "matvec")
+        return out
+
+    def multi_matvec(
+        self,
+        weights: tuple[torch.Tensor, ...],
+        x: torch.Tensor,
+        out: torch.Tensor,
+        *,
+        block_m: int = 8,
+        num_warps: int = 8,
+    ) -> torch.Tensor:
+        """Two to four dense matrices sharing x, concatenated output (triton_kernels.py:4978-5064)."""
+        if len(weights) == 4:
+            first = sum(int(w.shape[0]) for w in weights[:2])
+            self.multi_matvec(weights[:2], x, out[:first])
+            self.multi_matvec(weights[2:], x, out[first:])
+            return out
+        if len(weights) not in {2, 3}:
+            raise ValueError("multi_matvec supports two, three, or four matrices")
+        cols = int(weights[0].shape[1])
+        if any(int(w.shape[1]) != cols for w in weights):
+            raise ValueError("multi_matvec matrices must have the same column count")
+        _require_cuda(x, out, *weights)
+        wdt = _code(weights[0], "multi_matvec")
+        if any(_code(w, "multi_matvec") != wdt or w.stride(1) != 1 for w in weights):
+            raise ValueError("multi_matvec matrices must share a dtype and be row-major")
+        rows = [int(w.shape[0]) for w in weights]
+        if out.numel() != sum(rows) or x.numel() != cols:
+            raise ValueError("multi_matvec output/input size mismatch")
+        rc = self.lib.tt_multi_matvec(
+            len(weights), _lib.ptr_array([w.data_ptr() for w in weights]), wdt,
+            _lib.i64_array([w.stride(0) for w in weights]), _lib.i64_array(rows), x.data_ptr(), _code(x, "multi_matvec"),
+            out.data_ptr(), _code(out, "multi_matvec"), cols, _stream(out),
+        )
+        _lib.check(rc, "multi_matvec")
+        return out
+
+    # ------------------------------------------------------------ int4
+    def int4_scaled_matvec(
+        self,
+        packed_weight: torch.Tensor,
+        scales: torch.Tensor,
+        x: torch.Tensor,
+        out: torch.Tensor,
+        *,
+        rows: int,
+        cols: int,
+        group_size: int,
+    ) -> torch.Tensor:
+        """Group-scaled int4 GEMV (triton_kernels.py:4597-4743).
+
+        packed_weight: uint8 [rows, cols/2] (or its int32/uint32 view [rows, cols/8]);
+        scales: fp16/fp32 [rows, groups] (symmetric) or [rows, groups, 2] (affine s, m).
+        """
+        _require_cuda(packed_weight, scales, x, out)
+        row_bytes = packed_weight.stride(0) * packed_weight.element_size()
+        if int(packed_weight.shape[0]) != rows or packed_weight.shape[1] * packed_weight.element_size() * 2 != cols:
+            raise ValueError(f"int4 packed weight {tuple(packed_weight.shape)} does not match rows={rows} cols={cols}")
+        if x.numel() != cols or out.numel() != rows:
+            raise ValueError("int4_scaled_matvec input/output size mismatch")
+        affine = scales.ndim == 3
+        s_row = scales.stride(0)
+        s_group = scales.stride(1) if scales.ndim >= 2 else 0
+        s_pair = scales.stride(2) if affine else 0
+        rc = self.lib.tt_int4_scaled_matvec(
+            packed_weight.data_ptr(), row_bytes, scales.data_ptr(), _code(scales, "int4 scales"), s_row, s_group,
+            s_pair, int(affine), x.data_ptr(), _code(x, "int4_scaled_matvec"), out.data_ptr(),
+            _code(out, "int4_scaled_matvec"), rows, cols, group_size, _stream(out),
+        )
+        _lib.check(rc, "int4_scaled_matvec")
+        return out
+
+    def multi_int4_scaled_matvec(
+        self,
+        weights: tuple[torch.Tensor, ...],
+        scales: tuple[torch.Tensor, ...],
+        rows: tuple[int, ...],
+        cols: int,
+        x: torch.Tensor,
+        out: torch.Tensor,
+        *,
+        group_size: int | None = None,
+    ) -> torch.Tensor:
+        """Two or three int4 matrices in one launch (triton_kernels.py:5066-5117).
+
+        The reference only uses this for one scale per row; here any group size the
+        single-matrix op accepts works (``group_size`` defaults to one scale per row).
+        """
+        if len(weights) not in {2, 3} or len(scales) != len(weights):
+            raise ValueError("multi INT4 matvec supports two or three matrices")
+        _require_cuda(x, out, *weights, *scales)
+        group = cols if group_size is None else group_size
+        sdt = _code(scales[0], "int4 scales")
+        affine = scales[0].ndim == 3
+        if out.numel() != sum(rows) or x.numel() != cols:
+            raise ValueError("multi INT4 matvec output/input size mismatch")
+        rc = self.lib.tt_multi_int4_scaled_matvec(
+            len(weights), _lib.ptr_array([w.data_ptr() for w in weights]),
+            _lib.i64_array([w.stride(0) * w.element_size() for w in weights]),
+            _lib.ptr_array([s.data_ptr() for s in scales]), sdt, _lib.i64_array([s.stride(0) for s in scales]),
+            _lib.i64_array([s.stride(1) if s.ndim >= 2 else 0 for s in scales]),
+            scales[0].stride(2) if affine else 0, int(affine), _lib.i64_array(rows), x.data_ptr(),
+            _code(x, "multi_int4_scaled_matvec"), out.data_ptr(), _code(out, "multi_int4_scaled_matvec"), cols, group,
+            _stream(out),
+        )
+        _lib.check(rc, "multi_int4_scaled_matvec")
+        return out
+
+    def int4_selected_matvec(
+        self,
+        packed_weight: torch.Tensor,
+        scales: torch.Tensor,
+        x: torch.Tensor,
+        expert_indices: torch.Tensor,
+        out: torch.Tensor,
+        *,
+        group_size: int,
+        block_m: int = 8,
+        num_warps: int = 8,
+    ) -> torch.Tensor:
+        """Selected-expert int4 GEMV (triton_kernels.py:4745-4805)."""
+        if packed_weight.ndim != 3 or scales.ndim != 3:
+            raise ValueError("selected INT4 expert weights/scales must both be rank 3")
+        experts, rows, packed_cols = map(int, packed_weight.shape)
+        if int(scales.shape[0]) != experts or int(scales.shape[1]) != rows:
+            raise ValueError("selected INT4 expert scale shape mismatch")
+        cols = packed_cols * 2
+        selected = int(expert_indices.numel())
+        stride_xe = self._selected_x_stride(x, selected, cols, "selected INT4")
+        if tuple(out.shape) != (selected, rows):
+            raise ValueError(f"selected INT4 output must be {(selected, rows)}, got {tuple(out.shape)}")
+        self._check_indices(expert_indices)
+        _require_cuda(packed_weight, scales, x, out)
+        rc = self.lib.tt_int4_selected_matvec(
+            packed_weight.data_ptr(), packed_weight.stride(0), packed_weight.stride(1), scales.data_ptr(),
+            _code(scales, "int4 scales"), scales.stride(0), scales.stride(1), scales.stride(2), x.data_ptr(),
+            _code(x, "int4_selected_matvec"), stride_xe, expert_indices.data_ptr(), selected, out.data_ptr(),
+            _code(out, "int4_selected_matvec"), out.stride(0), rows, cols, group_size, _stream(out),
+        )
+        _lib.check(rc, "int4_selected_matvec")
+        return out
+
+    # ------------------------------------------------------------ fp8
+    def scaled_matvec(
+        self,
+        weight: torch.Tensor,
+        scales: torch.Tensor,
+        x: torch.Tensor,
+        out: torch.Tensor,
+        config_name: str | None = None,
+        *,
+        block_m: int | None = None,
+        num_warps: int | None = None,
+    ) -> torch.Tensor:
+        """y = (W_fp8 @ x) * s_row (triton_kernels.py:4452-4595, per-row scales)."""
+        _require_cuda(weight, scales, x, out)
+        if weight.dtype != torch.float8_e4m3fn:
+            raise ValueError(f"scaled_matvec supports float8_e4m3fn weights on this backend, got {weight.dtype}")
+        if scales.dim() != 1:
+            raise ValueError("scaled_matvec: block-scaled (2-D) scales are not supported by the HIP backend")
+        rows, cols = int(weight.shape[0]), int(weight.shape[1])
+        if scales.numel() != rows or x.numel() != cols or out.numel() != rows or weight.stride(1) != 1:
+            raise ValueError("scaled_matvec shape mismatch")
+        rc = self.lib.tt_scaled_matvec(
+            weight.data_ptr(), weight.stride(0), scales.data_ptr(), _code(scales, "fp8 scales"), x.data_ptr(),
+            _code(x, "scaled_matvec"), out.data_ptr(), _code(out, "scaled_matvec"), rows, cols, _stream(out),
+        )
+        _lib.check(rc, "scaled_matvec")
+        return out
+
+    # ------------------------------------------------------------ MoE experts
+    @staticmethod
+    def _selected_x_stride(x: torch.Tensor, selected: int, cols: int, what: str) -> int:
+        if x.ndim == 1:
+            if int(x.numel()) != cols:
+                raise ValueError(f"{what} vector has {x.numel()} values, expected {cols}")
+            return 0
+        if x.ndim == 2 and tuple(x.shape) == (selected, cols) and x.stride(1) == 1:
+            return int(x.stride(0))
+        raise ValueError(f"{what} input must be {(cols,)} or {(selected, cols)}, got {tuple(x.shape)}")
+
+    @staticmethod
+    def _check_indices(expert_indices: torch.Tensor) -> None:
+        if expert_indices.dtype != torch.int32 or not expert_indices.is_contiguous():
+            raise ValueError("expert_indices must be a contiguous int32 device tensor")
+
+    def mxfp4_selected_matvec(
+        self,
+        blocks: torch.Tensor,
+        scales: torch.Tensor,
+        x: torch.Tensor,
+        expert_indices: torch.Tensor,
+        out: torch.Tensor,
+        *,
+        block_m: int = 4,
+        num_warps: int = 8,
+    ) -> torch.Tensor:
+        """MXFP4 selected-expert GEMV (triton_kernels.py:3847-3911)."""
+        if blocks.ndim != 4 or scales.ndim != 3:
+            raise ValueError("MXFP4 expert blocks/scales must be rank 4/rank 3")
+        if blocks.shape[:-1] != scales.shape:
+            raise ValueError(f"MXFP4 blocks/scales mismatch: {blocks.shape} vs {scales.shape}")
+        rows = int(blocks.shape[1])
+        cols = int(blocks.shape[2] * blocks.shape[3] * 2)
+        selected = int(expert_indices.numel())
+        stride_xe = self._selected_x_stride(x, selected, cols, "MXFP4")
+        if tuple(out.shape) != (selected, rows):
+            raise ValueError(f"MXFP4 output must be {(selected, rows)}, got {tuple(out.shape)}")
+        if blocks.stride(3) != 1 or blocks.stride(2) != blocks.shape[3] or scales.stride(2) != 1:
+            raise ValueError("MXFP4 blocks/scales must be contiguous within a row")
+        self._check_indices(expert_indices)
+        _require_cuda(blocks, scales, x, out)
+        rc = self.lib.tt_mxfp4_selected_matvec(
+            blocks.data_ptr(), blocks.stride(0), blocks.stride(1), scales.data_ptr(), scales.stride(0),
+            scales.stride(1), x.data_ptr(), _code(x, "mxfp4_selected_matvec"), stride_xe, expert_indices.data_ptr(),
+            selected, out.data_ptr(), _code(out, "mxfp4_selected_matvec"), out.stride(0), rows, cols, _stream(out),
+        )
+        _lib.check(rc, "mxfp4_selected_matvec")
+        return out
+
+    # The reference's Blackwell tensor-core variant computes the same sum
+    # (triton_kernels.py:865-930, 3913-3976); on gfx950 it is the same kernel.
+    mxfp4_selected_tensorcore_matvec = mxfp4_selected_matvec
+
+    def mxfp_lowbit_selected_matvec(
+        self,
+        packed_weight: torch.Tensor,
+        scales: torch.Tensor,
+        x: torch.Tensor,
+        expert_indices: torch.Tensor,
+        out: torch.Tensor,
+        *,
+        bits: int,
+        block_m: int = 0,
+        block_k: int = 0,
+    ) -> torch.Tensor:
+        """Q1/Q2 E8M0 selected-expert GEMV (triton_kernels.py:4132-4176)."""
+        if bits not in {1, 2} or packed_weight.ndim != 4 or scales.ndim != 3:
+            raise ValueError("low-bit expert weights must be packed Q1 or Q2")
+        rows = int(packed_weight.shape[1])
+        cols = int(scales.shape[2] * 32)
+        selected = int(expert_indices.numel())
+        stride_xe = self._selected_x_stride(x, selected, cols, "low-bit expert")
+        if tuple(out.shape) != (selected, rows):
+            raise ValueError(f"low-bit output must be {(selected, rows)}, got {tuple(out.shape)}")
+        self._check_indices(expert_indices)
+        _require_cuda(packed_weight, scales, x, out)
+        rc = self.lib.tt_mxfp_lowbit_selected_matvec(
+            packed_weight.data_ptr(), packed_weight.stride(0), packed_weight.stride(1), scales.data_ptr(),
+            scales.stride(0), scales.stride(1), bits, x.data_ptr(), _code(x, "mxfp_lowbit_selected_matvec"), stride_xe,
+            expert_indices.data_ptr(), selected, out.data_ptr(), _code(out, "mxfp_lowbit_selected_matvec"),
+            out.stride(0), rows, cols, _stream(out),
+        )
+        _lib.check(rc, "mxfp_lowbit_selected_matvec")
+        return out
+
+    def mxfp_lowbit_selected_tensorcore_matvec(
+        self,
+        packed_weight: torch.Tensor,
+        scales: torch.Tensor,
+        x: torch.Tensor,
+        expert_indices: torch.Tensor,
+        out: torch.Tensor,
+        *,
+        bits: int,
+        **_: Any,
+    ) -> torch.Tensor:
+        """Same sum as the scalar variant (triton_kernels.py:3978-4055)."""
+        return self.mxfp_lowbit_selected_matvec(packed_weight, scales, x, expert_indices, out, bits=bits)
+
+    def mxfp_lowbit_selected_swiglu(
+        self,
+        packed_weight: torch.Tensor,
+        scales: torch.Tensor,
+        x: torch.Tensor,
+        expert_indices: torch.Tensor,
+        out: torch.Tensor,
+        *,
+        bits: int,
+        alpha: float,
+        limit: float,
+        bias: torch.Tensor | None = None,
+        block_m: int = 4,
+        block_k: int = 0,
+        num_warps: int = 8,
+    ) -> torch.Tensor:
+        """Fused interleaved gate/up GEMV + gpt-oss SwiGLU (triton_kernels.py:4178-4235).
+
+        ``bits`` 1/2 are the reference's E8M0 low-bit experts (bf16 rounding);
+        ``bits=4`` runs MXFP4 ``blocks`` with rounding in the activation dtype, which
+        reproduces the reference's unfused MXFP4 chain (gpu_runtime.py:9647-9704).
+        """
+        if bits not in {1, 2, 4} or packed_weight.ndim != 4 or scales.ndim != 3:
+            raise ValueError("fused SwiGLU requires packed Q1 or Q2 experts")
+        physical_rows = int(packed_weight.shape[1])
+        if physical_rows % 2:
+            raise ValueError("interleaved gate/up rows must be even")
+        activation_rows = physical_rows // 2
+        cols = int(scales.shape[2] * 32)
+        selected = int(expert_indices.numel())
+        if tuple(out.shape) != (selected, activation_rows):
+            raise ValueError("fused SwiGLU output shape mismatch")
+        stride_xe = self._selected_x_stride(x, selected, cols, "fused SwiGLU")
+        self._check_indices(expert_indices)
+        _require_cuda(packed_weight, scales, x, out)
+        rc = self.lib.tt_mxfp_lowbit_selected_swiglu(
+            packed_weight.data_ptr(), packed_weight.stride(0), packed_weight.stride(1), scales.data_ptr(),
+            scales.stride(0), scales.stride(1), bits, x.data_ptr(), _code(x, "swiglu"), stride_xe,
+            expert_indices.data_ptr(), selected, bias.data_ptr() if bias is not None else None,
+            _code(bias, "bias") if bias is not None else _lib.F32, bias.stride(0) if bias is not None else 0,
+            float(alpha), float(limit), out.data_ptr(), _code(out, "swiglu"), out.stride(0), activation_rows, cols,
+            _stream(out),
+        )
+        _lib.check(rc, "mxfp_lowbit_selected_swiglu")
+        return out
+
+    def mxfp_lowbit_weighted_down(
+        self,
+        packed_weight: torch.Tensor,
+        scales: torch.Tensor,
+        x: torch.Tensor,
+        expert_indices: torch.Tensor,
+        router_scores: torch.Tensor,
+        out: torch.Tensor,
+        *,
+        bits: int,
+        bias: torch.Tensor | None = None,
+        block_m: int = 4,
+        block_k: int = 0,
+        num_warps: int = 8,
+    ) -> torch.Tensor:
+        """Fused down GEMV + router-weighted expert sum (triton_kernels.py:4237-4285)."""
+        if bits not in {1, 2, 4} or packed_weight.ndim != 4 or scales.ndim != 3:
+            raise ValueError("fused down requires packed Q1 or Q2 experts")
+        rows = int(packed_weight.shape[1])
+        cols = int(scales.shape[2] * 32)
+        selected = int(expert_indices.numel())
+        if tuple(x.shape) != (selected, cols) or int(out.numel()) != rows:
+            raise ValueError("fused weighted-down tensor shape mismatch")
+        self._check_indices(expert_indices)
+        _require_cuda(packed_weight, scales, x, out, router_scores)
+        rc = self.lib.tt_mxfp_lowbit_weighted_down(
+            packed_weight.data_ptr(), packed_weight.stride(0), packed_weight.stride(1), scales.data_ptr(),
+            scales.stride(0), scales.stride(1), bits, x.data_ptr(), _code(x, "weighted_down"), x.stride(0),
+            expert_indices.data_ptr(), router_scores.data_ptr(), _code(router_scores, "router scores"), selected,
+            bias.data_ptr() if bias is not None else None, _code(bias, "bias") if bias is not None else _lib.F32,
+            bias.stride(0) if bias is not None else 0, out.data_ptr(), _code(out, "weighted_down"), rows, cols,
+            _stream(out),
+        )
+        _lib.check(rc, "mxfp_lowbit_weighted_down")
+        return out
+
+    # ------------------------------------------------------------ affine low-bit (no reference kernel)
+    def lowbit_affine_matvec(
+        self,
+        packed_weight: torch.Tensor,
+        scale_zero: torch.Tensor,
+        x: torch.Tensor,
+        out: torch.Tensor,
+        *,
+        bits: int,
+        rows: int,
+        cols: int,
+        group_size: int,
+    ) -> torch.Tensor:
+        """w = (c - z) * s with fp16 (s, z) [rows, cols/group, 2]; q2 or q1 codes packed per row."""
+        _require_cuda(packed_weight, scale_zero, x, out)
+        if scale_zero.ndim != 3 or scale_zero.shape[-1] != 2 or scale_zero.dtype != torch.float16:
+            raise ValueError("affine low-bit scale/zero must be fp16 [rows, groups, 2]")
+        if x.numel() != cols or out.numel() != rows:
+            raise ValueError("lowbit_affine_matvec input/output size mismatch")
+        rc = self.lib.tt_lowbit_affine_matvec(
+            packed_weight.data_ptr(), packed_weight.stride(0) * packed_weight.element_size(), scale_zero.data_ptr(),
+            scale_zero.stride(0), scale_zero.stride(1), bits, x.data_ptr(), _code(x, "lowbit_affine_matvec"),
+            out.data_ptr(), _code(out, "lowbit_affine_matvec"), rows, cols, group_size, _stream(out),
+        )
+        _lib.check(rc, "lowbit_affine_matvec")
+        return out

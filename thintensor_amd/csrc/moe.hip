@@ -1,0 +1,319 @@
+// Fused MoE expert kernels: gate/up GEMV + gpt-oss SwiGLU on interleaved rows and
+// down GEMV + router-weighted sum, for E8M0 block-scaled formats (q1, q2, MXFP4).
+// Expert ids and router scores are read on the device (no host synchronisation).
+//
+// RT is the precision the reference rounds the GEMV results and bias sums through:
+// bfloat16 for the reference's fused low-bit kernels (triton_kernels.py:1319-1333,
+// 1421-1434), the activation dtype for the MXFP4 chain that the reference runs as
+// separate kernels plus torch adds (gpu_runtime.py:9647-9704, 9855-9903).
+#include "tt_abi_internal.h"
+#include "tt_gemv.h"
+
+#include <type_traits>
+
+namespace tt {
+
+struct SwigluParams {
+  const uint8_t* w; int64_t w_expert, w_row;
+  const uint8_t* s; int64_t s_expert, s_row;
+  const void* x; int64_t x_slot;
+  const int32_t* experts;
+  const void* bias; int64_t bias_expert;
+  float alpha, limit;
+  void* out; int64_t out_slot;
+  int act_rows, cols, e8_extra;
+};
+
+template <typename BT> __device__ __forceinline__ float ld_bias(const void* b, int64_t i) {
+  return to_f32(reinterpret_cast<const BT*>(b)[i]);
+}
+
+// gate/up rows 2a and 2a+1 of the selected expert; APW activation rows per wave pass.
+template <Fmt F, typename XT, typename OT, typename RT, typename BT, int LPR, int APW>
+__global__ __launch_bounds__(256) void swiglu_kernel(SwigluParams P) {
+  extern __shared__ uint32_t xs_lds[];
+  constexpr int SUBS = 64 / LPR;
+  const int slot = blockIdx.y;
+  {
+    const uint32_t* xg = reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(P.x) + (int64_t)slot * P.x_slot);
+    for (int i = threadIdx.x; i < (P.cols >> 1); i += blockDim.x) xs_lds[i] = xg[i];
+  }
+  __syncthreads();
+  const int64_t e = P.experts[slot];
+  const uint8_t* wexp = P.w + e * P.w_expert;
+  const uint8_t* sexp = P.s + e * P.s_expert;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int sub = lane / LPR, l = lane % LPR;
+  const int nchunks = P.cols >> 5;
+  const int per_iter = APW * SUBS;
+  const int waves_total = gridDim.x * (blockDim.x >> 6);
+  for (int base = (blockIdx.x * (blockDim.x >> 6) + wave) * per_iter; base < P.act_rows; base += waves_total * per_iter) {
+    const uint8_t* wrow[2 * APW];
+    const uint8_t* srow[2 * APW];
+    bool rv[2 * APW];
+    int act[APW];
+#pragma unroll
+    for (int i = 0; i < APW; i++) {
+      act[i] = base + i * SUBS + sub;
+      const bool v = act[i] < P.act_rows;
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        const int64_t row = 2 * (int64_t)act[i] + h;
+        rv[2 * i + h] = v;
+        wrow[2 * i + h] = wexp + row * P.w_row;
+        srow[2 * i + h] = sexp + row * P.s_row;
+      }
+    }
+    float dot[2 * APW];
+    e8_rows_dot<F, XT, LPR, 2 * APW>(wrow, srow, rv, xs_lds, nchunks, l, P.e8_extra, dot);
+#pragma unroll
+    for (int i = 0; i < APW; i++) {
+      if (!rv[2 * i] || l != i) continue;
+      float g = round_to<RT>(dot[2 * i]);
+      float u = round_to<RT>(dot[2 * i + 1]);
+      if (P.bias != nullptr) {
+        const int64_t bb = e * P.bias_expert + 2 * (int64_t)act[i];
+        g = round_to<RT>(g + ld_bias<BT>(P.bias, bb));
+        u = round_to<RT>(u + ld_bias<BT>(P.bias, bb + 1));
+      }
+      g = fminf(g, P.limit);
+      u = fmaxf(fminf(u, P.limit), -P.limit);
+      const float num = (u + 1.0f) * g;
+      const float den = 1.0f + exp_f32(-g * P.alpha);
+      store<OT>(reinterpret_cast<OT*>(P.out) + (int64_t)slot * P.out_slot + act[i], num / den);
+    }
+  }
+}
+
+struct DownParams {
+  const uint8_t* w; int64_t w_expert, w_row;
+  const uint8_t* s; int64_t s_expert, s_row;
+  const void* x; int64_t x_slot;
+  const int32_t* experts;
+  const void* scores;
+  const void* bias; int64_t bias_expert;
+  void* out;
+  int rows, cols, slots, e8_extra;
+};
+
+template <typename ScT> __device__ __forceinline__ float ld_score(const void* p, int i) {
+  return to_f32(reinterpret_cast<const ScT*>(p)[i]);
+}
+
+template <Fmt F, typename XT, typename OT, typename RT, typename BT, typename ScT, int LPR, int RPW>
+__global__ __launch_bounds__(256) void weighted_down_kernel(DownParams P) {
+  extern __shared__ uint32_t xs_lds[];
+  constexpr int SUBS = 64 / LPR;
+  const int words = P.cols >> 1;
+  for (int s = 0; s < P.slots; s++) {
+    const uint32_t* xg = reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(P.x) + (int64_t)s * P.x_slot);
+    for (int i = threadIdx.x; i < words; i += blockDim.x) xs_lds[s * words + i] = xg[i];
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int sub = lane / LPR, l = lane % LPR;
+  const int nchunks = P.cols >> 5;
+  const int per_iter = RPW * SUBS;
+  const int waves_total = gridDim.x * (blockDim.x >> 6);
+  for (int base = (blockIdx.x * (blockDim.x >> 6) + wave) * per_iter; base < P.rows; base += waves_total * per_iter) {
+    int row[RPW];
+    bool rv[RPW];
+    float combined[RPW];
+#pragma unroll
+    for (int i = 0; i < RPW; i++) {
+      row[i] = base + i * SUBS + sub;
+      rv[i] = row[i] < P.rows;
+      combined[i] = 0.0f;
+    }
+    for (int s = 0; s < P.slots; s++) {
+      const int64_t e = P.experts[s];
+      const uint8_t* wrow[RPW];
+      const uint8_t* srow[RPW];
+#pragma unroll
+      for (int i = 0; i < RPW; i++) {
+        wrow[i] = P.w + e * P.w_expert + (int64_t)row[i] * P.w_row;
+        srow[i] = P.s + e * P.s_expert + (int64_t)row[i] * P.s_row;
+      }
+      float dot[RPW];
+      e8_rows_dot<F, XT, LPR, RPW>(wrow, srow, rv, xs_lds + s * words, nchunks, l, P.e8_extra, dot);
+      const float score = ld_score<ScT>(P.scores, s);
+#pragma unroll
+      for (int i = 0; i < RPW; i++) {
+        float v = round_to<RT>(dot[i]);
+        if (P.bias != nullptr && rv[i]) v = round_to<RT>(v + ld_bias<BT>(P.bias, e * P.bias_expert + row[i]));
+        combined[i] = __builtin_fmaf(v, score, combined[i]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < RPW; i++)
+      if (rv[i] && l == i) store<OT>(reinterpret_cast<OT*>(P.out) + row[i], combined[i]);
+  }
+}
+
+// ------------------------------------------------------------------ dispatch
+
+template <typename T> struct DT;
+template <> struct DT<f16_t> { static constexpr int code = TT_F16; };
+template <> struct DT<bf16_t> { static constexpr int code = TT_BF16; };
+template <> struct DT<float> { static constexpr int code = TT_F32; };
+
+// Calls f.template operator()<T>() for the storage type matching `code`.
+template <typename Fn> static int with_type(int code, Fn&& f) {
+  switch (code) {
+    case TT_F16: return f(f16_t{});
+    case TT_BF16: return f(bf16_t{});
+    case TT_F32: return f(float{});
+  }
+  set_error("unsupported dtype code %d", code);
+  return TT_ERR_INVALID;
+}
+
+template <Fmt F, typename XT, typename OT, typename RT, typename BT>
+static int launch_swiglu(const SwigluParams& P, int lpr, int slots, hipStream_t st) {
+  const size_t lds = (size_t)P.cols * 2;
+  auto go = [&](auto kern, int subs) {
+    constexpr int APW = 2;
+    const int per_block = 4 * APW * subs;
+    const int blocks = (P.act_rows + per_block - 1) / per_block;
+    hipLaunchKernelGGL(kern, dim3(blocks, slots), dim3(256), lds, st, P);
+    return check_launch("mxfp_lowbit_selected_swiglu");
+  };
+  switch (lpr) {
+    case 64: return go(swiglu_kernel<F, XT, OT, RT, BT, 64, 2>, 1);
+    case 32: return go(swiglu_kernel<F, XT, OT, RT, BT, 32, 2>, 2);
+    default: return go(swiglu_kernel<F, XT, OT, RT, BT, 16, 2>, 4);
+  }
+}
+
+template <Fmt F, typename XT, typename OT, typename RT, typename BT, typename ScT>
+static int launch_down(const DownParams& P, int lpr, hipStream_t st) {
+  const size_t lds = (size_t)P.cols * 2 * P.slots;
+  auto go = [&](auto kern, int subs) {
+    constexpr int RPW = 4;
+    const int per_block = 4 * RPW * subs;
+    const int blocks = (P.rows + per_block - 1) / per_block;
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), lds, st, P);
+    return check_launch("mxfp_lowbit_weighted_down");
+  };
+  switch (lpr) {
+    case 64: return go(weighted_down_kernel<F, XT, OT, RT, BT, ScT, 64, 4>, 1);
+    case 32: return go(weighted_down_kernel<F, XT, OT, RT, BT, ScT, 32, 4>, 2);
+    default: return go(weighted_down_kernel<F, XT, OT, RT, BT, ScT, 16, 4>, 4);
+  }
+}
+
+static Fmt fmt_for_bits(int bits) { return bits == 2 ? Fmt::kQ2E8 : (bits == 1 ? Fmt::kQ1E8 : Fmt::kMxfp4); }
+
+template <typename XT, typename RT>
+static int swiglu_dispatch(Fmt fmt, int out_dtype, int bias_dtype, const SwigluParams& P, int lpr, int slots, hipStream_t st) {
+  return with_type(out_dtype, [&](auto ot) -> int {
+    using OT = decltype(ot);
+    if constexpr (std::is_same_v<OT, float> || std::is_same_v<OT, XT>) {
+      return with_type(bias_dtype, [&](auto bt) -> int {
+        using BT = decltype(bt);
+        switch (fmt) {
+          case Fmt::kQ2E8: return launch_swiglu<Fmt::kQ2E8, XT, OT, RT, BT>(P, lpr, slots, st);
+          case Fmt::kQ1E8: return launch_swiglu<Fmt::kQ1E8, XT, OT, RT, BT>(P, lpr, slots, st);
+          default: return launch_swiglu<Fmt::kMxfp4, XT, OT, RT, BT>(P, lpr, slots, st);
+        }
+      });
+    } else {
+      set_error("swiglu: output dtype must match the activation dtype or be fp32");
+      return TT_ERR_UNSUPPORTED;
+    }
+  });
+}
+
+template <typename XT, typename RT>
+static int down_dispatch(Fmt fmt, int out_dtype, int bias_dtype, int score_dtype, const DownParams& P, int lpr, hipStream_t st) {
+  return with_type(out_dtype, [&](auto ot) -> int {
+    using OT = decltype(ot);
+    if constexpr (std::is_same_v<OT, float> || std::is_same_v<OT, XT>) {
+      return with_type(bias_dtype, [&](auto bt) -> int {
+        using BT = decltype(bt);
+        return with_type(score_dtype, [&](auto sct) -> int {
+          using ScT = decltype(sct);
+          switch (fmt) {
+            case Fmt::kQ2E8: return launch_down<Fmt::kQ2E8, XT, OT, RT, BT, ScT>(P, lpr, st);
+            case Fmt::kQ1E8: return launch_down<Fmt::kQ1E8, XT, OT, RT, BT, ScT>(P, lpr, st);
+            default: return launch_down<Fmt::kMxfp4, XT, OT, RT, BT, ScT>(P, lpr, st);
+          }
+        });
+      });
+    } else {
+      set_error("weighted_down: output dtype must match the activation dtype or be fp32");
+      return TT_ERR_UNSUPPORTED;
+    }
+  });
+}
+
+}  // namespace tt
+
+using namespace tt;
+
+// bits: 1 or 2 (E8M0 q1/q2, bf16 rounding), 4 (MXFP4, rounding in the activation dtype).
+extern "C" int tt_mxfp_lowbit_selected_swiglu(const void* packed, int64_t w_expert_bytes, int64_t w_row_bytes,
+                                              const void* scales, int64_t s_expert, int64_t s_row, int bits,
+                                              const void* x, int x_dtype, int64_t x_slot,
+                                              const int32_t* expert_indices, int64_t selected, const void* bias,
+                                              int bias_dtype, int64_t bias_expert, float alpha, float limit,
+                                              void* out, int out_dtype, int64_t out_slot, int64_t activation_rows,
+                                              int64_t cols, void* stream) {
+  const char* what = "mxfp_lowbit_selected_swiglu";
+  TT_REQUIRE(bits == 1 || bits == 2 || bits == 4, "%s: fused SwiGLU requires packed Q1, Q2 or MXFP4 experts", what);
+  TT_REQUIRE(valid_act_dtype(x_dtype) && valid_out_dtype(out_dtype), "%s: bad dtype codes", what);
+  TT_REQUIRE(cols > 0 && cols % 32 == 0 && cols <= 32768, "%s: cols must be a multiple of 32 up to 32768", what);
+  TT_REQUIRE(activation_rows > 0 && activation_rows < (1 << 29), "%s: bad activation rows", what);
+  TT_REQUIRE(selected >= 1 && selected <= 65535 && expert_indices, "%s: need selected experts", what);
+  const int align = bits == 4 ? 16 : (bits == 2 ? 8 : 4);
+  TT_REQUIRE(packed && aligned(packed, align) && w_row_bytes % align == 0 && w_expert_bytes % align == 0,
+             "%s: packed weights must be %d-byte aligned", what, align);
+  TT_REQUIRE(scales && x && aligned(x, 4) && x_slot % 2 == 0 && out, "%s: null or misaligned pointer", what);
+  if (bias) TT_REQUIRE(valid_out_dtype(bias_dtype), "%s: bad bias dtype", what);
+  SwigluParams P{static_cast<const uint8_t*>(packed), w_expert_bytes, w_row_bytes,
+                 static_cast<const uint8_t*>(scales), s_expert, s_row, x, x_slot, expert_indices, bias, bias_expert,
+                 alpha, limit, out, out_slot, (int)activation_rows, (int)cols, bits == 4 ? 14 : 0};
+  const int lpr = tt_gemv_lanes_per_row(cols / 32, 1);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const Fmt fmt = fmt_for_bits(bits);
+  const int bdt = bias ? bias_dtype : TT_F32;
+  if (x_dtype == TT_F16) {
+    if (bits == 4) return swiglu_dispatch<f16_t, f16_t>(fmt, out_dtype, bdt, P, lpr, (int)selected, st);
+    return swiglu_dispatch<f16_t, bf16_t>(fmt, out_dtype, bdt, P, lpr, (int)selected, st);
+  }
+  return swiglu_dispatch<bf16_t, bf16_t>(fmt, out_dtype, bdt, P, lpr, (int)selected, st);
+}
+
+extern "C" int tt_mxfp_lowbit_weighted_down(const void* packed, int64_t w_expert_bytes, int64_t w_row_bytes,
+                                            const void* scales, int64_t s_expert, int64_t s_row, int bits,
+                                            const void* x, int x_dtype, int64_t x_slot,
+                                            const int32_t* expert_indices, const void* router_scores,
+                                            int score_dtype, int64_t selected, const void* bias, int bias_dtype,
+                                            int64_t bias_expert, void* out, int out_dtype, int64_t rows,
+                                            int64_t cols, void* stream) {
+  const char* what = "mxfp_lowbit_weighted_down";
+  TT_REQUIRE(bits == 1 || bits == 2 || bits == 4, "%s: fused down requires packed Q1, Q2 or MXFP4 experts", what);
+  TT_REQUIRE(valid_act_dtype(x_dtype) && valid_out_dtype(out_dtype), "%s: bad dtype codes", what);
+  TT_REQUIRE(cols > 0 && cols % 32 == 0, "%s: cols must be a multiple of 32", what);
+  TT_REQUIRE(selected >= 1 && selected * cols <= 32768, "%s: selected * cols must fit the 64 KiB staged activations", what);
+  TT_REQUIRE(rows > 0 && rows < (1 << 30), "%s: bad rows", what);
+  const int align = bits == 4 ? 16 : (bits == 2 ? 8 : 4);
+  TT_REQUIRE(packed && aligned(packed, align) && w_row_bytes % align == 0 && w_expert_bytes % align == 0,
+             "%s: packed weights must be %d-byte aligned", what, align);
+  TT_REQUIRE(scales && x && aligned(x, 4) && x_slot % 2 == 0 && out && expert_indices && router_scores,
+             "%s: null or misaligned pointer", what);
+  TT_REQUIRE(valid_out_dtype(score_dtype), "%s: bad score dtype", what);
+  if (bias) TT_REQUIRE(valid_out_dtype(bias_dtype), "%s: bad bias dtype", what);
+  DownParams P{static_cast<const uint8_t*>(packed), w_expert_bytes, w_row_bytes,
+               static_cast<const uint8_t*>(scales), s_expert, s_row, x, x_slot, expert_indices, router_scores, bias,
+               bias_expert, out, (int)rows, (int)cols, (int)selected, bits == 4 ? 14 : 0};
+  const int lpr = tt_gemv_lanes_per_row(cols / 32, 1);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const Fmt fmt = fmt_for_bits(bits);
+  const int bdt = bias ? bias_dtype : TT_F32;
+  if (x_dtype == TT_F16) {
+    if (bits == 4) return down_dispatch<f16_t, f16_t>(fmt, out_dtype, bdt, score_dtype, P, lpr, st);
+    return down_dispatch<f16_t, bf16_t>(fmt, out_dtype, bdt, score_dtype, P, lpr, st);
+  }
+  return down_dispatch<bf16_t, bf16_t>(fmt, out_dtype, bdt, score_dtype, P, lpr, st);
+}

@@ -1,0 +1,46 @@
+// Internal helpers for the extern "C" entry points: error reporting and checks.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string>
+
+#include "../../include/thintensor_hip.h"
+
+namespace tt {
+
+void set_error(const char* fmt, ...);
+
+#define TT_REQUIRE(cond, ...)                 \
+  do {                                        \
+    if (!(cond)) {                            \
+      ::tt::set_error(__VA_ARGS__);           \
+      return TT_ERR_INVALID;                  \
+    }                                         \
+  } while (0)
+
+#define TT_UNSUPPORTED(cond, ...)             \
+  do {                                        \
+    if (!(cond)) {                            \
+      ::tt::set_error(__VA_ARGS__);           \
+      return TT_ERR_UNSUPPORTED;              \
+    }                                         \
+  } while (0)
+
+inline int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("%s: kernel launch failed: %s", what, hipGetErrorString(e));
+    return TT_ERR_HIP;
+  }
+  return TT_OK;
+}
+
+inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+inline bool valid_act_dtype(int d) { return d == TT_F16 || d == TT_BF16; }
+inline bool valid_out_dtype(int d) { return d == TT_F16 || d == TT_BF16 || d == TT_F32; }
+
+}  // namespace tt

@@ -1,0 +1,108 @@
+// Shared device helpers for the ThinTensor decode kernels on gfx950 (CDNA4, wave64).
+//
+// Numerics contract used by every kernel in this library:
+//   * only IEEE-754 binary32 operations with a single rounding are used for
+//     accumulation: fmaf, +, *, correctly rounded / and sqrt.  No v_dot2 (its
+//     internal accumulator truncates and cannot be reproduced on a CPU), no packed
+//     fp32, no approximate transcendental instructions.
+//   * every reduction has a fixed order that does not depend on the launch shape
+//     beyond the documented "lanes per row" parameter, so a CPU restatement can
+//     reproduce each output bit for bit.
+//   * fp16/bf16 stores round to nearest even.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tt {
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+
+enum DType : int { kF16 = 0, kBF16 = 1, kF32 = 2 };
+
+struct f16_t { uint16_t bits; };
+struct bf16_t { uint16_t bits; };
+
+__device__ __forceinline__ float to_f32(f16_t v) { return (float)__builtin_bit_cast(_Float16, v.bits); }
+__device__ __forceinline__ float to_f32(bf16_t v) { return __builtin_bit_cast(float, (uint32_t)v.bits << 16); }
+__device__ __forceinline__ float to_f32(float v) { return v; }
+
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);  // quiet NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+// Round a binary32 value to bfloat16 and back (used where the reference rounds
+// through bfloat16 regardless of the activation dtype).
+__device__ __forceinline__ float round_bf16(float f) { return __builtin_bit_cast(float, (uint32_t)f32_to_bf16_bits(f) << 16); }
+__device__ __forceinline__ float round_f16(float f) { return (float)(_Float16)f; }
+
+template <typename T> struct Store;
+template <> struct Store<f16_t> { __device__ static void st(f16_t* p, float v) { p->bits = f32_to_f16_bits(v); } };
+template <> struct Store<bf16_t> { __device__ static void st(bf16_t* p, float v) { p->bits = f32_to_bf16_bits(v); } };
+template <> struct Store<float> { __device__ static void st(float* p, float v) { *p = v; } };
+template <typename T> __device__ __forceinline__ void store(T* p, float v) { Store<T>::st(p, v); }
+
+// Round a value to the storage precision of T and return it as float.
+template <typename T> __device__ __forceinline__ float round_to(float v);
+template <> __device__ __forceinline__ float round_to<f16_t>(float v) { return round_f16(v); }
+template <> __device__ __forceinline__ float round_to<bf16_t>(float v) { return round_bf16(v); }
+template <> __device__ __forceinline__ float round_to<float>(float v) { return v; }
+
+// Two 16-bit activations packed in one 32-bit register -> binary32.
+template <typename XT> __device__ __forceinline__ float lo_f32(uint32_t w);
+template <typename XT> __device__ __forceinline__ float hi_f32(uint32_t w);
+template <> __device__ __forceinline__ float lo_f32<f16_t>(uint32_t w) { return (float)__builtin_bit_cast(h2, w)[0]; }
+template <> __device__ __forceinline__ float hi_f32<f16_t>(uint32_t w) { return (float)__builtin_bit_cast(h2, w)[1]; }
+template <> __device__ __forceinline__ float lo_f32<bf16_t>(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
+template <> __device__ __forceinline__ float hi_f32<bf16_t>(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
+
+// Butterfly sum over the lanes whose index differs only in bits [lo_mask, width):
+// after the call every participating lane holds the same value.  IEEE addition is
+// commutative, so lane i computing v_i + v_{i^m} and lane i^m computing
+// v_{i^m} + v_i yield identical bits: the tree is T(a[0..n)) = T(a[0..n/2)) + T(a[n/2..n)).
+__device__ __forceinline__ float xor_sum(float v, int m_begin, int m_end) {
+  for (int m = m_begin; m < m_end; m <<= 1) v = v + __shfl_xor(v, m, 64);
+  return v;
+}
+
+// exp(x) for binary32, reproducible bit for bit on the CPU: Cody-Waite reduction
+// x = n*ln2 + r (two-constant split), degree-7 Taylor polynomial of e^r in Horner
+// form with fmaf, then an exact scaling by 2^n.  Relative error < 2 ulp on
+// [-87, 88]; inputs below -87.3 return 0, above 88.7 return +inf.
+__device__ __forceinline__ float exp_f32(float x) {
+  if (x != x) return x;
+  if (x < -0x1.5d589ep+6f) return 0.0f;
+  if (x > 0x1.62e42ep+6f) return __builtin_bit_cast(float, 0x7f800000u);
+  const float log2e = 0x1.715476p+0f;
+  float n = __builtin_rintf(x * log2e);
+  float r = __builtin_fmaf(n, -0x1.62e4p-1f, x);       // ln2 high part (n*hi is exact)
+  r = __builtin_fmaf(n, -0x1.7f7d1cp-20f, r);    // ln2 low part
+  float p = 0x1.a01a02p-13f;                    // 1/7!
+  p = __builtin_fmaf(p, r, 0x1.6c16c2p-10f);    // 1/6!
+  p = __builtin_fmaf(p, r, 0x1.111112p-7f);     // 1/5!
+  p = __builtin_fmaf(p, r, 0x1.555556p-5f);     // 1/4!
+  p = __builtin_fmaf(p, r, 0x1.555556p-3f);     // 1/3!
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  int ni = (int)n;
+  // scale by 2^ni in two exact steps so that ni in [-126, 128] never overflows the
+  // exponent field of an intermediate.
+  int n1 = ni / 2, n2 = ni - n1;
+  p = p * __builtin_bit_cast(float, (uint32_t)(n1 + 127) << 23);
+  p = p * __builtin_bit_cast(float, (uint32_t)(n2 + 127) << 23);
+  return p;
+}
+
+// 2^e for an integer e in [-149, 127], built exactly (subnormal below -126).
+__device__ __forceinline__ float pow2i(int e) {
+  if (e >= -126) return __builtin_bit_cast(float, (uint32_t)(e + 127) << 23);
+  return __builtin_bit_cast(float, 1u << (e + 149));
+}
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+
+}  // namespace tt

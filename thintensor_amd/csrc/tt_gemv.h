@@ -1,0 +1,268 @@
+// Dequant-fused GEMV machinery shared by the dense, selected-expert and fused MoE
+// kernels.
+//
+// Reduction order (the contract the CPU restatement in oracle/ follows):
+//   * the K axis is cut into chunks of 32 consecutive elements; chunk j is handled
+//     by lane (j mod LPR) of the row's lane group in round (j div LPR);
+//   * chunk partial  p_j = fma-chain over its 32 elements in ascending k, from +0;
+//   * group formats: chunks of one quantisation group sit in L = group/32 adjacent
+//     lanes; S_g = xor-butterfly over those L lanes; t_g = S_g * scale_g (affine:
+//     fmaf(X_g, m_g, S_g * s_g) with X_g the same tree over sequential x-sums);
+//     every lane keeps A = ((+0 + t_round0) + t_round1) + ...; the row value is the
+//     xor-butterfly of A over the lane bits [L, LPR);
+//   * row formats (per-row scale or none): A = ((+0 + p_round0) + p_round1) + ...;
+//     row value = xor-butterfly over all LPR lanes, then * scale_row;
+//   * chunks past the end of K contribute +0 at the same positions.
+#pragma once
+
+#include "tt_common.h"
+
+namespace tt {
+
+enum class Fmt : int {
+  kInt4Sym = 0,   // code c in [0,15], w = (c - 8) * s_group
+  kInt4Aff = 1,   // w = c * s_group + m_group
+  kFp8 = 2,       // float8_e4m3fn, y = (sum w*x) * s_row
+  kF16W = 3,      // plain fp16 weights
+  kBF16W = 4,     // plain bf16 weights
+  kMxfp4 = 5,     // e2m1 codes, E8M0 scale per 32-element block
+  kQ2E8 = 6,      // 2-bit codebook {-1.5,-0.5,0.5,1.5}, E8M0 scale per 32-element block
+  kQ1E8 = 7,      // 1-bit codebook {-1,+1}, E8M0 scale per 32-element block
+  kQ2Aff = 8,     // 2-bit code c in [0,3], w = (c - z) * s per group
+  kQ1Aff = 9,     // 1-bit code c in {0,1}, w = (c - z) * s per group
+};
+
+template <Fmt F> struct FmtInfo;
+template <> struct FmtInfo<Fmt::kInt4Sym> { static constexpr int kBytes = 16; };
+template <> struct FmtInfo<Fmt::kInt4Aff> { static constexpr int kBytes = 16; };
+template <> struct FmtInfo<Fmt::kFp8> { static constexpr int kBytes = 32; };
+template <> struct FmtInfo<Fmt::kF16W> { static constexpr int kBytes = 64; };
+template <> struct FmtInfo<Fmt::kBF16W> { static constexpr int kBytes = 64; };
+template <> struct FmtInfo<Fmt::kMxfp4> { static constexpr int kBytes = 16; };
+template <> struct FmtInfo<Fmt::kQ2E8> { static constexpr int kBytes = 8; };
+template <> struct FmtInfo<Fmt::kQ1E8> { static constexpr int kBytes = 4; };
+template <> struct FmtInfo<Fmt::kQ2Aff> { static constexpr int kBytes = 8; };
+template <> struct FmtInfo<Fmt::kQ1Aff> { static constexpr int kBytes = 4; };
+
+template <int B> struct Raw { uint32_t w[B / 4]; };
+
+template <int B>
+__device__ __forceinline__ Raw<B> load_raw(const uint8_t* p) {
+  Raw<B> r;
+  if constexpr (B == 4) {
+    r.w[0] = *reinterpret_cast<const uint32_t*>(__builtin_assume_aligned(p, 4));
+  } else if constexpr (B == 8) {
+    uint2 v = *reinterpret_cast<const uint2*>(__builtin_assume_aligned(p, 8));
+    r.w[0] = v.x; r.w[1] = v.y;
+  } else {
+    const uint4* q = reinterpret_cast<const uint4*>(__builtin_assume_aligned(p, 16));
+#pragma unroll
+    for (int i = 0; i < B / 16; i++) {
+      uint4 v = q[i];
+      r.w[4 * i + 0] = v.x; r.w[4 * i + 1] = v.y; r.w[4 * i + 2] = v.z; r.w[4 * i + 3] = v.w;
+    }
+  }
+  return r;
+}
+
+template <typename XT>
+__device__ __forceinline__ float xv(const uint32_t* xw, int e) {
+  return (e & 1) ? hi_f32<XT>(xw[e >> 1]) : lo_f32<XT>(xw[e >> 1]);
+}
+
+__device__ __forceinline__ h2 as_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }
+__device__ __forceinline__ h2 hfma(h2 a, float b, float c) {
+  return __builtin_elementwise_fma(a, (h2){(_Float16)b, (_Float16)b}, (h2){(_Float16)c, (_Float16)c});
+}
+
+// Exact fp16 value pairs of 4-bit fields (f, f+4 of the word) minus `off`.
+// (w & 0x000F000F) | 0x6400 6400 encodes 1024 + c; (w & 0x00F000F0) encodes 1024 + 16c.
+__device__ __forceinline__ void nib_pairs(uint32_t w, float off, h2& a, h2& b, h2& c, h2& d) {
+  uint32_t w8 = w >> 8;
+  a = hfma(as_h2((w & 0x000F000Fu) | 0x64006400u), 1.0f, -(1024.0f + off));
+  b = hfma(as_h2((w & 0x00F000F0u) | 0x64006400u), 0.0625f, -(64.0f + off));
+  c = hfma(as_h2((w8 & 0x000F000Fu) | 0x64006400u), 1.0f, -(1024.0f + off));
+  d = hfma(as_h2((w8 & 0x00F000F0u) | 0x64006400u), 0.0625f, -(64.0f + off));
+}
+
+// Chunk partial: fma chain over the 32 elements of one chunk in ascending k.
+template <Fmt F, typename XT>
+__device__ __forceinline__ float chunk_dot(const Raw<FmtInfo<F>::kBytes>& r, const uint32_t* xw) {
+  float p = 0.0f;
+  if constexpr (F == Fmt::kInt4Sym || F == Fmt::kInt4Aff) {
+    // byte b holds k = 2b (low nibble) and k = 2b + 1 (high nibble); word i holds
+    // k = 8i .. 8i+7 with nibble n at bits 4n.
+    const float off = (F == Fmt::kInt4Sym) ? 8.0f : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      h2 a, b, c, d;
+      nib_pairs(r.w[i], off, a, b, c, d);
+      p = __builtin_fmaf((float)a[0], xv<XT>(xw, 8 * i + 0), p);
+      p = __builtin_fmaf((float)b[0], xv<XT>(xw, 8 * i + 1), p);
+      p = __builtin_fmaf((float)c[0], xv<XT>(xw, 8 * i + 2), p);
+      p = __builtin_fmaf((float)d[0], xv<XT>(xw, 8 * i + 3), p);
+      p = __builtin_fmaf((float)a[1], xv<XT>(xw, 8 * i + 4), p);
+      p = __builtin_fmaf((float)b[1], xv<XT>(xw, 8 * i + 5), p);
+      p = __builtin_fmaf((float)c[1], xv<XT>(xw, 8 * i + 6), p);
+      p = __builtin_fmaf((float)d[1], xv<XT>(xw, 8 * i + 7), p);
+    }
+  } else if constexpr (F == Fmt::kMxfp4) {
+    // e2m1 nibble (s e1 e0 m) -> fp16 bits s<<15 | (e1 e0 m)<<9, which is the e2m1
+    // value times 2^-14 exactly (e=0 lands in the fp16 subnormal range).  The 2^14
+    // factor is restored together with the block scale.
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      uint32_t w = r.w[i];
+      h2 a = as_h2(((w & 0x00070007u) << 9) | ((w & 0x00080008u) << 12));   // k 8i+0, 8i+4
+      h2 b = as_h2(((w & 0x00700070u) << 5) | ((w & 0x00800080u) << 8));    // k 8i+1, 8i+5
+      uint32_t w8 = w >> 8;
+      h2 c = as_h2(((w8 & 0x00070007u) << 9) | ((w8 & 0x00080008u) << 12)); // k 8i+2, 8i+6
+      h2 d = as_h2(((w8 & 0x00700070u) << 5) | ((w8 & 0x00800080u) << 8));  // k 8i+3, 8i+7
+      p = __builtin_fmaf((float)a[0], xv<XT>(xw, 8 * i + 0), p);
+      p = __builtin_fmaf((float)b[0], xv<XT>(xw, 8 * i + 1), p);
+      p = __builtin_fmaf((float)c[0], xv<XT>(xw, 8 * i + 2), p);
+      p = __builtin_fmaf((float)d[0], xv<XT>(xw, 8 * i + 3), p);
+      p = __builtin_fmaf((float)a[1], xv<XT>(xw, 8 * i + 4), p);
+      p = __builtin_fmaf((float)b[1], xv<XT>(xw, 8 * i + 5), p);
+      p = __builtin_fmaf((float)c[1], xv<XT>(xw, 8 * i + 6), p);
+      p = __builtin_fmaf((float)d[1], xv<XT>(xw, 8 * i + 7), p);
+    }
+  } else if constexpr (F == Fmt::kFp8) {
+    // 32 bytes, byte e = element e; e4m3fn -> f32 is exact.
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      auto lo = __builtin_amdgcn_cvt_pk_f32_fp8(r.w[i], false);
+      auto hi = __builtin_amdgcn_cvt_pk_f32_fp8(r.w[i], true);
+      p = __builtin_fmaf(lo[0], xv<XT>(xw, 4 * i + 0), p);
+      p = __builtin_fmaf(lo[1], xv<XT>(xw, 4 * i + 1), p);
+      p = __builtin_fmaf(hi[0], xv<XT>(xw, 4 * i + 2), p);
+      p = __builtin_fmaf(hi[1], xv<XT>(xw, 4 * i + 3), p);
+    }
+  } else if constexpr (F == Fmt::kF16W) {
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      h2 v = as_h2(r.w[i]);
+      p = __builtin_fmaf((float)v[0], xv<XT>(xw, 2 * i + 0), p);
+      p = __builtin_fmaf((float)v[1], xv<XT>(xw, 2 * i + 1), p);
+    }
+  } else if constexpr (F == Fmt::kBF16W) {
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      p = __builtin_fmaf(lo_f32<bf16_t>(r.w[i]), xv<XT>(xw, 2 * i + 0), p);
+      p = __builtin_fmaf(hi_f32<bf16_t>(r.w[i]), xv<XT>(xw, 2 * i + 1), p);
+    }
+  } else if constexpr (F == Fmt::kQ2E8 || F == Fmt::kQ2Aff) {
+    // 8 bytes; element i at byte i/4, bits 2*(i%4), so word q holds elements
+    // 16q..16q+15 with element n at bits 2n.  Fields are moved to bits 2..9 (and
+    // 18..25) first so that every fp16 constant below is exactly representable:
+    // field f' (1..4) encodes 1024 + 4^f' c, scaled back by 4^-f'.
+    const float off = (F == Fmt::kQ2E8) ? 1.5f : 0.0f;
+#pragma unroll
+    for (int q = 0; q < 2; q++) {
+      const uint32_t u0 = r.w[q] << 2;   // elements 0..3 | 8..11 of this word
+      const uint32_t u1 = r.w[q] >> 6;   // elements 4..7 | 12..15
+      h2 a0 = hfma(as_h2((u0 & 0x000C000Cu) | 0x64006400u), 0.25f, -(256.0f + off));
+      h2 a1 = hfma(as_h2((u0 & 0x00300030u) | 0x64006400u), 0.0625f, -(64.0f + off));
+      h2 a2 = hfma(as_h2((u0 & 0x00C000C0u) | 0x64006400u), 0.015625f, -(16.0f + off));
+      h2 a3 = hfma(as_h2((u0 & 0x03000300u) | 0x64006400u), 0.00390625f, -(4.0f + off));
+      h2 b0 = hfma(as_h2((u1 & 0x000C000Cu) | 0x64006400u), 0.25f, -(256.0f + off));
+      h2 b1 = hfma(as_h2((u1 & 0x00300030u) | 0x64006400u), 0.0625f, -(64.0f + off));
+      h2 b2 = hfma(as_h2((u1 & 0x00C000C0u) | 0x64006400u), 0.015625f, -(16.0f + off));
+      h2 b3 = hfma(as_h2((u1 & 0x03000300u) | 0x64006400u), 0.00390625f, -(4.0f + off));
+      const int e = 16 * q;
+      p = __builtin_fmaf((float)a0[0], xv<XT>(xw, e + 0), p);
+      p = __builtin_fmaf((float)a1[0], xv<XT>(xw, e + 1), p);
+      p = __builtin_fmaf((float)a2[0], xv<XT>(xw, e + 2), p);
+      p = __builtin_fmaf((float)a3[0], xv<XT>(xw, e + 3), p);
+      p = __builtin_fmaf((float)b0[0], xv<XT>(xw, e + 4), p);
+      p = __builtin_fmaf((float)b1[0], xv<XT>(xw, e + 5), p);
+      p = __builtin_fmaf((float)b2[0], xv<XT>(xw, e + 6), p);
+      p = __builtin_fmaf((float)b3[0], xv<XT>(xw, e + 7), p);
+      p = __builtin_fmaf((float)a0[1], xv<XT>(xw, e + 8), p);
+      p = __builtin_fmaf((float)a1[1], xv<XT>(xw, e + 9), p);
+      p = __builtin_fmaf((float)a2[1], xv<XT>(xw, e + 10), p);
+      p = __builtin_fmaf((float)a3[1], xv<XT>(xw, e + 11), p);
+      p = __builtin_fmaf((float)b0[1], xv<XT>(xw, e + 12), p);
+      p = __builtin_fmaf((float)b1[1], xv<XT>(xw, e + 13), p);
+      p = __builtin_fmaf((float)b2[1], xv<XT>(xw, e + 14), p);
+      p = __builtin_fmaf((float)b3[1], xv<XT>(xw, e + 15), p);
+    }
+  } else if constexpr (F == Fmt::kQ1E8 || F == Fmt::kQ1Aff) {
+    // 4 bytes; element i at byte i/8, bit i%8, i.e. bit i of the word.  Bits move
+    // to positions 1..8 (17..24) so the fp16 constants stay exact: bit n' encodes
+    // 1024 + 2^n' b.  E8M0 q1 maps b to 2b - 1, the affine form keeps b.
+    const uint32_t w = r.w[0];
+#pragma unroll
+    for (int quarter = 0; quarter < 4; quarter++) {
+      const uint32_t u = (quarter & 1) ? (w >> 7) : (w << 1);
+      const int hi = quarter >> 1;
+#pragma unroll
+      for (int n = 1; n <= 8; n++) {
+        h2 t = as_h2((u & (0x00010001u << n)) | 0x64006400u);
+        h2 v;
+        if constexpr (F == Fmt::kQ1E8)
+          v = hfma(t, 2.0f / (float)(1 << n), -(2048.0f / (float)(1 << n) + 1.0f));
+        else
+          v = hfma(t, 1.0f / (float)(1 << n), -(1024.0f / (float)(1 << n)));
+        p = __builtin_fmaf((float)v[hi], xv<XT>(xw, 8 * quarter + n - 1), p);
+      }
+    }
+  }
+  return p;
+}
+
+// Row values of NR rows in the E8M0 block-scale order (one 32-element block per
+// chunk): t_j = (p_j * 2^extra) * 2^(e_j - 127), A = ((+0 + t_round0) + ...),
+// value = xor-butterfly over the LPR lanes.  `xs` is the activation vector in LDS.
+template <Fmt F, typename XT, int LPR, int NR>
+__device__ __forceinline__ void e8_rows_dot(const uint8_t* const* wrow, const uint8_t* const* srow, const bool* rv,
+                                            const uint32_t* xs, int nchunks, int l, int e8_extra, float* out) {
+  constexpr int B = FmtInfo<F>::kBytes;
+  const int rounds = (nchunks + LPR - 1) / LPR;
+  float acc[NR];
+#pragma unroll
+  for (int i = 0; i < NR; i++) acc[i] = 0.0f;
+  for (int r = 0; r < rounds; r++) {
+    const int j = r * LPR + l;
+    const bool cv = j < nchunks;
+    uint32_t xw[16];
+    if (cv) {
+      const uint4* xp = reinterpret_cast<const uint4*>(xs + j * 16);
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        uint4 v = xp[q];
+        xw[4 * q] = v.x; xw[4 * q + 1] = v.y; xw[4 * q + 2] = v.z; xw[4 * q + 3] = v.w;
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < 16; q++) xw[q] = 0u;
+    }
+    Raw<B> raw[NR];
+    int ex[NR];
+#pragma unroll
+    for (int i = 0; i < NR; i++) {
+      if (cv && rv[i]) {
+        raw[i] = load_raw<B>(wrow[i] + (int64_t)j * B);
+        ex[i] = srow[i][j];
+      } else {
+#pragma unroll
+        for (int q = 0; q < B / 4; q++) raw[i].w[q] = 0u;
+        ex[i] = 127;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NR; i++) {
+      float t = 0.0f;
+      if (cv && rv[i]) {
+        float q = chunk_dot<F, XT>(raw[i], xw);
+        if (e8_extra) q = q * pow2i(e8_extra);
+        t = q * pow2i(ex[i] - 127);
+      }
+      acc[i] = acc[i] + t;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < NR; i++) out[i] = xor_sum(acc[i], 1, LPR);
+}
+
+}  // namespace tt
