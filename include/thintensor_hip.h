@@ -115,7 +115,9 @@ int tt_mxfp_lowbit_selected_matvec(const void* packed, int64_t w_expert_bytes, i
                                    void* out, int out_dtype, int64_t out_slot,
                                    int64_t rows, int64_t cols, void* stream);
 
-/* Fused gate/up GEMV on interleaved rows (2i gate, 2i+1 up) + gpt-oss SwiGLU:
+/* Fused gate/up GEMV on interleaved rows (2i gate, 2i+1 up) + gpt-oss SwiGLU;
+ * bits 1/2 = E8M0 low-bit experts (bf16 rounding), bits 4 = MXFP4 blocks (rounding
+ * in the activation dtype, the reference's unfused MXFP4 chain):
  * g = bf16(bf16(dot) + bias), u likewise; g = min(g, L); u = clamp(u, -L, L);
  * out = (u + 1) * g / (1 + exp(-alpha g)).  bias [E, 2I] (nullable).
  * Replaces TritonDecodeBackend.mxfp_lowbit_selected_swiglu
@@ -159,6 +161,98 @@ int tt_int4_selected_matvec(const void* packed, int64_t w_expert_bytes, int64_t 
                             const int32_t* expert_indices, int64_t selected,
                             void* out, int out_dtype, int64_t out_slot,
                             int64_t rows, int64_t cols, int64_t group_size, void* stream);
+
+/* Greedy lm_head: logits = round(W x) (stored when `logits` is non-null), token =
+ * first index of the maximum rounded logit (NaN counts as the maximum, +0 == -0),
+ * written as int64 to out_idx and the value to out_val (nullable).  `partials` is
+ * caller scratch of tt_matvec_argmax_partials(rows, cols) uint64 entries.
+ * Replaces TritonDecodeBackend.matvec_argmax_tensor and its two-stage / persistent
+ * variants (triton_kernels.py:5365-5398, 5516-5625; kernels :2222-2285, :2456-2558). */
+int64_t tt_matvec_argmax_partials(int64_t rows, int64_t cols);
+int tt_matvec_argmax(const void* weight, int w_dtype, int64_t w_row, const void* x, int x_dtype,
+                     void* logits, int logits_dtype, int64_t rows, int64_t cols, uint64_t* partials,
+                     int64_t partials_capacity, int64_t* out_idx, float* out_val, void* stream);
+
+/* ---------------------------------------------------------------- norms / elementwise */
+
+/* out = x * (1 / sqrt(mean(x^2) + eps)) * (w + weight_offset)
+ * Replaces TritonDecodeBackend.rms_norm (triton_kernels.py:5632-5644; kernel :2562-2577). */
+int tt_rms_norm(const void* x, int x_dtype, const void* weight, int w_dtype, void* out, int out_dtype,
+                int64_t n, float eps, float weight_offset, void* stream);
+
+/* residual_out = bf16(left + right); out = residual * rsqrt(mean(residual^2) + eps) * w
+ * Replaces TritonDecodeBackend.add_rms_norm (triton_kernels.py:5646-5667; kernel :2581-2614). */
+int tt_add_rms_norm(const void* left, const void* right, void* residual_out, int x_dtype,
+                    const void* weight, int w_dtype, void* out, int out_dtype, int64_t n, float eps,
+                    void* stream);
+
+/* out = a + b.  Replaces TritonDecodeBackend.add (triton_kernels.py:5862-5873). */
+int tt_add(const void* a, const void* b, void* out, int dtype, int64_t n, void* stream);
+
+/* out = silu(gate) * up.  Replaces TritonDecodeBackend.silu_mul (triton_kernels.py:5751-5762). */
+int tt_silu_mul(const void* gate, const void* up, void* out, int dtype, int64_t n, void* stream);
+
+/* gpt-oss SwiGLU on interleaved gate/up rows [rows, 2n] -> [rows, n].
+ * Replaces TritonDecodeBackend.interleaved_swiglu (triton_kernels.py:5764-5782). */
+int tt_interleaved_swiglu(const void* gate_up, int64_t in_row, void* out, int64_t out_row, int dtype,
+                          int64_t rows, int64_t n, float alpha, float limit, void* stream);
+
+/* out[n] = sum_e experts[e, n] * scores[e] in expert order.
+ * Replaces TritonDecodeBackend.weighted_expert_sum (triton_kernels.py:5784-5801). */
+int tt_weighted_expert_sum(const void* experts, int dtype, int64_t stride, int64_t count,
+                           const void* scores, int score_dtype, void* out, int64_t width, void* stream);
+
+/* In-place RoPE of q [heads, D] and k [kv_heads, D] with cos/sin rows taken from a
+ * [positions, D/2] table at the position read from position_dev (if non-null) or
+ * `position`.  Replaces TritonDecodeBackend.rope_qk_inplace
+ * (triton_kernels.py:5689-5714; kernel :2638-2687), with the position on the device. */
+int tt_rope_qk_inplace(void* q, void* k, int dtype, const void* cos_table, const void* sin_table,
+                       int64_t table_row, const int32_t* position_dev, int64_t position, int64_t heads,
+                       int64_t kv_heads, int64_t head_dim, void* stream);
+
+/* out = embed[token] with the token read from token_dev (int64) if non-null.
+ * Replaces the runtime's embedding row copy (gpu_runtime.py:11396-11427). */
+int tt_embedding(const void* embed, int64_t row_stride, const int64_t* token_dev, int64_t token, void* out,
+                 int64_t n, void* stream);
+
+/* keys[h, pos, :] = k[h, :]; values[h, pos, :] = v[h, :] (16-bit elements).
+ * Replaces PagedKVCache.append for a flat cache (gpu_runtime.py:4132-4229). */
+int tt_kv_append(const void* k, const void* v, void* keys, void* values, int64_t stride_head,
+                 int64_t stride_token, const int32_t* position_dev, int64_t position, int64_t kv_heads,
+                 int64_t head_dim, void* stream);
+
+/* position_dev[0] += step (keeps graph replays moving along the sequence). */
+int tt_advance_position(int32_t* position_dev, int32_t step, void* stream);
+
+/* ---------------------------------------------------------------- attention / router */
+
+/* Floats of scratch tt_single_token_gqa_attention needs. */
+int tt_attention_scratch_floats(int64_t heads, int64_t max_tokens, int64_t head_dim);
+
+/* Single-token GQA attention over keys/values [kv_heads, tokens, D] (strides in
+ * elements) with optional sinks [heads]; the token count is read from tokens_dev
+ * (int32) when non-null.  out [heads, D].
+ * Replaces TritonDecodeBackend.single_token_gqa_attention and
+ * split_single_token_gqa_attention (triton_kernels.py:5228-5363; kernels :15-245). */
+int tt_single_token_gqa_attention(const void* q, const void* keys, const void* values, int dtype,
+                                  int64_t k_head, int64_t k_tok, int64_t v_head, int64_t v_tok,
+                                  const void* sinks, int sink_dtype, const int32_t* tokens_dev,
+                                  int64_t tokens, int64_t max_tokens, int64_t heads, int64_t kv_heads,
+                                  int64_t head_dim, float* scratch, int64_t scratch_floats, void* out,
+                                  void* stream);
+
+/* Router GEMV + bias + top-k + softmax (E <= 128), logits rounded through bf16.
+ * Replaces TritonDecodeBackend.moe_router_matvec_topk (triton_kernels.py:5826-5860;
+ * kernel :2855-2921). */
+int tt_moe_router_matvec_topk(const void* weight, int w_dtype, int64_t w_row, const void* hidden,
+                              int x_dtype, int64_t hidden_size, const void* bias, int bias_dtype,
+                              int64_t experts, int64_t top_k, int renormalize, int32_t* indices_out,
+                              void* scores_out, int score_dtype, void* stream);
+
+/* Top-k + softmax on given logits.  Replaces TritonDecodeBackend.moe_router_topk
+ * (triton_kernels.py:5803-5824; kernel :2821-2851). */
+int tt_moe_router_topk(const void* logits, int logits_dtype, int64_t experts, int64_t top_k, int renormalize,
+                       int32_t* indices_out, void* scores_out, int score_dtype, void* stream);
 
 #ifdef __cplusplus
 }

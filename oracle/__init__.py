@@ -46,15 +46,27 @@ def lib() -> ctypes.CDLL:
 
 
 def _register_extra(L: ctypes.CDLL) -> None:
-    """Signatures of the non-GEMV operators (added as they are restated)."""
+    """Signatures of the non-GEMV operators."""
     for name, argtypes in EXTRA_SIGNATURES.items():
-        fn = getattr(L, name, None)
-        if fn is not None:
-            fn.argtypes = argtypes
-            fn.restype = _I
+        fn = getattr(L, name)
+        fn.argtypes = argtypes
+        fn.restype = _I
+    L.tto_argmax.argtypes = [_P, _I, _L]
+    L.tto_argmax.restype = _L
 
+
+_F = ctypes.c_float
 
 EXTRA_SIGNATURES: dict[str, list] = {
+    "tto_rms_norm": [_P, _I, _P, _I, _P, _I, _I, ctypes.c_float, ctypes.c_float],
+    "tto_add_rms_norm": [_P, _P, _P, _I, _P, _I, _P, _I, _I, ctypes.c_float],
+    "tto_silu_mul": [_P, _P, _P, _I, _I],
+    "tto_interleaved_swiglu": [_P, _P, _I, _I, _I, ctypes.c_float, ctypes.c_float],
+    "tto_weighted_expert_sum": [_P, _I, _P, _I, _P, _I, _I],
+    "tto_rope": [_P, _P, _I, _P, _P, _I, _I, _I],
+    "tto_attention": [_P, _P, _P, _I, _L, _L, _L, _L, _P, _I, _I, _I, _I, _I, _P],
+    "tto_router": [_P, _I, _L, _P, _I, _I, _P, _I, _I, _I, _I, _P, _P, _I],
+    "tto_topk": [_P, _I, _I, _I, _I, _P, _P, _I],
     "tto_swiglu": [_I, _I, _P, _L, _L, _P, _L, _L, _P, _I, _L, _P, _I, _P, _I, _L, ctypes.c_float, ctypes.c_float,
                    _P, _I, _L, _I, _I, _I],
     "tto_weighted_down": [_I, _I, _P, _L, _L, _P, _L, _L, _P, _I, _L, _P, _P, _I, _I, _P, _I, _L, _P, _I, _I, _I,

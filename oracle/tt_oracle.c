@@ -345,3 +345,234 @@ int tto_weighted_down(int fmt, int rt, const uint8_t* w, int64_t w_expert, int64
   }
   return 0;
 }
+
+/* ------------------------------------------------------------ norms / elementwise */
+
+/* 256-thread block sum: per-wave butterfly over 64 lanes, then (w0 + w1) + (w2 + w3). */
+static float block_sum256(const float* part) {
+  float w[4];
+  for (int wv = 0; wv < 4; wv++) {
+    float v[64];
+    memcpy(v, part + 64 * wv, sizeof v);
+    xor_sum(v, 64, 1, 64);
+    w[wv] = v[0];
+  }
+  return (w[0] + w[1]) + (w[2] + w[3]);
+}
+
+/* RMSNorm (triton_kernels.py:2562-2577): out = (x * inv) * (w + offset). */
+int tto_rms_norm(const void* x, int xdt, const void* w, int wdt, void* out, int odt, int n, float eps, float offset) {
+  float part[256];
+  for (int t = 0; t < 256; t++) {
+    float s = 0.0f;
+    for (int i = t; i < n; i += 256) {
+      const float v = act_get(x, xdt, i);
+      s = fmaf(v, v, s);
+    }
+    part[t] = s;
+  }
+  const float total = block_sum256(part);
+  const float inv = 1.0f / sqrtf(total / (float)n + eps);
+  for (int i = 0; i < n; i++) act_put(out, odt, i, (act_get(x, xdt, i) * inv) * (act_get(w, wdt, i) + offset));
+  return 0;
+}
+
+/* add + RMSNorm with the residual rounded through bf16 (triton_kernels.py:2581-2614). */
+int tto_add_rms_norm(const void* l, const void* r, void* res_out, int xdt, const void* w, int wdt, void* out, int odt,
+                     int n, float eps) {
+  float part[256];
+  for (int t = 0; t < 256; t++) {
+    float s = 0.0f;
+    for (int i = t; i < n; i += 256) {
+      const float v = tto_round_bf16(act_get(l, xdt, i) + act_get(r, xdt, i));
+      s = fmaf(v, v, s);
+    }
+    part[t] = s;
+  }
+  const float total = block_sum256(part);
+  const float inv = 1.0f / sqrtf(total / (float)n + eps);
+  for (int i = 0; i < n; i++) {
+    const float v = tto_round_bf16(act_get(l, xdt, i) + act_get(r, xdt, i));
+    act_put(res_out, xdt, i, v);
+    act_put(out, odt, i, (v * inv) * act_get(w, wdt, i));
+  }
+  return 0;
+}
+
+/* silu(g) * u = (g / (1 + exp(-g))) * u (triton_kernels.py:2761-2774) */
+int tto_silu_mul(const void* g, const void* u, void* out, int dt, int n) {
+  for (int i = 0; i < n; i++) {
+    const float gv = act_get(g, dt, i);
+    act_put(out, dt, i, (gv / (1.0f + tto_exp_f32(-gv))) * act_get(u, dt, i));
+  }
+  return 0;
+}
+
+/* gpt-oss SwiGLU on interleaved gate/up (triton_kernels.py:2778-2793) */
+int tto_interleaved_swiglu(const void* gu, void* out, int dt, int rows, int n, float alpha, float limit) {
+  for (int r = 0; r < rows; r++)
+    for (int i = 0; i < n; i++) {
+      float g = act_get(gu, dt, (int64_t)r * 2 * n + 2 * i), u = act_get(gu, dt, (int64_t)r * 2 * n + 2 * i + 1);
+      g = fminf(g, limit);
+      u = fmaxf(fminf(u, limit), -limit);
+      act_put(out, dt, (int64_t)r * n + i, ((u + 1.0f) * g) / (1.0f + tto_exp_f32(-g * alpha)));
+    }
+  return 0;
+}
+
+/* sum_e experts[e] * scores[e] in expert order (triton_kernels.py:2797-2817) */
+int tto_weighted_expert_sum(const void* ex, int dt, const void* sc, int sdt, void* out, int width, int count) {
+  for (int i = 0; i < width; i++) {
+    float acc = 0.0f;
+    for (int e = 0; e < count; e++) acc = fmaf(act_get(ex, dt, (int64_t)e * width + i), act_get(sc, sdt, e), acc);
+    act_put(out, dt, i, acc);
+  }
+  return 0;
+}
+
+/* RoPE with per-op rounding to the activation dtype (gpu_runtime.py:8696-8705). */
+int tto_rope(void* q, void* k, int dt, const void* cos_row, const void* sin_row, int heads, int kv_heads, int head_dim) {
+  const int half = head_dim / 2;
+  for (int h = 0; h < heads + kv_heads; h++) {
+    void* base = h < heads ? q : k;
+    const int64_t off = (int64_t)(h < heads ? h : h - heads) * head_dim;
+    for (int i = 0; i < half; i++) {
+      const float c = act_get(cos_row, dt, i), s = act_get(sin_row, dt, i);
+      const float a = act_get(base, dt, off + i), b = act_get(base, dt, off + i + half);
+      const float ac = round_to(dt, a * c), bs = round_to(dt, b * s), bc = round_to(dt, b * c), as = round_to(dt, a * s);
+      act_put(base, dt, off + i, ac - bs);
+      act_put(base, dt, off + i + half, bc + as);
+    }
+  }
+  return 0;
+}
+
+/* ------------------------------------------------------------ attention */
+
+/*
+ * Single-token GQA attention (triton_kernels.py:15-109) in the kernel's split-KV
+ * order (thintensor_amd/csrc/attention.hip): 64-token chunks, score = fma chain over
+ * d times scale, chunk max, p = exp(s - m), l = 64-lane butterfly, o = fma over the
+ * chunk's tokens; chunks combined in order with an optional sink.
+ * keys/values: [kv_heads][...] with strides (elements).
+ */
+int tto_attention(const void* q, const void* keys, const void* values, int dt, int64_t k_head, int64_t k_tok,
+                  int64_t v_head, int64_t v_tok, const void* sinks, int sdt, int tokens, int heads, int kv_heads,
+                  int D, void* out) {
+  const int G = heads / kv_heads;
+  const int nc = (tokens + 63) / 64;
+  const float scale = (float)(1.0 / sqrt((double)D));
+  float* pm = (float*)malloc(sizeof(float) * (size_t)nc);
+  float* pl = (float*)malloc(sizeof(float) * (size_t)nc);
+  float* po = (float*)malloc(sizeof(float) * (size_t)nc * (size_t)D);
+  for (int h = 0; h < heads; h++) {
+    const int kvh = h / G;
+    for (int c = 0; c < nc; c++) {
+      float s[64], p[64];
+      float m = -INFINITY;
+      for (int lane = 0; lane < 64; lane++) {
+        const int t = c * 64 + lane;
+        if (t < tokens) {
+          float acc = 0.0f;
+          for (int d = 0; d < D; d++)
+            acc = fmaf(act_get(q, dt, (int64_t)h * D + d), act_get(keys, dt, kvh * k_head + (int64_t)t * k_tok + d), acc);
+          s[lane] = acc * scale;
+        } else {
+          s[lane] = -INFINITY;
+        }
+        m = fmaxf(m, s[lane]);
+      }
+      for (int lane = 0; lane < 64; lane++) p[lane] = (c * 64 + lane < tokens) ? tto_exp_f32(s[lane] - m) : 0.0f;
+      float l[64];
+      memcpy(l, p, sizeof l);
+      xor_sum(l, 64, 1, 64);
+      pm[c] = m;
+      pl[c] = l[0];
+      const int nt = tokens - c * 64 < 64 ? tokens - c * 64 : 64;
+      for (int d = 0; d < D; d++) {
+        float o = 0.0f;
+        for (int tt = 0; tt < nt; tt++) o = fmaf(p[tt], act_get(values, dt, kvh * v_head + (int64_t)(c * 64 + tt) * v_tok + d), o);
+        po[(size_t)c * D + d] = o;
+      }
+    }
+    float M = -INFINITY, sink = 0.0f;
+    if (sinks) {
+      sink = act_get(sinks, sdt, h);
+      M = sink;
+    }
+    for (int c = 0; c < nc; c++) M = fmaxf(M, pm[c]);
+    float den = sinks ? tto_exp_f32(sink - M) : 0.0f;
+    for (int c = 0; c < nc; c++) den = fmaf(pl[c], tto_exp_f32(pm[c] - M), den);
+    for (int d = 0; d < D; d++) {
+      float acc = 0.0f;
+      for (int c = 0; c < nc; c++) acc = fmaf(po[(size_t)c * D + d], tto_exp_f32(pm[c] - M), acc);
+      act_put(out, dt, (int64_t)h * D + d, acc / den);
+    }
+  }
+  free(pm);
+  free(pl);
+  free(po);
+  return 0;
+}
+
+/* ------------------------------------------------------------ router / argmax */
+
+/* Top-k by iterated argmax (lowest index on ties) + softmax (triton_kernels.py:2821-2851). */
+static void topk_softmax(const float* lg, int E, int k, int renorm, int32_t* idx, float* score) {
+  float maximum = -INFINITY;
+  for (int e = 0; e < E; e++) maximum = fmaxf(maximum, lg[e]);
+  char taken[1024] = {0};
+  for (int s = 0; s < k; s++) {
+    int bi = -1;
+    float bv = 0.0f;
+    for (int e = 0; e < E; e++) {
+      if (taken[e]) continue;
+      if (bi < 0 || lg[e] > bv) { bi = e; bv = lg[e]; }
+    }
+    taken[bi] = 1;
+    idx[s] = bi;
+    score[s] = bv;
+  }
+  float den = 0.0f;
+  if (renorm) for (int s = 0; s < k; s++) den = den + tto_exp_f32(score[s] - maximum);
+  else for (int e = 0; e < E; e++) den = den + tto_exp_f32(lg[e] - maximum);
+  for (int s = 0; s < k; s++) score[s] = tto_exp_f32(score[s] - maximum) / den;
+}
+
+/* Router GEMV (64 lanes per row) + bf16 logits + bias + top-k + softmax
+ * (triton_kernels.py:2855-2921). */
+int tto_router(const void* w, int wdt, int64_t w_row, const void* x, int xdt, int H, const void* bias, int bdt, int E,
+               int k, int renorm, int32_t* idx, void* scores, int odt) {
+  float lg[1024], sc[1024];
+  const int fmt = wdt == TTO_BF16 ? FMT_BF16W : FMT_F16W;
+  for (int e = 0; e < E; e++) {
+    float v = tto_gemv_row(fmt, SM_NONE, (const uint8_t*)w + (size_t)(e * w_row) * 2, NULL, TTO_F32, 0, 0, 0, 0, x, xdt,
+                           H, 1, 64);
+    v = tto_round_bf16(v);
+    if (bias) v = tto_round_bf16(v + act_get(bias, bdt, e));
+    lg[e] = v;
+  }
+  topk_softmax(lg, E, k, renorm, idx, sc);
+  for (int s = 0; s < k; s++) act_put(scores, odt, s, sc[s]);
+  return 0;
+}
+
+int tto_topk(const void* logits, int ldt, int E, int k, int renorm, int32_t* idx, void* scores, int odt) {
+  float lg[1024], sc[1024];
+  for (int e = 0; e < E; e++) lg[e] = act_get(logits, ldt, e);
+  topk_softmax(lg, E, k, renorm, idx, sc);
+  for (int s = 0; s < k; s++) act_put(scores, odt, s, sc[s]);
+  return 0;
+}
+
+/* torch.argmax over rounded logits: first index of the maximum, NaN wins. */
+int64_t tto_argmax(const void* logits, int dt, int64_t n) {
+  int64_t bi = 0;
+  float bv = act_get(logits, dt, 0);
+  for (int64_t i = 1; i < n; i++) {
+    const float v = act_get(logits, dt, i);
+    if (bv != bv) break;
+    if (v != v || v > bv) { bi = i; bv = v; }
+  }
+  return bi;
+}

@@ -1,0 +1,168 @@
+"""GPU parity of norms, elementwise ops, RoPE, attention, router and lm_head argmax
+against the CPU oracle (bit for bit) and the float64 closed forms (tolerance)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests.helpers import f16_normal, from_torch_bits, rng, to_torch
+from tests.test_gemv_gpu import assert_bits_equal, lanes
+
+pytestmark = pytest.mark.gpu
+
+
+def P(a):
+    return a.ctypes.data
+
+
+@pytest.mark.parametrize("n,offset", [(2048, 0.0), (2880, 1.0), (5120, 0.0), (100, 0.0)])
+def test_rms_norm(backend, device, n, offset):
+    g = rng(n)
+    x = f16_normal(g, n, 3.0)
+    w = f16_normal(g, n, 0.1)
+    out = torch.empty(n, device=device, dtype=torch.float16)
+    backend.rms_norm(to_torch(x, device), to_torch(w, device), out, 1e-5, weight_offset=offset)
+    want = np.empty(n, dtype=np.float16)
+    oracle.lib().tto_rms_norm(P(x), oracle.F16, P(w), oracle.F16, P(want), oracle.F16, n, 1e-5, offset)
+    assert_bits_equal(from_torch_bits(out), want, "rms_norm")
+
+
+@pytest.mark.parametrize("n", [2048, 2880])
+def test_add_rms_norm(backend, device, n):
+    g = rng(n + 1)
+    a, b = f16_normal(g, n), f16_normal(g, n, 0.5)
+    w = f16_normal(g, n, 0.1)
+    res = torch.empty(n, device=device, dtype=torch.float16)
+    out = torch.empty(n, device=device, dtype=torch.float16)
+    backend.add_rms_norm(to_torch(a, device), to_torch(b, device), res, to_torch(w, device), out, 1e-5)
+    want_res = np.empty(n, dtype=np.float16)
+    want = np.empty(n, dtype=np.float16)
+    oracle.lib().tto_add_rms_norm(P(a), P(b), P(want_res), oracle.F16, P(w), oracle.F16, P(want), oracle.F16, n, 1e-5)
+    assert_bits_equal(from_torch_bits(res), want_res, "residual")
+    assert_bits_equal(from_torch_bits(out), want, "normed")
+
+
+def test_silu_swiglu_weighted_sum_add(backend, device):
+    g = rng(3)
+    n = 8192
+    gt, up = f16_normal(g, n, 3.0), f16_normal(g, n)
+    out = torch.empty(n, device=device, dtype=torch.float16)
+    backend.silu_mul(to_torch(gt, device), to_torch(up, device), out)
+    want = np.empty(n, dtype=np.float16)
+    oracle.lib().tto_silu_mul(P(gt), P(up), P(want), oracle.F16, n)
+    assert_bits_equal(from_torch_bits(out), want, "silu_mul")
+
+    gu = f16_normal(g, (4, 2 * 2880), 6.0)
+    out2 = torch.empty((4, 2880), device=device, dtype=torch.float16)
+    backend.interleaved_swiglu(to_torch(gu, device), out2, alpha=1.702, limit=7.0)
+    want2 = np.empty((4, 2880), dtype=np.float16)
+    oracle.lib().tto_interleaved_swiglu(P(gu), P(want2), oracle.F16, 4, 2880, 1.702, 7.0)
+    assert_bits_equal(from_torch_bits(out2).reshape(-1), want2.reshape(-1), "interleaved_swiglu")
+
+    ex = f16_normal(g, (4, 2880))
+    sc = np.array([0.5, 0.25, 0.125, 0.125], dtype=np.float16)
+    out3 = torch.empty(2880, device=device, dtype=torch.float16)
+    backend.weighted_expert_sum(to_torch(ex, device), to_torch(sc, device), out3)
+    want3 = np.empty(2880, dtype=np.float16)
+    oracle.lib().tto_weighted_expert_sum(P(ex), oracle.F16, P(sc), oracle.F16, P(want3), 2880, 4)
+    assert_bits_equal(from_torch_bits(out3), want3, "weighted_expert_sum")
+
+    out4 = torch.empty(n, device=device, dtype=torch.float16)
+    backend.add(to_torch(gt, device), to_torch(up, device), out4)
+    assert_bits_equal(from_torch_bits(out4), (gt.astype(np.float32) + up.astype(np.float32)).astype(np.float16), "add")
+
+
+def test_rope_table_and_device_position(backend, device):
+    heads, kv_heads, D = 32, 8, 64
+    g = rng(4)
+    positions = 600
+    inv = (500000.0 ** (-np.arange(0, D, 2, dtype=np.float32) / D)).astype(np.float32)
+    ang = np.arange(positions, dtype=np.float32)[:, None] * inv[None, :]
+    cos = np.cos(ang).astype(np.float16)
+    sin = np.sin(ang).astype(np.float16)
+    q = f16_normal(g, heads * D)
+    k = f16_normal(g, kv_heads * D)
+    pos = torch.tensor([517], dtype=torch.int32, device=device)
+    q_t, k_t = to_torch(q, device), to_torch(k, device)
+    backend.rope_qk_inplace(q_t, k_t, to_torch(cos, device), to_torch(sin, device), heads, kv_heads, D, position=pos)
+    qw, kw = q.copy(), k.copy()
+    oracle.lib().tto_rope(P(qw), P(kw), oracle.F16, P(cos[517]), P(sin[517]), heads, kv_heads, D)
+    assert_bits_equal(from_torch_bits(q_t), qw, "rope q")
+    assert_bits_equal(from_torch_bits(k_t), kw, "rope k")
+
+
+@pytest.mark.parametrize("heads,kv_heads,tokens,sinks", [(32, 8, 513, False), (64, 8, 1025, True), (8, 8, 5, False),
+                                                         (32, 8, 64, True)])
+def test_gqa_attention(backend, device, heads, kv_heads, tokens, sinks):
+    D, cap = 64, 1100
+    g = rng(heads + tokens)
+    q = f16_normal(g, heads * D)
+    keys = f16_normal(g, (kv_heads, cap, D))
+    vals = f16_normal(g, (kv_heads, cap, D))
+    sk = f16_normal(g, heads) if sinks else None
+    out = torch.empty(heads * D, device=device, dtype=torch.float16)
+    tok = torch.tensor([tokens], dtype=torch.int32, device=device)
+    backend.single_token_gqa_attention(to_torch(q, device), to_torch(keys, device), to_torch(vals, device), out, heads,
+                                       kv_heads, D, sinks=to_torch(sk, device) if sinks else None, active_tokens=tok)
+    want = np.empty(heads * D, dtype=np.float16)
+    oracle.lib().tto_attention(P(q), P(keys), P(vals), oracle.F16, cap * D, D, cap * D, D, P(sk) if sinks else None,
+                               oracle.F16, tokens, heads, kv_heads, D, P(want))
+    assert_bits_equal(from_torch_bits(out), want, "attention")
+
+
+@pytest.mark.parametrize("renorm,with_bias", [(True, True), (False, False)])
+def test_router(backend, device, renorm, with_bias):
+    E, H, k = 32, 2880, 4
+    g = rng(7 + renorm)
+    w = f16_normal(g, (E, H), 0.02)
+    x = f16_normal(g, H)
+    b = f16_normal(g, E, 0.1) if with_bias else None
+    idx = torch.empty(k, device=device, dtype=torch.int32)
+    sc = torch.empty(k, device=device, dtype=torch.float16)
+    backend.moe_router_matvec_topk(to_torch(w, device), to_torch(x, device), idx, sc,
+                                   bias=to_torch(b, device) if with_bias else None, renormalize=renorm)
+    widx = np.empty(k, dtype=np.int32)
+    wsc = np.empty(k, dtype=np.float16)
+    oracle.lib().tto_router(P(w), oracle.F16, H, P(x), oracle.F16, H, P(b) if with_bias else None, oracle.F16, E, k,
+                            int(renorm), P(widx), P(wsc), oracle.F16)
+    assert np.array_equal(idx.cpu().numpy(), widx)
+    assert_bits_equal(from_torch_bits(sc), wsc, "router scores")
+
+
+def test_router_topk_on_logits_with_ties(backend, device):
+    lg = np.array([1.0, 3.0, 3.0, -2.0, 3.0, 0.5, 2.0, 2.0], dtype=np.float16)
+    idx = torch.empty(4, device=device, dtype=torch.int32)
+    sc = torch.empty(4, device=device, dtype=torch.float16)
+    backend.moe_router_topk(to_torch(lg, device), idx, sc, renormalize=True)
+    assert idx.cpu().tolist() == [1, 2, 4, 6]  # equal logits: lowest index first
+    widx = np.empty(4, dtype=np.int32)
+    wsc = np.empty(4, dtype=np.float16)
+    oracle.lib().tto_topk(P(lg), oracle.F16, 8, 4, 1, P(widx), P(wsc), oracle.F16)
+    assert_bits_equal(from_torch_bits(sc), wsc, "topk scores")
+
+
+@pytest.mark.parametrize("rows,cols", [(128256, 2048), (201088, 2880), (4099, 5120)])
+def test_lm_head_argmax(backend, device, rows, cols):
+    g = rng(rows)
+    w = f16_normal(g, (rows, cols), 0.02)
+    x = f16_normal(g, cols)
+    w_t = to_torch(w, device)
+    tok = backend.matvec_argmax_tensor(w_t, to_torch(x, device))
+    logits = from_torch_bits(backend.logits_buffer(rows, torch.float16))
+    want_logits = oracle.gemv("f16w", "none", w.view(np.uint8).reshape(rows, -1), None, x, cols=cols, lpr=lanes(cols))
+    assert_bits_equal(logits, want_logits, "lm_head logits")
+    want = int(np.argmax(want_logits.astype(np.float32)))
+    assert int(tok.item()) == want == int(oracle.lib().tto_argmax(P(want_logits), oracle.F16, rows))
+
+
+def test_argmax_ties_pick_lowest_index(backend, device):
+    rows, cols = 5000, 64
+    w = np.zeros((rows, cols), dtype=np.float16)
+    w[[17, 3001, 4999], 0] = 1.0   # three identical maxima
+    x = np.zeros(cols, dtype=np.float16)
+    x[0] = 2.0
+    tok = backend.matvec_argmax_tensor(to_torch(w, device), to_torch(x, device))
+    assert int(tok.item()) == 17

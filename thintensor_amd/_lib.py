@@ -41,8 +41,25 @@ SIGNATURES: dict[str, list] = {
                                      _L, _P],
     "tt_lowbit_affine_matvec": [_P, _L, _P, _L, _L, _I, _P, _I, _P, _I, _L, _L, _L, _P],
     "tt_int4_selected_matvec": [_P, _L, _L, _P, _I, _L, _L, _L, _P, _I, _L, _P, _L, _P, _I, _L, _L, _L, _L, _P],
+    "tt_matvec_argmax_partials": [_L, _L],
+    "tt_matvec_argmax": [_P, _I, _L, _P, _I, _P, _I, _L, _L, _P, _L, _P, _P, _P],
+    "tt_rms_norm": [_P, _I, _P, _I, _P, _I, _L, _F, _F, _P],
+    "tt_add_rms_norm": [_P, _P, _P, _I, _P, _I, _P, _I, _L, _F, _P],
+    "tt_add": [_P, _P, _P, _I, _L, _P],
+    "tt_silu_mul": [_P, _P, _P, _I, _L, _P],
+    "tt_interleaved_swiglu": [_P, _L, _P, _L, _I, _L, _L, _F, _F, _P],
+    "tt_weighted_expert_sum": [_P, _I, _L, _L, _P, _I, _P, _L, _P],
+    "tt_rope_qk_inplace": [_P, _P, _I, _P, _P, _L, _P, _L, _L, _L, _L, _P],
+    "tt_embedding": [_P, _L, _P, _L, _P, _L, _P],
+    "tt_kv_append": [_P, _P, _P, _P, _L, _L, _P, _L, _L, _L, _P],
+    "tt_advance_position": [_P, ctypes.c_int32, _P],
+    "tt_attention_scratch_floats": [_L, _L, _L],
+    "tt_single_token_gqa_attention": [_P, _P, _P, _I, _L, _L, _L, _L, _P, _I, _P, _L, _L, _L, _L, _L, _P, _L, _P,
+                                      _P],
+    "tt_moe_router_matvec_topk": [_P, _I, _L, _P, _I, _L, _P, _I, _L, _L, _I, _P, _P, _I, _P],
+    "tt_moe_router_topk": [_P, _I, _L, _L, _I, _P, _P, _I, _P],
 }
-_RESTYPES = {"tt_last_error": ctypes.c_char_p}
+_RESTYPES = {"tt_last_error": ctypes.c_char_p, "tt_matvec_argmax_partials": ctypes.c_int64}
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

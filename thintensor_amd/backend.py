@@ -513,3 +513,257 @@ class HipDecodeBackend:
         )
         _lib.check(rc, "lowbit_affine_matvec")
         return out
+
+    # ------------------------------------------------------------ lm_head + greedy argmax
+    def _argmax_scratch(self, rows: int, cols: int) -> torch.Tensor:
+        need = int(self.lib.tt_matvec_argmax_partials(rows, cols))
+        if self._argmax_partials is None or self._argmax_partials.numel() < need:
+            self._argmax_partials = torch.empty(need, device=self.device, dtype=torch.int64)
+        return self._argmax_partials
+
+    def _matvec_argmax(self, weight: torch.Tensor, x: torch.Tensor, logits: torch.Tensor | None) -> torch.Tensor:
+        _require_cuda(weight, x)
+        rows, cols = int(weight.shape[0]), int(weight.shape[1])
+        if weight.stride(1) != 1 or x.numel() != cols:
+            raise ValueError("matvec_argmax shape mismatch")
+        partials = self._argmax_scratch(rows, cols)
+        rc = self.lib.tt_matvec_argmax(
+            weight.data_ptr(), _code(weight, "matvec_argmax"), weight.stride(0), x.data_ptr(), _code(x, "matvec_argmax"),
+            logits.data_ptr() if logits is not None else None, _code(logits, "logits") if logits is not None else _code(x, "x"),
+            rows, cols, partials.data_ptr(), partials.numel(), self._argmax_out_idx.data_ptr(),
+            self._argmax_out_val.data_ptr(), _stream(x),
+        )
+        _lib.check(rc, "matvec_argmax")
+        return self._argmax_out_idx
+
+    def matvec_argmax_tensor(
+        self,
+        weight: torch.Tensor,
+        x: torch.Tensor,
+        *,
+        block_m: int | None = None,
+        num_warps: int | None = None,
+        config_name: str | None = None,
+    ) -> torch.Tensor:
+        """Greedy lm_head: first index of the maximum logit rounded to x's dtype
+        (triton_kernels.py:5365-5398).  Logits are also written to ``logits_buffer``.
+        Returns a 0-d int64 device tensor that later calls overwrite."""
+        logits = self.logits_buffer(int(weight.shape[0]), x.dtype)
+        return self._matvec_argmax(weight, x, logits)
+
+    def _matvec_argmax_tensor_triton_two_stage(self, weight: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+        """The reference's two-stage mode argmaxes unrounded fp32 logits; this backend
+        keeps one semantic (rounded logits, first index) for every mode."""
+        return self._matvec_argmax(weight, x, None)
+
+    def persistent_vocab_block_matvec_argmax_tensor(self, weight: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+        return self._matvec_argmax(weight, x, None)
+
+    def matvec_argmax(self, weight: torch.Tensor, x: torch.Tensor) -> int:
+        raise RuntimeError("matvec_argmax() synchronizes CUDA; use matvec_argmax_tensor()")
+
+    # ------------------------------------------------------------ norms / elementwise
+    def rms_norm(self, x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor, eps: float,
+                 weight_offset: float = 0.0) -> torch.Tensor:
+        """(triton_kernels.py:5632-5644)"""
+        _require_cuda(x, weight, out)
+        n = x.numel()
+        if weight.numel() != n or out.numel() != n:
+            raise ValueError("rms_norm size mismatch")
+        rc = self.lib.tt_rms_norm(x.data_ptr(), _code(x, "rms_norm"), weight.data_ptr(), _code(weight, "rms_norm"),
+                                  out.data_ptr(), _code(out, "rms_norm"), n, float(eps), float(weight_offset), _stream(x))
+        _lib.check(rc, "rms_norm")
+        return out
+
+    def add_rms_norm(self, left: torch.Tensor, right: torch.Tensor, residual_out: torch.Tensor, weight: torch.Tensor,
+                     norm_out: torch.Tensor, eps: float) -> tuple[torch.Tensor, torch.Tensor]:
+        """(triton_kernels.py:5646-5667)"""
+        _require_cuda(left, right, residual_out, weight, norm_out)
+        n = left.numel()
+        if any(t.numel() != n for t in (right, residual_out, weight, norm_out)):
+            raise ValueError("add_rms_norm size mismatch")
+        if right.dtype != left.dtype or residual_out.dtype != left.dtype:
+            raise ValueError("add_rms_norm: left, right and residual_out must share a dtype")
+        rc = self.lib.tt_add_rms_norm(left.data_ptr(), right.data_ptr(), residual_out.data_ptr(), _code(left, "add_rms_norm"),
+                                      weight.data_ptr(), _code(weight, "add_rms_norm"), norm_out.data_ptr(),
+                                      _code(norm_out, "add_rms_norm"), n, float(eps), _stream(left))
+        _lib.check(rc, "add_rms_norm")
+        return residual_out, norm_out
+
+    def add(self, left: torch.Tensor, right: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+        _require_cuda(left, right, out)
+        rc = self.lib.tt_add(left.data_ptr(), right.data_ptr(), out.data_ptr(), _code(out, "add"), left.numel(), _stream(out))
+        _lib.check(rc, "add")
+        return out
+
+    def silu_mul(self, gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+        _require_cuda(gate, up, out)
+        rc = self.lib.tt_silu_mul(gate.data_ptr(), up.data_ptr(), out.data_ptr(), _code(out, "silu_mul"), gate.numel(),
+                                  _stream(out))
+        _lib.check(rc, "silu_mul")
+        return out
+
+    def interleaved_swiglu(self, gate_up: torch.Tensor, out: torch.Tensor, *, alpha: float, limit: float) -> torch.Tensor:
+        """gpt-oss SwiGLU on interleaved gate/up (triton_kernels.py:5764-5782)."""
+        _require_cuda(gate_up, out)
+        rows = int(gate_up.shape[0]) if gate_up.ndim == 2 else 1
+        n = int(out.shape[-1])
+        in_row = gate_up.stride(0) if gate_up.ndim == 2 else 0
+        out_row = out.stride(0) if out.ndim == 2 else 0
+        rc = self.lib.tt_interleaved_swiglu(gate_up.data_ptr(), in_row, out.data_ptr(), out_row, _code(out, "swiglu"),
+                                            rows, n, float(alpha), float(limit), _stream(out))
+        _lib.check(rc, "interleaved_swiglu")
+        return out
+
+    def weighted_expert_sum(self, experts: torch.Tensor, scores: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+        """(triton_kernels.py:5784-5801)"""
+        _require_cuda(experts, scores, out)
+        rc = self.lib.tt_weighted_expert_sum(experts.data_ptr(), _code(experts, "weighted_expert_sum"), experts.stride(0),
+                                             int(experts.shape[0]), scores.data_ptr(), _code(scores, "scores"),
+                                             out.data_ptr(), int(experts.shape[1]), _stream(out))
+        _lib.check(rc, "weighted_expert_sum")
+        return out
+
+    def rope_qk_inplace(self, q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, heads: int,
+                        kv_heads: int, head_dim: int, *, position: torch.Tensor | int | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+        """RoPE in place (triton_kernels.py:5689-5714).  ``cos``/``sin`` are either the
+        row for the current token ([head_dim/2]) or a full table [positions,
+        head_dim/2] indexed by ``position`` (an int or a 0-d int32 device tensor)."""
+        if head_dim % 2:
+            raise ValueError(f"RoPE head_dim must be even, got {head_dim}")
+        _require_cuda(q, k, cos, sin)
+        if cos.ndim == 1:
+            table_row, pos_dev, pos = 0, None, 0
+        else:
+            table_row = cos.stride(0)
+            if isinstance(position, torch.Tensor):
+                if position.dtype != torch.int32:
+                    raise ValueError("device position must be int32")
+                pos_dev, pos = position.data_ptr(), 0
+            else:
+                pos_dev, pos = None, int(position or 0)
+        rc = self.lib.tt_rope_qk_inplace(q.data_ptr(), k.data_ptr(), _code(q, "rope"), cos.data_ptr(), sin.data_ptr(),
+                                         table_row, pos_dev, pos, heads, kv_heads, head_dim, _stream(q))
+        _lib.check(rc, "rope_qk_inplace")
+        return q, k
+
+    # ------------------------------------------------------------ attention
+    def _attention_scratch(self, heads: int, max_tokens: int, head_dim: int) -> torch.Tensor:
+        need = int(self.lib.tt_attention_scratch_floats(heads, max_tokens, head_dim))
+        if self._attention_partials is None or self._attention_partials.numel() < need:
+            self._attention_partials = torch.empty(need, device=self.device, dtype=torch.float32)
+        return self._attention_partials
+
+    def single_token_gqa_attention(
+        self,
+        query: torch.Tensor,
+        keys: torch.Tensor,
+        values: torch.Tensor,
+        out: torch.Tensor,
+        heads: int,
+        kv_heads: int,
+        head_dim: int,
+        sinks: torch.Tensor | None = None,
+        active_tokens: torch.Tensor | int | None = None,
+    ) -> torch.Tensor:
+        """Decode attention over keys/values [kv_heads, tokens, head_dim]
+        (triton_kernels.py:5228-5278).  ``active_tokens`` may be an int32 device
+        scalar; the KV tensors then give the capacity."""
+        capacity = int(keys.shape[1])
+        tokens = capacity if active_tokens is None else active_tokens
+        if isinstance(tokens, int) and tokens <= 0:
+            raise ValueError("attention requires at least one KV token")
+        if head_dim > 256:
+            raise ValueError("fused single-token attention supports head_dim <= 256")
+        _require_cuda(query, keys, values, out)
+        scratch = self._attention_scratch(heads, capacity, head_dim)
+        tok_dev = tokens.data_ptr() if isinstance(tokens, torch.Tensor) else None
+        if isinstance(tokens, torch.Tensor) and tokens.dtype != torch.int32:
+            raise ValueError("active_tokens device tensor must be int32")
+        rc = self.lib.tt_single_token_gqa_attention(
+            query.data_ptr(), keys.data_ptr(), values.data_ptr(), _code(keys, "attention"), keys.stride(0), keys.stride(1),
+            values.stride(0), values.stride(1), sinks.data_ptr() if sinks is not None else None,
+            _code(sinks, "sinks") if sinks is not None else _lib.F16, tok_dev,
+            tokens if isinstance(tokens, int) else 0, capacity, heads, kv_heads, head_dim, scratch.data_ptr(),
+            scratch.numel(), out.data_ptr(), _stream(out),
+        )
+        _lib.check(rc, "single_token_gqa_attention")
+        return out
+
+    def split_single_token_gqa_attention(self, query, keys, values, out, heads, kv_heads, head_dim):
+        """Split-KV attention (triton_kernels.py:5280-5363): the HIP kernel always splits
+        the sequence into 64-token chunks."""
+        return self.single_token_gqa_attention(query, keys, values, out, heads, kv_heads, head_dim)
+
+    # ------------------------------------------------------------ router
+    def moe_router_matvec_topk(
+        self,
+        weight: torch.Tensor,
+        hidden: torch.Tensor,
+        indices_out: torch.Tensor,
+        scores_out: torch.Tensor,
+        *,
+        bias: torch.Tensor | None = None,
+        renormalize: bool,
+    ) -> tuple[torch.Tensor, torch.Tensor]:
+        """(triton_kernels.py:5826-5860)"""
+        experts, hidden_size = map(int, weight.shape)
+        if hidden.ndim != 1 or int(hidden.numel()) != hidden_size:
+            raise ValueError("router hidden vector does not match weight shape")
+        if experts > 128:
+            raise ValueError("fused router supports at most 128 experts")
+        if bias is not None and int(bias.numel()) != experts:
+            raise ValueError("router bias does not match expert count")
+        self._check_indices(indices_out)
+        _require_cuda(weight, hidden, indices_out, scores_out)
+        rc = self.lib.tt_moe_router_matvec_topk(
+            weight.data_ptr(), _code(weight, "router"), weight.stride(0), hidden.data_ptr(), _code(hidden, "router"),
+            hidden_size, bias.data_ptr() if bias is not None else None, _code(bias, "bias") if bias is not None else _lib.F32,
+            experts, int(indices_out.numel()), int(bool(renormalize)), indices_out.data_ptr(), scores_out.data_ptr(),
+            _code(scores_out, "scores"), _stream(hidden),
+        )
+        _lib.check(rc, "moe_router_matvec_topk")
+        return indices_out, scores_out
+
+    def moe_router_topk(self, logits: torch.Tensor, indices_out: torch.Tensor, scores_out: torch.Tensor, *,
+                        renormalize: bool) -> tuple[torch.Tensor, torch.Tensor]:
+        """(triton_kernels.py:5803-5824)"""
+        self._check_indices(indices_out)
+        _require_cuda(logits, indices_out, scores_out)
+        rc = self.lib.tt_moe_router_topk(logits.data_ptr(), _code(logits, "logits"), int(logits.numel()),
+                                         int(indices_out.numel()), int(bool(renormalize)), indices_out.data_ptr(),
+                                         scores_out.data_ptr(), _code(scores_out, "scores"), _stream(logits))
+        _lib.check(rc, "moe_router_topk")
+        return indices_out, scores_out
+
+    # ------------------------------------------------------------ decode-step helpers (no reference counterpart)
+    def embedding(self, embed: torch.Tensor, token: torch.Tensor | int, out: torch.Tensor) -> torch.Tensor:
+        """out = embed[token]; a device token (0-d/1-element int64) is read on the GPU."""
+        _require_cuda(embed, out)
+        if isinstance(token, torch.Tensor):
+            if token.dtype != torch.int64:
+                raise ValueError("device token id must be int64")
+            tok_dev, tok = token.data_ptr(), 0
+        else:
+            tok_dev, tok = None, int(token)
+        rc = self.lib.tt_embedding(embed.data_ptr(), embed.stride(0), tok_dev, tok, out.data_ptr(), out.numel(), _stream(out))
+        _lib.check(rc, "embedding")
+        return out
+
+    def kv_append(self, k: torch.Tensor, v: torch.Tensor, keys: torch.Tensor, values: torch.Tensor,
+                  position: torch.Tensor | int, kv_heads: int, head_dim: int) -> None:
+        """keys/values [kv_heads, capacity, head_dim]: write token `position`."""
+        _require_cuda(k, v, keys, values)
+        if keys.stride() != values.stride():
+            raise ValueError("keys and values must share a layout")
+        if isinstance(position, torch.Tensor):
+            pos_dev, pos = position.data_ptr(), 0
+        else:
+            pos_dev, pos = None, int(position)
+        rc = self.lib.tt_kv_append(k.data_ptr(), v.data_ptr(), keys.data_ptr(), values.data_ptr(), keys.stride(0),
+                                   keys.stride(1), pos_dev, pos, kv_heads, head_dim, _stream(k))
+        _lib.check(rc, "kv_append")
+
+    def advance_position(self, position: torch.Tensor, step: int = 1) -> None:
+        rc = self.lib.tt_advance_position(position.data_ptr(), int(step), _stream(position))
+        _lib.check(rc, "advance_position")

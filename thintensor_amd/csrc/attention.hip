@@ -1,0 +1,193 @@
+// Single-token GQA decode attention (fp16/bf16 KV) for gfx950, split over the KV
+// sequence.  Semantics follow the reference kernel (triton_kernels.py:15-109):
+// softmax(q.k * head_dim^-0.5) v in binary32 with an optional per-head sink that
+// joins the softmax denominator but carries no value.
+//
+// Order of evaluation (restated in oracle/tt_oracle.c):
+//   * the KV sequence is cut into chunks of 64 tokens; one wave handles one
+//     (kv_head, chunk) for all query heads of that KV head;
+//   * score_t = (fma chain over d ascending of q_d k_td) * scale;
+//   * chunk max m_c (order free), p_t = exp(score_t - m_c), l_c = butterfly sum of p
+//     over the 64 token lanes, o_c[d] = fma chain over the chunk's tokens ascending;
+//   * combine in chunk order: M = max(sink, m_c...), den starts at exp(sink - M)
+//     (or 0), den = fma(l_c, e_c, den), acc_d = fma(o_c[d], e_c, acc_d) with
+//     e_c = exp(m_c - M); out_d = acc_d / den.
+// The active token count may be read from device memory so graph replays follow
+// the growing cache; chunks past it exit without work.
+#include "tt_abi_internal.h"
+#include "tt_common.h"
+
+namespace tt {
+
+constexpr int kChunk = 64;
+
+struct AttnParams {
+  const void* q;          // [heads, D]
+  const void* keys;       // [kv_heads, tokens, D] with strides
+  const void* values;
+  int64_t k_head, k_tok, v_head, v_tok;
+  const void* sinks;      // [heads] or null
+  const int32_t* tokens_dev;
+  int tokens;
+  float* part_m;          // [heads, max_chunks]
+  float* part_l;
+  float* part_o;          // [heads, max_chunks, D]
+  int heads, kv_heads, head_dim, max_chunks;
+  float scale;
+  void* out;              // [heads, D]
+};
+
+template <typename T, int G>
+__global__ __launch_bounds__(64) void attn_partial_kernel(AttnParams P) {
+  const int kvh = blockIdx.y;
+  const int c = blockIdx.x;
+  const int T_act = P.tokens_dev ? P.tokens_dev[0] : P.tokens;
+  if (c * kChunk >= T_act) return;
+  const int D = P.head_dim;
+  const int lane = threadIdx.x;
+  __shared__ float q_s[G * 256];
+  __shared__ float p_s[G * kChunk];
+  const int h0 = kvh * G;
+  for (int i = lane; i < G * D; i += 64) q_s[i] = to_f32(reinterpret_cast<const T*>(P.q)[(int64_t)h0 * D + i]);
+  __syncthreads();
+  // phase 1: lane = token
+  const int t = c * kChunk + lane;
+  const bool valid = t < T_act;
+  const T* krow = reinterpret_cast<const T*>(P.keys) + kvh * P.k_head + (int64_t)(valid ? t : 0) * P.k_tok;
+  float sc[G];
+#pragma unroll
+  for (int g = 0; g < G; g++) sc[g] = 0.0f;
+  for (int d = 0; d < D; d++) {
+    const float kv = to_f32(krow[d]);
+#pragma unroll
+    for (int g = 0; g < G; g++) sc[g] = __builtin_fmaf(q_s[g * D + d], kv, sc[g]);
+  }
+  const float ninf = __builtin_bit_cast(float, 0xff800000u);
+#pragma unroll
+  for (int g = 0; g < G; g++) {
+    float s = valid ? sc[g] * P.scale : ninf;
+    float m = s;
+    // chunk max (order-independent)
+    m = fmaxf(m, xor_partner<1>(m));
+    m = fmaxf(m, xor_partner<2>(m));
+    m = fmaxf(m, xor_partner<4>(m));
+    m = fmaxf(m, xor_partner<8>(m));
+    m = fmaxf(m, xor_partner<16>(m));
+    m = fmaxf(m, xor_partner<32>(m));
+    const float p = valid ? exp_f32(s - m) : 0.0f;
+    const float l = xor_sum(p, 1, 64);
+    p_s[g * kChunk + lane] = p;
+    if (lane == 0) {
+      P.part_m[(int64_t)(h0 + g) * P.max_chunks + c] = m;
+      P.part_l[(int64_t)(h0 + g) * P.max_chunks + c] = l;
+    }
+  }
+  __syncthreads();
+  // phase 2: lane = dimension
+  const int nt = min(kChunk, T_act - c * kChunk);
+  for (int d = lane; d < D; d += 64) {
+    float o[G];
+#pragma unroll
+    for (int g = 0; g < G; g++) o[g] = 0.0f;
+    const T* vcol = reinterpret_cast<const T*>(P.values) + kvh * P.v_head + (int64_t)(c * kChunk) * P.v_tok + d;
+    for (int tt = 0; tt < nt; tt++) {
+      const float vv = to_f32(vcol[(int64_t)tt * P.v_tok]);
+#pragma unroll
+      for (int g = 0; g < G; g++) o[g] = __builtin_fmaf(p_s[g * kChunk + tt], vv, o[g]);
+    }
+#pragma unroll
+    for (int g = 0; g < G; g++) P.part_o[((int64_t)(h0 + g) * P.max_chunks + c) * D + d] = o[g];
+  }
+}
+
+template <typename T, typename SKT>
+__global__ __launch_bounds__(64) void attn_combine_kernel(AttnParams P) {
+  const int h = blockIdx.x;
+  const int T_act = P.tokens_dev ? P.tokens_dev[0] : P.tokens;
+  const int nc = (T_act + kChunk - 1) / kChunk;
+  const float* pm = P.part_m + (int64_t)h * P.max_chunks;
+  const float* pl = P.part_l + (int64_t)h * P.max_chunks;
+  float M = __builtin_bit_cast(float, 0xff800000u);
+  const bool has_sink = P.sinks != nullptr;
+  float sink = 0.0f;
+  if (has_sink) {
+    sink = to_f32(reinterpret_cast<const SKT*>(P.sinks)[h]);
+    M = sink;
+  }
+  for (int c = 0; c < nc; c++) M = fmaxf(M, pm[c]);
+  float den = has_sink ? exp_f32(sink - M) : 0.0f;
+  for (int c = 0; c < nc; c++) den = __builtin_fmaf(pl[c], exp_f32(pm[c] - M), den);
+  for (int d = threadIdx.x; d < P.head_dim; d += 64) {
+    float acc = 0.0f;
+    for (int c = 0; c < nc; c++)
+      acc = __builtin_fmaf(P.part_o[((int64_t)h * P.max_chunks + c) * P.head_dim + d], exp_f32(pm[c] - M), acc);
+    store<T>(reinterpret_cast<T*>(P.out) + (int64_t)h * P.head_dim + d, acc / den);
+  }
+}
+
+template <typename T, int G>
+static int launch_attn(const AttnParams& P, int sink_dtype, hipStream_t st) {
+  hipLaunchKernelGGL((attn_partial_kernel<T, G>), dim3(P.max_chunks, P.kv_heads), dim3(64), 0, st, P);
+  int rc = check_launch("gqa_attention");
+  if (rc) return rc;
+  switch (sink_dtype) {
+    case TT_BF16: hipLaunchKernelGGL((attn_combine_kernel<T, bf16_t>), dim3(P.heads), dim3(64), 0, st, P); break;
+    case TT_F32: hipLaunchKernelGGL((attn_combine_kernel<T, float>), dim3(P.heads), dim3(64), 0, st, P); break;
+    default: hipLaunchKernelGGL((attn_combine_kernel<T, f16_t>), dim3(P.heads), dim3(64), 0, st, P); break;
+  }
+  return check_launch("gqa_attention");
+}
+
+}  // namespace tt
+
+using namespace tt;
+
+extern "C" int tt_attention_scratch_floats(int64_t heads, int64_t max_tokens, int64_t head_dim) {
+  const int64_t chunks = (max_tokens + kChunk - 1) / kChunk;
+  return (int)(heads * chunks * (2 + head_dim));
+}
+
+extern "C" int tt_single_token_gqa_attention(const void* q, const void* keys, const void* values, int dtype,
+                                             int64_t k_head, int64_t k_tok, int64_t v_head, int64_t v_tok,
+                                             const void* sinks, int sink_dtype, const int32_t* tokens_dev,
+                                             int64_t tokens, int64_t max_tokens, int64_t heads, int64_t kv_heads,
+                                             int64_t head_dim, float* scratch, int64_t scratch_floats, void* out,
+                                             void* stream) {
+  const char* what = "single_token_gqa_attention";
+  TT_REQUIRE(q && keys && values && out && scratch, "%s: null pointer", what);
+  TT_REQUIRE(head_dim > 0 && head_dim <= 256, "%s: fused single-token attention supports head_dim <= 256", what);
+  TT_REQUIRE(heads > 0 && kv_heads > 0 && heads % kv_heads == 0, "%s: heads must be a multiple of kv_heads", what);
+  TT_REQUIRE(tokens_dev != nullptr || (tokens > 0 && tokens <= max_tokens), "%s: attention requires at least one KV token", what);
+  TT_REQUIRE(max_tokens > 0, "%s: bad max_tokens", what);
+  const int64_t chunks = (max_tokens + kChunk - 1) / kChunk;
+  TT_REQUIRE(scratch_floats >= heads * chunks * (2 + head_dim), "%s: scratch too small", what);
+  TT_REQUIRE(chunks <= 65535 && kv_heads <= 65535, "%s: sequence too long", what);
+  AttnParams P{};
+  P.q = q; P.keys = keys; P.values = values;
+  P.k_head = k_head; P.k_tok = k_tok; P.v_head = v_head; P.v_tok = v_tok;
+  P.sinks = sinks; P.tokens_dev = tokens_dev; P.tokens = (int)tokens;
+  P.part_m = scratch;
+  P.part_l = scratch + heads * chunks;
+  P.part_o = scratch + 2 * heads * chunks;
+  P.heads = (int)heads; P.kv_heads = (int)kv_heads; P.head_dim = (int)head_dim; P.max_chunks = (int)chunks;
+  P.scale = (float)(1.0 / __builtin_sqrt((double)head_dim));
+  P.out = out;
+  const int G = (int)(heads / kv_heads);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  auto by_g = [&](auto t) -> int {
+    using T = decltype(t);
+    switch (G) {
+      case 1: return launch_attn<T, 1>(P, sink_dtype, st);
+      case 2: return launch_attn<T, 2>(P, sink_dtype, st);
+      case 4: return launch_attn<T, 4>(P, sink_dtype, st);
+      case 8: return launch_attn<T, 8>(P, sink_dtype, st);
+      case 16: return launch_attn<T, 16>(P, sink_dtype, st);
+    }
+    set_error("%s: query heads per KV head must be 1, 2, 4, 8 or 16 (got %d)", what, G);
+    return TT_ERR_UNSUPPORTED;
+  };
+  if (dtype == TT_F16) return by_g(f16_t{});
+  if (dtype == TT_BF16) return by_g(bf16_t{});
+  set_error("%s: KV dtype must be fp16 or bf16", what);
+  return TT_ERR_INVALID;
+}

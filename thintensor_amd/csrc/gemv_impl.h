@@ -1,0 +1,412 @@
+// Dequant-fused GEMV kernels (dense, multi-matrix and selected-expert) for gfx950.
+//
+// Design (memory-bound regime):
+//   * packed weights stream from HBM with 128-bit (or 64/32-bit for q2/q1 chunks)
+//     coalesced loads: a wave reads LPR consecutive chunks of one row per round;
+//   * the activation vector is staged once per workgroup in LDS and each lane keeps
+//     its 32-element slice in registers for ROWS rows at a time;
+//   * unpacking happens in registers (magic-number fp16 construction, exact), the
+//     multiply-accumulate is an IEEE fp32 fma chain (v_fma_mix_f32 for fp16 inputs);
+//   * rows are reduced with wave-level butterflies; per-group scales are applied to
+//     the group sums, as the reference does (triton_kernels.py:1628-1651).
+// The reduction order is documented in tt_gemv.h and restated in oracle/.
+#pragma once
+
+#include "tt_abi_internal.h"
+#include "tt_gemv.h"
+
+namespace tt {
+
+enum class SMode : int { kNone = 0, kRow = 1, kGroup = 2, kGroupAff = 3, kBlockE8 = 4 };
+
+struct Seg {
+  const uint8_t* w;     // weight bytes of expert 0 / the matrix
+  int64_t w_row;        // bytes between rows
+  const void* s;        // scales
+  int64_t s_row, s_grp; // scale element strides
+  void* out;            // output (slot 0)
+  int rows;
+  int vbegin;           // first virtual row (batches never straddle segments)
+};
+
+struct GemvParams {
+  Seg seg[3];
+  int nseg;
+  int vtotal;              // virtual rows (segments padded to whole batches)
+  const void* x;
+  int64_t x_slot;          // activation elements between slots (0: shared vector)
+  const int32_t* experts;  // expert id per slot (nullptr: dense)
+  int64_t w_expert;        // bytes between experts
+  int64_t s_expert;        // scale elements between experts
+  int64_t out_slot;        // output elements between slots
+  int64_t s_pair;          // affine: element offset of the second scale value
+  int aff_zero;            // affine pair holds (s, z) instead of (s, m)
+  int cols;
+  int e8_extra;            // extra power of two folded into E8M0 block scales
+  uint64_t* am_partials;   // argmax epilogue: one key per wave (null: plain GEMV)
+};
+
+// Order-preserving argmax key of a rounded logit at row `idx`: larger value wins,
+// equal values (+0 == -0) go to the lower index, NaN beats every number (first NaN
+// wins), matching torch.argmax on the rounded logits.
+__device__ __forceinline__ uint64_t argmax_key(float v, uint32_t idx) {
+  uint32_t b = __builtin_bit_cast(uint32_t, v);
+  if ((b & 0x7fffffffu) == 0) b = 0;
+  uint32_t o;
+  if ((b & 0x7fffffffu) > 0x7f800000u) o = 0xffffffffu;
+  else o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  return ((uint64_t)o << 32) | (uint64_t)(0xffffffffu - idx);
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t k) {
+#define TT_MAXSTEP(M)                                                                                     \
+  {                                                                                                       \
+    const uint32_t hi = __builtin_bit_cast(uint32_t, xor_partner<M>(__builtin_bit_cast(float, (uint32_t)(k >> 32)))); \
+    const uint32_t lo = __builtin_bit_cast(uint32_t, xor_partner<M>(__builtin_bit_cast(float, (uint32_t)k)));         \
+    const uint64_t o = ((uint64_t)hi << 32) | lo;                                                         \
+    k = o > k ? o : k;                                                                                    \
+  }
+  TT_MAXSTEP(1) TT_MAXSTEP(2) TT_MAXSTEP(4) TT_MAXSTEP(8) TT_MAXSTEP(16) TT_MAXSTEP(32)
+#undef TT_MAXSTEP
+  return k;
+}
+
+constexpr int log2c(int v) { return v <= 1 ? 0 : 1 + log2c(v / 2); }
+
+// Reduce per-lane values v[0..NV) over lane bits [M, MEND): reduce-scatter levels
+// while more than one value is left, plain butterfly levels afterwards.
+template <int NV, int M, int MEND>
+__device__ __forceinline__ void reduce_range(float* v) {
+  if constexpr (M < MEND) {
+    if constexpr (NV > 1) {
+      float t[NV / 2];
+      rs_level<NV, M>(v, t);
+#pragma unroll
+      for (int i = 0; i < NV / 2; i++) v[i] = t[i];
+      reduce_range<NV / 2, M * 2, MEND>(v);
+    } else {
+      v[0] = bfly<M>(v[0]);
+      reduce_range<1, M * 2, MEND>(v);
+    }
+  }
+}
+
+// Row (within the batch) of value k held by lane l after reduce-scatter levels on
+// the lowest `levels` lane bits of a batch of ROWS rows.
+template <int ROWS>
+__device__ __forceinline__ int rs_row(int l, int levels, int k) {
+  int off = 0;
+#pragma unroll
+  for (int j = 0; j < log2c(ROWS); j++)
+    if (j < levels) off += ((l >> j) & 1) * (ROWS >> (j + 1));
+  return off + k;
+}
+
+template <Fmt F, SMode SM, typename ST, int ROWS, int NVG>
+struct GemvBatch {
+  bool active;
+  int lr0, rows;
+  const uint8_t* wb;
+  const ST* sb;
+  int64_t s_row, s_grp;
+  void* out;
+  int64_t woffs[ROWS];
+  int rcl[ROWS];
+  bool rv[ROWS];
+  int64_t soffs[NVG];
+};
+
+template <Fmt F, typename ST, int ROWS, int NVG>
+struct GemvData {
+  Raw<FmtInfo<F>::kBytes> w[ROWS];
+  float s[NVG], m[NVG];
+  int e[ROWS];
+};
+
+template <Fmt F, SMode SM, typename XT, typename OT, typename ST, int LPR, int ROWS, int L, bool AM>
+__global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
+  extern __shared__ uint32_t xs_lds[];
+  constexpr int B = FmtInfo<F>::kBytes;
+  constexpr int SUBS = 64 / LPR;
+  constexpr bool kGroup = SM == SMode::kGroup || SM == SMode::kGroupAff;
+  constexpr int LG = kGroup ? L : 1;                        // lanes per quantisation group
+  constexpr int NVG = ROWS / LG > 0 ? ROWS / LG : 1;        // values per lane after the group levels
+  constexpr int GLEV = log2c(LG) < log2c(ROWS) ? log2c(LG) : log2c(ROWS);
+  static_assert(ROWS <= LPR && LG <= LPR, "batch rows and groups must fit the lane group");
+  using Batch = GemvBatch<F, SM, ST, ROWS, NVG>;
+  using Data = GemvData<F, ST, ROWS, NVG>;
+
+  const int slot = blockIdx.y;
+  int64_t woff = 0, soff = 0;
+  if (P.experts != nullptr) {
+    const int64_t e = P.experts[slot];
+    woff = e * P.w_expert;
+    soff = e * P.s_expert;
+  }
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int sub = lane / LPR;
+  const int l = lane % LPR;
+  const int nchunks = P.cols >> 5;
+  const int rounds = (nchunks + LPR - 1) / LPR;
+  const int per_iter = ROWS * SUBS;
+  const int nwaves = gridDim.x * (blockDim.x >> 6);
+  int grow[NVG];
+#pragma unroll
+  for (int k = 0; k < NVG; k++) grow[k] = rs_row<ROWS>(l, GLEV, k) * SUBS + sub;
+  const int frow = rs_row<ROWS>(l, log2c(ROWS), 0) * SUBS + sub;  // row stored by this lane
+  const bool fstore = (l >> log2c(ROWS)) == 0;
+  uint64_t best = 0;
+
+  auto setup = [&](int b, Batch& bt) {
+    const int v0 = __builtin_amdgcn_readfirstlane(b * per_iter);
+    bt.active = v0 < P.vtotal;
+    int si = 0;
+    if (P.nseg > 1 && v0 >= P.seg[1].vbegin) si = 1;
+    if (P.nseg > 2 && v0 >= P.seg[2].vbegin) si = 2;
+    si = __builtin_amdgcn_readfirstlane(si);
+    const Seg& S = si == 0 ? P.seg[0] : (si == 1 ? P.seg[1] : P.seg[2]);
+    bt.lr0 = v0 - S.vbegin;
+    bt.rows = S.rows;
+    bt.wb = S.w + woff + (int64_t)bt.lr0 * S.w_row;
+    bt.sb = reinterpret_cast<const ST*>(S.s) + soff + (int64_t)bt.lr0 * S.s_row;
+    bt.s_row = S.s_row;
+    bt.s_grp = S.s_grp;
+    bt.out = S.out;
+#pragma unroll
+    for (int i = 0; i < ROWS; i++) {
+      const int r = i * SUBS + sub;
+      bt.rv[i] = bt.lr0 + r < bt.rows;
+      bt.rcl[i] = bt.rv[i] ? r : (bt.rows - 1 - bt.lr0);
+      bt.woffs[i] = (int64_t)bt.rcl[i] * S.w_row;
+    }
+#pragma unroll
+    for (int k = 0; k < NVG; k++)
+      bt.soffs[k] = (int64_t)(bt.lr0 + grow[k] < bt.rows ? grow[k] : bt.rows - 1 - bt.lr0) * S.s_row;
+  };
+
+  auto fetch = [&](const Batch& bt, int r, Data& d) {
+    int j = r * LPR + l;
+    j = j < nchunks ? j : nchunks - 1;
+#pragma unroll
+    for (int i = 0; i < ROWS; i++) d.w[i] = load_raw<B>(bt.wb + bt.woffs[i] + (int64_t)j * B);
+    if constexpr (kGroup) {
+#pragma unroll
+      for (int k = 0; k < NVG; k++) {
+        const int64_t off = bt.soffs[k] + (int64_t)(j / LG) * bt.s_grp;
+        d.s[k] = to_f32(bt.sb[off]);
+        if constexpr (SM == SMode::kGroupAff) d.m[k] = to_f32(bt.sb[off + P.s_pair]);
+      }
+    }
+    if constexpr (SM == SMode::kBlockE8) {
+#pragma unroll
+      for (int i = 0; i < ROWS; i++) d.e[i] = reinterpret_cast<const uint8_t*>(bt.sb)[(int64_t)bt.rcl[i] * bt.s_row + j];
+    }
+  };
+
+  int b = blockIdx.x * (blockDim.x >> 6) + wave;
+  Batch cb;
+  setup(b, cb);
+  Data cd;
+  if (cb.active) fetch(cb, 0, cd);
+  {
+    // Stage the activation vector while the first weight loads are in flight.
+    const uint4* xg = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(P.x) + (int64_t)slot * P.x_slot);
+    uint4* xl = reinterpret_cast<uint4*>(xs_lds);
+    for (int i = threadIdx.x; i < (P.cols >> 3); i += blockDim.x) xl[i] = xg[i];
+    __syncthreads();
+  }
+
+  while (cb.active) {
+    Batch nb;
+    nb.active = false;
+    float acc[ROWS];
+#pragma unroll
+    for (int i = 0; i < ROWS; i++) acc[i] = 0.0f;
+
+    for (int r = 0; r < rounds; r++) {
+      Data nd;
+      if (r + 1 < rounds) {
+        fetch(cb, r + 1, nd);
+      } else {
+        setup(b + nwaves, nb);
+        if (nb.active) fetch(nb, 0, nd);
+      }
+      const int j = r * LPR + l;
+      const bool cv = j < nchunks;
+      uint32_t xw[16];
+      {
+        const uint4* xp = reinterpret_cast<const uint4*>(xs_lds + (cv ? j : 0) * 16);
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          uint4 v = xp[q];
+          xw[4 * q] = v.x; xw[4 * q + 1] = v.y; xw[4 * q + 2] = v.z; xw[4 * q + 3] = v.w;
+        }
+      }
+      float p[ROWS];
+      chunk_dot_rows<F, XT, ROWS>(cd.w, xw, p);
+#pragma unroll
+      for (int i = 0; i < ROWS; i++) p[i] = (cv && cb.rv[i]) ? p[i] : 0.0f;
+      if constexpr (SM == SMode::kNone || SM == SMode::kRow) {
+#pragma unroll
+        for (int i = 0; i < ROWS; i++) acc[i] = acc[i] + p[i];
+      } else if constexpr (SM == SMode::kBlockE8) {
+#pragma unroll
+        for (int i = 0; i < ROWS; i++) {
+          float q = p[i];
+          if (P.e8_extra) q = q * pow2i(P.e8_extra);
+          const float t = q * pow2i(cd.e[i] - 127);
+          acc[i] = acc[i] + ((cv && cb.rv[i]) ? t : 0.0f);
+        }
+      } else {
+        float xsum = 0.0f;
+        if constexpr (SM == SMode::kGroupAff) {
+#pragma unroll
+          for (int e = 0; e < 32; e++) xsum = xsum + xv<XT>(xw, e);
+          xsum = cv ? xsum : 0.0f;
+          reduce_range<1, 1, LG>(&xsum);
+        }
+        reduce_range<ROWS, 1, LG>(p);
+#pragma unroll
+        for (int k = 0; k < NVG; k++) {
+          float t;
+          if constexpr (SM == SMode::kGroupAff) {
+            float m = cd.m[k];
+            if (P.aff_zero) m = -(m * cd.s[k]);
+            t = __builtin_fmaf(xsum, m, p[k] * cd.s[k]);
+          } else {
+            t = p[k] * cd.s[k];
+          }
+          const bool ok = cv && (cb.lr0 + grow[k] < cb.rows);
+          acc[k] = acc[k] + (ok ? t : 0.0f);
+        }
+      }
+      cd = nd;
+    }
+    if constexpr (kGroup) reduce_range<NVG, LG, LPR>(acc);
+    else reduce_range<ROWS, 1, LPR>(acc);
+    float v = acc[0];
+    const bool ok = fstore && cb.lr0 + frow < cb.rows;
+    if constexpr (SM == SMode::kRow) v = v * to_f32(cb.sb[(int64_t)(ok ? frow : 0) * cb.s_row]);
+    if (ok && cb.out != nullptr) store<OT>(reinterpret_cast<OT*>(cb.out) + (int64_t)slot * P.out_slot + cb.lr0 + frow, v);
+    if constexpr (AM) {
+      if (ok) {
+        const uint64_t key = argmax_key(round_to<OT>(v), (uint32_t)(cb.lr0 + frow));
+        best = key > best ? key : best;
+      }
+    }
+    cb = nb;
+    b += nwaves;
+  }
+  if constexpr (AM) {
+    best = wave_max_u64(best);
+    if (lane == 0) P.am_partials[blockIdx.x * (blockDim.x >> 6) + wave] = best;
+  }
+}
+
+// ------------------------------------------------------------------ dispatch
+
+// Workgroups of four waves; the grid is capped (waves loop over row batches) so that
+// argmax partials fit kMaxGemvWaves keys.
+constexpr int kMaxGemvBlocks = 2048;
+constexpr int kMaxGemvWaves = 4 * kMaxGemvBlocks;
+
+template <Fmt F, SMode SM, typename XT, typename OT, typename ST, int LPR, int ROWS, int L>
+static int launch_one(GemvParams P, int slots, hipStream_t stream, const char* what) {
+  constexpr int SUBS = 64 / LPR;
+  constexpr int per_iter = ROWS * SUBS;
+  int v = 0;
+  for (int i = 0; i < P.nseg; i++) {
+    P.seg[i].vbegin = v;
+    v += (P.seg[i].rows + per_iter - 1) / per_iter * per_iter;
+  }
+  P.vtotal = v;
+  const int batches = v / per_iter;
+  int blocks = (batches + 3) / 4;
+  if (blocks < 1) blocks = 1;
+  if (blocks > kMaxGemvBlocks) blocks = kMaxGemvBlocks;
+  const size_t lds = (size_t)P.cols * 2;
+  if (P.am_partials != nullptr) {
+    if constexpr (SM == SMode::kNone) {
+      // unused partial slots must not win the final reduction
+      hipLaunchKernelGGL((gemv_kernel<F, SM, XT, OT, ST, LPR, ROWS, L, true>), dim3(blocks, slots), dim3(256), lds,
+                         stream, P);
+      return check_launch(what);
+    }
+    set_error("%s: argmax epilogue is only available for dense weights", what);
+    return TT_ERR_UNSUPPORTED;
+  }
+  hipLaunchKernelGGL((gemv_kernel<F, SM, XT, OT, ST, LPR, ROWS, L, false>), dim3(blocks, slots), dim3(256), lds, stream,
+                     P);
+  return check_launch(what);
+}
+
+template <Fmt F, SMode SM, typename XT, typename OT, typename ST, int ROWS, int L>
+static int launch_lpr(int lpr, const GemvParams& P, int slots, hipStream_t stream, const char* what) {
+  switch (lpr) {
+    case 64: return launch_one<F, SM, XT, OT, ST, 64, ROWS, L>(P, slots, stream, what);
+    case 32:
+      if constexpr (L <= 32) return launch_one<F, SM, XT, OT, ST, 32, ROWS, L>(P, slots, stream, what);
+      break;
+    case 16:
+      if constexpr (L <= 16) return launch_one<F, SM, XT, OT, ST, 16, ROWS, L>(P, slots, stream, what);
+      break;
+    default: break;
+  }
+  set_error("%s: invalid lanes per row %d for a %d-chunk group", what, lpr, L);
+  return TT_ERR_INVALID;
+}
+
+template <Fmt F, SMode SM, typename XT, typename OT, typename ST, int ROWS>
+static int launch_group(int L, int lpr, const GemvParams& P, int slots, hipStream_t stream, const char* what) {
+  switch (L) {
+    case 1: return launch_lpr<F, SM, XT, OT, ST, ROWS, 1>(lpr, P, slots, stream, what);
+    case 2: return launch_lpr<F, SM, XT, OT, ST, ROWS, 2>(lpr, P, slots, stream, what);
+    case 4: return launch_lpr<F, SM, XT, OT, ST, ROWS, 4>(lpr, P, slots, stream, what);
+    case 8: return launch_lpr<F, SM, XT, OT, ST, ROWS, 8>(lpr, P, slots, stream, what);
+    case 16: return launch_lpr<F, SM, XT, OT, ST, ROWS, 16>(lpr, P, slots, stream, what);
+    case 32: return launch_lpr<F, SM, XT, OT, ST, ROWS, 32>(lpr, P, slots, stream, what);
+    case 64: return launch_lpr<F, SM, XT, OT, ST, ROWS, 64>(lpr, P, slots, stream, what);
+  }
+  set_error("%s: unsupported group of %d chunks", what, L);
+  return TT_ERR_UNSUPPORTED;
+}
+
+template <Fmt F, SMode SM, typename ST, int ROWS>
+static int launch_types(int x_dtype, int out_dtype, int L, int lpr, const GemvParams& P, int slots, hipStream_t stream,
+                        const char* what) {
+  constexpr bool kGroup = SM == SMode::kGroup || SM == SMode::kGroupAff;
+  auto go = [&](auto xt, auto ot) -> int {
+    using XT = decltype(xt);
+    using OT = decltype(ot);
+    if constexpr (kGroup) return launch_group<F, SM, XT, OT, ST, ROWS>(L, lpr, P, slots, stream, what);
+    else return launch_lpr<F, SM, XT, OT, ST, ROWS, 1>(lpr, P, slots, stream, what);
+  };
+  if (x_dtype == TT_F16) {
+    if (out_dtype == TT_F16) return go(f16_t{}, f16_t{});
+    if (out_dtype == TT_F32) return go(f16_t{}, float{});
+  } else if (x_dtype == TT_BF16) {
+    if (out_dtype == TT_BF16) return go(bf16_t{}, bf16_t{});
+    if (out_dtype == TT_F32) return go(bf16_t{}, float{});
+  }
+  set_error("%s: unsupported activation/output dtype pair (%d, %d); output must match the activation dtype or be fp32",
+            what, x_dtype, out_dtype);
+  return TT_ERR_UNSUPPORTED;
+}
+
+// Validates the common GEMV contract and fills group information.
+inline int plan_groups(const char* what, int64_t cols, int64_t group_size, int* L, bool* row_mode) {
+  TT_REQUIRE(cols > 0 && cols % 32 == 0, "%s: cols must be a positive multiple of 32 (got %lld)", what, (long long)cols);
+  TT_REQUIRE(cols <= 32768, "%s: cols %lld exceeds the staged-activation limit 32768", what, (long long)cols);
+  if (group_size >= cols) { *row_mode = true; *L = 1; return TT_OK; }
+  *row_mode = false;
+  TT_REQUIRE(group_size >= 32 && group_size % 32 == 0 && cols % group_size == 0,
+             "%s: group_size %lld must be a multiple of 32 dividing cols %lld", what, (long long)group_size, (long long)cols);
+  const int64_t Lg = group_size / 32;
+  TT_UNSUPPORTED(Lg <= 64 && (Lg & (Lg - 1)) == 0, "%s: group_size %lld must be 32 * 2^k <= 2048", what, (long long)group_size);
+  *L = (int)Lg;
+  return TT_OK;
+}
+
+
+}  // namespace tt

@@ -34,11 +34,6 @@ __global__ __launch_bounds__(256) void swiglu_kernel(SwigluParams P) {
   extern __shared__ uint32_t xs_lds[];
   constexpr int SUBS = 64 / LPR;
   const int slot = blockIdx.y;
-  {
-    const uint32_t* xg = reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(P.x) + (int64_t)slot * P.x_slot);
-    for (int i = threadIdx.x; i < (P.cols >> 1); i += blockDim.x) xs_lds[i] = xg[i];
-  }
-  __syncthreads();
   const int64_t e = P.experts[slot];
   const uint8_t* wexp = P.w + e * P.w_expert;
   const uint8_t* sexp = P.s + e * P.s_expert;
@@ -47,7 +42,9 @@ __global__ __launch_bounds__(256) void swiglu_kernel(SwigluParams P) {
   const int nchunks = P.cols >> 5;
   const int per_iter = APW * SUBS;
   const int waves_total = gridDim.x * (blockDim.x >> 6);
-  for (int base = (blockIdx.x * (blockDim.x >> 6) + wave) * per_iter; base < P.act_rows; base += waves_total * per_iter) {
+  bool staged = false;
+  for (int base = (blockIdx.x * (blockDim.x >> 6) + wave) * per_iter;; base += waves_total * per_iter) {
+    const bool active = base < P.act_rows;
     const uint8_t* wrow[2 * APW];
     const uint8_t* srow[2 * APW];
     bool rv[2 * APW];
@@ -64,8 +61,17 @@ __global__ __launch_bounds__(256) void swiglu_kernel(SwigluParams P) {
         srow[2 * i + h] = sexp + row * P.s_row;
       }
     }
+    E8Round<F, 2 * APW> cur;
+    if (active) e8_fetch<F, LPR, 2 * APW>(cur, 0, l, nchunks, wrow, srow, rv);
+    if (!staged) {
+      const uint32_t* xg = reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(P.x) + (int64_t)slot * P.x_slot);
+      for (int i = threadIdx.x; i < (P.cols >> 1); i += blockDim.x) xs_lds[i] = xg[i];
+      __syncthreads();
+      staged = true;
+    }
+    if (!active) break;
     float dot[2 * APW];
-    e8_rows_dot<F, XT, LPR, 2 * APW>(wrow, srow, rv, xs_lds, nchunks, l, P.e8_extra, dot);
+    e8_rows_dot<F, XT, LPR, 2 * APW>(cur, wrow, srow, rv, xs_lds, nchunks, l, P.e8_extra, dot);
 #pragma unroll
     for (int i = 0; i < APW; i++) {
       if (!rv[2 * i] || l != i) continue;
@@ -105,17 +111,14 @@ __global__ __launch_bounds__(256) void weighted_down_kernel(DownParams P) {
   extern __shared__ uint32_t xs_lds[];
   constexpr int SUBS = 64 / LPR;
   const int words = P.cols >> 1;
-  for (int s = 0; s < P.slots; s++) {
-    const uint32_t* xg = reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(P.x) + (int64_t)s * P.x_slot);
-    for (int i = threadIdx.x; i < words; i += blockDim.x) xs_lds[s * words + i] = xg[i];
-  }
-  __syncthreads();
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int sub = lane / LPR, l = lane % LPR;
   const int nchunks = P.cols >> 5;
   const int per_iter = RPW * SUBS;
   const int waves_total = gridDim.x * (blockDim.x >> 6);
-  for (int base = (blockIdx.x * (blockDim.x >> 6) + wave) * per_iter; base < P.rows; base += waves_total * per_iter) {
+  bool staged = false;
+  for (int base = (blockIdx.x * (blockDim.x >> 6) + wave) * per_iter;; base += waves_total * per_iter) {
+    const bool active = base < P.rows;
     int row[RPW];
     bool rv[RPW];
     float combined[RPW];
@@ -125,17 +128,37 @@ __global__ __launch_bounds__(256) void weighted_down_kernel(DownParams P) {
       rv[i] = row[i] < P.rows;
       combined[i] = 0.0f;
     }
-    for (int s = 0; s < P.slots; s++) {
-      const int64_t e = P.experts[s];
-      const uint8_t* wrow[RPW];
-      const uint8_t* srow[RPW];
+    const uint8_t* wrow[RPW];
+    const uint8_t* srow[RPW];
+    int64_t e = P.experts[0];
 #pragma unroll
-      for (int i = 0; i < RPW; i++) {
-        wrow[i] = P.w + e * P.w_expert + (int64_t)row[i] * P.w_row;
-        srow[i] = P.s + e * P.s_expert + (int64_t)row[i] * P.s_row;
+    for (int i = 0; i < RPW; i++) {
+      wrow[i] = P.w + e * P.w_expert + (int64_t)row[i] * P.w_row;
+      srow[i] = P.s + e * P.s_expert + (int64_t)row[i] * P.s_row;
+    }
+    E8Round<F, RPW> cur;
+    if (active) e8_fetch<F, LPR, RPW>(cur, 0, l, nchunks, wrow, srow, rv);
+    if (!staged) {
+      for (int s = 0; s < P.slots; s++) {
+        const uint32_t* xg = reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(P.x) + (int64_t)s * P.x_slot);
+        for (int i = threadIdx.x; i < words; i += blockDim.x) xs_lds[s * words + i] = xg[i];
+      }
+      __syncthreads();
+      staged = true;
+    }
+    if (!active) break;
+    for (int s = 0; s < P.slots; s++) {
+      if (s > 0) {
+        e = P.experts[s];
+#pragma unroll
+        for (int i = 0; i < RPW; i++) {
+          wrow[i] = P.w + e * P.w_expert + (int64_t)row[i] * P.w_row;
+          srow[i] = P.s + e * P.s_expert + (int64_t)row[i] * P.s_row;
+        }
+        e8_fetch<F, LPR, RPW>(cur, 0, l, nchunks, wrow, srow, rv);
       }
       float dot[RPW];
-      e8_rows_dot<F, XT, LPR, RPW>(wrow, srow, rv, xs_lds + s * words, nchunks, l, P.e8_extra, dot);
+      e8_rows_dot<F, XT, LPR, RPW>(cur, wrow, srow, rv, xs_lds + s * words, nchunks, l, P.e8_extra, dot);
       const float score = ld_score<ScT>(P.scores, s);
 #pragma unroll
       for (int i = 0; i < RPW; i++) {

@@ -1,0 +1,301 @@
+// Decode-step elementwise and normalisation operators for gfx950:
+// rms_norm, add_rms_norm, add, silu_mul, interleaved_swiglu, weighted_expert_sum,
+// rope_qk_inplace, embedding row copy and KV-cache append.  Token ids and token
+// positions can be read from device memory so a whole decode step can be replayed
+// from a HIP graph.
+#include "tt_abi_internal.h"
+#include "tt_common.h"
+
+#include <type_traits>
+
+namespace tt {
+
+template <typename T> __device__ __forceinline__ float ld(const void* p, int64_t i) {
+  return to_f32(reinterpret_cast<const T*>(p)[i]);
+}
+
+// Block-wide sum in a fixed order: thread partials are reduced with the wave
+// butterfly, then the four wave sums are combined as (w0 + w1) + (w2 + w3).
+__device__ __forceinline__ float block_sum256(float v, float* red) {
+  v = xor_sum(v, 1, 64);
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) red[wave] = v;
+  __syncthreads();
+  const float t = (red[0] + red[1]) + (red[2] + red[3]);
+  __syncthreads();
+  return t;
+}
+
+// ---------------------------------------------------------------- RMSNorm
+// out_i = (x_i * (1 / sqrt(mean(x^2) + eps))) * (w_i + offset); sum of squares per
+// thread is an fma chain over elements t, t+256, ... (triton_kernels.py:2562-2577).
+template <typename XT, typename WT, typename OT>
+__global__ __launch_bounds__(256) void rms_norm_kernel(const void* x, const void* w, void* out, int n, float eps,
+                                                       float offset) {
+  __shared__ float red[4];
+  float s = 0.0f;
+  for (int i = threadIdx.x; i < n; i += 256) {
+    const float v = ld<XT>(x, i);
+    s = __builtin_fmaf(v, v, s);
+  }
+  const float total = block_sum256(s, red);
+  const float inv = 1.0f / __builtin_sqrtf(total / (float)n + eps);
+  for (int i = threadIdx.x; i < n; i += 256)
+    store<OT>(reinterpret_cast<OT*>(out) + i, (ld<XT>(x, i) * inv) * (ld<WT>(w, i) + offset));
+}
+
+// residual = bf16(left + right) stored to residual_out; out = (r * inv) * w with the
+// RMS taken over the rounded residual (triton_kernels.py:2581-2614).
+template <typename XT, typename WT, typename OT>
+__global__ __launch_bounds__(256) void add_rms_norm_kernel(const void* left, const void* right, void* residual_out,
+                                                           const void* w, void* out, int n, float eps) {
+  __shared__ float red[4];
+  float s = 0.0f;
+  for (int i = threadIdx.x; i < n; i += 256) {
+    const float r = round_bf16(ld<XT>(left, i) + ld<XT>(right, i));
+    s = __builtin_fmaf(r, r, s);
+  }
+  const float total = block_sum256(s, red);
+  const float inv = 1.0f / __builtin_sqrtf(total / (float)n + eps);
+  for (int i = threadIdx.x; i < n; i += 256) {
+    const float r = round_bf16(ld<XT>(left, i) + ld<XT>(right, i));
+    store<XT>(reinterpret_cast<XT*>(residual_out) + i, r);
+    store<OT>(reinterpret_cast<OT*>(out) + i, (r * inv) * ld<WT>(w, i));
+  }
+}
+
+// ---------------------------------------------------------------- elementwise
+template <typename T>
+__global__ void add_kernel(const void* a, const void* b, void* out, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) store<T>(reinterpret_cast<T*>(out) + i, ld<T>(a, i) + ld<T>(b, i));
+}
+
+// silu(g) * u = (g / (1 + exp(-g))) * u (triton_kernels.py:2761-2774)
+template <typename T>
+__global__ void silu_mul_kernel(const void* g, const void* u, void* out, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) {
+    const float gv = ld<T>(g, i);
+    const float s = gv / (1.0f + exp_f32(-gv));
+    store<T>(reinterpret_cast<T*>(out) + i, s * ld<T>(u, i));
+  }
+}
+
+// gpt-oss SwiGLU on interleaved [.., 2n] gate/up (triton_kernels.py:2778-2793)
+template <typename T>
+__global__ void interleaved_swiglu_kernel(const void* gu, void* out, int n, int64_t in_row, int64_t out_row,
+                                          float alpha, float limit) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  const int r = blockIdx.y;
+  if (i < n) {
+    float g = ld<T>(gu, r * in_row + 2 * (int64_t)i);
+    float u = ld<T>(gu, r * in_row + 2 * (int64_t)i + 1);
+    g = fminf(g, limit);
+    u = fmaxf(fminf(u, limit), -limit);
+    const float num = (u + 1.0f) * g;
+    const float den = 1.0f + exp_f32(-g * alpha);
+    store<T>(reinterpret_cast<T*>(out) + r * out_row + i, num / den);
+  }
+}
+
+// out[n] = sum_e fma(experts[e, n], scores[e], .) in expert order (triton_kernels.py:2797-2817)
+template <typename T, typename ST>
+__global__ void weighted_expert_sum_kernel(const void* ex, const void* scores, void* out, int width, int count,
+                                           int64_t stride) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < width) {
+    float acc = 0.0f;
+    for (int e = 0; e < count; e++) acc = __builtin_fmaf(ld<T>(ex, e * stride + i), ld<ST>(scores, e), acc);
+    store<T>(reinterpret_cast<T*>(out) + i, acc);
+  }
+}
+
+// ---------------------------------------------------------------- RoPE
+// q1' = r(r(q1 c) - r(q2 s)), q2' = r(r(q2 c) + r(q1 s)) with r() rounding to the
+// activation dtype, as the reference's torch RoPE path (gpu_runtime.py:8696-8705).
+// cos/sin rows come from a table indexed by the token position, which may be read
+// from device memory (pos_dev) so graph replays advance with the position.
+template <typename T>
+__global__ void rope_kernel(void* q, void* k, const void* cos_t, const void* sin_t, int64_t table_row,
+                            const int32_t* pos_dev, int pos, int heads, int kv_heads, int head_dim) {
+  const int half = head_dim >> 1;
+  const int64_t p = pos_dev ? (int64_t)pos_dev[0] : (int64_t)pos;
+  const int total = (heads + kv_heads) * half;
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= total) return;
+  const int h = idx / half, i = idx - h * half;
+  T* base = h < heads ? reinterpret_cast<T*>(q) + (int64_t)h * head_dim : reinterpret_cast<T*>(k) + (int64_t)(h - heads) * head_dim;
+  const float c = ld<T>(cos_t, p * table_row + i);
+  const float s = ld<T>(sin_t, p * table_row + i);
+  const float a = to_f32(base[i]);
+  const float b = to_f32(base[i + half]);
+  const float ac = round_to<T>(a * c), bs = round_to<T>(b * s);
+  const float bc = round_to<T>(b * c), as = round_to<T>(a * s);
+  store<T>(base + i, ac - bs);
+  store<T>(base + i + half, bc + as);
+}
+
+// ---------------------------------------------------------------- embedding / KV
+// out = embed[token] (row copy), token read from device memory when token_dev is set.
+__global__ void embed_kernel(const uint16_t* embed, int64_t row, const int64_t* token_dev, int64_t token, uint16_t* out,
+                             int n) {
+  const int64_t t = token_dev ? token_dev[0] : token;
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) out[i] = embed[t * row + i];
+}
+
+// keys[h, pos, :] = k[h, :], values[h, pos, :] = v[h, :]
+__global__ void kv_append_kernel(const uint16_t* k, const uint16_t* v, uint16_t* keys, uint16_t* values,
+                                 int64_t stride_h, int64_t stride_t, const int32_t* pos_dev, int pos, int kv_heads,
+                                 int head_dim) {
+  const int64_t p = pos_dev ? (int64_t)pos_dev[0] : (int64_t)pos;
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= kv_heads * head_dim) return;
+  const int h = idx / head_dim, d = idx - h * head_dim;
+  keys[h * stride_h + p * stride_t + d] = k[idx];
+  values[h * stride_h + p * stride_t + d] = v[idx];
+}
+
+__global__ void advance_position_kernel(int32_t* pos, int32_t step) {
+  if (threadIdx.x == 0) pos[0] += step;
+}
+
+template <typename Fn> static int with_act(int code, Fn&& f) {
+  if (code == TT_F16) return f(f16_t{});
+  if (code == TT_BF16) return f(bf16_t{});
+  set_error("activation dtype must be fp16 or bf16 (got %d)", code);
+  return TT_ERR_INVALID;
+}
+template <typename Fn> static int with_any(int code, Fn&& f) {
+  if (code == TT_F16) return f(f16_t{});
+  if (code == TT_BF16) return f(bf16_t{});
+  if (code == TT_F32) return f(float{});
+  set_error("unsupported dtype code %d", code);
+  return TT_ERR_INVALID;
+}
+
+}  // namespace tt
+
+using namespace tt;
+
+extern "C" int tt_rms_norm(const void* x, int x_dtype, const void* weight, int w_dtype, void* out, int out_dtype,
+                           int64_t n, float eps, float weight_offset, void* stream) {
+  TT_REQUIRE(x && weight && out && n > 0 && n <= (1 << 24), "rms_norm: bad arguments");
+  return with_act(x_dtype, [&](auto xt) {
+    using XT = decltype(xt);
+    return with_any(w_dtype, [&](auto wt) {
+      using WT = decltype(wt);
+      return with_any(out_dtype, [&](auto ot) {
+        using OT = decltype(ot);
+        hipLaunchKernelGGL((rms_norm_kernel<XT, WT, OT>), dim3(1), dim3(256), 0, static_cast<hipStream_t>(stream), x,
+                           weight, out, (int)n, eps, weight_offset);
+        return check_launch("rms_norm");
+      });
+    });
+  });
+}
+
+extern "C" int tt_add_rms_norm(const void* left, const void* right, void* residual_out, int x_dtype,
+                               const void* weight, int w_dtype, void* out, int out_dtype, int64_t n, float eps,
+                               void* stream) {
+  TT_REQUIRE(left && right && residual_out && weight && out && n > 0 && n <= (1 << 24), "add_rms_norm: bad arguments");
+  return with_act(x_dtype, [&](auto xt) {
+    using XT = decltype(xt);
+    return with_any(w_dtype, [&](auto wt) {
+      using WT = decltype(wt);
+      return with_any(out_dtype, [&](auto ot) {
+        using OT = decltype(ot);
+        hipLaunchKernelGGL((add_rms_norm_kernel<XT, WT, OT>), dim3(1), dim3(256), 0, static_cast<hipStream_t>(stream),
+                           left, right, residual_out, weight, out, (int)n, eps);
+        return check_launch("add_rms_norm");
+      });
+    });
+  });
+}
+
+extern "C" int tt_add(const void* a, const void* b, void* out, int dtype, int64_t n, void* stream) {
+  TT_REQUIRE(a && b && out && n > 0 && n < (1LL << 31), "add: bad arguments");
+  return with_any(dtype, [&](auto t) {
+    using T = decltype(t);
+    hipLaunchKernelGGL((add_kernel<T>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       a, b, out, (int)n);
+    return check_launch("add");
+  });
+}
+
+extern "C" int tt_silu_mul(const void* gate, const void* up, void* out, int dtype, int64_t n, void* stream) {
+  TT_REQUIRE(gate && up && out && n > 0 && n < (1LL << 31), "silu_mul: bad arguments");
+  return with_any(dtype, [&](auto t) {
+    using T = decltype(t);
+    hipLaunchKernelGGL((silu_mul_kernel<T>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), gate, up, out, (int)n);
+    return check_launch("silu_mul");
+  });
+}
+
+extern "C" int tt_interleaved_swiglu(const void* gate_up, int64_t in_row, void* out, int64_t out_row, int dtype,
+                                     int64_t rows, int64_t n, float alpha, float limit, void* stream) {
+  TT_REQUIRE(gate_up && out && n > 0 && rows > 0 && rows <= 65535, "interleaved_swiglu: bad arguments");
+  return with_any(dtype, [&](auto t) {
+    using T = decltype(t);
+    hipLaunchKernelGGL((interleaved_swiglu_kernel<T>), dim3((unsigned)((n + 255) / 256), (unsigned)rows), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), gate_up, out, (int)n, in_row, out_row, alpha, limit);
+    return check_launch("interleaved_swiglu");
+  });
+}
+
+extern "C" int tt_weighted_expert_sum(const void* experts, int dtype, int64_t stride, int64_t count,
+                                      const void* scores, int score_dtype, void* out, int64_t width, void* stream) {
+  TT_REQUIRE(experts && scores && out && width > 0 && count > 0, "weighted_expert_sum: bad arguments");
+  return with_any(dtype, [&](auto t) {
+    using T = decltype(t);
+    return with_any(score_dtype, [&](auto st) {
+      using ST = decltype(st);
+      hipLaunchKernelGGL((weighted_expert_sum_kernel<T, ST>), dim3((unsigned)((width + 255) / 256)), dim3(256), 0,
+                         static_cast<hipStream_t>(stream), experts, scores, out, (int)width, (int)count, stride);
+      return check_launch("weighted_expert_sum");
+    });
+  });
+}
+
+extern "C" int tt_rope_qk_inplace(void* q, void* k, int dtype, const void* cos_table, const void* sin_table,
+                                  int64_t table_row, const int32_t* position_dev, int64_t position, int64_t heads,
+                                  int64_t kv_heads, int64_t head_dim, void* stream) {
+  TT_REQUIRE(q && k && cos_table && sin_table && head_dim > 0 && head_dim % 2 == 0, "rope: RoPE head_dim must be even");
+  TT_REQUIRE(heads > 0 && kv_heads >= 0, "rope: bad head counts");
+  const int total = (int)((heads + kv_heads) * (head_dim / 2));
+  return with_act(dtype, [&](auto t) {
+    using T = decltype(t);
+    hipLaunchKernelGGL((rope_kernel<T>), dim3((total + 255) / 256), dim3(256), 0, static_cast<hipStream_t>(stream), q, k,
+                       cos_table, sin_table, table_row, position_dev, (int)position, (int)heads, (int)kv_heads,
+                       (int)head_dim);
+    return check_launch("rope_qk_inplace");
+  });
+}
+
+extern "C" int tt_embedding(const void* embed, int64_t row_stride, const int64_t* token_dev, int64_t token, void* out,
+                            int64_t n, void* stream) {
+  TT_REQUIRE(embed && out && n > 0, "embedding: bad arguments");
+  hipLaunchKernelGGL(embed_kernel, dim3((unsigned)((n + 255) / 256 < 64 ? (n + 255) / 256 : 64)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(embed), row_stride, token_dev, token,
+                     static_cast<uint16_t*>(out), (int)n);
+  return check_launch("embedding");
+}
+
+extern "C" int tt_kv_append(const void* k, const void* v, void* keys, void* values, int64_t stride_head,
+                            int64_t stride_token, const int32_t* position_dev, int64_t position, int64_t kv_heads,
+                            int64_t head_dim, void* stream) {
+  TT_REQUIRE(k && v && keys && values && kv_heads > 0 && head_dim > 0, "kv_append: bad arguments");
+  const int total = (int)(kv_heads * head_dim);
+  hipLaunchKernelGGL(kv_append_kernel, dim3((total + 255) / 256), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v), static_cast<uint16_t*>(keys),
+                     static_cast<uint16_t*>(values), stride_head, stride_token, position_dev, (int)position,
+                     (int)kv_heads, (int)head_dim);
+  return check_launch("kv_append");
+}
+
+extern "C" int tt_advance_position(int32_t* position_dev, int32_t step, void* stream) {
+  TT_REQUIRE(position_dev != nullptr, "advance_position: null pointer");
+  hipLaunchKernelGGL(advance_position_kernel, dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream), position_dev, step);
+  return check_launch("advance_position");
+}

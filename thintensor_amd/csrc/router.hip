@@ -1,0 +1,157 @@
+// MoE router for gfx950: router GEMV + bias + top-k + softmax in one launch
+// (triton_kernels.py:2855-2921), and top-k + softmax on given logits
+// (triton_kernels.py:2821-2851).
+//
+//   logit_e = bf16(dot_e) (+ bias_e, rounded to bf16 again) -- the reference rounds
+//             through bfloat16 whatever the activation dtype;
+//   dot_e   = GEMV row in the library order with 64 lanes per row;
+//   top-k   = iterated argmax, lowest index on ties;
+//   score_i = exp(v_i - max_all) / D, D summed in slot order over the selected
+//             experts (renormalize) or in expert order over all experts.
+// Indices are written as int32 and stay on the device.
+#include "tt_abi_internal.h"
+#include "tt_common.h"
+#include "tt_gemv.h"
+
+#include <type_traits>
+
+namespace tt {
+
+template <typename T> __device__ __forceinline__ float ldv(const void* p, int64_t i) {
+  return to_f32(reinterpret_cast<const T*>(p)[i]);
+}
+
+__device__ void select_topk(const float* logits, int E, int top_k, bool renorm, int32_t* idx_out, float* sel_out,
+                            float* den_out) {
+  float maximum = __builtin_bit_cast(float, 0xff800000u);
+  for (int e = 0; e < E; e++) maximum = fmaxf(maximum, logits[e]);
+  bool taken[128];
+  for (int e = 0; e < E; e++) taken[e] = false;
+  for (int s = 0; s < top_k; s++) {
+    int bi = -1;
+    float bv = 0.0f;
+    for (int e = 0; e < E; e++) {
+      if (taken[e]) continue;
+      if (bi < 0 || logits[e] > bv) { bi = e; bv = logits[e]; }
+    }
+    taken[bi] = true;
+    idx_out[s] = bi;
+    sel_out[s] = bv;
+  }
+  float den = 0.0f;
+  if (renorm) {
+    for (int s = 0; s < top_k; s++) den = den + exp_f32(sel_out[s] - maximum);
+  } else {
+    for (int e = 0; e < E; e++) den = den + exp_f32(logits[e] - maximum);
+  }
+  for (int s = 0; s < top_k; s++) sel_out[s] = exp_f32(sel_out[s] - maximum) / den;
+  *den_out = den;
+}
+
+template <typename WT, typename XT, typename BT, typename OT>
+__global__ __launch_bounds__(1024) void router_kernel(const void* w, int64_t w_row, const void* x, int H, const void* bias,
+                                                      int E, int top_k, int renorm, int32_t* idx_out, void* score_out) {
+  __shared__ float logits[128];
+  constexpr Fmt F = std::is_same_v<WT, bf16_t> ? Fmt::kBF16W : Fmt::kF16W;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nwaves = blockDim.x >> 6;
+  const int nchunks = H >> 5;
+  const int rounds = (nchunks + 63) / 64;
+  for (int e = wave; e < E; e += nwaves) {
+    float acc = 0.0f;
+    for (int r = 0; r < rounds; r++) {
+      const int j = r * 64 + lane;
+      float p = 0.0f;
+      if (j < nchunks) {
+        const Raw<64> wr = load_raw<64>(reinterpret_cast<const uint8_t*>(w) + ((int64_t)e * w_row + 32 * j) * 2);
+        const Raw<64> xr = load_raw<64>(reinterpret_cast<const uint8_t*>(x) + (int64_t)32 * j * 2);
+        p = chunk_dot<F, XT>(wr, xr.w);
+      }
+      acc = acc + p;
+    }
+    acc = xor_sum(acc, 1, 64);
+    float lg = round_bf16(acc);
+    if (bias != nullptr) lg = round_bf16(lg + ldv<BT>(bias, e));
+    if (lane == 0) logits[e] = lg;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float sel[128];
+    float den;
+    select_topk(logits, E, top_k, renorm != 0, idx_out, sel, &den);
+    for (int s = 0; s < top_k; s++) store<OT>(reinterpret_cast<OT*>(score_out) + s, sel[s]);
+  }
+}
+
+template <typename LT, typename OT>
+__global__ void topk_kernel(const void* logits_in, int E, int top_k, int renorm, int32_t* idx_out, void* score_out) {
+  if (threadIdx.x != 0) return;
+  float logits[128];
+  for (int e = 0; e < E; e++) logits[e] = ldv<LT>(logits_in, e);
+  float sel[128];
+  float den;
+  select_topk(logits, E, top_k, renorm != 0, idx_out, sel, &den);
+  for (int s = 0; s < top_k; s++) store<OT>(reinterpret_cast<OT*>(score_out) + s, sel[s]);
+}
+
+template <typename Fn> static int dt3(int code, Fn&& f) {
+  if (code == TT_F16) return f(f16_t{});
+  if (code == TT_BF16) return f(bf16_t{});
+  if (code == TT_F32) return f(float{});
+  set_error("unsupported dtype code %d", code);
+  return TT_ERR_INVALID;
+}
+
+}  // namespace tt
+
+using namespace tt;
+
+extern "C" int tt_moe_router_matvec_topk(const void* weight, int w_dtype, int64_t w_row, const void* hidden,
+                                         int x_dtype, int64_t hidden_size, const void* bias, int bias_dtype,
+                                         int64_t experts, int64_t top_k, int renormalize, int32_t* indices_out,
+                                         void* scores_out, int score_dtype, void* stream) {
+  const char* what = "moe_router_matvec_topk";
+  TT_REQUIRE(experts > 0 && experts <= 128, "%s: fused router supports at most 128 experts", what);
+  TT_REQUIRE(top_k > 0 && top_k <= experts, "%s: top_k must be in [1, experts]", what);
+  TT_REQUIRE(hidden_size > 0 && hidden_size % 32 == 0, "%s: hidden size must be a multiple of 32", what);
+  TT_REQUIRE(weight && hidden && indices_out && scores_out, "%s: null pointer", what);
+  TT_REQUIRE(aligned(weight, 16) && aligned(hidden, 16) && w_row % 8 == 0, "%s: weight rows and hidden must be 16-byte aligned", what);
+  const int bdt = bias ? bias_dtype : TT_F32;
+  return dt3(w_dtype, [&](auto wt) {
+    using WT = decltype(wt);
+    return dt3(x_dtype, [&](auto xt) {
+      using XT = decltype(xt);
+      return dt3(bdt, [&](auto bt) {
+        using BT = decltype(bt);
+        return dt3(score_dtype, [&](auto ot) {
+          using OT = decltype(ot);
+          if constexpr (std::is_same_v<WT, float> || std::is_same_v<XT, float>) {
+            set_error("%s: router weight and hidden must be fp16 or bf16", what);
+            return TT_ERR_UNSUPPORTED;
+          } else {
+            hipLaunchKernelGGL((router_kernel<WT, XT, BT, OT>), dim3(1), dim3(1024), 0, static_cast<hipStream_t>(stream),
+                               weight, w_row, hidden, (int)hidden_size, bias, (int)experts, (int)top_k, renormalize,
+                               indices_out, scores_out);
+            return check_launch(what);
+          }
+        });
+      });
+    });
+  });
+}
+
+extern "C" int tt_moe_router_topk(const void* logits, int logits_dtype, int64_t experts, int64_t top_k, int renormalize,
+                                  int32_t* indices_out, void* scores_out, int score_dtype, void* stream) {
+  const char* what = "moe_router_topk";
+  TT_REQUIRE(experts > 0 && experts <= 128 && top_k > 0 && top_k <= experts, "%s: bad expert counts", what);
+  TT_REQUIRE(logits && indices_out && scores_out, "%s: null pointer", what);
+  return dt3(logits_dtype, [&](auto lt) {
+    using LT = decltype(lt);
+    return dt3(score_dtype, [&](auto ot) {
+      using OT = decltype(ot);
+      hipLaunchKernelGGL((topk_kernel<LT, OT>), dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream), logits,
+                         (int)experts, (int)top_k, renormalize, indices_out, scores_out);
+      return check_launch(what);
+    });
+  });
+}

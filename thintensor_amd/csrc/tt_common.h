@@ -59,13 +59,59 @@ template <> __device__ __forceinline__ float hi_f32<f16_t>(uint32_t w) { return 
 template <> __device__ __forceinline__ float lo_f32<bf16_t>(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
 template <> __device__ __forceinline__ float hi_f32<bf16_t>(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
 
-// Butterfly sum over the lanes whose index differs only in bits [lo_mask, width):
-// after the call every participating lane holds the same value.  IEEE addition is
-// commutative, so lane i computing v_i + v_{i^m} and lane i^m computing
-// v_{i^m} + v_i yield identical bits: the tree is T(a[0..n)) = T(a[0..n/2)) + T(a[n/2..n)).
+// Exact xor partner: value of lane (lane ^ M) for M in {1,2,4,8,16,32}, for any
+// lane values.  1 and 2 use DPP quad_perm, 4 two bank-masked DPP row shifts, 8 DPP
+// row_ror:8 (== xor 8 inside a 16-lane row), 16 and 32 the gfx950 permlane swaps.
+template <int M>
+__device__ __forceinline__ float xor_partner(float v) {
+  const int iv = __builtin_bit_cast(int, v);
+  if constexpr (M == 1) return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0xB1, 0xF, 0xF, false));
+  else if constexpr (M == 2) return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0x4E, 0xF, 0xF, false));
+  else if constexpr (M == 4) {
+    // banks 0,2 (lanes 0-3, 8-11 of each row) read lane+4 (row_shl:4); banks 1,3 read lane-4 (row_shr:4)
+    int t = __builtin_amdgcn_update_dpp(iv, iv, 0x104, 0xF, 0x5, false);
+    t = __builtin_amdgcn_update_dpp(t, iv, 0x114, 0xF, 0xA, false);
+    return __builtin_bit_cast(float, t);
+  } else if constexpr (M == 8) return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0x128, 0xF, 0xF, false));
+  else if constexpr (M == 16) {
+    auto r = __builtin_amdgcn_permlane16_swap(iv, iv, false, false);
+    return __builtin_bit_cast(float, (threadIdx.x & 16) ? r[0] : r[1]);
+  } else {
+    auto r = __builtin_amdgcn_permlane32_swap(iv, iv, false, false);
+    return __builtin_bit_cast(float, (threadIdx.x & 32) ? r[0] : r[1]);
+  }
+}
+
+// One butterfly level on lane bit M: v_i <- v_i + v_{i^M}.  IEEE addition is
+// commutative, so lanes i and i^M produce identical bits.
+template <int M> __device__ __forceinline__ float bfly(float v) { return v + xor_partner<M>(v); }
+
+// Butterfly sum over lane bits [m_begin, m_end) (wave-uniform powers of two), levels
+// in increasing order: every participating lane ends with
+// T(a[0..n)) = T(a[0..n/2)) + T(a[n/2..n)).  All 64 lanes must be active.
 __device__ __forceinline__ float xor_sum(float v, int m_begin, int m_end) {
-  for (int m = m_begin; m < m_end; m <<= 1) v = v + __shfl_xor(v, m, 64);
+  if (m_begin <= 1 && m_end > 1) v = bfly<1>(v);
+  if (m_begin <= 2 && m_end > 2) v = bfly<2>(v);
+  if (m_begin <= 4 && m_end > 4) v = bfly<4>(v);
+  if (m_begin <= 8 && m_end > 8) v = bfly<8>(v);
+  if (m_begin <= 16 && m_end > 16) v = bfly<16>(v);
+  if (m_begin <= 32 && m_end > 32) v = bfly<32>(v);
   return v;
+}
+
+// Reduce-scatter level on lane bit M for NV per-lane values (one per row): lanes
+// with bit M clear keep values [0, NV/2), lanes with it set keep [NV/2, NV); each
+// kept value becomes own + partner's value of the same row.  The additions are the
+// butterfly's additions for that row, only spread over fewer lanes.
+template <int NV, int M>
+__device__ __forceinline__ void rs_level(const float* in, float* out) {
+  const bool hi = (threadIdx.x & M) != 0;
+#pragma unroll
+  for (int i = 0; i < NV / 2; i++) {
+    const float keep = hi ? in[NV / 2 + i] : in[i];
+    const float give = hi ? in[i] : in[NV / 2 + i];
+    out[i] = keep + xor_partner<M>(give);
+  }
 }
 
 // exp(x) for binary32, reproducible bit for bit on the CPU: Cody-Waite reduction

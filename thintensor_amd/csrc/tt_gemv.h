@@ -71,6 +71,14 @@ __device__ __forceinline__ float xv(const uint32_t* xw, int e) {
 }
 
 __device__ __forceinline__ h2 as_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }
+
+// (a & mask) | bits in one VALU op (v_and_or_b32).  The compiler splits this into
+// v_and + v_or when both constants are literals, so it is spelled out here.
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t bits) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(mask), "v"(bits));
+  return r;
+}
 __device__ __forceinline__ h2 hfma(h2 a, float b, float c) {
   return __builtin_elementwise_fma(a, (h2){(_Float16)b, (_Float16)b}, (h2){(_Float16)c, (_Float16)c});
 }
@@ -79,16 +87,21 @@ __device__ __forceinline__ h2 hfma(h2 a, float b, float c) {
 // (w & 0x000F000F) | 0x6400 6400 encodes 1024 + c; (w & 0x00F000F0) encodes 1024 + 16c.
 __device__ __forceinline__ void nib_pairs(uint32_t w, float off, h2& a, h2& b, h2& c, h2& d) {
   uint32_t w8 = w >> 8;
-  a = hfma(as_h2((w & 0x000F000Fu) | 0x64006400u), 1.0f, -(1024.0f + off));
-  b = hfma(as_h2((w & 0x00F000F0u) | 0x64006400u), 0.0625f, -(64.0f + off));
-  c = hfma(as_h2((w8 & 0x000F000Fu) | 0x64006400u), 1.0f, -(1024.0f + off));
-  d = hfma(as_h2((w8 & 0x00F000F0u) | 0x64006400u), 0.0625f, -(64.0f + off));
+  a = hfma(as_h2(and_or(w, 0x000F000Fu, 0x64006400u)), 1.0f, -(1024.0f + off));
+  b = hfma(as_h2(and_or(w, 0x00F000F0u, 0x64006400u)), 0.0625f, -(64.0f + off));
+  c = hfma(as_h2(and_or(w8, 0x000F000Fu, 0x64006400u)), 1.0f, -(1024.0f + off));
+  d = hfma(as_h2(and_or(w8, 0x00F000F0u, 0x64006400u)), 0.0625f, -(64.0f + off));
 }
 
-// Chunk partial: fma chain over the 32 elements of one chunk in ascending k.
-template <Fmt F, typename XT>
-__device__ __forceinline__ float chunk_dot(const Raw<FmtInfo<F>::kBytes>& r, const uint32_t* xw) {
-  float p = 0.0f;
+// Decoded weights of one chunk, element e of the chunk in wv[e] (exact values; MXFP4
+// carries an extra 2^-14).  Formats whose values fit binary16 exactly decode to
+// _Float16 so the fma consumes them through v_fma_mix without a conversion.
+template <Fmt F> struct WVal { using T = _Float16; };
+template <> struct WVal<Fmt::kFp8> { using T = float; };
+template <> struct WVal<Fmt::kBF16W> { using T = float; };
+
+template <Fmt F>
+__device__ __forceinline__ void decode_chunk(const Raw<FmtInfo<F>::kBytes>& r, typename WVal<F>::T* wv) {
   if constexpr (F == Fmt::kInt4Sym || F == Fmt::kInt4Aff) {
     // byte b holds k = 2b (low nibble) and k = 2b + 1 (high nibble); word i holds
     // k = 8i .. 8i+7 with nibble n at bits 4n.
@@ -97,14 +110,8 @@ __device__ __forceinline__ float chunk_dot(const Raw<FmtInfo<F>::kBytes>& r, con
     for (int i = 0; i < 4; i++) {
       h2 a, b, c, d;
       nib_pairs(r.w[i], off, a, b, c, d);
-      p = __builtin_fmaf((float)a[0], xv<XT>(xw, 8 * i + 0), p);
-      p = __builtin_fmaf((float)b[0], xv<XT>(xw, 8 * i + 1), p);
-      p = __builtin_fmaf((float)c[0], xv<XT>(xw, 8 * i + 2), p);
-      p = __builtin_fmaf((float)d[0], xv<XT>(xw, 8 * i + 3), p);
-      p = __builtin_fmaf((float)a[1], xv<XT>(xw, 8 * i + 4), p);
-      p = __builtin_fmaf((float)b[1], xv<XT>(xw, 8 * i + 5), p);
-      p = __builtin_fmaf((float)c[1], xv<XT>(xw, 8 * i + 6), p);
-      p = __builtin_fmaf((float)d[1], xv<XT>(xw, 8 * i + 7), p);
+      wv[8 * i + 0] = a[0]; wv[8 * i + 1] = b[0]; wv[8 * i + 2] = c[0]; wv[8 * i + 3] = d[0];
+      wv[8 * i + 4] = a[1]; wv[8 * i + 5] = b[1]; wv[8 * i + 6] = c[1]; wv[8 * i + 7] = d[1];
     }
   } else if constexpr (F == Fmt::kMxfp4) {
     // e2m1 nibble (s e1 e0 m) -> fp16 bits s<<15 | (e1 e0 m)<<9, which is the e2m1
@@ -112,20 +119,14 @@ __device__ __forceinline__ float chunk_dot(const Raw<FmtInfo<F>::kBytes>& r, con
     // factor is restored together with the block scale.
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      uint32_t w = r.w[i];
-      h2 a = as_h2(((w & 0x00070007u) << 9) | ((w & 0x00080008u) << 12));   // k 8i+0, 8i+4
-      h2 b = as_h2(((w & 0x00700070u) << 5) | ((w & 0x00800080u) << 8));    // k 8i+1, 8i+5
-      uint32_t w8 = w >> 8;
-      h2 c = as_h2(((w8 & 0x00070007u) << 9) | ((w8 & 0x00080008u) << 12)); // k 8i+2, 8i+6
-      h2 d = as_h2(((w8 & 0x00700070u) << 5) | ((w8 & 0x00800080u) << 8));  // k 8i+3, 8i+7
-      p = __builtin_fmaf((float)a[0], xv<XT>(xw, 8 * i + 0), p);
-      p = __builtin_fmaf((float)b[0], xv<XT>(xw, 8 * i + 1), p);
-      p = __builtin_fmaf((float)c[0], xv<XT>(xw, 8 * i + 2), p);
-      p = __builtin_fmaf((float)d[0], xv<XT>(xw, 8 * i + 3), p);
-      p = __builtin_fmaf((float)a[1], xv<XT>(xw, 8 * i + 4), p);
-      p = __builtin_fmaf((float)b[1], xv<XT>(xw, 8 * i + 5), p);
-      p = __builtin_fmaf((float)c[1], xv<XT>(xw, 8 * i + 6), p);
-      p = __builtin_fmaf((float)d[1], xv<XT>(xw, 8 * i + 7), p);
+      const uint32_t w = r.w[i];
+      const uint32_t w8 = w >> 8;
+      h2 a = as_h2(((w & 0x00070007u) << 9) | ((w & 0x00080008u) << 12));    // k 8i+0, 8i+4
+      h2 b = as_h2(((w & 0x00700070u) << 5) | ((w & 0x00800080u) << 8));     // k 8i+1, 8i+5
+      h2 c = as_h2(((w8 & 0x00070007u) << 9) | ((w8 & 0x00080008u) << 12));  // k 8i+2, 8i+6
+      h2 d = as_h2(((w8 & 0x00700070u) << 5) | ((w8 & 0x00800080u) << 8));   // k 8i+3, 8i+7
+      wv[8 * i + 0] = a[0]; wv[8 * i + 1] = b[0]; wv[8 * i + 2] = c[0]; wv[8 * i + 3] = d[0];
+      wv[8 * i + 4] = a[1]; wv[8 * i + 5] = b[1]; wv[8 * i + 6] = c[1]; wv[8 * i + 7] = d[1];
     }
   } else if constexpr (F == Fmt::kFp8) {
     // 32 bytes, byte e = element e; e4m3fn -> f32 is exact.
@@ -133,23 +134,19 @@ __device__ __forceinline__ float chunk_dot(const Raw<FmtInfo<F>::kBytes>& r, con
     for (int i = 0; i < 8; i++) {
       auto lo = __builtin_amdgcn_cvt_pk_f32_fp8(r.w[i], false);
       auto hi = __builtin_amdgcn_cvt_pk_f32_fp8(r.w[i], true);
-      p = __builtin_fmaf(lo[0], xv<XT>(xw, 4 * i + 0), p);
-      p = __builtin_fmaf(lo[1], xv<XT>(xw, 4 * i + 1), p);
-      p = __builtin_fmaf(hi[0], xv<XT>(xw, 4 * i + 2), p);
-      p = __builtin_fmaf(hi[1], xv<XT>(xw, 4 * i + 3), p);
+      wv[4 * i + 0] = lo[0]; wv[4 * i + 1] = lo[1]; wv[4 * i + 2] = hi[0]; wv[4 * i + 3] = hi[1];
     }
   } else if constexpr (F == Fmt::kF16W) {
 #pragma unroll
     for (int i = 0; i < 16; i++) {
       h2 v = as_h2(r.w[i]);
-      p = __builtin_fmaf((float)v[0], xv<XT>(xw, 2 * i + 0), p);
-      p = __builtin_fmaf((float)v[1], xv<XT>(xw, 2 * i + 1), p);
+      wv[2 * i] = v[0]; wv[2 * i + 1] = v[1];
     }
   } else if constexpr (F == Fmt::kBF16W) {
 #pragma unroll
     for (int i = 0; i < 16; i++) {
-      p = __builtin_fmaf(lo_f32<bf16_t>(r.w[i]), xv<XT>(xw, 2 * i + 0), p);
-      p = __builtin_fmaf(hi_f32<bf16_t>(r.w[i]), xv<XT>(xw, 2 * i + 1), p);
+      wv[2 * i] = lo_f32<bf16_t>(r.w[i]);
+      wv[2 * i + 1] = hi_f32<bf16_t>(r.w[i]);
     }
   } else if constexpr (F == Fmt::kQ2E8 || F == Fmt::kQ2Aff) {
     // 8 bytes; element i at byte i/4, bits 2*(i%4), so word q holds elements
@@ -161,31 +158,18 @@ __device__ __forceinline__ float chunk_dot(const Raw<FmtInfo<F>::kBytes>& r, con
     for (int q = 0; q < 2; q++) {
       const uint32_t u0 = r.w[q] << 2;   // elements 0..3 | 8..11 of this word
       const uint32_t u1 = r.w[q] >> 6;   // elements 4..7 | 12..15
-      h2 a0 = hfma(as_h2((u0 & 0x000C000Cu) | 0x64006400u), 0.25f, -(256.0f + off));
-      h2 a1 = hfma(as_h2((u0 & 0x00300030u) | 0x64006400u), 0.0625f, -(64.0f + off));
-      h2 a2 = hfma(as_h2((u0 & 0x00C000C0u) | 0x64006400u), 0.015625f, -(16.0f + off));
-      h2 a3 = hfma(as_h2((u0 & 0x03000300u) | 0x64006400u), 0.00390625f, -(4.0f + off));
-      h2 b0 = hfma(as_h2((u1 & 0x000C000Cu) | 0x64006400u), 0.25f, -(256.0f + off));
-      h2 b1 = hfma(as_h2((u1 & 0x00300030u) | 0x64006400u), 0.0625f, -(64.0f + off));
-      h2 b2 = hfma(as_h2((u1 & 0x00C000C0u) | 0x64006400u), 0.015625f, -(16.0f + off));
-      h2 b3 = hfma(as_h2((u1 & 0x03000300u) | 0x64006400u), 0.00390625f, -(4.0f + off));
-      const int e = 16 * q;
-      p = __builtin_fmaf((float)a0[0], xv<XT>(xw, e + 0), p);
-      p = __builtin_fmaf((float)a1[0], xv<XT>(xw, e + 1), p);
-      p = __builtin_fmaf((float)a2[0], xv<XT>(xw, e + 2), p);
-      p = __builtin_fmaf((float)a3[0], xv<XT>(xw, e + 3), p);
-      p = __builtin_fmaf((float)b0[0], xv<XT>(xw, e + 4), p);
-      p = __builtin_fmaf((float)b1[0], xv<XT>(xw, e + 5), p);
-      p = __builtin_fmaf((float)b2[0], xv<XT>(xw, e + 6), p);
-      p = __builtin_fmaf((float)b3[0], xv<XT>(xw, e + 7), p);
-      p = __builtin_fmaf((float)a0[1], xv<XT>(xw, e + 8), p);
-      p = __builtin_fmaf((float)a1[1], xv<XT>(xw, e + 9), p);
-      p = __builtin_fmaf((float)a2[1], xv<XT>(xw, e + 10), p);
-      p = __builtin_fmaf((float)a3[1], xv<XT>(xw, e + 11), p);
-      p = __builtin_fmaf((float)b0[1], xv<XT>(xw, e + 12), p);
-      p = __builtin_fmaf((float)b1[1], xv<XT>(xw, e + 13), p);
-      p = __builtin_fmaf((float)b2[1], xv<XT>(xw, e + 14), p);
-      p = __builtin_fmaf((float)b3[1], xv<XT>(xw, e + 15), p);
+      const uint32_t m[4] = {0x000C000Cu, 0x00300030u, 0x00C000C0u, 0x03000300u};
+      const float k[4] = {0.25f, 0.0625f, 0.015625f, 0.00390625f};
+      const float c[4] = {256.0f, 64.0f, 16.0f, 4.0f};
+#pragma unroll
+      for (int f = 0; f < 4; f++) {
+        h2 a = hfma(as_h2(and_or(u0, m[f], 0x64006400u)), k[f], -(c[f] + off));
+        h2 b = hfma(as_h2(and_or(u1, m[f], 0x64006400u)), k[f], -(c[f] + off));
+        wv[16 * q + f] = a[0];
+        wv[16 * q + 4 + f] = b[0];
+        wv[16 * q + 8 + f] = a[1];
+        wv[16 * q + 12 + f] = b[1];
+      }
     }
   } else if constexpr (F == Fmt::kQ1E8 || F == Fmt::kQ1Aff) {
     // 4 bytes; element i at byte i/8, bit i%8, i.e. bit i of the word.  Bits move
@@ -193,73 +177,109 @@ __device__ __forceinline__ float chunk_dot(const Raw<FmtInfo<F>::kBytes>& r, con
     // 1024 + 2^n' b.  E8M0 q1 maps b to 2b - 1, the affine form keeps b.
     const uint32_t w = r.w[0];
 #pragma unroll
-    for (int quarter = 0; quarter < 4; quarter++) {
-      const uint32_t u = (quarter & 1) ? (w >> 7) : (w << 1);
-      const int hi = quarter >> 1;
+    for (int half = 0; half < 2; half++) {
+      const uint32_t u = half ? (w >> 7) : (w << 1);   // elements 8*half + n | 16 + 8*half + n
 #pragma unroll
       for (int n = 1; n <= 8; n++) {
-        h2 t = as_h2((u & (0x00010001u << n)) | 0x64006400u);
+        h2 t = as_h2(and_or(u, 0x00010001u << n, 0x64006400u));
         h2 v;
         if constexpr (F == Fmt::kQ1E8)
           v = hfma(t, 2.0f / (float)(1 << n), -(2048.0f / (float)(1 << n) + 1.0f));
         else
           v = hfma(t, 1.0f / (float)(1 << n), -(1024.0f / (float)(1 << n)));
-        p = __builtin_fmaf((float)v[hi], xv<XT>(xw, 8 * quarter + n - 1), p);
+        wv[8 * half + n - 1] = v[0];
+        wv[16 + 8 * half + n - 1] = v[1];
       }
     }
   }
+}
+
+// Chunk partials of NR rows: for each row an fma chain over the chunk's 32 elements
+// in ascending k, starting from +0.  The rows' chains are interleaved element by
+// element so no fma waits on the one issued just before it.
+template <Fmt F, typename XT, int NR>
+__device__ __forceinline__ void chunk_dot_rows(const Raw<FmtInfo<F>::kBytes>* r, const uint32_t* xw, float* p) {
+  typename WVal<F>::T wv[NR][32];
+#pragma unroll
+  for (int i = 0; i < NR; i++) decode_chunk<F>(r[i], wv[i]);
+#pragma unroll
+  for (int i = 0; i < NR; i++) p[i] = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 32; e++) {
+    const float xe = xv<XT>(xw, e);
+#pragma unroll
+    for (int i = 0; i < NR; i++) p[i] = __builtin_fmaf((float)wv[i][e], xe, p[i]);
+  }
+}
+
+template <Fmt F, typename XT>
+__device__ __forceinline__ float chunk_dot(const Raw<FmtInfo<F>::kBytes>& r, const uint32_t* xw) {
+  float p;
+  chunk_dot_rows<F, XT, 1>(&r, xw, &p);
   return p;
 }
 
 // Row values of NR rows in the E8M0 block-scale order (one 32-element block per
 // chunk): t_j = (p_j * 2^extra) * 2^(e_j - 127), A = ((+0 + t_round0) + ...),
 // value = xor-butterfly over the LPR lanes.  `xs` is the activation vector in LDS.
-template <Fmt F, typename XT, int LPR, int NR>
-__device__ __forceinline__ void e8_rows_dot(const uint8_t* const* wrow, const uint8_t* const* srow, const bool* rv,
-                                            const uint32_t* xs, int nchunks, int l, int e8_extra, float* out) {
+// Weights and exponents of round r+1 are loaded while round r is computed.
+template <Fmt F, int NR>
+struct E8Round {
+  Raw<FmtInfo<F>::kBytes> w[NR];
+  int e[NR];
+};
+
+template <Fmt F, int LPR, int NR>
+__device__ __forceinline__ void e8_fetch(E8Round<F, NR>& d, int r, int l, int nchunks, const uint8_t* const* wrow,
+                                         const uint8_t* const* srow, const bool* rv) {
   constexpr int B = FmtInfo<F>::kBytes;
+  const int j = r * LPR + l;
+  const bool cv = j < nchunks;
+#pragma unroll
+  for (int i = 0; i < NR; i++) {
+    if (cv && rv[i]) {
+      d.w[i] = load_raw<B>(wrow[i] + (int64_t)j * B);
+      d.e[i] = srow[i][j];
+    } else {
+#pragma unroll
+      for (int q = 0; q < B / 4; q++) d.w[i].w[q] = 0u;
+      d.e[i] = 127;
+    }
+  }
+}
+
+template <Fmt F, typename XT, int LPR, int NR>
+__device__ __forceinline__ void e8_rows_dot(E8Round<F, NR>& cur, const uint8_t* const* wrow, const uint8_t* const* srow,
+                                            const bool* rv, const uint32_t* xs, int nchunks, int l, int e8_extra,
+                                            float* out) {
   const int rounds = (nchunks + LPR - 1) / LPR;
   float acc[NR];
 #pragma unroll
   for (int i = 0; i < NR; i++) acc[i] = 0.0f;
   for (int r = 0; r < rounds; r++) {
+    E8Round<F, NR> nxt;
+    if (r + 1 < rounds) e8_fetch<F, LPR, NR>(nxt, r + 1, l, nchunks, wrow, srow, rv);
     const int j = r * LPR + l;
     const bool cv = j < nchunks;
     uint32_t xw[16];
-    if (cv) {
-      const uint4* xp = reinterpret_cast<const uint4*>(xs + j * 16);
+    {
+      const uint4* xp = reinterpret_cast<const uint4*>(xs + (cv ? j : 0) * 16);
 #pragma unroll
       for (int q = 0; q < 4; q++) {
         uint4 v = xp[q];
         xw[4 * q] = v.x; xw[4 * q + 1] = v.y; xw[4 * q + 2] = v.z; xw[4 * q + 3] = v.w;
       }
-    } else {
-#pragma unroll
-      for (int q = 0; q < 16; q++) xw[q] = 0u;
     }
-    Raw<B> raw[NR];
-    int ex[NR];
+    float pr[NR];
+    chunk_dot_rows<F, XT, NR>(cur.w, xw, pr);
 #pragma unroll
     for (int i = 0; i < NR; i++) {
-      if (cv && rv[i]) {
-        raw[i] = load_raw<B>(wrow[i] + (int64_t)j * B);
-        ex[i] = srow[i][j];
-      } else {
-#pragma unroll
-        for (int q = 0; q < B / 4; q++) raw[i].w[q] = 0u;
-        ex[i] = 127;
-      }
+      float q = pr[i];
+      if (e8_extra) q = q * pow2i(e8_extra);
+      const float t = q * pow2i(cur.e[i] - 127);
+      acc[i] = acc[i] + ((cv && rv[i]) ? t : 0.0f);
     }
-#pragma unroll
-    for (int i = 0; i < NR; i++) {
-      float t = 0.0f;
-      if (cv && rv[i]) {
-        float q = chunk_dot<F, XT>(raw[i], xw);
-        if (e8_extra) q = q * pow2i(e8_extra);
-        t = q * pow2i(ex[i] - 127);
-      }
-      acc[i] = acc[i] + t;
-    }
+    if (r + 1 < rounds) cur = nxt;
   }
 #pragma unroll
   for (int i = 0; i < NR; i++) out[i] = xor_sum(acc[i], 1, LPR);
