@@ -173,6 +173,13 @@ int tt_matvec_argmax(const void* weight, int w_dtype, int64_t w_row, const void*
                      void* logits, int logits_dtype, int64_t rows, int64_t cols, uint64_t* partials,
                      int64_t partials_capacity, int64_t* out_idx, float* out_val, void* stream);
 
+/* tt_multi_matvec with a per-matrix bias (nullable entries) fused into the
+ * epilogue: out = round(round(dot) + bias), identical to the runtime's GEMV followed
+ * by its in-place bias add (gpu_runtime.py:9100-9114, 9213-9221). */
+int tt_multi_matvec_bias(int count, const void* const* weights, int w_dtype, const int64_t* w_row,
+                         const int64_t* rows, const void* const* biases, const void* x, int x_dtype,
+                         void* out, int out_dtype, int64_t cols, void* stream);
+
 /* ---------------------------------------------------------------- norms / elementwise */
 
 /* out = x * (1 / sqrt(mean(x^2) + eps)) * (w + weight_offset)
@@ -203,26 +210,33 @@ int tt_weighted_expert_sum(const void* experts, int dtype, int64_t stride, int64
                            const void* scores, int score_dtype, void* out, int64_t width, void* stream);
 
 /* In-place RoPE of q [heads, D] and k [kv_heads, D] with cos/sin rows taken from a
- * [positions, D/2] table at the position read from position_dev (if non-null) or
- * `position`.  Replaces TritonDecodeBackend.rope_qk_inplace
+ * [table_rows, D/2] table at the position read from position_dev (if non-null) or
+ * `position`; a device position outside the table leaves q and k unchanged.  Replaces TritonDecodeBackend.rope_qk_inplace
  * (triton_kernels.py:5689-5714; kernel :2638-2687), with the position on the device. */
 int tt_rope_qk_inplace(void* q, void* k, int dtype, const void* cos_table, const void* sin_table,
-                       int64_t table_row, const int32_t* position_dev, int64_t position, int64_t heads,
-                       int64_t kv_heads, int64_t head_dim, void* stream);
+                       int64_t table_row, int64_t table_rows, const int32_t* position_dev, int64_t position,
+                       int64_t heads, int64_t kv_heads, int64_t head_dim, void* stream);
 
-/* out = embed[token] with the token read from token_dev (int64) if non-null.
+/* out = embed[token] with the token read from token_dev (int64) if non-null; a device
+ * token outside [0, vocab) leaves out unchanged.
  * Replaces the runtime's embedding row copy (gpu_runtime.py:11396-11427). */
-int tt_embedding(const void* embed, int64_t row_stride, const int64_t* token_dev, int64_t token, void* out,
-                 int64_t n, void* stream);
+int tt_embedding(const void* embed, int64_t row_stride, int64_t vocab, const int64_t* token_dev, int64_t token,
+                 void* out, int64_t n, void* stream);
 
-/* keys[h, pos, :] = k[h, :]; values[h, pos, :] = v[h, :] (16-bit elements).
+/* keys[h, pos, :] = k[h, :]; values[h, pos, :] = v[h, :] (16-bit elements); a device
+ * position outside [0, capacity) writes nothing.
  * Replaces PagedKVCache.append for a flat cache (gpu_runtime.py:4132-4229). */
 int tt_kv_append(const void* k, const void* v, void* keys, void* values, int64_t stride_head,
-                 int64_t stride_token, const int32_t* position_dev, int64_t position, int64_t kv_heads,
-                 int64_t head_dim, void* stream);
+                 int64_t stride_token, const int32_t* position_dev, int64_t position, int64_t capacity,
+                 int64_t kv_heads, int64_t head_dim, void* stream);
 
 /* position_dev[0] += step (keeps graph replays moving along the sequence). */
 int tt_advance_position(int32_t* position_dev, int32_t step, void* stream);
+
+/* history[position - base] = token, all read on the device (token log of graph
+ * replays); indices outside [0, capacity) are skipped. */
+int tt_record_token(const int64_t* token_dev, const int32_t* position_dev, const int32_t* base_dev,
+                    int64_t* history, int32_t capacity, void* stream);
 
 /* ---------------------------------------------------------------- attention / router */
 
@@ -230,8 +244,9 @@ int tt_advance_position(int32_t* position_dev, int32_t step, void* stream);
 int tt_attention_scratch_floats(int64_t heads, int64_t max_tokens, int64_t head_dim);
 
 /* Single-token GQA attention over keys/values [kv_heads, tokens, D] (strides in
- * elements) with optional sinks [heads]; the token count is read from tokens_dev
- * (int32) when non-null.  out [heads, D].
+ * elements) with optional sinks [heads]; the token count is `tokens`, or
+ * tokens_dev[0] + tokens when tokens_dev (int32) is non-null (a decode step passes its
+ * position and 1).  max_tokens bounds the count (it sizes the scratch).  out [heads, D].
  * Replaces TritonDecodeBackend.single_token_gqa_attention and
  * split_single_token_gqa_attention (triton_kernels.py:5228-5363; kernels :15-245). */
 int tt_single_token_gqa_attention(const void* q, const void* keys, const void* values, int dtype,

@@ -188,18 +188,23 @@ static float scale_get(const void* s, int sdtype, int64_t i) {
   return ((const float*)s)[i];
 }
 
+/* Decode the 32 weights of one chunk (values as fed to the fma). */
+static void chunk_weights(int fmt, const uint8_t* c, float* wv) {
+  for (int e = 0; e < 32; e++) wv[e] = chunk_weight(fmt, c, e);
+}
+
 /*
  * One output row in the kernels' reduction order (thintensor_amd/csrc/tt_gemv.h):
  * chunks of 32, chunk j -> lane j % lpr, round j / lpr; fma chain per chunk; group
  * butterfly and scale; sequential accumulation over rounds; final butterfly.
+ * xf: the activation vector already converted to binary32.
  */
-float tto_gemv_row(int fmt, int smode, const uint8_t* wrow, const void* srow, int sdtype, int64_t s_grp,
-                   int64_t s_pair, int aff_zero, int e8_extra, const void* x, int xdtype, int cols, int L,
-                   int lpr) {
+static float gemv_row_f(int fmt, int smode, const uint8_t* wrow, const void* srow, int sdtype, int64_t s_grp,
+                        int64_t s_pair, int aff_zero, int e8_extra, const float* xf, int cols, int L, int lpr) {
   const int B = fmt_bytes(fmt);
   const int nchunks = cols / 32;
   const int rounds = (nchunks + lpr - 1) / lpr;
-  float A[64], p[64], xs[64];
+  float A[64], p[64], xs[64], wv[32];
   for (int l = 0; l < lpr; l++) A[l] = 0.0f;
   for (int r = 0; r < rounds; r++) {
     for (int l = 0; l < lpr; l++) {
@@ -207,14 +212,15 @@ float tto_gemv_row(int fmt, int smode, const uint8_t* wrow, const void* srow, in
       p[l] = 0.0f;
       xs[l] = 0.0f;
       if (j < nchunks) {
-        const uint8_t* c = wrow + (int64_t)j * B;
+        chunk_weights(fmt, wrow + (int64_t)j * B, wv);
+        const float* xc = xf + 32 * (int64_t)j;
         float acc = 0.0f;
-        for (int e = 0; e < 32; e++) acc = fmaf(chunk_weight(fmt, c, e), act_get(x, xdtype, 32 * j + e), acc);
+        for (int e = 0; e < 32; e++) acc = fmaf(wv[e], xc[e], acc);
         p[l] = acc;
         if (smode == SM_GROUP_AFF) {
-          float s = 0.0f;
-          for (int e = 0; e < 32; e++) s = s + act_get(x, xdtype, 32 * j + e);
-          xs[l] = s;
+          float sx = 0.0f;
+          for (int e = 0; e < 32; e++) sx = sx + xc[e];
+          xs[l] = sx;
         }
       }
     }
@@ -260,6 +266,21 @@ float tto_gemv_row(int fmt, int smode, const uint8_t* wrow, const void* srow, in
   return v;
 }
 
+static float* to_f32_vec(const void* x, int xdtype, int n) {
+  float* xf = (float*)malloc(sizeof(float) * (size_t)n);
+  for (int i = 0; i < n; i++) xf[i] = act_get(x, xdtype, i);
+  return xf;
+}
+
+float tto_gemv_row(int fmt, int smode, const uint8_t* wrow, const void* srow, int sdtype, int64_t s_grp,
+                   int64_t s_pair, int aff_zero, int e8_extra, const void* x, int xdtype, int cols, int L,
+                   int lpr) {
+  float* xf = to_f32_vec(x, xdtype, cols);
+  const float v = gemv_row_f(fmt, smode, wrow, srow, sdtype, s_grp, s_pair, aff_zero, e8_extra, xf, cols, L, lpr);
+  free(xf);
+  return v;
+}
+
 /*
  * Generic GEMV over `rows` rows (optionally a selected expert and a per-slot
  * activation row).  w points at the first row of the chosen matrix/expert.
@@ -268,16 +289,16 @@ int tto_gemv(int fmt, int smode, const uint8_t* w, int64_t w_row_bytes, const vo
              int64_t s_grp, int64_t s_pair, int aff_zero, int e8_extra, const void* x, int xdtype, void* out,
              int odtype, int64_t rows, int cols, int L, int lpr) {
   if (cols % 32 || lpr < 1 || lpr > 64) return -1;
+  float* xf = to_f32_vec(x, xdtype, cols);
+  const size_t es = smode == SM_BLOCK_E8 ? 1 : (sdtype == TTO_F32 ? 4 : 2);
+#pragma omp parallel for schedule(static)
   for (int64_t n = 0; n < rows; n++) {
-    const void* srow = NULL;
-    if (s) {
-      const size_t es = smode == SM_BLOCK_E8 ? 1 : (sdtype == TTO_F32 ? 4 : 2);
-      srow = (const uint8_t*)s + (size_t)(n * s_row) * es;
-    }
-    const float v = tto_gemv_row(fmt, smode, w + n * w_row_bytes, srow, sdtype, s_grp, s_pair, aff_zero, e8_extra,
-                                 x, xdtype, cols, L, lpr);
+    const void* srow = s ? (const void*)((const uint8_t*)s + (size_t)(n * s_row) * es) : NULL;
+    const float v = gemv_row_f(fmt, smode, w + n * w_row_bytes, srow, sdtype, s_grp, s_pair, aff_zero, e8_extra, xf,
+                               cols, L, lpr);
     act_put(out, odtype, n, v);
   }
+  free(xf);
   return 0;
 }
 
@@ -300,13 +321,13 @@ int tto_swiglu(int fmt, int rt, const uint8_t* w, int64_t w_expert, int64_t w_ro
   for (int slot = 0; slot < selected; slot++) {
     const int64_t e = experts[slot];
     const void* xs = (const uint8_t*)x + (size_t)(slot * x_slot) * xes;
+    float* xf = to_f32_vec(xs, xdtype, cols);
+#pragma omp parallel for schedule(static)
     for (int a = 0; a < act_rows; a++) {
-      float g = tto_gemv_row(fmt, SM_BLOCK_E8, w + e * w_expert + (2 * (int64_t)a) * w_row,
-                             s + e * s_expert + (2 * (int64_t)a) * s_row, TTO_F32, 1, 0, 0, extra, xs, xdtype, cols, 1,
-                             lpr);
-      float u = tto_gemv_row(fmt, SM_BLOCK_E8, w + e * w_expert + (2 * (int64_t)a + 1) * w_row,
-                             s + e * s_expert + (2 * (int64_t)a + 1) * s_row, TTO_F32, 1, 0, 0, extra, xs, xdtype,
-                             cols, 1, lpr);
+      float g = gemv_row_f(fmt, SM_BLOCK_E8, w + e * w_expert + (2 * (int64_t)a) * w_row,
+                           s + e * s_expert + (2 * (int64_t)a) * s_row, TTO_F32, 1, 0, 0, extra, xf, cols, 1, lpr);
+      float u = gemv_row_f(fmt, SM_BLOCK_E8, w + e * w_expert + (2 * (int64_t)a + 1) * w_row,
+                           s + e * s_expert + (2 * (int64_t)a + 1) * s_row, TTO_F32, 1, 0, 0, extra, xf, cols, 1, lpr);
       g = round_rt(rt, g);
       u = round_rt(rt, u);
       if (bias) {
@@ -319,6 +340,7 @@ int tto_swiglu(int fmt, int rt, const uint8_t* w, int64_t w_expert, int64_t w_ro
       const float den = 1.0f + tto_exp_f32(-g * alpha);
       act_put(out, odtype, slot * out_slot + a, num / den);
     }
+    free(xf);
   }
   return 0;
 }
@@ -330,19 +352,23 @@ int tto_weighted_down(int fmt, int rt, const uint8_t* w, int64_t w_expert, int64
                       int bdtype, int64_t bias_expert, void* out, int odtype, int rows, int cols, int lpr) {
   const int extra = fmt == FMT_MXFP4 ? 14 : 0;
   const size_t xes = xdtype == TTO_F32 ? 4 : 2;
+  float* xf[64];
+  for (int slot = 0; slot < selected && slot < 64; slot++)
+    xf[slot] = to_f32_vec((const uint8_t*)x + (size_t)(slot * x_slot) * xes, xdtype, cols);
+#pragma omp parallel for schedule(static)
   for (int n = 0; n < rows; n++) {
     float combined = 0.0f;
     for (int slot = 0; slot < selected; slot++) {
       const int64_t e = experts[slot];
-      const void* xs = (const uint8_t*)x + (size_t)(slot * x_slot) * xes;
-      float v = tto_gemv_row(fmt, SM_BLOCK_E8, w + e * w_expert + (int64_t)n * w_row, s + e * s_expert + (int64_t)n * s_row,
-                             TTO_F32, 1, 0, 0, extra, xs, xdtype, cols, 1, lpr);
+      float v = gemv_row_f(fmt, SM_BLOCK_E8, w + e * w_expert + (int64_t)n * w_row, s + e * s_expert + (int64_t)n * s_row,
+                           TTO_F32, 1, 0, 0, extra, xf[slot], cols, 1, lpr);
       v = round_rt(rt, v);
       if (bias) v = round_rt(rt, v + act_get(bias, bdtype, e * bias_expert + n));
       combined = fmaf(v, act_get(scores, sdtype, slot), combined);
     }
     act_put(out, odtype, n, combined);
   }
+  for (int slot = 0; slot < selected && slot < 64; slot++) free(xf[slot]);
   return 0;
 }
 
@@ -462,10 +488,11 @@ int tto_attention(const void* q, const void* keys, const void* values, int dt, i
   const int G = heads / kv_heads;
   const int nc = (tokens + 63) / 64;
   const float scale = (float)(1.0 / sqrt((double)D));
-  float* pm = (float*)malloc(sizeof(float) * (size_t)nc);
-  float* pl = (float*)malloc(sizeof(float) * (size_t)nc);
-  float* po = (float*)malloc(sizeof(float) * (size_t)nc * (size_t)D);
+#pragma omp parallel for schedule(static)
   for (int h = 0; h < heads; h++) {
+    float* pm = (float*)malloc(sizeof(float) * (size_t)nc);
+    float* pl = (float*)malloc(sizeof(float) * (size_t)nc);
+    float* po = (float*)malloc(sizeof(float) * (size_t)nc * (size_t)D);
     const int kvh = h / G;
     for (int c = 0; c < nc; c++) {
       float s[64], p[64];
@@ -508,10 +535,10 @@ int tto_attention(const void* q, const void* keys, const void* values, int dt, i
       for (int c = 0; c < nc; c++) acc = fmaf(po[(size_t)c * D + d], tto_exp_f32(pm[c] - M), acc);
       act_put(out, dt, (int64_t)h * D + d, acc / den);
     }
+    free(pm);
+    free(pl);
+    free(po);
   }
-  free(pm);
-  free(pl);
-  free(po);
   return 0;
 }
 

@@ -41,6 +41,8 @@ SIGNATURES: dict[str, list] = {
                                      _L, _P],
     "tt_lowbit_affine_matvec": [_P, _L, _P, _L, _L, _I, _P, _I, _P, _I, _L, _L, _L, _P],
     "tt_int4_selected_matvec": [_P, _L, _L, _P, _I, _L, _L, _L, _P, _I, _L, _P, _L, _P, _I, _L, _L, _L, _L, _P],
+    "tt_multi_matvec_bias": [_I, _PP, _I, _LP, _LP, _PP, _P, _I, _P, _I, _L, _P],
+    "tt_record_token": [_P, _P, _P, _P, ctypes.c_int32, _P],
     "tt_matvec_argmax_partials": [_L, _L],
     "tt_matvec_argmax": [_P, _I, _L, _P, _I, _P, _I, _L, _L, _P, _L, _P, _P, _P],
     "tt_rms_norm": [_P, _I, _P, _I, _P, _I, _L, _F, _F, _P],
@@ -49,9 +51,9 @@ SIGNATURES: dict[str, list] = {
     "tt_silu_mul": [_P, _P, _P, _I, _L, _P],
     "tt_interleaved_swiglu": [_P, _L, _P, _L, _I, _L, _L, _F, _F, _P],
     "tt_weighted_expert_sum": [_P, _I, _L, _L, _P, _I, _P, _L, _P],
-    "tt_rope_qk_inplace": [_P, _P, _I, _P, _P, _L, _P, _L, _L, _L, _L, _P],
-    "tt_embedding": [_P, _L, _P, _L, _P, _L, _P],
-    "tt_kv_append": [_P, _P, _P, _P, _L, _L, _P, _L, _L, _L, _P],
+    "tt_rope_qk_inplace": [_P, _P, _I, _P, _P, _L, _L, _P, _L, _L, _L, _L, _P],
+    "tt_embedding": [_P, _L, _L, _P, _L, _P, _L, _P],
+    "tt_kv_append": [_P, _P, _P, _P, _L, _L, _P, _L, _L, _L, _L, _P],
     "tt_advance_position": [_P, ctypes.c_int32, _P],
     "tt_attention_scratch_floats": [_L, _L, _L],
     "tt_single_token_gqa_attention": [_P, _P, _P, _I, _L, _L, _L, _L, _P, _I, _P, _L, _L, _L, _L, _L, _P, _L, _P,

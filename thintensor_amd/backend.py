@@ -633,9 +633,9 @@ class HipDecodeBackend:
             raise ValueError(f"RoPE head_dim must be even, got {head_dim}")
         _require_cuda(q, k, cos, sin)
         if cos.ndim == 1:
-            table_row, pos_dev, pos = 0, None, 0
+            table_row, table_rows, pos_dev, pos = 0, 1, None, 0
         else:
-            table_row = cos.stride(0)
+            table_row, table_rows = cos.stride(0), int(cos.shape[0])
             if isinstance(position, torch.Tensor):
                 if position.dtype != torch.int32:
                     raise ValueError("device position must be int32")
@@ -643,7 +643,7 @@ class HipDecodeBackend:
             else:
                 pos_dev, pos = None, int(position or 0)
         rc = self.lib.tt_rope_qk_inplace(q.data_ptr(), k.data_ptr(), _code(q, "rope"), cos.data_ptr(), sin.data_ptr(),
-                                         table_row, pos_dev, pos, heads, kv_heads, head_dim, _stream(q))
+                                         table_row, table_rows, pos_dev, pos, heads, kv_heads, head_dim, _stream(q))
         _lib.check(rc, "rope_qk_inplace")
         return q, k
 
@@ -667,25 +667,31 @@ class HipDecodeBackend:
         active_tokens: torch.Tensor | int | None = None,
     ) -> torch.Tensor:
         """Decode attention over keys/values [kv_heads, tokens, head_dim]
-        (triton_kernels.py:5228-5278).  ``active_tokens`` may be an int32 device
-        scalar; the KV tensors then give the capacity."""
+        (triton_kernels.py:5228-5278).  ``active_tokens`` may be an int, an int32
+        device scalar holding the count, or ``(position_tensor, 1)`` meaning
+        position + 1 read on the device; the KV tensors give the capacity."""
         capacity = int(keys.shape[1])
+        offset = 0
         tokens = capacity if active_tokens is None else active_tokens
+        if isinstance(tokens, tuple):
+            tokens, offset = tokens
         if isinstance(tokens, int) and tokens <= 0:
             raise ValueError("attention requires at least one KV token")
         if head_dim > 256:
             raise ValueError("fused single-token attention supports head_dim <= 256")
         _require_cuda(query, keys, values, out)
         scratch = self._attention_scratch(heads, capacity, head_dim)
-        tok_dev = tokens.data_ptr() if isinstance(tokens, torch.Tensor) else None
-        if isinstance(tokens, torch.Tensor) and tokens.dtype != torch.int32:
-            raise ValueError("active_tokens device tensor must be int32")
+        if isinstance(tokens, torch.Tensor):
+            if tokens.dtype != torch.int32:
+                raise ValueError("active_tokens device tensor must be int32")
+            tok_dev, tok = tokens.data_ptr(), int(offset)
+        else:
+            tok_dev, tok = None, int(tokens)
         rc = self.lib.tt_single_token_gqa_attention(
             query.data_ptr(), keys.data_ptr(), values.data_ptr(), _code(keys, "attention"), keys.stride(0), keys.stride(1),
             values.stride(0), values.stride(1), sinks.data_ptr() if sinks is not None else None,
-            _code(sinks, "sinks") if sinks is not None else _lib.F16, tok_dev,
-            tokens if isinstance(tokens, int) else 0, capacity, heads, kv_heads, head_dim, scratch.data_ptr(),
-            scratch.numel(), out.data_ptr(), _stream(out),
+            _code(sinks, "sinks") if sinks is not None else _lib.F16, tok_dev, tok, capacity, heads, kv_heads, head_dim,
+            scratch.data_ptr(), scratch.numel(), out.data_ptr(), _stream(out),
         )
         _lib.check(rc, "single_token_gqa_attention")
         return out
@@ -746,7 +752,8 @@ class HipDecodeBackend:
             tok_dev, tok = token.data_ptr(), 0
         else:
             tok_dev, tok = None, int(token)
-        rc = self.lib.tt_embedding(embed.data_ptr(), embed.stride(0), tok_dev, tok, out.data_ptr(), out.numel(), _stream(out))
+        rc = self.lib.tt_embedding(embed.data_ptr(), embed.stride(0), int(embed.shape[0]), tok_dev, tok, out.data_ptr(),
+                                   out.numel(), _stream(out))
         _lib.check(rc, "embedding")
         return out
 
@@ -761,9 +768,31 @@ class HipDecodeBackend:
         else:
             pos_dev, pos = None, int(position)
         rc = self.lib.tt_kv_append(k.data_ptr(), v.data_ptr(), keys.data_ptr(), values.data_ptr(), keys.stride(0),
-                                   keys.stride(1), pos_dev, pos, kv_heads, head_dim, _stream(k))
+                                   keys.stride(1), pos_dev, pos, int(keys.shape[1]), kv_heads, head_dim, _stream(k))
         _lib.check(rc, "kv_append")
 
     def advance_position(self, position: torch.Tensor, step: int = 1) -> None:
         rc = self.lib.tt_advance_position(position.data_ptr(), int(step), _stream(position))
         _lib.check(rc, "advance_position")
+
+    def record_token(self, token: torch.Tensor, position: torch.Tensor, base: torch.Tensor, history: torch.Tensor) -> None:
+        """history[position - base] = token, all on the device (int64 / int32 / int32)."""
+        rc = self.lib.tt_record_token(token.data_ptr(), position.data_ptr(), base.data_ptr(), history.data_ptr(),
+                                      int(history.numel()), _stream(token))
+        _lib.check(rc, "record_token")
+
+    def multi_matvec_bias(self, weights: tuple[torch.Tensor, ...], biases: tuple[torch.Tensor | None, ...],
+                          x: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+        """multi_matvec followed by the per-matrix bias add, fused (same rounding as
+        GEMV-then-add_ in the runtime, gpu_runtime.py:9100-9114)."""
+        cols = int(weights[0].shape[1])
+        rows = [int(w.shape[0]) for w in weights]
+        _require_cuda(x, out, *weights)
+        rc = self.lib.tt_multi_matvec_bias(
+            len(weights), _lib.ptr_array([w.data_ptr() for w in weights]), _code(weights[0], "multi_matvec"),
+            _lib.i64_array([w.stride(0) for w in weights]), _lib.i64_array(rows),
+            _lib.ptr_array([b.data_ptr() if b is not None else None for b in biases]), x.data_ptr(),
+            _code(x, "multi_matvec"), out.data_ptr(), _code(out, "multi_matvec"), cols, _stream(out),
+        )
+        _lib.check(rc, "multi_matvec_bias")
+        return out

@@ -12,8 +12,10 @@
 //   * combine in chunk order: M = max(sink, m_c...), den starts at exp(sink - M)
 //     (or 0), den = fma(l_c, e_c, den), acc_d = fma(o_c[d], e_c, acc_d) with
 //     e_c = exp(m_c - M); out_d = acc_d / den.
-// The active token count may be read from device memory so graph replays follow
-// the growing cache; chunks past it exit without work.
+// The active token count may be read from device memory (count = tokens_dev[0] +
+// tokens, so a decode step can pass its position and 1) so graph replays follow the
+// growing cache; chunks past the count exit without work.  The count is clamped to
+// max_tokens so a runaway device counter can never read past the cache.
 #include "tt_abi_internal.h"
 #include "tt_common.h"
 
@@ -32,7 +34,7 @@ struct AttnParams {
   float* part_m;          // [heads, max_chunks]
   float* part_l;
   float* part_o;          // [heads, max_chunks, D]
-  int heads, kv_heads, head_dim, max_chunks;
+  int heads, kv_heads, head_dim, max_chunks, max_tokens;
   float scale;
   void* out;              // [heads, D]
 };
@@ -41,7 +43,7 @@ template <typename T, int G>
 __global__ __launch_bounds__(64) void attn_partial_kernel(AttnParams P) {
   const int kvh = blockIdx.y;
   const int c = blockIdx.x;
-  const int T_act = P.tokens_dev ? P.tokens_dev[0] : P.tokens;
+  const int T_act = min(P.tokens_dev ? P.tokens_dev[0] + P.tokens : P.tokens, P.max_tokens);
   if (c * kChunk >= T_act) return;
   const int D = P.head_dim;
   const int lane = threadIdx.x;
@@ -103,7 +105,7 @@ __global__ __launch_bounds__(64) void attn_partial_kernel(AttnParams P) {
 template <typename T, typename SKT>
 __global__ __launch_bounds__(64) void attn_combine_kernel(AttnParams P) {
   const int h = blockIdx.x;
-  const int T_act = P.tokens_dev ? P.tokens_dev[0] : P.tokens;
+  const int T_act = min(P.tokens_dev ? P.tokens_dev[0] + P.tokens : P.tokens, P.max_tokens);
   const int nc = (T_act + kChunk - 1) / kChunk;
   const float* pm = P.part_m + (int64_t)h * P.max_chunks;
   const float* pl = P.part_l + (int64_t)h * P.max_chunks;
@@ -158,6 +160,7 @@ extern "C" int tt_single_token_gqa_attention(const void* q, const void* keys, co
   TT_REQUIRE(head_dim > 0 && head_dim <= 256, "%s: fused single-token attention supports head_dim <= 256", what);
   TT_REQUIRE(heads > 0 && kv_heads > 0 && heads % kv_heads == 0, "%s: heads must be a multiple of kv_heads", what);
   TT_REQUIRE(tokens_dev != nullptr || (tokens > 0 && tokens <= max_tokens), "%s: attention requires at least one KV token", what);
+  TT_REQUIRE(tokens_dev == nullptr || (tokens >= 0 && tokens <= 1), "%s: device token count offset must be 0 or 1", what);
   TT_REQUIRE(max_tokens > 0, "%s: bad max_tokens", what);
   const int64_t chunks = (max_tokens + kChunk - 1) / kChunk;
   TT_REQUIRE(scratch_floats >= heads * chunks * (2 + head_dim), "%s: scratch too small", what);
@@ -170,6 +173,7 @@ extern "C" int tt_single_token_gqa_attention(const void* q, const void* keys, co
   P.part_l = scratch + heads * chunks;
   P.part_o = scratch + 2 * heads * chunks;
   P.heads = (int)heads; P.kv_heads = (int)kv_heads; P.head_dim = (int)head_dim; P.max_chunks = (int)chunks;
+  P.max_tokens = (int)max_tokens;
   P.scale = (float)(1.0 / __builtin_sqrt((double)head_dim));
   P.out = out;
   const int G = (int)(heads / kv_heads);

@@ -28,9 +28,9 @@ extern "C" int tt_scaled_matvec(const void* weight, int64_t w_row_bytes, const v
   return launch_types<Fmt::kFp8, SMode::kRow, float, 4>(x_dtype, out_dtype, Lg, lpr, P, 1, st, what);
 }
 
-extern "C" int tt_multi_matvec(int count, const void* const* weights, int w_dtype, const int64_t* w_row,
-                               const int64_t* rows, const void* x, int x_dtype, void* out, int out_dtype,
-                               int64_t cols, void* stream) {
+extern "C" int tt_multi_matvec_bias(int count, const void* const* weights, int w_dtype, const int64_t* w_row,
+                                    const int64_t* rows, const void* const* biases, const void* x, int x_dtype,
+                                    void* out, int out_dtype, int64_t cols, void* stream) {
   const char* what = "matvec";
   TT_REQUIRE(count >= 1 && count <= 3, "%s: supports one to three matrices", what);
   TT_REQUIRE(w_dtype == TT_F16 || w_dtype == TT_BF16, "%s: weights must be fp16 or bf16", what);
@@ -49,7 +49,7 @@ extern "C" int tt_multi_matvec(int count, const void* const* weights, int w_dtyp
     TT_REQUIRE(weights[i] && aligned(weights[i], 16) && (w_row[i] * 2) % 16 == 0 && w_row[i] >= cols,
                "%s: weights must be 16-byte aligned with a row stride that is a multiple of 8 elements", what);
     P.seg[i] = Seg{static_cast<const uint8_t*>(weights[i]), w_row[i] * 2, nullptr, 0, 0,
-                   static_cast<char*>(out) + acc_rows * osz, (int)rows[i]};
+                   static_cast<char*>(out) + acc_rows * osz, (int)rows[i], 0, biases ? biases[i] : nullptr};
     acc_rows += rows[i];
   }
   TT_REQUIRE(acc_rows < (1LL << 30), "%s: too many rows", what);
@@ -60,6 +60,12 @@ extern "C" int tt_multi_matvec(int count, const void* const* weights, int w_dtyp
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (w_dtype == TT_F16) return launch_types<Fmt::kF16W, SMode::kNone, float, 2>(x_dtype, out_dtype, Lg, lpr, P, 1, st, what);
   return launch_types<Fmt::kBF16W, SMode::kNone, float, 2>(x_dtype, out_dtype, Lg, lpr, P, 1, st, what);
+}
+
+extern "C" int tt_multi_matvec(int count, const void* const* weights, int w_dtype, const int64_t* w_row,
+                               const int64_t* rows, const void* x, int x_dtype, void* out, int out_dtype,
+                               int64_t cols, void* stream) {
+  return tt_multi_matvec_bias(count, weights, w_dtype, w_row, rows, nullptr, x, x_dtype, out, out_dtype, cols, stream);
 }
 
 extern "C" int tt_matvec(const void* weight, int w_dtype, int64_t w_row, const void* x, int x_dtype, void* out,

@@ -27,6 +27,7 @@ struct Seg {
   void* out;            // output (slot 0)
   int rows;
   int vbegin;           // first virtual row (batches never straddle segments)
+  const void* bias;     // optional per-row bias in the output dtype: out = r(r(dot) + b)
 };
 
 struct GemvParams {
@@ -110,6 +111,7 @@ struct GemvBatch {
   const ST* sb;
   int64_t s_row, s_grp;
   void* out;
+  const void* bias;
   int64_t woffs[ROWS];
   int rcl[ROWS];
   bool rv[ROWS];
@@ -173,6 +175,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
     bt.s_row = S.s_row;
     bt.s_grp = S.s_grp;
     bt.out = S.out;
+    bt.bias = S.bias;
 #pragma unroll
     for (int i = 0; i < ROWS; i++) {
       const int r = i * SUBS + sub;
@@ -288,6 +291,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
     float v = acc[0];
     const bool ok = fstore && cb.lr0 + frow < cb.rows;
     if constexpr (SM == SMode::kRow) v = v * to_f32(cb.sb[(int64_t)(ok ? frow : 0) * cb.s_row]);
+    if (cb.bias != nullptr && ok) v = round_to<OT>(v) + to_f32(reinterpret_cast<const OT*>(cb.bias)[cb.lr0 + frow]);
     if (ok && cb.out != nullptr) store<OT>(reinterpret_cast<OT*>(cb.out) + (int64_t)slot * P.out_slot + cb.lr0 + frow, v);
     if constexpr (AM) {
       if (ok) {

@@ -117,10 +117,11 @@ __global__ void weighted_expert_sum_kernel(const void* ex, const void* scores, v
 // cos/sin rows come from a table indexed by the token position, which may be read
 // from device memory (pos_dev) so graph replays advance with the position.
 template <typename T>
-__global__ void rope_kernel(void* q, void* k, const void* cos_t, const void* sin_t, int64_t table_row,
+__global__ void rope_kernel(void* q, void* k, const void* cos_t, const void* sin_t, int64_t table_row, int64_t table_rows,
                             const int32_t* pos_dev, int pos, int heads, int kv_heads, int head_dim) {
   const int half = head_dim >> 1;
   const int64_t p = pos_dev ? (int64_t)pos_dev[0] : (int64_t)pos;
+  if (p < 0 || p >= table_rows) return;
   const int total = (heads + kv_heads) * half;
   const int idx = blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= total) return;
@@ -138,17 +139,19 @@ __global__ void rope_kernel(void* q, void* k, const void* cos_t, const void* sin
 
 // ---------------------------------------------------------------- embedding / KV
 // out = embed[token] (row copy), token read from device memory when token_dev is set.
-__global__ void embed_kernel(const uint16_t* embed, int64_t row, const int64_t* token_dev, int64_t token, uint16_t* out,
-                             int n) {
+__global__ void embed_kernel(const uint16_t* embed, int64_t row, int64_t vocab, const int64_t* token_dev, int64_t token,
+                             uint16_t* out, int n) {
   const int64_t t = token_dev ? token_dev[0] : token;
+  if (t < 0 || t >= vocab) return;
   for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) out[i] = embed[t * row + i];
 }
 
 // keys[h, pos, :] = k[h, :], values[h, pos, :] = v[h, :]
 __global__ void kv_append_kernel(const uint16_t* k, const uint16_t* v, uint16_t* keys, uint16_t* values,
-                                 int64_t stride_h, int64_t stride_t, const int32_t* pos_dev, int pos, int kv_heads,
-                                 int head_dim) {
+                                 int64_t stride_h, int64_t stride_t, const int32_t* pos_dev, int pos, int64_t capacity,
+                                 int kv_heads, int head_dim) {
   const int64_t p = pos_dev ? (int64_t)pos_dev[0] : (int64_t)pos;
+  if (p < 0 || p >= capacity) return;
   const int idx = blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= kv_heads * head_dim) return;
   const int h = idx / head_dim, d = idx - h * head_dim;
@@ -158,6 +161,15 @@ __global__ void kv_append_kernel(const uint16_t* k, const uint16_t* v, uint16_t*
 
 __global__ void advance_position_kernel(int32_t* pos, int32_t step) {
   if (threadIdx.x == 0) pos[0] += step;
+}
+
+// history[pos - base] = token (all read on the device)
+__global__ void record_token_kernel(const int64_t* token, const int32_t* pos, const int32_t* base, int64_t* history,
+                                    int32_t capacity) {
+  if (threadIdx.x == 0) {
+    const int32_t i = pos[0] - base[0];
+    if (i >= 0 && i < capacity) history[i] = token[0];
+  }
 }
 
 template <typename Fn> static int with_act(int code, Fn&& f) {
@@ -259,37 +271,41 @@ extern "C" int tt_weighted_expert_sum(const void* experts, int dtype, int64_t st
 }
 
 extern "C" int tt_rope_qk_inplace(void* q, void* k, int dtype, const void* cos_table, const void* sin_table,
-                                  int64_t table_row, const int32_t* position_dev, int64_t position, int64_t heads,
-                                  int64_t kv_heads, int64_t head_dim, void* stream) {
+                                  int64_t table_row, int64_t table_rows, const int32_t* position_dev, int64_t position,
+                                  int64_t heads, int64_t kv_heads, int64_t head_dim, void* stream) {
   TT_REQUIRE(q && k && cos_table && sin_table && head_dim > 0 && head_dim % 2 == 0, "rope: RoPE head_dim must be even");
   TT_REQUIRE(heads > 0 && kv_heads >= 0, "rope: bad head counts");
+  TT_REQUIRE(table_rows > 0 && (position_dev != nullptr || (position >= 0 && position < table_rows)),
+             "rope: position outside the cos/sin table");
   const int total = (int)((heads + kv_heads) * (head_dim / 2));
   return with_act(dtype, [&](auto t) {
     using T = decltype(t);
     hipLaunchKernelGGL((rope_kernel<T>), dim3((total + 255) / 256), dim3(256), 0, static_cast<hipStream_t>(stream), q, k,
-                       cos_table, sin_table, table_row, position_dev, (int)position, (int)heads, (int)kv_heads,
+                       cos_table, sin_table, table_row, table_rows, position_dev, (int)position, (int)heads, (int)kv_heads,
                        (int)head_dim);
     return check_launch("rope_qk_inplace");
   });
 }
 
-extern "C" int tt_embedding(const void* embed, int64_t row_stride, const int64_t* token_dev, int64_t token, void* out,
-                            int64_t n, void* stream) {
-  TT_REQUIRE(embed && out && n > 0, "embedding: bad arguments");
+extern "C" int tt_embedding(const void* embed, int64_t row_stride, int64_t vocab, const int64_t* token_dev,
+                            int64_t token, void* out, int64_t n, void* stream) {
+  TT_REQUIRE(embed && out && n > 0 && vocab > 0, "embedding: bad arguments");
+  TT_REQUIRE(token_dev != nullptr || (token >= 0 && token < vocab), "embedding: token id out of range");
   hipLaunchKernelGGL(embed_kernel, dim3((unsigned)((n + 255) / 256 < 64 ? (n + 255) / 256 : 64)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(embed), row_stride, token_dev, token,
+                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(embed), row_stride, vocab, token_dev, token,
                      static_cast<uint16_t*>(out), (int)n);
   return check_launch("embedding");
 }
 
 extern "C" int tt_kv_append(const void* k, const void* v, void* keys, void* values, int64_t stride_head,
-                            int64_t stride_token, const int32_t* position_dev, int64_t position, int64_t kv_heads,
-                            int64_t head_dim, void* stream) {
-  TT_REQUIRE(k && v && keys && values && kv_heads > 0 && head_dim > 0, "kv_append: bad arguments");
+                            int64_t stride_token, const int32_t* position_dev, int64_t position, int64_t capacity,
+                            int64_t kv_heads, int64_t head_dim, void* stream) {
+  TT_REQUIRE(k && v && keys && values && kv_heads > 0 && head_dim > 0 && capacity > 0, "kv_append: bad arguments");
+  TT_REQUIRE(position_dev != nullptr || (position >= 0 && position < capacity), "kv_append: position beyond the cache");
   const int total = (int)(kv_heads * head_dim);
   hipLaunchKernelGGL(kv_append_kernel, dim3((total + 255) / 256), dim3(256), 0, static_cast<hipStream_t>(stream),
                      static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v), static_cast<uint16_t*>(keys),
-                     static_cast<uint16_t*>(values), stride_head, stride_token, position_dev, (int)position,
+                     static_cast<uint16_t*>(values), stride_head, stride_token, position_dev, (int)position, capacity,
                      (int)kv_heads, (int)head_dim);
   return check_launch("kv_append");
 }
@@ -298,4 +314,12 @@ extern "C" int tt_advance_position(int32_t* position_dev, int32_t step, void* st
   TT_REQUIRE(position_dev != nullptr, "advance_position: null pointer");
   hipLaunchKernelGGL(advance_position_kernel, dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream), position_dev, step);
   return check_launch("advance_position");
+}
+
+extern "C" int tt_record_token(const int64_t* token_dev, const int32_t* position_dev, const int32_t* base_dev,
+                               int64_t* history, int32_t capacity, void* stream) {
+  TT_REQUIRE(token_dev && position_dev && base_dev && history && capacity > 0, "record_token: bad arguments");
+  hipLaunchKernelGGL(record_token_kernel, dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream), token_dev, position_dev,
+                     base_dev, history, capacity);
+  return check_launch("record_token");
 }

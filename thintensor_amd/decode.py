@@ -1,0 +1,205 @@
+"""Minimal bs=1 greedy decode harness on the HIP backend.
+
+The step order and every rounding point mirror the reference runtime's Triton
+paths, with the fused options the Triton backend provides:
+
+* ``DenseDecoder`` follows ``_forward_token_triton`` (gpu_runtime.py:11429-11726)
+  with fused residual+RMSNorm, fused RoPE, the fused Triton attention backend and
+  Triton elementwise ops; the greedy token comes from ``next_token_tensor``
+  (gpu_runtime.py:11130-11209) in its default lm_head mode;
+* ``MoEDecoder`` follows ``_forward_token_moe`` and ``_packed_moe_forward``
+  (gpu_runtime.py:8968-9908) for MXFP4 experts.
+
+Differences from the reference, by design:
+
+* a flat KV cache ``[layers, kv_heads, capacity, head_dim]`` replaces the paged
+  cache (same values, same attention);
+* the token id and the position live on the device, so one decode step is captured
+  once in a HIP graph and replayed for every token (the reference disables its
+  CUDA graph for causal KV because it hard-codes the position,
+  gpu_runtime.py:12594-12601);
+* QKV and gate/up projections are one multi-matrix launch each, the MoE experts
+  run as two fused launches, and attention biases are fused into the GEMV
+  epilogue -- each with the reference's rounding points, so outputs are unchanged;
+* the post-attention add_rms_norm the MoE path issues twice per layer
+  (gpu_runtime.py:9233-9252 and 9254-9275, idempotent) runs once.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .backend import HipDecodeBackend
+from .synth import DenseWeights, MoEWeights
+
+
+class _GraphedDecoder:
+    """Common state: device token / position, token history, graph capture."""
+
+    def __init__(self, backend: HipDecodeBackend, device: torch.device, capacity: int, max_new: int) -> None:
+        self.be = backend
+        self.device = device
+        self.capacity = capacity
+        self.token = backend._argmax_out_idx               # int64 0-d, written by the lm_head argmax
+        self.position = torch.zeros(1, device=device, dtype=torch.int32)
+        self.history = torch.zeros(max_new, device=device, dtype=torch.int64)
+        self.base = torch.zeros(1, device=device, dtype=torch.int32)   # position of the first generated step
+        self.graph: torch.cuda.CUDAGraph | None = None
+        self._graph_stream: torch.cuda.Stream | None = None
+
+    def prime(self, token: int, position: int) -> None:
+        """Set the next input token and its position (host -> device, outside graphs)."""
+        if not 0 <= position < self.capacity:
+            raise ValueError("position outside the KV cache")
+        self.token.fill_(int(token))
+        self.position.fill_(int(position))
+        self.base.fill_(int(position))
+        self.history.zero_()
+
+    def step(self) -> None:  # pragma: no cover - implemented by subclasses
+        raise NotImplementedError
+
+    def _step_and_record(self) -> None:
+        self.step()
+        self.be.record_token(self.token, self.position, self.base, self.history)
+        self.be.advance_position(self.position)
+
+    def _reserve_scratch(self) -> None:  # pragma: no cover - implemented by subclasses
+        raise NotImplementedError
+
+    def capture(self) -> None:
+        """Record one decode step (including token logging and the position advance)
+        into a HIP graph.  The graph reads token/position from device memory.  All
+        scratch is reserved beforehand, so no step runs (and no state changes) here."""
+        self._reserve_scratch()
+        torch.cuda.synchronize(self.device)
+        self._graph_stream = torch.cuda.Stream(self.device)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph, stream=self._graph_stream):
+            self._step_and_record()
+
+    def generate(self, start_token: int, position: int, steps: int, use_graph: bool = True) -> list[int]:
+        """Greedy-decode `steps` tokens; returns the generated ids."""
+        if position + steps > self.capacity:
+            raise ValueError("not enough KV capacity for the requested steps")
+        if steps > self.history.numel():
+            raise ValueError("history buffer too small")
+        if use_graph and self.graph is None:
+            self.capture()
+        self.prime(start_token, position)
+        for _ in range(steps):
+            if use_graph:
+                self.graph.replay()
+            else:
+                self._step_and_record()
+        torch.cuda.synchronize(self.device)
+        return self.history[:steps].cpu().tolist()
+
+
+class DenseDecoder(_GraphedDecoder):
+    """Llama-3.2-1B-shaped int4 g128 decoder."""
+
+    def __init__(self, backend: HipDecodeBackend, weights: DenseWeights) -> None:
+        s = weights.shape
+        super().__init__(backend, weights.embed.device, int(weights.k_cache.shape[2]), s.max_new_tokens)
+        self.w = weights
+        self.s = s
+        dev, dt = weights.embed.device, torch.float16
+        self.hidden_a = torch.empty(s.hidden, device=dev, dtype=dt)
+        self.hidden_b = torch.empty(s.hidden, device=dev, dtype=dt)
+        self.normed = torch.empty(s.hidden, device=dev, dtype=dt)
+        self.qkv = torch.empty(s.q_dim + 2 * s.kv_dim, device=dev, dtype=dt)
+        self.attn = torch.empty(s.q_dim, device=dev, dtype=dt)
+        self.attn_out = torch.empty(s.hidden, device=dev, dtype=dt)
+        self.gate_up = torch.empty(2 * s.intermediate, device=dev, dtype=dt)
+        self.act = torch.empty(s.intermediate, device=dev, dtype=dt)
+        self.mlp = torch.empty(s.hidden, device=dev, dtype=dt)
+        self.final = torch.empty(s.hidden, device=dev, dtype=dt)
+
+    def _reserve_scratch(self) -> None:
+        s = self.s
+        self.be._attention_scratch(s.heads, self.capacity, s.head_dim)
+        self.be._argmax_scratch(int(self.w.lm_head.shape[0]), s.hidden)
+        self.be.logits_buffer(int(self.w.lm_head.shape[0]), torch.float16)
+
+    def step(self) -> None:
+        be, w, s = self.be, self.w, self.s
+        q, k, v = self.qkv[: s.q_dim], self.qkv[s.q_dim: s.q_dim + s.kv_dim], self.qkv[s.q_dim + s.kv_dim:]
+        gate, up = self.gate_up[: s.intermediate], self.gate_up[s.intermediate:]
+        be.embedding(w.embed, self.token, self.hidden_a)
+        be.rms_norm(self.hidden_a, w.layers[0].ln1, self.normed, s.eps)
+        for li, L in enumerate(w.layers):
+            be.multi_int4_scaled_matvec((L.q[0], L.k[0], L.v[0]), (L.q[1], L.k[1], L.v[1]),
+                                        (s.q_dim, s.kv_dim, s.kv_dim), s.hidden, self.normed, self.qkv,
+                                        group_size=s.group)
+            be.rope_qk_inplace(q, k, w.cos, w.sin, s.heads, s.kv_heads, s.head_dim, position=self.position)
+            be.kv_append(k, v, w.k_cache[li], w.v_cache[li], self.position, s.kv_heads, s.head_dim)
+            be.single_token_gqa_attention(q, w.k_cache[li], w.v_cache[li], self.attn, s.heads, s.kv_heads,
+                                          s.head_dim, active_tokens=(self.position, 1))
+            be.int4_scaled_matvec(L.o[0], L.o[1], self.attn, self.attn_out, rows=s.hidden, cols=s.q_dim,
+                                  group_size=s.group)
+            be.add_rms_norm(self.hidden_a, self.attn_out, self.hidden_b, L.ln2, self.normed, s.eps)
+            be.multi_int4_scaled_matvec((L.gate[0], L.up[0]), (L.gate[1], L.up[1]), (s.intermediate, s.intermediate),
+                                        s.hidden, self.normed, self.gate_up, group_size=s.group)
+            be.silu_mul(gate, up, self.act)
+            be.int4_scaled_matvec(L.down[0], L.down[1], self.act, self.mlp, rows=s.hidden, cols=s.intermediate,
+                                  group_size=s.group)
+            if li + 1 < len(w.layers):
+                be.add_rms_norm(self.hidden_b, self.mlp, self.hidden_a, w.layers[li + 1].ln1, self.normed, s.eps)
+            else:
+                be.add_rms_norm(self.hidden_b, self.mlp, self.hidden_a, w.final_norm, self.final, s.eps)
+        be.matvec_argmax_tensor(w.lm_head, self.final)
+
+
+class MoEDecoder(_GraphedDecoder):
+    """gpt-oss-20B-shaped decoder with MXFP4 experts, fp16 attention with sinks."""
+
+    def __init__(self, backend: HipDecodeBackend, weights: MoEWeights) -> None:
+        s = weights.shape
+        super().__init__(backend, weights.embed.device, int(weights.k_cache.shape[2]), s.max_new_tokens)
+        self.w = weights
+        self.s = s
+        dev, dt = weights.embed.device, torch.float16
+        self.hidden_a = torch.empty(s.hidden, device=dev, dtype=dt)
+        self.hidden_b = torch.empty(s.hidden, device=dev, dtype=dt)
+        self.normed = torch.empty(s.hidden, device=dev, dtype=dt)
+        self.qkv = torch.empty(s.q_dim + 2 * s.kv_dim, device=dev, dtype=dt)
+        self.attn = torch.empty(s.q_dim, device=dev, dtype=dt)
+        self.attn_out = torch.empty(s.hidden, device=dev, dtype=dt)
+        self.router_idx = torch.empty(s.top_k, device=dev, dtype=torch.int32)
+        self.router_scores = torch.empty(s.top_k, device=dev, dtype=dt)
+        self.act = torch.empty((s.top_k, s.intermediate), device=dev, dtype=dt)
+        self.moe = torch.empty(s.hidden, device=dev, dtype=dt)
+        self.final = torch.empty(s.hidden, device=dev, dtype=dt)
+
+    def _reserve_scratch(self) -> None:
+        s = self.s
+        self.be._attention_scratch(s.heads, self.capacity, s.head_dim)
+        self.be._argmax_scratch(int(self.w.lm_head.shape[0]), s.hidden)
+        self.be.logits_buffer(int(self.w.lm_head.shape[0]), torch.float16)
+
+    def step(self) -> None:
+        be, w, s = self.be, self.w, self.s
+        q, k, v = self.qkv[: s.q_dim], self.qkv[s.q_dim: s.q_dim + s.kv_dim], self.qkv[s.q_dim + s.kv_dim:]
+        be.embedding(w.embed, self.token, self.hidden_a)
+        be.rms_norm(self.hidden_a, w.layers[0].ln1, self.normed, s.eps)
+        for li, L in enumerate(w.layers):
+            be.multi_matvec_bias((L.q, L.k, L.v), (L.q_bias, L.k_bias, L.v_bias), self.normed, self.qkv)
+            be.rope_qk_inplace(q, k, w.cos, w.sin, s.heads, s.kv_heads, s.head_dim, position=self.position)
+            be.kv_append(k, v, w.k_cache[li], w.v_cache[li], self.position, s.kv_heads, s.head_dim)
+            be.single_token_gqa_attention(q, w.k_cache[li], w.v_cache[li], self.attn, s.heads, s.kv_heads,
+                                          s.head_dim, sinks=L.sinks, active_tokens=(self.position, 1))
+            be.multi_matvec_bias((L.o,), (L.o_bias,), self.attn, self.attn_out)
+            be.add_rms_norm(self.hidden_a, self.attn_out, self.hidden_b, L.ln2, self.normed, s.eps)
+            be.moe_router_matvec_topk(L.router, self.normed, self.router_idx, self.router_scores, bias=L.router_bias,
+                                      renormalize=True)
+            be.mxfp_lowbit_selected_swiglu(L.gate_up_blocks, L.gate_up_scales, self.normed, self.router_idx, self.act,
+                                           bits=4, alpha=s.swiglu_alpha, limit=s.swiglu_limit, bias=L.gate_up_bias)
+            be.mxfp_lowbit_weighted_down(L.down_blocks, L.down_scales, self.act, self.router_idx, self.router_scores,
+                                         self.moe, bits=4, bias=L.down_bias)
+            if li + 1 < len(w.layers):
+                be.add_rms_norm(self.hidden_b, self.moe, self.hidden_a, w.layers[li + 1].ln1, self.normed, s.eps)
+            else:
+                be.add(self.hidden_b, self.moe, self.hidden_a)
+                be.rms_norm(self.hidden_a, w.final_norm, self.final, s.eps)
+        be.matvec_argmax_tensor(w.lm_head, self.final)
