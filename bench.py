@@ -1,0 +1,381 @@
+"""Benchmark of the gfx950 decode hot path on one MI355X.
+
+Default run (N=1):
+
+* ``value``: bs=1 greedy decode tokens/s of the Llama-3.2-1B-shaped model (int4 g128
+  linear layers, fp16 embeddings/lm_head, fp16 KV cache with 512 prior tokens).  One
+  "step" is one generated token: a replay of the HIP graph that holds the whole
+  decode step (embedding -> 16 layers -> lm_head GEMV + greedy argmax -> token log).
+  Warm-up steps decode from the 512-token prefix; the position is then reset to 512
+  and exactly ``--steps`` tokens are timed from the same prefix.
+* ``roofline``: the int4 g128 dequant-GEMV at the single-GEMV shape (8192 x 2048),
+  the kernel the headline GB/s figure is quoted on.  Each timed launch reads a
+  different one of 64 weight/scale copies (555 MB > the 256 MB last-level cache),
+  so every byte comes from HBM; launches are replayed from a HIP graph and bracketed
+  with HIP events on the stream the kernels run on.
+* extra fields: gpt-oss-20B-shaped MoE decode tok/s (MXFP4 experts), the lm_head
+  GEMV+argmax and other GEMV shapes in GB/s, and the token ids of the timed run.
+* ``cpu_baseline``: the reference's CPU path (torch ``_weight_int4pack_mm_for_cpu``
+  for int4 layers, torch CPU ops elsewhere) decoding the same synthetic model on the
+  host cores for a bounded ~12 s sample.
+
+All weights are seeded synthetic tensors (no checkpoints offline).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+HBM_PEAK_GBS = 8000.0
+
+
+def _parse() -> argparse.Namespace:
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=64, help="timed decode steps (tokens)")
+    p.add_argument("--warmup", type=int, default=8, help="untimed decode steps before the timed region")
+    p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--no-moe", action="store_true", help="skip the gpt-oss-20B-shaped decode")
+    p.add_argument("--no-extra", action="store_true", help="skip the extra GEMV shapes")
+    p.add_argument("--roofline-only", action="store_true",
+                   help="only the int4 roofline phase (used for hardware-counter runs)")
+    return p.parse_args()
+
+
+def _log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+# --------------------------------------------------------------------------- GEMV timing
+def _time_rotated(launch, copies: int, trials: int = 20) -> float:
+    """Median seconds per launch: `launch(i)` for i in 0..copies-1 captured in one HIP
+    graph, replayed `trials` times between HIP events on the current stream."""
+    import torch
+
+    for i in range(copies):
+        launch(i)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream()
+    with torch.cuda.graph(graph, stream=cap):
+        for i in range(copies):
+            launch(i)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        graph.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    t = []
+    for _ in range(trials):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        graph.replay()
+        e1.record(stream)
+        e1.synchronize()
+        t.append(e0.elapsed_time(e1) * 1e-3 / copies)
+    del graph
+    return statistics.median(t)
+
+
+def int4_gemv_phase(be, rows: int, cols: int, group: int, copies: int, seed: int) -> dict:
+    """int4 g128 GEMV over `copies` rotated weight copies (HBM-resident)."""
+    import torch
+
+    dev = be.device
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    W = torch.randint(0, 256, (copies, rows, cols // 2), generator=g, device=dev, dtype=torch.uint8)
+    S = (torch.randn((copies, rows, cols // group), generator=g, device=dev).abs() * 0.02).to(torch.float16)
+    x = torch.randn(cols, generator=g, device=dev).to(torch.float16)
+    out = torch.empty((copies, rows), device=dev, dtype=torch.float16)
+
+    def launch(i):
+        be.int4_scaled_matvec(W[i], S[i], x, out[i], rows=rows, cols=cols, group_size=group)
+
+    t = _time_rotated(launch, copies)
+    nbytes = rows * cols // 2 + rows * (cols // group) * 2 + cols * 2 + rows * 2
+    del W, S
+    return {"shape": [rows, cols], "group": group, "us_per_call": t * 1e6, "bytes_per_call": nbytes,
+            "GB_s": nbytes / t / 1e9, "frac_of_hbm_peak": nbytes / t / 1e9 / HBM_PEAK_GBS, "rotated_copies": copies}
+
+
+def lm_head_phase(be, rows: int, cols: int, copies: int, seed: int) -> dict:
+    """fp16 lm_head GEMV + greedy argmax (rotated copies)."""
+    import torch
+
+    dev = be.device
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    W = [(torch.randn((rows, cols), generator=g, device=dev) * 0.02).to(torch.float16) for _ in range(copies)]
+    x = torch.randn(cols, generator=g, device=dev).to(torch.float16)
+    be._argmax_scratch(rows, cols)
+    be.logits_buffer(rows, torch.float16)
+
+    def launch(i):
+        be.matvec_argmax_tensor(W[i], x)
+
+    t = _time_rotated(launch, copies, trials=10)
+    nbytes = rows * cols * 2 + cols * 2 + rows * 2 + 8
+    del W
+    return {"shape": [rows, cols], "us_per_call": t * 1e6, "bytes_per_call": nbytes, "GB_s": nbytes / t / 1e9,
+            "frac_of_hbm_peak": nbytes / t / 1e9 / HBM_PEAK_GBS, "rotated_copies": copies}
+
+
+def affine_lowbit_phase(be, bits: int, rows: int, cols: int, copies: int, seed: int) -> dict:
+    """q2 / q1 g64 affine GEMV (rotated copies)."""
+    import torch
+
+    dev = be.device
+    group = 64
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    W = torch.randint(0, 256, (copies, rows, cols * bits // 8), generator=g, device=dev, dtype=torch.uint8)
+    sz = torch.empty((copies, rows, cols // group, 2), device=dev, dtype=torch.float16)
+    sz[..., 0] = (torch.randn((copies, rows, cols // group), generator=g, device=dev).abs() * 0.05).to(torch.float16)
+    sz[..., 1] = (torch.rand((copies, rows, cols // group), generator=g, device=dev) * (2 ** bits - 1)).to(torch.float16)
+    x = torch.randn(cols, generator=g, device=dev).to(torch.float16)
+    out = torch.empty((copies, rows), device=dev, dtype=torch.float16)
+
+    def launch(i):
+        be.lowbit_affine_matvec(W[i], sz[i], x, out[i], bits=bits, rows=rows, cols=cols, group_size=group)
+
+    t = _time_rotated(launch, copies)
+    nbytes = rows * cols * bits // 8 + rows * (cols // group) * 4 + cols * 2 + rows * 2
+    del W, sz
+    return {"bits": bits, "shape": [rows, cols], "group": group, "us_per_call": t * 1e6, "bytes_per_call": nbytes,
+            "GB_s": nbytes / t / 1e9, "frac_of_hbm_peak": nbytes / t / 1e9 / HBM_PEAK_GBS, "rotated_copies": copies}
+
+
+# --------------------------------------------------------------------------- decode timing
+def _time_decode(dec, start_token: int, position: int, warmup: int, steps: int) -> dict:
+    import torch
+
+    dec.capture()
+    dec.prime(start_token, position)
+    for _ in range(warmup):
+        dec.graph.replay()
+    torch.cuda.synchronize()
+    dec.prime(start_token, position)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(steps):
+        dec.graph.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    tokens = dec.history[:steps].cpu().tolist()
+    return {"wall_s": wall, "event_s": e0.elapsed_time(e1) * 1e-3, "tokens": tokens}
+
+
+def dense_decode_phase(args) -> tuple[dict, object]:
+    import torch
+
+    from thintensor_amd.backend import HipDecodeBackend
+    from thintensor_amd.decode import DenseDecoder
+    from thintensor_amd.synth import LLAMA_1B, make_dense
+
+    s = LLAMA_1B
+    dev = torch.device("cuda:0")
+    cap = s.prior_tokens + max(args.steps, args.warmup)
+    w = make_dense(s, device=dev, seed=args.seed, capacity=cap)
+    be = HipDecodeBackend(dev, torch.float16, s.hidden, s.q_dim, s.kv_dim, s.intermediate)
+    dec = DenseDecoder(be, w)
+    if args.steps > dec.history.numel():
+        dec.history = torch.zeros(args.steps, device=dev, dtype=torch.int64)
+    r = _time_decode(dec, 1, s.prior_tokens, args.warmup, args.steps)
+    per_token = sum(int(t.numel()) * t.element_size() for L in w.layers
+                    for name in ("q", "k", "v", "o", "gate", "up", "down") for t in getattr(L, name))
+    per_token += int(w.lm_head.numel()) * 2 + s.hidden * 2 * (2 * s.layers + 1)
+    mean_ctx = s.prior_tokens + (args.steps + 1) / 2
+    per_token += int(2 * s.layers * s.kv_heads * mean_ctx * s.head_dim * 2)
+    r["bytes_per_token"] = per_token
+    return r, be
+
+
+def moe_decode_phase(args) -> dict:
+    import torch
+
+    from thintensor_amd.backend import HipDecodeBackend
+    from thintensor_amd.decode import MoEDecoder
+    from thintensor_amd.synth import GPT_OSS_20B, make_moe
+
+    s = GPT_OSS_20B
+    dev = torch.device("cuda:0")
+    steps = min(args.steps, 32)
+    warm = min(args.warmup, 4)
+    w = make_moe(s, device=dev, seed=args.seed, capacity=s.prior_tokens + max(steps, warm))
+    be = HipDecodeBackend(dev, torch.float16, s.hidden, s.q_dim, s.kv_dim, s.intermediate)
+    dec = MoEDecoder(be, w)
+    r = _time_decode(dec, 1, s.prior_tokens, warm, steps)
+    tok_s = steps / r["event_s"]
+    out = {"workload": "gpt-oss-20b-shaped bs=1 greedy decode, MXFP4 experts top-4 of 32, 1024 prior tokens",
+           "steps": steps, "tok_s": tok_s, "ms_per_token": 1e3 / tok_s, "tokens": r["tokens"]}
+    del dec, w, be
+    torch.cuda.empty_cache()
+    return out
+
+
+# --------------------------------------------------------------------------- CPU baseline
+def cpu_phase(args) -> tuple[dict, dict]:
+    """CPU baselines from the reference's CPU path on a bounded sample (rank 0, N=1)."""
+    import torch
+
+    from oracle.cpu_path import Int4CPU, cpu_threads, dense_decode_baseline
+    from thintensor_amd.synth import LLAMA_1B, make_dense
+
+    torch.set_num_threads(cpu_threads())
+    # single int4 GEMV at the 8192 x 2048 shape
+    g = torch.Generator().manual_seed(args.seed)
+    rows, cols, group = 8192, 2048, 128
+    m = Int4CPU(torch.randint(0, 256, (rows, cols // 2), generator=g, dtype=torch.uint8),
+                (torch.randn((rows, cols // group), generator=g).abs() * 0.02).to(torch.float16), group)
+    x = torch.randn(cols, generator=g).to(torch.float16)
+    for _ in range(3):
+        m.mv(x)
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < 2.0:
+        m.mv(x)
+        n += 1
+    us = (time.perf_counter() - t0) / n * 1e6
+    gemv = {"us_per_call": us, "GB_s": (rows * cols // 2 + rows * (cols // group) * 2) / us / 1e3, "calls": n,
+            "cores": cpu_threads(), "op": "torch.ops.aten._weight_int4pack_mm_for_cpu"}
+    # full decode on a bounded sample, weights generated on the GPU with the same seed
+    s = LLAMA_1B
+    w = make_dense(s, device=torch.device("cuda:0"), seed=args.seed, capacity=s.prior_tokens + 64)
+    return dense_decode_baseline(w, 1, budget_s=12.0, max_tokens=32), gemv
+
+
+# --------------------------------------------------------------------------- traffic (hardware counters)
+def _traffic_from_profiles(kernel: str) -> float | None:
+    """HBM bytes per launch from the committed hardware-counter summary, if present.
+
+    The summary holds one JSON line {"kernel": ..., "traffic_bytes": ...} written
+    from rocprofv3 FETCH_SIZE / WRITE_SIZE runs (scaled by a copy kernel's reading).
+    """
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "int4_gemv_8192x2048_traffic.txt")
+    try:
+        with open(path) as f:
+            for line in f:
+                line = line.strip()
+                if line.startswith("{") and kernel in line:
+                    return float(json.loads(line)["traffic_bytes"])
+    except (OSError, ValueError, KeyError):
+        return None
+    return None
+
+
+# --------------------------------------------------------------------------- main
+def main() -> int:
+    args = _parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build measures one GPU only: the decode hot path runs on a single MI355X "
+                                   "and has no multi-GPU mode; run with --gpus 1"}), flush=True)
+        return 2
+    import torch
+
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU visible: bench.py measures the HIP path and has no CPU fallback"}))
+        return 1
+    from thintensor_amd import _lib
+
+    _lib.load()  # fails loudly when the HIP library is missing
+
+    if args.roofline_only:
+        from thintensor_amd.backend import HipDecodeBackend
+        be = HipDecodeBackend(torch.device("cuda:0"), torch.float16, 2048, 2048, 512, 8192)
+        r = int4_gemv_phase(be, 8192, 2048, 128, 64, args.seed)
+        print(json.dumps({"int4_gemv": r}), flush=True)
+        return 0
+
+    _log("dense decode (llama-3.2-1b-shaped)")
+    torch.cuda.synchronize()
+    dense, be = dense_decode_phase(args)
+    tok_s = args.steps / dense["wall_s"]
+    _log(f"dense decode: {tok_s:.1f} tok/s")
+
+    _log("int4 g128 GEMV roofline (8192 x 2048, 64 rotated copies)")
+    roof = int4_gemv_phase(be, 8192, 2048, 128, 64, args.seed)
+    _log(f"int4 GEMV: {roof['us_per_call']:.2f} us/call, {roof['GB_s']:.0f} GB/s")
+
+    extra = {}
+    if not args.no_extra:
+        _log("extra GEMV shapes")
+        extra["int4_gemv_gate_up_16384x2048"] = int4_gemv_phase(be, 16384, 2048, 128, 32, args.seed + 1)
+        extra["int4_gemv_17920x5120"] = int4_gemv_phase(be, 17920, 5120, 128, 12, args.seed + 2)
+        extra["lm_head_argmax_128256x2048"] = lm_head_phase(be, 128256, 2048, 2, args.seed + 3)
+        extra["q2_affine_g64_17920x5120"] = affine_lowbit_phase(be, 2, 17920, 5120, 24, args.seed + 4)
+        extra["q1_affine_g64_5120x5120"] = affine_lowbit_phase(be, 1, 5120, 5120, 64, args.seed + 5)
+        torch.cuda.empty_cache()
+    del be
+    torch.cuda.empty_cache()
+
+    moe = None
+    if not args.no_moe:
+        _log("MoE decode (gpt-oss-20b-shaped)")
+        moe = moe_decode_phase(args)
+        _log(f"MoE decode: {moe['tok_s']:.1f} tok/s")
+
+    cpu = cpu_gemv = None
+    if not args.no_cpu:
+        _log("CPU baseline (reference CPU path, bounded sample)")
+        cpu, cpu_gemv = cpu_phase(args)
+        _log(f"CPU decode: {cpu['value']:.2f} tok/s on {cpu['cores']} threads")
+
+    traffic = _traffic_from_profiles("int4")
+    line = {
+        "metric": "int4 GEMV HBM GB/s (% of peak); bs=1 decode tok/s, 1B dense & 20B MoE",
+        "value": tok_s,
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": dense["wall_s"] * 1e3 / args.steps,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (seeded random weights of the named shapes; no checkpoints offline)",
+        "config": {
+            "workload": "llama-3.2-1b-shaped bs=1 greedy decode: 16 layers, hidden 2048, 32q/8kv heads x 64, "
+                        "SwiGLU 8192, vocab 128256, int4 g128 linear layers, fp16 embeddings/lm_head, fp16 KV cache "
+                        "with 512 prior tokens; one step = one generated token (HIP graph replay)",
+            "batch": 1,
+            "prior_tokens": 512,
+            "arithmetic": "fp16 activations, int4/fp16 weights, fp32 accumulation",
+        },
+        "roofline": {
+            "kernel": "int4 g128 dequant-GEMV (tt_int4_scaled_matvec), 8192 x 2048",
+            "bound": "hbm",
+            "achieved": roof["GB_s"],
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": roof["GB_s"] / HBM_PEAK_GBS,
+            "traffic": traffic,
+            "bytes_per_launch": roof["bytes_per_call"],
+            "us_per_launch": roof["us_per_call"],
+        },
+        "cpu_baseline": cpu,
+        "decode_bytes_per_token": dense["bytes_per_token"],
+        "decode_frac_of_hbm_peak": dense["bytes_per_token"] * tok_s / 1e9 / HBM_PEAK_GBS,
+        "decode_event_tok_s": args.steps / dense["event_s"],
+        "decode_tokens": dense["tokens"],
+        "moe_decode": moe,
+        "cpu_int4_gemv_8192x2048": cpu_gemv,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
