@@ -35,7 +35,7 @@ _L = ctypes.c_int64
 def lib() -> ctypes.CDLL:
     path = _build.ensure_built()
     L = ctypes.CDLL(str(path))
-    L.tto_gemv.argtypes = [_I, _I, _P, _L, _P, _I, _L, _L, _L, _I, _I, _P, _I, _P, _I, _L, _I, _I, _I]
+    L.tto_gemv.argtypes = [_I, _I, _P, _L, _P, _I, _L, _L, _L, _I, _P, _I, _P, _I, _L, _I, _I, _I]
     L.tto_gemv.restype = _I
     L.tto_f32_to_f16.argtypes = [ctypes.c_float]
     L.tto_f32_to_f16.restype = ctypes.c_uint16
@@ -97,7 +97,7 @@ def out_array(rows: int, odtype: int) -> np.ndarray:
 
 
 def gemv(fmt: str, smode: str, w: np.ndarray, scales: np.ndarray | None, x: np.ndarray, *, cols: int, lpr: int,
-         L: int = 1, s_row: int = 0, s_grp: int = 0, s_pair: int = 0, aff_zero: int = 0, e8_extra: int = 0,
+         L: int = 1, s_row: int = 0, s_grp: int = 0, s_pair: int = 0, aff_zero: int = 0,
          odtype: int = F16, sdtype: int | None = None) -> np.ndarray:
     """Bit-exact restatement of one GEMV launch.  ``w`` is uint8 [rows, row_bytes]."""
     w = np.ascontiguousarray(w)
@@ -112,7 +112,7 @@ def gemv(fmt: str, smode: str, w: np.ndarray, scales: np.ndarray | None, x: np.n
     else:
         sdtype = F32
     rc = lib().tto_gemv(FMT[fmt], SMODE[smode], _ptr(wb), wb.strides[0], _ptr(scales), sdtype, s_row, s_grp, s_pair,
-                        aff_zero, e8_extra, _ptr(x), dtype_code(x), _ptr(out), odtype, rows, cols, L, lpr)
+                        aff_zero, _ptr(x), dtype_code(x), _ptr(out), odtype, rows, cols, L, lpr)
     if rc != 0:
         raise ValueError(f"oracle gemv rejected the configuration ({rc})")
     return out

@@ -156,7 +156,7 @@ float tto_e2m1(int code) {
 }
 
 /* Value of element e (0..31) of one chunk as the kernel feeds it to the fma.
- * MXFP4 values carry an extra 2^-14 that the block scale removes again. */
+ */
 static float chunk_weight(int fmt, const uint8_t* c, int e) {
   switch (fmt) {
     case FMT_INT4_SYM: return (float)(((c[e >> 1] >> ((e & 1) * 4)) & 15) - 8);
@@ -164,7 +164,7 @@ static float chunk_weight(int fmt, const uint8_t* c, int e) {
     case FMT_FP8: return tto_fp8e4m3_to_f32(c[e]);
     case FMT_F16W: return tto_f16_to_f32(((const uint16_t*)c)[e]);
     case FMT_BF16W: return tto_bf16_to_f32(((const uint16_t*)c)[e]);
-    case FMT_MXFP4: return ldexpf(tto_e2m1((c[e >> 1] >> ((e & 1) * 4)) & 15), -14);
+    case FMT_MXFP4: return tto_e2m1((c[e >> 1] >> ((e & 1) * 4)) & 15);
     case FMT_Q2E8: return (float)((c[e >> 2] >> ((e & 3) * 2)) & 3) - 1.5f;
     case FMT_Q1E8: return ((c[e >> 3] >> (e & 7)) & 1) ? 1.0f : -1.0f;
     case FMT_Q2AFF: return (float)((c[e >> 2] >> ((e & 3) * 2)) & 3);
@@ -200,7 +200,7 @@ static void chunk_weights(int fmt, const uint8_t* c, float* wv) {
  * xf: the activation vector already converted to binary32.
  */
 static float gemv_row_f(int fmt, int smode, const uint8_t* wrow, const void* srow, int sdtype, int64_t s_grp,
-                        int64_t s_pair, int aff_zero, int e8_extra, const float* xf, int cols, int L, int lpr) {
+                        int64_t s_pair, int aff_zero, const float* xf, int cols, int L, int lpr) {
   const int B = fmt_bytes(fmt);
   const int nchunks = cols / 32;
   const int rounds = (nchunks + lpr - 1) / lpr;
@@ -232,9 +232,7 @@ static float gemv_row_f(int fmt, int smode, const uint8_t* wrow, const void* sro
         float t = 0.0f;
         if (j < nchunks) {
           const int e = ((const uint8_t*)srow)[j];
-          float q = p[l];
-          if (e8_extra) q = q * pow2i(e8_extra);
-          t = q * pow2i(e - 127);
+          t = p[l] * pow2i(e - 127);
         }
         A[l] = A[l] + t;
       }
@@ -273,10 +271,10 @@ static float* to_f32_vec(const void* x, int xdtype, int n) {
 }
 
 float tto_gemv_row(int fmt, int smode, const uint8_t* wrow, const void* srow, int sdtype, int64_t s_grp,
-                   int64_t s_pair, int aff_zero, int e8_extra, const void* x, int xdtype, int cols, int L,
+                   int64_t s_pair, int aff_zero, const void* x, int xdtype, int cols, int L,
                    int lpr) {
   float* xf = to_f32_vec(x, xdtype, cols);
-  const float v = gemv_row_f(fmt, smode, wrow, srow, sdtype, s_grp, s_pair, aff_zero, e8_extra, xf, cols, L, lpr);
+  const float v = gemv_row_f(fmt, smode, wrow, srow, sdtype, s_grp, s_pair, aff_zero, xf, cols, L, lpr);
   free(xf);
   return v;
 }
@@ -286,7 +284,7 @@ float tto_gemv_row(int fmt, int smode, const uint8_t* wrow, const void* srow, in
  * activation row).  w points at the first row of the chosen matrix/expert.
  */
 int tto_gemv(int fmt, int smode, const uint8_t* w, int64_t w_row_bytes, const void* s, int sdtype, int64_t s_row,
-             int64_t s_grp, int64_t s_pair, int aff_zero, int e8_extra, const void* x, int xdtype, void* out,
+             int64_t s_grp, int64_t s_pair, int aff_zero, const void* x, int xdtype, void* out,
              int odtype, int64_t rows, int cols, int L, int lpr) {
   if (cols % 32 || lpr < 1 || lpr > 64) return -1;
   float* xf = to_f32_vec(x, xdtype, cols);
@@ -294,7 +292,7 @@ int tto_gemv(int fmt, int smode, const uint8_t* w, int64_t w_row_bytes, const vo
 #pragma omp parallel for schedule(static)
   for (int64_t n = 0; n < rows; n++) {
     const void* srow = s ? (const void*)((const uint8_t*)s + (size_t)(n * s_row) * es) : NULL;
-    const float v = gemv_row_f(fmt, smode, w + n * w_row_bytes, srow, sdtype, s_grp, s_pair, aff_zero, e8_extra, xf,
+    const float v = gemv_row_f(fmt, smode, w + n * w_row_bytes, srow, sdtype, s_grp, s_pair, aff_zero, xf,
                                cols, L, lpr);
     act_put(out, odtype, n, v);
   }
@@ -316,7 +314,6 @@ int tto_swiglu(int fmt, int rt, const uint8_t* w, int64_t w_expert, int64_t w_ro
                int64_t s_expert, int64_t s_row, const void* x, int xdtype, int64_t x_slot, const int32_t* experts,
                int selected, const void* bias, int bdtype, int64_t bias_expert, float alpha, float limit, void* out,
                int odtype, int64_t out_slot, int act_rows, int cols, int lpr) {
-  const int extra = fmt == FMT_MXFP4 ? 14 : 0;
   const size_t xes = xdtype == TTO_F32 ? 4 : 2;
   for (int slot = 0; slot < selected; slot++) {
     const int64_t e = experts[slot];
@@ -325,9 +322,9 @@ int tto_swiglu(int fmt, int rt, const uint8_t* w, int64_t w_expert, int64_t w_ro
 #pragma omp parallel for schedule(static)
     for (int a = 0; a < act_rows; a++) {
       float g = gemv_row_f(fmt, SM_BLOCK_E8, w + e * w_expert + (2 * (int64_t)a) * w_row,
-                           s + e * s_expert + (2 * (int64_t)a) * s_row, TTO_F32, 1, 0, 0, extra, xf, cols, 1, lpr);
+                           s + e * s_expert + (2 * (int64_t)a) * s_row, TTO_F32, 1, 0, 0, xf, cols, 1, lpr);
       float u = gemv_row_f(fmt, SM_BLOCK_E8, w + e * w_expert + (2 * (int64_t)a + 1) * w_row,
-                           s + e * s_expert + (2 * (int64_t)a + 1) * s_row, TTO_F32, 1, 0, 0, extra, xf, cols, 1, lpr);
+                           s + e * s_expert + (2 * (int64_t)a + 1) * s_row, TTO_F32, 1, 0, 0, xf, cols, 1, lpr);
       g = round_rt(rt, g);
       u = round_rt(rt, u);
       if (bias) {
@@ -350,7 +347,6 @@ int tto_weighted_down(int fmt, int rt, const uint8_t* w, int64_t w_expert, int64
                       int64_t s_expert, int64_t s_row, const void* x, int xdtype, int64_t x_slot,
                       const int32_t* experts, const void* scores, int sdtype, int selected, const void* bias,
                       int bdtype, int64_t bias_expert, void* out, int odtype, int rows, int cols, int lpr) {
-  const int extra = fmt == FMT_MXFP4 ? 14 : 0;
   const size_t xes = xdtype == TTO_F32 ? 4 : 2;
   float* xf[64];
   for (int slot = 0; slot < selected && slot < 64; slot++)
@@ -361,7 +357,7 @@ int tto_weighted_down(int fmt, int rt, const uint8_t* w, int64_t w_expert, int64
     for (int slot = 0; slot < selected; slot++) {
       const int64_t e = experts[slot];
       float v = gemv_row_f(fmt, SM_BLOCK_E8, w + e * w_expert + (int64_t)n * w_row, s + e * s_expert + (int64_t)n * s_row,
-                           TTO_F32, 1, 0, 0, extra, xf[slot], cols, 1, lpr);
+                           TTO_F32, 1, 0, 0, xf[slot], cols, 1, lpr);
       v = round_rt(rt, v);
       if (bias) v = round_rt(rt, v + act_get(bias, bdtype, e * bias_expert + n));
       combined = fmaf(v, act_get(scores, sdtype, slot), combined);
@@ -573,7 +569,7 @@ int tto_router(const void* w, int wdt, int64_t w_row, const void* x, int xdt, in
   float lg[1024], sc[1024];
   const int fmt = wdt == TTO_BF16 ? FMT_BF16W : FMT_F16W;
   for (int e = 0; e < E; e++) {
-    float v = tto_gemv_row(fmt, SM_NONE, (const uint8_t*)w + (size_t)(e * w_row) * 2, NULL, TTO_F32, 0, 0, 0, 0, x, xdt,
+    float v = tto_gemv_row(fmt, SM_NONE, (const uint8_t*)w + (size_t)(e * w_row) * 2, NULL, TTO_F32, 0, 0, 0, x, xdt,
                            H, 1, 64);
     v = tto_round_bf16(v);
     if (bias) v = tto_round_bf16(v + act_get(bias, bdt, e));

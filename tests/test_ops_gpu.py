@@ -94,10 +94,11 @@ def test_rope_table_and_device_position(backend, device):
     assert_bits_equal(from_torch_bits(k_t), kw, "rope k")
 
 
+@pytest.mark.parametrize("cap", [1100, 1152])  # 1152: whole chunks, contiguous rows -> vector-load kernel
 @pytest.mark.parametrize("heads,kv_heads,tokens,sinks", [(32, 8, 513, False), (64, 8, 1025, True), (8, 8, 5, False),
-                                                         (32, 8, 64, True)])
-def test_gqa_attention(backend, device, heads, kv_heads, tokens, sinks):
-    D, cap = 64, 1100
+                                                         (32, 8, 64, True), (128, 8, 1100, False)])
+def test_gqa_attention(backend, device, heads, kv_heads, tokens, sinks, cap):
+    D = 64
     g = rng(heads + tokens)
     q = f16_normal(g, heads * D)
     keys = f16_normal(g, (kv_heads, cap, D))
@@ -141,6 +142,28 @@ def test_router_topk_on_logits_with_ties(backend, device):
     widx = np.empty(4, dtype=np.int32)
     wsc = np.empty(4, dtype=np.float16)
     oracle.lib().tto_topk(P(lg), oracle.F16, 8, 4, 1, P(widx), P(wsc), oracle.F16)
+    assert_bits_equal(from_torch_bits(sc), wsc, "topk scores")
+
+
+@pytest.mark.parametrize("E,k,renorm,special", [(128, 128, True, False), (128, 100, False, True), (65, 64, True, True),
+                                                (100, 7, False, False), (32, 4, True, True), (3, 3, False, True)])
+def test_router_topk_wave_selection(backend, device, E, k, renorm, special):
+    """Many equal values (coarse quantisation), signed zeros, -inf and NaN logits:
+    slot order, indices and scores equal the sequential oracle scan."""
+    g = rng(E * 1000 + k)
+    lg = (np.round(g.standard_normal(E) * 2) / 2).astype(np.float16)
+    if special:
+        lg[g.integers(0, E, size=max(1, E // 8))] = np.float16(0.0)
+        lg[g.integers(0, E, size=max(1, E // 8))] = np.float16(-0.0)
+        lg[g.integers(0, E, size=max(1, E // 16))] = np.float16(-np.inf)
+        lg[g.integers(1, E, size=max(1, E // 16))] = np.float16(np.nan)
+    idx = torch.empty(k, device=device, dtype=torch.int32)
+    sc = torch.empty(k, device=device, dtype=torch.float16)
+    backend.moe_router_topk(to_torch(lg, device), idx, sc, renormalize=renorm)
+    widx = np.empty(k, dtype=np.int32)
+    wsc = np.empty(k, dtype=np.float16)
+    oracle.lib().tto_topk(P(lg), oracle.F16, E, k, int(renorm), P(widx), P(wsc), oracle.F16)
+    assert np.array_equal(idx.cpu().numpy(), widx)
     assert_bits_equal(from_torch_bits(sc), wsc, "topk scores")
 
 

@@ -133,7 +133,7 @@ def test_mxfp4_and_lowbit_emulation_vs_closed_form():
     scales = g.integers(119, 124, size=(rows, cols // 32), dtype=np.uint8)
     x = f16_normal(g, cols)
     got = oracle.gemv("mxfp4", "block_e8", blocks.reshape(rows, -1), scales, x, cols=cols, lpr=32, s_row=cols // 32,
-                      e8_extra=14, odtype=oracle.F32)
+                      odtype=oracle.F32)
     assert ref.max_rel_err(got, ref.gemv64(ref.mxfp4_dequant(blocks, scales), x)) < 1e-5
     for bits in (1, 2):
         c = g.integers(0, 1 << bits, size=(1, rows, cols), dtype=np.uint8)

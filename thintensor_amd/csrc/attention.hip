@@ -39,13 +39,17 @@ struct AttnParams {
   void* out;              // [heads, D]
 };
 
-template <typename T, int G>
+// DC: head_dim known at compile time (0: runtime head_dim, scalar loads).  With DC
+// set and contiguous rows (token stride DC), the K row of a lane is read with
+// 128-bit loads and the V column of the chunk is loaded in full before the weighted
+// sum, so each phase waits for memory once.
+template <typename T, int G, int DC>
 __global__ __launch_bounds__(64) void attn_partial_kernel(AttnParams P) {
   const int kvh = blockIdx.y;
   const int c = blockIdx.x;
   const int T_act = min(P.tokens_dev ? P.tokens_dev[0] + P.tokens : P.tokens, P.max_tokens);
   if (c * kChunk >= T_act) return;
-  const int D = P.head_dim;
+  const int D = DC ? DC : P.head_dim;
   const int lane = threadIdx.x;
   __shared__ float q_s[G * 256];
   __shared__ float p_s[G * kChunk];
@@ -55,14 +59,34 @@ __global__ __launch_bounds__(64) void attn_partial_kernel(AttnParams P) {
   // phase 1: lane = token
   const int t = c * kChunk + lane;
   const bool valid = t < T_act;
-  const T* krow = reinterpret_cast<const T*>(P.keys) + kvh * P.k_head + (int64_t)(valid ? t : 0) * P.k_tok;
+  const int nt = min(kChunk, T_act - c * kChunk);
   float sc[G];
 #pragma unroll
   for (int g = 0; g < G; g++) sc[g] = 0.0f;
-  for (int d = 0; d < D; d++) {
-    const float kv = to_f32(krow[d]);
+  if constexpr (DC != 0) {
+    // contiguous rows, capacity a whole number of chunks: every row of the chunk is in
+    // bounds, rows past the count are read and masked
+    const uint4* krow = reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(P.keys) + kvh * P.k_head + (int64_t)t * DC);
+    uint4 kr[DC / 8];
 #pragma unroll
-    for (int g = 0; g < G; g++) sc[g] = __builtin_fmaf(q_s[g * D + d], kv, sc[g]);
+    for (int i = 0; i < DC / 8; i++) kr[i] = krow[i];
+#pragma unroll
+    for (int i = 0; i < DC / 8; i++) {
+      const uint32_t kw[4] = {kr[i].x, kr[i].y, kr[i].z, kr[i].w};
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const float kv = (e & 1) ? hi_f32<T>(kw[e >> 1]) : lo_f32<T>(kw[e >> 1]);
+#pragma unroll
+        for (int g = 0; g < G; g++) sc[g] = __builtin_fmaf(q_s[g * DC + 8 * i + e], kv, sc[g]);
+      }
+    }
+  } else {
+    const T* krow = reinterpret_cast<const T*>(P.keys) + kvh * P.k_head + (int64_t)(valid ? t : 0) * P.k_tok;
+    for (int d = 0; d < D; d++) {
+      const float kv = to_f32(krow[d]);
+#pragma unroll
+      for (int g = 0; g < G; g++) sc[g] = __builtin_fmaf(q_s[g * D + d], kv, sc[g]);
+    }
   }
   const float ninf = __builtin_bit_cast(float, 0xff800000u);
 #pragma unroll
@@ -85,51 +109,115 @@ __global__ __launch_bounds__(64) void attn_partial_kernel(AttnParams P) {
     }
   }
   __syncthreads();
-  // phase 2: lane = dimension
-  const int nt = min(kChunk, T_act - c * kChunk);
-  for (int d = lane; d < D; d += 64) {
+  // phase 2: lane = dimension, o = fma chain over the chunk's tokens ascending
+  if constexpr (DC == 64) {
+    const T* vcol = reinterpret_cast<const T*>(P.values) + kvh * P.v_head + (int64_t)(c * kChunk) * DC + lane;
+    float vv[kChunk];
+#pragma unroll
+    for (int tt = 0; tt < kChunk; tt++) vv[tt] = to_f32(vcol[tt * DC]);
     float o[G];
 #pragma unroll
     for (int g = 0; g < G; g++) o[g] = 0.0f;
-    const T* vcol = reinterpret_cast<const T*>(P.values) + kvh * P.v_head + (int64_t)(c * kChunk) * P.v_tok + d;
-    for (int tt = 0; tt < nt; tt++) {
-      const float vv = to_f32(vcol[(int64_t)tt * P.v_tok]);
+    // tokens past the count add fma(0, 0, o) == o (p is 0 there and o is never -0)
 #pragma unroll
-      for (int g = 0; g < G; g++) o[g] = __builtin_fmaf(p_s[g * kChunk + tt], vv, o[g]);
+    for (int tt = 0; tt < kChunk; tt++) {
+      const float v = tt < nt ? vv[tt] : 0.0f;
+#pragma unroll
+      for (int g = 0; g < G; g++) o[g] = __builtin_fmaf(p_s[g * kChunk + tt], v, o[g]);
     }
 #pragma unroll
-    for (int g = 0; g < G; g++) P.part_o[((int64_t)(h0 + g) * P.max_chunks + c) * D + d] = o[g];
+    for (int g = 0; g < G; g++) P.part_o[((int64_t)(h0 + g) * P.max_chunks + c) * DC + lane] = o[g];
+  } else {
+    for (int d = lane; d < D; d += 64) {
+      float o[G];
+#pragma unroll
+      for (int g = 0; g < G; g++) o[g] = 0.0f;
+      const T* vcol = reinterpret_cast<const T*>(P.values) + kvh * P.v_head + (int64_t)(c * kChunk) * P.v_tok + d;
+      for (int tt = 0; tt < nt; tt++) {
+        const float vv = to_f32(vcol[(int64_t)tt * P.v_tok]);
+#pragma unroll
+        for (int g = 0; g < G; g++) o[g] = __builtin_fmaf(p_s[g * kChunk + tt], vv, o[g]);
+      }
+#pragma unroll
+      for (int g = 0; g < G; g++) P.part_o[((int64_t)(h0 + g) * P.max_chunks + c) * D + d] = o[g];
+    }
   }
 }
 
+// Combine of one head, same arithmetic as the sequential description above: the
+// chunk metadata is loaded one chunk per lane, exp(m_c - M) is evaluated per lane and
+// the chunk-order folds read it back lane by lane.
 template <typename T, typename SKT>
 __global__ __launch_bounds__(64) void attn_combine_kernel(AttnParams P) {
   const int h = blockIdx.x;
+  const int lane = threadIdx.x;
   const int T_act = min(P.tokens_dev ? P.tokens_dev[0] + P.tokens : P.tokens, P.max_tokens);
-  const int nc = (T_act + kChunk - 1) / kChunk;
+  const int nc = T_act > 0 ? (T_act + kChunk - 1) / kChunk : 0;
   const float* pm = P.part_m + (int64_t)h * P.max_chunks;
   const float* pl = P.part_l + (int64_t)h * P.max_chunks;
-  float M = __builtin_bit_cast(float, 0xff800000u);
+  const float ninf = __builtin_bit_cast(float, 0xff800000u);
+  float M = ninf;
   const bool has_sink = P.sinks != nullptr;
   float sink = 0.0f;
   if (has_sink) {
     sink = to_f32(reinterpret_cast<const SKT*>(P.sinks)[h]);
     M = sink;
   }
-  for (int c = 0; c < nc; c++) M = fmaxf(M, pm[c]);
+  // the maximum ignores NaN and does not depend on the order
+  for (int c0 = 0; c0 < nc; c0 += 64) {
+    float m = c0 + lane < nc ? pm[c0 + lane] : ninf;
+    m = fmaxf(m, xor_partner<1>(m));
+    m = fmaxf(m, xor_partner<2>(m));
+    m = fmaxf(m, xor_partner<4>(m));
+    m = fmaxf(m, xor_partner<8>(m));
+    m = fmaxf(m, xor_partner<16>(m));
+    m = fmaxf(m, xor_partner<32>(m));
+    M = fmaxf(M, m);
+  }
   float den = has_sink ? exp_f32(sink - M) : 0.0f;
-  for (int c = 0; c < nc; c++) den = __builtin_fmaf(pl[c], exp_f32(pm[c] - M), den);
-  for (int d = threadIdx.x; d < P.head_dim; d += 64) {
-    float acc = 0.0f;
-    for (int c = 0; c < nc; c++)
-      acc = __builtin_fmaf(P.part_o[((int64_t)h * P.max_chunks + c) * P.head_dim + d], exp_f32(pm[c] - M), acc);
-    store<T>(reinterpret_cast<T*>(P.out) + (int64_t)h * P.head_dim + d, acc / den);
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  const int D = P.head_dim;
+  for (int c0 = 0; c0 < nc; c0 += 64) {
+    const int n = min(64, nc - c0);
+    const float e = c0 + lane < nc ? exp_f32(pm[c0 + lane] - M) : 0.0f;
+    const float l = c0 + lane < nc ? pl[c0 + lane] : 0.0f;
+    for (int c1 = 0; c1 < n; c1 += 8) {
+      // partials of eight chunks are loaded before they are folded in chunk order
+      float po[8][4];
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const int d = lane + 64 * q;
+          po[u][q] = (c1 + u < n && d < D) ? P.part_o[((int64_t)h * P.max_chunks + c0 + c1 + u) * D + d] : 0.0f;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        if (c1 + u < n) {
+          const int c = c1 + u;
+          const float ec = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e), c));
+          const float lc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, l), c));
+          den = __builtin_fmaf(lc, ec, den);
+#pragma unroll
+          for (int q = 0; q < 4; q++) acc[q] = __builtin_fmaf(po[u][q], ec, acc[q]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    const int d = lane + 64 * q;
+    if (d < D) store<T>(reinterpret_cast<T*>(P.out) + (int64_t)h * D + d, acc[q] / den);
   }
 }
 
 template <typename T, int G>
-static int launch_attn(const AttnParams& P, int sink_dtype, hipStream_t st) {
-  hipLaunchKernelGGL((attn_partial_kernel<T, G>), dim3(P.max_chunks, P.kv_heads), dim3(64), 0, st, P);
+static int launch_attn(const AttnParams& P, int sink_dtype, bool contiguous64, hipStream_t st) {
+  if (contiguous64)
+    hipLaunchKernelGGL((attn_partial_kernel<T, G, 64>), dim3(P.max_chunks, P.kv_heads), dim3(64), 0, st, P);
+  else
+    hipLaunchKernelGGL((attn_partial_kernel<T, G, 0>), dim3(P.max_chunks, P.kv_heads), dim3(64), 0, st, P);
   int rc = check_launch("gqa_attention");
   if (rc) return rc;
   switch (sink_dtype) {
@@ -178,14 +266,18 @@ extern "C" int tt_single_token_gqa_attention(const void* q, const void* keys, co
   P.out = out;
   const int G = (int)(heads / kv_heads);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  // 128-bit K loads and whole-chunk V loads need contiguous 64-wide rows and a
+  // capacity that is a whole number of chunks
+  const bool c64 = head_dim == 64 && k_tok == 64 && v_tok == 64 && max_tokens % kChunk == 0 && aligned(keys, 16) &&
+                   k_head % 8 == 0 && heads / kv_heads <= 8;
   auto by_g = [&](auto t) -> int {
     using T = decltype(t);
     switch (G) {
-      case 1: return launch_attn<T, 1>(P, sink_dtype, st);
-      case 2: return launch_attn<T, 2>(P, sink_dtype, st);
-      case 4: return launch_attn<T, 4>(P, sink_dtype, st);
-      case 8: return launch_attn<T, 8>(P, sink_dtype, st);
-      case 16: return launch_attn<T, 16>(P, sink_dtype, st);
+      case 1: return launch_attn<T, 1>(P, sink_dtype, c64, st);
+      case 2: return launch_attn<T, 2>(P, sink_dtype, c64, st);
+      case 4: return launch_attn<T, 4>(P, sink_dtype, c64, st);
+      case 8: return launch_attn<T, 8>(P, sink_dtype, c64, st);
+      case 16: return launch_attn<T, 16>(P, sink_dtype, c64, st);
     }
     set_error("%s: query heads per KV head must be 1, 2, 4, 8 or 16 (got %d)", what, G);
     return TT_ERR_UNSUPPORTED;

@@ -31,7 +31,6 @@ int selected_e8(const char* what, Fmt fmt, const void* packed, int64_t w_expert_
   P.out_slot = out_slot;
   P.cols = (int)cols;
   const int Lg = 1;
-  P.e8_extra = fmt == Fmt::kMxfp4 ? 14 : 0;
   const int lpr = tt_gemv_lanes_per_row(cols / 32, 1);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int slots = (int)selected;

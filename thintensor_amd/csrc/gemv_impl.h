@@ -43,7 +43,6 @@ struct GemvParams {
   int64_t s_pair;          // affine: element offset of the second scale value
   int aff_zero;            // affine pair holds (s, z) instead of (s, m)
   int cols;
-  int e8_extra;            // extra power of two folded into E8M0 block scales
   uint64_t* am_partials;   // argmax epilogue: one key per wave (null: plain GEMV)
 };
 
@@ -57,19 +56,6 @@ __device__ __forceinline__ uint64_t argmax_key(float v, uint32_t idx) {
   if ((b & 0x7fffffffu) > 0x7f800000u) o = 0xffffffffu;
   else o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
   return ((uint64_t)o << 32) | (uint64_t)(0xffffffffu - idx);
-}
-
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t k) {
-#define TT_MAXSTEP(M)                                                                                     \
-  {                                                                                                       \
-    const uint32_t hi = __builtin_bit_cast(uint32_t, xor_partner<M>(__builtin_bit_cast(float, (uint32_t)(k >> 32)))); \
-    const uint32_t lo = __builtin_bit_cast(uint32_t, xor_partner<M>(__builtin_bit_cast(float, (uint32_t)k)));         \
-    const uint64_t o = ((uint64_t)hi << 32) | lo;                                                         \
-    k = o > k ? o : k;                                                                                    \
-  }
-  TT_MAXSTEP(1) TT_MAXSTEP(2) TT_MAXSTEP(4) TT_MAXSTEP(8) TT_MAXSTEP(16) TT_MAXSTEP(32)
-#undef TT_MAXSTEP
-  return k;
 }
 
 constexpr int log2c(int v) { return v <= 1 ? 0 : 1 + log2c(v / 2); }
@@ -256,9 +242,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
       } else if constexpr (SM == SMode::kBlockE8) {
 #pragma unroll
         for (int i = 0; i < ROWS; i++) {
-          float q = p[i];
-          if (P.e8_extra) q = q * pow2i(P.e8_extra);
-          const float t = q * pow2i(cd.e[i] - 127);
+          const float t = p[i] * pow2i(cd.e[i] - 127);
           acc[i] = acc[i] + ((cv && cb.rv[i]) ? t : 0.0f);
         }
       } else {

@@ -21,7 +21,7 @@ struct SwigluParams {
   const void* bias; int64_t bias_expert;
   float alpha, limit;
   void* out; int64_t out_slot;
-  int act_rows, cols, e8_extra;
+  int act_rows, cols;
 };
 
 template <typename BT> __device__ __forceinline__ float ld_bias(const void* b, int64_t i) {
@@ -71,7 +71,7 @@ __global__ __launch_bounds__(256) void swiglu_kernel(SwigluParams P) {
     }
     if (!active) break;
     float dot[2 * APW];
-    e8_rows_dot<F, XT, LPR, 2 * APW>(cur, wrow, srow, rv, xs_lds, nchunks, l, P.e8_extra, dot);
+    e8_rows_dot<F, XT, LPR, 2 * APW>(cur, wrow, srow, rv, xs_lds, nchunks, l, dot);
 #pragma unroll
     for (int i = 0; i < APW; i++) {
       if (!rv[2 * i] || l != i) continue;
@@ -99,77 +99,78 @@ struct DownParams {
   const void* scores;
   const void* bias; int64_t bias_expert;
   void* out;
-  int rows, cols, slots, e8_extra;
+  int rows, cols, slots;
 };
 
 template <typename ScT> __device__ __forceinline__ float ld_score(const void* p, int i) {
   return to_f32(reinterpret_cast<const ScT*>(p)[i]);
 }
 
+// One block owns RB = RPW * (64 / LPR) output rows.  Its four waves split the
+// selected slots (wave w computes slots w, w + 4, ...), each slot's row values
+// v = round(dot) (+ bias, rounded again) go to LDS, and after the barrier lane t of
+// the block combines row t in slot order: c = fma(v_s, score_s, c) from +0.
 template <Fmt F, typename XT, typename OT, typename RT, typename BT, typename ScT, int LPR, int RPW>
 __global__ __launch_bounds__(256) void weighted_down_kernel(DownParams P) {
   extern __shared__ uint32_t xs_lds[];
   constexpr int SUBS = 64 / LPR;
+  constexpr int RB = RPW * SUBS;
   const int words = P.cols >> 1;
+  float* vals = reinterpret_cast<float*>(xs_lds + P.slots * words);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nwaves = blockDim.x >> 6;
   const int sub = lane / LPR, l = lane % LPR;
   const int nchunks = P.cols >> 5;
-  const int per_iter = RPW * SUBS;
-  const int waves_total = gridDim.x * (blockDim.x >> 6);
-  bool staged = false;
-  for (int base = (blockIdx.x * (blockDim.x >> 6) + wave) * per_iter;; base += waves_total * per_iter) {
-    const bool active = base < P.rows;
-    int row[RPW];
-    bool rv[RPW];
-    float combined[RPW];
+  const int row0 = blockIdx.x * RB;
+  int row[RPW];
+  bool rv[RPW];
 #pragma unroll
-    for (int i = 0; i < RPW; i++) {
-      row[i] = base + i * SUBS + sub;
-      rv[i] = row[i] < P.rows;
-      combined[i] = 0.0f;
-    }
-    const uint8_t* wrow[RPW];
-    const uint8_t* srow[RPW];
-    int64_t e = P.experts[0];
+  for (int i = 0; i < RPW; i++) {
+    row[i] = row0 + i * SUBS + sub;
+    rv[i] = row[i] < P.rows;
+  }
+  const uint8_t* wrow[RPW];
+  const uint8_t* srow[RPW];
+  int64_t e = 0;
+  auto point = [&](int s) {
+    e = P.experts[s];
 #pragma unroll
     for (int i = 0; i < RPW; i++) {
       wrow[i] = P.w + e * P.w_expert + (int64_t)row[i] * P.w_row;
       srow[i] = P.s + e * P.s_expert + (int64_t)row[i] * P.s_row;
     }
-    E8Round<F, RPW> cur;
-    if (active) e8_fetch<F, LPR, RPW>(cur, 0, l, nchunks, wrow, srow, rv);
-    if (!staged) {
-      for (int s = 0; s < P.slots; s++) {
-        const uint32_t* xg = reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(P.x) + (int64_t)s * P.x_slot);
-        for (int i = threadIdx.x; i < words; i += blockDim.x) xs_lds[s * words + i] = xg[i];
-      }
-      __syncthreads();
-      staged = true;
+  };
+  E8Round<F, RPW> cur;
+  int s = wave;
+  if (s < P.slots) {
+    point(s);
+    e8_fetch<F, LPR, RPW>(cur, 0, l, nchunks, wrow, srow, rv);
+  }
+  for (int t = 0; t < P.slots; t++) {
+    const uint32_t* xg = reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(P.x) + (int64_t)t * P.x_slot);
+    for (int i = threadIdx.x; i < words; i += blockDim.x) xs_lds[t * words + i] = xg[i];
+  }
+  __syncthreads();
+  for (; s < P.slots; s += nwaves) {
+    if (s != wave) {
+      point(s);
+      e8_fetch<F, LPR, RPW>(cur, 0, l, nchunks, wrow, srow, rv);
     }
-    if (!active) break;
-    for (int s = 0; s < P.slots; s++) {
-      if (s > 0) {
-        e = P.experts[s];
+    float dot[RPW];
+    e8_rows_dot<F, XT, LPR, RPW>(cur, wrow, srow, rv, xs_lds + s * words, nchunks, l, dot);
 #pragma unroll
-        for (int i = 0; i < RPW; i++) {
-          wrow[i] = P.w + e * P.w_expert + (int64_t)row[i] * P.w_row;
-          srow[i] = P.s + e * P.s_expert + (int64_t)row[i] * P.s_row;
-        }
-        e8_fetch<F, LPR, RPW>(cur, 0, l, nchunks, wrow, srow, rv);
-      }
-      float dot[RPW];
-      e8_rows_dot<F, XT, LPR, RPW>(cur, wrow, srow, rv, xs_lds + s * words, nchunks, l, P.e8_extra, dot);
-      const float score = ld_score<ScT>(P.scores, s);
-#pragma unroll
-      for (int i = 0; i < RPW; i++) {
-        float v = round_to<RT>(dot[i]);
-        if (P.bias != nullptr && rv[i]) v = round_to<RT>(v + ld_bias<BT>(P.bias, e * P.bias_expert + row[i]));
-        combined[i] = __builtin_fmaf(v, score, combined[i]);
-      }
+    for (int i = 0; i < RPW; i++) {
+      if (l != i || !rv[i]) continue;
+      float v = round_to<RT>(dot[i]);
+      if (P.bias != nullptr) v = round_to<RT>(v + ld_bias<BT>(P.bias, e * P.bias_expert + row[i]));
+      vals[s * RB + i * SUBS + sub] = v;
     }
-#pragma unroll
-    for (int i = 0; i < RPW; i++)
-      if (rv[i] && l == i) store<OT>(reinterpret_cast<OT*>(P.out) + row[i], combined[i]);
+  }
+  __syncthreads();
+  if (threadIdx.x < RB && row0 + (int)threadIdx.x < P.rows) {
+    float c = 0.0f;
+    for (int t = 0; t < P.slots; t++) c = __builtin_fmaf(vals[t * RB + threadIdx.x], ld_score<ScT>(P.scores, t), c);
+    store<OT>(reinterpret_cast<OT*>(P.out) + row0 + threadIdx.x, c);
   }
 }
 
@@ -210,18 +211,16 @@ static int launch_swiglu(const SwigluParams& P, int lpr, int slots, hipStream_t 
 
 template <Fmt F, typename XT, typename OT, typename RT, typename BT, typename ScT>
 static int launch_down(const DownParams& P, int lpr, hipStream_t st) {
-  const size_t lds = (size_t)P.cols * 2 * P.slots;
-  auto go = [&](auto kern, int subs) {
-    constexpr int RPW = 4;
-    const int per_block = 4 * RPW * subs;
-    const int blocks = (P.rows + per_block - 1) / per_block;
+  auto go = [&](auto kern, int rb) {
+    const size_t lds = (size_t)P.cols * 2 * P.slots + (size_t)rb * 4 * P.slots;
+    const int blocks = (P.rows + rb - 1) / rb;
     hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), lds, st, P);
     return check_launch("mxfp_lowbit_weighted_down");
   };
   switch (lpr) {
-    case 64: return go(weighted_down_kernel<F, XT, OT, RT, BT, ScT, 64, 4>, 1);
-    case 32: return go(weighted_down_kernel<F, XT, OT, RT, BT, ScT, 32, 4>, 2);
-    default: return go(weighted_down_kernel<F, XT, OT, RT, BT, ScT, 16, 4>, 4);
+    case 64: return go(weighted_down_kernel<F, XT, OT, RT, BT, ScT, 64, 4>, 4);
+    case 32: return go(weighted_down_kernel<F, XT, OT, RT, BT, ScT, 32, 4>, 8);
+    default: return go(weighted_down_kernel<F, XT, OT, RT, BT, ScT, 16, 4>, 16);
   }
 }
 
@@ -295,7 +294,7 @@ extern "C" int tt_mxfp_lowbit_selected_swiglu(const void* packed, int64_t w_expe
   if (bias) TT_REQUIRE(valid_out_dtype(bias_dtype), "%s: bad bias dtype", what);
   SwigluParams P{static_cast<const uint8_t*>(packed), w_expert_bytes, w_row_bytes,
                  static_cast<const uint8_t*>(scales), s_expert, s_row, x, x_slot, expert_indices, bias, bias_expert,
-                 alpha, limit, out, out_slot, (int)activation_rows, (int)cols, bits == 4 ? 14 : 0};
+                 alpha, limit, out, out_slot, (int)activation_rows, (int)cols};
   const int lpr = tt_gemv_lanes_per_row(cols / 32, 1);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const Fmt fmt = fmt_for_bits(bits);
@@ -318,7 +317,8 @@ extern "C" int tt_mxfp_lowbit_weighted_down(const void* packed, int64_t w_expert
   TT_REQUIRE(bits == 1 || bits == 2 || bits == 4, "%s: fused down requires packed Q1, Q2 or MXFP4 experts", what);
   TT_REQUIRE(valid_act_dtype(x_dtype) && valid_out_dtype(out_dtype), "%s: bad dtype codes", what);
   TT_REQUIRE(cols > 0 && cols % 32 == 0, "%s: cols must be a multiple of 32", what);
-  TT_REQUIRE(selected >= 1 && selected * cols <= 32768, "%s: selected * cols must fit the 64 KiB staged activations", what);
+  TT_REQUIRE(selected >= 1 && selected * (2 * cols + 64) <= 65536,
+             "%s: selected activations and row values must fit 64 KiB of LDS", what);
   TT_REQUIRE(rows > 0 && rows < (1 << 30), "%s: bad rows", what);
   const int align = bits == 4 ? 16 : (bits == 2 ? 8 : 4);
   TT_REQUIRE(packed && aligned(packed, align) && w_row_bytes % align == 0 && w_expert_bytes % align == 0,
@@ -329,7 +329,7 @@ extern "C" int tt_mxfp_lowbit_weighted_down(const void* packed, int64_t w_expert
   if (bias) TT_REQUIRE(valid_out_dtype(bias_dtype), "%s: bad bias dtype", what);
   DownParams P{static_cast<const uint8_t*>(packed), w_expert_bytes, w_row_bytes,
                static_cast<const uint8_t*>(scales), s_expert, s_row, x, x_slot, expert_indices, router_scores, bias,
-               bias_expert, out, (int)rows, (int)cols, (int)selected, bits == 4 ? 14 : 0};
+               bias_expert, out, (int)rows, (int)cols, (int)selected};
   const int lpr = tt_gemv_lanes_per_row(cols / 32, 1);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const Fmt fmt = fmt_for_bits(bits);

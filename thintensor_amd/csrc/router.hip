@@ -21,31 +21,80 @@ template <typename T> __device__ __forceinline__ float ldv(const void* p, int64_
   return to_f32(reinterpret_cast<const T*>(p)[i]);
 }
 
-__device__ void select_topk(const float* logits, int E, int top_k, bool renorm, int32_t* idx_out, float* sel_out,
-                            float* den_out) {
-  float maximum = __builtin_bit_cast(float, 0xff800000u);
-  for (int e = 0; e < E; e++) maximum = fmaxf(maximum, logits[e]);
-  bool taken[128];
-  for (int e = 0; e < E; e++) taken[e] = false;
+// Ordered key of a router logit: larger value wins, equal values (+0 == -0) go to
+// the lowest expert index.  NaN never wins through the key (see wave_topk).
+__device__ __forceinline__ uint64_t topk_key(float v, uint32_t e) {
+  uint32_t b = __builtin_bit_cast(uint32_t, v);
+  if ((b & 0x7fffffffu) == 0) b = 0;
+  const uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  return ((uint64_t)o << 32) | (uint64_t)(0xffffffffu - e);
+}
+
+__device__ __forceinline__ float lane_value(float a, float b, int i) {
+  return i < 64 ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a), i))
+                : __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, b), i - 64));
+}
+
+// Top-k + softmax over E <= 128 logits held by one wave (expert e in lane e % 64,
+// register e / 64).  Same result as scanning the experts in order for each slot:
+// the first untaken expert starts the scan and a later one replaces it only when
+// strictly greater -- so a NaN at the first untaken position is selected, any other
+// NaN never is, and equal values keep the lowest index.  The denominator is summed
+// sequentially in slot order (renormalize) or expert order, each term
+// exp(v - max) with max the NaN-ignoring maximum over all experts.
+template <typename OT>
+__device__ void wave_topk(float lg0, float lg1, int E, int top_k, bool renorm, int32_t* idx_out, OT* score_out) {
+  const int lane = lane_id();
+  const bool v0 = lane < E, v1 = lane + 64 < E;
+  float m = __builtin_bit_cast(float, 0xff800000u);
+  if (v0) m = fmaxf(m, lg0);
+  if (v1) m = fmaxf(m, lg1);
+  m = fmaxf(m, xor_partner<1>(m));
+  m = fmaxf(m, xor_partner<2>(m));
+  m = fmaxf(m, xor_partner<4>(m));
+  m = fmaxf(m, xor_partner<8>(m));
+  m = fmaxf(m, xor_partner<16>(m));
+  m = fmaxf(m, xor_partner<32>(m));
+  bool t0 = !v0, t1 = !v1;
+  float sel0 = 0.0f, sel1 = 0.0f;
   for (int s = 0; s < top_k; s++) {
-    int bi = -1;
-    float bv = 0.0f;
-    for (int e = 0; e < E; e++) {
-      if (taken[e]) continue;
-      if (bi < 0 || logits[e] > bv) { bi = e; bv = logits[e]; }
+    uint64_t k = 0, f = 0;
+    if (!t0) {
+      f = 0xffffffffu - (uint32_t)lane;
+      if (!__builtin_isnan(lg0)) k = topk_key(lg0, lane);
     }
-    taken[bi] = true;
-    idx_out[s] = bi;
-    sel_out[s] = bv;
+    if (!t1) {
+      if (f == 0) f = 0xffffffffu - (uint32_t)(lane + 64);
+      if (!__builtin_isnan(lg1)) {
+        const uint64_t k1 = topk_key(lg1, lane + 64);
+        k = k1 > k ? k1 : k;
+      }
+    }
+    k = wave_max_u64(k);
+    f = wave_max_u64(f);
+    const int first = __builtin_amdgcn_readfirstlane((int)(0xffffffffu - (uint32_t)f));
+    const float fv = lane_value(lg0, lg1, first);
+    int bi = first;
+    if (!__builtin_isnan(fv)) bi = __builtin_amdgcn_readfirstlane((int)(0xffffffffu - (uint32_t)k));
+    const float bv = lane_value(lg0, lg1, bi);
+    if (lane == bi) t0 = true;
+    if (lane + 64 == bi) t1 = true;
+    if (lane == (s & 63)) {
+      if (s < 64) sel0 = bv;
+      else sel1 = bv;
+    }
+    if (lane == 0) idx_out[s] = bi;
   }
+  const float e0 = exp_f32(sel0 - m), e1 = exp_f32(sel1 - m);
   float den = 0.0f;
   if (renorm) {
-    for (int s = 0; s < top_k; s++) den = den + exp_f32(sel_out[s] - maximum);
+    for (int s = 0; s < top_k; s++) den = den + lane_value(e0, e1, s);
   } else {
-    for (int e = 0; e < E; e++) den = den + exp_f32(logits[e] - maximum);
+    const float a0 = exp_f32(lg0 - m), a1 = exp_f32(lg1 - m);
+    for (int e = 0; e < E; e++) den = den + lane_value(a0, a1, e);
   }
-  for (int s = 0; s < top_k; s++) sel_out[s] = exp_f32(sel_out[s] - maximum) / den;
-  *den_out = den;
+  if (lane < top_k) store<OT>(score_out + lane, e0 / den);
+  if (lane + 64 < top_k) store<OT>(score_out + lane + 64, e1 / den);
 }
 
 template <typename WT, typename XT, typename BT, typename OT>
@@ -75,23 +124,20 @@ __global__ __launch_bounds__(1024) void router_kernel(const void* w, int64_t w_r
     if (lane == 0) logits[e] = lg;
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    float sel[128];
-    float den;
-    select_topk(logits, E, top_k, renorm != 0, idx_out, sel, &den);
-    for (int s = 0; s < top_k; s++) store<OT>(reinterpret_cast<OT*>(score_out) + s, sel[s]);
+  if (wave == 0) {
+    const float l0 = lane < E ? logits[lane] : 0.0f;
+    const float l1 = lane + 64 < E ? logits[lane + 64] : 0.0f;
+    wave_topk<OT>(l0, l1, E, top_k, renorm != 0, idx_out, reinterpret_cast<OT*>(score_out));
   }
 }
 
 template <typename LT, typename OT>
-__global__ void topk_kernel(const void* logits_in, int E, int top_k, int renorm, int32_t* idx_out, void* score_out) {
-  if (threadIdx.x != 0) return;
-  float logits[128];
-  for (int e = 0; e < E; e++) logits[e] = ldv<LT>(logits_in, e);
-  float sel[128];
-  float den;
-  select_topk(logits, E, top_k, renorm != 0, idx_out, sel, &den);
-  for (int s = 0; s < top_k; s++) store<OT>(reinterpret_cast<OT*>(score_out) + s, sel[s]);
+__global__ __launch_bounds__(64) void topk_kernel(const void* logits_in, int E, int top_k, int renorm, int32_t* idx_out,
+                                                  void* score_out) {
+  const int lane = lane_id();
+  const float l0 = lane < E ? ldv<LT>(logits_in, lane) : 0.0f;
+  const float l1 = lane + 64 < E ? ldv<LT>(logits_in, lane + 64) : 0.0f;
+  wave_topk<OT>(l0, l1, E, top_k, renorm != 0, idx_out, reinterpret_cast<OT*>(score_out));
 }
 
 template <typename Fn> static int dt3(int code, Fn&& f) {

@@ -151,4 +151,18 @@ __device__ __forceinline__ float pow2i(int e) {
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 
+// Maximum of a 64-bit key over the wave (every lane gets the result).
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t k) {
+#define TT_MAXSTEP(M)                                                                                     \
+  {                                                                                                       \
+    const uint32_t hi = __builtin_bit_cast(uint32_t, xor_partner<M>(__builtin_bit_cast(float, (uint32_t)(k >> 32)))); \
+    const uint32_t lo = __builtin_bit_cast(uint32_t, xor_partner<M>(__builtin_bit_cast(float, (uint32_t)k)));         \
+    const uint64_t o = ((uint64_t)hi << 32) | lo;                                                         \
+    k = o > k ? o : k;                                                                                    \
+  }
+  TT_MAXSTEP(1) TT_MAXSTEP(2) TT_MAXSTEP(4) TT_MAXSTEP(8) TT_MAXSTEP(16) TT_MAXSTEP(32)
+#undef TT_MAXSTEP
+  return k;
+}
+
 }  // namespace tt

@@ -93,9 +93,9 @@ __device__ __forceinline__ void nib_pairs(uint32_t w, float off, h2& a, h2& b, h
   d = hfma(as_h2(and_or(w8, 0x00F000F0u, 0x64006400u)), 0.0625f, -(64.0f + off));
 }
 
-// Decoded weights of one chunk, element e of the chunk in wv[e] (exact values; MXFP4
-// carries an extra 2^-14).  Formats whose values fit binary16 exactly decode to
-// _Float16 so the fma consumes them through v_fma_mix without a conversion.
+// Decoded weights of one chunk, element e of the chunk in wv[e] (exact values).
+// Formats whose values fit binary16 exactly decode to _Float16 so the fma consumes
+// them through v_fma_mix without a conversion.
 template <Fmt F> struct WVal { using T = _Float16; };
 template <> struct WVal<Fmt::kFp8> { using T = float; };
 template <> struct WVal<Fmt::kBF16W> { using T = float; };
@@ -114,19 +114,17 @@ __device__ __forceinline__ void decode_chunk(const Raw<FmtInfo<F>::kBytes>& r, t
       wv[8 * i + 4] = a[1]; wv[8 * i + 5] = b[1]; wv[8 * i + 6] = c[1]; wv[8 * i + 7] = d[1];
     }
   } else if constexpr (F == Fmt::kMxfp4) {
-    // e2m1 nibble (s e1 e0 m) -> fp16 bits s<<15 | (e1 e0 m)<<9, which is the e2m1
-    // value times 2^-14 exactly (e=0 lands in the fp16 subnormal range).  The 2^14
-    // factor is restored together with the block scale.
+    // e2m1 pairs: byte b of word i holds k = 8i + 2b (low nibble) and 8i + 2b + 1
+    // (high nibble); v_cvt_scalef32_pk_f16_fp4 with scale 1 turns one byte into the
+    // two exact binary16 values (low nibble in the low half).
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      const uint32_t w = r.w[i];
-      const uint32_t w8 = w >> 8;
-      h2 a = as_h2(((w & 0x00070007u) << 9) | ((w & 0x00080008u) << 12));    // k 8i+0, 8i+4
-      h2 b = as_h2(((w & 0x00700070u) << 5) | ((w & 0x00800080u) << 8));     // k 8i+1, 8i+5
-      h2 c = as_h2(((w8 & 0x00070007u) << 9) | ((w8 & 0x00080008u) << 12));  // k 8i+2, 8i+6
-      h2 d = as_h2(((w8 & 0x00700070u) << 5) | ((w8 & 0x00800080u) << 8));   // k 8i+3, 8i+7
-      wv[8 * i + 0] = a[0]; wv[8 * i + 1] = b[0]; wv[8 * i + 2] = c[0]; wv[8 * i + 3] = d[0];
-      wv[8 * i + 4] = a[1]; wv[8 * i + 5] = b[1]; wv[8 * i + 6] = c[1]; wv[8 * i + 7] = d[1];
+      const h2 p0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(r.w[i], 1.0f, 0);
+      const h2 p1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(r.w[i], 1.0f, 1);
+      const h2 p2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(r.w[i], 1.0f, 2);
+      const h2 p3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(r.w[i], 1.0f, 3);
+      wv[8 * i + 0] = p0[0]; wv[8 * i + 1] = p0[1]; wv[8 * i + 2] = p1[0]; wv[8 * i + 3] = p1[1];
+      wv[8 * i + 4] = p2[0]; wv[8 * i + 5] = p2[1]; wv[8 * i + 6] = p3[0]; wv[8 * i + 7] = p3[1];
     }
   } else if constexpr (F == Fmt::kFp8) {
     // 32 bytes, byte e = element e; e4m3fn -> f32 is exact.
@@ -220,7 +218,7 @@ __device__ __forceinline__ float chunk_dot(const Raw<FmtInfo<F>::kBytes>& r, con
 }
 
 // Row values of NR rows in the E8M0 block-scale order (one 32-element block per
-// chunk): t_j = (p_j * 2^extra) * 2^(e_j - 127), A = ((+0 + t_round0) + ...),
+// chunk): t_j = p_j * 2^(e_j - 127), A = ((+0 + t_round0) + ...),
 // value = xor-butterfly over the LPR lanes.  `xs` is the activation vector in LDS.
 // Weights and exponents of round r+1 are loaded while round r is computed.
 template <Fmt F, int NR>
@@ -250,7 +248,7 @@ __device__ __forceinline__ void e8_fetch(E8Round<F, NR>& d, int r, int l, int nc
 
 template <Fmt F, typename XT, int LPR, int NR>
 __device__ __forceinline__ void e8_rows_dot(E8Round<F, NR>& cur, const uint8_t* const* wrow, const uint8_t* const* srow,
-                                            const bool* rv, const uint32_t* xs, int nchunks, int l, int e8_extra,
+                                            const bool* rv, const uint32_t* xs, int nchunks, int l,
                                             float* out) {
   const int rounds = (nchunks + LPR - 1) / LPR;
   float acc[NR];
@@ -274,9 +272,7 @@ __device__ __forceinline__ void e8_rows_dot(E8Round<F, NR>& cur, const uint8_t* 
     chunk_dot_rows<F, XT, NR>(cur.w, xw, pr);
 #pragma unroll
     for (int i = 0; i < NR; i++) {
-      float q = pr[i];
-      if (e8_extra) q = q * pow2i(e8_extra);
-      const float t = q * pow2i(cur.e[i] - 127);
+      const float t = pr[i] * pow2i(cur.e[i] - 127);
       acc[i] = acc[i] + ((cv && rv[i]) ? t : 0.0f);
     }
     if (r + 1 < rounds) cur = nxt;
