@@ -291,10 +291,17 @@ def main() -> int:
     _lib.load()  # fails loudly when the HIP library is missing
 
     if args.roofline_only:
+        # the roofline kernel alone, plus a plain 256 MiB device copy whose byte count
+        # calibrates hardware traffic counters (FETCH_SIZE / WRITE_SIZE) of the same run
         from thintensor_amd.backend import HipDecodeBackend
         be = HipDecodeBackend(torch.device("cuda:0"), torch.float16, 2048, 2048, 512, 8192)
         r = int4_gemv_phase(be, 8192, 2048, 128, 64, args.seed)
-        print(json.dumps({"int4_gemv": r}), flush=True)
+        src = torch.empty(128 * 1024 * 1024, device="cuda:0", dtype=torch.float16)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"int4_gemv": r, "copy_calibration_bytes": src.numel() * 2}), flush=True)
         return 0
 
     _log("dense decode (llama-3.2-1b-shaped)")

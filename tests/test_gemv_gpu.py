@@ -47,6 +47,9 @@ INT4_CASES = [
     (384, 2048, 2048, np.float16, "f16", "f16"),   # one scale per row
     (300, 1024, 64, np.float16, "bf16", "bf16"),   # bf16 activations
     (257, 4096, 2048, np.float32, "f16", "f16"),   # group spanning many lanes
+    (1, 32, 32, np.float16, "f16", "f16"),         # one row, one chunk
+    (5, 2880, 32, np.float16, "f16", "f16"),       # 90 chunks: ragged last round of 32 lanes
+    (7, 160, 32, np.float32, "f16", "f32"),        # 5 chunks on 16 lanes
 ]
 
 
