@@ -43,6 +43,7 @@ def _parse() -> argparse.Namespace:
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-moe", action="store_true", help="skip the gpt-oss-20B-shaped decode")
     p.add_argument("--no-extra", action="store_true", help="skip the extra GEMV shapes")
+    p.add_argument("--unfused", action="store_true", help="decode with one launch per reference operator")
     p.add_argument("--roofline-only", action="store_true",
                    help="only the int4 roofline phase (used for hardware-counter runs)")
     return p.parse_args()
@@ -188,7 +189,7 @@ def dense_decode_phase(args) -> tuple[dict, object]:
     cap = s.prior_tokens + max(args.steps, args.warmup)
     w = make_dense(s, device=dev, seed=args.seed, capacity=cap)
     be = HipDecodeBackend(dev, torch.float16, s.hidden, s.q_dim, s.kv_dim, s.intermediate)
-    dec = DenseDecoder(be, w)
+    dec = DenseDecoder(be, w, fused=not args.unfused)
     if args.steps > dec.history.numel():
         dec.history = torch.zeros(args.steps, device=dev, dtype=torch.int64)
     r = _time_decode(dec, 1, s.prior_tokens, args.warmup, args.steps)
@@ -214,7 +215,7 @@ def moe_decode_phase(args) -> dict:
     warm = min(args.warmup, 4)
     w = make_moe(s, device=dev, seed=args.seed, capacity=s.prior_tokens + max(steps, warm))
     be = HipDecodeBackend(dev, torch.float16, s.hidden, s.q_dim, s.kv_dim, s.intermediate)
-    dec = MoEDecoder(be, w)
+    dec = MoEDecoder(be, w, fused=not args.unfused)
     r = _time_decode(dec, 1, s.prior_tokens, warm, steps)
     tok_s = steps / r["event_s"]
     out = {"workload": "gpt-oss-20b-shaped bs=1 greedy decode, MXFP4 experts top-4 of 32, 1024 prior tokens",

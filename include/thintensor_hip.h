@@ -269,6 +269,99 @@ int tt_moe_router_matvec_topk(const void* weight, int w_dtype, int64_t w_row, co
 int tt_moe_router_topk(const void* logits, int logits_dtype, int64_t experts, int64_t top_k, int renormalize,
                        int32_t* indices_out, void* scores_out, int score_dtype, void* stream);
 
+/* ---------------------------------------------------------------- fused decode-step GEMVs
+ *
+ * One launch of the GEMV engine with the neighbouring decode-step operators folded
+ * in.  These have no single counterpart in the reference: they fuse, per launch,
+ * operators the reference issues back to back in _forward_token_triton
+ * (gpu_runtime.py:11429-11726) and _forward_token_moe (:8968-9908), with each
+ * operator's own rounding points, so the outputs equal the unfused sequence bit for
+ * bit:
+ *   prologue  TT_PRO_ADD_NORM:   add_rms_norm (triton_kernels.py:5646-5667) producing
+ *                                the GEMV input (residual_out written once);
+ *             TT_PRO_EMBED_NORM: embedding row copy + rms_norm (gpu_runtime.py:11396-11427,
+ *                                triton_kernels.py:5632-5644);
+ *             TT_PRO_ADD_RMS_NORM: add (:5862-5873) then rms_norm, the final norm of the MoE
+ *                                step (gpu_runtime.py:9338-9349);
+ *   segments  TT_SEG_ROPE_OUT / TT_SEG_ROPE_CACHE: rope_qk_inplace (:5689-5714) on the q / k
+ *                                rows, k then stored to the cache at the device position
+ *                                like the KV append (gpu_runtime.py:4132-4229);
+ *             TT_SEG_CACHE:      v rows stored to the cache at the position;
+ *             TT_SEG_SILU:       silu_mul (:5751-5762) of the gate and up rows;
+ *             TT_SEG_PLAIN:      the GEMV output (+ bias, as multi_matvec_bias).
+ * Weight formats: TT_FMT_INT4_G (symmetric int4, fp16 scales, group 128) and
+ * TT_FMT_DENSE (fp16 / bf16 rows).  Activations and outputs use act_dtype. */
+#define TT_FMT_INT4_G 0
+#define TT_FMT_DENSE 1
+#define TT_PRO_LOAD 0
+#define TT_PRO_ADD_NORM 1
+#define TT_PRO_EMBED_NORM 2
+#define TT_PRO_ADD_RMS_NORM 3
+#define TT_SEG_PLAIN 0
+#define TT_SEG_ROPE_OUT 1
+#define TT_SEG_ROPE_CACHE 2
+#define TT_SEG_CACHE 3
+#define TT_SEG_SILU 4
+
+typedef struct tt_fused_segment {
+  const void* weight;      /* int4: uint8 [rows, cols/2]; dense: [rows, cols] */
+  const void* weight2;     /* TT_SEG_SILU: the up-projection rows, same layout */
+  int64_t w_row_bytes;
+  const void* scales;      /* int4: fp16 [rows, cols/group] */
+  const void* scales2;     /* TT_SEG_SILU: scales of weight2 */
+  int64_t s_row;           /* scale elements between rows */
+  void* out;               /* output vector, or this layer's cache [kv_heads, capacity, head_dim] */
+  const void* bias;        /* TT_FMT_DENSE only; nullable */
+  int64_t rows;            /* output rows (TT_SEG_SILU: activation rows) */
+  int32_t kind;            /* TT_SEG_* */
+  int32_t reserved;
+} tt_fused_segment;
+
+typedef struct tt_fused_gemv {
+  int32_t weight_format;   /* TT_FMT_* */
+  int32_t weight_dtype;    /* TT_FMT_DENSE: TT_F16 / TT_BF16 */
+  int64_t group_size;      /* TT_FMT_INT4_G */
+  int32_t act_dtype;       /* TT_F16 / TT_BF16 */
+  int32_t prologue;        /* TT_PRO_* */
+  int64_t cols;
+  const void* x;           /* TT_PRO_LOAD */
+  const void* left;        /* TT_PRO_ADD_NORM: residual = bf16(left + right); TT_PRO_ADD_RMS_NORM: round(left + right) */
+  const void* right;
+  const void* embed;       /* TT_PRO_EMBED_NORM: residual = embed[token[0]] (token clamped to [0, vocab)) */
+  int64_t embed_row;
+  int64_t vocab;
+  const int64_t* token;
+  const void* norm_weight; /* RMSNorm weight [cols], act_dtype */
+  float eps;
+  int32_t count;           /* segments, 1 to 3 */
+  void* residual_out;      /* nullable */
+  tt_fused_segment seg[3];
+  const int32_t* position; /* device position for RoPE / cache segments */
+  int64_t capacity;        /* cache tokens */
+  int64_t cache_head;      /* elements between KV heads of one layer's cache */
+  const void* cos_table;   /* [table_rows, table_row], act_dtype */
+  const void* sin_table;
+  int64_t table_row;
+  int64_t table_rows;
+  int64_t head_dim;
+} tt_fused_gemv;
+
+int tt_fused_gemv_run(const tt_fused_gemv* desc, void* stream);
+
+/* sizeof(tt_fused_segment) and sizeof(tt_fused_gemv), so bindings can check their layout. */
+int tt_fused_struct_sizes(int64_t* segment_size, int64_t* desc_size);
+
+/* Fused greedy lm_head: the prologue of `desc` builds the input, seg[0] (TT_FMT_DENSE,
+ * TT_SEG_PLAIN, out = logits or null) is the lm_head, the token is chosen as by
+ * tt_matvec_argmax, and then, when position is non-null, the step's bookkeeping
+ * runs in the same finishing kernel: history[position - base] = token (skipped
+ * outside [0, history_len)) and position += 1 -- the sequence record_token +
+ * advance_position of a decode step.  `partials` needs
+ * tt_matvec_argmax_partials(rows, cols) entries. */
+int tt_fused_lm_head_argmax(const tt_fused_gemv* desc, uint64_t* partials, int64_t partials_capacity,
+                            int64_t* out_idx, float* out_val, int32_t* position, const int32_t* base,
+                            int64_t* history, int32_t history_len, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

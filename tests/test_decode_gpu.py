@@ -28,12 +28,13 @@ def _final_logits(dec) -> np.ndarray:
     return dec.be.logits_buffer(int(dec.w.lm_head.shape[0]), torch.float16).cpu().numpy()
 
 
+@pytest.mark.parametrize("fused", [False, True])
 @pytest.mark.parametrize("graph", [True, False])
-def test_small_dense_64_tokens(device, graph):
+def test_small_dense_64_tokens(device, graph, fused):
     s = SMALL_DENSE
     w = make_dense(s, device=device, seed=1)
     ref = DenseRef(w)
-    dec = DenseDecoder(_backend(device, s), w)
+    dec = DenseDecoder(_backend(device, s), w, fused=fused)
     start, pos = 7, s.prior_tokens
     got = dec.generate(start, pos, s.max_new_tokens, use_graph=graph)
     want = ref.generate(start, pos, s.max_new_tokens)
@@ -43,21 +44,25 @@ def test_small_dense_64_tokens(device, graph):
     assert np.array_equal(_final_logits(dec).view(np.uint16), logits.view(np.uint16))
 
 
-def test_small_moe_32_tokens(device):
+@pytest.mark.parametrize("fused", [False, True])
+def test_small_moe_32_tokens(device, fused):
     s = SMALL_MOE
     w = make_moe(s, device=device, seed=2)
     ref = MoERef(w)
-    dec = MoEDecoder(_backend(device, s), w)
+    dec = MoEDecoder(_backend(device, s), w, fused=fused)
     start, pos = 11, s.prior_tokens
     got = dec.generate(start, pos, s.max_new_tokens)
     want = ref.generate(start, pos, s.max_new_tokens)
     assert got == want
+    _, logits = ref.step(want[-2], pos + s.max_new_tokens - 1)
+    assert np.array_equal(_final_logits(dec).view(np.uint16), logits.view(np.uint16))
 
 
-def test_llama_1b_shaped_tokens(device):
+@pytest.mark.parametrize("fused", [False, True])
+def test_llama_1b_shaped_tokens(device, fused):
     s = LLAMA_1B
     w = make_dense(s, device=device, seed=0)
-    dec = DenseDecoder(_backend(device, s), w)
+    dec = DenseDecoder(_backend(device, s), w, fused=fused)
     ref = DenseRef(w)
     start, pos, n = 1, s.prior_tokens, 6
     got = dec.generate(start, pos, n)
@@ -65,10 +70,11 @@ def test_llama_1b_shaped_tokens(device):
     assert got == want
 
 
-def test_gpt_oss_20b_shaped_tokens(device):
+@pytest.mark.parametrize("fused", [False, True])
+def test_gpt_oss_20b_shaped_tokens(device, fused):
     s = GPT_OSS_20B
     w = make_moe(s, device=device, seed=0)
-    dec = MoEDecoder(_backend(device, s), w)
+    dec = MoEDecoder(_backend(device, s), w, fused=fused)
     ref = MoERef(w)
     start, pos, n = 1, s.prior_tokens, 3
     got = dec.generate(start, pos, n)

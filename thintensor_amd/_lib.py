@@ -23,6 +23,33 @@ _F = ctypes.c_float
 _PP = ctypes.POINTER(ctypes.c_void_p)
 _LP = ctypes.POINTER(ctypes.c_int64)
 
+# Fused decode-step descriptors (mirror tt_fused_segment / tt_fused_gemv in
+# include/thintensor_hip.h; tt_fused_struct_sizes checks the layout at load time).
+FMT_INT4_G, FMT_DENSE = 0, 1
+PRO_LOAD, PRO_ADD_NORM, PRO_EMBED_NORM, PRO_ADD_RMS_NORM = 0, 1, 2, 3
+SEG_PLAIN, SEG_ROPE_OUT, SEG_ROPE_CACHE, SEG_CACHE, SEG_SILU = 0, 1, 2, 3, 4
+
+
+class FusedSegment(ctypes.Structure):
+    _fields_ = [
+        ("weight", _P), ("weight2", _P), ("w_row_bytes", _L), ("scales", _P), ("scales2", _P), ("s_row", _L),
+        ("out", _P), ("bias", _P), ("rows", _L), ("kind", ctypes.c_int32), ("reserved", ctypes.c_int32),
+    ]
+
+
+class FusedGemv(ctypes.Structure):
+    _fields_ = [
+        ("weight_format", ctypes.c_int32), ("weight_dtype", ctypes.c_int32), ("group_size", _L),
+        ("act_dtype", ctypes.c_int32), ("prologue", ctypes.c_int32), ("cols", _L), ("x", _P), ("left", _P),
+        ("right", _P), ("embed", _P), ("embed_row", _L), ("vocab", _L), ("token", _P), ("norm_weight", _P),
+        ("eps", ctypes.c_float), ("count", ctypes.c_int32), ("residual_out", _P), ("seg", FusedSegment * 3),
+        ("position", _P), ("capacity", _L), ("cache_head", _L), ("cos_table", _P), ("sin_table", _P),
+        ("table_row", _L), ("table_rows", _L), ("head_dim", _L),
+    ]
+
+
+_FGP = ctypes.POINTER(FusedGemv)
+
 # name -> argtypes (restype is int unless listed in _RESTYPES)
 SIGNATURES: dict[str, list] = {
     "tt_version": [],
@@ -60,6 +87,9 @@ SIGNATURES: dict[str, list] = {
                                       _P],
     "tt_moe_router_matvec_topk": [_P, _I, _L, _P, _I, _L, _P, _I, _L, _L, _I, _P, _P, _I, _P],
     "tt_moe_router_topk": [_P, _I, _L, _L, _I, _P, _P, _I, _P],
+    "tt_fused_struct_sizes": [_LP, _LP],
+    "tt_fused_gemv_run": [_FGP, _P],
+    "tt_fused_lm_head_argmax": [_FGP, _P, _L, _P, _P, _P, _P, _P, ctypes.c_int32, _P],
 }
 _RESTYPES = {"tt_last_error": ctypes.c_char_p, "tt_matvec_argmax_partials": ctypes.c_int64}
 
@@ -99,6 +129,11 @@ def load(build_if_missing: bool = True) -> ctypes.CDLL:
             fn.restype = _RESTYPES.get(name, ctypes.c_int)
         if missing:
             raise KernelLibraryError(f"{path} lacks entry points {missing}; rebuild with thintensor_amd.build")
+        seg, desc = ctypes.c_int64(), ctypes.c_int64()
+        lib.tt_fused_struct_sizes(ctypes.byref(seg), ctypes.byref(desc))
+        if (seg.value, desc.value) != (ctypes.sizeof(FusedSegment), ctypes.sizeof(FusedGemv)):
+            raise KernelLibraryError(f"fused descriptor layout mismatch: library {seg.value}/{desc.value} bytes, "
+                                     f"binding {ctypes.sizeof(FusedSegment)}/{ctypes.sizeof(FusedGemv)}")
         _lib = lib
         return lib
 

@@ -15,6 +15,7 @@ depends only on the tensor shapes.
 
 from __future__ import annotations
 
+import ctypes
 from dataclasses import dataclass
 from typing import Any
 
@@ -741,6 +742,30 @@ class HipDecodeBackend:
                                          scores_out.data_ptr(), _code(scores_out, "scores"), _stream(logits))
         _lib.check(rc, "moe_router_topk")
         return indices_out, scores_out
+
+    # ------------------------------------------------------------ fused decode-step GEMVs (no reference counterpart)
+    def fused_gemv(self, desc: "_lib.FusedGemv") -> None:
+        """One GEMV launch with its decode-step neighbours folded in (RMSNorm prologue,
+        RoPE / KV-cache / SiLU epilogues); see tt_fused_gemv_run.  The outputs equal the
+        unfused operator sequence bit for bit."""
+        rc = self.lib.tt_fused_gemv_run(ctypes.byref(desc), torch.cuda.current_stream(self.device).cuda_stream)
+        _lib.check(rc, "fused_gemv")
+
+    def fused_lm_head_argmax(self, desc: "_lib.FusedGemv", *, position: torch.Tensor | None = None,
+                             base: torch.Tensor | None = None, history: torch.Tensor | None = None) -> torch.Tensor:
+        """Greedy lm_head with a fused prologue; with ``position`` the finishing kernel
+        also logs the token at history[position - base] and advances the position.
+        Returns the reused 0-d int64 token tensor."""
+        rows = int(desc.seg[0].rows)
+        partials = self._argmax_scratch(rows, int(desc.cols))
+        rc = self.lib.tt_fused_lm_head_argmax(
+            ctypes.byref(desc), partials.data_ptr(), partials.numel(), self._argmax_out_idx.data_ptr(),
+            self._argmax_out_val.data_ptr(), position.data_ptr() if position is not None else None,
+            base.data_ptr() if base is not None else None, history.data_ptr() if history is not None else None,
+            int(history.numel()) if history is not None else 0, torch.cuda.current_stream(self.device).cuda_stream,
+        )
+        _lib.check(rc, "fused_lm_head_argmax")
+        return self._argmax_out_idx
 
     # ------------------------------------------------------------ decode-step helpers (no reference counterpart)
     def embedding(self, embed: torch.Tensor, token: torch.Tensor | int, out: torch.Tensor) -> torch.Tensor:

@@ -19,15 +19,55 @@ namespace tt {
 
 enum class SMode : int { kNone = 0, kRow = 1, kGroup = 2, kGroupAff = 3, kBlockE8 = 4 };
 
+// Epilogue of a segment in the fused decode kernels (EPI instantiations only).
+enum SegKind : int {
+  kSegPlain = 0,      // store row values to out (+ bias)
+  kSegRopeOut = 1,    // rows of heads, RoPE applied, stored to out
+  kSegRopeCache = 2,  // rows of KV heads, RoPE applied, stored to the K cache at the position
+  kSegCache = 3,      // rows of KV heads stored to the V cache at the position
+  kSegSilu = 4,       // gate rows from w/s, up rows from w2/s2; out[i] = silu(gate_i) * up_i
+};
+
 struct Seg {
   const uint8_t* w;     // weight bytes of expert 0 / the matrix
   int64_t w_row;        // bytes between rows
   const void* s;        // scales
   int64_t s_row, s_grp; // scale element strides
   void* out;            // output (slot 0)
-  int rows;
+  int rows;             // virtual rows (kSegSilu: 2 x activation rows)
   int vbegin;           // first virtual row (batches never straddle segments)
   const void* bias;     // optional per-row bias in the output dtype: out = r(r(dot) + b)
+  int kind;             // SegKind
+  const uint8_t* w2;    // kSegSilu: up-projection weights and scales
+  const void* s2;
+};
+
+// Context of the fused prologue (activation vector built in the kernel) and the
+// position-dependent epilogues.
+struct FuseParams {
+  const void* left;           // add+RMSNorm prologue: residual = bf16(left + right)
+  const void* right;
+  const void* embed;          // embedding prologue: residual = embed[token]
+  int64_t embed_row, vocab;
+  const int64_t* token;
+  const void* norm_w;         // RMSNorm weight (activation dtype)
+  float eps;
+  void* residual_out;         // written by workgroup (0, 0)
+  const int32_t* pos;         // decode position (device)
+  int64_t capacity;           // KV cache tokens
+  int64_t cache_head;         // elements between KV heads of one layer's cache
+  const void* cos;            // RoPE tables [rows, table_row]
+  const void* sin;
+  int64_t table_row, table_rows;
+  int head_dim;
+};
+
+// How the activation vector reaches LDS.
+enum class Pro : int {
+  kLoad = 0,       // copy x
+  kAddNorm = 1,    // x = RMSNorm(bf16(left + right)) * w, residual stored
+  kEmbedNorm = 2,  // x = RMSNorm(embed[token]) * w, residual (the embedding row) stored
+  kAddRmsNorm = 3, // x = RMSNorm(round(left + right)) * w: add then rms_norm, residual stored
 };
 
 struct GemvParams {
@@ -44,6 +84,7 @@ struct GemvParams {
   int aff_zero;            // affine pair holds (s, z) instead of (s, m)
   int cols;
   uint64_t* am_partials;   // argmax epilogue: one key per wave (null: plain GEMV)
+  FuseParams f;
 };
 
 // Order-preserving argmax key of a rounded logit at row `idx`: larger value wins,
@@ -92,17 +133,33 @@ __device__ __forceinline__ int rs_row(int l, int levels, int k) {
 template <Fmt F, SMode SM, typename ST, int ROWS, int NVG>
 struct GemvBatch {
   bool active;
-  int lr0, rows;
-  const uint8_t* wb;
-  const ST* sb;
+  int lr0, rows, kind;
+  const uint8_t* wb;         // weight base of the segment (expert applied)
+  const ST* sb;              // scale base of the segment (expert applied)
   int64_t s_row, s_grp;
   void* out;
   const void* bias;
-  int64_t woffs[ROWS];
-  int rcl[ROWS];
+  int64_t woffs[ROWS];       // byte offset of each batch row's weights from wb
+  int rcl[ROWS];             // physical row of each batch row (clamped)
   bool rv[ROWS];
-  int64_t soffs[NVG];
+  int64_t soffs[NVG];        // element offset of each kept value's scale row from sb
 };
+
+// Physical row of virtual row v of a paired segment (RoPE pairs or gate/up pairs):
+// virtual rows 2m*SUBS + sub and (2m + 1)*SUBS + sub of a block of 2*SUBS rows form
+// pair m*SUBS + sub, so both halves of a pair land in the same lane group and the
+// epilogue exchanges them with one cross-lane move.  RoPE: pair p of head h is
+// (h*D + j, h*D + j + D/2) with j = p mod D/2; SiLU: pair p is (gate p, up p).
+template <int SUBS>
+__device__ __forceinline__ int paired_row(int v, int kind, int head_dim, bool& odd) {
+  const int blk = v / (2 * SUBS), rem = v - blk * (2 * SUBS);
+  odd = rem >= SUBS;
+  const int pidx = blk * SUBS + (odd ? rem - SUBS : rem);
+  if (kind == kSegSilu) return pidx;
+  const int half = head_dim >> 1;
+  const int h = pidx / half, j = pidx - h * half;
+  return h * head_dim + j + (odd ? half : 0);
+}
 
 template <Fmt F, typename ST, int ROWS, int NVG>
 struct GemvData {
@@ -111,7 +168,8 @@ struct GemvData {
   int e[ROWS];
 };
 
-template <Fmt F, SMode SM, typename XT, typename OT, typename ST, int LPR, int ROWS, int L, bool AM>
+template <Fmt F, SMode SM, typename XT, typename OT, typename ST, int LPR, int ROWS, int L, bool AM,
+          Pro PRO = Pro::kLoad, bool EPI = false>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
   extern __shared__ uint32_t xs_lds[];
   constexpr int B = FmtInfo<F>::kBytes;
@@ -156,22 +214,46 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
     const Seg& S = si == 0 ? P.seg[0] : (si == 1 ? P.seg[1] : P.seg[2]);
     bt.lr0 = v0 - S.vbegin;
     bt.rows = S.rows;
-    bt.wb = S.w + woff + (int64_t)bt.lr0 * S.w_row;
-    bt.sb = reinterpret_cast<const ST*>(S.s) + soff + (int64_t)bt.lr0 * S.s_row;
+    bt.kind = EPI ? S.kind : kSegPlain;
+    bt.wb = S.w + woff;
+    bt.sb = reinterpret_cast<const ST*>(S.s) + soff;
     bt.s_row = S.s_row;
     bt.s_grp = S.s_grp;
     bt.out = S.out;
     bt.bias = S.bias;
+    if (!EPI || bt.kind == kSegPlain || bt.kind == kSegCache) {
 #pragma unroll
-    for (int i = 0; i < ROWS; i++) {
-      const int r = i * SUBS + sub;
-      bt.rv[i] = bt.lr0 + r < bt.rows;
-      bt.rcl[i] = bt.rv[i] ? r : (bt.rows - 1 - bt.lr0);
-      bt.woffs[i] = (int64_t)bt.rcl[i] * S.w_row;
+      for (int i = 0; i < ROWS; i++) {
+        const int r = i * SUBS + sub;
+        bt.rv[i] = bt.lr0 + r < bt.rows;
+        bt.rcl[i] = bt.rv[i] ? bt.lr0 + r : bt.rows - 1;
+        bt.woffs[i] = (int64_t)bt.rcl[i] * S.w_row;
+      }
+#pragma unroll
+      for (int k = 0; k < NVG; k++)
+        bt.soffs[k] = (int64_t)(bt.lr0 + grow[k] < bt.rows ? bt.lr0 + grow[k] : bt.rows - 1) * S.s_row;
+    } else if constexpr (EPI) {
+      // paired segments: the up rows of a SiLU pair live in a second matrix, reached
+      // by the byte / element distance between the two allocations
+      const int64_t w2d = bt.kind == kSegSilu ? (int64_t)(S.w2 - S.w) : 0;
+      const int64_t s2d = bt.kind == kSegSilu ? (int64_t)(reinterpret_cast<const ST*>(S.s2) - reinterpret_cast<const ST*>(S.s)) : 0;
+#pragma unroll
+      for (int i = 0; i < ROWS; i++) {
+        const int r = i * SUBS + sub;
+        bt.rv[i] = bt.lr0 + r < bt.rows;
+        bool odd;
+        const int ph = paired_row<SUBS>(bt.rv[i] ? bt.lr0 + r : bt.rows - 1, bt.kind, P.f.head_dim, odd);
+        bt.rcl[i] = ph;
+        bt.woffs[i] = (int64_t)ph * S.w_row + (odd ? w2d : 0);
+      }
+#pragma unroll
+      for (int k = 0; k < NVG; k++) {
+        bool odd;
+        const int ph = paired_row<SUBS>(bt.lr0 + grow[k] < bt.rows ? bt.lr0 + grow[k] : bt.rows - 1, bt.kind,
+                                        P.f.head_dim, odd);
+        bt.soffs[k] = (int64_t)ph * S.s_row + (odd ? s2d : 0);
+      }
     }
-#pragma unroll
-    for (int k = 0; k < NVG; k++)
-      bt.soffs[k] = (int64_t)(bt.lr0 + grow[k] < bt.rows ? grow[k] : bt.rows - 1 - bt.lr0) * S.s_row;
   };
 
   auto fetch = [&](const Batch& bt, int r, Data& d) {
@@ -198,11 +280,47 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
   setup(b, cb);
   Data cd;
   if (cb.active) fetch(cb, 0, cd);
-  {
+  if constexpr (PRO == Pro::kLoad) {
     // Stage the activation vector while the first weight loads are in flight.
     const uint4* xg = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(P.x) + (int64_t)slot * P.x_slot);
     uint4* xl = reinterpret_cast<uint4*>(xs_lds);
     for (int i = threadIdx.x; i < (P.cols >> 3); i += blockDim.x) xl[i] = xg[i];
+    __syncthreads();
+  } else {
+    // Build the activation vector: RMSNorm of the residual stream, with the same
+    // thread partition, reduction order and rounding points as the standalone
+    // rms_norm / add_rms_norm kernels (every workgroup computes the identical vector;
+    // workgroup (0, 0) also stores the residual).
+    __shared__ float red[4];
+    const int n = P.cols;
+    const XT* erow = nullptr;
+    if constexpr (PRO == Pro::kEmbedNorm) {
+      int64_t t = P.f.token[0];
+      t = t < 0 ? 0 : (t >= P.f.vocab ? P.f.vocab - 1 : t);
+      erow = reinterpret_cast<const XT*>(P.f.embed) + t * P.f.embed_row;
+    }
+    auto resid = [&](int i) -> float {
+      if constexpr (PRO == Pro::kAddNorm) return norm_residual<XT>(P.f.left, P.f.right, i);
+      else if constexpr (PRO == Pro::kAddRmsNorm) return round_to<XT>(ld<XT>(P.f.left, i) + ld<XT>(P.f.right, i));
+      else return to_f32(erow[i]);
+    };
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < n; i += 256) {
+      const float r = resid(i);
+      ss = __builtin_fmaf(r, r, ss);
+    }
+    const float total = block_sum256(ss, red);
+    const float inv = 1.0f / __builtin_sqrtf(total / (float)n + P.f.eps);
+    const bool writer = blockIdx.x == 0 && blockIdx.y == 0 && P.f.residual_out != nullptr;
+    XT* xl = reinterpret_cast<XT*>(xs_lds);
+    for (int i = threadIdx.x; i < n; i += 256) {
+      const float r = resid(i);
+      if (writer) store<XT>(reinterpret_cast<XT*>(P.f.residual_out) + i, r);
+      float y;
+      if constexpr (PRO == Pro::kAddNorm) y = (r * inv) * ld<XT>(P.f.norm_w, i);
+      else y = (r * inv) * (ld<XT>(P.f.norm_w, i) + 0.0f);
+      store<XT>(xl + i, y);
+    }
     __syncthreads();
   }
 
@@ -274,9 +392,45 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
     else reduce_range<ROWS, 1, LPR>(acc);
     float v = acc[0];
     const bool ok = fstore && cb.lr0 + frow < cb.rows;
-    if constexpr (SM == SMode::kRow) v = v * to_f32(cb.sb[(int64_t)(ok ? frow : 0) * cb.s_row]);
-    if (cb.bias != nullptr && ok) v = round_to<OT>(v) + to_f32(reinterpret_cast<const OT*>(cb.bias)[cb.lr0 + frow]);
-    if (ok && cb.out != nullptr) store<OT>(reinterpret_cast<OT*>(cb.out) + (int64_t)slot * P.out_slot + cb.lr0 + frow, v);
+    if constexpr (SM == SMode::kRow) v = v * to_f32(cb.sb[(int64_t)(ok ? cb.lr0 + frow : 0) * cb.s_row]);
+    if (!EPI || cb.kind == kSegPlain) {
+      if (cb.bias != nullptr && ok) v = round_to<OT>(v) + to_f32(reinterpret_cast<const OT*>(cb.bias)[cb.lr0 + frow]);
+      if (ok && cb.out != nullptr) store<OT>(reinterpret_cast<OT*>(cb.out) + (int64_t)slot * P.out_slot + cb.lr0 + frow, v);
+    } else if constexpr (EPI) {
+      // fused epilogues: the row value rounded to OT as the unfused operator would
+      // store it, then RoPE / cache placement / SiLU on it
+      bool odd = false;
+      const int fr = cb.lr0 + frow;
+      const int ph = cb.kind == kSegCache ? fr : paired_row<SUBS>(fr, cb.kind, P.f.head_dim, odd);
+      if (cb.bias != nullptr && ok) v = round_to<OT>(v) + to_f32(reinterpret_cast<const OT*>(cb.bias)[ph]);
+      const float val = round_to<OT>(v);
+      const float pv = xor_partner<ROWS / 2 < 1 ? 1 : ROWS / 2>(val);   // the other half of the pair
+      const int64_t pos = P.f.pos != nullptr ? (int64_t)P.f.pos[0] : 0;
+      const int D = P.f.head_dim;
+      if (cb.kind == kSegSilu) {
+        if (ok && !odd) store<OT>(reinterpret_cast<OT*>(cb.out) + ph, silu_mul_val(val, pv));
+      } else {
+        float o = val;
+        if (cb.kind != kSegCache && pos >= 0 && pos < P.f.table_rows) {
+          const int half = D >> 1;
+          const int j = (ph % D) - (odd ? half : 0);
+          const float c = ld<OT>(P.f.cos, pos * P.f.table_row + j);
+          const float sn = ld<OT>(P.f.sin, pos * P.f.table_row + j);
+          float o1, o2;
+          if (odd) rope_pair<OT>(pv, val, c, sn, o1, o2);
+          else rope_pair<OT>(val, pv, c, sn, o1, o2);
+          o = odd ? o2 : o1;
+        }
+        if (ok) {
+          if (cb.kind == kSegRopeOut) {
+            store<OT>(reinterpret_cast<OT*>(cb.out) + ph, o);
+          } else if (pos >= 0 && pos < P.f.capacity) {
+            const int64_t h = ph / D, d = ph - h * D;
+            store<OT>(reinterpret_cast<OT*>(cb.out) + h * P.f.cache_head + pos * D + d, o);
+          }
+        }
+      }
+    }
     if constexpr (AM) {
       if (ok) {
         const uint64_t key = argmax_key(round_to<OT>(v), (uint32_t)(cb.lr0 + frow));
@@ -299,7 +453,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
 constexpr int kMaxGemvBlocks = 2048;
 constexpr int kMaxGemvWaves = 4 * kMaxGemvBlocks;
 
-template <Fmt F, SMode SM, typename XT, typename OT, typename ST, int LPR, int ROWS, int L>
+template <Fmt F, SMode SM, typename XT, typename OT, typename ST, int LPR, int ROWS, int L, Pro PRO = Pro::kLoad,
+          bool EPI = false>
 static int launch_one(GemvParams P, int slots, hipStream_t stream, const char* what) {
   constexpr int SUBS = 64 / LPR;
   constexpr int per_iter = ROWS * SUBS;
@@ -317,27 +472,27 @@ static int launch_one(GemvParams P, int slots, hipStream_t stream, const char* w
   if (P.am_partials != nullptr) {
     if constexpr (SM == SMode::kNone) {
       // unused partial slots must not win the final reduction
-      hipLaunchKernelGGL((gemv_kernel<F, SM, XT, OT, ST, LPR, ROWS, L, true>), dim3(blocks, slots), dim3(256), lds,
-                         stream, P);
+      hipLaunchKernelGGL((gemv_kernel<F, SM, XT, OT, ST, LPR, ROWS, L, true, PRO, EPI>), dim3(blocks, slots), dim3(256),
+                         lds, stream, P);
       return check_launch(what);
     }
     set_error("%s: argmax epilogue is only available for dense weights", what);
     return TT_ERR_UNSUPPORTED;
   }
-  hipLaunchKernelGGL((gemv_kernel<F, SM, XT, OT, ST, LPR, ROWS, L, false>), dim3(blocks, slots), dim3(256), lds, stream,
-                     P);
+  hipLaunchKernelGGL((gemv_kernel<F, SM, XT, OT, ST, LPR, ROWS, L, false, PRO, EPI>), dim3(blocks, slots), dim3(256), lds,
+                     stream, P);
   return check_launch(what);
 }
 
-template <Fmt F, SMode SM, typename XT, typename OT, typename ST, int ROWS, int L>
+template <Fmt F, SMode SM, typename XT, typename OT, typename ST, int ROWS, int L, Pro PRO = Pro::kLoad, bool EPI = false>
 static int launch_lpr(int lpr, const GemvParams& P, int slots, hipStream_t stream, const char* what) {
   switch (lpr) {
-    case 64: return launch_one<F, SM, XT, OT, ST, 64, ROWS, L>(P, slots, stream, what);
+    case 64: return launch_one<F, SM, XT, OT, ST, 64, ROWS, L, PRO, EPI>(P, slots, stream, what);
     case 32:
-      if constexpr (L <= 32) return launch_one<F, SM, XT, OT, ST, 32, ROWS, L>(P, slots, stream, what);
+      if constexpr (L <= 32) return launch_one<F, SM, XT, OT, ST, 32, ROWS, L, PRO, EPI>(P, slots, stream, what);
       break;
     case 16:
-      if constexpr (L <= 16) return launch_one<F, SM, XT, OT, ST, 16, ROWS, L>(P, slots, stream, what);
+      if constexpr (L <= 16) return launch_one<F, SM, XT, OT, ST, 16, ROWS, L, PRO, EPI>(P, slots, stream, what);
       break;
     default: break;
   }

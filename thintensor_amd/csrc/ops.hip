@@ -10,22 +10,6 @@
 
 namespace tt {
 
-template <typename T> __device__ __forceinline__ float ld(const void* p, int64_t i) {
-  return to_f32(reinterpret_cast<const T*>(p)[i]);
-}
-
-// Block-wide sum in a fixed order: thread partials are reduced with the wave
-// butterfly, then the four wave sums are combined as (w0 + w1) + (w2 + w3).
-__device__ __forceinline__ float block_sum256(float v, float* red) {
-  v = xor_sum(v, 1, 64);
-  const int wave = threadIdx.x >> 6;
-  if ((threadIdx.x & 63) == 0) red[wave] = v;
-  __syncthreads();
-  const float t = (red[0] + red[1]) + (red[2] + red[3]);
-  __syncthreads();
-  return t;
-}
-
 // ---------------------------------------------------------------- RMSNorm
 // out_i = (x_i * (1 / sqrt(mean(x^2) + eps))) * (w_i + offset); sum of squares per
 // thread is an fma chain over elements t, t+256, ... (triton_kernels.py:2562-2577).
@@ -52,13 +36,13 @@ __global__ __launch_bounds__(256) void add_rms_norm_kernel(const void* left, con
   __shared__ float red[4];
   float s = 0.0f;
   for (int i = threadIdx.x; i < n; i += 256) {
-    const float r = round_bf16(ld<XT>(left, i) + ld<XT>(right, i));
+    const float r = norm_residual<XT>(left, right, i);
     s = __builtin_fmaf(r, r, s);
   }
   const float total = block_sum256(s, red);
   const float inv = 1.0f / __builtin_sqrtf(total / (float)n + eps);
   for (int i = threadIdx.x; i < n; i += 256) {
-    const float r = round_bf16(ld<XT>(left, i) + ld<XT>(right, i));
+    const float r = norm_residual<XT>(left, right, i);
     store<XT>(reinterpret_cast<XT*>(residual_out) + i, r);
     store<OT>(reinterpret_cast<OT*>(out) + i, (r * inv) * ld<WT>(w, i));
   }
@@ -76,9 +60,7 @@ template <typename T>
 __global__ void silu_mul_kernel(const void* g, const void* u, void* out, int n) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) {
-    const float gv = ld<T>(g, i);
-    const float s = gv / (1.0f + exp_f32(-gv));
-    store<T>(reinterpret_cast<T*>(out) + i, s * ld<T>(u, i));
+    store<T>(reinterpret_cast<T*>(out) + i, silu_mul_val(ld<T>(g, i), ld<T>(u, i)));
   }
 }
 
@@ -129,12 +111,10 @@ __global__ void rope_kernel(void* q, void* k, const void* cos_t, const void* sin
   T* base = h < heads ? reinterpret_cast<T*>(q) + (int64_t)h * head_dim : reinterpret_cast<T*>(k) + (int64_t)(h - heads) * head_dim;
   const float c = ld<T>(cos_t, p * table_row + i);
   const float s = ld<T>(sin_t, p * table_row + i);
-  const float a = to_f32(base[i]);
-  const float b = to_f32(base[i + half]);
-  const float ac = round_to<T>(a * c), bs = round_to<T>(b * s);
-  const float bc = round_to<T>(b * c), as = round_to<T>(a * s);
-  store<T>(base + i, ac - bs);
-  store<T>(base + i + half, bc + as);
+  float o1, o2;
+  rope_pair<T>(to_f32(base[i]), to_f32(base[i + half]), c, s, o1, o2);
+  store<T>(base + i, o1);
+  store<T>(base + i + half, o2);
 }
 
 // ---------------------------------------------------------------- embedding / KV

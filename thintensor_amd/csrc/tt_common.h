@@ -165,4 +165,41 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t k) {
   return k;
 }
 
+template <typename T> __device__ __forceinline__ float ld(const void* p, int64_t i) {
+  return to_f32(reinterpret_cast<const T*>(p)[i]);
+}
+
+// Block-wide sum of a 256-thread workgroup in a fixed order: thread partials are
+// reduced with the wave butterfly, then the four wave sums as (w0 + w1) + (w2 + w3).
+__device__ __forceinline__ float block_sum256(float v, float* red) {
+  v = xor_sum(v, 1, 64);
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) red[wave] = v;
+  __syncthreads();
+  const float t = (red[0] + red[1]) + (red[2] + red[3]);
+  __syncthreads();
+  return t;
+}
+
+// Residual element of add+RMSNorm: the reference rounds left + right through
+// bfloat16 whatever the activation dtype (triton_kernels.py:2603-2606).
+template <typename XT>
+__device__ __forceinline__ float norm_residual(const void* left, const void* right, int64_t i) {
+  return round_bf16(ld<XT>(left, i) + ld<XT>(right, i));
+}
+
+// RoPE on one (first-half, second-half) pair with rounding to T after every product
+// and sum, as the reference's torch path (gpu_runtime.py:8696-8705):
+// o1 = r(r(a c) - r(b s)), o2 = r(r(b c) + r(a s)); the caller's store rounds o1, o2.
+template <typename T>
+__device__ __forceinline__ void rope_pair(float a, float b, float c, float s, float& o1, float& o2) {
+  const float ac = round_to<T>(a * c), bs = round_to<T>(b * s);
+  const float bc = round_to<T>(b * c), as = round_to<T>(a * s);
+  o1 = ac - bs;
+  o2 = bc + as;
+}
+
+// silu(g) * u = (g / (1 + exp(-g))) * u in binary32 (triton_kernels.py:2761-2774).
+__device__ __forceinline__ float silu_mul_val(float g, float u) { return (g / (1.0f + exp_f32(-g))) * u; }
+
 }  // namespace tt

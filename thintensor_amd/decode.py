@@ -29,15 +29,56 @@ from __future__ import annotations
 
 import torch
 
+from . import _lib
 from .backend import HipDecodeBackend
 from .synth import DenseWeights, MoEWeights
+
+_ACT = {torch.float16: _lib.F16, torch.bfloat16: _lib.BF16}
+
+
+def _int4_segment(seg: _lib.FusedSegment, weight, out: torch.Tensor, rows: int, kind: int, weight2=None) -> None:
+    packed, scales = weight
+    seg.weight = packed.data_ptr()
+    seg.w_row_bytes = packed.stride(0) * packed.element_size()
+    seg.scales = scales.data_ptr()
+    seg.s_row = scales.stride(0)
+    if weight2 is not None:
+        seg.weight2 = weight2[0].data_ptr()
+        seg.scales2 = weight2[1].data_ptr()
+    seg.out = out.data_ptr()
+    seg.rows = rows
+    seg.kind = kind
+
+
+def _dense_segment(seg: _lib.FusedSegment, weight: torch.Tensor, bias: torch.Tensor | None, out: torch.Tensor | None,
+                   kind: int) -> None:
+    seg.weight = weight.data_ptr()
+    seg.w_row_bytes = weight.stride(0) * weight.element_size()
+    seg.bias = bias.data_ptr() if bias is not None else None
+    seg.out = out.data_ptr() if out is not None else None
+    seg.rows = int(weight.shape[0])
+    seg.kind = kind
+
+
+def _kv_context(d: _lib.FusedGemv, dec: "_GraphedDecoder", cos: torch.Tensor, sin: torch.Tensor, head_dim: int,
+                cache: torch.Tensor) -> None:
+    d.position = dec.position.data_ptr()
+    d.capacity = dec.capacity
+    d.cache_head = cache.stride(0)
+    d.cos_table = cos.data_ptr()
+    d.sin_table = sin.data_ptr()
+    d.table_row = cos.stride(0)
+    d.table_rows = int(cos.shape[0])
+    d.head_dim = head_dim
 
 
 class _GraphedDecoder:
     """Common state: device token / position, token history, graph capture."""
 
-    def __init__(self, backend: HipDecodeBackend, device: torch.device, capacity: int, max_new: int) -> None:
+    def __init__(self, backend: HipDecodeBackend, device: torch.device, capacity: int, max_new: int,
+                 fused: bool = False) -> None:
         self.be = backend
+        self.fused = fused
         self.device = device
         self.capacity = capacity
         self.token = backend._argmax_out_idx               # int64 0-d, written by the lm_head argmax
@@ -60,9 +101,16 @@ class _GraphedDecoder:
         raise NotImplementedError
 
     def _step_and_record(self) -> None:
+        if self.fused:
+            # the fused step logs the token and advances the position in its last kernel
+            self.fused_step()
+            return
         self.step()
         self.be.record_token(self.token, self.position, self.base, self.history)
         self.be.advance_position(self.position)
+
+    def fused_step(self) -> None:  # pragma: no cover - implemented by subclasses
+        raise NotImplementedError
 
     def _reserve_scratch(self) -> None:  # pragma: no cover - implemented by subclasses
         raise NotImplementedError
@@ -97,11 +145,19 @@ class _GraphedDecoder:
 
 
 class DenseDecoder(_GraphedDecoder):
-    """Llama-3.2-1B-shaped int4 g128 decoder."""
+    """Llama-3.2-1B-shaped int4 g128 decoder.
 
-    def __init__(self, backend: HipDecodeBackend, weights: DenseWeights) -> None:
+    ``fused=True`` runs the step as five launches per layer (QKV GEMV with the
+    residual add + RMSNorm prologue and the RoPE / KV-append epilogue, attention
+    partials and combine, o_proj, gate/up GEMV with the add + RMSNorm prologue and the
+    SiLU epilogue, down_proj) and a final lm_head launch whose prologue is the last
+    add + RMSNorm and whose finishing kernel also logs the token and advances the
+    position.  Every rounding point is the unfused operator's, so both modes give
+    the same bits."""
+
+    def __init__(self, backend: HipDecodeBackend, weights: DenseWeights, fused: bool = False) -> None:
         s = weights.shape
-        super().__init__(backend, weights.embed.device, int(weights.k_cache.shape[2]), s.max_new_tokens)
+        super().__init__(backend, weights.embed.device, int(weights.k_cache.shape[2]), s.max_new_tokens, fused)
         self.w = weights
         self.s = s
         dev, dt = weights.embed.device, torch.float16
@@ -150,13 +206,73 @@ class DenseDecoder(_GraphedDecoder):
                 be.add_rms_norm(self.hidden_b, self.mlp, self.hidden_a, w.final_norm, self.final, s.eps)
         be.matvec_argmax_tensor(w.lm_head, self.final)
 
+    def _build_fused(self) -> None:
+        w, s = self.w, self.s
+        act = _ACT[self.hidden_a.dtype]
+        q = self.qkv[: s.q_dim]
+        self._qkv_desc, self._gu_desc = [], []
+        for li, L in enumerate(w.layers):
+            d = _lib.FusedGemv()
+            d.weight_format, d.group_size, d.act_dtype, d.cols = _lib.FMT_INT4_G, s.group, act, s.hidden
+            if li == 0:
+                d.prologue = _lib.PRO_EMBED_NORM
+                d.embed, d.embed_row, d.vocab = w.embed.data_ptr(), w.embed.stride(0), int(w.embed.shape[0])
+                d.token = self.token.data_ptr()
+            else:
+                d.prologue = _lib.PRO_ADD_NORM
+                d.left, d.right = self.hidden_b.data_ptr(), self.mlp.data_ptr()
+            d.norm_weight, d.eps, d.residual_out = L.ln1.data_ptr(), s.eps, self.hidden_a.data_ptr()
+            d.count = 3
+            _int4_segment(d.seg[0], L.q, q, s.q_dim, _lib.SEG_ROPE_OUT)
+            _int4_segment(d.seg[1], L.k, w.k_cache[li], s.kv_dim, _lib.SEG_ROPE_CACHE)
+            _int4_segment(d.seg[2], L.v, w.v_cache[li], s.kv_dim, _lib.SEG_CACHE)
+            _kv_context(d, self, w.cos, w.sin, s.head_dim, w.k_cache[li])
+            self._qkv_desc.append(d)
+            g = _lib.FusedGemv()
+            g.weight_format, g.group_size, g.act_dtype, g.cols = _lib.FMT_INT4_G, s.group, act, s.hidden
+            g.prologue = _lib.PRO_ADD_NORM
+            g.left, g.right = self.hidden_a.data_ptr(), self.attn_out.data_ptr()
+            g.norm_weight, g.eps, g.residual_out = L.ln2.data_ptr(), s.eps, self.hidden_b.data_ptr()
+            g.count = 1
+            _int4_segment(g.seg[0], L.gate, self.act, s.intermediate, _lib.SEG_SILU, weight2=L.up)
+            self._gu_desc.append(g)
+        h = _lib.FusedGemv()
+        h.weight_format, h.weight_dtype, h.act_dtype, h.cols = _lib.FMT_DENSE, _ACT[w.lm_head.dtype], act, s.hidden
+        h.prologue = _lib.PRO_ADD_NORM
+        h.left, h.right = self.hidden_b.data_ptr(), self.mlp.data_ptr()
+        h.norm_weight, h.eps = w.final_norm.data_ptr(), s.eps
+        h.count = 1
+        _dense_segment(h.seg[0], w.lm_head, None, self.be.logits_buffer(int(w.lm_head.shape[0]), self.hidden_a.dtype),
+                       _lib.SEG_PLAIN)
+        self._head_desc = h
+
+    def fused_step(self) -> None:
+        be, w, s = self.be, self.w, self.s
+        if not hasattr(self, "_head_desc"):
+            self._build_fused()
+        q = self.qkv[: s.q_dim]
+        for li, L in enumerate(w.layers):
+            be.fused_gemv(self._qkv_desc[li])
+            be.single_token_gqa_attention(q, w.k_cache[li], w.v_cache[li], self.attn, s.heads, s.kv_heads, s.head_dim,
+                                          active_tokens=(self.position, 1))
+            be.int4_scaled_matvec(L.o[0], L.o[1], self.attn, self.attn_out, rows=s.hidden, cols=s.q_dim,
+                                  group_size=s.group)
+            be.fused_gemv(self._gu_desc[li])
+            be.int4_scaled_matvec(L.down[0], L.down[1], self.act, self.mlp, rows=s.hidden, cols=s.intermediate,
+                                  group_size=s.group)
+        be.fused_lm_head_argmax(self._head_desc, position=self.position, base=self.base, history=self.history)
+
 
 class MoEDecoder(_GraphedDecoder):
-    """gpt-oss-20B-shaped decoder with MXFP4 experts, fp16 attention with sinks."""
+    """gpt-oss-20B-shaped decoder with MXFP4 experts, fp16 attention with sinks.
 
-    def __init__(self, backend: HipDecodeBackend, weights: MoEWeights) -> None:
+    ``fused=True`` folds the embedding / residual add + RMSNorm into the QKV launch,
+    RoPE and the KV append into its epilogue, and the final add + RMSNorm, token log
+    and position advance into the lm_head launches, with the unfused rounding points."""
+
+    def __init__(self, backend: HipDecodeBackend, weights: MoEWeights, fused: bool = False) -> None:
         s = weights.shape
-        super().__init__(backend, weights.embed.device, int(weights.k_cache.shape[2]), s.max_new_tokens)
+        super().__init__(backend, weights.embed.device, int(weights.k_cache.shape[2]), s.max_new_tokens, fused)
         self.w = weights
         self.s = s
         dev, dt = weights.embed.device, torch.float16
@@ -203,3 +319,54 @@ class MoEDecoder(_GraphedDecoder):
                 be.add(self.hidden_b, self.moe, self.hidden_a)
                 be.rms_norm(self.hidden_a, w.final_norm, self.final, s.eps)
         be.matvec_argmax_tensor(w.lm_head, self.final)
+
+    def _build_fused(self) -> None:
+        w, s = self.w, self.s
+        act = _ACT[self.hidden_a.dtype]
+        q = self.qkv[: s.q_dim]
+        self._qkv_desc = []
+        for li, L in enumerate(w.layers):
+            d = _lib.FusedGemv()
+            d.weight_format, d.weight_dtype, d.act_dtype, d.cols = _lib.FMT_DENSE, _ACT[L.q.dtype], act, s.hidden
+            if li == 0:
+                d.prologue = _lib.PRO_EMBED_NORM
+                d.embed, d.embed_row, d.vocab = w.embed.data_ptr(), w.embed.stride(0), int(w.embed.shape[0])
+                d.token = self.token.data_ptr()
+            else:
+                d.prologue = _lib.PRO_ADD_NORM
+                d.left, d.right = self.hidden_b.data_ptr(), self.moe.data_ptr()
+            d.norm_weight, d.eps, d.residual_out = L.ln1.data_ptr(), s.eps, self.hidden_a.data_ptr()
+            d.count = 3
+            _dense_segment(d.seg[0], L.q, L.q_bias, q, _lib.SEG_ROPE_OUT)
+            _dense_segment(d.seg[1], L.k, L.k_bias, w.k_cache[li], _lib.SEG_ROPE_CACHE)
+            _dense_segment(d.seg[2], L.v, L.v_bias, w.v_cache[li], _lib.SEG_CACHE)
+            _kv_context(d, self, w.cos, w.sin, s.head_dim, w.k_cache[li])
+            self._qkv_desc.append(d)
+        h = _lib.FusedGemv()
+        h.weight_format, h.weight_dtype, h.act_dtype, h.cols = _lib.FMT_DENSE, _ACT[w.lm_head.dtype], act, s.hidden
+        h.prologue = _lib.PRO_ADD_RMS_NORM
+        h.left, h.right = self.hidden_b.data_ptr(), self.moe.data_ptr()
+        h.norm_weight, h.eps = w.final_norm.data_ptr(), s.eps
+        h.count = 1
+        _dense_segment(h.seg[0], w.lm_head, None, self.be.logits_buffer(int(w.lm_head.shape[0]), self.hidden_a.dtype),
+                       _lib.SEG_PLAIN)
+        self._head_desc = h
+
+    def fused_step(self) -> None:
+        be, w, s = self.be, self.w, self.s
+        if not hasattr(self, "_head_desc"):
+            self._build_fused()
+        q = self.qkv[: s.q_dim]
+        for li, L in enumerate(w.layers):
+            be.fused_gemv(self._qkv_desc[li])
+            be.single_token_gqa_attention(q, w.k_cache[li], w.v_cache[li], self.attn, s.heads, s.kv_heads,
+                                          s.head_dim, sinks=L.sinks, active_tokens=(self.position, 1))
+            be.multi_matvec_bias((L.o,), (L.o_bias,), self.attn, self.attn_out)
+            be.add_rms_norm(self.hidden_a, self.attn_out, self.hidden_b, L.ln2, self.normed, s.eps)
+            be.moe_router_matvec_topk(L.router, self.normed, self.router_idx, self.router_scores, bias=L.router_bias,
+                                      renormalize=True)
+            be.mxfp_lowbit_selected_swiglu(L.gate_up_blocks, L.gate_up_scales, self.normed, self.router_idx, self.act,
+                                           bits=4, alpha=s.swiglu_alpha, limit=s.swiglu_limit, bias=L.gate_up_bias)
+            be.mxfp_lowbit_weighted_down(L.down_blocks, L.down_scales, self.act, self.router_idx, self.router_scores,
+                                         self.moe, bits=4, bias=L.down_bias)
+        be.fused_lm_head_argmax(self._head_desc, position=self.position, base=self.base, history=self.history)
