@@ -102,7 +102,7 @@ class KernelLibraryError(RuntimeError):
 
 
 def library_path() -> Path:
-    override = os.environ.get("THINTENSOR_HIP_LIB")
+    override = os.environ.get("THINTENSOR_HIP_LIB") or None
     return Path(override) if override else _build.LIB_PATH
 
 

@@ -160,8 +160,13 @@ GemvParams params(const tt_fused_gemv* d) {
 
 template <typename AT, Pro PRO>
 int launch(const tt_fused_gemv* d, GemvParams& P, int lpr, bool argmax, hipStream_t st) {
-  if (d->weight_format == TT_FMT_INT4_G)
-    return launch_lpr<Fmt::kInt4Sym, SMode::kGroup, AT, AT, f16_t, 4, 4, PRO, true>(lpr, P, 1, st, kWhat);
+  if (d->weight_format == TT_FMT_INT4_G) {
+    int64_t rows = 0;
+    for (int i = 0; i < d->count; i++) rows += d->seg[i].kind == TT_SEG_SILU ? 2 * d->seg[i].rows : d->seg[i].rows;
+    int rpw, pf;
+    int4_shape(rows, (int)((d->cols / 32 + lpr - 1) / lpr), true, &rpw, &pf);
+    return launch_int4_g128<AT, AT, PRO, true>(lpr, rpw, pf, P, st, kWhat);
+  }
   if (argmax) {
     if (d->weight_dtype == TT_F16)
       return launch_lpr<Fmt::kF16W, SMode::kNone, AT, AT, float, 2, 1, PRO, false>(lpr, P, 1, st, kWhat);

@@ -169,7 +169,7 @@ struct GemvData {
 };
 
 template <Fmt F, SMode SM, typename XT, typename OT, typename ST, int LPR, int ROWS, int L, bool AM,
-          Pro PRO = Pro::kLoad, bool EPI = false>
+          Pro PRO = Pro::kLoad, bool EPI = false, int PF = 1>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
   extern __shared__ uint32_t xs_lds[];
   constexpr int B = FmtInfo<F>::kBytes;
@@ -278,8 +278,14 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
   int b = blockIdx.x * (blockDim.x >> 6) + wave;
   Batch cb;
   setup(b, cb);
-  Data cd;
-  if (cb.active) fetch(cb, 0, cd);
+  // PF == 1: one round in flight ahead of the one being computed.  PF > 1 (rounds <=
+  // PF): every round of the next batch is fetched while the current batch computes.
+  Data cd[PF];
+  if (cb.active) {
+#pragma unroll
+    for (int r = 0; r < PF; r++)
+      if (r < rounds) fetch(cb, r, cd[r]);
+  }
   if constexpr (PRO == Pro::kLoad) {
     // Stage the activation vector while the first weight loads are in flight.
     const uint4* xg = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(P.x) + (int64_t)slot * P.x_slot);
@@ -304,114 +310,130 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
       else if constexpr (PRO == Pro::kAddRmsNorm) return round_to<XT>(ld<XT>(P.f.left, i) + ld<XT>(P.f.right, i));
       else return to_f32(erow[i]);
     };
-    float ss = 0.0f;
-    for (int i = threadIdx.x; i < n; i += 256) {
-      const float r = resid(i);
-      ss = __builtin_fmaf(r, r, ss);
-    }
-    const float total = block_sum256(ss, red);
-    const float inv = 1.0f / __builtin_sqrtf(total / (float)n + P.f.eps);
     const bool writer = blockIdx.x == 0 && blockIdx.y == 0 && P.f.residual_out != nullptr;
     XT* xl = reinterpret_cast<XT*>(xs_lds);
-    for (int i = threadIdx.x; i < n; i += 256) {
-      const float r = resid(i);
-      if (writer) store<XT>(reinterpret_cast<XT*>(P.f.residual_out) + i, r);
-      float y;
-      if constexpr (PRO == Pro::kAddNorm) y = (r * inv) * ld<XT>(P.f.norm_w, i);
-      else y = (r * inv) * (ld<XT>(P.f.norm_w, i) + 0.0f);
-      store<XT>(xl + i, y);
+    auto normed = [&](float r, float inv, float w) -> float {
+      if constexpr (PRO == Pro::kAddNorm) return (r * inv) * w;
+      else return (r * inv) * (w + 0.0f);
+    };
+    constexpr int kHeld = 16;   // elements per thread kept in registers (cols <= 4096)
+    if (n <= 256 * kHeld) {
+      // one pass over memory: residual and weight loads issued together
+      float rr[kHeld], wn[kHeld];
+#pragma unroll
+      for (int k = 0; k < kHeld; k++) {
+        const int i = threadIdx.x + 256 * k;
+        rr[k] = i < n ? resid(i) : 0.0f;
+        wn[k] = i < n ? ld<XT>(P.f.norm_w, i) : 0.0f;
+      }
+      float ss = 0.0f;
+#pragma unroll
+      for (int k = 0; k < kHeld; k++)
+        if (threadIdx.x + 256 * k < n) ss = __builtin_fmaf(rr[k], rr[k], ss);
+      const float total = block_sum256(ss, red);
+      const float inv = 1.0f / __builtin_sqrtf(total / (float)n + P.f.eps);
+#pragma unroll
+      for (int k = 0; k < kHeld; k++) {
+        const int i = threadIdx.x + 256 * k;
+        if (i < n) {
+          if (writer) store<XT>(reinterpret_cast<XT*>(P.f.residual_out) + i, rr[k]);
+          store<XT>(xl + i, normed(rr[k], inv, wn[k]));
+        }
+      }
+    } else {
+      float ss = 0.0f;
+      for (int i = threadIdx.x; i < n; i += 256) {
+        const float r = resid(i);
+        ss = __builtin_fmaf(r, r, ss);
+      }
+      const float total = block_sum256(ss, red);
+      const float inv = 1.0f / __builtin_sqrtf(total / (float)n + P.f.eps);
+      for (int i = threadIdx.x; i < n; i += 256) {
+        const float r = resid(i);
+        if (writer) store<XT>(reinterpret_cast<XT*>(P.f.residual_out) + i, r);
+        store<XT>(xl + i, normed(r, inv, ld<XT>(P.f.norm_w, i)));
+      }
     }
     __syncthreads();
   }
 
-  while (cb.active) {
-    Batch nb;
-    nb.active = false;
-    float acc[ROWS];
+  // One round: chunk partials of the batch rows, scaled and accumulated in round order.
+  auto consume = [&](const Batch& bt, const Data& d, int r, float* acc) {
+    const int j = r * LPR + l;
+    const bool cv = j < nchunks;
+    uint32_t xw[16];
+    {
+      const uint4* xp = reinterpret_cast<const uint4*>(xs_lds + (cv ? j : 0) * 16);
 #pragma unroll
-    for (int i = 0; i < ROWS; i++) acc[i] = 0.0f;
-
-    for (int r = 0; r < rounds; r++) {
-      Data nd;
-      if (r + 1 < rounds) {
-        fetch(cb, r + 1, nd);
-      } else {
-        setup(b + nwaves, nb);
-        if (nb.active) fetch(nb, 0, nd);
+      for (int q = 0; q < 4; q++) {
+        uint4 v = xp[q];
+        xw[4 * q] = v.x; xw[4 * q + 1] = v.y; xw[4 * q + 2] = v.z; xw[4 * q + 3] = v.w;
       }
-      const int j = r * LPR + l;
-      const bool cv = j < nchunks;
-      uint32_t xw[16];
-      {
-        const uint4* xp = reinterpret_cast<const uint4*>(xs_lds + (cv ? j : 0) * 16);
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-          uint4 v = xp[q];
-          xw[4 * q] = v.x; xw[4 * q + 1] = v.y; xw[4 * q + 2] = v.z; xw[4 * q + 3] = v.w;
-        }
-      }
-      float p[ROWS];
-      chunk_dot_rows<F, XT, ROWS>(cd.w, xw, p);
-#pragma unroll
-      for (int i = 0; i < ROWS; i++) p[i] = (cv && cb.rv[i]) ? p[i] : 0.0f;
-      if constexpr (SM == SMode::kNone || SM == SMode::kRow) {
-#pragma unroll
-        for (int i = 0; i < ROWS; i++) acc[i] = acc[i] + p[i];
-      } else if constexpr (SM == SMode::kBlockE8) {
-#pragma unroll
-        for (int i = 0; i < ROWS; i++) {
-          const float t = p[i] * pow2i(cd.e[i] - 127);
-          acc[i] = acc[i] + ((cv && cb.rv[i]) ? t : 0.0f);
-        }
-      } else {
-        float xsum = 0.0f;
-        if constexpr (SM == SMode::kGroupAff) {
-#pragma unroll
-          for (int e = 0; e < 32; e++) xsum = xsum + xv<XT>(xw, e);
-          xsum = cv ? xsum : 0.0f;
-          reduce_range<1, 1, LG>(&xsum);
-        }
-        reduce_range<ROWS, 1, LG>(p);
-#pragma unroll
-        for (int k = 0; k < NVG; k++) {
-          float t;
-          if constexpr (SM == SMode::kGroupAff) {
-            float m = cd.m[k];
-            if (P.aff_zero) m = -(m * cd.s[k]);
-            t = __builtin_fmaf(xsum, m, p[k] * cd.s[k]);
-          } else {
-            t = p[k] * cd.s[k];
-          }
-          const bool ok = cv && (cb.lr0 + grow[k] < cb.rows);
-          acc[k] = acc[k] + (ok ? t : 0.0f);
-        }
-      }
-      cd = nd;
     }
+    float p[ROWS];
+    chunk_dot_rows<F, XT, ROWS>(d.w, xw, p);
+#pragma unroll
+    for (int i = 0; i < ROWS; i++) p[i] = (cv && bt.rv[i]) ? p[i] : 0.0f;
+    if constexpr (SM == SMode::kNone || SM == SMode::kRow) {
+#pragma unroll
+      for (int i = 0; i < ROWS; i++) acc[i] = acc[i] + p[i];
+    } else if constexpr (SM == SMode::kBlockE8) {
+#pragma unroll
+      for (int i = 0; i < ROWS; i++) {
+        const float t = p[i] * pow2i(d.e[i] - 127);
+        acc[i] = acc[i] + ((cv && bt.rv[i]) ? t : 0.0f);
+      }
+    } else {
+      float xsum = 0.0f;
+      if constexpr (SM == SMode::kGroupAff) {
+#pragma unroll
+        for (int e = 0; e < 32; e++) xsum = xsum + xv<XT>(xw, e);
+        xsum = cv ? xsum : 0.0f;
+        reduce_range<1, 1, LG>(&xsum);
+      }
+      reduce_range<ROWS, 1, LG>(p);
+#pragma unroll
+      for (int k = 0; k < NVG; k++) {
+        float t;
+        if constexpr (SM == SMode::kGroupAff) {
+          float m = d.m[k];
+          if (P.aff_zero) m = -(m * d.s[k]);
+          t = __builtin_fmaf(xsum, m, p[k] * d.s[k]);
+        } else {
+          t = p[k] * d.s[k];
+        }
+        const bool ok = cv && (bt.lr0 + grow[k] < bt.rows);
+        acc[k] = acc[k] + (ok ? t : 0.0f);
+      }
+    }
+  };
+
+  // Row values of a finished batch: final lane reduction, then the epilogue.
+  auto finish = [&](const Batch& bt, float* acc) {
     if constexpr (kGroup) reduce_range<NVG, LG, LPR>(acc);
     else reduce_range<ROWS, 1, LPR>(acc);
     float v = acc[0];
-    const bool ok = fstore && cb.lr0 + frow < cb.rows;
-    if constexpr (SM == SMode::kRow) v = v * to_f32(cb.sb[(int64_t)(ok ? cb.lr0 + frow : 0) * cb.s_row]);
-    if (!EPI || cb.kind == kSegPlain) {
-      if (cb.bias != nullptr && ok) v = round_to<OT>(v) + to_f32(reinterpret_cast<const OT*>(cb.bias)[cb.lr0 + frow]);
-      if (ok && cb.out != nullptr) store<OT>(reinterpret_cast<OT*>(cb.out) + (int64_t)slot * P.out_slot + cb.lr0 + frow, v);
+    const bool ok = fstore && bt.lr0 + frow < bt.rows;
+    if constexpr (SM == SMode::kRow) v = v * to_f32(bt.sb[(int64_t)(ok ? bt.lr0 + frow : 0) * bt.s_row]);
+    if (!EPI || bt.kind == kSegPlain) {
+      if (bt.bias != nullptr && ok) v = round_to<OT>(v) + to_f32(reinterpret_cast<const OT*>(bt.bias)[bt.lr0 + frow]);
+      if (ok && bt.out != nullptr) store<OT>(reinterpret_cast<OT*>(bt.out) + (int64_t)slot * P.out_slot + bt.lr0 + frow, v);
     } else if constexpr (EPI) {
       // fused epilogues: the row value rounded to OT as the unfused operator would
       // store it, then RoPE / cache placement / SiLU on it
       bool odd = false;
-      const int fr = cb.lr0 + frow;
-      const int ph = cb.kind == kSegCache ? fr : paired_row<SUBS>(fr, cb.kind, P.f.head_dim, odd);
-      if (cb.bias != nullptr && ok) v = round_to<OT>(v) + to_f32(reinterpret_cast<const OT*>(cb.bias)[ph]);
+      const int fr = bt.lr0 + frow;
+      const int ph = bt.kind == kSegCache ? fr : paired_row<SUBS>(fr, bt.kind, P.f.head_dim, odd);
+      if (bt.bias != nullptr && ok) v = round_to<OT>(v) + to_f32(reinterpret_cast<const OT*>(bt.bias)[ph]);
       const float val = round_to<OT>(v);
       const float pv = xor_partner<ROWS / 2 < 1 ? 1 : ROWS / 2>(val);   // the other half of the pair
       const int64_t pos = P.f.pos != nullptr ? (int64_t)P.f.pos[0] : 0;
       const int D = P.f.head_dim;
-      if (cb.kind == kSegSilu) {
-        if (ok && !odd) store<OT>(reinterpret_cast<OT*>(cb.out) + ph, silu_mul_val(val, pv));
+      if (bt.kind == kSegSilu) {
+        if (ok && !odd) store<OT>(reinterpret_cast<OT*>(bt.out) + ph, silu_mul_val(val, pv));
       } else {
         float o = val;
-        if (cb.kind != kSegCache && pos >= 0 && pos < P.f.table_rows) {
+        if (bt.kind != kSegCache && pos >= 0 && pos < P.f.table_rows) {
           const int half = D >> 1;
           const int j = (ph % D) - (odd ? half : 0);
           const float c = ld<OT>(P.f.cos, pos * P.f.table_row + j);
@@ -422,23 +444,67 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
           o = odd ? o2 : o1;
         }
         if (ok) {
-          if (cb.kind == kSegRopeOut) {
-            store<OT>(reinterpret_cast<OT*>(cb.out) + ph, o);
+          if (bt.kind == kSegRopeOut) {
+            store<OT>(reinterpret_cast<OT*>(bt.out) + ph, o);
           } else if (pos >= 0 && pos < P.f.capacity) {
             const int64_t h = ph / D, d = ph - h * D;
-            store<OT>(reinterpret_cast<OT*>(cb.out) + h * P.f.cache_head + pos * D + d, o);
+            store<OT>(reinterpret_cast<OT*>(bt.out) + h * P.f.cache_head + pos * D + d, o);
           }
         }
       }
     }
     if constexpr (AM) {
       if (ok) {
-        const uint64_t key = argmax_key(round_to<OT>(v), (uint32_t)(cb.lr0 + frow));
+        const uint64_t key = argmax_key(round_to<OT>(v), (uint32_t)(bt.lr0 + frow));
         best = key > best ? key : best;
       }
     }
-    cb = nb;
-    b += nwaves;
+  };
+
+  if constexpr (PF == 1) {
+    while (cb.active) {
+      Batch nb;
+      nb.active = false;
+      float acc[ROWS];
+#pragma unroll
+      for (int i = 0; i < ROWS; i++) acc[i] = 0.0f;
+      for (int r = 0; r < rounds; r++) {
+        Data nd;
+        if (r + 1 < rounds) {
+          fetch(cb, r + 1, nd);
+        } else {
+          setup(b + nwaves, nb);
+          if (nb.active) fetch(nb, 0, nd);
+        }
+        consume(cb, cd[0], r, acc);
+        cd[0] = nd;
+      }
+      finish(cb, acc);
+      cb = nb;
+      b += nwaves;
+    }
+  } else {
+    while (cb.active) {
+      Batch nb;
+      setup(b + nwaves, nb);
+      Data nd[PF];
+      if (nb.active) {
+#pragma unroll
+        for (int r = 0; r < PF; r++)
+          if (r < rounds) fetch(nb, r, nd[r]);
+      }
+      float acc[ROWS];
+#pragma unroll
+      for (int i = 0; i < ROWS; i++) acc[i] = 0.0f;
+#pragma unroll
+      for (int r = 0; r < PF; r++)
+        if (r < rounds) consume(cb, cd[r], r, acc);
+      finish(cb, acc);
+      cb = nb;
+#pragma unroll
+      for (int r = 0; r < PF; r++) cd[r] = nd[r];
+      b += nwaves;
+    }
   }
   if constexpr (AM) {
     best = wave_max_u64(best);
@@ -454,7 +520,7 @@ constexpr int kMaxGemvBlocks = 2048;
 constexpr int kMaxGemvWaves = 4 * kMaxGemvBlocks;
 
 template <Fmt F, SMode SM, typename XT, typename OT, typename ST, int LPR, int ROWS, int L, Pro PRO = Pro::kLoad,
-          bool EPI = false>
+          bool EPI = false, int PF = 1>
 static int launch_one(GemvParams P, int slots, hipStream_t stream, const char* what) {
   constexpr int SUBS = 64 / LPR;
   constexpr int per_iter = ROWS * SUBS;
@@ -469,30 +535,53 @@ static int launch_one(GemvParams P, int slots, hipStream_t stream, const char* w
   if (blocks < 1) blocks = 1;
   if (blocks > kMaxGemvBlocks) blocks = kMaxGemvBlocks;
   const size_t lds = (size_t)P.cols * 2;
+  if (P.am_partials == nullptr && slots == 1) {
+    // Persistent grid of at most the workgroups the chip holds at once: waves loop
+    // over row batches with the next batch in flight, instead of a second
+    // generation of workgroups starting behind the first.
+    static size_t cached_lds = ~(size_t)0;
+    static int cached_cap = 0;
+    if (cached_lds != lds) {
+      int per_cu = 0, dev = 0, cus = 0;
+      if (hipGetDevice(&dev) == hipSuccess &&
+          hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+          hipOccupancyMaxActiveBlocksPerMultiprocessor(
+              &per_cu, reinterpret_cast<const void*>(&gemv_kernel<F, SM, XT, OT, ST, LPR, ROWS, L, false, PRO, EPI, PF>),
+              256, lds) == hipSuccess &&
+          per_cu > 0 && cus > 0) {
+        cached_cap = per_cu * cus;
+      } else {
+        cached_cap = kMaxGemvBlocks;
+      }
+      cached_lds = lds;
+    }
+    if (blocks > cached_cap) blocks = cached_cap;
+  }
   if (P.am_partials != nullptr) {
     if constexpr (SM == SMode::kNone) {
       // unused partial slots must not win the final reduction
-      hipLaunchKernelGGL((gemv_kernel<F, SM, XT, OT, ST, LPR, ROWS, L, true, PRO, EPI>), dim3(blocks, slots), dim3(256),
-                         lds, stream, P);
+      hipLaunchKernelGGL((gemv_kernel<F, SM, XT, OT, ST, LPR, ROWS, L, true, PRO, EPI, PF>), dim3(blocks, slots),
+                         dim3(256), lds, stream, P);
       return check_launch(what);
     }
     set_error("%s: argmax epilogue is only available for dense weights", what);
     return TT_ERR_UNSUPPORTED;
   }
-  hipLaunchKernelGGL((gemv_kernel<F, SM, XT, OT, ST, LPR, ROWS, L, false, PRO, EPI>), dim3(blocks, slots), dim3(256), lds,
-                     stream, P);
+  hipLaunchKernelGGL((gemv_kernel<F, SM, XT, OT, ST, LPR, ROWS, L, false, PRO, EPI, PF>), dim3(blocks, slots), dim3(256),
+                     lds, stream, P);
   return check_launch(what);
 }
 
-template <Fmt F, SMode SM, typename XT, typename OT, typename ST, int ROWS, int L, Pro PRO = Pro::kLoad, bool EPI = false>
+template <Fmt F, SMode SM, typename XT, typename OT, typename ST, int ROWS, int L, Pro PRO = Pro::kLoad, bool EPI = false,
+          int PF = 1>
 static int launch_lpr(int lpr, const GemvParams& P, int slots, hipStream_t stream, const char* what) {
   switch (lpr) {
-    case 64: return launch_one<F, SM, XT, OT, ST, 64, ROWS, L, PRO, EPI>(P, slots, stream, what);
+    case 64: return launch_one<F, SM, XT, OT, ST, 64, ROWS, L, PRO, EPI, PF>(P, slots, stream, what);
     case 32:
-      if constexpr (L <= 32) return launch_one<F, SM, XT, OT, ST, 32, ROWS, L, PRO, EPI>(P, slots, stream, what);
+      if constexpr (L <= 32) return launch_one<F, SM, XT, OT, ST, 32, ROWS, L, PRO, EPI, PF>(P, slots, stream, what);
       break;
     case 16:
-      if constexpr (L <= 16) return launch_one<F, SM, XT, OT, ST, 16, ROWS, L, PRO, EPI>(P, slots, stream, what);
+      if constexpr (L <= 16) return launch_one<F, SM, XT, OT, ST, 16, ROWS, L, PRO, EPI, PF>(P, slots, stream, what);
       break;
     default: break;
   }
@@ -535,6 +624,38 @@ static int launch_types(int x_dtype, int out_dtype, int L, int lpr, const GemvPa
   set_error("%s: unsupported activation/output dtype pair (%d, %d); output must match the activation dtype or be fp32",
             what, x_dtype, out_dtype);
   return TT_ERR_UNSUPPORTED;
+}
+
+// Launch shape of the symmetric int4 group-128 GEMV (the decode hot path): rows per
+// wave and rounds prefetched per batch.  Fewer rows per wave when the matrix is short,
+// so that the grid still fills the chip; whole-batch prefetch when a row takes 2 to 4
+// rounds, so a wave waits for memory once per batch instead of once per round.
+// Paired (RoPE / SiLU) segments need at least two rows per wave.  The reduction order
+// does not depend on either choice.
+inline void int4_shape(int64_t rows, int rounds, bool paired, int* rows_per_wave, int* prefetch) {
+  int rpw = rows >= 16384 ? 4 : (rows >= 4096 || paired ? 2 : 1);
+  if (paired && rpw < 2) rpw = 2;
+  int pf = rounds >= 2 && rounds <= 4 && rpw <= 2 ? 4 : 1;
+  *rows_per_wave = rpw;
+  *prefetch = pf;
+}
+
+template <typename XT, typename OT, Pro PRO, bool EPI>
+static int launch_int4_g128(int lpr, int rows_per_wave, int prefetch, const GemvParams& P, hipStream_t st,
+                            const char* what) {
+  constexpr Fmt F = Fmt::kInt4Sym;
+  constexpr SMode SM = SMode::kGroup;
+  if (rows_per_wave == 4) return launch_lpr<F, SM, XT, OT, f16_t, 4, 4, PRO, EPI, 1>(lpr, P, 1, st, what);
+  if (rows_per_wave == 2) {
+    if (prefetch == 4) return launch_lpr<F, SM, XT, OT, f16_t, 2, 4, PRO, EPI, 4>(lpr, P, 1, st, what);
+    return launch_lpr<F, SM, XT, OT, f16_t, 2, 4, PRO, EPI, 1>(lpr, P, 1, st, what);
+  }
+  if constexpr (!EPI) {
+    if (prefetch == 4) return launch_lpr<F, SM, XT, OT, f16_t, 1, 4, PRO, EPI, 4>(lpr, P, 1, st, what);
+    return launch_lpr<F, SM, XT, OT, f16_t, 1, 4, PRO, EPI, 1>(lpr, P, 1, st, what);
+  }
+  set_error("%s: paired segments need two rows per wave", what);
+  return TT_ERR_INVALID;
 }
 
 // Validates the common GEMV contract and fills group information.

@@ -81,6 +81,13 @@ extern "C" int tt_multi_int4_scaled_matvec(int count, const void* const* packed,
     if (scale_dtype == TT_F16) return launch_types<Fmt::kInt4Sym, SMode::kRow, f16_t, 4>(x_dtype, out_dtype, Lg, lpr, P, 1, st, what);
     return launch_types<Fmt::kInt4Sym, SMode::kRow, float, 4>(x_dtype, out_dtype, Lg, lpr, P, 1, st, what);
   }
+  if (scale_dtype == TT_F16 && Lg == 4 && x_dtype == out_dtype) {
+    // the decode hot path (group 128, fp16 scales): launch shape chosen from the matrix
+    int rpw, pf;
+    int4_shape(acc_rows, (int)((cols / 32 + lpr - 1) / lpr), false, &rpw, &pf);
+    if (x_dtype == TT_F16) return launch_int4_g128<f16_t, f16_t, Pro::kLoad, false>(lpr, rpw, pf, P, st, what);
+    return launch_int4_g128<bf16_t, bf16_t, Pro::kLoad, false>(lpr, rpw, pf, P, st, what);
+  }
   if (scale_dtype == TT_F16) return launch_types<Fmt::kInt4Sym, SMode::kGroup, f16_t, 4>(x_dtype, out_dtype, Lg, lpr, P, 1, st, what);
   return launch_types<Fmt::kInt4Sym, SMode::kGroup, float, 4>(x_dtype, out_dtype, Lg, lpr, P, 1, st, what);
 }

@@ -192,21 +192,56 @@ __device__ __forceinline__ void decode_chunk(const Raw<FmtInfo<F>::kBytes>& r, t
   }
 }
 
+// Decoded values of word q (elements 8q .. 8q+7) of a 16-byte int4 / MXFP4 chunk.
+template <Fmt F>
+__device__ __forceinline__ void decode_word8(uint32_t w, _Float16* v) {
+  if constexpr (F == Fmt::kInt4Sym || F == Fmt::kInt4Aff) {
+    const float off = (F == Fmt::kInt4Sym) ? 8.0f : 0.0f;
+    h2 a, b, c, d;
+    nib_pairs(w, off, a, b, c, d);
+    v[0] = a[0]; v[1] = b[0]; v[2] = c[0]; v[3] = d[0];
+    v[4] = a[1]; v[5] = b[1]; v[6] = c[1]; v[7] = d[1];
+  } else {
+    const h2 p0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 0);
+    const h2 p1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 1);
+    const h2 p2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 2);
+    const h2 p3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 3);
+    v[0] = p0[0]; v[1] = p0[1]; v[2] = p1[0]; v[3] = p1[1];
+    v[4] = p2[0]; v[5] = p2[1]; v[6] = p3[0]; v[7] = p3[1];
+  }
+}
+
 // Chunk partials of NR rows: for each row an fma chain over the chunk's 32 elements
 // in ascending k, starting from +0.  The rows' chains are interleaved element by
-// element so no fma waits on the one issued just before it.
+// element so no fma waits on the one issued just before it.  The 4-bit formats are
+// decoded one 32-bit word (8 elements) at a time so only 8 values per row are live.
 template <Fmt F, typename XT, int NR>
 __device__ __forceinline__ void chunk_dot_rows(const Raw<FmtInfo<F>::kBytes>* r, const uint32_t* xw, float* p) {
-  typename WVal<F>::T wv[NR][32];
-#pragma unroll
-  for (int i = 0; i < NR; i++) decode_chunk<F>(r[i], wv[i]);
 #pragma unroll
   for (int i = 0; i < NR; i++) p[i] = 0.0f;
+  if constexpr (F == Fmt::kInt4Sym || F == Fmt::kInt4Aff || F == Fmt::kMxfp4) {
 #pragma unroll
-  for (int e = 0; e < 32; e++) {
-    const float xe = xv<XT>(xw, e);
+    for (int q = 0; q < 4; q++) {
+      _Float16 wv[NR][8];
 #pragma unroll
-    for (int i = 0; i < NR; i++) p[i] = __builtin_fmaf((float)wv[i][e], xe, p[i]);
+      for (int i = 0; i < NR; i++) decode_word8<F>(r[i].w[q], wv[i]);
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const float xe = xv<XT>(xw, 8 * q + e);
+#pragma unroll
+        for (int i = 0; i < NR; i++) p[i] = __builtin_fmaf((float)wv[i][e], xe, p[i]);
+      }
+    }
+  } else {
+    typename WVal<F>::T wv[NR][32];
+#pragma unroll
+    for (int i = 0; i < NR; i++) decode_chunk<F>(r[i], wv[i]);
+#pragma unroll
+    for (int e = 0; e < 32; e++) {
+      const float xe = xv<XT>(xw, e);
+#pragma unroll
+      for (int i = 0; i < NR; i++) p[i] = __builtin_fmaf((float)wv[i][e], xe, p[i]);
+    }
   }
 }
 
