@@ -105,13 +105,17 @@ def test_gqa_attention(backend, device, heads, kv_heads, tokens, sinks, cap):
     vals = f16_normal(g, (kv_heads, cap, D))
     sk = f16_normal(g, heads) if sinks else None
     out = torch.empty(heads * D, device=device, dtype=torch.float16)
-    tok = torch.tensor([tokens], dtype=torch.int32, device=device)
-    backend.single_token_gqa_attention(to_torch(q, device), to_torch(keys, device), to_torch(vals, device), out, heads,
-                                       kv_heads, D, sinks=to_torch(sk, device) if sinks else None, active_tokens=tok)
-    want = np.empty(heads * D, dtype=np.float16)
-    oracle.lib().tto_attention(P(q), P(keys), P(vals), oracle.F16, cap * D, D, cap * D, D, P(sk) if sinks else None,
-                               oracle.F16, tokens, heads, kv_heads, D, P(want))
-    assert_bits_equal(from_torch_bits(out), want, "attention")
+    qd, kd, vd = to_torch(q, device), to_torch(keys, device), to_torch(vals, device)
+    skd = to_torch(sk, device) if sinks else None
+    # two calls in a row (the single-launch path counts chunk arrivals in the scratch and
+    # must leave the counters ready for the next call), the second with fewer tokens
+    for n in (tokens, max(1, tokens // 2 - 3)):
+        tok = torch.tensor([n], dtype=torch.int32, device=device)
+        backend.single_token_gqa_attention(qd, kd, vd, out, heads, kv_heads, D, sinks=skd, active_tokens=tok)
+        want = np.empty(heads * D, dtype=np.float16)
+        oracle.lib().tto_attention(P(q), P(keys), P(vals), oracle.F16, cap * D, D, cap * D, D, P(sk) if sinks else None,
+                                   oracle.F16, n, heads, kv_heads, D, P(want))
+        assert_bits_equal(from_torch_bits(out), want, f"attention ({n} tokens)")
 
 
 @pytest.mark.parametrize("renorm,with_bias", [(True, True), (False, False)])

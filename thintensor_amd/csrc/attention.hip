@@ -44,11 +44,7 @@ struct AttnParams {
 // 128-bit loads and the V column of the chunk is loaded in full before the weighted
 // sum, so each phase waits for memory once.
 template <typename T, int G, int DC>
-__global__ __launch_bounds__(64) void attn_partial_kernel(AttnParams P) {
-  const int kvh = blockIdx.y;
-  const int c = blockIdx.x;
-  const int T_act = min(P.tokens_dev ? P.tokens_dev[0] + P.tokens : P.tokens, P.max_tokens);
-  if (c * kChunk >= T_act) return;
+__device__ void attn_chunk(const AttnParams& P, int kvh, int c, int T_act) {
   const int D = DC ? DC : P.head_dim;
   const int lane = threadIdx.x;
   __shared__ float q_s[G * 256];
@@ -63,6 +59,9 @@ __global__ __launch_bounds__(64) void attn_partial_kernel(AttnParams P) {
   float sc[G];
 #pragma unroll
   for (int g = 0; g < G; g++) sc[g] = 0.0f;
+  // V column requested together with K when the registers allow it (G <= 4)
+  constexpr bool kVEarly = DC == 64 && G <= 4;
+  float vv[DC == 64 ? kChunk : 1];
   if constexpr (DC != 0) {
     // contiguous rows, capacity a whole number of chunks: every row of the chunk is in
     // bounds, rows past the count are read and masked
@@ -70,6 +69,12 @@ __global__ __launch_bounds__(64) void attn_partial_kernel(AttnParams P) {
     uint4 kr[DC / 8];
 #pragma unroll
     for (int i = 0; i < DC / 8; i++) kr[i] = krow[i];
+    if constexpr (kVEarly) {
+      // the chunk's V column (lane = dimension) is requested together with K
+      const T* vcol = reinterpret_cast<const T*>(P.values) + kvh * P.v_head + (int64_t)(c * kChunk) * DC + lane;
+#pragma unroll
+      for (int tt = 0; tt < kChunk; tt++) vv[tt] = to_f32(vcol[tt * DC]);
+    }
 #pragma unroll
     for (int i = 0; i < DC / 8; i++) {
       const uint32_t kw[4] = {kr[i].x, kr[i].y, kr[i].z, kr[i].w};
@@ -111,10 +116,11 @@ __global__ __launch_bounds__(64) void attn_partial_kernel(AttnParams P) {
   __syncthreads();
   // phase 2: lane = dimension, o = fma chain over the chunk's tokens ascending
   if constexpr (DC == 64) {
-    const T* vcol = reinterpret_cast<const T*>(P.values) + kvh * P.v_head + (int64_t)(c * kChunk) * DC + lane;
-    float vv[kChunk];
+    if constexpr (!kVEarly) {
+      const T* vcol = reinterpret_cast<const T*>(P.values) + kvh * P.v_head + (int64_t)(c * kChunk) * DC + lane;
 #pragma unroll
-    for (int tt = 0; tt < kChunk; tt++) vv[tt] = to_f32(vcol[tt * DC]);
+      for (int tt = 0; tt < kChunk; tt++) vv[tt] = to_f32(vcol[tt * DC]);
+    }
     float o[G];
 #pragma unroll
     for (int g = 0; g < G; g++) o[g] = 0.0f;
@@ -144,13 +150,19 @@ __global__ __launch_bounds__(64) void attn_partial_kernel(AttnParams P) {
   }
 }
 
+template <typename T, int G, int DC>
+__global__ __launch_bounds__(64) void attn_partial_kernel(AttnParams P) {
+  const int kvh = blockIdx.y;
+  const int c = blockIdx.x;
+  const int T_act = min(P.tokens_dev ? P.tokens_dev[0] + P.tokens : P.tokens, P.max_tokens);
+  if (c * kChunk < T_act) attn_chunk<T, G, DC>(P, kvh, c, T_act);
+}
+
 // Combine of one head, same arithmetic as the sequential description above: the
 // chunk metadata is loaded one chunk per lane, exp(m_c - M) is evaluated per lane and
-// the chunk-order folds read it back lane by lane.
+// the chunk-order folds read it back lane by lane.  One wave.
 template <typename T, typename SKT>
-__global__ __launch_bounds__(64) void attn_combine_kernel(AttnParams P) {
-  const int h = blockIdx.x;
-  const int lane = threadIdx.x;
+__device__ void combine_head(const AttnParams& P, int h, int lane) {
   const int T_act = min(P.tokens_dev ? P.tokens_dev[0] + P.tokens : P.tokens, P.max_tokens);
   const int nc = T_act > 0 ? (T_act + kChunk - 1) / kChunk : 0;
   const float* pm = P.part_m + (int64_t)h * P.max_chunks;
@@ -210,6 +222,11 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(AttnParams P) {
     const int d = lane + 64 * q;
     if (d < D) store<T>(reinterpret_cast<T*>(P.out) + (int64_t)h * D + d, acc[q] / den);
   }
+}
+
+template <typename T, typename SKT>
+__global__ __launch_bounds__(64) void attn_combine_kernel(AttnParams P) {
+  combine_head<T, SKT>(P, blockIdx.x, threadIdx.x);
 }
 
 template <typename T, int G>
