@@ -153,6 +153,48 @@ def affine_lowbit_phase(be, bits: int, rows: int, cols: int, copies: int, seed: 
             "GB_s": nbytes / t / 1e9, "frac_of_hbm_peak": nbytes / t / 1e9 / HBM_PEAK_GBS, "rotated_copies": copies}
 
 
+def batched_phase(be, seed: int) -> dict:
+    """Batched small-M GEMMs at hidden 5120 (M in {1, 4, 16, 64}; MFMA for M >= 16):
+    int4 g128 and fp8-e4m3 + per-row scale, N = 17920; and the M-row lm_head argmax."""
+    import torch
+
+    dev = be.device
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    rows, cols = 17920, 5120
+    res = {}
+    copies = 12
+    W = torch.randint(0, 256, (copies, rows, cols // 2), generator=g, device=dev, dtype=torch.uint8)
+    S = (torch.randn((copies, rows, cols // 128), generator=g, device=dev).abs() * 0.02).to(torch.float16)
+    for m in (1, 4, 16, 64):
+        x = torch.randn((m, cols), generator=g, device=dev).to(torch.float16)
+        out = torch.empty((m, rows), device=dev, dtype=torch.float16)
+        t = _time_rotated(lambda i: be.int4_batched_matvec(W[i], S[i], x, out), copies, trials=10)
+        nbytes = rows * cols // 2 + rows * cols // 128 * 2 + m * (cols + rows) * 2
+        res[f"int4_g128_M{m}"] = {"us": t * 1e6, "GB_s": nbytes / t / 1e9, "TFLOP_s": 2 * m * rows * cols / t / 1e12}
+    del W, S
+    copies = 6
+    F8 = torch.randint(0, 126, (copies, rows, cols), generator=g, device=dev, dtype=torch.uint8).view(torch.float8_e4m3fn)
+    FS = torch.rand((copies, rows), generator=g, device=dev) * 0.01
+    for m in (1, 4, 16, 64):
+        x = torch.randn((m, cols), generator=g, device=dev).to(torch.float16)
+        out = torch.empty((m, rows), device=dev, dtype=torch.float16)
+        t = _time_rotated(lambda i: be.scaled_batched_matvec(F8[i], FS[i], x, out), copies, trials=10)
+        nbytes = rows * cols + rows * 4 + m * (cols + rows) * 2
+        res[f"fp8_row_M{m}"] = {"us": t * 1e6, "GB_s": nbytes / t / 1e9, "TFLOP_s": 2 * m * rows * cols / t / 1e12}
+    del F8, FS
+    V = 152064
+    LM = (torch.randn((V, cols), generator=g, device=dev) * 0.02).to(torch.float16)
+    for m in (1, 4):
+        x = torch.randn((m, cols), generator=g, device=dev).to(torch.float16)
+        t = _time_rotated(lambda i: be.matvec_argmax_batched(LM, x), 1, trials=5)
+        nbytes = V * cols * 2 + m * cols * 2
+        res[f"lm_head_argmax_152064x5120_M{m}"] = {"us": t * 1e6, "GB_s": nbytes / t / 1e9}
+    del LM
+    torch.cuda.empty_cache()
+    return res
+
+
 # --------------------------------------------------------------------------- decode timing
 def _time_decode(dec, start_token: int, position: int, warmup: int, steps: int) -> dict:
     import torch
@@ -324,6 +366,8 @@ def main() -> int:
         extra["q2_affine_g64_17920x5120"] = affine_lowbit_phase(be, 2, 17920, 5120, 24, args.seed + 4)
         extra["q1_affine_g64_5120x5120"] = affine_lowbit_phase(be, 1, 5120, 5120, 64, args.seed + 5)
         torch.cuda.empty_cache()
+        _log("batched small-M GEMM (hidden 5120)")
+        extra["batched_5120"] = batched_phase(be, args.seed + 6)
     del be
     torch.cuda.empty_cache()
 

@@ -269,6 +269,34 @@ int tt_moe_router_matvec_topk(const void* weight, int w_dtype, int64_t w_row, co
 int tt_moe_router_topk(const void* logits, int logits_dtype, int64_t experts, int64_t top_k, int renormalize,
                        int32_t* indices_out, void* scores_out, int score_dtype, void* stream);
 
+/* ---------------------------------------------------------------- batched small-M GEMM
+ *
+ * y[m] = W x[m] for M activation rows x [M, x_row] (fp16), y [M, out_row] (fp16).
+ * The reference has no batched variant (its kernels take one activation vector and
+ * its tensor-core variants broadcast it, triton_kernels.py:596-638); these extend
+ * TritonDecodeBackend.int4_scaled_matvec (:4597-4743) and scaled_matvec (:4452-4595)
+ * to M rows.  M < 16 runs the GEMV engine on up to four rows per launch (row m equals
+ * the single-row operator bit for bit); M >= 16 (up to 64) runs an MFMA kernel
+ * whose fp32 sums follow the hardware's order (tolerance parity).  cols must be a
+ * multiple of 256 up to 8192. */
+int tt_int4_batched_matvec(const void* packed, int64_t w_row_bytes, const void* scales_f16, int64_t s_row,
+                           const void* x, int64_t x_row, void* out, int64_t out_row, int64_t m, int64_t rows,
+                           int64_t cols, int64_t group_size, void* stream);
+/* fp8-e4m3 rows with an fp32 scale per output row. */
+int tt_scaled_batched_matvec(const void* weight, int64_t w_row_bytes, const float* scales, const void* x,
+                             int64_t x_row, void* out, int64_t out_row, int64_t m, int64_t rows, int64_t cols,
+                             void* stream);
+
+/* Greedy lm_head for M activation rows: out_idx[m] = first index of the maximum of
+ * round(W x[m]) (the tt_matvec_argmax semantics per row), logits [M, logits_row]
+ * stored when non-null.  `partials` needs tt_matvec_argmax_batched_partials(m, rows,
+ * cols) entries.  Extends matvec_argmax_tensor (triton_kernels.py:5365-5398) to M
+ * rows. */
+int64_t tt_matvec_argmax_batched_partials(int64_t m, int64_t rows, int64_t cols);
+int tt_matvec_argmax_batched(const void* weight, int64_t w_row, const void* x, int64_t x_row, int64_t m,
+                             void* logits, int64_t logits_row, int64_t rows, int64_t cols, uint64_t* partials,
+                             int64_t partials_capacity, int64_t* out_idx, float* out_val, void* stream);
+
 /* ---------------------------------------------------------------- fused decode-step GEMVs
  *
  * One launch of the GEMV engine with the neighbouring decode-step operators folded

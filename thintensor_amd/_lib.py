@@ -87,11 +87,16 @@ SIGNATURES: dict[str, list] = {
                                       _P],
     "tt_moe_router_matvec_topk": [_P, _I, _L, _P, _I, _L, _P, _I, _L, _L, _I, _P, _P, _I, _P],
     "tt_moe_router_topk": [_P, _I, _L, _L, _I, _P, _P, _I, _P],
+    "tt_int4_batched_matvec": [_P, _L, _P, _L, _P, _L, _P, _L, _L, _L, _L, _L, _P],
+    "tt_scaled_batched_matvec": [_P, _L, _P, _P, _L, _P, _L, _L, _L, _L, _P],
+    "tt_matvec_argmax_batched_partials": [_L, _L, _L],
+    "tt_matvec_argmax_batched": [_P, _L, _P, _L, _L, _P, _L, _L, _L, _P, _L, _P, _P, _P],
     "tt_fused_struct_sizes": [_LP, _LP],
     "tt_fused_gemv_run": [_FGP, _P],
     "tt_fused_lm_head_argmax": [_FGP, _P, _L, _P, _P, _P, _P, _P, ctypes.c_int32, _P],
 }
-_RESTYPES = {"tt_last_error": ctypes.c_char_p, "tt_matvec_argmax_partials": ctypes.c_int64}
+_RESTYPES = {"tt_last_error": ctypes.c_char_p, "tt_matvec_argmax_partials": ctypes.c_int64,
+             "tt_matvec_argmax_batched_partials": ctypes.c_int64}
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

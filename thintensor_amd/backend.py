@@ -743,6 +743,60 @@ class HipDecodeBackend:
         _lib.check(rc, "moe_router_topk")
         return indices_out, scores_out
 
+    # ------------------------------------------------------------ batched small-M GEMM (no reference counterpart)
+    def int4_batched_matvec(self, packed_weight: torch.Tensor, scales: torch.Tensor, x: torch.Tensor,
+                            out: torch.Tensor, *, group_size: int = 128) -> torch.Tensor:
+        """out[m] = dequant(W) x[m] for x fp16 [M, cols], out fp16 [M, rows]; int4 group-128
+        weights with fp16 scales.  M < 16 is bit-identical to int4_scaled_matvec per row;
+        M >= 16 uses MFMA (tolerance parity)."""
+        _require_cuda(packed_weight, scales, x, out)
+        if x.ndim != 2 or out.ndim != 2 or x.shape[0] != out.shape[0]:
+            raise ValueError("batched matvec takes x [M, cols] and out [M, rows]")
+        if scales.dtype != torch.float16 or x.dtype != torch.float16 or out.dtype != torch.float16:
+            raise ValueError("batched int4 matvec takes fp16 scales, activations and outputs")
+        rows, cols = int(packed_weight.shape[0]), int(x.shape[1])
+        if packed_weight.shape[1] * packed_weight.element_size() * 2 != cols or out.shape[1] != rows:
+            raise ValueError("batched int4 matvec shape mismatch")
+        rc = self.lib.tt_int4_batched_matvec(
+            packed_weight.data_ptr(), packed_weight.stride(0) * packed_weight.element_size(), scales.data_ptr(),
+            scales.stride(0), x.data_ptr(), x.stride(0), out.data_ptr(), out.stride(0), int(x.shape[0]), rows, cols,
+            group_size, _stream(out))
+        _lib.check(rc, "int4_batched_matvec")
+        return out
+
+    def scaled_batched_matvec(self, weight: torch.Tensor, scales: torch.Tensor, x: torch.Tensor,
+                              out: torch.Tensor) -> torch.Tensor:
+        """out[m] = (W x[m]) * s for fp8-e4m3 W [rows, cols] and fp32 s [rows]."""
+        _require_cuda(weight, scales, x, out)
+        if x.ndim != 2 or out.ndim != 2 or x.shape[0] != out.shape[0] or scales.dtype != torch.float32:
+            raise ValueError("batched scaled matvec takes x [M, cols], out [M, rows] and fp32 scales")
+        if x.dtype != torch.float16 or out.dtype != torch.float16:
+            raise ValueError("batched scaled matvec takes fp16 activations and outputs")
+        rows, cols = int(weight.shape[0]), int(weight.shape[1])
+        rc = self.lib.tt_scaled_batched_matvec(
+            weight.data_ptr(), weight.stride(0) * weight.element_size(), scales.data_ptr(), x.data_ptr(), x.stride(0),
+            out.data_ptr(), out.stride(0), int(x.shape[0]), rows, cols, _stream(out))
+        _lib.check(rc, "scaled_batched_matvec")
+        return out
+
+    def matvec_argmax_batched(self, weight: torch.Tensor, x: torch.Tensor,
+                              logits: torch.Tensor | None = None) -> torch.Tensor:
+        """Greedy lm_head for x [M, cols]: int64 [M] tokens (first index of each row's
+        maximum rounded logit)."""
+        _require_cuda(weight, x)
+        m, rows, cols = int(x.shape[0]), int(weight.shape[0]), int(weight.shape[1])
+        if x.ndim != 2 or x.shape[1] != cols or weight.dtype != torch.float16 or x.dtype != torch.float16:
+            raise ValueError("batched matvec_argmax takes fp16 W [rows, cols] and x [M, cols]")
+        need = int(self.lib.tt_matvec_argmax_batched_partials(m, rows, cols))
+        partials = torch.empty(need, device=self.device, dtype=torch.int64)
+        idx = torch.empty(m, device=self.device, dtype=torch.int64)
+        rc = self.lib.tt_matvec_argmax_batched(
+            weight.data_ptr(), weight.stride(0), x.data_ptr(), x.stride(0), m,
+            logits.data_ptr() if logits is not None else None, logits.stride(0) if logits is not None else 0, rows,
+            cols, partials.data_ptr(), need, idx.data_ptr(), None, _stream(x))
+        _lib.check(rc, "matvec_argmax_batched")
+        return idx
+
     # ------------------------------------------------------------ fused decode-step GEMVs (no reference counterpart)
     def fused_gemv(self, desc: "_lib.FusedGemv") -> None:
         """One GEMV launch with its decode-step neighbours folded in (RMSNorm prologue,

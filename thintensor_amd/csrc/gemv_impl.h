@@ -169,8 +169,11 @@ struct GemvData {
 };
 
 template <Fmt F, SMode SM, typename XT, typename OT, typename ST, int LPR, int ROWS, int L, bool AM,
-          Pro PRO = Pro::kLoad, bool EPI = false, int PF = 1>
+          Pro PRO = Pro::kLoad, bool EPI = false, int PF = 1, int MR = 1>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
+  // MR > 1: MR activation rows (x + m * x_slot) share every weight load; output row m
+  // at out + m * out_slot, each with the single-row reduction order.
+  static_assert(MR == 1 || (PRO == Pro::kLoad && !EPI), "several activation rows only with a loaded x");
   extern __shared__ uint32_t xs_lds[];
   constexpr int B = FmtInfo<F>::kBytes;
   constexpr int SUBS = 64 / LPR;
@@ -202,7 +205,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
   for (int k = 0; k < NVG; k++) grow[k] = rs_row<ROWS>(l, GLEV, k) * SUBS + sub;
   const int frow = rs_row<ROWS>(l, log2c(ROWS), 0) * SUBS + sub;  // row stored by this lane
   const bool fstore = (l >> log2c(ROWS)) == 0;
-  uint64_t best = 0;
+  uint64_t best[MR];
+#pragma unroll
+  for (int m = 0; m < MR; m++) best[m] = 0;
 
   auto setup = [&](int b, Batch& bt) {
     const int v0 = __builtin_amdgcn_readfirstlane(b * per_iter);
@@ -287,10 +292,14 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
       if (r < rounds) fetch(cb, r, cd[r]);
   }
   if constexpr (PRO == Pro::kLoad) {
-    // Stage the activation vector while the first weight loads are in flight.
-    const uint4* xg = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(P.x) + (int64_t)slot * P.x_slot);
-    uint4* xl = reinterpret_cast<uint4*>(xs_lds);
-    for (int i = threadIdx.x; i < (P.cols >> 3); i += blockDim.x) xl[i] = xg[i];
+    // Stage the activation vector(s) while the first weight loads are in flight.
+#pragma unroll
+    for (int m = 0; m < MR; m++) {
+      const uint4* xg =
+          reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(P.x) + (int64_t)(slot + m) * P.x_slot);
+      uint4* xl = reinterpret_cast<uint4*>(xs_lds + m * (P.cols >> 1));
+      for (int i = threadIdx.x; i < (P.cols >> 3); i += blockDim.x) xl[i] = xg[i];
+    }
     __syncthreads();
   } else {
     // Build the activation vector: RMSNorm of the residual stream, with the same
@@ -358,105 +367,116 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
   }
 
   // One round: chunk partials of the batch rows, scaled and accumulated in round order.
-  auto consume = [&](const Batch& bt, const Data& d, int r, float* acc) {
+  auto consume = [&](const Batch& bt, const Data& d, int r, float (*accs)[ROWS]) {
     const int j = r * LPR + l;
     const bool cv = j < nchunks;
-    uint32_t xw[16];
-    {
-      const uint4* xp = reinterpret_cast<const uint4*>(xs_lds + (cv ? j : 0) * 16);
+    uint32_t xws[MR][16];
+#pragma unroll
+    for (int m = 0; m < MR; m++) {
+      const uint4* xp = reinterpret_cast<const uint4*>(xs_lds + m * (P.cols >> 1) + (cv ? j : 0) * 16);
 #pragma unroll
       for (int q = 0; q < 4; q++) {
         uint4 v = xp[q];
-        xw[4 * q] = v.x; xw[4 * q + 1] = v.y; xw[4 * q + 2] = v.z; xw[4 * q + 3] = v.w;
+        xws[m][4 * q] = v.x; xws[m][4 * q + 1] = v.y; xws[m][4 * q + 2] = v.z; xws[m][4 * q + 3] = v.w;
       }
     }
-    float p[ROWS];
-    chunk_dot_rows<F, XT, ROWS>(d.w, xw, p);
+    float ps[MR][ROWS];
+    chunk_dot_rows_multi<F, XT, ROWS, MR>(d.w, xws, ps);
 #pragma unroll
-    for (int i = 0; i < ROWS; i++) p[i] = (cv && bt.rv[i]) ? p[i] : 0.0f;
-    if constexpr (SM == SMode::kNone || SM == SMode::kRow) {
+    for (int m = 0; m < MR; m++) {
+      float* acc = accs[m];
+      float* p = ps[m];
+      const uint32_t* xw = xws[m];
 #pragma unroll
-      for (int i = 0; i < ROWS; i++) acc[i] = acc[i] + p[i];
-    } else if constexpr (SM == SMode::kBlockE8) {
+      for (int i = 0; i < ROWS; i++) p[i] = (cv && bt.rv[i]) ? p[i] : 0.0f;
+      if constexpr (SM == SMode::kNone || SM == SMode::kRow) {
 #pragma unroll
-      for (int i = 0; i < ROWS; i++) {
-        const float t = p[i] * pow2i(d.e[i] - 127);
-        acc[i] = acc[i] + ((cv && bt.rv[i]) ? t : 0.0f);
-      }
-    } else {
-      float xsum = 0.0f;
-      if constexpr (SM == SMode::kGroupAff) {
+        for (int i = 0; i < ROWS; i++) acc[i] = acc[i] + p[i];
+      } else if constexpr (SM == SMode::kBlockE8) {
 #pragma unroll
-        for (int e = 0; e < 32; e++) xsum = xsum + xv<XT>(xw, e);
-        xsum = cv ? xsum : 0.0f;
-        reduce_range<1, 1, LG>(&xsum);
-      }
-      reduce_range<ROWS, 1, LG>(p);
-#pragma unroll
-      for (int k = 0; k < NVG; k++) {
-        float t;
-        if constexpr (SM == SMode::kGroupAff) {
-          float m = d.m[k];
-          if (P.aff_zero) m = -(m * d.s[k]);
-          t = __builtin_fmaf(xsum, m, p[k] * d.s[k]);
-        } else {
-          t = p[k] * d.s[k];
+        for (int i = 0; i < ROWS; i++) {
+          const float t = p[i] * pow2i(d.e[i] - 127);
+          acc[i] = acc[i] + ((cv && bt.rv[i]) ? t : 0.0f);
         }
-        const bool ok = cv && (bt.lr0 + grow[k] < bt.rows);
-        acc[k] = acc[k] + (ok ? t : 0.0f);
+      } else {
+        float xsum = 0.0f;
+        if constexpr (SM == SMode::kGroupAff) {
+#pragma unroll
+          for (int e = 0; e < 32; e++) xsum = xsum + xv<XT>(xw, e);
+          xsum = cv ? xsum : 0.0f;
+          reduce_range<1, 1, LG>(&xsum);
+        }
+        reduce_range<ROWS, 1, LG>(p);
+#pragma unroll
+        for (int k = 0; k < NVG; k++) {
+          float t;
+          if constexpr (SM == SMode::kGroupAff) {
+            float m = d.m[k];
+            if (P.aff_zero) m = -(m * d.s[k]);
+            t = __builtin_fmaf(xsum, m, p[k] * d.s[k]);
+          } else {
+            t = p[k] * d.s[k];
+          }
+          const bool ok = cv && (bt.lr0 + grow[k] < bt.rows);
+          acc[k] = acc[k] + (ok ? t : 0.0f);
+        }
       }
     }
   };
 
   // Row values of a finished batch: final lane reduction, then the epilogue.
-  auto finish = [&](const Batch& bt, float* acc) {
-    if constexpr (kGroup) reduce_range<NVG, LG, LPR>(acc);
-    else reduce_range<ROWS, 1, LPR>(acc);
-    float v = acc[0];
-    const bool ok = fstore && bt.lr0 + frow < bt.rows;
-    if constexpr (SM == SMode::kRow) v = v * to_f32(bt.sb[(int64_t)(ok ? bt.lr0 + frow : 0) * bt.s_row]);
-    if (!EPI || bt.kind == kSegPlain) {
-      if (bt.bias != nullptr && ok) v = round_to<OT>(v) + to_f32(reinterpret_cast<const OT*>(bt.bias)[bt.lr0 + frow]);
-      if (ok && bt.out != nullptr) store<OT>(reinterpret_cast<OT*>(bt.out) + (int64_t)slot * P.out_slot + bt.lr0 + frow, v);
-    } else if constexpr (EPI) {
-      // fused epilogues: the row value rounded to OT as the unfused operator would
-      // store it, then RoPE / cache placement / SiLU on it
-      bool odd = false;
-      const int fr = bt.lr0 + frow;
-      const int ph = bt.kind == kSegCache ? fr : paired_row<SUBS>(fr, bt.kind, P.f.head_dim, odd);
-      if (bt.bias != nullptr && ok) v = round_to<OT>(v) + to_f32(reinterpret_cast<const OT*>(bt.bias)[ph]);
-      const float val = round_to<OT>(v);
-      const float pv = xor_partner<ROWS / 2 < 1 ? 1 : ROWS / 2>(val);   // the other half of the pair
-      const int64_t pos = P.f.pos != nullptr ? (int64_t)P.f.pos[0] : 0;
-      const int D = P.f.head_dim;
-      if (bt.kind == kSegSilu) {
-        if (ok && !odd) store<OT>(reinterpret_cast<OT*>(bt.out) + ph, silu_mul_val(val, pv));
-      } else {
-        float o = val;
-        if (bt.kind != kSegCache && pos >= 0 && pos < P.f.table_rows) {
-          const int half = D >> 1;
-          const int j = (ph % D) - (odd ? half : 0);
-          const float c = ld<OT>(P.f.cos, pos * P.f.table_row + j);
-          const float sn = ld<OT>(P.f.sin, pos * P.f.table_row + j);
-          float o1, o2;
-          if (odd) rope_pair<OT>(pv, val, c, sn, o1, o2);
-          else rope_pair<OT>(val, pv, c, sn, o1, o2);
-          o = odd ? o2 : o1;
-        }
-        if (ok) {
-          if (bt.kind == kSegRopeOut) {
-            store<OT>(reinterpret_cast<OT*>(bt.out) + ph, o);
-          } else if (pos >= 0 && pos < P.f.capacity) {
-            const int64_t h = ph / D, d = ph - h * D;
-            store<OT>(reinterpret_cast<OT*>(bt.out) + h * P.f.cache_head + pos * D + d, o);
+  auto finish = [&](const Batch& bt, float (*accs)[ROWS]) {
+#pragma unroll
+    for (int m = 0; m < MR; m++) {
+      float* acc = accs[m];
+      if constexpr (kGroup) reduce_range<NVG, LG, LPR>(acc);
+      else reduce_range<ROWS, 1, LPR>(acc);
+      float v = acc[0];
+      const bool ok = fstore && bt.lr0 + frow < bt.rows;
+      if constexpr (SM == SMode::kRow) v = v * to_f32(bt.sb[(int64_t)(ok ? bt.lr0 + frow : 0) * bt.s_row]);
+      if (!EPI || bt.kind == kSegPlain) {
+        if (bt.bias != nullptr && ok) v = round_to<OT>(v) + to_f32(reinterpret_cast<const OT*>(bt.bias)[bt.lr0 + frow]);
+        if (ok && bt.out != nullptr) store<OT>(reinterpret_cast<OT*>(bt.out) + (int64_t)(slot + m) * P.out_slot + bt.lr0 + frow, v);
+      } else if constexpr (EPI) {
+        // fused epilogues: the row value rounded to OT as the unfused operator would
+        // store it, then RoPE / cache placement / SiLU on it
+        bool odd = false;
+        const int fr = bt.lr0 + frow;
+        const int ph = bt.kind == kSegCache ? fr : paired_row<SUBS>(fr, bt.kind, P.f.head_dim, odd);
+        if (bt.bias != nullptr && ok) v = round_to<OT>(v) + to_f32(reinterpret_cast<const OT*>(bt.bias)[ph]);
+        const float val = round_to<OT>(v);
+        const float pv = xor_partner<ROWS / 2 < 1 ? 1 : ROWS / 2>(val);   // the other half of the pair
+        const int64_t pos = P.f.pos != nullptr ? (int64_t)P.f.pos[0] : 0;
+        const int D = P.f.head_dim;
+        if (bt.kind == kSegSilu) {
+          if (ok && !odd) store<OT>(reinterpret_cast<OT*>(bt.out) + ph, silu_mul_val(val, pv));
+        } else {
+          float o = val;
+          if (bt.kind != kSegCache && pos >= 0 && pos < P.f.table_rows) {
+            const int half = D >> 1;
+            const int j = (ph % D) - (odd ? half : 0);
+            const float c = ld<OT>(P.f.cos, pos * P.f.table_row + j);
+            const float sn = ld<OT>(P.f.sin, pos * P.f.table_row + j);
+            float o1, o2;
+            if (odd) rope_pair<OT>(pv, val, c, sn, o1, o2);
+            else rope_pair<OT>(val, pv, c, sn, o1, o2);
+            o = odd ? o2 : o1;
+          }
+          if (ok) {
+            if (bt.kind == kSegRopeOut) {
+              store<OT>(reinterpret_cast<OT*>(bt.out) + ph, o);
+            } else if (pos >= 0 && pos < P.f.capacity) {
+              const int64_t h = ph / D, d = ph - h * D;
+              store<OT>(reinterpret_cast<OT*>(bt.out) + h * P.f.cache_head + pos * D + d, o);
+            }
           }
         }
       }
-    }
-    if constexpr (AM) {
-      if (ok) {
-        const uint64_t key = argmax_key(round_to<OT>(v), (uint32_t)(bt.lr0 + frow));
-        best = key > best ? key : best;
+      if constexpr (AM) {
+        if (ok) {
+          const uint64_t key = argmax_key(round_to<OT>(v), (uint32_t)(bt.lr0 + frow));
+          best[m] = key > best[m] ? key : best[m];
+        }
       }
     }
   };
@@ -465,9 +485,11 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
     while (cb.active) {
       Batch nb;
       nb.active = false;
-      float acc[ROWS];
+      float acc[MR][ROWS];
 #pragma unroll
-      for (int i = 0; i < ROWS; i++) acc[i] = 0.0f;
+      for (int m = 0; m < MR; m++)
+#pragma unroll
+        for (int i = 0; i < ROWS; i++) acc[m][i] = 0.0f;
       for (int r = 0; r < rounds; r++) {
         Data nd;
         if (r + 1 < rounds) {
@@ -493,9 +515,11 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
         for (int r = 0; r < PF; r++)
           if (r < rounds) fetch(nb, r, nd[r]);
       }
-      float acc[ROWS];
+      float acc[MR][ROWS];
 #pragma unroll
-      for (int i = 0; i < ROWS; i++) acc[i] = 0.0f;
+      for (int m = 0; m < MR; m++)
+#pragma unroll
+        for (int i = 0; i < ROWS; i++) acc[m][i] = 0.0f;
 #pragma unroll
       for (int r = 0; r < PF; r++)
         if (r < rounds) consume(cb, cd[r], r, acc);
@@ -507,8 +531,11 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
     }
   }
   if constexpr (AM) {
-    best = wave_max_u64(best);
-    if (lane == 0) P.am_partials[blockIdx.x * (blockDim.x >> 6) + wave] = best;
+#pragma unroll
+    for (int m = 0; m < MR; m++) {
+      const uint64_t bm = wave_max_u64(best[m]);
+      if (lane == 0) P.am_partials[(int64_t)(blockIdx.x * (blockDim.x >> 6) + wave) * MR + m] = bm;
+    }
   }
 }
 
@@ -520,7 +547,7 @@ constexpr int kMaxGemvBlocks = 2048;
 constexpr int kMaxGemvWaves = 4 * kMaxGemvBlocks;
 
 template <Fmt F, SMode SM, typename XT, typename OT, typename ST, int LPR, int ROWS, int L, Pro PRO = Pro::kLoad,
-          bool EPI = false, int PF = 1>
+          bool EPI = false, int PF = 1, int MR = 1>
 static int launch_one(GemvParams P, int slots, hipStream_t stream, const char* what) {
   constexpr int SUBS = 64 / LPR;
   constexpr int per_iter = ROWS * SUBS;
@@ -534,7 +561,7 @@ static int launch_one(GemvParams P, int slots, hipStream_t stream, const char* w
   int blocks = (batches + 3) / 4;
   if (blocks < 1) blocks = 1;
   if (blocks > kMaxGemvBlocks) blocks = kMaxGemvBlocks;
-  const size_t lds = (size_t)P.cols * 2;
+  const size_t lds = (size_t)P.cols * 2 * MR;
   if (P.am_partials == nullptr && slots == 1) {
     // Persistent grid of at most the workgroups the chip holds at once: waves loop
     // over row batches with the next batch in flight, instead of a second
@@ -546,7 +573,7 @@ static int launch_one(GemvParams P, int slots, hipStream_t stream, const char* w
       if (hipGetDevice(&dev) == hipSuccess &&
           hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
           hipOccupancyMaxActiveBlocksPerMultiprocessor(
-              &per_cu, reinterpret_cast<const void*>(&gemv_kernel<F, SM, XT, OT, ST, LPR, ROWS, L, false, PRO, EPI, PF>),
+              &per_cu, reinterpret_cast<const void*>(&gemv_kernel<F, SM, XT, OT, ST, LPR, ROWS, L, false, PRO, EPI, PF, MR>),
               256, lds) == hipSuccess &&
           per_cu > 0 && cus > 0) {
         cached_cap = per_cu * cus;
@@ -560,28 +587,28 @@ static int launch_one(GemvParams P, int slots, hipStream_t stream, const char* w
   if (P.am_partials != nullptr) {
     if constexpr (SM == SMode::kNone) {
       // unused partial slots must not win the final reduction
-      hipLaunchKernelGGL((gemv_kernel<F, SM, XT, OT, ST, LPR, ROWS, L, true, PRO, EPI, PF>), dim3(blocks, slots),
+      hipLaunchKernelGGL((gemv_kernel<F, SM, XT, OT, ST, LPR, ROWS, L, true, PRO, EPI, PF, MR>), dim3(blocks, slots),
                          dim3(256), lds, stream, P);
       return check_launch(what);
     }
     set_error("%s: argmax epilogue is only available for dense weights", what);
     return TT_ERR_UNSUPPORTED;
   }
-  hipLaunchKernelGGL((gemv_kernel<F, SM, XT, OT, ST, LPR, ROWS, L, false, PRO, EPI, PF>), dim3(blocks, slots), dim3(256),
-                     lds, stream, P);
+  hipLaunchKernelGGL((gemv_kernel<F, SM, XT, OT, ST, LPR, ROWS, L, false, PRO, EPI, PF, MR>), dim3(blocks, slots),
+                     dim3(256), lds, stream, P);
   return check_launch(what);
 }
 
 template <Fmt F, SMode SM, typename XT, typename OT, typename ST, int ROWS, int L, Pro PRO = Pro::kLoad, bool EPI = false,
-          int PF = 1>
+          int PF = 1, int MR = 1>
 static int launch_lpr(int lpr, const GemvParams& P, int slots, hipStream_t stream, const char* what) {
   switch (lpr) {
-    case 64: return launch_one<F, SM, XT, OT, ST, 64, ROWS, L, PRO, EPI, PF>(P, slots, stream, what);
+    case 64: return launch_one<F, SM, XT, OT, ST, 64, ROWS, L, PRO, EPI, PF, MR>(P, slots, stream, what);
     case 32:
-      if constexpr (L <= 32) return launch_one<F, SM, XT, OT, ST, 32, ROWS, L, PRO, EPI, PF>(P, slots, stream, what);
+      if constexpr (L <= 32) return launch_one<F, SM, XT, OT, ST, 32, ROWS, L, PRO, EPI, PF, MR>(P, slots, stream, what);
       break;
     case 16:
-      if constexpr (L <= 16) return launch_one<F, SM, XT, OT, ST, 16, ROWS, L, PRO, EPI, PF>(P, slots, stream, what);
+      if constexpr (L <= 16) return launch_one<F, SM, XT, OT, ST, 16, ROWS, L, PRO, EPI, PF, MR>(P, slots, stream, what);
       break;
     default: break;
   }

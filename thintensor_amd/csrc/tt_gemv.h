@@ -245,6 +245,52 @@ __device__ __forceinline__ void chunk_dot_rows(const Raw<FmtInfo<F>::kBytes>* r,
   }
 }
 
+// chunk_dot_rows for MR activation rows at once: every weight word is decoded once
+// and feeds the fma chains of all MR activation rows (each chain in the single-row
+// order, so row m's partials equal chunk_dot_rows on activation row m).
+template <Fmt F, typename XT, int NR, int MR>
+__device__ __forceinline__ void chunk_dot_rows_multi(const Raw<FmtInfo<F>::kBytes>* r, const uint32_t (*xw)[16],
+                                                     float (*p)[NR]) {
+  if constexpr (MR == 1) {
+    chunk_dot_rows<F, XT, NR>(r, xw[0], p[0]);
+  } else {
+#pragma unroll
+    for (int m = 0; m < MR; m++)
+#pragma unroll
+      for (int i = 0; i < NR; i++) p[m][i] = 0.0f;
+    if constexpr (F == Fmt::kInt4Sym || F == Fmt::kInt4Aff || F == Fmt::kMxfp4) {
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        _Float16 wv[NR][8];
+#pragma unroll
+        for (int i = 0; i < NR; i++) decode_word8<F>(r[i].w[q], wv[i]);
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+#pragma unroll
+          for (int m = 0; m < MR; m++) {
+            const float xe = xv<XT>(xw[m], 8 * q + e);
+#pragma unroll
+            for (int i = 0; i < NR; i++) p[m][i] = __builtin_fmaf((float)wv[i][e], xe, p[m][i]);
+          }
+        }
+      }
+    } else {
+      typename WVal<F>::T wv[NR][32];
+#pragma unroll
+      for (int i = 0; i < NR; i++) decode_chunk<F>(r[i], wv[i]);
+#pragma unroll
+      for (int e = 0; e < 32; e++) {
+#pragma unroll
+        for (int m = 0; m < MR; m++) {
+          const float xe = xv<XT>(xw[m], e);
+#pragma unroll
+          for (int i = 0; i < NR; i++) p[m][i] = __builtin_fmaf((float)wv[i][e], xe, p[m][i]);
+        }
+      }
+    }
+  }
+}
+
 template <Fmt F, typename XT>
 __device__ __forceinline__ float chunk_dot(const Raw<FmtInfo<F>::kBytes>& r, const uint32_t* xw) {
   float p;
