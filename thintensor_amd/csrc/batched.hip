@@ -42,15 +42,25 @@ struct MfmaParams {
 
 // Weights of one 128-column group for this lane: row n0 + lane % 16, columns
 // 128 g + 32 (lane / 16) + [0, 32).
+// int4 chunks carry the group scales of the four output rows the lane accumulates
+// (rows n0 + 4 (lane / 16) + i), requested together with the weights.
 template <WFmt W>
-struct WChunk { uint32_t w[W == WFmt::kInt4G128 ? 4 : 8]; };
+struct WChunk {
+  uint32_t w[W == WFmt::kInt4G128 ? 4 : 8];
+  f16_t sc[W == WFmt::kInt4G128 ? 4 : 1];
+};
 
 template <WFmt W>
-__device__ __forceinline__ WChunk<W> load_chunk(const MfmaParams& P, int row, int grp, int lane) {
+__device__ __forceinline__ WChunk<W> load_chunk(const MfmaParams& P, int row, int grp, int lane, int n0) {
   WChunk<W> c;
   if constexpr (W == WFmt::kInt4G128) {
     const uint4 v = *reinterpret_cast<const uint4*>(P.w + (int64_t)row * P.w_row + (int64_t)grp * 64 + 16 * (lane >> 4));
     c.w[0] = v.x; c.w[1] = v.y; c.w[2] = v.z; c.w[3] = v.w;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int r = n0 + 4 * (lane >> 4) + i;
+      c.sc[i] = reinterpret_cast<const f16_t*>(P.s)[(int64_t)(r < P.n ? r : P.n - 1) * P.s_row + grp];
+    }
   } else {
     const uint4* p = reinterpret_cast<const uint4*>(P.w + (int64_t)row * P.w_row + (int64_t)grp * 128 + 32 * (lane >> 4));
     const uint4 a = p[0], b = p[1];
@@ -85,59 +95,87 @@ __device__ __forceinline__ h8 a_operand(const WChunk<W>& c, int q) {
 
 template <WFmt W, int MT>
 __global__ __launch_bounds__(256) void mfma_gemm_kernel(MfmaParams P) {
-  __shared__ __attribute__((aligned(16))) uint16_t xs[MT * 16 * kSlice];
+  // Two LDS buffers of activation slices: slice s + 1 is loaded into registers while
+  // slice s computes, then written to the other buffer (one barrier per slice).  The
+  // weights of a slice are requested kAhead slices before they are used.
+  constexpr int kAhead = 4;
+  constexpr int XS = MT * 16 * kSlice;                 // halves per buffer
+  constexpr int XV = XS / 8 / 256;                     // 16-byte pieces per thread per slice
+  __shared__ __attribute__((aligned(16))) uint16_t xs[2 * XS];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n0 = (blockIdx.x * 4 + wave) * 16;
   const int arow = n0 + (lane & 15);                 // weight row this lane loads (A operand)
   const int lrow = arow < P.n ? arow : P.n - 1;
   const int g = lane >> 4;
+  const int slices = P.k / kSlice;
+  auto load_x = [&](int sl, uint4* regs) {
+#pragma unroll
+    for (int v = 0; v < XV; v++) {
+      const int i = threadIdx.x + 256 * v;
+      const int r = i / (kSlice / 8), c8 = i - r * (kSlice / 8);
+      regs[v] = r < P.m ? *reinterpret_cast<const uint4*>(P.x + (int64_t)r * P.x_row + (int64_t)sl * kSlice + 8 * c8)
+                        : (uint4){0u, 0u, 0u, 0u};
+    }
+  };
+  auto store_x = [&](int buf, const uint4* regs) {
+#pragma unroll
+    for (int v = 0; v < XV; v++) {
+      const int i = threadIdx.x + 256 * v;
+      const int r = i / (kSlice / 8), c8 = i - r * (kSlice / 8);
+      *reinterpret_cast<uint4*>(xs + buf * XS + r * kSlice + 8 * c8) = regs[v];
+    }
+  };
   f4 acc[MT];
 #pragma unroll
   for (int t = 0; t < MT; t++) acc[t] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
-  const int groups = P.k / 128;
-  WChunk<W> cur = load_chunk<W>(P, lrow, 0, lane);
-  for (int s0 = 0; s0 < P.k; s0 += kSlice) {
-    // stage x[0 : MT*16][s0 : s0 + kSlice] (rows past M are zero)
-    __syncthreads();
-    for (int i = threadIdx.x; i < MT * 16 * (kSlice / 8); i += blockDim.x) {
-      const int r = i / (kSlice / 8), c8 = i - r * (kSlice / 8);
-      uint4 v = {0u, 0u, 0u, 0u};
-      if (r < P.m) v = *reinterpret_cast<const uint4*>(P.x + (int64_t)r * P.x_row + s0 + 8 * c8);
-      *reinterpret_cast<uint4*>(xs + r * kSlice + 8 * c8) = v;
-    }
-    __syncthreads();
+  WChunk<W> ring[kAhead][kSlice / 128];
 #pragma unroll
-    for (int gs = 0; gs < kSlice / 128; gs++) {
-      const int grp = s0 / 128 + gs;
-      WChunk<W> nxt;
-      if (grp + 1 < groups) nxt = load_chunk<W>(P, lrow, grp + 1, lane);
-      f4 part[MT];
+  for (int u = 0; u < kAhead; u++)
+    if (u < slices)
 #pragma unroll
-      for (int t = 0; t < MT; t++) part[t] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
+      for (int gs = 0; gs < kSlice / 128; gs++) ring[u][gs] = load_chunk<W>(P, lrow, u * (kSlice / 128) + gs, lane, n0);
+  uint4 xr[XV];
+  load_x(0, xr);
+  store_x(0, xr);
+  __syncthreads();
+  for (int s0 = 0; s0 < slices; s0 += kAhead) {
 #pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const h8 a = a_operand<W>(cur, q);
+    for (int u = 0; u < kAhead; u++) {
+      const int sl = s0 + u;
+      if (sl < slices) {
+        if (sl + 1 < slices) load_x(sl + 1, xr);
+        const uint16_t* xb = xs + (sl & 1) * XS;
 #pragma unroll
-        for (int t = 0; t < MT; t++) {
-          const h8 b = *reinterpret_cast<const h8*>(xs + (16 * t + (lane & 15)) * kSlice + 128 * gs + 32 * g + 8 * q);
-          if constexpr (W == WFmt::kInt4G128) part[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, part[t], 0, 0, 0);
-          else acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[t], 0, 0, 0);
+        for (int gs = 0; gs < kSlice / 128; gs++) {
+          f4 part[MT];
+#pragma unroll
+          for (int t = 0; t < MT; t++) part[t] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (int q = 0; q < 4; q++) {
+            const h8 a = a_operand<W>(ring[u][gs], q);
+#pragma unroll
+            for (int t = 0; t < MT; t++) {
+              const h8 b = *reinterpret_cast<const h8*>(xb + (16 * t + (lane & 15)) * kSlice + 128 * gs + 32 * g + 8 * q);
+              if constexpr (W == WFmt::kInt4G128) part[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, part[t], 0, 0, 0);
+              else acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[t], 0, 0, 0);
+            }
+          }
+          if constexpr (W == WFmt::kInt4G128) {
+            // group scale of the four output rows this lane holds (rows n0 + 4g + i)
+#pragma unroll
+            for (int t = 0; t < MT; t++)
+#pragma unroll
+              for (int i = 0; i < 4; i++) acc[t][i] = __builtin_fmaf(part[t][i], to_f32(ring[u][gs].sc[i]), acc[t][i]);
+          }
         }
-      }
-      if constexpr (W == WFmt::kInt4G128) {
-        // group scale of the four output rows this lane holds (rows n0 + 4g + i)
-        float sc[4];
+        if (sl + kAhead < slices) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const int r = n0 + 4 * g + i;
-          sc[i] = to_f32(reinterpret_cast<const f16_t*>(P.s)[(int64_t)(r < P.n ? r : P.n - 1) * P.s_row + grp]);
+          for (int gs = 0; gs < kSlice / 128; gs++)
+            ring[u][gs] = load_chunk<W>(P, lrow, (sl + kAhead) * (kSlice / 128) + gs, lane, n0);
         }
-#pragma unroll
-        for (int t = 0; t < MT; t++)
-#pragma unroll
-          for (int i = 0; i < 4; i++) acc[t][i] = __builtin_fmaf(part[t][i], sc[i], acc[t][i]);
+        if (sl + 1 < slices) store_x((sl + 1) & 1, xr);
+        __syncthreads();
       }
-      if (grp + 1 < groups) cur = nxt;
     }
   }
   // out[m][n]: lane holds rows n0 + 4g + i of activation row 16t + lane % 16
