@@ -25,6 +25,10 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
 constexpr int kSlice = 256;   // columns of x staged in LDS per step (two int4 groups)
+// LDS row pitch of a staged slice, in halves: 16 bytes of padding per row put the 16
+// rows that one B-operand read touches in 16 different 4-bank groups (an unpadded
+// 512-byte pitch maps them all to the same banks).
+constexpr int kPitch = kSlice + 8;
 
 enum class WFmt : int { kInt4G128 = 0, kFp8Row = 1 };
 
@@ -42,25 +46,17 @@ struct MfmaParams {
 
 // Weights of one 128-column group for this lane: row n0 + lane % 16, columns
 // 128 g + 32 (lane / 16) + [0, 32).
-// int4 chunks carry the group scales of the four output rows the lane accumulates
-// (rows n0 + 4 (lane / 16) + i), requested together with the weights.
 template <WFmt W>
 struct WChunk {
   uint32_t w[W == WFmt::kInt4G128 ? 4 : 8];
-  f16_t sc[W == WFmt::kInt4G128 ? 4 : 1];
 };
 
 template <WFmt W>
-__device__ __forceinline__ WChunk<W> load_chunk(const MfmaParams& P, int row, int grp, int lane, int n0) {
+__device__ __forceinline__ WChunk<W> load_chunk(const MfmaParams& P, int row, int grp, int lane) {
   WChunk<W> c;
   if constexpr (W == WFmt::kInt4G128) {
     const uint4 v = *reinterpret_cast<const uint4*>(P.w + (int64_t)row * P.w_row + (int64_t)grp * 64 + 16 * (lane >> 4));
     c.w[0] = v.x; c.w[1] = v.y; c.w[2] = v.z; c.w[3] = v.w;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int r = n0 + 4 * (lane >> 4) + i;
-      c.sc[i] = reinterpret_cast<const f16_t*>(P.s)[(int64_t)(r < P.n ? r : P.n - 1) * P.s_row + grp];
-    }
   } else {
     const uint4* p = reinterpret_cast<const uint4*>(P.w + (int64_t)row * P.w_row + (int64_t)grp * 128 + 32 * (lane >> 4));
     const uint4 a = p[0], b = p[1];
@@ -70,113 +66,202 @@ __device__ __forceinline__ WChunk<W> load_chunk(const MfmaParams& P, int row, in
   return c;
 }
 
-// A operand of step q (8 consecutive columns of this lane's 32) as exact fp16 values.
+// A operand of step q: the 8 weights of word q of this lane's 32 columns as fp16.
+//   int4: (c - 8) * s rounded once to fp16 (the dequantised weight), in the order
+//         the nibble decode yields them: k = 0, 4, 1, 5, 2, 6, 3, 7 of the word (the
+//         activations are staged in LDS in the same order, so the products pair up);
+//   fp8:  the exact fp16 value of each byte, natural order (row scale at the end).
 template <WFmt W>
-__device__ __forceinline__ h8 a_operand(const WChunk<W>& c, int q) {
+__device__ __forceinline__ h8 a_operand(const WChunk<W>& c, int q, h2 s2) {
   h8 a;
   if constexpr (W == WFmt::kInt4G128) {
-    _Float16 v[8];
-    decode_word8<Fmt::kInt4Sym>(c.w[q], v);
-#pragma unroll
-    for (int e = 0; e < 8; e++) a[e] = v[e];
+    h2 p0, p1, p2, p3;
+    nib_pairs(c.w[q], 8.0f, p0, p1, p2, p3);   // exact c - 8
+    p0 = p0 * s2; p1 = p1 * s2; p2 = p2 * s2; p3 = p3 * s2;
+    a[0] = p0[0]; a[1] = p0[1]; a[2] = p1[0]; a[3] = p1[1];
+    a[4] = p2[0]; a[5] = p2[1]; a[6] = p3[0]; a[7] = p3[1];
   } else {
 #pragma unroll
     for (int h = 0; h < 2; h++) {
-      const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8(c.w[2 * q + h], false);
-      const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8(c.w[2 * q + h], true);
-      a[4 * h + 0] = (_Float16)lo[0];
-      a[4 * h + 1] = (_Float16)lo[1];
-      a[4 * h + 2] = (_Float16)hi[0];
-      a[4 * h + 3] = (_Float16)hi[1];
+      const h2 lo = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(c.w[2 * q + h], 1.0f, false);
+      const h2 hi = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(c.w[2 * q + h], 1.0f, true);
+      a[4 * h + 0] = lo[0]; a[4 * h + 1] = lo[1]; a[4 * h + 2] = hi[0]; a[4 * h + 3] = hi[1];
     }
   }
   return a;
 }
 
+// Eight consecutive activations (x0 .. x7 in four dwords) reordered to the int4
+// operand order x0 x4 x1 x5 x2 x6 x3 x7.
+__device__ __forceinline__ uint4 nib_order(uint4 v) {
+  return (uint4){__builtin_amdgcn_perm(v.z, v.x, 0x05040100u), __builtin_amdgcn_perm(v.z, v.x, 0x07060302u),
+                 __builtin_amdgcn_perm(v.w, v.y, 0x05040100u), __builtin_amdgcn_perm(v.w, v.y, 0x07060302u)};
+}
+
+constexpr int kMaxGroups = 8192 / 128;   // int4 scale groups per row (cols <= 8192)
+
+// f(integral_constant<I>) for I = B .. E-1, unrolled at compile time.
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
+// Pipeline depth (slices in flight) per activation tile count: as deep as two
+// workgroups per CU (256 registers per wave) allow.
+template <bool I4, int MT> constexpr int mfma_depth() { return MT == 1 ? 8 : (MT == 2 ? 4 : (I4 ? 4 : 2)); }
+
 template <WFmt W, int MT>
-__global__ __launch_bounds__(256) void mfma_gemm_kernel(MfmaParams P) {
-  // Two LDS buffers of activation slices: slice s + 1 is loaded into registers while
-  // slice s computes, then written to the other buffer (one barrier per slice).  The
-  // weights of a slice are requested kAhead slices before they are used.
-  constexpr int kAhead = 4;
-  constexpr int XS = MT * 16 * kSlice;                 // halves per buffer
-  constexpr int XV = XS / 8 / 256;                     // 16-byte pieces per thread per slice
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void mfma_gemm_kernel(MfmaParams P) {
+  // Software pipeline of depth D slices, held in registers:
+  //   * the weights and the activations of slice s are both requested D slices
+  //     before s computes (vector loads complete in issue order, so a load issued
+  //     later than another can never be waited for earlier: both streams get the same
+  //     lead);
+  //   * the activations of slice s + 1 go from registers to one of two LDS buffers at
+  //     the end of slice s;
+  //   * the workgroup's int4 group scales are staged in LDS once ([row][group]);
+  //   * barriers order LDS only, so the global loads stay in flight across them.
+  // int4 weights enter the MFMA already scaled (fp16), so every product of a row
+  // accumulates into one fp32 tile; with a single activation tile the accumulation
+  // alternates between two tiles (summed at the end) to halve the dependency chain.
+  constexpr bool kI4 = W == WFmt::kInt4G128;
+  constexpr int kAhead = mfma_depth<kI4, MT>();
+  constexpr int NA = MT == 1 ? 2 : 1;                  // accumulator tiles per activation tile
+  constexpr int XS = MT * 16 * kPitch;                 // halves per buffer
+  constexpr int XV = MT * 16 * kSlice / 8 / 256;       // 16-byte pieces per thread per slice
+  constexpr int GPS = kSlice / 128;                    // quantisation groups per slice
   __shared__ __attribute__((aligned(16))) uint16_t xs[2 * XS];
+  __shared__ __attribute__((aligned(16))) uint16_t scl[kI4 ? kMaxGroups * 64 : 4];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int n0 = (blockIdx.x * 4 + wave) * 16;
+  const int nb = blockIdx.x * 64;
+  const int n0 = nb + wave * 16;
   const int arow = n0 + (lane & 15);                 // weight row this lane loads (A operand)
   const int lrow = arow < P.n ? arow : P.n - 1;
   const int g = lane >> 4;
   const int slices = P.k / kSlice;
-  auto load_x = [&](int sl, uint4* regs) {
+  const int groups = P.k / 128;
+  // Every load below is unconditional (indices are clamped) so the compiler keeps
+  // exact outstanding-load counts across the unrolled pipeline; rows of x past m and
+  // slices past the end are loaded again, and only feed outputs that are not stored.
+  // activation slot u: xq_even / xq_odd[(u / 2) * XV + v] (two arrays: smaller
+  // private arrays are the ones the compiler keeps in registers)
+  uint4 xq_even[kAhead / 2 * XV], xq_odd[kAhead / 2 * XV];
+  auto load_x = [&](int sl, auto uc) __attribute__((always_inline)) {
+    constexpr int u = decltype(uc)::value;
+#pragma unroll
+    for (int v = 0; v < XV; v++) {
+      const int i = threadIdx.x + 256 * v;
+      int r = i / (kSlice / 8);
+      const int c8 = i - r * (kSlice / 8);
+      r = r < P.m ? r : P.m - 1;
+      const uint4 t = *reinterpret_cast<const uint4*>(P.x + (int64_t)r * P.x_row + (int64_t)sl * kSlice + 8 * c8);
+      if constexpr ((u & 1) == 0) xq_even[u / 2 * XV + v] = t;
+      else xq_odd[u / 2 * XV + v] = t;
+    }
+  };
+  auto store_x = [&](int buf, auto uc) __attribute__((always_inline)) {
+    constexpr int u = decltype(uc)::value;
 #pragma unroll
     for (int v = 0; v < XV; v++) {
       const int i = threadIdx.x + 256 * v;
       const int r = i / (kSlice / 8), c8 = i - r * (kSlice / 8);
-      regs[v] = r < P.m ? *reinterpret_cast<const uint4*>(P.x + (int64_t)r * P.x_row + (int64_t)sl * kSlice + 8 * c8)
-                        : (uint4){0u, 0u, 0u, 0u};
+      uint4 t = (u & 1) == 0 ? xq_even[u / 2 * XV + v] : xq_odd[u / 2 * XV + v];
+      if constexpr (kI4) t = nib_order(t);
+      *reinterpret_cast<uint4*>(xs + buf * XS + r * kPitch + 8 * c8) = t;
     }
   };
-  auto store_x = [&](int buf, const uint4* regs) {
+  f4 acc[NA][MT];
 #pragma unroll
-    for (int v = 0; v < XV; v++) {
-      const int i = threadIdx.x + 256 * v;
-      const int r = i / (kSlice / 8), c8 = i - r * (kSlice / 8);
-      *reinterpret_cast<uint4*>(xs + buf * XS + r * kSlice + 8 * c8) = regs[v];
-    }
-  };
-  f4 acc[MT];
+  for (int j = 0; j < NA; j++)
 #pragma unroll
-  for (int t = 0; t < MT; t++) acc[t] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
-  WChunk<W> ring[kAhead][kSlice / 128];
+    for (int t = 0; t < MT; t++) acc[j][t] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
+  WChunk<W> ring[kAhead][GPS];
 #pragma unroll
   for (int u = 0; u < kAhead; u++)
-    if (u < slices)
 #pragma unroll
-      for (int gs = 0; gs < kSlice / 128; gs++) ring[u][gs] = load_chunk<W>(P, lrow, u * (kSlice / 128) + gs, lane, n0);
-  uint4 xr[XV];
-  load_x(0, xr);
-  store_x(0, xr);
-  __syncthreads();
-  for (int s0 = 0; s0 < slices; s0 += kAhead) {
+    for (int gs = 0; gs < GPS; gs++) ring[u][gs] = load_chunk<W>(P, lrow, (u < slices ? u : slices - 1) * GPS + gs, lane);
+  static_for<0, kAhead>([&](auto uc) __attribute__((always_inline)) {
+    load_x(decltype(uc)::value < slices ? decltype(uc)::value : slices - 1, uc);
+  });
+  if constexpr (kI4) {
+    // thread t stages row t / 4, groups t % 4 + 4 j, into scl[row * groups + group]
+    const int r = threadIdx.x >> 2;
+    const int row = nb + r < P.n ? nb + r : P.n - 1;
+    const uint16_t* sg = reinterpret_cast<const uint16_t*>(P.s) + (int64_t)row * P.s_row;
+    uint16_t sv[kMaxGroups / 4];
 #pragma unroll
-    for (int u = 0; u < kAhead; u++) {
-      const int sl = s0 + u;
-      if (sl < slices) {
-        if (sl + 1 < slices) load_x(sl + 1, xr);
-        const uint16_t* xb = xs + (sl & 1) * XS;
+    for (int j = 0; j < kMaxGroups / 4; j++) {
+      const int gi = (threadIdx.x & 3) + 4 * j;
+      sv[j] = sg[gi < groups ? gi : groups - 1];
+    }
 #pragma unroll
-        for (int gs = 0; gs < kSlice / 128; gs++) {
-          f4 part[MT];
+    for (int j = 0; j < kMaxGroups / 4; j++) {
+      const int gi = (threadIdx.x & 3) + 4 * j;
+      if (gi < groups) scl[r * groups + gi] = sv[j];
+    }
+  }
+  store_x(0, std::integral_constant<int, 0>{});
+  lds_barrier();
+
+  const uint16_t* my_scl = scl + (wave * 16 + (lane & 15)) * groups;
+  auto step = [&](int sl, auto uc) __attribute__((always_inline)) {
+    constexpr int u = decltype(uc)::value;
+    const uint16_t* xl = xs + (u & 1) * XS;
+    // this lane's row scales of the slice's two groups, as (s, s) pairs
+    h2 s2[GPS];
+    if constexpr (kI4) {
 #pragma unroll
-          for (int t = 0; t < MT; t++) part[t] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-          for (int q = 0; q < 4; q++) {
-            const h8 a = a_operand<W>(ring[u][gs], q);
-#pragma unroll
-            for (int t = 0; t < MT; t++) {
-              const h8 b = *reinterpret_cast<const h8*>(xb + (16 * t + (lane & 15)) * kSlice + 128 * gs + 32 * g + 8 * q);
-              if constexpr (W == WFmt::kInt4G128) part[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, part[t], 0, 0, 0);
-              else acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[t], 0, 0, 0);
-            }
-          }
-          if constexpr (W == WFmt::kInt4G128) {
-            // group scale of the four output rows this lane holds (rows n0 + 4g + i)
-#pragma unroll
-            for (int t = 0; t < MT; t++)
-#pragma unroll
-              for (int i = 0; i < 4; i++) acc[t][i] = __builtin_fmaf(part[t][i], to_f32(ring[u][gs].sc[i]), acc[t][i]);
-          }
-        }
-        if (sl + kAhead < slices) {
-#pragma unroll
-          for (int gs = 0; gs < kSlice / 128; gs++)
-            ring[u][gs] = load_chunk<W>(P, lrow, (sl + kAhead) * (kSlice / 128) + gs, lane, n0);
-        }
-        if (sl + 1 < slices) store_x((sl + 1) & 1, xr);
-        __syncthreads();
+      for (int gs = 0; gs < GPS; gs++) {
+        const _Float16 sc = __builtin_bit_cast(_Float16, my_scl[sl * GPS + gs]);
+        s2[gs] = (h2){sc, sc};
       }
     }
+    // B operands of a group are read from LDS together, the next group's while the
+    // current one's MFMAs run (with one wave per SIMD nothing else hides LDS latency)
+    h8 bb[GPS][4][MT];
+    auto read_b = [&](int gs) __attribute__((always_inline)) {
+#pragma unroll
+      for (int q = 0; q < 4; q++)
+#pragma unroll
+        for (int t = 0; t < MT; t++)
+          bb[gs][q][t] = *reinterpret_cast<const h8*>(xl + (16 * t + (lane & 15)) * kPitch + 128 * gs + 32 * g + 8 * q);
+    };
+    read_b(0);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int gs = 0; gs < GPS; gs++) {
+      if (gs + 1 < GPS) read_b(gs + 1);
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const h8 a = a_operand<W>(ring[u][gs], q, kI4 ? s2[gs] : (h2){});
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+          f4& d = acc[NA == 2 ? (q & 1) : 0][t];
+          d = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bb[gs][q][t], d, 0, 0, 0);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    const int nx = sl + kAhead < slices ? sl + kAhead : slices - 1;
+#pragma unroll
+    for (int gs = 0; gs < GPS; gs++) ring[u][gs] = load_chunk<W>(P, lrow, nx * GPS + gs, lane);
+    load_x(nx, uc);                                                  // slot u held slice sl, stored a step ago
+    store_x((u + 1) & 1, std::integral_constant<int, (u + 1) % kAhead>{});  // slice sl + 1
+    lds_barrier();
+  };
+  int s0 = 0;
+  for (; s0 + kAhead <= slices; s0 += kAhead)
+    static_for<0, kAhead>([&](auto uc) __attribute__((always_inline)) { step(s0 + decltype(uc)::value, uc); });
+  // tail: fewer than kAhead slices, still with static ring slots
+  static_for<0, kAhead - 1>([&](auto uc) __attribute__((always_inline)) {
+    if (s0 + decltype(uc)::value < slices) step(s0 + decltype(uc)::value, uc);
+  });
+  if constexpr (NA == 2) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) acc[0][0][i] = acc[0][0][i] + acc[1][0][i];
   }
   // out[m][n]: lane holds rows n0 + 4g + i of activation row 16t + lane % 16
 #pragma unroll
@@ -189,7 +274,7 @@ __global__ __launch_bounds__(256) void mfma_gemm_kernel(MfmaParams P) {
     for (int t = 0; t < MT; t++) {
       const int m = 16 * t + (lane & 15);
       if (m < P.m) {
-        const float v = W == WFmt::kFp8Row ? acc[t][i] * rs : acc[t][i];
+        const float v = W == WFmt::kFp8Row ? acc[0][t][i] * rs : acc[0][t][i];
         P.out[(int64_t)m * P.out_row + r] = f32_to_f16_bits(v);
       }
     }

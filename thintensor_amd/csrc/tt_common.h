@@ -165,6 +165,15 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t k) {
   return k;
 }
 
+// Workgroup barrier that orders LDS accesses only.  __syncthreads() also waits for
+// every outstanding global load of the wave, which would drain a register prefetch
+// pipeline at each barrier; this one leaves those loads in flight.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 template <typename T> __device__ __forceinline__ float ld(const void* p, int64_t i) {
   return to_f32(reinterpret_cast<const T*>(p)[i]);
 }
