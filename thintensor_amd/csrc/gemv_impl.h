@@ -161,10 +161,12 @@ __device__ __forceinline__ int paired_row(int v, int kind, int head_dim, bool& o
   return h * head_dim + j + (odd ? half : 0);
 }
 
+// One round's loads.  Scales stay in their storage type until the round is consumed,
+// so issuing a fetch never waits for a load to return.
 template <Fmt F, typename ST, int ROWS, int NVG>
 struct GemvData {
   Raw<FmtInfo<F>::kBytes> w[ROWS];
-  float s[NVG], m[NVG];
+  ST s[NVG], m[NVG];
   int e[ROWS];
 };
 
@@ -270,8 +272,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
 #pragma unroll
       for (int k = 0; k < NVG; k++) {
         const int64_t off = bt.soffs[k] + (int64_t)(j / LG) * bt.s_grp;
-        d.s[k] = to_f32(bt.sb[off]);
-        if constexpr (SM == SMode::kGroupAff) d.m[k] = to_f32(bt.sb[off + P.s_pair]);
+        d.s[k] = bt.sb[off];
+        if constexpr (SM == SMode::kGroupAff) d.m[k] = bt.sb[off + P.s_pair];
       }
     }
     if constexpr (SM == SMode::kBlockE8) {
@@ -280,25 +282,50 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
     }
   };
 
+  // Activation loads are issued before the weight fetch and written to LDS once they
+  // return, so a wave waits for memory once (weights, scales and x in flight together).
+  // Piece idx (16 bytes) of the staged activations is piece idx - m * xn of row m; the
+  // first 256 * kXR pieces go through registers, with indices clamped to the last piece
+  // (duplicate loads and stores of the same value) so that no branch separates them.
+  constexpr int kXR = 4;                  // 16-byte activation pieces per thread in registers
+  const int xn = P.cols >> 3;             // 16-byte pieces per activation row
+  const int xtotal = xn * MR;
+  uint4 xreg[kXR];
+  int xidx[kXR];
+  if constexpr (PRO == Pro::kLoad) {
+#pragma unroll
+    for (int k = 0; k < kXR; k++) {
+      const int idx = threadIdx.x + 256 * k;
+      xidx[k] = idx < xtotal ? idx : xtotal - 1;
+      const int m = MR == 1 ? 0 : xidx[k] / xn;
+      const uint4* xg = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(P.x) +
+                                                       (int64_t)(slot + m) * P.x_slot);
+      xreg[k] = xg[xidx[k] - m * xn];
+    }
+  }
+
   int b = blockIdx.x * (blockDim.x >> 6) + wave;
   Batch cb;
   setup(b, cb);
   // PF == 1: one round in flight ahead of the one being computed.  PF > 1 (rounds <=
   // PF): every round of the next batch is fetched while the current batch computes.
+  // The first fetch is unconditional: an inactive batch (past the last row) clamps every
+  // row to the last row of the last segment, so its loads stay in bounds, and round 0
+  // always exists (the host requires cols >= 32).
   Data cd[PF];
-  if (cb.active) {
 #pragma unroll
-    for (int r = 0; r < PF; r++)
-      if (r < rounds) fetch(cb, r, cd[r]);
-  }
+  for (int r = 0; r < PF; r++)
+    if (r == 0 || r < rounds) fetch(cb, r, cd[r]);
   if constexpr (PRO == Pro::kLoad) {
-    // Stage the activation vector(s) while the first weight loads are in flight.
+    // LDS holds activation row m at uint4 offset m * xn.
+    uint4* xl = reinterpret_cast<uint4*>(xs_lds);
 #pragma unroll
-    for (int m = 0; m < MR; m++) {
-      const uint4* xg =
-          reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(P.x) + (int64_t)(slot + m) * P.x_slot);
-      uint4* xl = reinterpret_cast<uint4*>(xs_lds + m * (P.cols >> 1));
-      for (int i = threadIdx.x; i < (P.cols >> 3); i += blockDim.x) xl[i] = xg[i];
+    for (int k = 0; k < kXR; k++) xl[xidx[k]] = xreg[k];
+    for (int idx = threadIdx.x + 256 * kXR; idx < xtotal; idx += 256) {
+      const int m = MR == 1 ? 0 : idx / xn;
+      const uint4* xg = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(P.x) +
+                                                       (int64_t)(slot + m) * P.x_slot);
+      xl[idx] = xg[idx - m * xn];
     }
     __syncthreads();
   } else {
@@ -327,13 +354,34 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
     };
     constexpr int kHeld = 16;   // elements per thread kept in registers (cols <= 4096)
     if (n <= 256 * kHeld) {
-      // one pass over memory: residual and weight loads issued together
-      float rr[kHeld], wn[kHeld];
+      // one pass over memory: every residual and weight load is issued before any is
+      // used (indices past n clamp to n - 1 and their values are discarded), so the
+      // prologue waits for memory once
+      uint16_t ra[kHeld], rb[kHeld], rw[kHeld];
+      const uint16_t* pa = PRO == Pro::kEmbedNorm ? reinterpret_cast<const uint16_t*>(erow)
+                                                  : reinterpret_cast<const uint16_t*>(P.f.left);
+      const uint16_t* pb = reinterpret_cast<const uint16_t*>(P.f.right);
+      const uint16_t* pw = reinterpret_cast<const uint16_t*>(P.f.norm_w);
 #pragma unroll
       for (int k = 0; k < kHeld; k++) {
         const int i = threadIdx.x + 256 * k;
-        rr[k] = i < n ? resid(i) : 0.0f;
-        wn[k] = i < n ? ld<XT>(P.f.norm_w, i) : 0.0f;
+        const int ic = i < n ? i : n - 1;
+        ra[k] = pa[ic];
+        if constexpr (PRO != Pro::kEmbedNorm) rb[k] = pb[ic];
+        rw[k] = pw[ic];
+      }
+      __builtin_amdgcn_sched_barrier(0);   // raw bits only above: no use between the loads
+      float rr[kHeld], wn[kHeld];
+#pragma unroll
+      for (int k = 0; k < kHeld; k++) {
+        const bool in = threadIdx.x + 256 * k < n;
+        const float a = to_f32(XT{ra[k]});
+        float r;
+        if constexpr (PRO == Pro::kAddNorm) r = round_bf16(a + to_f32(XT{rb[k]}));
+        else if constexpr (PRO == Pro::kAddRmsNorm) r = round_to<XT>(a + to_f32(XT{rb[k]}));
+        else r = a;
+        rr[k] = in ? r : 0.0f;
+        wn[k] = in ? to_f32(XT{rw[k]}) : 0.0f;
       }
       float ss = 0.0f;
 #pragma unroll
@@ -410,12 +458,13 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
 #pragma unroll
         for (int k = 0; k < NVG; k++) {
           float t;
+          const float sk = to_f32(d.s[k]);
           if constexpr (SM == SMode::kGroupAff) {
-            float m = d.m[k];
-            if (P.aff_zero) m = -(m * d.s[k]);
-            t = __builtin_fmaf(xsum, m, p[k] * d.s[k]);
+            float m = to_f32(d.m[k]);
+            if (P.aff_zero) m = -(m * sk);
+            t = __builtin_fmaf(xsum, m, p[k] * sk);
           } else {
-            t = p[k] * d.s[k];
+            t = p[k] * sk;
           }
           const bool ok = cv && (bt.lr0 + grow[k] < bt.rows);
           acc[k] = acc[k] + (ok ? t : 0.0f);

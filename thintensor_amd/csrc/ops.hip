@@ -13,10 +13,41 @@ namespace tt {
 // ---------------------------------------------------------------- RMSNorm
 // out_i = (x_i * (1 / sqrt(mean(x^2) + eps))) * (w_i + offset); sum of squares per
 // thread is an fma chain over elements t, t+256, ... (triton_kernels.py:2562-2577).
+// Vectors of up to kNormHeld * 256 elements are held in registers: every load is issued
+// before the first one is used (indices past n clamp to n - 1, their values discarded),
+// so the kernel waits for memory once instead of once per element.
+constexpr int kNormHeld = 16;
+
 template <typename XT, typename WT, typename OT>
 __global__ __launch_bounds__(256) void rms_norm_kernel(const void* x, const void* w, void* out, int n, float eps,
                                                        float offset) {
   __shared__ float red[4];
+  if (n <= 256 * kNormHeld) {
+    XT xr[kNormHeld];
+    WT wr[kNormHeld];
+#pragma unroll
+    for (int k = 0; k < kNormHeld; k++) {
+      const int i = threadIdx.x + 256 * k;
+      const int ic = i < n ? i : n - 1;
+      xr[k] = reinterpret_cast<const XT*>(x)[ic];
+      wr[k] = reinterpret_cast<const WT*>(w)[ic];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kNormHeld; k++) {
+      const float v = to_f32(xr[k]);
+      if (threadIdx.x + 256 * k < n) s = __builtin_fmaf(v, v, s);
+    }
+    const float total = block_sum256(s, red);
+    const float inv = 1.0f / __builtin_sqrtf(total / (float)n + eps);
+#pragma unroll
+    for (int k = 0; k < kNormHeld; k++) {
+      const int i = threadIdx.x + 256 * k;
+      if (i < n) store<OT>(reinterpret_cast<OT*>(out) + i, (to_f32(xr[k]) * inv) * (to_f32(wr[k]) + offset));
+    }
+    return;
+  }
   float s = 0.0f;
   for (int i = threadIdx.x; i < n; i += 256) {
     const float v = ld<XT>(x, i);
@@ -34,6 +65,37 @@ template <typename XT, typename WT, typename OT>
 __global__ __launch_bounds__(256) void add_rms_norm_kernel(const void* left, const void* right, void* residual_out,
                                                            const void* w, void* out, int n, float eps) {
   __shared__ float red[4];
+  if (n <= 256 * kNormHeld) {
+    XT lr[kNormHeld], rr[kNormHeld];
+    WT wr[kNormHeld];
+#pragma unroll
+    for (int k = 0; k < kNormHeld; k++) {
+      const int i = threadIdx.x + 256 * k;
+      const int ic = i < n ? i : n - 1;
+      lr[k] = reinterpret_cast<const XT*>(left)[ic];
+      rr[k] = reinterpret_cast<const XT*>(right)[ic];
+      wr[k] = reinterpret_cast<const WT*>(w)[ic];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float res[kNormHeld];
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kNormHeld; k++) {
+      res[k] = round_bf16(to_f32(lr[k]) + to_f32(rr[k]));
+      if (threadIdx.x + 256 * k < n) s = __builtin_fmaf(res[k], res[k], s);
+    }
+    const float total = block_sum256(s, red);
+    const float inv = 1.0f / __builtin_sqrtf(total / (float)n + eps);
+#pragma unroll
+    for (int k = 0; k < kNormHeld; k++) {
+      const int i = threadIdx.x + 256 * k;
+      if (i < n) {
+        store<XT>(reinterpret_cast<XT*>(residual_out) + i, res[k]);
+        store<OT>(reinterpret_cast<OT*>(out) + i, (res[k] * inv) * to_f32(wr[k]));
+      }
+    }
+    return;
+  }
   float s = 0.0f;
   for (int i = threadIdx.x; i < n; i += 256) {
     const float r = norm_residual<XT>(left, right, i);
