@@ -721,6 +721,9 @@ static int launch_int4_g128(int lpr, int rows_per_wave, int prefetch, const Gemv
                             const char* what) {
   constexpr Fmt F = Fmt::kInt4Sym;
   constexpr SMode SM = SMode::kGroup;
+  // whole-batch prefetch holds every round of a batch in registers
+  TT_REQUIRE(prefetch == 1 || (P.cols / 32 + lpr - 1) / lpr <= prefetch, "%s: prefetch %d below the rounds per row",
+             what, prefetch);
   if (rows_per_wave == 4) return launch_lpr<F, SM, XT, OT, f16_t, 4, 4, PRO, EPI, 1>(lpr, P, 1, st, what);
   if (rows_per_wave == 2) {
     if (prefetch == 4) return launch_lpr<F, SM, XT, OT, f16_t, 2, 4, PRO, EPI, 4>(lpr, P, 1, st, what);

@@ -3,6 +3,229 @@
 
 using namespace tt;
 
+namespace {
+
+// Symmetric int4, fp16 group-128 scales: the single-matrix GEMV of the decode hot path.
+// Same reduction order as gemv_kernel (chunk j on lane j mod LPR in round j div LPR,
+// group butterflies over 4 lanes, scaled sums accumulated in round order, row
+// butterfly over the remaining lane bits), without its segment / expert / epilogue
+// machinery: one batch of ROWS * (64 / LPR) rows per wave and a short argument list.
+// Row bases are wave-uniform scalars and every per-lane offset is 32-bit (the host
+// keeps each operand under 4 GiB), so addressing costs almost no vector work.  The
+// weight, scale and activation loads of round 0 are issued before the first wait;
+// later rounds are fetched one ahead.  Activation staging XM: 0 = one copy per
+// workgroup in LDS behind a barrier; 1 = each lane reads its chunk from global memory;
+// 2 = each wave stages the whole vector in its own LDS slice with coalesced loads
+// (no workgroup barrier; a wave's LDS accesses complete in order).
+template <typename XT, int LPR, int ROWS, int XM>
+__global__ __launch_bounds__(256) void int4g128_kernel(const uint8_t* __restrict__ W, uint32_t w_row,
+                                                       const f16_t* __restrict__ S, uint32_t s_row, uint32_t s_grp,
+                                                       const uint16_t* __restrict__ x, XT* __restrict__ y, int rows,
+                                                       int cols) {
+  constexpr int L = 4;                       // 32-element chunks per group of 128
+  constexpr int SUBS = 64 / LPR;
+  constexpr int NVG = ROWS / L > 0 ? ROWS / L : 1;
+  constexpr int GLEV = log2c(L) < log2c(ROWS) ? log2c(L) : log2c(ROWS);
+  constexpr int kXR = 4;                     // 16-byte activation pieces per thread via registers
+  extern __shared__ uint32_t xs_lds[];
+  const int lane = threadIdx.x & 63;
+  const int sub = lane / LPR;
+  const int l = lane % LPR;
+  const int nchunks = cols >> 5;
+  const int rounds = (nchunks + LPR - 1) / LPR;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int row0 = (int)(blockIdx.x * 4 + wave) * (ROWS * SUBS);   // wave-uniform
+
+  // activation pieces for LDS (clamped indices: duplicates of the last piece, no branch)
+  const int xn = cols >> 3;
+  uint4 xreg[kXR];
+  uint32_t xidx[kXR];
+  constexpr bool XG = XM == 1;
+  constexpr int kXW = 4;                     // pieces per lane when a wave stages its own copy
+  uint4 xwreg[kXW];
+  uint32_t xwidx[kXW];
+  if constexpr (XM == 0) {
+#pragma unroll
+    for (int k = 0; k < kXR; k++) {
+      const int idx = threadIdx.x + 256 * k;
+      xidx[k] = idx < xn ? idx : xn - 1;
+      xreg[k] = reinterpret_cast<const uint4*>(x)[xidx[k]];
+    }
+  } else if constexpr (XM == 2) {
+#pragma unroll
+    for (int k = 0; k < kXW; k++) {
+      const int idx = lane + 64 * k;
+      xwidx[k] = idx < xn ? idx : xn - 1;
+      xwreg[k] = reinterpret_cast<const uint4*>(x)[xwidx[k]];
+    }
+  }
+
+  // weights: row i of lane group `sub` is row0 + i * SUBS + sub (clamped to the last row)
+  const uint8_t* wrow[ROWS];
+  bool rv[ROWS];
+#pragma unroll
+  for (int i = 0; i < ROWS; i++) {
+    const int r0 = row0 + i * SUBS;                       // lane group 0's row (uniform)
+    const int rc = r0 < rows - 1 ? r0 : rows - 1;
+    wrow[i] = W + (size_t)rc * w_row;
+    rv[i] = r0 + sub < rows;
+  }
+  // per-lane part: sub * w_row for the lane's group (0 when one row spans the wave),
+  // clamped so the last rows never step past the matrix
+  uint32_t wlane[ROWS];
+#pragma unroll
+  for (int i = 0; i < ROWS; i++) {
+    const int r0 = row0 + i * SUBS;
+    const int rc = r0 < rows - 1 ? r0 : rows - 1;
+    const int rl = r0 + sub < rows ? r0 + sub : rows - 1;
+    wlane[i] = SUBS == 1 ? 0u : (uint32_t)(rl - rc) * w_row;
+  }
+  // scales: value k of this lane belongs to batch row rs_row(l, GLEV, k) * SUBS + sub
+  const f16_t* sbase = S + (size_t)(row0 < rows ? row0 : rows - 1) * s_row;
+  uint32_t soff[NVG];
+  bool sv[NVG];
+#pragma unroll
+  for (int k = 0; k < NVG; k++) {
+    const int r = row0 + rs_row<ROWS>(l, GLEV, k) * SUBS + sub;
+    sv[k] = r < rows;
+    soff[k] = (uint32_t)((sv[k] ? r : rows - 1) - (row0 < rows ? row0 : rows - 1)) * s_row;
+  }
+  auto fetch = [&](int r, Raw<16>* w, f16_t* sc, uint4* xc) {
+    uint32_t j = (uint32_t)(r * LPR + l);
+    j = j < (uint32_t)nchunks ? j : (uint32_t)nchunks - 1;
+#pragma unroll
+    for (int i = 0; i < ROWS; i++) w[i] = load_raw<16>(wrow[i] + (wlane[i] + j * 16u));
+    if constexpr (XG) {
+#pragma unroll
+      for (int q = 0; q < 4; q++) xc[q] = *reinterpret_cast<const uint4*>(x + (j * 32u + 8u * q));
+    }
+#pragma unroll
+    for (int k = 0; k < NVG; k++) sc[k] = sbase[soff[k] + (j >> 2) * s_grp];
+  };
+  Raw<16> wc[ROWS];
+  f16_t sc[NVG];
+  uint4 xc[4];
+  fetch(0, wc, sc, xc);
+
+  uint32_t* xs = xs_lds;                     // this wave's activation copy
+  if constexpr (XM == 0) {
+    uint4* xl = reinterpret_cast<uint4*>(xs_lds);
+#pragma unroll
+    for (int k = 0; k < kXR; k++) xl[xidx[k]] = xreg[k];
+    for (int idx = threadIdx.x + 256 * kXR; idx < xn; idx += 256) xl[idx] = reinterpret_cast<const uint4*>(x)[idx];
+    lds_barrier();
+  } else if constexpr (XM == 2) {
+    xs = xs_lds + wave * (cols >> 1);
+    uint4* xl = reinterpret_cast<uint4*>(xs);
+#pragma unroll
+    for (int k = 0; k < kXW; k++) xl[xwidx[k]] = xwreg[k];
+    for (int idx = lane + 64 * kXW; idx < xn; idx += 64) xl[idx] = reinterpret_cast<const uint4*>(x)[idx];
+  }
+
+  float acc[NVG];
+#pragma unroll
+  for (int k = 0; k < NVG; k++) acc[k] = 0.0f;
+  // do-while: the host guarantees one round (cols >= 32), and no loop-entry test keeps
+  // every argument load in the one scalar batch at the top
+  int r = 0;
+  do {
+    Raw<16> wn[ROWS];
+    f16_t sn[NVG];
+    uint4 xnx[4];
+    const bool more = r + 1 < rounds;
+    if (more) fetch(r + 1, wn, sn, xnx);
+    const int j = r * LPR + l;
+    const bool cv = j < nchunks;
+    uint32_t xw[16];
+    {
+      const uint4* xp = reinterpret_cast<const uint4*>(xs + (cv ? j : 0) * 16);
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const uint4 v = XG ? xc[q] : xp[q];
+        xw[4 * q] = v.x; xw[4 * q + 1] = v.y; xw[4 * q + 2] = v.z; xw[4 * q + 3] = v.w;
+      }
+    }
+    float p[ROWS];
+    chunk_dot_rows<Fmt::kInt4Sym, XT, ROWS>(wc, xw, p);
+#pragma unroll
+    for (int i = 0; i < ROWS; i++) p[i] = (cv && rv[i]) ? p[i] : 0.0f;
+    reduce_range<ROWS, 1, L>(p);
+#pragma unroll
+    for (int k = 0; k < NVG; k++) {
+      const float t = p[k] * to_f32(sc[k]);
+      acc[k] = acc[k] + ((cv && sv[k]) ? t : 0.0f);
+    }
+    if (more) {
+#pragma unroll
+      for (int i = 0; i < ROWS; i++) wc[i] = wn[i];
+#pragma unroll
+      for (int k = 0; k < NVG; k++) sc[k] = sn[k];
+      if constexpr (XG) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) xc[q] = xnx[q];
+      }
+    }
+  } while (++r < rounds);
+  reduce_range<NVG, L, LPR>(acc);
+  const int frow = row0 + rs_row<ROWS>(l, log2c(ROWS), 0) * SUBS + sub;
+  if ((l >> log2c(ROWS)) == 0 && frow < rows) store<XT>(y + frow, acc[0]);
+}
+
+// Activation staging mode (see int4g128_kernel).
+inline int int4g128_x_mode(int64_t rows, int64_t cols, int lpr) { return cols / 32 <= lpr ? 1 : 0; }
+
+template <typename XT, int LPR>
+int launch_int4g128_lpr(int rpw, const void* W, int64_t w_row, const void* S, int64_t s_row, int64_t s_grp,
+                        const void* x, void* y, int rows, int cols, hipStream_t st) {
+  const int per_wave = rpw * (64 / LPR);
+  const int64_t waves = ((int64_t)rows + per_wave - 1) / per_wave;
+  const dim3 grid((unsigned)((waves + 3) / 4));
+  const auto* w = static_cast<const uint8_t*>(W);
+  const auto* s = static_cast<const f16_t*>(S);
+  const auto* xv = static_cast<const uint16_t*>(x);
+  auto* yv = static_cast<XT*>(y);
+  const int xm = int4g128_x_mode(rows, cols, LPR);
+  const size_t lds = xm == 1 ? 0 : (size_t)cols * 2 * (xm == 2 ? 4 : 1);
+  const uint32_t wr = (uint32_t)w_row, sr = (uint32_t)s_row, sg = (uint32_t)s_grp;
+#define TT_INT4G_LAUNCH(R, M) \
+  hipLaunchKernelGGL((int4g128_kernel<XT, LPR, R, M>), grid, dim3(256), lds, st, w, wr, s, sr, sg, xv, yv, rows, cols)
+#define TT_INT4G_MODES(R) \
+  if (xm == 1) TT_INT4G_LAUNCH(R, 1); else if (xm == 2) TT_INT4G_LAUNCH(R, 2); else TT_INT4G_LAUNCH(R, 0);
+  if (rpw == 4) { TT_INT4G_MODES(4) }
+  else if (rpw == 2) { TT_INT4G_MODES(2) }
+  else { TT_INT4G_MODES(1) }
+#undef TT_INT4G_MODES
+#undef TT_INT4G_LAUNCH
+  return check_launch("int4_scaled_matvec");
+}
+
+// Rows per wave of the single-matrix path: enough waves to cover the chip several
+// times over before a wave takes more than one row.
+inline int int4g128_rows_per_wave(int64_t rows, int lpr) {
+  const int64_t groups = rows * lpr / 64;   // lane groups needed at one row each
+  if (groups >= 16384) return 4;
+  if (groups >= 2048) return 2;
+  return 1;
+}
+
+// The lean kernel addresses each operand with 32-bit offsets.
+inline bool int4g128_fits(int64_t rows, int64_t w_row, int64_t s_row, int64_t s_grp, int64_t cols) {
+  const int64_t lim = (int64_t)1 << 31;
+  return w_row > 0 && s_row >= 0 && s_grp >= 0 && rows * w_row < lim && (rows * s_row + cols / 128 * s_grp) * 2 < lim &&
+         cols * 2 < lim;
+}
+
+template <typename XT>
+int launch_int4g128(int lpr, const void* W, int64_t w_row, const void* S, int64_t s_row, int64_t s_grp, const void* x,
+                    void* y, int rows, int cols, hipStream_t st) {
+  const int rpw = int4g128_rows_per_wave(rows, lpr);
+  if (lpr == 64) return launch_int4g128_lpr<XT, 64>(rpw, W, w_row, S, s_row, s_grp, x, y, rows, cols, st);
+  if (lpr == 32) return launch_int4g128_lpr<XT, 32>(rpw, W, w_row, S, s_row, s_grp, x, y, rows, cols, st);
+  return launch_int4g128_lpr<XT, 16>(rpw, W, w_row, S, s_row, s_grp, x, y, rows, cols, st);
+}
+
+}  // namespace
+
 extern "C" int tt_gemv_lanes_per_row(int64_t chunks, int64_t group_chunks) {
   if (chunks <= 0) return 0;
   int best = 0;
@@ -80,6 +303,15 @@ extern "C" int tt_multi_int4_scaled_matvec(int count, const void* const* packed,
   if (row_mode) {
     if (scale_dtype == TT_F16) return launch_types<Fmt::kInt4Sym, SMode::kRow, f16_t, 4>(x_dtype, out_dtype, Lg, lpr, P, 1, st, what);
     return launch_types<Fmt::kInt4Sym, SMode::kRow, float, 4>(x_dtype, out_dtype, Lg, lpr, P, 1, st, what);
+  }
+  if (count == 1 && scale_dtype == TT_F16 && Lg == 4 && x_dtype == out_dtype && (lpr == 64 || lpr == 32 || lpr == 16) &&
+      int4g128_fits(rows[0], w_row_bytes[0], s_row[0], s_group[0], cols)) {
+    // one matrix, group 128, fp16 scales: the lean single-matrix kernel
+    if (x_dtype == TT_F16)
+      return launch_int4g128<f16_t>(lpr, packed[0], w_row_bytes[0], scales[0], s_row[0], s_group[0], x, out,
+                                    (int)rows[0], (int)cols, st);
+    return launch_int4g128<bf16_t>(lpr, packed[0], w_row_bytes[0], scales[0], s_row[0], s_group[0], x, out,
+                                   (int)rows[0], (int)cols, st);
   }
   if (scale_dtype == TT_F16 && Lg == 4 && x_dtype == out_dtype) {
     // the decode hot path (group 128, fp16 scales): launch shape chosen from the matrix
