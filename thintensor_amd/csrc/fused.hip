@@ -11,6 +11,332 @@ namespace {
 
 constexpr const char* kWhat = "fused_gemv";
 
+// ----------------------------------------------------------------------------
+// Lean fused int4 g128 GEMV of the decode step: one batch of ROWS * (64 / LPR) virtual
+// rows per wave (segments padded to whole batches, as in gemv_kernel), the RMSNorm
+// prologue and the RoPE / KV-cache / SiLU epilogues of gemv_kernel with the same
+// row pairing, rounding points and reduction order, without its persistent loop.
+// The weight and scale loads of round 0 are issued before the prologue's loads, so
+// the prologue's memory wait overlaps the weight stream.
+struct LeanSeg {
+  const uint8_t* w;     // weights (kSegSilu: gate rows)
+  const uint8_t* w2;    // kSegSilu: up rows
+  const f16_t* s;
+  const f16_t* s2;
+  void* out;
+  uint32_t w_row, s_row;
+  int rows;             // virtual rows (kSegSilu: 2 x activation rows)
+  int vbegin;
+  int kind;
+};
+
+struct LeanFused {
+  LeanSeg seg[3];
+  int nseg, vtotal, cols, head_dim;
+  const void* x;
+  const void* left;
+  const void* right;
+  const void* embed;
+  int64_t embed_row, vocab;
+  const int64_t* token;
+  const void* norm_w;
+  float eps;
+  void* residual_out;
+  const int32_t* pos;
+  int64_t capacity, cache_head;
+  const void* cos;
+  const void* sin;
+  int64_t table_row, table_rows;
+};
+
+template <typename XT, int LPR, int ROWS, Pro PRO>
+__global__ __launch_bounds__(256) void fused_int4_kernel(const LeanFused P) {
+  constexpr int L = 4;
+  constexpr int SUBS = 64 / LPR;
+  constexpr int NVG = ROWS / L > 0 ? ROWS / L : 1;
+  constexpr int GLEV = log2c(L) < log2c(ROWS) ? log2c(L) : log2c(ROWS);
+  static_assert(ROWS >= 2, "paired segments need two rows per wave");
+  extern __shared__ uint32_t xs_lds[];
+  const int lane = threadIdx.x & 63;
+  const int sub = lane / LPR;
+  const int l = lane % LPR;
+  const int cols = P.cols;
+  const int nchunks = cols >> 5;
+  const int rounds = (nchunks + LPR - 1) / LPR;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int v0 = (int)(blockIdx.x * 4 + wave) * (ROWS * SUBS);   // first virtual row (uniform)
+  const bool active = v0 < P.vtotal;
+  const int si = (P.nseg > 1 && v0 >= P.seg[1].vbegin ? 1 : 0) + (P.nseg > 2 && v0 >= P.seg[2].vbegin ? 1 : 0);
+  const LeanSeg& S = si == 0 ? P.seg[0] : (si == 1 ? P.seg[1] : P.seg[2]);
+  const int kind = S.kind;
+  const int srows = S.rows;
+  const int lr0 = v0 - S.vbegin;
+  const bool paired = kind == kSegRopeOut || kind == kSegRopeCache || kind == kSegSilu;
+
+  // physical row (and matrix) of segment-local virtual row v
+  auto phys = [&](int v, bool& up) -> int {
+    up = false;
+    if (!paired) return v;
+    bool odd;
+    const int ph = paired_row<SUBS>(v, kind, P.head_dim, odd);
+    up = odd && kind == kSegSilu;
+    return ph;
+  };
+  const uint8_t* wrow[ROWS];
+  bool rv[ROWS];
+#pragma unroll
+  for (int i = 0; i < ROWS; i++) {
+    const int v = lr0 + i * SUBS + sub;
+    rv[i] = v < srows;
+    bool up;
+    const int ph = phys(rv[i] ? v : srows - 1, up);
+    wrow[i] = (up ? S.w2 : S.w) + (size_t)ph * S.w_row;
+  }
+  const f16_t* srow[NVG];
+  bool sv[NVG];
+#pragma unroll
+  for (int k = 0; k < NVG; k++) {
+    const int v = lr0 + rs_row<ROWS>(l, GLEV, k) * SUBS + sub;
+    sv[k] = v < srows;
+    bool up;
+    const int ph = phys(sv[k] ? v : srows - 1, up);
+    srow[k] = (up ? S.s2 : S.s) + (size_t)ph * S.s_row;
+  }
+  auto fetch = [&](int r, Raw<16>* w, f16_t* sc) {
+    uint32_t j = (uint32_t)(r * LPR + l);
+    j = j < (uint32_t)nchunks ? j : (uint32_t)nchunks - 1;
+#pragma unroll
+    for (int i = 0; i < ROWS; i++) w[i] = load_raw<16>(wrow[i] + j * 16u);
+#pragma unroll
+    for (int k = 0; k < NVG; k++) sc[k] = srow[k][j >> 2];
+  };
+  Raw<16> wc[ROWS];
+  f16_t sc[NVG];
+  fetch(0, wc, sc);   // in bounds for inactive waves too (rows clamped)
+
+  // ---- activation vector into LDS
+  if constexpr (PRO == Pro::kLoad) {
+    const int xn = cols >> 3;
+    for (int idx = threadIdx.x; idx < xn; idx += 256)
+      reinterpret_cast<uint4*>(xs_lds)[idx] = reinterpret_cast<const uint4*>(P.x)[idx];
+  } else {
+    // RMSNorm of the residual stream with the thread partition, reduction order and
+    // rounding points of the standalone rms_norm / add_rms_norm kernels; workgroup 0
+    // stores the residual.
+    __shared__ float red[4];
+    const int n = cols;
+    constexpr int kHeld = 16;
+    const uint16_t* pa;
+    if constexpr (PRO == Pro::kEmbedNorm) {
+      int64_t t = P.token[0];
+      t = t < 0 ? 0 : (t >= P.vocab ? P.vocab - 1 : t);
+      pa = reinterpret_cast<const uint16_t*>(P.embed) + t * P.embed_row;
+    } else {
+      pa = reinterpret_cast<const uint16_t*>(P.left);
+    }
+    const uint16_t* pb = reinterpret_cast<const uint16_t*>(P.right);
+    const uint16_t* pw = reinterpret_cast<const uint16_t*>(P.norm_w);
+    const bool writer = blockIdx.x == 0 && P.residual_out != nullptr;
+    XT* xl = reinterpret_cast<XT*>(xs_lds);
+    uint16_t ra[kHeld], rb[kHeld], rw[kHeld];
+#pragma unroll
+    for (int k = 0; k < kHeld; k++) {
+      const int i = threadIdx.x + 256 * k;
+      const int ic = i < n ? i : n - 1;
+      ra[k] = pa[ic];
+      if constexpr (PRO != Pro::kEmbedNorm) rb[k] = pb[ic];
+      rw[k] = pw[ic];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float rr[kHeld];
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kHeld; k++) {
+      const float a = to_f32(XT{ra[k]});
+      float r;
+      if constexpr (PRO == Pro::kAddNorm) r = round_bf16(a + to_f32(XT{rb[k]}));
+      else if constexpr (PRO == Pro::kAddRmsNorm) r = round_to<XT>(a + to_f32(XT{rb[k]}));
+      else r = a;
+      rr[k] = r;
+      if (threadIdx.x + 256 * k < n) ss = __builtin_fmaf(r, r, ss);
+    }
+    const float total = block_sum256(ss, red);
+    const float inv = 1.0f / __builtin_sqrtf(total / (float)n + P.eps);
+#pragma unroll
+    for (int k = 0; k < kHeld; k++) {
+      const int i = threadIdx.x + 256 * k;
+      if (i < n) {
+        const float w = to_f32(XT{rw[k]});
+        if (writer) store<XT>(reinterpret_cast<XT*>(P.residual_out) + i, rr[k]);
+        store<XT>(xl + i, PRO == Pro::kAddNorm ? (rr[k] * inv) * w : (rr[k] * inv) * (w + 0.0f));
+      }
+    }
+  }
+  lds_barrier();
+  if (!active) return;
+
+  float acc[NVG];
+#pragma unroll
+  for (int k = 0; k < NVG; k++) acc[k] = 0.0f;
+  int r = 0;
+  do {
+    Raw<16> wn[ROWS];
+    f16_t sn[NVG];
+    const bool more = r + 1 < rounds;
+    if (more) fetch(r + 1, wn, sn);
+    const int j = r * LPR + l;
+    const bool cv = j < nchunks;
+    uint32_t xw[16];
+    {
+      const uint4* xp = reinterpret_cast<const uint4*>(xs_lds + (cv ? j : 0) * 16);
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const uint4 v = xp[q];
+        xw[4 * q] = v.x; xw[4 * q + 1] = v.y; xw[4 * q + 2] = v.z; xw[4 * q + 3] = v.w;
+      }
+    }
+    float p[ROWS];
+    chunk_dot_rows<Fmt::kInt4Sym, XT, ROWS>(wc, xw, p);
+#pragma unroll
+    for (int i = 0; i < ROWS; i++) p[i] = (cv && rv[i]) ? p[i] : 0.0f;
+    reduce_range<ROWS, 1, L>(p);
+#pragma unroll
+    for (int k = 0; k < NVG; k++) {
+      const float t = p[k] * to_f32(sc[k]);
+      acc[k] = acc[k] + ((cv && sv[k]) ? t : 0.0f);
+    }
+    if (more) {
+#pragma unroll
+      for (int i = 0; i < ROWS; i++) wc[i] = wn[i];
+#pragma unroll
+      for (int k = 0; k < NVG; k++) sc[k] = sn[k];
+    }
+  } while (++r < rounds);
+  reduce_range<NVG, L, LPR>(acc);
+
+  // ---- epilogue on the row held by this lane (same as gemv_kernel's fused epilogues)
+  const int frow = rs_row<ROWS>(l, log2c(ROWS), 0) * SUBS + sub;
+  const bool fstore = (l >> log2c(ROWS)) == 0;
+  const int fr = lr0 + frow;
+  const bool ok = fstore && fr < srows;
+  const float val = round_to<XT>(acc[0]);
+  if (kind == kSegPlain) {
+    if (ok) store<XT>(reinterpret_cast<XT*>(S.out) + fr, acc[0]);
+    return;
+  }
+  bool odd = false;
+  const int ph = kind == kSegCache ? fr : paired_row<SUBS>(fr < srows ? fr : srows - 1, kind, P.head_dim, odd);
+  const float pv = xor_partner<ROWS / 2 < 1 ? 1 : ROWS / 2>(val);   // the other half of the pair
+  if (kind == kSegSilu) {
+    if (ok && !odd) store<XT>(reinterpret_cast<XT*>(S.out) + ph, silu_mul_val(val, pv));
+    return;
+  }
+  const int64_t pos = P.pos != nullptr ? (int64_t)P.pos[0] : 0;
+  const int D = P.head_dim;
+  float o = val;
+  if (kind != kSegCache && pos >= 0 && pos < P.table_rows) {
+    const int half = D >> 1;
+    const int j = (ph % D) - (odd ? half : 0);
+    const float c = ld<XT>(P.cos, pos * P.table_row + j);
+    const float sn = ld<XT>(P.sin, pos * P.table_row + j);
+    float o1, o2;
+    if (odd) rope_pair<XT>(pv, val, c, sn, o1, o2);
+    else rope_pair<XT>(val, pv, c, sn, o1, o2);
+    o = odd ? o2 : o1;
+  }
+  if (ok) {
+    if (kind == kSegRopeOut) {
+      store<XT>(reinterpret_cast<XT*>(S.out) + ph, o);
+    } else if (pos >= 0 && pos < P.capacity) {
+      const int64_t h = ph / D, d = ph - h * D;
+      store<XT>(reinterpret_cast<XT*>(S.out) + h * P.cache_head + pos * D + d, o);
+    }
+  }
+}
+
+// Rows per wave of the lean fused kernel (paired segments need two).
+inline int fused_rows_per_wave(int64_t vrows, int lpr) {
+  const int64_t groups = vrows * lpr / 64;
+  return groups >= 16384 ? 4 : 2;
+}
+
+LeanFused lean_params(const tt_fused_gemv* d, int per_batch) {
+  LeanFused P{};
+  P.nseg = d->count;
+  int v = 0;
+  for (int i = 0; i < d->count; i++) {
+    const tt_fused_segment& g = d->seg[i];
+    LeanSeg& S = P.seg[i];
+    S.w = static_cast<const uint8_t*>(g.weight);
+    S.w2 = static_cast<const uint8_t*>(g.weight2);
+    S.s = static_cast<const f16_t*>(g.scales);
+    S.s2 = static_cast<const f16_t*>(g.scales2);
+    S.out = g.out;
+    S.w_row = (uint32_t)g.w_row_bytes;
+    S.s_row = (uint32_t)g.s_row;
+    S.rows = (int)(g.kind == TT_SEG_SILU ? 2 * g.rows : g.rows);
+    S.vbegin = v;
+    S.kind = g.kind;
+    v += (S.rows + per_batch - 1) / per_batch * per_batch;
+  }
+  P.vtotal = v;
+  P.cols = (int)d->cols;
+  P.head_dim = (int)d->head_dim;
+  P.x = d->x;
+  P.left = d->left;
+  P.right = d->right;
+  P.embed = d->embed;
+  P.embed_row = d->embed_row;
+  P.vocab = d->vocab;
+  P.token = d->token;
+  P.norm_w = d->norm_weight;
+  P.eps = d->eps;
+  P.residual_out = d->residual_out;
+  P.pos = d->position;
+  P.capacity = d->capacity;
+  P.cache_head = d->cache_head;
+  P.cos = d->cos_table;
+  P.sin = d->sin_table;
+  P.table_row = d->table_row;
+  P.table_rows = d->table_rows;
+  return P;
+}
+
+// The lean kernel covers int4 g128 segments whose operands fit 32-bit offsets and
+// whose activation vector fits the register-held prologue.
+bool lean_fits(const tt_fused_gemv* d) {
+  if (d->weight_format != TT_FMT_INT4_G || d->cols > 4096) return false;
+  for (int i = 0; i < d->count; i++) {
+    const tt_fused_segment& g = d->seg[i];
+    const int64_t rows = g.rows;
+    if (g.w_row_bytes >= ((int64_t)1 << 31) || rows * g.w_row_bytes >= ((int64_t)1 << 31)) return false;
+    if (g.s_row >= ((int64_t)1 << 30)) return false;
+  }
+  return true;
+}
+
+template <typename XT, int LPR, Pro PRO>
+int launch_lean_lpr(const tt_fused_gemv* d, hipStream_t st) {
+  int64_t vrows = 0;
+  for (int i = 0; i < d->count; i++) vrows += d->seg[i].kind == TT_SEG_SILU ? 2 * d->seg[i].rows : d->seg[i].rows;
+  const int rpw = fused_rows_per_wave(vrows, LPR);
+  const int per_batch = rpw * (64 / LPR);
+  const LeanFused P = lean_params(d, per_batch);
+  const int64_t waves = P.vtotal / per_batch;
+  const dim3 grid((unsigned)((waves + 3) / 4));
+  const size_t lds = (size_t)d->cols * 2;
+  if (rpw == 4) hipLaunchKernelGGL((fused_int4_kernel<XT, LPR, 4, PRO>), grid, dim3(256), lds, st, P);
+  else hipLaunchKernelGGL((fused_int4_kernel<XT, LPR, 2, PRO>), grid, dim3(256), lds, st, P);
+  return check_launch(kWhat);
+}
+
+template <typename XT, Pro PRO>
+int launch_lean(const tt_fused_gemv* d, int lpr, hipStream_t st) {
+  if (lpr == 64) return launch_lean_lpr<XT, 64, PRO>(d, st);
+  if (lpr == 32) return launch_lean_lpr<XT, 32, PRO>(d, st);
+  return launch_lean_lpr<XT, 16, PRO>(d, st);
+}
+
 // Highest key among n partials (256 threads), then token / value / bookkeeping.
 __global__ __launch_bounds__(256) void argmax_step_kernel(const uint64_t* partials, int n, int64_t* out_idx,
                                                           float* out_val, int32_t* pos, const int32_t* base,
@@ -160,6 +486,7 @@ GemvParams params(const tt_fused_gemv* d) {
 
 template <typename AT, Pro PRO>
 int launch(const tt_fused_gemv* d, GemvParams& P, int lpr, bool argmax, hipStream_t st) {
+  if (!argmax && lean_fits(d)) return launch_lean<AT, PRO>(d, lpr, st);
   if (d->weight_format == TT_FMT_INT4_G) {
     int64_t rows = 0;
     for (int i = 0; i < d->count; i++) rows += d->seg[i].kind == TT_SEG_SILU ? 2 * d->seg[i].rows : d->seg[i].rows;

@@ -1,5 +1,5 @@
 // fp16/bf16 and fp8 GEMV entry points.
-#include "gemv_impl.h"
+#include "gemv_lean.h"
 
 using namespace tt;
 
@@ -24,6 +24,18 @@ extern "C" int tt_scaled_matvec(const void* weight, int64_t w_row_bytes, const v
   const int Lg = 1;
   const int lpr = tt_gemv_lanes_per_row(cols / 32, 1);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (scale_dtype == TT_F32 && x_dtype == out_dtype && lean_fits(rows, w_row_bytes, 4, cols)) {
+    LeanParams L{};
+    L.w = static_cast<const uint8_t*>(weight);
+    L.s = scales;
+    L.x = x;
+    L.out = out;
+    L.w_row = (uint32_t)w_row_bytes;
+    L.s_row = 1;
+    L.rows = (int)rows;
+    L.cols = (int)cols;
+    return lean_launch<Fmt::kFp8, SMode::kRow, float, 1>(x_dtype, lpr, L, 1, st, what);
+  }
   if (scale_dtype == TT_F16) return launch_types<Fmt::kFp8, SMode::kRow, f16_t, 4>(x_dtype, out_dtype, Lg, lpr, P, 1, st, what);
   return launch_types<Fmt::kFp8, SMode::kRow, float, 4>(x_dtype, out_dtype, Lg, lpr, P, 1, st, what);
 }
@@ -58,6 +70,18 @@ extern "C" int tt_multi_matvec_bias(int count, const void* const* weights, int w
   const int Lg = 1;
   const int lpr = tt_gemv_lanes_per_row(cols / 32, 1);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (count == 1 && x_dtype == out_dtype && lean_fits(rows[0], w_row[0] * 2, 0, cols)) {
+    LeanParams L{};
+    L.w = static_cast<const uint8_t*>(weights[0]);
+    L.x = x;
+    L.out = out;
+    L.bias = biases ? biases[0] : nullptr;
+    L.w_row = (uint32_t)(w_row[0] * 2);
+    L.rows = (int)rows[0];
+    L.cols = (int)cols;
+    if (w_dtype == TT_F16) return lean_launch<Fmt::kF16W, SMode::kNone, float, 1>(x_dtype, lpr, L, 1, st, what);
+    return lean_launch<Fmt::kBF16W, SMode::kNone, float, 1>(x_dtype, lpr, L, 1, st, what);
+  }
   if (w_dtype == TT_F16) return launch_types<Fmt::kF16W, SMode::kNone, float, 2>(x_dtype, out_dtype, Lg, lpr, P, 1, st, what);
   return launch_types<Fmt::kBF16W, SMode::kNone, float, 2>(x_dtype, out_dtype, Lg, lpr, P, 1, st, what);
 }

@@ -1,5 +1,5 @@
 // E8M0 block-scaled (MXFP4, q1, q2) and affine low-bit GEMV entry points.
-#include "gemv_impl.h"
+#include "gemv_lean.h"
 
 using namespace tt;
 
@@ -34,6 +34,28 @@ int selected_e8(const char* what, Fmt fmt, const void* packed, int64_t w_expert_
   const int lpr = tt_gemv_lanes_per_row(cols / 32, 1);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int slots = (int)selected;
+  if (x_dtype == out_dtype && lean_fits(rows, w_row_bytes, s_row, cols)) {
+    LeanParams L{};
+    L.w = static_cast<const uint8_t*>(packed);
+    L.s = scales;
+    L.x = x;
+    L.out = out;
+    L.experts = experts;
+    L.w_expert = w_expert_bytes;
+    L.s_expert = s_expert;
+    L.x_slot = x_slot;
+    L.out_slot = out_slot;
+    L.w_row = (uint32_t)w_row_bytes;
+    L.s_row = (uint32_t)s_row;
+    L.rows = (int)rows;
+    L.cols = (int)cols;
+    switch (fmt) {
+      case Fmt::kMxfp4: return lean_launch<Fmt::kMxfp4, SMode::kBlockE8, uint8_t, 1>(x_dtype, lpr, L, slots, st, what);
+      case Fmt::kQ2E8: return lean_launch<Fmt::kQ2E8, SMode::kBlockE8, uint8_t, 1>(x_dtype, lpr, L, slots, st, what);
+      case Fmt::kQ1E8: return lean_launch<Fmt::kQ1E8, SMode::kBlockE8, uint8_t, 1>(x_dtype, lpr, L, slots, st, what);
+      default: break;
+    }
+  }
   switch (fmt) {
     case Fmt::kMxfp4: return launch_types<Fmt::kMxfp4, SMode::kBlockE8, uint8_t, 4>(x_dtype, out_dtype, Lg, lpr, P, slots, st, what);
     case Fmt::kQ2E8: return launch_types<Fmt::kQ2E8, SMode::kBlockE8, uint8_t, 4>(x_dtype, out_dtype, Lg, lpr, P, slots, st, what);
@@ -96,6 +118,23 @@ extern "C" int tt_lowbit_affine_matvec(const void* packed, int64_t w_row_bytes, 
   P.aff_zero = 1;
   const int lpr = tt_gemv_lanes_per_row(cols / 32, L);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (x_dtype == out_dtype && lean_group_ok(Lg) && lean_fits(rows, w_row_bytes, 2 * s_row, cols) && s_group >= 0 &&
+      s_group * (cols / group_size) < (1LL << 30)) {
+    LeanParams Q{};
+    Q.w = static_cast<const uint8_t*>(packed);
+    Q.s = scale_zero;
+    Q.x = x;
+    Q.out = out;
+    Q.s_pair = 1;
+    Q.aff_zero = 1;
+    Q.w_row = (uint32_t)w_row_bytes;
+    Q.s_row = (uint32_t)s_row;
+    Q.s_grp = (uint32_t)s_group;
+    Q.rows = (int)rows;
+    Q.cols = (int)cols;
+    if (bits == 2) return lean_launch_group<Fmt::kQ2Aff, SMode::kGroupAff, f16_t>(Lg, x_dtype, lpr, Q, 1, st, what);
+    return lean_launch_group<Fmt::kQ1Aff, SMode::kGroupAff, f16_t>(Lg, x_dtype, lpr, Q, 1, st, what);
+  }
   if (bits == 2) return launch_types<Fmt::kQ2Aff, SMode::kGroupAff, f16_t, 4>(x_dtype, out_dtype, Lg, lpr, P, 1, st, what);
   return launch_types<Fmt::kQ1Aff, SMode::kGroupAff, f16_t, 4>(x_dtype, out_dtype, Lg, lpr, P, 1, st, what);
 }

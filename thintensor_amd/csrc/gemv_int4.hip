@@ -1,5 +1,5 @@
 // int4 GEMV entry points (dense, multi-matrix, selected expert).
-#include "gemv_impl.h"
+#include "gemv_lean.h"
 
 using namespace tt;
 
@@ -226,6 +226,7 @@ int launch_int4g128(int lpr, const void* W, int64_t w_row, const void* S, int64_
 
 }  // namespace
 
+
 extern "C" int tt_gemv_lanes_per_row(int64_t chunks, int64_t group_chunks) {
   if (chunks <= 0) return 0;
   int best = 0;
@@ -304,14 +305,28 @@ extern "C" int tt_multi_int4_scaled_matvec(int count, const void* const* packed,
     if (scale_dtype == TT_F16) return launch_types<Fmt::kInt4Sym, SMode::kRow, f16_t, 4>(x_dtype, out_dtype, Lg, lpr, P, 1, st, what);
     return launch_types<Fmt::kInt4Sym, SMode::kRow, float, 4>(x_dtype, out_dtype, Lg, lpr, P, 1, st, what);
   }
-  if (count == 1 && scale_dtype == TT_F16 && Lg == 4 && x_dtype == out_dtype && (lpr == 64 || lpr == 32 || lpr == 16) &&
-      int4g128_fits(rows[0], w_row_bytes[0], s_row[0], s_group[0], cols)) {
-    // one matrix, group 128, fp16 scales: the lean single-matrix kernel
-    if (x_dtype == TT_F16)
-      return launch_int4g128<f16_t>(lpr, packed[0], w_row_bytes[0], scales[0], s_row[0], s_group[0], x, out,
-                                    (int)rows[0], (int)cols, st);
-    return launch_int4g128<bf16_t>(lpr, packed[0], w_row_bytes[0], scales[0], s_row[0], s_group[0], x, out,
-                                   (int)rows[0], (int)cols, st);
+  if (count == 1 && !affine && !row_mode && scale_dtype == TT_F16 && x_dtype == out_dtype && lean_group_ok(Lg) &&
+      lean_fits(rows[0], w_row_bytes[0], 2 * s_row[0], cols) && s_group[0] >= 0 && s_group[0] * (cols / group_size) < (1LL << 30)) {
+    // one matrix, symmetric, fp16 group scales: the lean single-matrix kernels (a
+    // dedicated one for group 128, the decode hot path)
+    if (Lg == 4 && int4g128_fits(rows[0], w_row_bytes[0], s_row[0], s_group[0], cols)) {
+      if (x_dtype == TT_F16)
+        return launch_int4g128<f16_t>(lpr, packed[0], w_row_bytes[0], scales[0], s_row[0], s_group[0], x, out,
+                                      (int)rows[0], (int)cols, st);
+      return launch_int4g128<bf16_t>(lpr, packed[0], w_row_bytes[0], scales[0], s_row[0], s_group[0], x, out,
+                                     (int)rows[0], (int)cols, st);
+    }
+    LeanParams L{};
+    L.w = static_cast<const uint8_t*>(packed[0]);
+    L.s = scales[0];
+    L.x = x;
+    L.out = out;
+    L.w_row = (uint32_t)w_row_bytes[0];
+    L.s_row = (uint32_t)s_row[0];
+    L.s_grp = (uint32_t)s_group[0];
+    L.rows = (int)rows[0];
+    L.cols = (int)cols;
+    return lean_launch_group<Fmt::kInt4Sym, SMode::kGroup, f16_t>(Lg, x_dtype, lpr, L, 1, st, what);
   }
   if (scale_dtype == TT_F16 && Lg == 4 && x_dtype == out_dtype) {
     // the decode hot path (group 128, fp16 scales): launch shape chosen from the matrix
@@ -355,6 +370,25 @@ extern "C" int tt_int4_selected_matvec(const void* packed, int64_t w_expert_byte
   const int Lg = L;
   const int lpr = tt_gemv_lanes_per_row(cols / 32, row_mode ? 1 : L);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (!row_mode && scale_dtype == TT_F16 && x_dtype == out_dtype && lean_group_ok(Lg) &&
+      lean_fits(rows, w_row_bytes, 2 * s_row, cols) && s_group >= 0 && s_group * (cols / group_size) < (1LL << 30)) {
+    LeanParams Q{};
+    Q.w = static_cast<const uint8_t*>(packed);
+    Q.s = scales;
+    Q.x = x;
+    Q.out = out;
+    Q.experts = expert_indices;
+    Q.w_expert = w_expert_bytes;
+    Q.s_expert = s_expert;
+    Q.x_slot = x_slot;
+    Q.out_slot = out_slot;
+    Q.w_row = (uint32_t)w_row_bytes;
+    Q.s_row = (uint32_t)s_row;
+    Q.s_grp = (uint32_t)s_group;
+    Q.rows = (int)rows;
+    Q.cols = (int)cols;
+    return lean_launch_group<Fmt::kInt4Sym, SMode::kGroup, f16_t>(Lg, x_dtype, lpr, Q, (int)selected, st, what);
+  }
   if (row_mode) {
     if (scale_dtype == TT_F16) return launch_types<Fmt::kInt4Sym, SMode::kRow, f16_t, 4>(x_dtype, out_dtype, Lg, lpr, P, (int)selected, st, what);
     return launch_types<Fmt::kInt4Sym, SMode::kRow, float, 4>(x_dtype, out_dtype, Lg, lpr, P, (int)selected, st, what);
