@@ -16,6 +16,11 @@
 // tokens, so a decode step can pass its position and 1) so graph replays follow the
 // growing cache; chunks past the count exit without work.  The count is clamped to
 // max_tokens so a runaway device counter can never read past the cache.
+//
+// Contiguous head_dim-64 caches use kernels that issue every load before the first
+// wait: the chunk wave requests its K row, V column and query rows before the active
+// count is known (all rows up to the capacity are in bounds), and the combine wave
+// requests the chunk metadata and up to 32 chunks of partial outputs at once.
 #include "tt_abi_internal.h"
 #include "tt_common.h"
 
@@ -229,8 +234,159 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(AttnParams P) {
   combine_head<T, SKT>(P, blockIdx.x, threadIdx.x);
 }
 
+// Chunk partials for contiguous head_dim-64 caches whose capacity is a whole number
+// of chunks (every row of every chunk is in bounds, so all loads are issued before the
+// active count is known).  Same arithmetic as attn_chunk.
+template <typename T, int G>
+__global__ __launch_bounds__(64) void attn_partial64_kernel(AttnParams P) {
+  constexpr int D = 64;
+  const int kvh = blockIdx.y;
+  const int c = blockIdx.x;
+  const int lane = threadIdx.x;
+  const int h0 = kvh * G;
+  __shared__ float q_s[G * D];
+  __shared__ float p_s[G * kChunk];
+  // K row of this lane's token, the chunk's V column (lane = dimension), query rows
+  const int t = c * kChunk + lane;
+  const uint4* krow = reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(P.keys) + kvh * P.k_head + (int64_t)t * D);
+  uint4 kr[D / 8];
+#pragma unroll
+  for (int i = 0; i < D / 8; i++) kr[i] = krow[i];
+  const T* vcol = reinterpret_cast<const T*>(P.values) + kvh * P.v_head + (int64_t)(c * kChunk) * D + lane;
+  T vraw[kChunk];
+#pragma unroll
+  for (int tt = 0; tt < kChunk; tt++) vraw[tt] = vcol[tt * D];
+  T qraw[G];
+#pragma unroll
+  for (int g = 0; g < G; g++) qraw[g] = reinterpret_cast<const T*>(P.q)[(int64_t)h0 * D + g * D + lane];
+  const int T_act = min(P.tokens_dev ? P.tokens_dev[0] + P.tokens : P.tokens, P.max_tokens);
+  if (c * kChunk >= T_act) return;
+  const bool valid = t < T_act;
+  const int nt = min(kChunk, T_act - c * kChunk);
+#pragma unroll
+  for (int g = 0; g < G; g++) q_s[g * D + lane] = to_f32(qraw[g]);
+  __syncthreads();
+  float sc[G];
+#pragma unroll
+  for (int g = 0; g < G; g++) sc[g] = 0.0f;
+#pragma unroll
+  for (int i = 0; i < D / 8; i++) {
+    const uint32_t kw[4] = {kr[i].x, kr[i].y, kr[i].z, kr[i].w};
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      const float kv = (e & 1) ? hi_f32<T>(kw[e >> 1]) : lo_f32<T>(kw[e >> 1]);
+#pragma unroll
+      for (int g = 0; g < G; g++) sc[g] = __builtin_fmaf(q_s[g * D + 8 * i + e], kv, sc[g]);
+    }
+  }
+  const float ninf = __builtin_bit_cast(float, 0xff800000u);
+#pragma unroll
+  for (int g = 0; g < G; g++) {
+    const float s = valid ? sc[g] * P.scale : ninf;
+    float m = s;
+    m = fmaxf(m, xor_partner<1>(m));
+    m = fmaxf(m, xor_partner<2>(m));
+    m = fmaxf(m, xor_partner<4>(m));
+    m = fmaxf(m, xor_partner<8>(m));
+    m = fmaxf(m, xor_partner<16>(m));
+    m = fmaxf(m, xor_partner<32>(m));
+    const float p = valid ? exp_f32(s - m) : 0.0f;
+    const float l = xor_sum(p, 1, 64);
+    p_s[g * kChunk + lane] = p;
+    if (lane == 0) {
+      P.part_m[(int64_t)(h0 + g) * P.max_chunks + c] = m;
+      P.part_l[(int64_t)(h0 + g) * P.max_chunks + c] = l;
+    }
+  }
+  __syncthreads();
+  float o[G];
+#pragma unroll
+  for (int g = 0; g < G; g++) o[g] = 0.0f;
+#pragma unroll
+  for (int tt = 0; tt < kChunk; tt++) {
+    const float v = tt < nt ? to_f32(vraw[tt]) : 0.0f;
+#pragma unroll
+    for (int g = 0; g < G; g++) o[g] = __builtin_fmaf(p_s[g * kChunk + tt], v, o[g]);
+  }
+#pragma unroll
+  for (int g = 0; g < G; g++) P.part_o[((int64_t)(h0 + g) * P.max_chunks + c) * D + lane] = o[g];
+}
+
+// Combine of one head of dimension 64 (lane = dimension), the arithmetic of
+// combine_head; the chunk metadata and the partial outputs of up to kBlk chunks are
+// requested together before the maximum is formed.
+template <typename T, typename SKT>
+__global__ __launch_bounds__(64) void attn_combine64_kernel(AttnParams P) {
+  constexpr int D = 64, kBlk = 32;
+  const int h = blockIdx.x;
+  const int lane = threadIdx.x;
+  const int T_act = min(P.tokens_dev ? P.tokens_dev[0] + P.tokens : P.tokens, P.max_tokens);
+  const int nc = T_act > 0 ? (T_act + kChunk - 1) / kChunk : 0;
+  const float* pm = P.part_m + (int64_t)h * P.max_chunks;
+  const float* pl = P.part_l + (int64_t)h * P.max_chunks;
+  const float* po = P.part_o + (int64_t)h * P.max_chunks * D + lane;
+  const int last = P.max_chunks - 1;
+  // first block of every operand, clamped to the scratch (values past nc are unused)
+  float mv = pm[lane < last ? lane : last];
+  float lv = pl[lane < last ? lane : last];
+  float ov[kBlk];
+#pragma unroll
+  for (int u = 0; u < kBlk; u++) ov[u] = po[(int64_t)(u < last ? u : last) * D];
+  const float ninf = __builtin_bit_cast(float, 0xff800000u);
+  const bool has_sink = P.sinks != nullptr;
+  const float sink = has_sink ? to_f32(reinterpret_cast<const SKT*>(P.sinks)[h]) : 0.0f;
+  float M = has_sink ? sink : ninf;
+  for (int c0 = 0; c0 < nc; c0 += 64) {
+    float m = c0 + lane < nc ? (c0 == 0 ? mv : pm[c0 + lane]) : ninf;
+    m = fmaxf(m, xor_partner<1>(m));
+    m = fmaxf(m, xor_partner<2>(m));
+    m = fmaxf(m, xor_partner<4>(m));
+    m = fmaxf(m, xor_partner<8>(m));
+    m = fmaxf(m, xor_partner<16>(m));
+    m = fmaxf(m, xor_partner<32>(m));
+    M = fmaxf(M, m);
+  }
+  float den = has_sink ? exp_f32(sink - M) : 0.0f;
+  float acc = 0.0f;
+  for (int c0 = 0; c0 < nc; c0 += 64) {
+    const int n = min(64, nc - c0);
+    const float e = c0 + lane < nc ? exp_f32((c0 == 0 ? mv : pm[c0 + lane]) - M) : 0.0f;
+    const float l = c0 + lane < nc ? (c0 == 0 ? lv : pl[c0 + lane]) : 0.0f;
+    for (int c1 = 0; c1 < n; c1 += kBlk) {
+      if (c0 + c1 > 0) {
+#pragma unroll
+        for (int u = 0; u < kBlk; u++) {
+          const int cc = c0 + c1 + u;
+          ov[u] = po[(int64_t)(cc < last ? cc : last) * D];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kBlk; u++) {
+        if (c1 + u < n) {
+          const float ec = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e), c1 + u));
+          const float lc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, l), c1 + u));
+          den = __builtin_fmaf(lc, ec, den);
+          acc = __builtin_fmaf(ov[u], ec, acc);
+        }
+      }
+    }
+  }
+  store<T>(reinterpret_cast<T*>(P.out) + (int64_t)h * D + lane, acc / den);
+}
+
 template <typename T, int G>
 static int launch_attn(const AttnParams& P, int sink_dtype, bool contiguous64, hipStream_t st) {
+  if (contiguous64) {
+    hipLaunchKernelGGL((attn_partial64_kernel<T, G>), dim3(P.max_chunks, P.kv_heads), dim3(64), 0, st, P);
+    int rc = check_launch("gqa_attention");
+    if (rc) return rc;
+    switch (sink_dtype) {
+      case TT_BF16: hipLaunchKernelGGL((attn_combine64_kernel<T, bf16_t>), dim3(P.heads), dim3(64), 0, st, P); break;
+      case TT_F32: hipLaunchKernelGGL((attn_combine64_kernel<T, float>), dim3(P.heads), dim3(64), 0, st, P); break;
+      default: hipLaunchKernelGGL((attn_combine64_kernel<T, f16_t>), dim3(P.heads), dim3(64), 0, st, P); break;
+    }
+    return check_launch("gqa_attention");
+  }
   if (contiguous64)
     hipLaunchKernelGGL((attn_partial_kernel<T, G, 64>), dim3(P.max_chunks, P.kv_heads), dim3(64), 0, st, P);
   else
@@ -286,7 +442,7 @@ extern "C" int tt_single_token_gqa_attention(const void* q, const void* keys, co
   // 128-bit K loads and whole-chunk V loads need contiguous 64-wide rows and a
   // capacity that is a whole number of chunks
   const bool c64 = head_dim == 64 && k_tok == 64 && v_tok == 64 && max_tokens % kChunk == 0 && aligned(keys, 16) &&
-                   k_head % 8 == 0 && heads / kv_heads <= 8;
+                   k_head % 8 == 0 && v_head % 8 == 0 && heads / kv_heads <= 8;
   auto by_g = [&](auto t) -> int {
     using T = decltype(t);
     switch (G) {
