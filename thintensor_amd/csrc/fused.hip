@@ -12,7 +12,7 @@ namespace {
 constexpr const char* kWhat = "fused_gemv";
 
 // ----------------------------------------------------------------------------
-// Lean fused int4 g128 GEMV of the decode step: one batch of ROWS * (64 / LPR) virtual
+// Lean fused GEMV of the decode step (int4 g128 or dense fp16/bf16 weights): one batch of ROWS * (64 / LPR) virtual
 // rows per wave (segments padded to whole batches, as in gemv_kernel), the RMSNorm
 // prologue and the RoPE / KV-cache / SiLU epilogues of gemv_kernel with the same
 // row pairing, rounding points and reduction order, without its persistent loop.
@@ -24,6 +24,7 @@ struct LeanSeg {
   const f16_t* s;
   const f16_t* s2;
   void* out;
+  const void* bias;     // dense segments: optional per-row bias (activation dtype)
   uint32_t w_row, s_row;
   int rows;             // virtual rows (kSegSilu: 2 x activation rows)
   int vbegin;
@@ -49,12 +50,15 @@ struct LeanFused {
   int64_t table_row, table_rows;
 };
 
-template <typename XT, int LPR, int ROWS, Pro PRO>
-__global__ __launch_bounds__(256) void fused_int4_kernel(const LeanFused P) {
-  constexpr int L = 4;
+template <Fmt F, typename XT, int LPR, int ROWS, Pro PRO>
+__global__ __launch_bounds__(256) void fused_lean_kernel(const LeanFused P) {
+  constexpr bool kInt4 = F == Fmt::kInt4Sym;
+  constexpr int B = FmtInfo<F>::kBytes;
+  constexpr int L = kInt4 ? 4 : 1;
   constexpr int SUBS = 64 / LPR;
-  constexpr int NVG = ROWS / L > 0 ? ROWS / L : 1;
-  constexpr int GLEV = log2c(L) < log2c(ROWS) ? log2c(L) : log2c(ROWS);
+  constexpr int NVG = kInt4 ? (ROWS / L > 0 ? ROWS / L : 1) : ROWS;
+  constexpr int NS = kInt4 ? NVG : 1;
+  constexpr int GLEV = kInt4 ? (log2c(L) < log2c(ROWS) ? log2c(L) : log2c(ROWS)) : 0;
   static_assert(ROWS >= 2, "paired segments need two rows per wave");
   extern __shared__ uint32_t xs_lds[];
   const int lane = threadIdx.x & 63;
@@ -92,26 +96,30 @@ __global__ __launch_bounds__(256) void fused_int4_kernel(const LeanFused P) {
     const int ph = phys(rv[i] ? v : srows - 1, up);
     wrow[i] = (up ? S.w2 : S.w) + (size_t)ph * S.w_row;
   }
-  const f16_t* srow[NVG];
-  bool sv[NVG];
+  const f16_t* srow[NS];
+  bool sv[NS];
+  if constexpr (kInt4) {
 #pragma unroll
-  for (int k = 0; k < NVG; k++) {
-    const int v = lr0 + rs_row<ROWS>(l, GLEV, k) * SUBS + sub;
-    sv[k] = v < srows;
-    bool up;
-    const int ph = phys(sv[k] ? v : srows - 1, up);
-    srow[k] = (up ? S.s2 : S.s) + (size_t)ph * S.s_row;
+    for (int k = 0; k < NS; k++) {
+      const int v = lr0 + rs_row<ROWS>(l, GLEV, k) * SUBS + sub;
+      sv[k] = v < srows;
+      bool up;
+      const int ph = phys(sv[k] ? v : srows - 1, up);
+      srow[k] = (up ? S.s2 : S.s) + (size_t)ph * S.s_row;
+    }
   }
-  auto fetch = [&](int r, Raw<16>* w, f16_t* sc) {
+  auto fetch = [&](int r, Raw<B>* w, f16_t* sc) {
     uint32_t j = (uint32_t)(r * LPR + l);
     j = j < (uint32_t)nchunks ? j : (uint32_t)nchunks - 1;
 #pragma unroll
-    for (int i = 0; i < ROWS; i++) w[i] = load_raw<16>(wrow[i] + j * 16u);
+    for (int i = 0; i < ROWS; i++) w[i] = load_raw<B>(wrow[i] + j * (uint32_t)B);
+    if constexpr (kInt4) {
 #pragma unroll
-    for (int k = 0; k < NVG; k++) sc[k] = srow[k][j >> 2];
+      for (int k = 0; k < NS; k++) sc[k] = srow[k][j >> 2];
+    }
   };
-  Raw<16> wc[ROWS];
-  f16_t sc[NVG];
+  Raw<B> wc[ROWS];
+  f16_t sc[NS];
   fetch(0, wc, sc);   // in bounds for inactive waves too (rows clamped)
 
   // ---- activation vector into LDS
@@ -180,8 +188,8 @@ __global__ __launch_bounds__(256) void fused_int4_kernel(const LeanFused P) {
   for (int k = 0; k < NVG; k++) acc[k] = 0.0f;
   int r = 0;
   do {
-    Raw<16> wn[ROWS];
-    f16_t sn[NVG];
+    Raw<B> wn[ROWS];
+    f16_t sn[NS];
     const bool more = r + 1 < rounds;
     if (more) fetch(r + 1, wn, sn);
     const int j = r * LPR + l;
@@ -196,36 +204,49 @@ __global__ __launch_bounds__(256) void fused_int4_kernel(const LeanFused P) {
       }
     }
     float p[ROWS];
-    chunk_dot_rows<Fmt::kInt4Sym, XT, ROWS>(wc, xw, p);
+    chunk_dot_rows<F, XT, ROWS>(wc, xw, p);
 #pragma unroll
     for (int i = 0; i < ROWS; i++) p[i] = (cv && rv[i]) ? p[i] : 0.0f;
-    reduce_range<ROWS, 1, L>(p);
+    if constexpr (kInt4) {
+      reduce_range<ROWS, 1, L>(p);
 #pragma unroll
-    for (int k = 0; k < NVG; k++) {
-      const float t = p[k] * to_f32(sc[k]);
-      acc[k] = acc[k] + ((cv && sv[k]) ? t : 0.0f);
+      for (int k = 0; k < NVG; k++) {
+        const float t = p[k] * to_f32(sc[k]);
+        acc[k] = acc[k] + ((cv && sv[k]) ? t : 0.0f);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < ROWS; i++) acc[i] = acc[i] + p[i];
     }
     if (more) {
 #pragma unroll
       for (int i = 0; i < ROWS; i++) wc[i] = wn[i];
+      if constexpr (kInt4) {
 #pragma unroll
-      for (int k = 0; k < NVG; k++) sc[k] = sn[k];
+        for (int k = 0; k < NS; k++) sc[k] = sn[k];
+      }
     }
   } while (++r < rounds);
-  reduce_range<NVG, L, LPR>(acc);
+  if constexpr (kInt4) reduce_range<NVG, L, LPR>(acc);
+  else reduce_range<ROWS, 1, LPR>(acc);
 
   // ---- epilogue on the row held by this lane (same as gemv_kernel's fused epilogues)
   const int frow = rs_row<ROWS>(l, log2c(ROWS), 0) * SUBS + sub;
   const bool fstore = (l >> log2c(ROWS)) == 0;
   const int fr = lr0 + frow;
   const bool ok = fstore && fr < srows;
-  const float val = round_to<XT>(acc[0]);
+  float v = acc[0];
   if (kind == kSegPlain) {
-    if (ok) store<XT>(reinterpret_cast<XT*>(S.out) + fr, acc[0]);
+    if (ok) {
+      if (S.bias != nullptr) v = round_to<XT>(v) + to_f32(reinterpret_cast<const XT*>(S.bias)[fr]);
+      store<XT>(reinterpret_cast<XT*>(S.out) + fr, v);
+    }
     return;
   }
   bool odd = false;
   const int ph = kind == kSegCache ? fr : paired_row<SUBS>(fr < srows ? fr : srows - 1, kind, P.head_dim, odd);
+  if (S.bias != nullptr && ok) v = round_to<XT>(v) + to_f32(reinterpret_cast<const XT*>(S.bias)[ph]);
+  const float val = round_to<XT>(v);
   const float pv = xor_partner<ROWS / 2 < 1 ? 1 : ROWS / 2>(val);   // the other half of the pair
   if (kind == kSegSilu) {
     if (ok && !odd) store<XT>(reinterpret_cast<XT*>(S.out) + ph, silu_mul_val(val, pv));
@@ -272,6 +293,7 @@ LeanFused lean_params(const tt_fused_gemv* d, int per_batch) {
     S.s = static_cast<const f16_t*>(g.scales);
     S.s2 = static_cast<const f16_t*>(g.scales2);
     S.out = g.out;
+    S.bias = g.bias;
     S.w_row = (uint32_t)g.w_row_bytes;
     S.s_row = (uint32_t)g.s_row;
     S.rows = (int)(g.kind == TT_SEG_SILU ? 2 * g.rows : g.rows);
@@ -302,10 +324,10 @@ LeanFused lean_params(const tt_fused_gemv* d, int per_batch) {
   return P;
 }
 
-// The lean kernel covers int4 g128 segments whose operands fit 32-bit offsets and
-// whose activation vector fits the register-held prologue.
+// The lean kernel covers int4 g128 and dense segments whose operands fit 32-bit
+// offsets and whose activation vector fits the register-held prologue.
 bool lean_fits(const tt_fused_gemv* d) {
-  if (d->weight_format != TT_FMT_INT4_G || d->cols > 4096) return false;
+  if (d->cols > 4096) return false;
   for (int i = 0; i < d->count; i++) {
     const tt_fused_segment& g = d->seg[i];
     const int64_t rows = g.rows;
@@ -315,7 +337,7 @@ bool lean_fits(const tt_fused_gemv* d) {
   return true;
 }
 
-template <typename XT, int LPR, Pro PRO>
+template <Fmt F, typename XT, int LPR, Pro PRO>
 int launch_lean_lpr(const tt_fused_gemv* d, hipStream_t st) {
   int64_t vrows = 0;
   for (int i = 0; i < d->count; i++) vrows += d->seg[i].kind == TT_SEG_SILU ? 2 * d->seg[i].rows : d->seg[i].rows;
@@ -325,16 +347,23 @@ int launch_lean_lpr(const tt_fused_gemv* d, hipStream_t st) {
   const int64_t waves = P.vtotal / per_batch;
   const dim3 grid((unsigned)((waves + 3) / 4));
   const size_t lds = (size_t)d->cols * 2;
-  if (rpw == 4) hipLaunchKernelGGL((fused_int4_kernel<XT, LPR, 4, PRO>), grid, dim3(256), lds, st, P);
-  else hipLaunchKernelGGL((fused_int4_kernel<XT, LPR, 2, PRO>), grid, dim3(256), lds, st, P);
+  if (rpw == 4) hipLaunchKernelGGL((fused_lean_kernel<F, XT, LPR, 4, PRO>), grid, dim3(256), lds, st, P);
+  else hipLaunchKernelGGL((fused_lean_kernel<F, XT, LPR, 2, PRO>), grid, dim3(256), lds, st, P);
   return check_launch(kWhat);
+}
+
+template <Fmt F, typename XT, Pro PRO>
+int launch_lean_f(const tt_fused_gemv* d, int lpr, hipStream_t st) {
+  if (lpr == 64) return launch_lean_lpr<F, XT, 64, PRO>(d, st);
+  if (lpr == 32) return launch_lean_lpr<F, XT, 32, PRO>(d, st);
+  return launch_lean_lpr<F, XT, 16, PRO>(d, st);
 }
 
 template <typename XT, Pro PRO>
 int launch_lean(const tt_fused_gemv* d, int lpr, hipStream_t st) {
-  if (lpr == 64) return launch_lean_lpr<XT, 64, PRO>(d, st);
-  if (lpr == 32) return launch_lean_lpr<XT, 32, PRO>(d, st);
-  return launch_lean_lpr<XT, 16, PRO>(d, st);
+  if (d->weight_format == TT_FMT_INT4_G) return launch_lean_f<Fmt::kInt4Sym, XT, PRO>(d, lpr, st);
+  if (d->weight_dtype == TT_F16) return launch_lean_f<Fmt::kF16W, XT, PRO>(d, lpr, st);
+  return launch_lean_f<Fmt::kBF16W, XT, PRO>(d, lpr, st);
 }
 
 // Highest key among n partials (256 threads), then token / value / bookkeeping.

@@ -97,6 +97,51 @@ __device__ void wave_topk(float lg0, float lg1, int E, int top_k, bool renorm, i
   if (lane + 64 < top_k) store<OT>(score_out + lane + 64, e1 / den);
 }
 
+// Rows of E <= 32 experts with H <= 4096 (two rounds of 64 lanes): every wave requests
+// the weights of both of its experts and the activation chunks of both rounds before
+// the first wait (chunk indices clamped, contributions masked), then reduces as the
+// general loop below does.
+template <typename WT, typename XT, typename BT>
+__device__ __forceinline__ void router_rows_held(const void* w, int64_t w_row, const void* x, int H, const void* bias,
+                                                 int E, int wave, int lane, float (&lg)[2]) {
+  constexpr Fmt F = std::is_same_v<WT, bf16_t> ? Fmt::kBF16W : Fmt::kF16W;
+  const int nchunks = H >> 5;
+  Raw<64> wr[2][2], xr[2];
+#pragma unroll
+  for (int r = 0; r < 2; r++) {
+    int j = r * 64 + lane;
+    j = j < nchunks ? j : nchunks - 1;
+    xr[r] = load_raw<64>(reinterpret_cast<const uint8_t*>(x) + (int64_t)32 * j * 2);
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+      int e = wave + 16 * k;
+      e = e < E ? e : E - 1;
+      wr[k][r] = load_raw<64>(reinterpret_cast<const uint8_t*>(w) + ((int64_t)e * w_row + 32 * j) * 2);
+    }
+  }
+  BT braw[2];
+#pragma unroll
+  for (int k = 0; k < 2; k++) {
+    const int e = wave + 16 * k;
+    if (bias != nullptr) braw[k] = reinterpret_cast<const BT*>(bias)[e < E ? e : E - 1];
+  }
+  __builtin_amdgcn_sched_barrier(0);   // every load above is issued before the first use
+#pragma unroll
+  for (int k = 0; k < 2; k++) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+      const bool cv = r * 64 + lane < nchunks;
+      const float p = chunk_dot<F, XT>(wr[k][r], xr[r].w);
+      if (r == 0 || (nchunks > 64)) acc = acc + (cv ? p : 0.0f);
+    }
+    // logit = bf16(dot) (+ bias, rounded to bf16 again)
+    float v = round_bf16(xor_sum(acc, 1, 64));
+    if (bias != nullptr) v = round_bf16(v + to_f32(braw[k]));
+    lg[k] = v;
+  }
+}
+
 template <typename WT, typename XT, typename BT, typename OT>
 __global__ __launch_bounds__(1024) void router_kernel(const void* w, int64_t w_row, const void* x, int H, const void* bias,
                                                       int E, int top_k, int renorm, int32_t* idx_out, void* score_out) {
@@ -106,6 +151,21 @@ __global__ __launch_bounds__(1024) void router_kernel(const void* w, int64_t w_r
   const int nwaves = blockDim.x >> 6;
   const int nchunks = H >> 5;
   const int rounds = (nchunks + 63) / 64;
+  if (E <= 32 && nchunks <= 128 && nwaves == 16) {
+    float lg[2];
+    router_rows_held<WT, XT, BT>(w, w_row, x, H, bias, E, wave, lane, lg);
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+      const int e = wave + 16 * k;
+      if (e < E && lane == 0) logits[e] = lg[k];
+    }
+    __syncthreads();
+    if (wave == 0) {
+      const float l0 = lane < E ? logits[lane] : 0.0f;
+      wave_topk<OT>(l0, 0.0f, E, top_k, renorm != 0, idx_out, reinterpret_cast<OT*>(score_out));
+    }
+    return;
+  }
   for (int e = wave; e < E; e += nwaves) {
     float acc = 0.0f;
     for (int r = 0; r < rounds; r++) {
