@@ -374,8 +374,144 @@ __global__ __launch_bounds__(64) void attn_combine64_kernel(AttnParams P) {
   store<T>(reinterpret_cast<T*>(P.out) + (int64_t)h * D + lane, acc / den);
 }
 
+// One workgroup per query head (contiguous head_dim-64 caches, whole-chunk capacity,
+// groups of at least eight query heads per KV head -- measured faster than the two
+// launches there, slower for smaller groups):
+// its 16 waves compute the head's chunk partials (chunk c on wave c mod 16) into LDS with
+// the arithmetic of attn_partial64_kernel, and after one barrier wave 0 combines them
+// in chunk order with the arithmetic of attn_combine64_kernel -- one launch, no
+// communication between workgroups.  The query heads of a KV head read the same K/V
+// rows, which the L2 serves after the first.
+constexpr int kHeadWaves = 16;
+constexpr int kHeadMaxChunks = 256;   // LDS partials: 66 floats per chunk
+
+template <typename T, typename SKT>
+__global__ __launch_bounds__(1024) void attn_head_kernel(AttnParams P) {
+  constexpr int D = 64;
+  const int h = blockIdx.x;
+  const int G = P.heads / P.kv_heads;
+  const int kvh = h / G;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  __shared__ float q_s[D];
+  __shared__ float p_s[kHeadWaves][kChunk];
+  __shared__ float pm_s[kHeadMaxChunks], pl_s[kHeadMaxChunks];
+  __shared__ float po_s[kHeadMaxChunks][D];
+  const float ninf = __builtin_bit_cast(float, 0xff800000u);
+  const T* kbase = reinterpret_cast<const T*>(P.keys) + kvh * P.k_head;
+  const T* vbase = reinterpret_cast<const T*>(P.values) + kvh * P.v_head;
+  // first chunk of this wave: every load is issued before the active count is known
+  // (chunks below max_chunks are inside the capacity)
+  const int c_first = wave;
+  uint4 kr[D / 8];
+  T vraw[kChunk];
+  if (c_first < P.max_chunks) {
+    const uint4* krow = reinterpret_cast<const uint4*>(kbase + (int64_t)(c_first * kChunk + lane) * D);
+#pragma unroll
+    for (int i = 0; i < D / 8; i++) kr[i] = krow[i];
+    const T* vcol = vbase + (int64_t)(c_first * kChunk) * D + lane;
+#pragma unroll
+    for (int tt = 0; tt < kChunk; tt++) vraw[tt] = vcol[tt * D];
+  }
+  const T qraw = reinterpret_cast<const T*>(P.q)[(int64_t)h * D + lane];
+  const int T_act = min(P.tokens_dev ? P.tokens_dev[0] + P.tokens : P.tokens, P.max_tokens);
+  const int nc = T_act > 0 ? (T_act + kChunk - 1) / kChunk : 0;
+  if (wave == 0) q_s[lane] = to_f32(qraw);
+  __syncthreads();
+
+  for (int c = c_first; c < nc; c += kHeadWaves) {
+    if (c != c_first) {
+      const uint4* krow = reinterpret_cast<const uint4*>(kbase + (int64_t)(c * kChunk + lane) * D);
+#pragma unroll
+      for (int i = 0; i < D / 8; i++) kr[i] = krow[i];
+      const T* vcol = vbase + (int64_t)(c * kChunk) * D + lane;
+#pragma unroll
+      for (int tt = 0; tt < kChunk; tt++) vraw[tt] = vcol[tt * D];
+    }
+    const int t = c * kChunk + lane;
+    const bool valid = t < T_act;
+    const int nt = min(kChunk, T_act - c * kChunk);
+    // score: fma chain over d ascending, lane = token
+    float sc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < D / 8; i++) {
+      const uint32_t kw[4] = {kr[i].x, kr[i].y, kr[i].z, kr[i].w};
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const float kv = (e & 1) ? hi_f32<T>(kw[e >> 1]) : lo_f32<T>(kw[e >> 1]);
+        sc = __builtin_fmaf(q_s[8 * i + e], kv, sc);
+      }
+    }
+    const float s = valid ? sc * P.scale : ninf;
+    float m = s;
+    m = fmaxf(m, xor_partner<1>(m));
+    m = fmaxf(m, xor_partner<2>(m));
+    m = fmaxf(m, xor_partner<4>(m));
+    m = fmaxf(m, xor_partner<8>(m));
+    m = fmaxf(m, xor_partner<16>(m));
+    m = fmaxf(m, xor_partner<32>(m));
+    const float p = valid ? exp_f32(s - m) : 0.0f;
+    const float l = xor_sum(p, 1, 64);
+    p_s[wave][lane] = p;
+    if (lane == 0) {
+      pm_s[c] = m;
+      pl_s[c] = l;
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's p_s stores done
+    __builtin_amdgcn_wave_barrier();
+    // weighted values: lane = dimension, fma chain over the chunk's tokens ascending
+    float o = 0.0f;
+#pragma unroll
+    for (int tt = 0; tt < kChunk; tt++) {
+      const float v = tt < nt ? to_f32(vraw[tt]) : 0.0f;
+      o = __builtin_fmaf(p_s[wave][tt], v, o);
+    }
+    po_s[c][lane] = o;
+    __builtin_amdgcn_wave_barrier();
+  }
+  __syncthreads();
+  if (wave != 0) return;
+
+  // combine in chunk order (the arithmetic of combine_head)
+  const bool has_sink = P.sinks != nullptr;
+  const float sink = has_sink ? to_f32(reinterpret_cast<const SKT*>(P.sinks)[h]) : 0.0f;
+  float M = has_sink ? sink : ninf;
+  for (int c0 = 0; c0 < nc; c0 += 64) {
+    float mm = c0 + lane < nc ? pm_s[c0 + lane] : ninf;
+    mm = fmaxf(mm, xor_partner<1>(mm));
+    mm = fmaxf(mm, xor_partner<2>(mm));
+    mm = fmaxf(mm, xor_partner<4>(mm));
+    mm = fmaxf(mm, xor_partner<8>(mm));
+    mm = fmaxf(mm, xor_partner<16>(mm));
+    mm = fmaxf(mm, xor_partner<32>(mm));
+    M = fmaxf(M, mm);
+  }
+  float den = has_sink ? exp_f32(sink - M) : 0.0f;
+  float acc = 0.0f;
+  for (int c0 = 0; c0 < nc; c0 += 64) {
+    const int n = min(64, nc - c0);
+    const float e = c0 + lane < nc ? exp_f32(pm_s[c0 + lane] - M) : 0.0f;
+    const float lv = c0 + lane < nc ? pl_s[c0 + lane] : 0.0f;
+    for (int u = 0; u < n; u++) {
+      const float ec = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e), u));
+      const float lc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lv), u));
+      den = __builtin_fmaf(lc, ec, den);
+      acc = __builtin_fmaf(po_s[c0 + u][lane], ec, acc);
+    }
+  }
+  store<T>(reinterpret_cast<T*>(P.out) + (int64_t)h * D + lane, acc / den);
+}
+
 template <typename T, int G>
 static int launch_attn(const AttnParams& P, int sink_dtype, bool contiguous64, hipStream_t st) {
+  if (contiguous64 && G >= 8 && P.max_chunks <= kHeadMaxChunks) {
+    switch (sink_dtype) {
+      case TT_BF16: hipLaunchKernelGGL((attn_head_kernel<T, bf16_t>), dim3(P.heads), dim3(1024), 0, st, P); break;
+      case TT_F32: hipLaunchKernelGGL((attn_head_kernel<T, float>), dim3(P.heads), dim3(1024), 0, st, P); break;
+      default: hipLaunchKernelGGL((attn_head_kernel<T, f16_t>), dim3(P.heads), dim3(1024), 0, st, P); break;
+    }
+    return check_launch("gqa_attention");
+  }
   if (contiguous64) {
     hipLaunchKernelGGL((attn_partial64_kernel<T, G>), dim3(P.max_chunks, P.kv_heads), dim3(64), 0, st, P);
     int rc = check_launch("gqa_attention");
