@@ -6,8 +6,7 @@
 // bfloat16 for the reference's fused low-bit kernels (triton_kernels.py:1319-1333,
 // 1421-1434), the activation dtype for the MXFP4 chain that the reference runs as
 // separate kernels plus torch adds (gpu_runtime.py:9647-9704, 9855-9903).
-#include "tt_abi_internal.h"
-#include "tt_gemv.h"
+#include "gemv_impl.h"
 
 #include <type_traits>
 
@@ -174,6 +173,226 @@ __global__ __launch_bounds__(256) void weighted_down_kernel(DownParams P) {
   }
 }
 
+// ------------------------------------------------------------------ lean variants
+// Same arithmetic as swiglu_kernel / weighted_down_kernel, laid out like the lean GEMV
+// (gemv_lean.h): one batch per wave, every load of a round issued before its first
+// use, the next round in flight while one is consumed, and the cross-row work done in
+// registers after one reduce-scatter.
+
+// SwiGLU: a lane group's batch is APL activation rows, i.e. 2 * APL weight rows with
+// gate row 2a and up row 2a + 1 adjacent, so after the reduction the gate value and its
+// up partner sit on lanes that one cross-lane move connects.
+template <Fmt F, typename XT, typename OT, typename RT, typename BT, int LPR, int ROWS>
+__global__ __launch_bounds__(256) void swiglu_lean_kernel(const SwigluParams P) {
+  static_assert(ROWS >= 2 && ROWS % 2 == 0, "gate/up pairs");
+  constexpr int B = FmtInfo<F>::kBytes;
+  constexpr int SUBS = 64 / LPR;
+  constexpr int APL = ROWS / 2;
+  extern __shared__ uint32_t xs_lds[];
+  const int slot = blockIdx.y;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int sub = lane / LPR, l = lane % LPR;
+  const int nchunks = P.cols >> 5;
+  const int rounds = (nchunks + LPR - 1) / LPR;
+  const int a0 = (int)(blockIdx.x * 4 + wave) * (APL * SUBS);
+  // the slot's activations go to LDS (loads first, clamped indices)
+  const int xn = P.cols >> 3;
+  const uint4* xg = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(P.x) + (int64_t)slot * P.x_slot);
+  uint4 xreg[4];
+  int xidx[4];
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const int idx = threadIdx.x + 256 * k;
+    xidx[k] = idx < xn ? idx : xn - 1;
+    xreg[k] = xg[xidx[k]];
+  }
+  const int64_t e = P.experts[slot];
+  const uint8_t* wexp = P.w + e * P.w_expert;
+  const uint8_t* sexp = P.s + e * P.s_expert;
+  const uint8_t* wrow[ROWS];
+  const uint8_t* srow[ROWS];
+  bool rv[ROWS];
+#pragma unroll
+  for (int i = 0; i < ROWS; i++) {
+    const int a = a0 + (i >> 1) * SUBS + sub;
+    rv[i] = a < P.act_rows;
+    const int64_t row = 2 * (int64_t)(rv[i] ? a : P.act_rows - 1) + (i & 1);
+    wrow[i] = wexp + row * P.w_row;
+    srow[i] = sexp + row * P.s_row;
+  }
+  struct Round {
+    Raw<B> w[ROWS];
+    uint8_t ex[ROWS];
+  };
+  auto fetch = [&](int r, Round& d) {
+    uint32_t j = (uint32_t)(r * LPR + l);
+    j = j < (uint32_t)nchunks ? j : (uint32_t)nchunks - 1;
+#pragma unroll
+    for (int i = 0; i < ROWS; i++) {
+      d.w[i] = load_raw<B>(wrow[i] + j * (uint32_t)B);
+      d.ex[i] = srow[i][j];
+    }
+  };
+  Round cur;
+  fetch(0, cur);
+  uint4* xl = reinterpret_cast<uint4*>(xs_lds);
+#pragma unroll
+  for (int k = 0; k < 4; k++) xl[xidx[k]] = xreg[k];
+  for (int idx = threadIdx.x + 1024; idx < xn; idx += 256) xl[idx] = xg[idx];
+  lds_barrier();
+
+  float acc[ROWS];
+#pragma unroll
+  for (int i = 0; i < ROWS; i++) acc[i] = 0.0f;
+  int r = 0;
+  do {   // cols >= 32: at least one round
+    Round nxt;
+    const bool more = r + 1 < rounds;
+    if (more) fetch(r + 1, nxt);
+    const int j = r * LPR + l;
+    const bool cv = j < nchunks;
+    uint32_t xw[16];
+    const uint4* xp = reinterpret_cast<const uint4*>(xs_lds + (cv ? j : 0) * 16);
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const uint4 v = xp[q];
+      xw[4 * q] = v.x; xw[4 * q + 1] = v.y; xw[4 * q + 2] = v.z; xw[4 * q + 3] = v.w;
+    }
+    float p[ROWS];
+    chunk_dot_rows<F, XT, ROWS>(cur.w, xw, p);
+#pragma unroll
+    for (int i = 0; i < ROWS; i++) {
+      const float t = p[i] * pow2i((int)cur.ex[i] - 127);
+      acc[i] = acc[i] + ((cv && rv[i]) ? t : 0.0f);
+    }
+    if (more) cur = nxt;
+  } while (++r < rounds);
+  reduce_range<ROWS, 1, LPR>(acc);
+  const float v = acc[0];
+  const float pv = xor_partner<ROWS / 2>(v);   // the other row of the gate/up pair
+  const int br = rs_row<ROWS>(l, log2c(ROWS), 0);
+  if ((l >> log2c(ROWS)) != 0 || (br & 1) != 0) return;
+  const int a = a0 + (br >> 1) * SUBS + sub;
+  if (a >= P.act_rows) return;
+  float g = round_to<RT>(v);
+  float u = round_to<RT>(pv);
+  if (P.bias != nullptr) {
+    const int64_t bb = e * P.bias_expert + 2 * (int64_t)a;
+    g = round_to<RT>(g + ld_bias<BT>(P.bias, bb));
+    u = round_to<RT>(u + ld_bias<BT>(P.bias, bb + 1));
+  }
+  g = fminf(g, P.limit);
+  u = fmaxf(fminf(u, P.limit), -P.limit);
+  const float num = (u + 1.0f) * g;
+  const float den = 1.0f + exp_f32(-g * P.alpha);
+  store<OT>(reinterpret_cast<OT*>(P.out) + (int64_t)slot * P.out_slot + a, num / den);
+}
+
+// Weighted down: every wave computes its ROWS rows (per lane group) for all S selected
+// slots, each round requesting the weights of all slots; after the reduction the lane
+// holding a row folds the slots in slot order: c = fma(v_s, score_s, c) from +0.
+template <Fmt F, typename XT, typename OT, typename RT, typename BT, typename ScT, int LPR, int ROWS, int S>
+__global__ __launch_bounds__(256) void down_lean_kernel(const DownParams P) {
+  constexpr int B = FmtInfo<F>::kBytes;
+  constexpr int SUBS = 64 / LPR;
+  extern __shared__ uint32_t xs_lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int sub = lane / LPR, l = lane % LPR;
+  const int nchunks = P.cols >> 5;
+  const int rounds = (nchunks + LPR - 1) / LPR;
+  const int words = P.cols >> 1;
+  const int n0 = (int)(blockIdx.x * 4 + wave) * (ROWS * SUBS);
+  int64_t e[S];
+#pragma unroll
+  for (int s = 0; s < S; s++) e[s] = P.experts[s];
+  const uint8_t* wrow[S][ROWS];
+  const uint8_t* srow[S][ROWS];
+  bool rv[ROWS];
+  int rcl[ROWS];
+#pragma unroll
+  for (int i = 0; i < ROWS; i++) {
+    const int n = n0 + i * SUBS + sub;
+    rv[i] = n < P.rows;
+    rcl[i] = rv[i] ? n : P.rows - 1;
+  }
+#pragma unroll
+  for (int s = 0; s < S; s++)
+#pragma unroll
+    for (int i = 0; i < ROWS; i++) {
+      wrow[s][i] = P.w + e[s] * P.w_expert + (int64_t)rcl[i] * P.w_row;
+      srow[s][i] = P.s + e[s] * P.s_expert + (int64_t)rcl[i] * P.s_row;
+    }
+  struct Round {
+    Raw<B> w[S][ROWS];
+    uint8_t ex[S][ROWS];
+  };
+  auto fetch = [&](int r, Round& d) {
+    uint32_t j = (uint32_t)(r * LPR + l);
+    j = j < (uint32_t)nchunks ? j : (uint32_t)nchunks - 1;
+#pragma unroll
+    for (int s = 0; s < S; s++)
+#pragma unroll
+      for (int i = 0; i < ROWS; i++) {
+        d.w[s][i] = load_raw<B>(wrow[s][i] + j * (uint32_t)B);
+        d.ex[s][i] = srow[s][i][j];
+      }
+  };
+  Round cur;
+  fetch(0, cur);
+  // the slots' activations to LDS, slot t at word t * words
+  for (int t = 0; t < S; t++) {
+    const uint4* xg = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(P.x) + (int64_t)t * P.x_slot);
+    for (int i = threadIdx.x; i < (words >> 2); i += 256) reinterpret_cast<uint4*>(xs_lds + t * words)[i] = xg[i];
+  }
+  lds_barrier();
+
+  float acc[S][ROWS];
+#pragma unroll
+  for (int s = 0; s < S; s++)
+#pragma unroll
+    for (int i = 0; i < ROWS; i++) acc[s][i] = 0.0f;
+  int r = 0;
+  do {
+    Round nxt;
+    const bool more = r + 1 < rounds;
+    if (more) fetch(r + 1, nxt);
+    const int j = r * LPR + l;
+    const bool cv = j < nchunks;
+#pragma unroll
+    for (int s = 0; s < S; s++) {
+      uint32_t xw[16];
+      const uint4* xp = reinterpret_cast<const uint4*>(xs_lds + s * words + (cv ? j : 0) * 16);
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const uint4 v = xp[q];
+        xw[4 * q] = v.x; xw[4 * q + 1] = v.y; xw[4 * q + 2] = v.z; xw[4 * q + 3] = v.w;
+      }
+      float p[ROWS];
+      chunk_dot_rows<F, XT, ROWS>(cur.w[s], xw, p);
+#pragma unroll
+      for (int i = 0; i < ROWS; i++) {
+        const float t = p[i] * pow2i((int)cur.ex[s][i] - 127);
+        acc[s][i] = acc[s][i] + ((cv && rv[i]) ? t : 0.0f);
+      }
+    }
+    if (more) cur = nxt;
+  } while (++r < rounds);
+#pragma unroll
+  for (int s = 0; s < S; s++) reduce_range<ROWS, 1, LPR>(acc[s]);
+  const int n = n0 + rs_row<ROWS>(l, log2c(ROWS), 0) * SUBS + sub;
+  if ((l >> log2c(ROWS)) != 0 || n >= P.rows) return;
+  float c = 0.0f;
+#pragma unroll
+  for (int s = 0; s < S; s++) {
+    float v = round_to<RT>(acc[s][0]);
+    if (P.bias != nullptr) v = round_to<RT>(v + ld_bias<BT>(P.bias, e[s] * P.bias_expert + n));
+    c = __builtin_fmaf(v, ld_score<ScT>(P.scores, s), c);
+  }
+  store<OT>(reinterpret_cast<OT*>(P.out) + n, c);
+}
+
 // ------------------------------------------------------------------ dispatch
 
 template <typename T> struct DT;
@@ -192,8 +411,23 @@ template <typename Fn> static int with_type(int code, Fn&& f) {
   return TT_ERR_INVALID;
 }
 
+template <Fmt F, typename XT, typename OT, typename RT, typename BT, int LPR>
+static int launch_swiglu_lean(const SwigluParams& P, int slots, hipStream_t st) {
+  constexpr int SUBS = 64 / LPR;
+  const int per_wave = SUBS;   // one activation row (two weight rows) per lane group
+  const int64_t waves = ((int64_t)P.act_rows + per_wave - 1) / per_wave;
+  hipLaunchKernelGGL((swiglu_lean_kernel<F, XT, OT, RT, BT, LPR, 2>), dim3((unsigned)((waves + 3) / 4), slots),
+                     dim3(256), (size_t)P.cols * 2, st, P);
+  return check_launch("mxfp_lowbit_selected_swiglu");
+}
+
 template <Fmt F, typename XT, typename OT, typename RT, typename BT>
 static int launch_swiglu(const SwigluParams& P, int lpr, int slots, hipStream_t st) {
+  if (P.cols <= 8192) {
+    if (lpr == 64) return launch_swiglu_lean<F, XT, OT, RT, BT, 64>(P, slots, st);
+    if (lpr == 32) return launch_swiglu_lean<F, XT, OT, RT, BT, 32>(P, slots, st);
+    if (lpr == 16) return launch_swiglu_lean<F, XT, OT, RT, BT, 16>(P, slots, st);
+  }
   const size_t lds = (size_t)P.cols * 2;
   auto go = [&](auto kern, int subs) {
     constexpr int APW = 2;
@@ -209,8 +443,33 @@ static int launch_swiglu(const SwigluParams& P, int lpr, int slots, hipStream_t 
   }
 }
 
+template <Fmt F, typename XT, typename OT, typename RT, typename BT, typename ScT, int LPR, int S>
+static int launch_down_lean(const DownParams& P, hipStream_t st) {
+  constexpr int SUBS = 64 / LPR;
+  const int64_t waves = ((int64_t)P.rows + SUBS - 1) / SUBS;   // one row per lane group
+  hipLaunchKernelGGL((down_lean_kernel<F, XT, OT, RT, BT, ScT, LPR, 1, S>), dim3((unsigned)((waves + 3) / 4)), dim3(256),
+                     (size_t)P.cols * 2 * S, st, P);
+  return check_launch("mxfp_lowbit_weighted_down");
+}
+
+template <Fmt F, typename XT, typename OT, typename RT, typename BT, typename ScT, int LPR>
+static int launch_down_lean_s(const DownParams& P, hipStream_t st) {
+  switch (P.slots) {
+    case 1: return launch_down_lean<F, XT, OT, RT, BT, ScT, LPR, 1>(P, st);
+    case 2: return launch_down_lean<F, XT, OT, RT, BT, ScT, LPR, 2>(P, st);
+    case 4: return launch_down_lean<F, XT, OT, RT, BT, ScT, LPR, 4>(P, st);
+    default: return launch_down_lean<F, XT, OT, RT, BT, ScT, LPR, 8>(P, st);
+  }
+}
+
 template <Fmt F, typename XT, typename OT, typename RT, typename BT, typename ScT>
 static int launch_down(const DownParams& P, int lpr, hipStream_t st) {
+  if ((P.slots == 1 || P.slots == 2 || P.slots == 4 || P.slots == 8) && P.cols % 8 == 0 &&
+      (int64_t)P.cols * 2 * P.slots <= 65536 && P.x_slot % 8 == 0) {
+    if (lpr == 64) return launch_down_lean_s<F, XT, OT, RT, BT, ScT, 64>(P, st);
+    if (lpr == 32) return launch_down_lean_s<F, XT, OT, RT, BT, ScT, 32>(P, st);
+    if (lpr == 16) return launch_down_lean_s<F, XT, OT, RT, BT, ScT, 16>(P, st);
+  }
   auto go = [&](auto kern, int rb) {
     const size_t lds = (size_t)P.cols * 2 * P.slots + (size_t)rb * 4 * P.slots;
     const int blocks = (P.rows + rb - 1) / rb;
