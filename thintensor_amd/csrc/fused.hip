@@ -86,6 +86,10 @@ __global__ __launch_bounds__(256) void fused_lean_kernel(const LeanFused P) {
     up = odd && kind == kSegSilu;
     return ph;
   };
+  // both matrices' base pointers in scalar registers, so the per-lane choice between them
+  // is a select and not a vector load of the chosen kernel argument
+  const uint8_t* const wlo = uniform_ptr(S.w);
+  const uint8_t* const whi = uniform_ptr(S.w2);
   const uint8_t* wrow[ROWS];
   bool rv[ROWS];
 #pragma unroll
@@ -94,18 +98,20 @@ __global__ __launch_bounds__(256) void fused_lean_kernel(const LeanFused P) {
     rv[i] = v < srows;
     bool up;
     const int ph = phys(rv[i] ? v : srows - 1, up);
-    wrow[i] = (up ? S.w2 : S.w) + (size_t)ph * S.w_row;
+    wrow[i] = (up ? whi : wlo) + (size_t)ph * S.w_row;
   }
   const f16_t* srow[NS];
   bool sv[NS];
   if constexpr (kInt4) {
+    const f16_t* const slo = uniform_ptr(S.s);
+    const f16_t* const shi = uniform_ptr(S.s2);
 #pragma unroll
     for (int k = 0; k < NS; k++) {
       const int v = lr0 + rs_row<ROWS>(l, GLEV, k) * SUBS + sub;
       sv[k] = v < srows;
       bool up;
       const int ph = phys(sv[k] ? v : srows - 1, up);
-      srow[k] = (up ? S.s2 : S.s) + (size_t)ph * S.s_row;
+      srow[k] = (up ? shi : slo) + (size_t)ph * S.s_row;
     }
   }
   auto fetch = [&](int r, Raw<B>* w, f16_t* sc) {
@@ -118,6 +124,33 @@ __global__ __launch_bounds__(256) void fused_lean_kernel(const LeanFused P) {
       for (int k = 0; k < NS; k++) sc[k] = srow[k][j >> 2];
     }
   };
+  // ---- the prologue's inputs are requested before round 0 of the weights, so that
+  // waiting for them never waits for the weight stream
+  __shared__ float red[4];
+  const int n = cols;
+  constexpr int kHeld = 16;   // prologue elements per thread (cols <= 4096)
+  uint16_t ra[kHeld], rb[kHeld], rw[kHeld];
+  if constexpr (PRO != Pro::kLoad) {
+    const uint16_t* pa;
+    if constexpr (PRO == Pro::kEmbedNorm) {
+      int64_t t = P.token[0];
+      t = t < 0 ? 0 : (t >= P.vocab ? P.vocab - 1 : t);
+      pa = reinterpret_cast<const uint16_t*>(P.embed) + t * P.embed_row;
+    } else {
+      pa = reinterpret_cast<const uint16_t*>(P.left);
+    }
+    const uint16_t* pb = reinterpret_cast<const uint16_t*>(P.right);
+    const uint16_t* pw = reinterpret_cast<const uint16_t*>(P.norm_w);
+#pragma unroll
+    for (int k = 0; k < kHeld; k++) {
+      const int i = threadIdx.x + 256 * k;
+      const int ic = i < n ? i : n - 1;
+      ra[k] = pa[ic];
+      if constexpr (PRO != Pro::kEmbedNorm) rb[k] = pb[ic];
+      rw[k] = pw[ic];
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
   Raw<B> wc[ROWS];
   f16_t sc[NS];
   fetch(0, wc, sc);   // in bounds for inactive waves too (rows clamped)
@@ -131,31 +164,8 @@ __global__ __launch_bounds__(256) void fused_lean_kernel(const LeanFused P) {
     // RMSNorm of the residual stream with the thread partition, reduction order and
     // rounding points of the standalone rms_norm / add_rms_norm kernels; workgroup 0
     // stores the residual.
-    __shared__ float red[4];
-    const int n = cols;
-    constexpr int kHeld = 16;
-    const uint16_t* pa;
-    if constexpr (PRO == Pro::kEmbedNorm) {
-      int64_t t = P.token[0];
-      t = t < 0 ? 0 : (t >= P.vocab ? P.vocab - 1 : t);
-      pa = reinterpret_cast<const uint16_t*>(P.embed) + t * P.embed_row;
-    } else {
-      pa = reinterpret_cast<const uint16_t*>(P.left);
-    }
-    const uint16_t* pb = reinterpret_cast<const uint16_t*>(P.right);
-    const uint16_t* pw = reinterpret_cast<const uint16_t*>(P.norm_w);
     const bool writer = blockIdx.x == 0 && P.residual_out != nullptr;
     XT* xl = reinterpret_cast<XT*>(xs_lds);
-    uint16_t ra[kHeld], rb[kHeld], rw[kHeld];
-#pragma unroll
-    for (int k = 0; k < kHeld; k++) {
-      const int i = threadIdx.x + 256 * k;
-      const int ic = i < n ? i : n - 1;
-      ra[k] = pa[ic];
-      if constexpr (PRO != Pro::kEmbedNorm) rb[k] = pb[ic];
-      rw[k] = pw[ic];
-    }
-    __builtin_amdgcn_sched_barrier(0);
     float rr[kHeld];
     float ss = 0.0f;
 #pragma unroll

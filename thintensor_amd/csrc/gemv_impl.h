@@ -304,6 +304,34 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
     }
   }
 
+  // The RMSNorm prologue's inputs (cols <= 256 * kHeld) are requested here too, ahead of
+  // the weights, as raw bits: indices past cols clamp to cols - 1 (values discarded), so
+  // no branch separates the loads and waiting for them never waits for the weight stream.
+  constexpr int kHeld = 16;   // prologue elements per thread kept in registers
+  uint16_t ra[kHeld], rb[kHeld], rw[kHeld];
+  if constexpr (PRO != Pro::kLoad) {
+    const int n = P.cols;
+    const uint16_t* pa;
+    if constexpr (PRO == Pro::kEmbedNorm) {
+      int64_t t = P.f.token[0];
+      t = t < 0 ? 0 : (t >= P.f.vocab ? P.f.vocab - 1 : t);
+      pa = reinterpret_cast<const uint16_t*>(P.f.embed) + t * P.f.embed_row;
+    } else {
+      pa = reinterpret_cast<const uint16_t*>(P.f.left);
+    }
+    const uint16_t* pb = reinterpret_cast<const uint16_t*>(P.f.right);
+    const uint16_t* pw = reinterpret_cast<const uint16_t*>(P.f.norm_w);
+#pragma unroll
+    for (int k = 0; k < kHeld; k++) {
+      const int i = threadIdx.x + 256 * k;
+      const int ic = i < n ? i : n - 1;
+      ra[k] = pa[ic];
+      if constexpr (PRO != Pro::kEmbedNorm) rb[k] = pb[ic];
+      rw[k] = pw[ic];
+    }
+    __builtin_amdgcn_sched_barrier(0);   // raw bits only above: no use between the loads
+  }
+
   int b = blockIdx.x * (blockDim.x >> 6) + wave;
   Batch cb;
   setup(b, cb);
@@ -352,25 +380,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
       if constexpr (PRO == Pro::kAddNorm) return (r * inv) * w;
       else return (r * inv) * (w + 0.0f);
     };
-    constexpr int kHeld = 16;   // elements per thread kept in registers (cols <= 4096)
     if (n <= 256 * kHeld) {
-      // one pass over memory: every residual and weight load is issued before any is
-      // used (indices past n clamp to n - 1 and their values are discarded), so the
-      // prologue waits for memory once
-      uint16_t ra[kHeld], rb[kHeld], rw[kHeld];
-      const uint16_t* pa = PRO == Pro::kEmbedNorm ? reinterpret_cast<const uint16_t*>(erow)
-                                                  : reinterpret_cast<const uint16_t*>(P.f.left);
-      const uint16_t* pb = reinterpret_cast<const uint16_t*>(P.f.right);
-      const uint16_t* pw = reinterpret_cast<const uint16_t*>(P.f.norm_w);
-#pragma unroll
-      for (int k = 0; k < kHeld; k++) {
-        const int i = threadIdx.x + 256 * k;
-        const int ic = i < n ? i : n - 1;
-        ra[k] = pa[ic];
-        if constexpr (PRO != Pro::kEmbedNorm) rb[k] = pb[ic];
-        rw[k] = pw[ic];
-      }
-      __builtin_amdgcn_sched_barrier(0);   // raw bits only above: no use between the loads
+      // one pass over memory: the raw bits requested before the weights
       float rr[kHeld], wn[kHeld];
 #pragma unroll
       for (int k = 0; k < kHeld; k++) {

@@ -45,6 +45,19 @@ template <> struct Store<bf16_t> { __device__ static void st(bf16_t* p, float v)
 template <> struct Store<float> { __device__ static void st(float* p, float v) { *p = v; } };
 template <typename T> __device__ __forceinline__ void store(T* p, float v) { Store<T>::st(p, v); }
 
+// A wave-uniform pointer pinned to scalar registers.  A per-lane choice between two such
+// pointers then compiles to a select; without it the compiler may instead turn the choice
+// into a vector load of whichever kernel argument the lane picked, which queues behind
+// every load issued before it.
+template <typename T> __device__ __forceinline__ T* uniform_ptr(T* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  // through the global address space, so that loads from it stay global (not flat) loads
+  typedef __attribute__((address_space(1))) T GlobalT;
+  return (T*)reinterpret_cast<GlobalT*>(((uint64_t)hi << 32) | lo);
+}
+
 // Round a value to the storage precision of T and return it as float.
 template <typename T> __device__ __forceinline__ float round_to(float v);
 template <> __device__ __forceinline__ float round_to<f16_t>(float v) { return round_f16(v); }
