@@ -264,6 +264,19 @@ int tt_moe_router_matvec_topk(const void* weight, int w_dtype, int64_t w_row, co
                               int64_t experts, int64_t top_k, int renormalize, int32_t* indices_out,
                               void* scores_out, int score_dtype, void* stream);
 
+/* add_rms_norm followed by moe_router_matvec_topk on its output, in one launch when
+ * experts <= 32, hidden_size <= 4096 and the activations, norm weight and norm output share
+ * an fp16/bf16 dtype (otherwise the two operators run one after the other).  Outputs and
+ * bits are those of tt_add_rms_norm then tt_moe_router_matvec_topk(hidden = norm_out).
+ * Fuses the reference's add_rms_norm (triton_kernels.py:5646-5667) and
+ * moe_router_matvec_topk (:5826-5860) as its MoE layer calls them back to back
+ * (gpu_runtime.py:9465-9513); the reference has no single entry point for the pair. */
+int tt_add_rms_norm_router_topk(const void* left, const void* right, void* residual_out, int x_dtype,
+                                const void* norm_weight, int norm_w_dtype, void* norm_out, int norm_dtype,
+                                int64_t hidden_size, float eps, const void* weight, int w_dtype, int64_t w_row,
+                                const void* bias, int bias_dtype, int64_t experts, int64_t top_k, int renormalize,
+                                int32_t* indices_out, void* scores_out, int score_dtype, void* stream);
+
 /* Top-k + softmax on given logits.  Replaces TritonDecodeBackend.moe_router_topk
  * (triton_kernels.py:5803-5824; kernel :2821-2851). */
 int tt_moe_router_topk(const void* logits, int logits_dtype, int64_t experts, int64_t top_k, int renormalize,

@@ -8,7 +8,7 @@ import pytest
 import torch
 
 import oracle
-from tests.helpers import f16_normal, from_torch_bits, rng, to_torch
+from tests.helpers import bf16_bits, f16_normal, from_torch_bits, rng, to_torch
 from tests.test_gemv_gpu import assert_bits_equal, lanes
 
 pytestmark = pytest.mark.gpu
@@ -30,9 +30,12 @@ def test_rms_norm(backend, device, n, offset):
     assert_bits_equal(from_torch_bits(out), want, "rms_norm")
 
 
-@pytest.mark.parametrize("n", [2048, 2880])
-def test_add_rms_norm(backend, device, n):
-    g = rng(n + 1)
+@pytest.mark.parametrize("n,seed", [(2048, 0), (2880, 0), (4096, 1), (5120, 0), (5120, 2), (8192, 3)])
+def test_add_rms_norm(backend, device, n, seed):
+    # ~27k outputs in all: a conversion that rounds the normalized product once,
+    # straight to fp16, instead of to binary32 first differs in about one output of
+    # several thousand, so these sizes catch it
+    g = rng(n + 1 + 1000 * seed)
     a, b = f16_normal(g, n), f16_normal(g, n, 0.5)
     w = f16_normal(g, n, 0.1)
     res = torch.empty(n, device=device, dtype=torch.float16)
@@ -134,6 +137,51 @@ def test_router(backend, device, renorm, with_bias):
     oracle.lib().tto_router(P(w), oracle.F16, H, P(x), oracle.F16, H, P(b) if with_bias else None, oracle.F16, E, k,
                             int(renorm), P(widx), P(wsc), oracle.F16)
     assert np.array_equal(idx.cpu().numpy(), widx)
+    assert_bits_equal(from_torch_bits(sc), wsc, "router scores")
+
+
+@pytest.mark.parametrize("E,H,k,renorm,bias_dtype,wbf16", [
+    (32, 2880, 4, True, "f16", False),    # gpt-oss router: one launch
+    (8, 2048, 2, False, None, False),
+    (32, 4096, 8, True, "bf16", True),    # largest one-launch hidden size, bf16 router weight
+    (1, 64, 1, True, "f32", False),
+    (17, 2080, 3, False, "f16", False),   # ragged second round of chunks
+    (64, 2880, 4, True, "f16", False),    # more experts than one launch takes: two launches
+    (32, 5120, 4, True, None, False),     # hidden above 4096: two launches
+])
+def test_add_rms_norm_router(backend, device, E, H, k, renorm, bias_dtype, wbf16):
+    """The combined launch equals add_rms_norm followed by the router on its output."""
+    g = rng(E * 7 + H + k)
+    a, b = f16_normal(g, H), f16_normal(g, H, 0.5)
+    nw = f16_normal(g, H, 0.1)
+    wf = (g.standard_normal((E, H)) * 0.05).astype(np.float32)
+    w = bf16_bits(wf) if wbf16 else wf.astype(np.float16)
+    bias = None
+    if bias_dtype == "f16":
+        bias = f16_normal(g, E, 0.1)
+    elif bias_dtype == "bf16":
+        bias = bf16_bits(g.standard_normal(E).astype(np.float32) * 0.1)
+    elif bias_dtype == "f32":
+        bias = (g.standard_normal(E) * 0.1).astype(np.float32)
+    bcode = {"f16": oracle.F16, "bf16": oracle.BF16, "f32": oracle.F32, None: oracle.F16}[bias_dtype]
+    res = torch.empty(H, device=device, dtype=torch.float16)
+    normed = torch.empty(H, device=device, dtype=torch.float16)
+    idx = torch.empty(k, device=device, dtype=torch.int32)
+    sc = torch.empty(k, device=device, dtype=torch.float16)
+    backend.add_rms_norm_router_topk(to_torch(a, device), to_torch(b, device), res, to_torch(nw, device), normed, 1e-5,
+                                     to_torch(w, device, bf16=wbf16), idx, sc,
+                                     bias=None if bias is None else to_torch(bias, device, bf16=bias_dtype == "bf16"),
+                                     renormalize=renorm)
+    want_res = np.empty(H, dtype=np.float16)
+    want_n = np.empty(H, dtype=np.float16)
+    oracle.lib().tto_add_rms_norm(P(a), P(b), P(want_res), oracle.F16, P(nw), oracle.F16, P(want_n), oracle.F16, H, 1e-5)
+    widx = np.empty(k, dtype=np.int32)
+    wsc = np.empty(k, dtype=np.float16)
+    oracle.lib().tto_router(P(w), oracle.BF16 if wbf16 else oracle.F16, H, P(want_n), oracle.F16, H,
+                            None if bias is None else P(bias), bcode, E, k, int(renorm), P(widx), P(wsc), oracle.F16)
+    assert_bits_equal(from_torch_bits(res), want_res, "residual")
+    assert_bits_equal(from_torch_bits(normed), want_n, "normed")
+    assert np.array_equal(idx.cpu().numpy(), widx), (idx.cpu().numpy(), widx)
     assert_bits_equal(from_torch_bits(sc), wsc, "router scores")
 
 

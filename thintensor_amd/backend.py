@@ -732,6 +732,53 @@ class HipDecodeBackend:
         _lib.check(rc, "moe_router_matvec_topk")
         return indices_out, scores_out
 
+    def add_rms_norm_router_topk(
+        self,
+        left: torch.Tensor,
+        right: torch.Tensor,
+        residual_out: torch.Tensor,
+        norm_weight: torch.Tensor,
+        norm_out: torch.Tensor,
+        eps: float,
+        router_weight: torch.Tensor,
+        indices_out: torch.Tensor,
+        scores_out: torch.Tensor,
+        *,
+        bias: torch.Tensor | None = None,
+        renormalize: bool,
+    ) -> tuple[torch.Tensor, torch.Tensor]:
+        """``add_rms_norm`` then ``moe_router_matvec_topk`` on its output, as one launch
+        where the shapes allow (<= 32 experts, hidden <= 4096, one activation dtype).
+
+        No single reference operator: the reference's MoE layer calls add_rms_norm
+        (triton_kernels.py:5646-5667) and moe_router_matvec_topk (:5826-5860) back to
+        back (gpu_runtime.py:9465-9513).  Outputs and bits equal that pair's."""
+        n = left.numel()
+        if any(t.numel() != n for t in (right, residual_out, norm_weight, norm_out)):
+            raise ValueError("add_rms_norm size mismatch")
+        if right.dtype != left.dtype or residual_out.dtype != left.dtype:
+            raise ValueError("add_rms_norm: left, right and residual_out must share a dtype")
+        experts, hidden_size = map(int, router_weight.shape)
+        if hidden_size != n:
+            raise ValueError("router hidden vector does not match weight shape")
+        if experts > 128:
+            raise ValueError("fused router supports at most 128 experts")
+        if bias is not None and int(bias.numel()) != experts:
+            raise ValueError("router bias does not match expert count")
+        self._check_indices(indices_out)
+        _require_cuda(left, right, residual_out, norm_weight, norm_out, router_weight, indices_out, scores_out)
+        rc = self.lib.tt_add_rms_norm_router_topk(
+            left.data_ptr(), right.data_ptr(), residual_out.data_ptr(), _code(left, "add_rms_norm"),
+            norm_weight.data_ptr(), _code(norm_weight, "add_rms_norm"), norm_out.data_ptr(),
+            _code(norm_out, "add_rms_norm"), n, float(eps), router_weight.data_ptr(), _code(router_weight, "router"),
+            router_weight.stride(0), bias.data_ptr() if bias is not None else None,
+            _code(bias, "bias") if bias is not None else _lib.F32, experts, int(indices_out.numel()),
+            int(bool(renormalize)), indices_out.data_ptr(), scores_out.data_ptr(), _code(scores_out, "scores"),
+            _stream(left),
+        )
+        _lib.check(rc, "add_rms_norm_router_topk")
+        return indices_out, scores_out
+
     def moe_router_topk(self, logits: torch.Tensor, indices_out: torch.Tensor, scores_out: torch.Tensor, *,
                         renormalize: bool) -> tuple[torch.Tensor, torch.Tensor]:
         """(triton_kernels.py:5803-5824)"""

@@ -191,6 +191,165 @@ __global__ __launch_bounds__(1024) void router_kernel(const void* w, int64_t w_r
   }
 }
 
+// add+RMSNorm and the router on its output in one workgroup (E <= 32, H <= 4096, one
+// activation dtype).  Every wave requests the weight rows of its two experts (wave and
+// wave + 16) and their bias right after the norm inputs (16-byte pieces staged through
+// LDS); waves 0-3 form the residual and the normalized vector with the thread
+// partition, reduction order and rounding points of add_rms_norm_kernel (ops.hip)
+// while the weights are still arriving.  The normalized vector is stored
+// (norm_out, residual_out) and kept in LDS, from which the router rows read their
+// activations.  Same bits as tt_add_rms_norm followed by tt_moe_router_matvec_topk on
+// norm_out.
+struct NormRouterParams {
+  const void* left;
+  const void* right;
+  void* residual_out;
+  const void* norm_w;
+  void* norm_out;
+  const void* w;       // router weight [E, H], row stride w_row elements
+  const void* bias;    // [E] or nullptr
+  int32_t* idx_out;
+  void* score_out;
+  int64_t w_row;
+  float eps;
+  int H, E, top_k, renorm;
+};
+
+constexpr int kNormRouterExperts = 32;   // 16 waves x 2 experts
+
+template <typename WT, typename XT, typename BT, typename OT>
+__global__ __launch_bounds__(1024) void norm_router_kernel(const NormRouterParams P) {
+  constexpr Fmt F = std::is_same_v<WT, bf16_t> ? Fmt::kBF16W : Fmt::kF16W;
+  constexpr int kHeld = 16;   // norm elements per thread of waves 0-3 (H <= 4096)
+  __shared__ float red[4];
+  __shared__ float logits[kNormRouterExperts];
+  __shared__ uint4 xs[4096 / 8];   // normalized vector, XT bits
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int n = P.H;
+  const int nchunks = n >> 5;
+  const bool norm_wave = wave < 4;
+
+  // ---- every load before the first wait: the norm inputs as 16-byte pieces (threads
+  // 0-511, one piece of each vector; n <= 4096), then this wave's router rows and bias
+  __shared__ uint4 raw_a[512], raw_b[512], raw_w[512];   // left, right, norm weight (raw bits)
+  static_assert(kHeld * 256 == 512 * 8, "the staging buffers hold whole vectors");
+  const int nq = n >> 3;
+  // every thread loads (threads past the vector repeat its last piece), so no branch
+  // separates these loads from the weight loads below
+  const int q = (int)threadIdx.x < nq ? (int)threadIdx.x : nq - 1;
+  const uint4 in_a = reinterpret_cast<const uint4*>(P.left)[q];
+  const uint4 in_b = reinterpret_cast<const uint4*>(P.right)[q];
+  const uint4 in_w = reinterpret_cast<const uint4*>(P.norm_w)[q];
+  Raw<64> wr[2][2];
+#pragma unroll
+  for (int r = 0; r < 2; r++) {
+    int j = r * 64 + lane;
+    j = j < nchunks ? j : nchunks - 1;
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+      int e = wave + 16 * k;
+      e = e < P.E ? e : P.E - 1;
+      wr[k][r] = load_raw<64>(reinterpret_cast<const uint8_t*>(P.w) + ((int64_t)e * P.w_row + 32 * j) * 2);
+    }
+  }
+  // bias loads without a branch: with no bias they read (and discard) the first elements
+  // of the weight matrix, which holds at least E * H >= 2E halves
+  const BT* bsrc = reinterpret_cast<const BT*>(P.bias != nullptr ? P.bias : P.w);
+  BT braw[2];
+#pragma unroll
+  for (int k = 0; k < 2; k++) {
+    const int e = wave + 16 * k;
+    braw[k] = bsrc[e < P.E ? e : P.E - 1];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  if ((int)threadIdx.x < nq) {
+    raw_a[threadIdx.x] = in_a;
+    raw_b[threadIdx.x] = in_b;
+    raw_w[threadIdx.x] = in_w;
+  }
+  __syncthreads();
+
+  // ---- add + RMSNorm in add_rms_norm_kernel's partition and order: thread t of waves
+  // 0-3 takes elements t + 256k, fma chain over k, wave butterfly, (w0 + w1) + (w2 + w3)
+  const XT* la = reinterpret_cast<const XT*>(raw_a);
+  const XT* lb = reinterpret_cast<const XT*>(raw_b);
+  const XT* lw = reinterpret_cast<const XT*>(raw_w);
+  float res[kHeld];
+  if (norm_wave) {
+    XT va[kHeld], vb[kHeld];
+#pragma unroll
+    for (int k = 0; k < kHeld; k++) {
+      const int i = threadIdx.x + 256 * k;
+      const int ic = i < n ? i : n - 1;
+      va[k] = la[ic];
+      vb[k] = lb[ic];
+    }
+    __builtin_amdgcn_sched_barrier(0);   // every LDS read issued before the first use
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kHeld; k++) {
+      res[k] = round_bf16(to_f32(va[k]) + to_f32(vb[k]));
+      if (threadIdx.x + 256 * k < n) ss = __builtin_fmaf(res[k], res[k], ss);
+    }
+    ss = xor_sum(ss, 1, 64);
+    if (lane == 0) red[wave] = ss;
+  }
+  __syncthreads();
+  if (norm_wave) {
+    const float total = (red[0] + red[1]) + (red[2] + red[3]);
+    const float inv = 1.0f / __builtin_sqrtf(total / (float)n + P.eps);
+    XT* xl = reinterpret_cast<XT*>(xs);
+#pragma unroll
+    for (int k = 0; k < kHeld; k++) {
+      const int i = threadIdx.x + 256 * k;
+      if (i < n) {
+        const float v = (res[k] * inv) * to_f32(lw[i]);
+        store<XT>(reinterpret_cast<XT*>(P.residual_out) + i, res[k]);
+        store<XT>(reinterpret_cast<XT*>(P.norm_out) + i, v);
+        store<XT>(xl + i, v);
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- router rows (router_rows_held's arithmetic) on the normalized vector from LDS
+  float acc[2];
+#pragma unroll
+  for (int r = 0; r < 2; r++) {
+    int j = r * 64 + lane;
+    j = j < nchunks ? j : nchunks - 1;
+    Raw<64> xr;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const uint4 v = xs[j * 4 + q];
+      xr.w[4 * q] = v.x;
+      xr.w[4 * q + 1] = v.y;
+      xr.w[4 * q + 2] = v.z;
+      xr.w[4 * q + 3] = v.w;
+    }
+    const bool cv = r * 64 + lane < nchunks;
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+      const float p = chunk_dot<F, XT>(wr[k][r], xr.w);
+      if (r == 0) acc[k] = 0.0f + (cv ? p : 0.0f);
+      else if (nchunks > 64) acc[k] = acc[k] + (cv ? p : 0.0f);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 2; k++) {
+    float v = round_bf16(xor_sum(acc[k], 1, 64));
+    if (P.bias != nullptr) v = round_bf16(v + to_f32(braw[k]));
+    const int e = wave + 16 * k;
+    if (e < P.E && lane == 0) logits[e] = v;
+  }
+  __syncthreads();
+  if (wave == 0) {
+    const float l0 = lane < P.E ? logits[lane] : 0.0f;
+    wave_topk<OT>(l0, 0.0f, P.E, P.top_k, P.renorm != 0, P.idx_out, reinterpret_cast<OT*>(P.score_out));
+  }
+}
+
 template <typename LT, typename OT>
 __global__ __launch_bounds__(64) void topk_kernel(const void* logits_in, int E, int top_k, int renorm, int32_t* idx_out,
                                                   void* score_out) {
@@ -258,6 +417,53 @@ extern "C" int tt_moe_router_topk(const void* logits, int logits_dtype, int64_t 
       hipLaunchKernelGGL((topk_kernel<LT, OT>), dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream), logits,
                          (int)experts, (int)top_k, renormalize, indices_out, scores_out);
       return check_launch(what);
+    });
+  });
+}
+
+extern "C" int tt_add_rms_norm_router_topk(const void* left, const void* right, void* residual_out, int x_dtype,
+                                           const void* norm_weight, int norm_w_dtype, void* norm_out, int norm_dtype,
+                                           int64_t hidden_size, float eps, const void* weight, int w_dtype,
+                                           int64_t w_row, const void* bias, int bias_dtype, int64_t experts,
+                                           int64_t top_k, int renormalize, int32_t* indices_out, void* scores_out,
+                                           int score_dtype, void* stream) {
+  const char* what = "add_rms_norm_router_topk";
+  TT_REQUIRE(left && right && residual_out && norm_weight && norm_out, "%s: null pointer", what);
+  const bool one_launch = experts <= kNormRouterExperts && hidden_size <= 4096 && hidden_size % 32 == 0 && hidden_size > 0 &&
+                          x_dtype != TT_F32 && norm_w_dtype == x_dtype && norm_dtype == x_dtype &&
+                          (w_dtype == TT_F16 || w_dtype == TT_BF16) && weight && indices_out && scores_out &&
+                          aligned(weight, 16) && w_row % 8 == 0 && experts > 0 && top_k > 0 && top_k <= experts;
+  if (!one_launch) {
+    // the two operators, each with its own checks
+    const int rc = tt_add_rms_norm(left, right, residual_out, x_dtype, norm_weight, norm_w_dtype, norm_out, norm_dtype,
+                                   hidden_size, eps, stream);
+    if (rc != TT_OK) return rc;
+    return tt_moe_router_matvec_topk(weight, w_dtype, w_row, norm_out, norm_dtype, hidden_size, bias, bias_dtype,
+                                     experts, top_k, renormalize, indices_out, scores_out, score_dtype, stream);
+  }
+  NormRouterParams P;
+  P.left = left; P.right = right; P.residual_out = residual_out; P.norm_w = norm_weight; P.norm_out = norm_out;
+  P.w = weight; P.bias = bias; P.idx_out = indices_out; P.score_out = scores_out; P.w_row = w_row; P.eps = eps;
+  P.H = (int)hidden_size; P.E = (int)experts; P.top_k = (int)top_k; P.renorm = renormalize;
+  const int bdt = bias ? bias_dtype : TT_F32;
+  return dt3(w_dtype, [&](auto wt) {
+    using WT = decltype(wt);
+    return dt3(x_dtype, [&](auto xt) {
+      using XT = decltype(xt);
+      return dt3(bdt, [&](auto bt) {
+        using BT = decltype(bt);
+        return dt3(score_dtype, [&](auto ot) {
+          using OT = decltype(ot);
+          if constexpr (std::is_same_v<WT, float> || std::is_same_v<XT, float>) {
+            set_error("%s: unsupported dtypes", what);
+            return TT_ERR_UNSUPPORTED;
+          } else {
+            hipLaunchKernelGGL((norm_router_kernel<WT, XT, BT, OT>), dim3(1), dim3(1024), 0,
+                               static_cast<hipStream_t>(stream), P);
+            return check_launch(what);
+          }
+        });
+      });
     });
   });
 }

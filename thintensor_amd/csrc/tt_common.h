@@ -27,7 +27,16 @@ __device__ __forceinline__ float to_f32(f16_t v) { return (float)__builtin_bit_c
 __device__ __forceinline__ float to_f32(bf16_t v) { return __builtin_bit_cast(float, (uint32_t)v.bits << 16); }
 __device__ __forceinline__ float to_f32(float v) { return v; }
 
-__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+// A binary32 value pinned in a register.  Every conversion to fp16 goes through it:
+// otherwise the compiler may fold the product or sum that feeds the conversion into one
+// mixed-precision fma with an fp16 result (v_fma_mixlo_f16), which rounds once, straight
+// to fp16, where the reference rounds to binary32 first and then to fp16 (the two
+// differ when the binary32 rounding lands on an fp16 halfway point).
+__device__ __forceinline__ float pin_f32(float f) {
+  asm("" : "+v"(f));
+  return f;
+}
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) { return __builtin_bit_cast(uint16_t, (_Float16)pin_f32(f)); }
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
   uint32_t u = __builtin_bit_cast(uint32_t, f);
   if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);  // quiet NaN
@@ -37,7 +46,7 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
 // Round a binary32 value to bfloat16 and back (used where the reference rounds
 // through bfloat16 regardless of the activation dtype).
 __device__ __forceinline__ float round_bf16(float f) { return __builtin_bit_cast(float, (uint32_t)f32_to_bf16_bits(f) << 16); }
-__device__ __forceinline__ float round_f16(float f) { return (float)(_Float16)f; }
+__device__ __forceinline__ float round_f16(float f) { return (float)(_Float16)pin_f32(f); }
 
 template <typename T> struct Store;
 template <> struct Store<f16_t> { __device__ static void st(f16_t* p, float v) { p->bits = f32_to_f16_bits(v); } };

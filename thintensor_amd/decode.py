@@ -267,8 +267,9 @@ class MoEDecoder(_GraphedDecoder):
     """gpt-oss-20B-shaped decoder with MXFP4 experts, fp16 attention with sinks.
 
     ``fused=True`` folds the embedding / residual add + RMSNorm into the QKV launch,
-    RoPE and the KV append into its epilogue, and the final add + RMSNorm, token log
-    and position advance into the lm_head launches, with the unfused rounding points."""
+    RoPE and the KV append into its epilogue, the post-attention add + RMSNorm into the
+    router launch, and the final add + RMSNorm, token log and position advance into the
+    lm_head launches, with the unfused rounding points."""
 
     def __init__(self, backend: HipDecodeBackend, weights: MoEWeights, fused: bool = False) -> None:
         s = weights.shape
@@ -362,9 +363,9 @@ class MoEDecoder(_GraphedDecoder):
             be.single_token_gqa_attention(q, w.k_cache[li], w.v_cache[li], self.attn, s.heads, s.kv_heads,
                                           s.head_dim, sinks=L.sinks, active_tokens=(self.position, 1))
             be.multi_matvec_bias((L.o,), (L.o_bias,), self.attn, self.attn_out)
-            be.add_rms_norm(self.hidden_a, self.attn_out, self.hidden_b, L.ln2, self.normed, s.eps)
-            be.moe_router_matvec_topk(L.router, self.normed, self.router_idx, self.router_scores, bias=L.router_bias,
-                                      renormalize=True)
+            be.add_rms_norm_router_topk(self.hidden_a, self.attn_out, self.hidden_b, L.ln2, self.normed, s.eps,
+                                        L.router, self.router_idx, self.router_scores, bias=L.router_bias,
+                                        renormalize=True)
             be.mxfp_lowbit_selected_swiglu(L.gate_up_blocks, L.gate_up_scales, self.normed, self.router_idx, self.act,
                                            bits=4, alpha=s.swiglu_alpha, limit=s.swiglu_limit, bias=L.gate_up_bias)
             be.mxfp_lowbit_weighted_down(L.down_blocks, L.down_scales, self.act, self.router_idx, self.router_scores,
