@@ -1,0 +1,73 @@
+// Shared parameter blocks and helpers of the fused MoE expert kernels: gate/up GEMV + gpt-oss SwiGLU on interleaved rows and
+// down GEMV + router-weighted sum, for E8M0 block-scaled formats (q1, q2, MXFP4).
+// Expert ids and router scores are read on the device (no host synchronisation).
+//
+// RT is the precision the reference rounds the GEMV results and bias sums through:
+// bfloat16 for the reference's fused low-bit kernels (triton_kernels.py:1319-1333,
+// 1421-1434), the activation dtype for the MXFP4 chain that the reference runs as
+// separate kernels plus torch adds (gpu_runtime.py:9647-9704, 9855-9903).
+#pragma once
+
+#include "gemv_impl.h"
+
+#include <type_traits>
+
+namespace tt {
+
+struct SwigluParams {
+  const uint8_t* w; int64_t w_expert, w_row;
+  const uint8_t* s; int64_t s_expert, s_row;
+  const void* x; int64_t x_slot;
+  const int32_t* experts;
+  const void* bias; int64_t bias_expert;
+  float alpha, limit;
+  void* out; int64_t out_slot;
+  int act_rows, cols;
+};
+
+template <typename BT> __device__ __forceinline__ float ld_bias(const void* b, int64_t i) {
+  return to_f32(reinterpret_cast<const BT*>(b)[i]);
+}
+
+
+struct DownParams {
+  const uint8_t* w; int64_t w_expert, w_row;
+  const uint8_t* s; int64_t s_expert, s_row;
+  const void* x; int64_t x_slot;
+  const int32_t* experts;
+  const void* scores;
+  const void* bias; int64_t bias_expert;
+  void* out;
+  int rows, cols, slots;
+  int bias_dtype, score_dtype;   // storage codes (TT_F16 / TT_BF16 / TT_F32)
+};
+
+// One element of a small vector (bias, router scores) whose storage type is a runtime
+// code: these are read once per row and slot, so a branch is cheaper than one more
+// template dimension.
+__device__ __forceinline__ float ld_typed(const void* p, int dtype, int64_t i) {
+  if (dtype == TT_F32) return reinterpret_cast<const float*>(p)[i];
+  const uint16_t b = reinterpret_cast<const uint16_t*>(p)[i];
+  return dtype == TT_BF16 ? to_f32(bf16_t{b}) : to_f32(f16_t{b});
+}
+
+
+template <typename T> struct DT;
+template <> struct DT<f16_t> { static constexpr int code = TT_F16; };
+template <> struct DT<bf16_t> { static constexpr int code = TT_BF16; };
+template <> struct DT<float> { static constexpr int code = TT_F32; };
+
+// Calls f.template operator()<T>() for the storage type matching `code`.
+template <typename Fn> static int with_type(int code, Fn&& f) {
+  switch (code) {
+    case TT_F16: return f(f16_t{});
+    case TT_BF16: return f(bf16_t{});
+    case TT_F32: return f(float{});
+  }
+  set_error("unsupported dtype code %d", code);
+  return TT_ERR_INVALID;
+}
+
+static Fmt fmt_for_bits(int bits) { return bits == 2 ? Fmt::kQ2E8 : (bits == 1 ? Fmt::kQ1E8 : Fmt::kMxfp4); }
+
+}  // namespace tt

@@ -1,0 +1,321 @@
+// Fused MoE down kernels: down GEMV of the selected experts + router-weighted sum in
+// slot order (E8M0 block-scaled q1, q2, MXFP4); expert ids and scores are read on the device.
+#include "moe_common.h"
+
+namespace tt {
+
+// One block owns RB = RPW * (64 / LPR) output rows.  Its four waves split the
+// selected slots (wave w computes slots w, w + 4, ...), each slot's row values
+// v = round(dot) (+ bias, rounded again) go to LDS, and after the barrier lane t of
+// the block combines row t in slot order: c = fma(v_s, score_s, c) from +0.
+template <Fmt F, typename XT, typename OT, typename RT, int LPR, int RPW>
+__global__ __launch_bounds__(256) void weighted_down_kernel(DownParams P) {
+  extern __shared__ uint32_t xs_lds[];
+  constexpr int SUBS = 64 / LPR;
+  constexpr int RB = RPW * SUBS;
+  const int words = P.cols >> 1;
+  float* vals = reinterpret_cast<float*>(xs_lds + P.slots * words);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nwaves = blockDim.x >> 6;
+  const int sub = lane / LPR, l = lane % LPR;
+  const int nchunks = P.cols >> 5;
+  const int row0 = blockIdx.x * RB;
+  int row[RPW];
+  bool rv[RPW];
+#pragma unroll
+  for (int i = 0; i < RPW; i++) {
+    row[i] = row0 + i * SUBS + sub;
+    rv[i] = row[i] < P.rows;
+  }
+  const uint8_t* wrow[RPW];
+  const uint8_t* srow[RPW];
+  int64_t e = 0;
+  auto point = [&](int s) {
+    e = P.experts[s];
+#pragma unroll
+    for (int i = 0; i < RPW; i++) {
+      wrow[i] = P.w + e * P.w_expert + (int64_t)row[i] * P.w_row;
+      srow[i] = P.s + e * P.s_expert + (int64_t)row[i] * P.s_row;
+    }
+  };
+  E8Round<F, RPW> cur;
+  int s = wave;
+  if (s < P.slots) {
+    point(s);
+    e8_fetch<F, LPR, RPW>(cur, 0, l, nchunks, wrow, srow, rv);
+  }
+  for (int t = 0; t < P.slots; t++) {
+    const uint32_t* xg = reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(P.x) + (int64_t)t * P.x_slot);
+    for (int i = threadIdx.x; i < words; i += blockDim.x) xs_lds[t * words + i] = xg[i];
+  }
+  __syncthreads();
+  for (; s < P.slots; s += nwaves) {
+    if (s != wave) {
+      point(s);
+      e8_fetch<F, LPR, RPW>(cur, 0, l, nchunks, wrow, srow, rv);
+    }
+    float dot[RPW];
+    e8_rows_dot<F, XT, LPR, RPW>(cur, wrow, srow, rv, xs_lds + s * words, nchunks, l, dot);
+#pragma unroll
+    for (int i = 0; i < RPW; i++) {
+      if (l != i || !rv[i]) continue;
+      float v = round_to<RT>(dot[i]);
+      if (P.bias != nullptr) v = round_to<RT>(v + ld_typed(P.bias, P.bias_dtype, e * P.bias_expert + row[i]));
+      vals[s * RB + i * SUBS + sub] = v;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < RB && row0 + (int)threadIdx.x < P.rows) {
+    float c = 0.0f;
+    for (int t = 0; t < P.slots; t++) c = __builtin_fmaf(vals[t * RB + threadIdx.x], ld_typed(P.scores, P.score_dtype, t), c);
+    store<OT>(reinterpret_cast<OT*>(P.out) + row0 + threadIdx.x, c);
+  }
+}
+
+// ------------------------------------------------------------------ lean variants
+// Same arithmetic as swiglu_kernel / weighted_down_kernel, laid out like the lean GEMV
+// (gemv_lean.h): one batch per wave, every load of a round issued before its first
+// use, the next round in flight while one is consumed, and the cross-row work done in
+// registers after one reduce-scatter.
+
+// Weighted down: every wave computes its ROWS rows (per lane group) for all S selected
+// slots; after the reduction the lane holding a row folds the slots in slot order:
+// c = fma(v_s, score_s, c) from +0.  The grid is small (one row per lane group), so
+// latency is hidden inside each wave: the slots' activations are requested first
+// (into registers, then LDS), then R rounds of every slot's weights at once.
+template <Fmt F, typename XT, typename OT, typename RT, int LPR, int ROWS, int S>
+__global__ __launch_bounds__(256) void down_lean_kernel(const DownParams P) {
+  constexpr int B = FmtInfo<F>::kBytes;
+  constexpr int SUBS = 64 / LPR;
+  constexpr int R = 16 / (S * ROWS) < 1 ? 1 : (16 / (S * ROWS) > 4 ? 4 : 16 / (S * ROWS));   // rounds in flight
+  constexpr int kXR = 4;   // 16-byte activation pieces per thread per register array (two arrays)
+  extern __shared__ uint32_t xs_lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int sub = lane / LPR, l = lane % LPR;
+  const int nchunks = P.cols >> 5;
+  const int rounds = (nchunks + LPR - 1) / LPR;
+  const int words = P.cols >> 1;
+  const int n0 = (int)(blockIdx.x * 4 + wave) * (ROWS * SUBS);
+
+  // activations: piece idx of the LDS copy (slot t at piece t * xn) is piece idx - t * xn
+  // of slot t; the first 256 * 2 * kXR pieces through registers, indices clamped
+  const int xn = P.cols >> 3;
+  const int xtotal = xn * S;
+  // (two arrays of four: one array of eight is kept in scratch memory by the compiler)
+  uint4 xra[kXR], xrb[kXR];
+  int xidx[2 * kXR];
+  auto xload = [&](int k) -> uint4 {
+    const int idx = threadIdx.x + 256 * k;
+    xidx[k] = idx < xtotal ? idx : xtotal - 1;
+    int t = 0;
+#pragma unroll
+    for (int q = 1; q < S; q++) t += xidx[k] >= q * xn ? 1 : 0;
+    const uint4* xg = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(P.x) + (int64_t)t * P.x_slot);
+    return xg[xidx[k] - t * xn];
+  };
+#pragma unroll
+  for (int k = 0; k < kXR; k++) xra[k] = xload(k);
+#pragma unroll
+  for (int k = 0; k < kXR; k++) xrb[k] = xload(kXR + k);
+
+  int64_t e[S];
+#pragma unroll
+  for (int s = 0; s < S; s++) e[s] = P.experts[s];
+  const uint8_t* wrow[S][ROWS];
+  const uint8_t* srow[S][ROWS];
+  bool rv[ROWS];
+  int rcl[ROWS];
+#pragma unroll
+  for (int i = 0; i < ROWS; i++) {
+    const int n = n0 + i * SUBS + sub;
+    rv[i] = n < P.rows;
+    rcl[i] = rv[i] ? n : P.rows - 1;
+  }
+#pragma unroll
+  for (int s = 0; s < S; s++)
+#pragma unroll
+    for (int i = 0; i < ROWS; i++) {
+      wrow[s][i] = P.w + e[s] * P.w_expert + (int64_t)rcl[i] * P.w_row;
+      srow[s][i] = P.s + e[s] * P.s_expert + (int64_t)rcl[i] * P.s_row;
+    }
+  struct Round {
+    Raw<B> w[S][ROWS];
+    uint8_t ex[S][ROWS];
+  };
+  // rounds past the last clamp to the last chunk (re-reads, results unused)
+  auto fetch = [&](int r, Round& d) {
+    uint32_t j = (uint32_t)(r * LPR + l);
+    j = j < (uint32_t)nchunks ? j : (uint32_t)nchunks - 1;
+#pragma unroll
+    for (int s = 0; s < S; s++)
+#pragma unroll
+      for (int i = 0; i < ROWS; i++) {
+        d.w[s][i] = load_raw<B>(wrow[s][i] + j * (uint32_t)B);
+        d.ex[s][i] = srow[s][i][j];
+      }
+  };
+  Round d[R];
+#pragma unroll
+  for (int k = 0; k < R; k++) fetch(k, d[k]);
+  __builtin_amdgcn_sched_barrier(0);
+  {
+    uint4* xl = reinterpret_cast<uint4*>(xs_lds);
+#pragma unroll
+    for (int k = 0; k < kXR; k++) xl[xidx[k]] = xra[k];
+#pragma unroll
+    for (int k = 0; k < kXR; k++) xl[xidx[kXR + k]] = xrb[k];
+    for (int idx = threadIdx.x + 256 * 2 * kXR; idx < xtotal; idx += 256) {
+      int t = 0;
+#pragma unroll
+      for (int q = 1; q < S; q++) t += idx >= q * xn ? 1 : 0;
+      xl[idx] = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(P.x) + (int64_t)t * P.x_slot)[idx - t * xn];
+    }
+  }
+  lds_barrier();
+
+  float acc[S][ROWS];
+#pragma unroll
+  for (int s = 0; s < S; s++)
+#pragma unroll
+    for (int i = 0; i < ROWS; i++) acc[s][i] = 0.0f;
+  auto consume = [&](const Round& c, int r) {
+    const int j = r * LPR + l;
+    const bool cv = j < nchunks;
+#pragma unroll
+    for (int s = 0; s < S; s++) {
+      uint32_t xw[16];
+      const uint4* xp = reinterpret_cast<const uint4*>(xs_lds + s * words + (cv ? j : 0) * 16);
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const uint4 v = xp[q];
+        xw[4 * q] = v.x; xw[4 * q + 1] = v.y; xw[4 * q + 2] = v.z; xw[4 * q + 3] = v.w;
+      }
+      float p[ROWS];
+      chunk_dot_rows<F, XT, ROWS>(c.w[s], xw, p);
+#pragma unroll
+      for (int i = 0; i < ROWS; i++) {
+        const float t = p[i] * pow2i((int)c.ex[s][i] - 127);
+        acc[s][i] = acc[s][i] + ((cv && rv[i]) ? t : 0.0f);
+      }
+    }
+  };
+  for (int r0 = 0;;) {
+#pragma unroll
+    for (int k = 0; k < R; k++)
+      if (r0 + k < rounds) consume(d[k], r0 + k);
+    r0 += R;
+    if (r0 >= rounds) break;
+#pragma unroll
+    for (int k = 0; k < R; k++) fetch(r0 + k, d[k]);
+  }
+#pragma unroll
+  for (int s = 0; s < S; s++) reduce_range<ROWS, 1, LPR>(acc[s]);
+  const int n = n0 + rs_row<ROWS>(l, log2c(ROWS), 0) * SUBS + sub;
+  if ((l >> log2c(ROWS)) != 0 || n >= P.rows) return;
+  float c = 0.0f;
+#pragma unroll
+  for (int s = 0; s < S; s++) {
+    float v = round_to<RT>(acc[s][0]);
+    if (P.bias != nullptr) v = round_to<RT>(v + ld_typed(P.bias, P.bias_dtype, e[s] * P.bias_expert + n));
+    c = __builtin_fmaf(v, ld_typed(P.scores, P.score_dtype, s), c);
+  }
+  store<OT>(reinterpret_cast<OT*>(P.out) + n, c);
+}
+
+// ------------------------------------------------------------------ dispatch
+
+template <Fmt F, typename XT, typename OT, typename RT, int LPR, int S>
+static int launch_down_lean(const DownParams& P, hipStream_t st) {
+  constexpr int SUBS = 64 / LPR;
+  const int64_t waves = ((int64_t)P.rows + SUBS - 1) / SUBS;   // one row per lane group
+  hipLaunchKernelGGL((down_lean_kernel<F, XT, OT, RT, LPR, 1, S>), dim3((unsigned)((waves + 3) / 4)), dim3(256),
+                     (size_t)P.cols * 2 * S, st, P);
+  return check_launch("mxfp_lowbit_weighted_down");
+}
+
+template <Fmt F, typename XT, typename OT, typename RT, int LPR>
+static int launch_down_lean_s(const DownParams& P, hipStream_t st) {
+  switch (P.slots) {
+    case 1: return launch_down_lean<F, XT, OT, RT, LPR, 1>(P, st);
+    case 2: return launch_down_lean<F, XT, OT, RT, LPR, 2>(P, st);
+    case 4: return launch_down_lean<F, XT, OT, RT, LPR, 4>(P, st);
+    default: return launch_down_lean<F, XT, OT, RT, LPR, 8>(P, st);
+  }
+}
+
+template <Fmt F, typename XT, typename OT, typename RT>
+static int launch_down(const DownParams& P, int lpr, hipStream_t st) {
+  if ((P.slots == 1 || P.slots == 2 || P.slots == 4 || P.slots == 8) && P.cols % 8 == 0 &&
+      (int64_t)P.cols * 2 * P.slots <= 65536 && P.x_slot % 8 == 0) {
+    if (lpr == 64) return launch_down_lean_s<F, XT, OT, RT, 64>(P, st);
+    if (lpr == 32) return launch_down_lean_s<F, XT, OT, RT, 32>(P, st);
+    if (lpr == 16) return launch_down_lean_s<F, XT, OT, RT, 16>(P, st);
+  }
+  auto go = [&](auto kern, int rb) {
+    const size_t lds = (size_t)P.cols * 2 * P.slots + (size_t)rb * 4 * P.slots;
+    const int blocks = (P.rows + rb - 1) / rb;
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), lds, st, P);
+    return check_launch("mxfp_lowbit_weighted_down");
+  };
+  switch (lpr) {
+    case 64: return go(weighted_down_kernel<F, XT, OT, RT, 64, 4>, 4);
+    case 32: return go(weighted_down_kernel<F, XT, OT, RT, 32, 4>, 8);
+    default: return go(weighted_down_kernel<F, XT, OT, RT, 16, 4>, 16);
+  }
+}
+
+template <typename XT, typename RT>
+static int down_dispatch(Fmt fmt, int out_dtype, const DownParams& P, int lpr, hipStream_t st) {
+  return with_type(out_dtype, [&](auto ot) -> int {
+    using OT = decltype(ot);
+    if constexpr (std::is_same_v<OT, float> || std::is_same_v<OT, XT>) {
+      switch (fmt) {
+        case Fmt::kQ2E8: return launch_down<Fmt::kQ2E8, XT, OT, RT>(P, lpr, st);
+        case Fmt::kQ1E8: return launch_down<Fmt::kQ1E8, XT, OT, RT>(P, lpr, st);
+        default: return launch_down<Fmt::kMxfp4, XT, OT, RT>(P, lpr, st);
+      }
+    } else {
+      set_error("weighted_down: output dtype must match the activation dtype or be fp32");
+      return TT_ERR_UNSUPPORTED;
+    }
+  });
+}
+
+}  // namespace tt
+
+using namespace tt;
+
+extern "C" int tt_mxfp_lowbit_weighted_down(const void* packed, int64_t w_expert_bytes, int64_t w_row_bytes,
+                                            const void* scales, int64_t s_expert, int64_t s_row, int bits,
+                                            const void* x, int x_dtype, int64_t x_slot,
+                                            const int32_t* expert_indices, const void* router_scores,
+                                            int score_dtype, int64_t selected, const void* bias, int bias_dtype,
+                                            int64_t bias_expert, void* out, int out_dtype, int64_t rows,
+                                            int64_t cols, void* stream) {
+  const char* what = "mxfp_lowbit_weighted_down";
+  TT_REQUIRE(bits == 1 || bits == 2 || bits == 4, "%s: fused down requires packed Q1, Q2 or MXFP4 experts", what);
+  TT_REQUIRE(valid_act_dtype(x_dtype) && valid_out_dtype(out_dtype), "%s: bad dtype codes", what);
+  TT_REQUIRE(cols > 0 && cols % 32 == 0, "%s: cols must be a multiple of 32", what);
+  TT_REQUIRE(selected >= 1 && selected * (2 * cols + 64) <= 65536,
+             "%s: selected activations and row values must fit 64 KiB of LDS", what);
+  TT_REQUIRE(rows > 0 && rows < (1 << 30), "%s: bad rows", what);
+  const int align = bits == 4 ? 16 : (bits == 2 ? 8 : 4);
+  TT_REQUIRE(packed && aligned(packed, align) && w_row_bytes % align == 0 && w_expert_bytes % align == 0,
+             "%s: packed weights must be %d-byte aligned", what, align);
+  TT_REQUIRE(scales && x && aligned(x, 4) && x_slot % 2 == 0 && out && expert_indices && router_scores,
+             "%s: null or misaligned pointer", what);
+  TT_REQUIRE(valid_out_dtype(score_dtype), "%s: bad score dtype", what);
+  if (bias) TT_REQUIRE(valid_out_dtype(bias_dtype), "%s: bad bias dtype", what);
+  DownParams P{static_cast<const uint8_t*>(packed), w_expert_bytes, w_row_bytes,
+               static_cast<const uint8_t*>(scales), s_expert, s_row, x, x_slot, expert_indices, router_scores, bias,
+               bias_expert, out, (int)rows, (int)cols, (int)selected, bias ? bias_dtype : TT_F32, score_dtype};
+  const int lpr = tt_gemv_lanes_per_row(cols / 32, 1);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const Fmt fmt = fmt_for_bits(bits);
+  if (x_dtype == TT_F16) {
+    if (bits == 4) return down_dispatch<f16_t, f16_t>(fmt, out_dtype, P, lpr, st);
+    return down_dispatch<f16_t, bf16_t>(fmt, out_dtype, P, lpr, st);
+  }
+  return down_dispatch<bf16_t, bf16_t>(fmt, out_dtype, P, lpr, st);
+}
