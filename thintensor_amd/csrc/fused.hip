@@ -376,30 +376,28 @@ int launch_lean(const tt_fused_gemv* d, int lpr, hipStream_t st) {
   return launch_lean_f<Fmt::kBF16W, XT, PRO>(d, lpr, st);
 }
 
-// Highest key among n partials (256 threads), then token / value / bookkeeping.
+// Highest key among n partials (256 threads), then token / value / bookkeeping; the
+// position inputs are requested before the partials.
 __global__ __launch_bounds__(256) void argmax_step_kernel(const uint64_t* partials, int n, int64_t* out_idx,
                                                           float* out_val, int32_t* pos, const int32_t* base,
                                                           int64_t* history, int32_t history_len) {
-  __shared__ uint64_t red[256];
-  uint64_t best = 0;
-  for (int i = threadIdx.x; i < n; i += 256) best = partials[i] > best ? partials[i] : best;
-  red[threadIdx.x] = best;
-  __syncthreads();
-  for (int s = 128; s > 0; s >>= 1) {
-    if (threadIdx.x < s) red[threadIdx.x] = red[threadIdx.x + s] > red[threadIdx.x] ? red[threadIdx.x + s] : red[threadIdx.x];
-    __syncthreads();
+  __shared__ uint64_t red[4];
+  int32_t p0 = 0, b0 = 0;
+  if (threadIdx.x == 0 && pos != nullptr) {
+    p0 = pos[0];
+    if (base != nullptr) b0 = base[0];
   }
+  const uint64_t k = block_max_u64(partials, n, red);
   if (threadIdx.x == 0) {
-    const uint64_t k = red[0];
     const uint32_t o = (uint32_t)(k >> 32);
     const uint32_t bits = o == 0xffffffffu ? 0x7fc00000u : ((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
     const int64_t token = (int64_t)(0xffffffffu - (uint32_t)k);
     out_idx[0] = token;
     if (out_val) out_val[0] = __builtin_bit_cast(float, bits);
     if (pos) {
-      const int32_t i = pos[0] - (base ? base[0] : 0);
+      const int32_t i = p0 - b0;
       if (history && i >= 0 && i < history_len) history[i] = token;
-      pos[0] += 1;
+      pos[0] = p0 + 1;
     }
   }
 }

@@ -105,17 +105,9 @@ namespace {
 
 __global__ __launch_bounds__(256) void argmax_finish_kernel(const uint64_t* partials, int n, int64_t* out_idx,
                                                             float* out_val) {
-  __shared__ uint64_t red[256];
-  uint64_t best = 0;
-  for (int i = threadIdx.x; i < n; i += 256) best = partials[i] > best ? partials[i] : best;
-  red[threadIdx.x] = best;
-  __syncthreads();
-  for (int s = 128; s > 0; s >>= 1) {
-    if (threadIdx.x < s) red[threadIdx.x] = red[threadIdx.x + s] > red[threadIdx.x] ? red[threadIdx.x + s] : red[threadIdx.x];
-    __syncthreads();
-  }
+  __shared__ uint64_t red[4];
+  const uint64_t k = block_max_u64(partials, n, red);
   if (threadIdx.x == 0) {
-    const uint64_t k = red[0];
     const uint32_t o = (uint32_t)(k >> 32);
     const uint32_t bits = o == 0xffffffffu ? 0x7fc00000u : ((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
     out_idx[0] = (int64_t)(0xffffffffu - (uint32_t)k);

@@ -55,8 +55,28 @@ __device__ void wave_topk(float lg0, float lg1, int E, int top_k, bool renorm, i
   m = fmaxf(m, xor_partner<8>(m));
   m = fmaxf(m, xor_partner<16>(m));
   m = fmaxf(m, xor_partner<32>(m));
-  bool t0 = !v0, t1 = !v1;
   float sel0 = 0.0f, sel1 = 0.0f;
+  const bool any_nan = __builtin_amdgcn_ballot_w64((v0 && __builtin_isnan(lg0)) || (v1 && __builtin_isnan(lg1))) != 0;
+  if (E <= 64 && !any_nan) {
+    // Without NaNs the iterated selection is the order of the keys (value, then lowest
+    // index), so slot s is the expert with exactly s greater keys: every lane counts the
+    // keys above its own, independently of the others.
+    const uint64_t mine = topk_key(lg0, lane);
+    int rank = 0;
+    for (int f = 0; f < E; f++) {
+      const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)mine, f);
+      const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(mine >> 32), f);
+      rank += (((uint64_t)hi << 32) | lo) > mine ? 1 : 0;
+    }
+    __shared__ float sel_lds[64];
+    if (v0 && rank < top_k) {
+      idx_out[rank] = lane;
+      sel_lds[rank] = lg0;
+    }
+    __builtin_amdgcn_wave_barrier();
+    if (lane < top_k) sel0 = sel_lds[lane];
+  } else {
+  bool t0 = !v0, t1 = !v1;
   for (int s = 0; s < top_k; s++) {
     uint64_t k = 0, f = 0;
     if (!t0) {
@@ -84,6 +104,7 @@ __device__ void wave_topk(float lg0, float lg1, int E, int top_k, bool renorm, i
       else sel1 = bv;
     }
     if (lane == 0) idx_out[s] = bi;
+  }
   }
   const float e0 = exp_f32(sel0 - m), e1 = exp_f32(sel1 - m);
   float den = 0.0f;

@@ -182,9 +182,36 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t k) {
     const uint64_t o = ((uint64_t)hi << 32) | lo;                                                         \
     k = o > k ? o : k;                                                                                    \
   }
+
   TT_MAXSTEP(1) TT_MAXSTEP(2) TT_MAXSTEP(4) TT_MAXSTEP(8) TT_MAXSTEP(16) TT_MAXSTEP(32)
 #undef TT_MAXSTEP
   return k;
+}
+
+// Maximum of n >= 1 uint64 keys over a 256-thread block: eight loads per thread are in
+// flight at a time (indices past n repeat the last key), then a wave maximum and one
+// barrier.  Every thread returns the result.  The maximum is exact, so its order does
+// not matter.
+__device__ __forceinline__ uint64_t block_max_u64(const uint64_t* p, int n, uint64_t* red4) {
+  uint64_t best = 0;
+  for (int i0 = 0; i0 < n; i0 += 256 * 8) {
+    uint64_t v[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const int i = i0 + (int)threadIdx.x + 256 * k;
+      v[k] = p[i < n ? i : n - 1];
+    }
+#pragma unroll
+    for (int k = 0; k < 8; k++) best = v[k] > best ? v[k] : best;
+  }
+  best = wave_max_u64(best);
+  if ((threadIdx.x & 63) == 0) red4[threadIdx.x >> 6] = best;
+  __syncthreads();
+  uint64_t m = red4[0];
+  m = red4[1] > m ? red4[1] : m;
+  m = red4[2] > m ? red4[2] : m;
+  m = red4[3] > m ? red4[3] : m;
+  return m;
 }
 
 // Workgroup barrier that orders LDS accesses only.  __syncthreads() also waits for
