@@ -50,6 +50,8 @@ INT4_CASES = [
     (1, 32, 32, np.float16, "f16", "f16"),         # one row, one chunk
     (5, 2880, 32, np.float16, "f16", "f16"),       # 90 chunks: ragged last round of 32 lanes
     (7, 160, 32, np.float32, "f16", "f32"),        # 5 chunks on 16 lanes
+    (96, 5632, 128, np.float16, "f16", "f16"),     # 16 lanes per row, 11 rounds: blocks of four and a tail
+    (2048, 6144, 128, np.float16, "f16", "f16"),   # three rounds, requested together
 ]
 
 

@@ -17,7 +17,7 @@ namespace {
 // workgroup in LDS behind a barrier; 1 = each lane reads its chunk from global memory;
 // 2 = each wave stages the whole vector in its own LDS slice with coalesced loads
 // (no workgroup barrier; a wave's LDS accesses complete in order).
-template <typename XT, int LPR, int ROWS, int XM>
+template <typename XT, int LPR, int ROWS, int XM, int PFR>
 __global__ __launch_bounds__(256) void int4g128_kernel(const uint8_t* __restrict__ W, uint32_t w_row,
                                                        const f16_t* __restrict__ S, uint32_t s_row, uint32_t s_grp,
                                                        const uint16_t* __restrict__ x, XT* __restrict__ y, int rows,
@@ -102,10 +102,13 @@ __global__ __launch_bounds__(256) void int4g128_kernel(const uint8_t* __restrict
 #pragma unroll
     for (int k = 0; k < NVG; k++) sc[k] = sbase[soff[k] + (j >> 2) * s_grp];
   };
-  Raw<16> wc[ROWS];
-  f16_t sc[NVG];
-  uint4 xc[4];
-  fetch(0, wc, sc, xc);
+  // PFR > 1: rounds are requested PFR at a time (rounds past the last re-read its chunk,
+  // unused), for shapes with few waves and several rounds per row
+  Raw<16> wc[PFR][ROWS];
+  f16_t sc[PFR][NVG];
+  uint4 xc[PFR][4];
+#pragma unroll
+  for (int k = 0; k < PFR; k++) fetch(k, wc[k], sc[k], xc[k]);
 
   uint32_t* xs = xs_lds;                     // this wave's activation copy
   if constexpr (XM == 0) {
@@ -125,15 +128,7 @@ __global__ __launch_bounds__(256) void int4g128_kernel(const uint8_t* __restrict
   float acc[NVG];
 #pragma unroll
   for (int k = 0; k < NVG; k++) acc[k] = 0.0f;
-  // do-while: the host guarantees one round (cols >= 32), and no loop-entry test keeps
-  // every argument load in the one scalar batch at the top
-  int r = 0;
-  do {
-    Raw<16> wn[ROWS];
-    f16_t sn[NVG];
-    uint4 xnx[4];
-    const bool more = r + 1 < rounds;
-    if (more) fetch(r + 1, wn, sn, xnx);
+  auto consume = [&](const Raw<16>* w, const f16_t* sk, const uint4* xk, int r) {
     const int j = r * LPR + l;
     const bool cv = j < nchunks;
     uint32_t xw[16];
@@ -141,31 +136,54 @@ __global__ __launch_bounds__(256) void int4g128_kernel(const uint8_t* __restrict
       const uint4* xp = reinterpret_cast<const uint4*>(xs + (cv ? j : 0) * 16);
 #pragma unroll
       for (int q = 0; q < 4; q++) {
-        const uint4 v = XG ? xc[q] : xp[q];
+        const uint4 v = XG ? xk[q] : xp[q];
         xw[4 * q] = v.x; xw[4 * q + 1] = v.y; xw[4 * q + 2] = v.z; xw[4 * q + 3] = v.w;
       }
     }
     float p[ROWS];
-    chunk_dot_rows<Fmt::kInt4Sym, XT, ROWS>(wc, xw, p);
+    chunk_dot_rows<Fmt::kInt4Sym, XT, ROWS>(w, xw, p);
 #pragma unroll
     for (int i = 0; i < ROWS; i++) p[i] = (cv && rv[i]) ? p[i] : 0.0f;
     reduce_range<ROWS, 1, L>(p);
 #pragma unroll
     for (int k = 0; k < NVG; k++) {
-      const float t = p[k] * to_f32(sc[k]);
+      const float t = p[k] * to_f32(sk[k]);
       acc[k] = acc[k] + ((cv && sv[k]) ? t : 0.0f);
     }
-    if (more) {
+  };
+  if constexpr (PFR == 1) {
+    // do-while: the host guarantees one round (cols >= 32), and no loop-entry test keeps
+    // every argument load in the one scalar batch at the top
+    int r = 0;
+    do {
+      Raw<16> wn[ROWS];
+      f16_t sn[NVG];
+      uint4 xnx[4];
+      const bool more = r + 1 < rounds;
+      if (more) fetch(r + 1, wn, sn, xnx);
+      consume(wc[0], sc[0], xc[0], r);
+      if (more) {
 #pragma unroll
-      for (int i = 0; i < ROWS; i++) wc[i] = wn[i];
+        for (int i = 0; i < ROWS; i++) wc[0][i] = wn[i];
 #pragma unroll
-      for (int k = 0; k < NVG; k++) sc[k] = sn[k];
-      if constexpr (XG) {
+        for (int k = 0; k < NVG; k++) sc[0][k] = sn[k];
+        if constexpr (XG) {
 #pragma unroll
-        for (int q = 0; q < 4; q++) xc[q] = xnx[q];
+          for (int q = 0; q < 4; q++) xc[0][q] = xnx[q];
+        }
       }
+    } while (++r < rounds);
+  } else {
+    for (int r0 = 0;;) {
+#pragma unroll
+      for (int k = 0; k < PFR; k++)
+        if (r0 + k < rounds) consume(wc[k], sc[k], xc[k], r0 + k);
+      r0 += PFR;
+      if (r0 >= rounds) break;
+#pragma unroll
+      for (int k = 0; k < PFR; k++) fetch(r0 + k, wc[k], sc[k], xc[k]);
     }
-  } while (++r < rounds);
+  }
   reduce_range<NVG, L, LPR>(acc);
   const int frow = row0 + rs_row<ROWS>(l, log2c(ROWS), 0) * SUBS + sub;
   if ((l >> log2c(ROWS)) == 0 && frow < rows) store<XT>(y + frow, acc[0]);
@@ -187,8 +205,17 @@ int launch_int4g128_lpr(int rpw, const void* W, int64_t w_row, const void* S, in
   const int xm = int4g128_x_mode(rows, cols, LPR);
   const size_t lds = xm == 1 ? 0 : (size_t)cols * 2 * (xm == 2 ? 4 : 1);
   const uint32_t wr = (uint32_t)w_row, sr = (uint32_t)s_row, sg = (uint32_t)s_grp;
-#define TT_INT4G_LAUNCH(R, M) \
-  hipLaunchKernelGGL((int4g128_kernel<XT, LPR, R, M>), grid, dim3(256), lds, st, w, wr, s, sr, sg, xv, yv, rows, cols)
+  const int rounds = (cols / 32 + LPR - 1) / LPR;
+  // several rounds per row and few rows per wave: four rounds in flight at a time
+#define TT_INT4G_LAUNCH(R, M)                                                                                  \
+  do {                                                                                                        \
+    if (rounds > 1 && R <= 2)                                                                                 \
+      hipLaunchKernelGGL((int4g128_kernel<XT, LPR, R, M, 4>), grid, dim3(256), lds, st, w, wr, s, sr, sg, xv, yv, \
+                         rows, cols);                                                                         \
+    else                                                                                                      \
+      hipLaunchKernelGGL((int4g128_kernel<XT, LPR, R, M, 1>), grid, dim3(256), lds, st, w, wr, s, sr, sg, xv, yv, \
+                         rows, cols);                                                                         \
+  } while (0)
 #define TT_INT4G_MODES(R) \
   if (xm == 1) TT_INT4G_LAUNCH(R, 1); else if (xm == 2) TT_INT4G_LAUNCH(R, 2); else TT_INT4G_LAUNCH(R, 0);
   if (rpw == 4) { TT_INT4G_MODES(4) }
