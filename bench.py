@@ -215,7 +215,7 @@ def _time_decode(dec, start_token: int, position: int, warmup: int, steps: int) 
     e1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    tokens = dec.history[:steps].cpu().tolist()
+    tokens = dec.history[..., :steps].cpu().tolist()   # [steps], or [batch, steps] for a batched decoder
     return {"wall_s": wall, "event_s": e0.elapsed_time(e1) * 1e-3, "tokens": tokens}
 
 
@@ -262,7 +262,28 @@ def moe_decode_phase(args) -> dict:
     tok_s = steps / r["event_s"]
     out = {"workload": "gpt-oss-20b-shaped bs=1 greedy decode, MXFP4 experts top-4 of 32, 1024 prior tokens",
            "steps": steps, "tok_s": tok_s, "ms_per_token": 1e3 / tok_s, "tokens": r["tokens"]}
-    del dec, w, be
+    del dec
+    if not args.unfused:
+        # bs=8: eight independent sequences in lockstep, each with its own random prior KV
+        from thintensor_amd.decode import MoEBatchDecoder
+
+        B = 8
+        g = torch.Generator(device=dev)
+        g.manual_seed(args.seed + 8)
+        cap, P = int(w.k_cache.shape[2]), s.prior_tokens
+        kc = torch.zeros((s.layers, B * s.kv_heads, cap, s.head_dim), device=dev, dtype=torch.float16)
+        vc = torch.zeros_like(kc)
+        kc[:, :, :P] = torch.randn((s.layers, B * s.kv_heads, P, s.head_dim), generator=g, device=dev).half()
+        vc[:, :, :P] = torch.randn((s.layers, B * s.kv_heads, P, s.head_dim), generator=g, device=dev).half()
+        bdec = MoEBatchDecoder(be, w, B, kc, vc)
+        rb = _time_decode(bdec, [1 + 1000 * b for b in range(B)], P, warm, steps)
+        tok_b = B * steps / rb["event_s"]
+        out["bs8"] = {"workload": "gpt-oss-20b-shaped greedy decode, 8 sequences in lockstep (one token each "
+                                  "per step), 1024 prior tokens each",
+                      "steps": steps, "tok_s": tok_b, "ms_per_step": 1e3 * rb["event_s"] / steps,
+                      "tokens_first_sequence": rb["tokens"][0]}
+        del bdec, kc, vc
+    del w, be
     torch.cuda.empty_cache()
     return out
 
@@ -375,7 +396,8 @@ def main() -> int:
     if not args.no_moe:
         _log("MoE decode (gpt-oss-20b-shaped)")
         moe = moe_decode_phase(args)
-        _log(f"MoE decode: {moe['tok_s']:.1f} tok/s")
+        _log(f"MoE decode: {moe['tok_s']:.1f} tok/s" +
+             (f"; bs=8: {moe['bs8']['tok_s']:.1f} tok/s" if "bs8" in moe else ""))
 
     cpu = cpu_gemv = None
     if not args.no_cpu:

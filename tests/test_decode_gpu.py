@@ -3,13 +3,15 @@ final logits must be identical (bit for bit), for graph replay and eager launche
 
 from __future__ import annotations
 
+import dataclasses
+
 import numpy as np
 import pytest
 import torch
 
 from oracle.decode_ref import DenseRef, MoERef
 from thintensor_amd.backend import HipDecodeBackend
-from thintensor_amd.decode import DenseDecoder, MoEDecoder
+from thintensor_amd.decode import DenseDecoder, MoEBatchDecoder, MoEDecoder
 from thintensor_amd.synth import GPT_OSS_20B, LLAMA_1B, DenseShape, MoEShape, make_dense, make_moe
 
 pytestmark = pytest.mark.gpu
@@ -42,6 +44,44 @@ def test_small_dense_64_tokens(device, graph, fused):
     # the last step's logits are bit-identical too
     _, logits = ref.step(want[-2], pos + s.max_new_tokens - 1)
     assert np.array_equal(_final_logits(dec).view(np.uint16), logits.view(np.uint16))
+
+
+def _batch_caches(s, w, batch, device, seed):
+    """Per-sequence KV caches [layers, batch * kv_heads, capacity, head_dim]: random prior
+    tokens, zeros after them (as make_moe fills its own cache)."""
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    cap, P = int(w.k_cache.shape[2]), s.prior_tokens
+    kc = torch.zeros((s.layers, batch * s.kv_heads, cap, s.head_dim), device=device, dtype=torch.float16)
+    vc = torch.zeros_like(kc)
+    shape = (s.layers, batch * s.kv_heads, P, s.head_dim)
+    kc[:, :, :P] = torch.randn(shape, generator=g, device=device).half()
+    vc[:, :, :P] = torch.randn(shape, generator=g, device=device).half()
+    return kc, vc
+
+
+def _sequence_weights(w, kc, vc, b, kv):
+    return dataclasses.replace(w, k_cache=kc[:, b * kv:(b + 1) * kv].clone(), v_cache=vc[:, b * kv:(b + 1) * kv].clone())
+
+
+@pytest.mark.parametrize("batch,against", [(3, "oracle"), (8, "bs1")])
+def test_small_moe_batch(device, batch, against):
+    """Lockstep decode of several sequences: every stream equals that sequence decoded
+    alone (the oracle, or the fused bs=1 HIP decoder, which the oracle pins above)."""
+    s = SMALL_MOE
+    w = make_moe(s, device=device, seed=4)
+    kc, vc = _batch_caches(s, w, batch, device, seed=9)
+    starts = [(37 * b + 5) % s.vocab for b in range(batch)]
+    steps, pos = 12, s.prior_tokens
+    want = []
+    for b in range(batch):
+        wb = _sequence_weights(w, kc, vc, b, s.kv_heads)
+        if against == "oracle":
+            want.append(MoERef(wb).generate(starts[b], pos, steps))
+        else:
+            want.append(MoEDecoder(_backend(device, s), wb, fused=True).generate(starts[b], pos, steps))
+    got = MoEBatchDecoder(_backend(device, s), w, batch, kc, vc).generate(starts, pos, steps)
+    assert got == want
 
 
 @pytest.mark.parametrize("fused", [False, True])

@@ -104,6 +104,7 @@ class HipDecodeBackend:
         self._argmax_out_val = torch.empty((), device=self.device, dtype=torch.float32)
         self._argmax_partials: torch.Tensor | None = None
         self._attention_partials: torch.Tensor | None = None
+        self._batched_partials: torch.Tensor | None = None
 
     # ------------------------------------------------------------ helpers
     @staticmethod
@@ -826,17 +827,26 @@ class HipDecodeBackend:
         _lib.check(rc, "scaled_batched_matvec")
         return out
 
+    def _batched_argmax_scratch(self, m: int, rows: int, cols: int) -> torch.Tensor:
+        need = int(self.lib.tt_matvec_argmax_batched_partials(m, rows, cols))
+        if self._batched_partials is None or self._batched_partials.numel() < need:
+            self._batched_partials = torch.empty(need, device=self.device, dtype=torch.int64)
+        return self._batched_partials
+
     def matvec_argmax_batched(self, weight: torch.Tensor, x: torch.Tensor,
-                              logits: torch.Tensor | None = None) -> torch.Tensor:
+                              logits: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
         """Greedy lm_head for x [M, cols]: int64 [M] tokens (first index of each row's
-        maximum rounded logit)."""
+        maximum rounded logit), written to ``out`` when given (a new tensor otherwise).
+        The partials scratch is reused between calls."""
         _require_cuda(weight, x)
         m, rows, cols = int(x.shape[0]), int(weight.shape[0]), int(weight.shape[1])
         if x.ndim != 2 or x.shape[1] != cols or weight.dtype != torch.float16 or x.dtype != torch.float16:
             raise ValueError("batched matvec_argmax takes fp16 W [rows, cols] and x [M, cols]")
-        need = int(self.lib.tt_matvec_argmax_batched_partials(m, rows, cols))
-        partials = torch.empty(need, device=self.device, dtype=torch.int64)
-        idx = torch.empty(m, device=self.device, dtype=torch.int64)
+        if out is not None and (out.dtype != torch.int64 or out.numel() != m or not out.is_contiguous()):
+            raise ValueError("batched matvec_argmax: out must be a contiguous int64 tensor of M tokens")
+        partials = self._batched_argmax_scratch(m, rows, cols)
+        need = int(partials.numel())
+        idx = out if out is not None else torch.empty(m, device=self.device, dtype=torch.int64)
         rc = self.lib.tt_matvec_argmax_batched(
             weight.data_ptr(), weight.stride(0), x.data_ptr(), x.stride(0), m,
             logits.data_ptr() if logits is not None else None, logits.stride(0) if logits is not None else 0, rows,

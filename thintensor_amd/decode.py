@@ -27,6 +27,8 @@ Differences from the reference, by design:
 
 from __future__ import annotations
 
+import dataclasses
+
 import torch
 
 from . import _lib
@@ -371,3 +373,123 @@ class MoEDecoder(_GraphedDecoder):
             be.mxfp_lowbit_weighted_down(L.down_blocks, L.down_scales, self.act, self.router_idx, self.router_scores,
                                          self.moe, bits=4, bias=L.down_bias)
         be.fused_lm_head_argmax(self._head_desc, position=self.position, base=self.base, history=self.history)
+
+
+class MoEBatchDecoder:
+    """``batch`` independent gpt-oss-shaped sequences decoded in lockstep, one token of each
+    per step (eight independent bs=1 routings at batch 8; the reference decodes one token
+    per step and has no batched path).
+
+    Every sequence has its own KV cache (``k_cache``/``v_cache`` [layers, batch * kv_heads,
+    capacity, head_dim]: sequence b owns KV heads b * kv_heads ...) and token; the position
+    is shared.  Per sequence the step runs the fused bs=1 launches (QKV with the norm
+    prologue and RoPE / cache epilogue, o_proj, add+RMSNorm+router, expert SwiGLU and
+    weighted down), so the weights stream once per sequence and layer, mostly from the
+    last-level cache after the first.  Two launches cover the whole batch: attention (the
+    batch's query heads and KV heads are the heads of one call, so each head's arithmetic
+    is the bs=1 arithmetic) and the M-row lm_head argmax.  Each sequence's tokens equal
+    MoEDecoder's stream for that sequence bit for bit."""
+
+    def __init__(self, backend: HipDecodeBackend, weights: MoEWeights, batch: int, k_cache: torch.Tensor,
+                 v_cache: torch.Tensor) -> None:
+        s = weights.shape
+        if batch < 1:
+            raise ValueError("batch must be at least 1")
+        want = (s.layers, batch * s.kv_heads)
+        if tuple(k_cache.shape[:2]) != want or k_cache.shape != v_cache.shape or k_cache.shape[3] != s.head_dim:
+            raise ValueError(f"KV caches must be [{s.layers}, {batch * s.kv_heads}, capacity, {s.head_dim}]")
+        self.be, self.w, self.s, self.batch = backend, weights, s, batch
+        dev = weights.embed.device
+        self.device = dev
+        self.k_cache, self.v_cache = k_cache, v_cache
+        self.capacity = int(k_cache.shape[2])
+        self.tokens = torch.zeros(batch, device=dev, dtype=torch.int64)
+        self.position = torch.zeros(1, device=dev, dtype=torch.int32)
+        self.base = torch.zeros(1, device=dev, dtype=torch.int32)
+        self.history = torch.zeros((batch, s.max_new_tokens), device=dev, dtype=torch.int64)
+        self.q_all = torch.empty((batch, s.q_dim), device=dev, dtype=torch.float16)
+        self.attn_all = torch.empty((batch, s.q_dim), device=dev, dtype=torch.float16)
+        self.final_all = torch.empty((batch, s.hidden), device=dev, dtype=torch.float16)
+        self.sinks = [L.sinks.repeat(batch).contiguous() for L in weights.layers]
+        kv = s.kv_heads
+        self.subs: list[MoEDecoder] = []
+        for b in range(batch):
+            wb = dataclasses.replace(weights, k_cache=k_cache[:, b * kv:(b + 1) * kv],
+                                     v_cache=v_cache[:, b * kv:(b + 1) * kv])
+            sub = MoEDecoder(backend, wb, fused=True)
+            sub.token = self.tokens[b]
+            sub.position = self.position
+            sub.qkv = self.q_all[b]
+            sub.attn = self.attn_all[b]
+            sub._build_fused()
+            self.subs.append(sub)
+        self.graph: torch.cuda.CUDAGraph | None = None
+        self._graph_stream: torch.cuda.Stream | None = None
+
+    def _reserve_scratch(self) -> None:
+        s = self.s
+        self.be._attention_scratch(self.batch * s.heads, self.capacity, s.head_dim)
+        self.be._batched_argmax_scratch(self.batch, int(self.w.lm_head.shape[0]), s.hidden)
+
+    def step(self) -> None:
+        """One token of every sequence, logged at history[:, position - base]; advances the position."""
+        be, w, s, B = self.be, self.w, self.s, self.batch
+        for li, L in enumerate(w.layers):
+            for sub in self.subs:
+                be.fused_gemv(sub._qkv_desc[li])
+            be.single_token_gqa_attention(self.q_all.view(-1), self.k_cache[li], self.v_cache[li],
+                                          self.attn_all.view(-1), B * s.heads, B * s.kv_heads, s.head_dim,
+                                          sinks=self.sinks[li], active_tokens=(self.position, 1))
+            for sub in self.subs:
+                be.multi_matvec_bias((L.o,), (L.o_bias,), sub.attn, sub.attn_out)
+                be.add_rms_norm_router_topk(sub.hidden_a, sub.attn_out, sub.hidden_b, L.ln2, sub.normed, s.eps,
+                                            L.router, sub.router_idx, sub.router_scores, bias=L.router_bias,
+                                            renormalize=True)
+                be.mxfp_lowbit_selected_swiglu(L.gate_up_blocks, L.gate_up_scales, sub.normed, sub.router_idx, sub.act,
+                                               bits=4, alpha=s.swiglu_alpha, limit=s.swiglu_limit,
+                                               bias=L.gate_up_bias)
+                be.mxfp_lowbit_weighted_down(L.down_blocks, L.down_scales, sub.act, sub.router_idx,
+                                             sub.router_scores, sub.moe, bits=4, bias=L.down_bias)
+        for b, sub in enumerate(self.subs):
+            be.add(sub.hidden_b, sub.moe, sub.hidden_a)
+            be.rms_norm(sub.hidden_a, w.final_norm, self.final_all[b], s.eps)
+        be.matvec_argmax_batched(w.lm_head, self.final_all, out=self.tokens)
+        for b in range(B):
+            be.record_token(self.tokens[b], self.position, self.base, self.history[b])
+        be.advance_position(self.position)
+
+    def capture(self) -> None:
+        """Record one batched step into a HIP graph (scratch reserved first)."""
+        self._reserve_scratch()
+        torch.cuda.synchronize(self.device)
+        self._graph_stream = torch.cuda.Stream(self.device)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph, stream=self._graph_stream):
+            self.step()
+
+    def prime(self, tokens: list[int], position: int) -> None:
+        if len(tokens) != self.batch:
+            raise ValueError("one start token per sequence")
+        if not 0 <= position < self.capacity:
+            raise ValueError("position outside the KV cache")
+        self.tokens.copy_(torch.tensor(tokens, dtype=torch.int64))
+        self.position.fill_(int(position))
+        self.base.fill_(int(position))
+        self.history.zero_()
+
+    def generate(self, start_tokens: list[int], position: int, steps: int, use_graph: bool = True) -> list[list[int]]:
+        """Greedy-decode `steps` tokens of every sequence; returns one id list per sequence."""
+        if position + steps > self.capacity:
+            raise ValueError("not enough KV capacity for the requested steps")
+        if steps > self.history.shape[1]:
+            raise ValueError("history buffer too small")
+        if use_graph and self.graph is None:
+            self.capture()
+        self.prime(start_tokens, position)
+        for _ in range(steps):
+            if use_graph:
+                self.graph.replay()
+            else:
+                self.step()
+        torch.cuda.synchronize(self.device)
+        return self.history[:, :steps].cpu().tolist()
