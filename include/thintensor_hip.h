@@ -142,6 +142,32 @@ int tt_mxfp_lowbit_weighted_down(const void* packed, int64_t w_expert_bytes, int
                                  const void* bias, int bias_dtype, int64_t bias_expert,
                                  void* out, int out_dtype, int64_t rows, int64_t cols, void* stream);
 
+/* Several tokens at once, each with `selected` experts (no reference counterpart: the
+ * reference decodes one token per step; these serve the batched decode of independent
+ * sequences).  Token t's activation vector is x + t * x_token; its slots are
+ * t * selected ... in expert_indices and in out (out_slot elements apart).  Each slot's
+ * values equal tt_mxfp_lowbit_selected_swiglu on that token alone. */
+int tt_mxfp_lowbit_selected_swiglu_tokens(const void* packed, int64_t w_expert_bytes, int64_t w_row_bytes,
+                                          const void* scales, int64_t s_expert, int64_t s_row, int bits,
+                                          const void* x, int x_dtype, int64_t x_token,
+                                          const int32_t* expert_indices, int64_t selected,
+                                          const void* bias, int bias_dtype, int64_t bias_expert,
+                                          float alpha, float limit, void* out, int out_dtype,
+                                          int64_t out_slot, int64_t activation_rows, int64_t cols,
+                                          int64_t tokens, void* stream);
+
+/* Token t sums its `selected` slots (x rows t * selected ..., x_slot elements apart;
+ * expert_indices and router_scores entries t * selected ...) into out + t * out_token;
+ * each token's output equals tt_mxfp_lowbit_weighted_down on that token alone.  No
+ * reference counterpart (batched decode of independent sequences). */
+int tt_mxfp_lowbit_weighted_down_tokens(const void* packed, int64_t w_expert_bytes, int64_t w_row_bytes,
+                                        const void* scales, int64_t s_expert, int64_t s_row, int bits,
+                                        const void* x, int x_dtype, int64_t x_slot,
+                                        const int32_t* expert_indices, const void* router_scores,
+                                        int score_dtype, int64_t selected, const void* bias, int bias_dtype,
+                                        int64_t bias_expert, void* out, int out_dtype, int64_t out_token,
+                                        int64_t rows, int64_t cols, int64_t tokens, void* stream);
+
 /* Affine low-bit GEMV with fp16 (scale, zero) per group: w = (c - z) * s,
  * evaluated as sum_g fmaf(X_g, -(z_g s_g), S_g s_g).  bits 2: c in [0,3]
  * (byte i/4, bits 2(i%4)); bits 1: c in {0,1} (byte i/8, bit i%8).
@@ -268,6 +294,8 @@ int tt_moe_router_matvec_topk(const void* weight, int w_dtype, int64_t w_row, co
  * experts <= 32, hidden_size <= 4096 and the activations, norm weight and norm output share
  * an fp16/bf16 dtype (otherwise the two operators run one after the other).  Outputs and
  * bits are those of tt_add_rms_norm then tt_moe_router_matvec_topk(hidden = norm_out).
+ * `tokens` rows at once: left/right/residual_out/norm_out [tokens, hidden_size],
+ * indices/scores [tokens, top_k], all contiguous (one workgroup per token).
  * Fuses the reference's add_rms_norm (triton_kernels.py:5646-5667) and
  * moe_router_matvec_topk (:5826-5860) as its MoE layer calls them back to back
  * (gpu_runtime.py:9465-9513); the reference has no single entry point for the pair. */
@@ -275,7 +303,8 @@ int tt_add_rms_norm_router_topk(const void* left, const void* right, void* resid
                                 const void* norm_weight, int norm_w_dtype, void* norm_out, int norm_dtype,
                                 int64_t hidden_size, float eps, const void* weight, int w_dtype, int64_t w_row,
                                 const void* bias, int bias_dtype, int64_t experts, int64_t top_k, int renormalize,
-                                int32_t* indices_out, void* scores_out, int score_dtype, void* stream);
+                                int32_t* indices_out, void* scores_out, int score_dtype, int64_t tokens,
+                                void* stream);
 
 /* Top-k + softmax on given logits.  Replaces TritonDecodeBackend.moe_router_topk
  * (triton_kernels.py:5803-5824; kernel :2821-2851). */

@@ -284,6 +284,42 @@ def test_fused_weighted_down(backend, device, bits):
     assert_bits_equal(from_torch_bits(out), want, f"weighted down bits={bits}")
 
 
+@pytest.mark.parametrize("bits,tokens", [(4, 8), (2, 3)])
+def test_expert_kernels_token_batched(backend, device, bits, tokens):
+    """SwiGLU and weighted down over several tokens (each with its own activation
+    vector, experts and scores) equal the single-token operators token by token."""
+    experts, inter, cols, top_k = 6, 2880, 2880, 4
+    g = rng(71 + bits)
+    if bits == 4:
+        gu, gus = _mxfp4_expert_weights(g, experts, 2 * inter, cols)
+        dw, dws = _mxfp4_expert_weights(g, experts, cols, inter)
+    else:
+        gu = layouts.pack_lowbit_blocks(g.integers(0, 4, size=(experts, 2 * inter, cols), dtype=np.uint8), 2)
+        gus = g.integers(118, 123, size=(experts, 2 * inter, cols // 32), dtype=np.uint8)
+        dw = layouts.pack_lowbit_blocks(g.integers(0, 4, size=(experts, cols, inter), dtype=np.uint8), 2)
+        dws = g.integers(118, 123, size=(experts, cols, inter // 32), dtype=np.uint8)
+    gub, db = f16_normal(g, (experts, 2 * inter), 0.5), f16_normal(g, (experts, cols), 0.5)
+    idx = np.stack([g.permutation(experts)[:top_k] for _ in range(tokens)]).astype(np.int32)
+    sc = g.dirichlet(np.ones(top_k), size=tokens).astype(np.float16)
+    x = f16_normal(g, (tokens, cols))
+    T = lambda a: to_torch(a, device)
+    gu_d, gus_d, dw_d, dws_d, gub_d, db_d = T(gu), T(gus), T(dw), T(dws), T(gub), T(db)
+    act = torch.empty((tokens * top_k, inter), device=device, dtype=torch.float16)
+    backend.mxfp_lowbit_selected_swiglu_tokens(gu_d, gus_d, T(x), T(idx), act, bits=bits, alpha=1.702, limit=7.0,
+                                               bias=gub_d)
+    out = torch.empty((tokens, cols), device=device, dtype=torch.float16)
+    backend.mxfp_lowbit_weighted_down_tokens(dw_d, dws_d, act, T(idx), T(sc), out, bits=bits, bias=db_d)
+    for t in range(tokens):
+        a1 = torch.empty((top_k, inter), device=device, dtype=torch.float16)
+        backend.mxfp_lowbit_selected_swiglu(gu_d, gus_d, T(x[t]), T(idx[t]), a1, bits=bits, alpha=1.702, limit=7.0,
+                                            bias=gub_d)
+        assert_bits_equal(from_torch_bits(act[t * top_k:(t + 1) * top_k]).reshape(-1),
+                          from_torch_bits(a1).reshape(-1), f"swiglu token {t}")
+        o1 = torch.empty(cols, device=device, dtype=torch.float16)
+        backend.mxfp_lowbit_weighted_down(dw_d, dws_d, a1, T(idx[t]), T(sc[t]), o1, bits=bits, bias=db_d)
+        assert_bits_equal(from_torch_bits(out[t]), from_torch_bits(o1), f"weighted down token {t}")
+
+
 @pytest.mark.parametrize("bits,rows", [(2, 17920), (1, 5120)])
 def test_lowbit_affine_matvec(backend, device, bits, rows):
     cols, group = 5120, 64

@@ -185,6 +185,32 @@ def test_add_rms_norm_router(backend, device, E, H, k, renorm, bias_dtype, wbf16
     assert_bits_equal(from_torch_bits(sc), wsc, "router scores")
 
 
+@pytest.mark.parametrize("tokens,H", [(8, 2880), (3, 5120)])
+def test_add_rms_norm_router_tokens(backend, device, tokens, H):
+    """Several tokens in one call (one workgroup each; above 4096 the per-token
+    operators) equal the single-token calls."""
+    E, k = 32, 4
+    g = rng(tokens + H)
+    a, b = f16_normal(g, (tokens, H)), f16_normal(g, (tokens, H), 0.5)
+    nw, w, bias = f16_normal(g, H, 0.1), f16_normal(g, (E, H), 0.05), f16_normal(g, E, 0.1)
+    T = lambda x: to_torch(x, device)
+    res = torch.empty((tokens, H), device=device, dtype=torch.float16)
+    normed = torch.empty_like(res)
+    idx = torch.empty((tokens, k), device=device, dtype=torch.int32)
+    sc = torch.empty((tokens, k), device=device, dtype=torch.float16)
+    backend.add_rms_norm_router_topk(T(a), T(b), res, T(nw), normed, 1e-5, T(w), idx, sc, bias=T(bias), renormalize=True)
+    for t in range(tokens):
+        r1, n1 = torch.empty(H, device=device, dtype=torch.float16), torch.empty(H, device=device, dtype=torch.float16)
+        i1 = torch.empty(k, device=device, dtype=torch.int32)
+        s1 = torch.empty(k, device=device, dtype=torch.float16)
+        backend.add_rms_norm_router_topk(T(a[t]), T(b[t]), r1, T(nw), n1, 1e-5, T(w), i1, s1, bias=T(bias),
+                                         renormalize=True)
+        assert_bits_equal(from_torch_bits(res[t]), from_torch_bits(r1), f"residual {t}")
+        assert_bits_equal(from_torch_bits(normed[t]), from_torch_bits(n1), f"normed {t}")
+        assert torch.equal(idx[t], i1)
+        assert_bits_equal(from_torch_bits(sc[t]), from_torch_bits(s1), f"scores {t}")
+
+
 def test_router_topk_on_logits_with_ties(backend, device):
     lg = np.array([1.0, 3.0, 3.0, -2.0, 3.0, 0.5, 2.0, 2.0], dtype=np.float16)
     idx = torch.empty(4, device=device, dtype=torch.int32)

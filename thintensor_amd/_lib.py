@@ -88,7 +88,11 @@ SIGNATURES: dict[str, list] = {
     "tt_moe_router_matvec_topk": [_P, _I, _L, _P, _I, _L, _P, _I, _L, _L, _I, _P, _P, _I, _P],
     "tt_moe_router_topk": [_P, _I, _L, _L, _I, _P, _P, _I, _P],
     "tt_add_rms_norm_router_topk": [_P, _P, _P, _I, _P, _I, _P, _I, _L, _F, _P, _I, _L, _P, _I, _L, _L, _I, _P, _P,
-                                    _I, _P],
+                                    _I, _L, _P],
+    "tt_mxfp_lowbit_selected_swiglu_tokens": [_P, _L, _L, _P, _L, _L, _I, _P, _I, _L, _P, _L, _P, _I, _L, _F, _F, _P,
+                                              _I, _L, _L, _L, _L, _P],
+    "tt_mxfp_lowbit_weighted_down_tokens": [_P, _L, _L, _P, _L, _L, _I, _P, _I, _L, _P, _P, _I, _L, _P, _I, _L, _P, _I,
+                                            _L, _L, _L, _L, _P],
     "tt_int4_batched_matvec": [_P, _L, _P, _L, _P, _L, _P, _L, _L, _L, _L, _L, _P],
     "tt_scaled_batched_matvec": [_P, _L, _P, _P, _L, _P, _L, _L, _L, _L, _P],
     "tt_matvec_argmax_batched_partials": [_L, _L, _L],

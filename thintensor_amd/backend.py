@@ -489,6 +489,67 @@ class HipDecodeBackend:
         _lib.check(rc, "mxfp_lowbit_weighted_down")
         return out
 
+    def mxfp_lowbit_selected_swiglu_tokens(self, packed_weight: torch.Tensor, scales: torch.Tensor, x: torch.Tensor,
+                                           expert_indices: torch.Tensor, out: torch.Tensor, *, bits: int,
+                                           alpha: float, limit: float,
+                                           bias: torch.Tensor | None = None) -> torch.Tensor:
+        """``mxfp_lowbit_selected_swiglu`` for T tokens at once: x [T, cols],
+        expert_indices [T, k], out [T * k, I] (token t's slots are rows t*k ...).  No
+        reference counterpart (batched decode of independent sequences); each token's
+        rows equal the single-token operator's."""
+        if bits not in {1, 2, 4} or packed_weight.ndim != 4 or scales.ndim != 3:
+            raise ValueError("fused SwiGLU requires packed Q1, Q2 or MXFP4 experts")
+        activation_rows = int(packed_weight.shape[1]) // 2
+        cols = int(scales.shape[2] * 32)
+        if x.ndim != 2 or expert_indices.ndim != 2 or int(x.shape[0]) != int(expert_indices.shape[0]):
+            raise ValueError("batched SwiGLU takes x [T, cols] and expert_indices [T, k]")
+        tokens, selected = map(int, expert_indices.shape)
+        if int(x.shape[1]) != cols or x.stride(1) != 1 or tuple(out.shape) != (tokens * selected, activation_rows):
+            raise ValueError("batched SwiGLU shape mismatch")
+        self._check_indices(expert_indices)
+        _require_cuda(packed_weight, scales, x, out)
+        rc = self.lib.tt_mxfp_lowbit_selected_swiglu_tokens(
+            packed_weight.data_ptr(), packed_weight.stride(0), packed_weight.stride(1), scales.data_ptr(),
+            scales.stride(0), scales.stride(1), bits, x.data_ptr(), _code(x, "swiglu"), x.stride(0),
+            expert_indices.data_ptr(), selected, bias.data_ptr() if bias is not None else None,
+            _code(bias, "bias") if bias is not None else _lib.F32, bias.stride(0) if bias is not None else 0,
+            float(alpha), float(limit), out.data_ptr(), _code(out, "swiglu"), out.stride(0), activation_rows, cols,
+            tokens, _stream(out),
+        )
+        _lib.check(rc, "mxfp_lowbit_selected_swiglu_tokens")
+        return out
+
+    def mxfp_lowbit_weighted_down_tokens(self, packed_weight: torch.Tensor, scales: torch.Tensor, x: torch.Tensor,
+                                         expert_indices: torch.Tensor, router_scores: torch.Tensor,
+                                         out: torch.Tensor, *, bits: int,
+                                         bias: torch.Tensor | None = None) -> torch.Tensor:
+        """``mxfp_lowbit_weighted_down`` for T tokens at once: x [T * k, cols],
+        expert_indices / router_scores [T, k], out [T, rows].  No reference counterpart;
+        each token's output equals the single-token operator's."""
+        if bits not in {1, 2, 4} or packed_weight.ndim != 4 or scales.ndim != 3:
+            raise ValueError("fused down requires packed Q1, Q2 or MXFP4 experts")
+        rows = int(packed_weight.shape[1])
+        cols = int(scales.shape[2] * 32)
+        if expert_indices.ndim != 2 or tuple(router_scores.shape) != tuple(expert_indices.shape):
+            raise ValueError("batched weighted-down takes expert_indices and router_scores [T, k]")
+        tokens, selected = map(int, expert_indices.shape)
+        if tuple(x.shape) != (tokens * selected, cols) or out.ndim != 2 or tuple(out.shape) != (tokens, rows):
+            raise ValueError("batched weighted-down shape mismatch")
+        if not router_scores.is_contiguous() or out.stride(1) != 1:
+            raise ValueError("batched weighted-down needs contiguous scores and output rows")
+        self._check_indices(expert_indices)
+        _require_cuda(packed_weight, scales, x, out, router_scores)
+        rc = self.lib.tt_mxfp_lowbit_weighted_down_tokens(
+            packed_weight.data_ptr(), packed_weight.stride(0), packed_weight.stride(1), scales.data_ptr(),
+            scales.stride(0), scales.stride(1), bits, x.data_ptr(), _code(x, "weighted_down"), x.stride(0),
+            expert_indices.data_ptr(), router_scores.data_ptr(), _code(router_scores, "router scores"), selected,
+            bias.data_ptr() if bias is not None else None, _code(bias, "bias") if bias is not None else _lib.F32,
+            bias.stride(0) if bias is not None else 0, out.data_ptr(), _code(out, "weighted_down"), out.stride(0),
+            rows, cols, tokens, _stream(out),
+        )
+        _lib.check(rc, "mxfp_lowbit_weighted_down_tokens")
+        return out
+
     # ------------------------------------------------------------ affine low-bit (no reference kernel)
     def lowbit_affine_matvec(
         self,
@@ -753,15 +814,21 @@ class HipDecodeBackend:
 
         No single reference operator: the reference's MoE layer calls add_rms_norm
         (triton_kernels.py:5646-5667) and moe_router_matvec_topk (:5826-5860) back to
-        back (gpu_runtime.py:9465-9513).  Outputs and bits equal that pair's."""
-        n = left.numel()
-        if any(t.numel() != n for t in (right, residual_out, norm_weight, norm_out)):
-            raise ValueError("add_rms_norm size mismatch")
+        back (gpu_runtime.py:9465-9513).  Outputs and bits equal that pair's.  The vectors
+        may hold several tokens ([tokens, hidden]; indices/scores [tokens, top_k]), one
+        workgroup each."""
+        experts, hidden_size = map(int, router_weight.shape)
+        n = hidden_size
+        tokens = int(left.numel()) // n if n else 0
+        if tokens < 1 or any(t.numel() != tokens * n for t in (left, right, residual_out, norm_out)) or \
+                int(norm_weight.numel()) != n:
+            raise ValueError("add_rms_norm_router_topk: vectors must be [tokens, hidden] matching the router weight")
+        if any(not t.is_contiguous() for t in (left, right, residual_out, norm_out, scores_out)):
+            raise ValueError("add_rms_norm_router_topk: vectors must be contiguous")
         if right.dtype != left.dtype or residual_out.dtype != left.dtype:
             raise ValueError("add_rms_norm: left, right and residual_out must share a dtype")
-        experts, hidden_size = map(int, router_weight.shape)
-        if hidden_size != n:
-            raise ValueError("router hidden vector does not match weight shape")
+        if int(indices_out.numel()) % tokens or int(scores_out.numel()) != int(indices_out.numel()):
+            raise ValueError("add_rms_norm_router_topk: indices/scores must be [tokens, top_k]")
         if experts > 128:
             raise ValueError("fused router supports at most 128 experts")
         if bias is not None and int(bias.numel()) != experts:
@@ -773,9 +840,9 @@ class HipDecodeBackend:
             norm_weight.data_ptr(), _code(norm_weight, "add_rms_norm"), norm_out.data_ptr(),
             _code(norm_out, "add_rms_norm"), n, float(eps), router_weight.data_ptr(), _code(router_weight, "router"),
             router_weight.stride(0), bias.data_ptr() if bias is not None else None,
-            _code(bias, "bias") if bias is not None else _lib.F32, experts, int(indices_out.numel()),
+            _code(bias, "bias") if bias is not None else _lib.F32, experts, int(indices_out.numel()) // tokens,
             int(bool(renormalize)), indices_out.data_ptr(), scores_out.data_ptr(), _code(scores_out, "scores"),
-            _stream(left),
+            tokens, _stream(left),
         )
         _lib.check(rc, "add_rms_norm_router_topk")
         return indices_out, scores_out

@@ -23,6 +23,7 @@ struct SwigluParams {
   float alpha, limit;
   void* out; int64_t out_slot;
   int act_rows, cols;
+  int x_div;   // slots sharing one activation vector: slot s reads x + (s / x_div) * x_slot
 };
 
 template <typename BT> __device__ __forceinline__ float ld_bias(const void* b, int64_t i) {
@@ -38,8 +39,10 @@ struct DownParams {
   const void* scores;
   const void* bias; int64_t bias_expert;
   void* out;
-  int rows, cols, slots;
+  int rows, cols, slots;          // slots per token
   int bias_dtype, score_dtype;   // storage codes (TT_F16 / TT_BF16 / TT_F32)
+  int64_t out_token;             // elements between tokens' outputs (token = blockIdx.y)
+  int tokens;                    // tokens, each with `slots` selected experts
 };
 
 // One element of a small vector (bias, router scores) whose storage type is a runtime

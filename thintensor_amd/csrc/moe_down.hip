@@ -31,7 +31,7 @@ __global__ __launch_bounds__(256) void weighted_down_kernel(DownParams P) {
   const uint8_t* srow[RPW];
   int64_t e = 0;
   auto point = [&](int s) {
-    e = P.experts[s];
+    e = P.experts[(int64_t)blockIdx.y * P.slots + s];
 #pragma unroll
     for (int i = 0; i < RPW; i++) {
       wrow[i] = P.w + e * P.w_expert + (int64_t)row[i] * P.w_row;
@@ -45,7 +45,8 @@ __global__ __launch_bounds__(256) void weighted_down_kernel(DownParams P) {
     e8_fetch<F, LPR, RPW>(cur, 0, l, nchunks, wrow, srow, rv);
   }
   for (int t = 0; t < P.slots; t++) {
-    const uint32_t* xg = reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(P.x) + (int64_t)t * P.x_slot);
+    const uint32_t* xg = reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(P.x) +
+                                                           ((int64_t)blockIdx.y * P.slots + t) * P.x_slot);
     for (int i = threadIdx.x; i < words; i += blockDim.x) xs_lds[t * words + i] = xg[i];
   }
   __syncthreads();
@@ -67,8 +68,9 @@ __global__ __launch_bounds__(256) void weighted_down_kernel(DownParams P) {
   __syncthreads();
   if (threadIdx.x < RB && row0 + (int)threadIdx.x < P.rows) {
     float c = 0.0f;
-    for (int t = 0; t < P.slots; t++) c = __builtin_fmaf(vals[t * RB + threadIdx.x], ld_typed(P.scores, P.score_dtype, t), c);
-    store<OT>(reinterpret_cast<OT*>(P.out) + row0 + threadIdx.x, c);
+    for (int t = 0; t < P.slots; t++)
+      c = __builtin_fmaf(vals[t * RB + threadIdx.x], ld_typed(P.scores, P.score_dtype, (int64_t)blockIdx.y * P.slots + t), c);
+    store<OT>(reinterpret_cast<OT*>(P.out) + (int64_t)blockIdx.y * P.out_token + row0 + threadIdx.x, c);
   }
 }
 
@@ -100,6 +102,8 @@ __global__ __launch_bounds__(256) void down_lean_kernel(const DownParams P) {
 
   // activations: piece idx of the LDS copy (slot t at piece t * xn) is piece idx - t * xn
   // of slot t; the first 256 * 2 * kXR pieces through registers, indices clamped
+  const int tok = blockIdx.y;   // token: its S slots' activations, experts and scores
+  const uint16_t* xtok = reinterpret_cast<const uint16_t*>(P.x) + (int64_t)tok * S * P.x_slot;
   const int xn = P.cols >> 3;
   const int xtotal = xn * S;
   // (two arrays of four: one array of eight is kept in scratch memory by the compiler)
@@ -111,7 +115,7 @@ __global__ __launch_bounds__(256) void down_lean_kernel(const DownParams P) {
     int t = 0;
 #pragma unroll
     for (int q = 1; q < S; q++) t += xidx[k] >= q * xn ? 1 : 0;
-    const uint4* xg = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(P.x) + (int64_t)t * P.x_slot);
+    const uint4* xg = reinterpret_cast<const uint4*>(xtok + (int64_t)t * P.x_slot);
     return xg[xidx[k] - t * xn];
   };
 #pragma unroll
@@ -121,7 +125,7 @@ __global__ __launch_bounds__(256) void down_lean_kernel(const DownParams P) {
 
   int64_t e[S];
 #pragma unroll
-  for (int s = 0; s < S; s++) e[s] = P.experts[s];
+  for (int s = 0; s < S; s++) e[s] = P.experts[tok * S + s];
   const uint8_t* wrow[S][ROWS];
   const uint8_t* srow[S][ROWS];
   bool rv[ROWS];
@@ -169,7 +173,7 @@ __global__ __launch_bounds__(256) void down_lean_kernel(const DownParams P) {
       int t = 0;
 #pragma unroll
       for (int q = 1; q < S; q++) t += idx >= q * xn ? 1 : 0;
-      xl[idx] = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(P.x) + (int64_t)t * P.x_slot)[idx - t * xn];
+      xl[idx] = reinterpret_cast<const uint4*>(xtok + (int64_t)t * P.x_slot)[idx - t * xn];
     }
   }
   lds_barrier();
@@ -218,9 +222,9 @@ __global__ __launch_bounds__(256) void down_lean_kernel(const DownParams P) {
   for (int s = 0; s < S; s++) {
     float v = round_to<RT>(acc[s][0]);
     if (P.bias != nullptr) v = round_to<RT>(v + ld_typed(P.bias, P.bias_dtype, e[s] * P.bias_expert + n));
-    c = __builtin_fmaf(v, ld_typed(P.scores, P.score_dtype, s), c);
+    c = __builtin_fmaf(v, ld_typed(P.scores, P.score_dtype, tok * S + s), c);
   }
-  store<OT>(reinterpret_cast<OT*>(P.out) + n, c);
+  store<OT>(reinterpret_cast<OT*>(P.out) + (int64_t)tok * P.out_token + n, c);
 }
 
 // ------------------------------------------------------------------ dispatch
@@ -229,7 +233,7 @@ template <Fmt F, typename XT, typename OT, typename RT, int LPR, int S>
 static int launch_down_lean(const DownParams& P, hipStream_t st) {
   constexpr int SUBS = 64 / LPR;
   const int64_t waves = ((int64_t)P.rows + SUBS - 1) / SUBS;   // one row per lane group
-  hipLaunchKernelGGL((down_lean_kernel<F, XT, OT, RT, LPR, 1, S>), dim3((unsigned)((waves + 3) / 4)), dim3(256),
+  hipLaunchKernelGGL((down_lean_kernel<F, XT, OT, RT, LPR, 1, S>), dim3((unsigned)((waves + 3) / 4), P.tokens), dim3(256),
                      (size_t)P.cols * 2 * S, st, P);
   return check_launch("mxfp_lowbit_weighted_down");
 }
@@ -255,7 +259,7 @@ static int launch_down(const DownParams& P, int lpr, hipStream_t st) {
   auto go = [&](auto kern, int rb) {
     const size_t lds = (size_t)P.cols * 2 * P.slots + (size_t)rb * 4 * P.slots;
     const int blocks = (P.rows + rb - 1) / rb;
-    hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), lds, st, P);
+    hipLaunchKernelGGL(kern, dim3(blocks, P.tokens), dim3(256), lds, st, P);
     return check_launch("mxfp_lowbit_weighted_down");
   };
   switch (lpr) {
@@ -286,14 +290,15 @@ static int down_dispatch(Fmt fmt, int out_dtype, const DownParams& P, int lpr, h
 
 using namespace tt;
 
-extern "C" int tt_mxfp_lowbit_weighted_down(const void* packed, int64_t w_expert_bytes, int64_t w_row_bytes,
+static int weighted_down_impl(const void* packed, int64_t w_expert_bytes, int64_t w_row_bytes,
                                             const void* scales, int64_t s_expert, int64_t s_row, int bits,
                                             const void* x, int x_dtype, int64_t x_slot,
                                             const int32_t* expert_indices, const void* router_scores,
                                             int score_dtype, int64_t selected, const void* bias, int bias_dtype,
                                             int64_t bias_expert, void* out, int out_dtype, int64_t rows,
-                                            int64_t cols, void* stream) {
+                                            int64_t cols, int64_t tokens, int64_t out_token, void* stream) {
   const char* what = "mxfp_lowbit_weighted_down";
+  TT_REQUIRE(tokens >= 1 && tokens <= 65535, "%s: bad token count", what);
   TT_REQUIRE(bits == 1 || bits == 2 || bits == 4, "%s: fused down requires packed Q1, Q2 or MXFP4 experts", what);
   TT_REQUIRE(valid_act_dtype(x_dtype) && valid_out_dtype(out_dtype), "%s: bad dtype codes", what);
   TT_REQUIRE(cols > 0 && cols % 32 == 0, "%s: cols must be a multiple of 32", what);
@@ -309,7 +314,8 @@ extern "C" int tt_mxfp_lowbit_weighted_down(const void* packed, int64_t w_expert
   if (bias) TT_REQUIRE(valid_out_dtype(bias_dtype), "%s: bad bias dtype", what);
   DownParams P{static_cast<const uint8_t*>(packed), w_expert_bytes, w_row_bytes,
                static_cast<const uint8_t*>(scales), s_expert, s_row, x, x_slot, expert_indices, router_scores, bias,
-               bias_expert, out, (int)rows, (int)cols, (int)selected, bias ? bias_dtype : TT_F32, score_dtype};
+               bias_expert, out, (int)rows, (int)cols, (int)selected, bias ? bias_dtype : TT_F32, score_dtype, out_token,
+               (int)tokens};
   const int lpr = tt_gemv_lanes_per_row(cols / 32, 1);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const Fmt fmt = fmt_for_bits(bits);
@@ -318,4 +324,28 @@ extern "C" int tt_mxfp_lowbit_weighted_down(const void* packed, int64_t w_expert
     return down_dispatch<f16_t, bf16_t>(fmt, out_dtype, P, lpr, st);
   }
   return down_dispatch<bf16_t, bf16_t>(fmt, out_dtype, P, lpr, st);
+}
+
+extern "C" int tt_mxfp_lowbit_weighted_down(const void* packed, int64_t w_expert_bytes, int64_t w_row_bytes,
+                                            const void* scales, int64_t s_expert, int64_t s_row, int bits,
+                                            const void* x, int x_dtype, int64_t x_slot,
+                                            const int32_t* expert_indices, const void* router_scores,
+                                            int score_dtype, int64_t selected, const void* bias, int bias_dtype,
+                                            int64_t bias_expert, void* out, int out_dtype, int64_t rows,
+                                            int64_t cols, void* stream) {
+  return weighted_down_impl(packed, w_expert_bytes, w_row_bytes, scales, s_expert, s_row, bits, x, x_dtype, x_slot,
+                            expert_indices, router_scores, score_dtype, selected, bias, bias_dtype, bias_expert, out,
+                            out_dtype, rows, cols, 1, 0, stream);
+}
+
+extern "C" int tt_mxfp_lowbit_weighted_down_tokens(const void* packed, int64_t w_expert_bytes, int64_t w_row_bytes,
+                                                   const void* scales, int64_t s_expert, int64_t s_row, int bits,
+                                                   const void* x, int x_dtype, int64_t x_slot,
+                                                   const int32_t* expert_indices, const void* router_scores,
+                                                   int score_dtype, int64_t selected, const void* bias, int bias_dtype,
+                                                   int64_t bias_expert, void* out, int out_dtype, int64_t out_token,
+                                                   int64_t rows, int64_t cols, int64_t tokens, void* stream) {
+  return weighted_down_impl(packed, w_expert_bytes, w_row_bytes, scales, s_expert, s_row, bits, x, x_dtype, x_slot,
+                            expert_indices, router_scores, score_dtype, selected, bias, bias_dtype, bias_expert, out,
+                            out_dtype, rows, cols, tokens, out_token, stream);
 }

@@ -40,7 +40,7 @@ __global__ __launch_bounds__(256) void swiglu_kernel(SwigluParams P) {
     E8Round<F, 2 * APW> cur;
     if (active) e8_fetch<F, LPR, 2 * APW>(cur, 0, l, nchunks, wrow, srow, rv);
     if (!staged) {
-      const uint32_t* xg = reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(P.x) + (int64_t)slot * P.x_slot);
+      const uint32_t* xg = reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(P.x) + (int64_t)(slot / P.x_div) * P.x_slot);
       for (int i = threadIdx.x; i < (P.cols >> 1); i += blockDim.x) xs_lds[i] = xg[i];
       __syncthreads();
       staged = true;
@@ -92,7 +92,7 @@ __global__ __launch_bounds__(256) void swiglu_lean_kernel(const SwigluParams P) 
   const int a0 = (int)(blockIdx.x * 4 + wave) * (APL * SUBS);
   // the slot's activations go to LDS (loads first, clamped indices)
   const int xn = P.cols >> 3;
-  const uint4* xg = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(P.x) + (int64_t)slot * P.x_slot);
+  const uint4* xg = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(P.x) + (int64_t)(slot / P.x_div) * P.x_slot);
   uint4 xreg[4];
   int xidx[4];
 #pragma unroll
@@ -249,15 +249,15 @@ static int swiglu_dispatch(Fmt fmt, int out_dtype, int bias_dtype, const SwigluP
 
 using namespace tt;
 
-// bits: 1 or 2 (E8M0 q1/q2, bf16 rounding), 4 (MXFP4, rounding in the activation dtype).
-extern "C" int tt_mxfp_lowbit_selected_swiglu(const void* packed, int64_t w_expert_bytes, int64_t w_row_bytes,
+static int selected_swiglu_impl(const void* packed, int64_t w_expert_bytes, int64_t w_row_bytes,
                                               const void* scales, int64_t s_expert, int64_t s_row, int bits,
                                               const void* x, int x_dtype, int64_t x_slot,
                                               const int32_t* expert_indices, int64_t selected, const void* bias,
                                               int bias_dtype, int64_t bias_expert, float alpha, float limit,
                                               void* out, int out_dtype, int64_t out_slot, int64_t activation_rows,
-                                              int64_t cols, void* stream) {
+                                              int64_t cols, int64_t tokens, void* stream) {
   const char* what = "mxfp_lowbit_selected_swiglu";
+  TT_REQUIRE(tokens >= 1 && tokens * selected <= 65535, "%s: bad token count", what);
   TT_REQUIRE(bits == 1 || bits == 2 || bits == 4, "%s: fused SwiGLU requires packed Q1, Q2 or MXFP4 experts", what);
   TT_REQUIRE(valid_act_dtype(x_dtype) && valid_out_dtype(out_dtype), "%s: bad dtype codes", what);
   TT_REQUIRE(cols > 0 && cols % 32 == 0 && cols <= 32768, "%s: cols must be a multiple of 32 up to 32768", what);
@@ -270,14 +270,40 @@ extern "C" int tt_mxfp_lowbit_selected_swiglu(const void* packed, int64_t w_expe
   if (bias) TT_REQUIRE(valid_out_dtype(bias_dtype), "%s: bad bias dtype", what);
   SwigluParams P{static_cast<const uint8_t*>(packed), w_expert_bytes, w_row_bytes,
                  static_cast<const uint8_t*>(scales), s_expert, s_row, x, x_slot, expert_indices, bias, bias_expert,
-                 alpha, limit, out, out_slot, (int)activation_rows, (int)cols};
+                 alpha, limit, out, out_slot, (int)activation_rows, (int)cols, tokens > 1 ? (int)selected : 1};
   const int lpr = tt_gemv_lanes_per_row(cols / 32, 1);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const Fmt fmt = fmt_for_bits(bits);
   const int bdt = bias ? bias_dtype : TT_F32;
   if (x_dtype == TT_F16) {
-    if (bits == 4) return swiglu_dispatch<f16_t, f16_t>(fmt, out_dtype, bdt, P, lpr, (int)selected, st);
-    return swiglu_dispatch<f16_t, bf16_t>(fmt, out_dtype, bdt, P, lpr, (int)selected, st);
+    if (bits == 4) return swiglu_dispatch<f16_t, f16_t>(fmt, out_dtype, bdt, P, lpr, (int)(tokens * selected), st);
+    return swiglu_dispatch<f16_t, bf16_t>(fmt, out_dtype, bdt, P, lpr, (int)(tokens * selected), st);
   }
-  return swiglu_dispatch<bf16_t, bf16_t>(fmt, out_dtype, bdt, P, lpr, (int)selected, st);
+  return swiglu_dispatch<bf16_t, bf16_t>(fmt, out_dtype, bdt, P, lpr, (int)(tokens * selected), st);
+}
+
+// bits: 1 or 2 (E8M0 q1/q2, bf16 rounding), 4 (MXFP4, rounding in the activation dtype).
+extern "C" int tt_mxfp_lowbit_selected_swiglu(const void* packed, int64_t w_expert_bytes, int64_t w_row_bytes,
+                                              const void* scales, int64_t s_expert, int64_t s_row, int bits,
+                                              const void* x, int x_dtype, int64_t x_slot,
+                                              const int32_t* expert_indices, int64_t selected, const void* bias,
+                                              int bias_dtype, int64_t bias_expert, float alpha, float limit,
+                                              void* out, int out_dtype, int64_t out_slot, int64_t activation_rows,
+                                              int64_t cols, void* stream) {
+  return selected_swiglu_impl(packed, w_expert_bytes, w_row_bytes, scales, s_expert, s_row, bits, x, x_dtype, x_slot,
+                              expert_indices, selected, bias, bias_dtype, bias_expert, alpha, limit, out, out_dtype,
+                              out_slot, activation_rows, cols, 1, stream);
+}
+
+extern "C" int tt_mxfp_lowbit_selected_swiglu_tokens(const void* packed, int64_t w_expert_bytes, int64_t w_row_bytes,
+                                                     const void* scales, int64_t s_expert, int64_t s_row, int bits,
+                                                     const void* x, int x_dtype, int64_t x_token,
+                                                     const int32_t* expert_indices, int64_t selected,
+                                                     const void* bias, int bias_dtype, int64_t bias_expert,
+                                                     float alpha, float limit, void* out, int out_dtype,
+                                                     int64_t out_slot, int64_t activation_rows, int64_t cols,
+                                                     int64_t tokens, void* stream) {
+  return selected_swiglu_impl(packed, w_expert_bytes, w_row_bytes, scales, s_expert, s_row, bits, x, x_dtype, x_token,
+                              expert_indices, selected, bias, bias_dtype, bias_expert, alpha, limit, out, out_dtype,
+                              out_slot, activation_rows, cols, tokens, stream);
 }

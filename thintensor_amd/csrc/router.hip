@@ -250,6 +250,14 @@ __global__ __launch_bounds__(1024) void norm_router_kernel(const NormRouterParam
   const int n = P.H;
   const int nchunks = n >> 5;
   const bool norm_wave = wave < 4;
+  // token blockIdx.x of a [tokens, H] batch (one workgroup per token)
+  const int64_t tok = blockIdx.x;
+  const XT* const left = reinterpret_cast<const XT*>(P.left) + tok * n;
+  const XT* const right = reinterpret_cast<const XT*>(P.right) + tok * n;
+  XT* const residual_out = reinterpret_cast<XT*>(P.residual_out) + tok * n;
+  XT* const norm_out = reinterpret_cast<XT*>(P.norm_out) + tok * n;
+  int32_t* const idx_out = P.idx_out + tok * P.top_k;
+  OT* const score_out = reinterpret_cast<OT*>(P.score_out) + tok * P.top_k;
 
   // ---- every load before the first wait: the norm inputs as 16-byte pieces (threads
   // 0-511, one piece of each vector; n <= 4096), then this wave's router rows and bias
@@ -259,8 +267,8 @@ __global__ __launch_bounds__(1024) void norm_router_kernel(const NormRouterParam
   // every thread loads (threads past the vector repeat its last piece), so no branch
   // separates these loads from the weight loads below
   const int q = (int)threadIdx.x < nq ? (int)threadIdx.x : nq - 1;
-  const uint4 in_a = reinterpret_cast<const uint4*>(P.left)[q];
-  const uint4 in_b = reinterpret_cast<const uint4*>(P.right)[q];
+  const uint4 in_a = reinterpret_cast<const uint4*>(left)[q];
+  const uint4 in_b = reinterpret_cast<const uint4*>(right)[q];
   const uint4 in_w = reinterpret_cast<const uint4*>(P.norm_w)[q];
   Raw<64> wr[2][2];
 #pragma unroll
@@ -326,8 +334,8 @@ __global__ __launch_bounds__(1024) void norm_router_kernel(const NormRouterParam
       const int i = threadIdx.x + 256 * k;
       if (i < n) {
         const float v = (res[k] * inv) * to_f32(lw[i]);
-        store<XT>(reinterpret_cast<XT*>(P.residual_out) + i, res[k]);
-        store<XT>(reinterpret_cast<XT*>(P.norm_out) + i, v);
+        store<XT>(residual_out + i, res[k]);
+        store<XT>(norm_out + i, v);
         store<XT>(xl + i, v);
       }
     }
@@ -367,7 +375,7 @@ __global__ __launch_bounds__(1024) void norm_router_kernel(const NormRouterParam
   __syncthreads();
   if (wave == 0) {
     const float l0 = lane < P.E ? logits[lane] : 0.0f;
-    wave_topk<OT>(l0, 0.0f, P.E, P.top_k, P.renorm != 0, P.idx_out, reinterpret_cast<OT*>(P.score_out));
+    wave_topk<OT>(l0, 0.0f, P.E, P.top_k, P.renorm != 0, idx_out, score_out);
   }
 }
 
@@ -447,20 +455,29 @@ extern "C" int tt_add_rms_norm_router_topk(const void* left, const void* right, 
                                            int64_t hidden_size, float eps, const void* weight, int w_dtype,
                                            int64_t w_row, const void* bias, int bias_dtype, int64_t experts,
                                            int64_t top_k, int renormalize, int32_t* indices_out, void* scores_out,
-                                           int score_dtype, void* stream) {
+                                           int score_dtype, int64_t tokens, void* stream) {
   const char* what = "add_rms_norm_router_topk";
+  TT_REQUIRE(tokens >= 1 && tokens <= 65535, "%s: bad token count", what);
   TT_REQUIRE(left && right && residual_out && norm_weight && norm_out, "%s: null pointer", what);
   const bool one_launch = experts <= kNormRouterExperts && hidden_size <= 4096 && hidden_size % 32 == 0 && hidden_size > 0 &&
                           x_dtype != TT_F32 && norm_w_dtype == x_dtype && norm_dtype == x_dtype &&
                           (w_dtype == TT_F16 || w_dtype == TT_BF16) && weight && indices_out && scores_out &&
                           aligned(weight, 16) && w_row % 8 == 0 && experts > 0 && top_k > 0 && top_k <= experts;
   if (!one_launch) {
-    // the two operators, each with its own checks
-    const int rc = tt_add_rms_norm(left, right, residual_out, x_dtype, norm_weight, norm_w_dtype, norm_out, norm_dtype,
-                                   hidden_size, eps, stream);
-    if (rc != TT_OK) return rc;
-    return tt_moe_router_matvec_topk(weight, w_dtype, w_row, norm_out, norm_dtype, hidden_size, bias, bias_dtype,
-                                     experts, top_k, renormalize, indices_out, scores_out, score_dtype, stream);
+    // the two operators per token, each with its own checks
+    const int64_t xs = hidden_size * (x_dtype == TT_F32 ? 4 : 2), ns = hidden_size * (norm_dtype == TT_F32 ? 4 : 2);
+    const int64_t ss = top_k * (score_dtype == TT_F32 ? 4 : 2);
+    for (int64_t t = 0; t < tokens; t++) {
+      auto at = [t](const void* p, int64_t bytes) { return static_cast<const char*>(p) + t * bytes; };
+      int rc = tt_add_rms_norm(at(left, xs), at(right, xs), const_cast<char*>(at(residual_out, xs)), x_dtype, norm_weight,
+                               norm_w_dtype, const_cast<char*>(at(norm_out, ns)), norm_dtype, hidden_size, eps, stream);
+      if (rc != TT_OK) return rc;
+      rc = tt_moe_router_matvec_topk(weight, w_dtype, w_row, at(norm_out, ns), norm_dtype, hidden_size, bias, bias_dtype,
+                                     experts, top_k, renormalize, indices_out + t * top_k,
+                                     const_cast<char*>(at(scores_out, ss)), score_dtype, stream);
+      if (rc != TT_OK) return rc;
+    }
+    return TT_OK;
   }
   NormRouterParams P;
   P.left = left; P.right = right; P.residual_out = residual_out; P.norm_w = norm_weight; P.norm_out = norm_out;
@@ -479,7 +496,7 @@ extern "C" int tt_add_rms_norm_router_topk(const void* left, const void* right, 
             set_error("%s: unsupported dtypes", what);
             return TT_ERR_UNSUPPORTED;
           } else {
-            hipLaunchKernelGGL((norm_router_kernel<WT, XT, BT, OT>), dim3(1), dim3(1024), 0,
+            hipLaunchKernelGGL((norm_router_kernel<WT, XT, BT, OT>), dim3((unsigned)tokens), dim3(1024), 0,
                                static_cast<hipStream_t>(stream), P);
             return check_launch(what);
           }

@@ -382,12 +382,13 @@ class MoEBatchDecoder:
 
     Every sequence has its own KV cache (``k_cache``/``v_cache`` [layers, batch * kv_heads,
     capacity, head_dim]: sequence b owns KV heads b * kv_heads ...) and token; the position
-    is shared.  Per sequence the step runs the fused bs=1 launches (QKV with the norm
-    prologue and RoPE / cache epilogue, o_proj, add+RMSNorm+router, expert SwiGLU and
-    weighted down), so the weights stream once per sequence and layer, mostly from the
-    last-level cache after the first.  Two launches cover the whole batch: attention (the
-    batch's query heads and KV heads are the heads of one call, so each head's arithmetic
-    is the bs=1 arithmetic) and the M-row lm_head argmax.  Each sequence's tokens equal
+    is shared.  Per sequence the step runs the fused bs=1 QKV (norm prologue, RoPE / cache
+    epilogue) and o_proj launches, whose dense weights stream once per sequence and layer
+    (mostly from the last-level cache after the first).  One launch each covers the whole
+    batch for attention (the batch's query and KV heads are the heads of one call, so each
+    head's arithmetic is the bs=1 arithmetic), add+RMSNorm+router (one workgroup per
+    token), the expert SwiGLU and weighted down (token-indexed slots) and the M-row lm_head
+    argmax.  Each sequence's tokens equal
     MoEDecoder's stream for that sequence bit for bit."""
 
     def __init__(self, backend: HipDecodeBackend, weights: MoEWeights, batch: int, k_cache: torch.Tensor,
@@ -407,9 +408,18 @@ class MoEBatchDecoder:
         self.position = torch.zeros(1, device=dev, dtype=torch.int32)
         self.base = torch.zeros(1, device=dev, dtype=torch.int32)
         self.history = torch.zeros((batch, s.max_new_tokens), device=dev, dtype=torch.int64)
-        self.q_all = torch.empty((batch, s.q_dim), device=dev, dtype=torch.float16)
-        self.attn_all = torch.empty((batch, s.q_dim), device=dev, dtype=torch.float16)
-        self.final_all = torch.empty((batch, s.hidden), device=dev, dtype=torch.float16)
+        dt = torch.float16
+        self.q_all = torch.empty((batch, s.q_dim), device=dev, dtype=dt)
+        self.attn_all = torch.empty((batch, s.q_dim), device=dev, dtype=dt)
+        self.final_all = torch.empty((batch, s.hidden), device=dev, dtype=dt)
+        self.hidden_a = torch.empty((batch, s.hidden), device=dev, dtype=dt)
+        self.hidden_b = torch.empty((batch, s.hidden), device=dev, dtype=dt)
+        self.normed = torch.empty((batch, s.hidden), device=dev, dtype=dt)
+        self.attn_out = torch.empty((batch, s.hidden), device=dev, dtype=dt)
+        self.moe = torch.empty((batch, s.hidden), device=dev, dtype=dt)
+        self.router_idx = torch.empty((batch, s.top_k), device=dev, dtype=torch.int32)
+        self.router_scores = torch.empty((batch, s.top_k), device=dev, dtype=dt)
+        self.act = torch.empty((batch * s.top_k, s.intermediate), device=dev, dtype=dt)
         self.sinks = [L.sinks.repeat(batch).contiguous() for L in weights.layers]
         kv = s.kv_heads
         self.subs: list[MoEDecoder] = []
@@ -421,6 +431,8 @@ class MoEBatchDecoder:
             sub.position = self.position
             sub.qkv = self.q_all[b]
             sub.attn = self.attn_all[b]
+            sub.hidden_a, sub.hidden_b, sub.normed = self.hidden_a[b], self.hidden_b[b], self.normed[b]
+            sub.attn_out, sub.moe = self.attn_out[b], self.moe[b]
             sub._build_fused()
             self.subs.append(sub)
         self.graph: torch.cuda.CUDAGraph | None = None
@@ -442,14 +454,14 @@ class MoEBatchDecoder:
                                           sinks=self.sinks[li], active_tokens=(self.position, 1))
             for sub in self.subs:
                 be.multi_matvec_bias((L.o,), (L.o_bias,), sub.attn, sub.attn_out)
-                be.add_rms_norm_router_topk(sub.hidden_a, sub.attn_out, sub.hidden_b, L.ln2, sub.normed, s.eps,
-                                            L.router, sub.router_idx, sub.router_scores, bias=L.router_bias,
-                                            renormalize=True)
-                be.mxfp_lowbit_selected_swiglu(L.gate_up_blocks, L.gate_up_scales, sub.normed, sub.router_idx, sub.act,
-                                               bits=4, alpha=s.swiglu_alpha, limit=s.swiglu_limit,
-                                               bias=L.gate_up_bias)
-                be.mxfp_lowbit_weighted_down(L.down_blocks, L.down_scales, sub.act, sub.router_idx,
-                                             sub.router_scores, sub.moe, bits=4, bias=L.down_bias)
+            be.add_rms_norm_router_topk(self.hidden_a, self.attn_out, self.hidden_b, L.ln2, self.normed, s.eps,
+                                        L.router, self.router_idx, self.router_scores, bias=L.router_bias,
+                                        renormalize=True)
+            be.mxfp_lowbit_selected_swiglu_tokens(L.gate_up_blocks, L.gate_up_scales, self.normed, self.router_idx,
+                                                  self.act, bits=4, alpha=s.swiglu_alpha, limit=s.swiglu_limit,
+                                                  bias=L.gate_up_bias)
+            be.mxfp_lowbit_weighted_down_tokens(L.down_blocks, L.down_scales, self.act, self.router_idx,
+                                                self.router_scores, self.moe, bits=4, bias=L.down_bias)
         for b, sub in enumerate(self.subs):
             be.add(sub.hidden_b, sub.moe, sub.hidden_a)
             be.rms_norm(sub.hidden_a, w.final_norm, self.final_all[b], s.eps)
