@@ -142,6 +142,14 @@ int tt_mxfp_lowbit_weighted_down(const void* packed, int64_t w_expert_bytes, int
                                  const void* bias, int bias_dtype, int64_t bias_expert,
                                  void* out, int out_dtype, int64_t rows, int64_t cols, void* stream);
 
+/* out[t] = W x[t] (+ bias) for m activation rows (x rows x_row elements apart, out rows
+ * out_row apart), fp16/bf16 dense W; each row equals tt_multi_matvec_bias on that row
+ * alone.  No reference counterpart: it serves the batched decode of independent
+ * sequences (the reference decodes one token per step). */
+int tt_matvec_bias_rows(const void* weight, int w_dtype, int64_t w_row, const void* bias, const void* x,
+                        int x_dtype, int64_t x_row, void* out, int out_dtype, int64_t out_row, int64_t m,
+                        int64_t rows, int64_t cols, void* stream);
+
 /* Several tokens at once, each with `selected` experts (no reference counterpart: the
  * reference decodes one token per step; these serve the batched decode of independent
  * sequences).  Token t's activation vector is x + t * x_token; its slots are
@@ -414,6 +422,15 @@ typedef struct tt_fused_gemv {
   int64_t table_row;
   int64_t table_rows;
   int64_t head_dim;
+  /* Several tokens (independent sequences at one shared position) in one launch; 0 or 1
+   * = one.  Token t reads x / left / right / embed row token[t] and writes residual_out
+   * at + t * token_x elements, TT_SEG_PLAIN / ROPE_OUT / SILU outputs at + t * token_out
+   * and ROPE_CACHE / CACHE outputs at + t * token_cache.  Each token's values equal the
+   * one-token launch's.  Not for the lm_head. */
+  int64_t tokens;
+  int64_t token_x;
+  int64_t token_out;
+  int64_t token_cache;
 } tt_fused_gemv;
 
 int tt_fused_gemv_run(const tt_fused_gemv* desc, void* stream);

@@ -284,6 +284,28 @@ def test_fused_weighted_down(backend, device, bits):
     assert_bits_equal(from_torch_bits(out), want, f"weighted down bits={bits}")
 
 
+@pytest.mark.parametrize("m,rows,cols,wdt", [(8, 2880, 4096, "f16"), (3, 1000, 2048, "bf16"), (5, 300, 5120, "f16")])
+def test_matvec_bias_rows(backend, device, m, rows, cols, wdt):
+    """M activation rows in one launch (or one per row past 4096 columns) equal the
+    single-row GEMV with bias row by row."""
+    g = rng(m + rows + cols)
+    T = lambda a, bf=False: to_torch(a, device, bf16=bf)
+    if wdt == "bf16":
+        w = T(bf16_bits(g.standard_normal((rows, cols)).astype(np.float32) * 0.02), True)
+        x = T(bf16_bits(g.standard_normal((m, cols)).astype(np.float32)), True)
+        b = T(bf16_bits(g.standard_normal(rows).astype(np.float32) * 0.1), True)
+        dt = torch.bfloat16
+    else:
+        w, x, b = T(f16_normal(g, (rows, cols), 0.02)), T(f16_normal(g, (m, cols))), T(f16_normal(g, rows, 0.1))
+        dt = torch.float16
+    out = torch.empty((m, rows), device=device, dtype=dt)
+    backend.matvec_bias_rows(w, b, x, out)
+    for t in range(m):
+        o1 = torch.empty(rows, device=device, dtype=dt)
+        backend.multi_matvec_bias((w,), (b,), x[t], o1)
+        assert_bits_equal(from_torch_bits(out[t]), from_torch_bits(o1), f"row {t}")
+
+
 @pytest.mark.parametrize("bits,tokens", [(4, 8), (2, 3)])
 def test_expert_kernels_token_batched(backend, device, bits, tokens):
     """SwiGLU and weighted down over several tokens (each with its own activation

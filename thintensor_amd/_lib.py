@@ -44,7 +44,8 @@ class FusedGemv(ctypes.Structure):
         ("right", _P), ("embed", _P), ("embed_row", _L), ("vocab", _L), ("token", _P), ("norm_weight", _P),
         ("eps", ctypes.c_float), ("count", ctypes.c_int32), ("residual_out", _P), ("seg", FusedSegment * 3),
         ("position", _P), ("capacity", _L), ("cache_head", _L), ("cos_table", _P), ("sin_table", _P),
-        ("table_row", _L), ("table_rows", _L), ("head_dim", _L),
+        ("table_row", _L), ("table_rows", _L), ("head_dim", _L), ("tokens", _L), ("token_x", _L),
+        ("token_out", _L), ("token_cache", _L),
     ]
 
 
@@ -89,6 +90,7 @@ SIGNATURES: dict[str, list] = {
     "tt_moe_router_topk": [_P, _I, _L, _L, _I, _P, _P, _I, _P],
     "tt_add_rms_norm_router_topk": [_P, _P, _P, _I, _P, _I, _P, _I, _L, _F, _P, _I, _L, _P, _I, _L, _L, _I, _P, _P,
                                     _I, _L, _P],
+    "tt_matvec_bias_rows": [_P, _I, _L, _P, _P, _I, _L, _P, _I, _L, _L, _L, _L, _P],
     "tt_mxfp_lowbit_selected_swiglu_tokens": [_P, _L, _L, _P, _L, _L, _I, _P, _I, _L, _P, _L, _P, _I, _L, _F, _F, _P,
                                               _I, _L, _L, _L, _L, _P],
     "tt_mxfp_lowbit_weighted_down_tokens": [_P, _L, _L, _P, _L, _L, _I, _P, _I, _L, _P, _P, _I, _L, _P, _I, _L, _P, _I,

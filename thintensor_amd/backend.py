@@ -489,6 +489,25 @@ class HipDecodeBackend:
         _lib.check(rc, "mxfp_lowbit_weighted_down")
         return out
 
+    def matvec_bias_rows(self, weight: torch.Tensor, bias: torch.Tensor | None, x: torch.Tensor,
+                         out: torch.Tensor) -> torch.Tensor:
+        """out[t] = W x[t] (+ bias) for x [M, cols], out [M, rows]; each row equals
+        ``multi_matvec_bias((weight,), (bias,), x[t], out[t])``.  No reference
+        counterpart (batched decode of independent sequences)."""
+        rows, cols = map(int, weight.shape)
+        if x.ndim != 2 or out.ndim != 2 or int(x.shape[1]) != cols or int(out.shape[1]) != rows or \
+                x.shape[0] != out.shape[0] or x.stride(1) != 1 or out.stride(1) != 1 or weight.stride(1) != 1:
+            raise ValueError("matvec_bias_rows takes W [rows, cols], x [M, cols] and out [M, rows]")
+        if bias is not None and int(bias.numel()) != rows:
+            raise ValueError("bias does not match the weight rows")
+        _require_cuda(weight, x, out)
+        rc = self.lib.tt_matvec_bias_rows(weight.data_ptr(), _code(weight, "matvec"), weight.stride(0),
+                                          bias.data_ptr() if bias is not None else None, x.data_ptr(),
+                                          _code(x, "matvec"), x.stride(0), out.data_ptr(), _code(out, "matvec"),
+                                          out.stride(0), int(x.shape[0]), rows, cols, _stream(out))
+        _lib.check(rc, "matvec_bias_rows")
+        return out
+
     def mxfp_lowbit_selected_swiglu_tokens(self, packed_weight: torch.Tensor, scales: torch.Tensor, x: torch.Tensor,
                                            expert_indices: torch.Tensor, out: torch.Tensor, *, bits: int,
                                            alpha: float, limit: float,

@@ -48,6 +48,7 @@ struct LeanFused {
   const void* cos;
   const void* sin;
   int64_t table_row, table_rows;
+  int64_t token_x, token_out, token_cache;   // strides of token blockIdx.y
 };
 
 template <Fmt F, typename XT, int LPR, int ROWS, Pro PRO>
@@ -70,6 +71,7 @@ __global__ __launch_bounds__(256) void fused_lean_kernel(const LeanFused P) {
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int v0 = (int)(blockIdx.x * 4 + wave) * (ROWS * SUBS);   // first virtual row (uniform)
   const bool active = v0 < P.vtotal;
+  const int64_t tok = blockIdx.y;   // token of a multi-token launch (0 otherwise)
   const int si = (P.nseg > 1 && v0 >= P.seg[1].vbegin ? 1 : 0) + (P.nseg > 2 && v0 >= P.seg[2].vbegin ? 1 : 0);
   const LeanSeg& S = si == 0 ? P.seg[0] : (si == 1 ? P.seg[1] : P.seg[2]);
   const int kind = S.kind;
@@ -133,13 +135,13 @@ __global__ __launch_bounds__(256) void fused_lean_kernel(const LeanFused P) {
   if constexpr (PRO != Pro::kLoad) {
     const uint16_t* pa;
     if constexpr (PRO == Pro::kEmbedNorm) {
-      int64_t t = P.token[0];
+      int64_t t = P.token[tok];
       t = t < 0 ? 0 : (t >= P.vocab ? P.vocab - 1 : t);
       pa = reinterpret_cast<const uint16_t*>(P.embed) + t * P.embed_row;
     } else {
-      pa = reinterpret_cast<const uint16_t*>(P.left);
+      pa = reinterpret_cast<const uint16_t*>(P.left) + tok * P.token_x;
     }
-    const uint16_t* pb = reinterpret_cast<const uint16_t*>(P.right);
+    const uint16_t* pb = reinterpret_cast<const uint16_t*>(P.right) + tok * P.token_x;
     const uint16_t* pw = reinterpret_cast<const uint16_t*>(P.norm_w);
 #pragma unroll
     for (int k = 0; k < kHeld; k++) {
@@ -159,7 +161,8 @@ __global__ __launch_bounds__(256) void fused_lean_kernel(const LeanFused P) {
   if constexpr (PRO == Pro::kLoad) {
     const int xn = cols >> 3;
     for (int idx = threadIdx.x; idx < xn; idx += 256)
-      reinterpret_cast<uint4*>(xs_lds)[idx] = reinterpret_cast<const uint4*>(P.x)[idx];
+      reinterpret_cast<uint4*>(xs_lds)[idx] = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(P.x) +
+                                                                             tok * P.token_x)[idx];
   } else {
     // RMSNorm of the residual stream with the thread partition, reduction order and
     // rounding points of the standalone rms_norm / add_rms_norm kernels; workgroup 0
@@ -185,7 +188,7 @@ __global__ __launch_bounds__(256) void fused_lean_kernel(const LeanFused P) {
       const int i = threadIdx.x + 256 * k;
       if (i < n) {
         const float w = to_f32(XT{rw[k]});
-        if (writer) store<XT>(reinterpret_cast<XT*>(P.residual_out) + i, rr[k]);
+        if (writer) store<XT>(reinterpret_cast<XT*>(P.residual_out) + tok * P.token_x + i, rr[k]);
         store<XT>(xl + i, PRO == Pro::kAddNorm ? (rr[k] * inv) * w : (rr[k] * inv) * (w + 0.0f));
       }
     }
@@ -249,7 +252,7 @@ __global__ __launch_bounds__(256) void fused_lean_kernel(const LeanFused P) {
   if (kind == kSegPlain) {
     if (ok) {
       if (S.bias != nullptr) v = round_to<XT>(v) + to_f32(reinterpret_cast<const XT*>(S.bias)[fr]);
-      store<XT>(reinterpret_cast<XT*>(S.out) + fr, v);
+      store<XT>(reinterpret_cast<XT*>(S.out) + tok * P.token_out + fr, v);
     }
     return;
   }
@@ -259,7 +262,7 @@ __global__ __launch_bounds__(256) void fused_lean_kernel(const LeanFused P) {
   const float val = round_to<XT>(v);
   const float pv = xor_partner<ROWS / 2 < 1 ? 1 : ROWS / 2>(val);   // the other half of the pair
   if (kind == kSegSilu) {
-    if (ok && !odd) store<XT>(reinterpret_cast<XT*>(S.out) + ph, silu_mul_val(val, pv));
+    if (ok && !odd) store<XT>(reinterpret_cast<XT*>(S.out) + tok * P.token_out + ph, silu_mul_val(val, pv));
     return;
   }
   const int64_t pos = P.pos != nullptr ? (int64_t)P.pos[0] : 0;
@@ -277,10 +280,10 @@ __global__ __launch_bounds__(256) void fused_lean_kernel(const LeanFused P) {
   }
   if (ok) {
     if (kind == kSegRopeOut) {
-      store<XT>(reinterpret_cast<XT*>(S.out) + ph, o);
+      store<XT>(reinterpret_cast<XT*>(S.out) + tok * P.token_out + ph, o);
     } else if (pos >= 0 && pos < P.capacity) {
       const int64_t h = ph / D, d = ph - h * D;
-      store<XT>(reinterpret_cast<XT*>(S.out) + h * P.cache_head + pos * D + d, o);
+      store<XT>(reinterpret_cast<XT*>(S.out) + tok * P.token_cache + h * P.cache_head + pos * D + d, o);
     }
   }
 }
@@ -331,6 +334,9 @@ LeanFused lean_params(const tt_fused_gemv* d, int per_batch) {
   P.sin = d->sin_table;
   P.table_row = d->table_row;
   P.table_rows = d->table_rows;
+  P.token_x = d->token_x;
+  P.token_out = d->token_out;
+  P.token_cache = d->token_cache;
   return P;
 }
 
@@ -355,7 +361,7 @@ int launch_lean_lpr(const tt_fused_gemv* d, hipStream_t st) {
   const int per_batch = rpw * (64 / LPR);
   const LeanFused P = lean_params(d, per_batch);
   const int64_t waves = P.vtotal / per_batch;
-  const dim3 grid((unsigned)((waves + 3) / 4));
+  const dim3 grid((unsigned)((waves + 3) / 4), (unsigned)(d->tokens > 1 ? d->tokens : 1));
   const size_t lds = (size_t)d->cols * 2;
   if (rpw == 4) hipLaunchKernelGGL((fused_lean_kernel<F, XT, LPR, 4, PRO>), grid, dim3(256), lds, st, P);
   else hipLaunchKernelGGL((fused_lean_kernel<F, XT, LPR, 2, PRO>), grid, dim3(256), lds, st, P);
@@ -476,6 +482,13 @@ int validate(const tt_fused_gemv* d, bool lm_head) {
   if (needs_rope) {
     TT_REQUIRE(d->cos_table && d->sin_table && d->table_rows > 0 && d->table_row >= d->head_dim / 2,
                "%s: RoPE segments need the cos / sin tables", kWhat);
+  }
+  TT_REQUIRE(d->tokens >= 0 && d->tokens <= 65535, "%s: bad token count", kWhat);
+  if (d->tokens > 1) {
+    TT_UNSUPPORTED(!lm_head && lean_fits(d), "%s: several tokens per launch need cols <= 4096 and 32-bit offsets",
+                   kWhat);
+    TT_REQUIRE(d->token_x >= d->cols && d->token_x % 8 == 0 && d->token_out >= 0 && d->token_cache >= 0,
+               "%s: bad token strides", kWhat);
   }
   return TT_OK;
 }

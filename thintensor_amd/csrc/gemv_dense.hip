@@ -86,6 +86,48 @@ extern "C" int tt_multi_matvec_bias(int count, const void* const* weights, int w
   return launch_types<Fmt::kBF16W, SMode::kNone, float, 2>(x_dtype, out_dtype, Lg, lpr, P, 1, st, what);
 }
 
+extern "C" int tt_matvec_bias_rows(const void* weight, int w_dtype, int64_t w_row, const void* bias, const void* x,
+                                   int x_dtype, int64_t x_row, void* out, int out_dtype, int64_t out_row, int64_t m,
+                                   int64_t rows, int64_t cols, void* stream) {
+  const char* what = "matvec_bias_rows";
+  TT_REQUIRE(m >= 1 && m <= 65535, "%s: 1 to 65535 activation rows", what);
+  TT_REQUIRE(weight && x && out && rows > 0 && cols > 0 && cols % 32 == 0, "%s: bad arguments", what);
+  TT_REQUIRE(w_dtype == TT_F16 || w_dtype == TT_BF16, "%s: weights must be fp16 or bf16", what);
+  const int64_t xsz = x_dtype == TT_F32 ? 4 : 2, osz = out_dtype == TT_F32 ? 4 : 2;
+  const bool one_launch = m > 1 && x_dtype == out_dtype && x_dtype != TT_F32 && aligned(weight, 16) &&
+                          (w_row * 2) % 16 == 0 && w_row >= cols && aligned(x, 16) && x_row % 8 == 0 &&
+                          x_row >= cols && out_row >= rows && lean_fits(rows, w_row * 2, 0, cols);
+  if (!one_launch) {
+    // the single-row operator per activation row
+    for (int64_t t = 0; t < m; t++) {
+      const void* w_arr[1] = {weight};
+      const int64_t wr[1] = {w_row};
+      const int64_t r[1] = {rows};
+      const void* b_arr[1] = {bias};
+      const int rc = tt_multi_matvec_bias(1, w_arr, w_dtype, wr, r, b_arr, static_cast<const char*>(x) + t * x_row * xsz,
+                                          x_dtype, static_cast<char*>(out) + t * out_row * osz, out_dtype, cols, stream);
+      if (rc != TT_OK) return rc;
+    }
+    return TT_OK;
+  }
+  // rows of the batch are slots of the lean kernel (blockIdx.y), each with its own
+  // activation and output row; the arithmetic per row is the single-row kernel's
+  LeanParams L{};
+  L.w = static_cast<const uint8_t*>(weight);
+  L.x = x;
+  L.out = out;
+  L.bias = bias;
+  L.x_slot = x_row;
+  L.out_slot = out_row;
+  L.w_row = (uint32_t)(w_row * 2);
+  L.rows = (int)rows;
+  L.cols = (int)cols;
+  const int lpr = tt_gemv_lanes_per_row(cols / 32, 1);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (w_dtype == TT_F16) return lean_launch<Fmt::kF16W, SMode::kNone, float, 1>(x_dtype, lpr, L, (int)m, st, what);
+  return lean_launch<Fmt::kBF16W, SMode::kNone, float, 1>(x_dtype, lpr, L, (int)m, st, what);
+}
+
 extern "C" int tt_multi_matvec(int count, const void* const* weights, int w_dtype, const int64_t* w_row,
                                const int64_t* rows, const void* x, int x_dtype, void* out, int out_dtype,
                                int64_t cols, void* stream) {

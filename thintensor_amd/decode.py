@@ -27,8 +27,6 @@ Differences from the reference, by design:
 
 from __future__ import annotations
 
-import dataclasses
-
 import torch
 
 from . import _lib
@@ -382,13 +380,12 @@ class MoEBatchDecoder:
 
     Every sequence has its own KV cache (``k_cache``/``v_cache`` [layers, batch * kv_heads,
     capacity, head_dim]: sequence b owns KV heads b * kv_heads ...) and token; the position
-    is shared.  Per sequence the step runs the fused bs=1 QKV (norm prologue, RoPE / cache
-    epilogue) and o_proj launches, whose dense weights stream once per sequence and layer
-    (mostly from the last-level cache after the first).  One launch each covers the whole
-    batch for attention (the batch's query and KV heads are the heads of one call, so each
-    head's arithmetic is the bs=1 arithmetic), add+RMSNorm+router (one workgroup per
-    token), the expert SwiGLU and weighted down (token-indexed slots) and the M-row lm_head
-    argmax.  Each sequence's tokens equal
+    is shared.  Every launch covers the whole batch: the fused QKV (norm prologue, RoPE /
+    cache epilogue) and o_proj with a token grid dimension, attention (the batch's query
+    and KV heads are the heads of one call, so each head's arithmetic is the bs=1
+    arithmetic), add+RMSNorm+router (one workgroup per token), the expert SwiGLU and
+    weighted down (token-indexed slots) and the M-row lm_head argmax; only the final
+    add + RMSNorm runs per sequence.  Each sequence's tokens equal
     MoEDecoder's stream for that sequence bit for bit."""
 
     def __init__(self, backend: HipDecodeBackend, weights: MoEWeights, batch: int, k_cache: torch.Tensor,
@@ -421,22 +418,35 @@ class MoEBatchDecoder:
         self.router_scores = torch.empty((batch, s.top_k), device=dev, dtype=dt)
         self.act = torch.empty((batch * s.top_k, s.intermediate), device=dev, dtype=dt)
         self.sinks = [L.sinks.repeat(batch).contiguous() for L in weights.layers]
-        kv = s.kv_heads
-        self.subs: list[MoEDecoder] = []
-        for b in range(batch):
-            wb = dataclasses.replace(weights, k_cache=k_cache[:, b * kv:(b + 1) * kv],
-                                     v_cache=v_cache[:, b * kv:(b + 1) * kv])
-            sub = MoEDecoder(backend, wb, fused=True)
-            sub.token = self.tokens[b]
-            sub.position = self.position
-            sub.qkv = self.q_all[b]
-            sub.attn = self.attn_all[b]
-            sub.hidden_a, sub.hidden_b, sub.normed = self.hidden_a[b], self.hidden_b[b], self.normed[b]
-            sub.attn_out, sub.moe = self.attn_out[b], self.moe[b]
-            sub._build_fused()
-            self.subs.append(sub)
+        self._build_qkv()
         self.graph: torch.cuda.CUDAGraph | None = None
         self._graph_stream: torch.cuda.Stream | None = None
+
+    def _build_qkv(self) -> None:
+        """One multi-token fused QKV descriptor per layer: MoEDecoder's descriptor with the
+        batch's buffers and per-token strides (sequence t's KV heads follow sequence t-1's)."""
+        w, s, B = self.w, self.s, self.batch
+        act = _ACT[torch.float16]
+        self._qkv_desc = []
+        for li, L in enumerate(w.layers):
+            d = _lib.FusedGemv()
+            d.weight_format, d.weight_dtype, d.act_dtype, d.cols = _lib.FMT_DENSE, _ACT[L.q.dtype], act, s.hidden
+            if li == 0:
+                d.prologue = _lib.PRO_EMBED_NORM
+                d.embed, d.embed_row, d.vocab = w.embed.data_ptr(), w.embed.stride(0), int(w.embed.shape[0])
+                d.token = self.tokens.data_ptr()
+            else:
+                d.prologue = _lib.PRO_ADD_NORM
+                d.left, d.right = self.hidden_b.data_ptr(), self.moe.data_ptr()
+            d.norm_weight, d.eps, d.residual_out = L.ln1.data_ptr(), s.eps, self.hidden_a.data_ptr()
+            d.count = 3
+            _dense_segment(d.seg[0], L.q, L.q_bias, self.q_all, _lib.SEG_ROPE_OUT)
+            _dense_segment(d.seg[1], L.k, L.k_bias, self.k_cache[li], _lib.SEG_ROPE_CACHE)
+            _dense_segment(d.seg[2], L.v, L.v_bias, self.v_cache[li], _lib.SEG_CACHE)
+            _kv_context(d, self, w.cos, w.sin, s.head_dim, self.k_cache[li])
+            d.tokens, d.token_x, d.token_out = B, s.hidden, s.q_dim
+            d.token_cache = s.kv_heads * self.k_cache[li].stride(0)
+            self._qkv_desc.append(d)
 
     def _reserve_scratch(self) -> None:
         s = self.s
@@ -447,13 +457,11 @@ class MoEBatchDecoder:
         """One token of every sequence, logged at history[:, position - base]; advances the position."""
         be, w, s, B = self.be, self.w, self.s, self.batch
         for li, L in enumerate(w.layers):
-            for sub in self.subs:
-                be.fused_gemv(sub._qkv_desc[li])
+            be.fused_gemv(self._qkv_desc[li])
             be.single_token_gqa_attention(self.q_all.view(-1), self.k_cache[li], self.v_cache[li],
                                           self.attn_all.view(-1), B * s.heads, B * s.kv_heads, s.head_dim,
                                           sinks=self.sinks[li], active_tokens=(self.position, 1))
-            for sub in self.subs:
-                be.multi_matvec_bias((L.o,), (L.o_bias,), sub.attn, sub.attn_out)
+            be.matvec_bias_rows(L.o, L.o_bias, self.attn_all, self.attn_out)
             be.add_rms_norm_router_topk(self.hidden_a, self.attn_out, self.hidden_b, L.ln2, self.normed, s.eps,
                                         L.router, self.router_idx, self.router_scores, bias=L.router_bias,
                                         renormalize=True)
@@ -462,9 +470,9 @@ class MoEBatchDecoder:
                                                   bias=L.gate_up_bias)
             be.mxfp_lowbit_weighted_down_tokens(L.down_blocks, L.down_scales, self.act, self.router_idx,
                                                 self.router_scores, self.moe, bits=4, bias=L.down_bias)
-        for b, sub in enumerate(self.subs):
-            be.add(sub.hidden_b, sub.moe, sub.hidden_a)
-            be.rms_norm(sub.hidden_a, w.final_norm, self.final_all[b], s.eps)
+        for b in range(B):
+            be.add(self.hidden_b[b], self.moe[b], self.hidden_a[b])
+            be.rms_norm(self.hidden_a[b], w.final_norm, self.final_all[b], s.eps)
         be.matvec_argmax_batched(w.lm_head, self.final_all, out=self.tokens)
         for b in range(B):
             be.record_token(self.tokens[b], self.position, self.base, self.history[b])
