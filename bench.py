@@ -46,6 +46,8 @@ def _parse() -> argparse.Namespace:
     p.add_argument("--unfused", action="store_true", help="decode with one launch per reference operator")
     p.add_argument("--roofline-only", action="store_true",
                    help="only the int4 roofline phase (used for hardware-counter runs)")
+    p.add_argument("--batched-only", action="store_true",
+                   help="only the batched small-M GEMM phase (used for MFMA counter runs)")
     return p.parse_args()
 
 
@@ -354,6 +356,11 @@ def main() -> int:
 
     _lib.load()  # fails loudly when the HIP library is missing
 
+    if args.batched_only:
+        from thintensor_amd.backend import HipDecodeBackend
+        be = HipDecodeBackend(torch.device("cuda:0"), torch.float16, 5120, 5120, 1024, 17920)
+        print(json.dumps({"batched_5120": batched_phase(be, args.seed + 6)}), flush=True)
+        return 0
     if args.roofline_only:
         # the roofline kernel alone, plus a plain 256 MiB device copy whose byte count
         # calibrates hardware traffic counters (FETCH_SIZE / WRITE_SIZE) of the same run
