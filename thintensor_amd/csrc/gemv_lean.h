@@ -31,7 +31,8 @@ struct LeanParams {
   int rows, cols, aff_zero;
 };
 
-template <Fmt F, SMode SM, typename XT, typename OT, typename ST, int LPR, int ROWS, int L, int XM, bool EXP>
+template <Fmt F, SMode SM, typename XT, typename OT, typename ST, int LPR, int ROWS, int L, int XM, bool EXP,
+          int PFR = 1>
 __global__ __launch_bounds__(256) void lean_gemv_kernel(const LeanParams P) {
   constexpr int B = FmtInfo<F>::kBytes;
   constexpr bool kGroup = SM == SMode::kGroup || SM == SMode::kGroupAff;
@@ -143,8 +144,10 @@ __global__ __launch_bounds__(256) void lean_gemv_kernel(const LeanParams P) {
       for (int i = 0; i < ROWS; i++) d.e[i] = reinterpret_cast<const uint8_t*>(sbase)[eoff[i] + j];
     }
   };
-  Round cur;
-  fetch(0, cur);
+  // PFR > 1: rounds requested PFR at a time (past the last they re-read its chunk, unused)
+  Round ring[PFR];
+#pragma unroll
+  for (int k = 0; k < PFR; k++) fetch(k, ring[k]);
 
   const uint32_t* xs = xs_lds;
   if constexpr (XM == 0) {
@@ -158,11 +161,7 @@ __global__ __launch_bounds__(256) void lean_gemv_kernel(const LeanParams P) {
   float acc[NVG];
 #pragma unroll
   for (int k = 0; k < NVG; k++) acc[k] = 0.0f;
-  int r = 0;
-  do {   // the host guarantees one round (cols >= 32)
-    Round nxt;
-    const bool more = r + 1 < rounds;
-    if (more) fetch(r + 1, nxt);
+  auto consume = [&](const Round& c, int r) {
     const int j = r * LPR + l;
     const bool cv = j < nchunks;
     uint32_t xw[16];
@@ -170,12 +169,12 @@ __global__ __launch_bounds__(256) void lean_gemv_kernel(const LeanParams P) {
       const uint4* xp = reinterpret_cast<const uint4*>(xs + (cv ? j : 0) * 16);
 #pragma unroll
       for (int q = 0; q < 4; q++) {
-        const uint4 v = XM == 1 ? cur.xc[q] : xp[q];
+        const uint4 v = XM == 1 ? c.xc[q] : xp[q];
         xw[4 * q] = v.x; xw[4 * q + 1] = v.y; xw[4 * q + 2] = v.z; xw[4 * q + 3] = v.w;
       }
     }
     float p[ROWS];
-    chunk_dot_rows<F, XT, ROWS>(cur.w, xw, p);
+    chunk_dot_rows<F, XT, ROWS>(c.w, xw, p);
 #pragma unroll
     for (int i = 0; i < ROWS; i++) p[i] = (cv && rv[i]) ? p[i] : 0.0f;
     if constexpr (SM == SMode::kNone || SM == SMode::kRow) {
@@ -184,7 +183,7 @@ __global__ __launch_bounds__(256) void lean_gemv_kernel(const LeanParams P) {
     } else if constexpr (SM == SMode::kBlockE8) {
 #pragma unroll
       for (int i = 0; i < ROWS; i++) {
-        const float t = p[i] * pow2i((int)cur.e[i] - 127);
+        const float t = p[i] * pow2i((int)c.e[i] - 127);
         acc[i] = acc[i] + ((cv && rv[i]) ? t : 0.0f);
       }
     } else {
@@ -198,10 +197,10 @@ __global__ __launch_bounds__(256) void lean_gemv_kernel(const LeanParams P) {
       reduce_range<ROWS, 1, LG>(p);
 #pragma unroll
       for (int k = 0; k < NVG; k++) {
-        const float sk = to_f32(cur.s[k]);
+        const float sk = to_f32(c.s[k]);
         float t;
         if constexpr (SM == SMode::kGroupAff) {
-          float m = to_f32(cur.m[k]);
+          float m = to_f32(c.m[k]);
           if (P.aff_zero) m = -(m * sk);
           t = __builtin_fmaf(xsum, m, p[k] * sk);
         } else {
@@ -210,8 +209,27 @@ __global__ __launch_bounds__(256) void lean_gemv_kernel(const LeanParams P) {
         acc[k] = acc[k] + ((cv && sv[k]) ? t : 0.0f);
       }
     }
-    if (more) cur = nxt;
-  } while (++r < rounds);
+  };
+  if constexpr (PFR == 1) {
+    int r = 0;
+    do {   // the host guarantees one round (cols >= 32)
+      Round nxt;
+      const bool more = r + 1 < rounds;
+      if (more) fetch(r + 1, nxt);
+      consume(ring[0], r);
+      if (more) ring[0] = nxt;
+    } while (++r < rounds);
+  } else {
+    for (int r0 = 0;;) {
+#pragma unroll
+      for (int k = 0; k < PFR; k++)
+        if (r0 + k < rounds) consume(ring[k], r0 + k);
+      r0 += PFR;
+      if (r0 >= rounds) break;
+#pragma unroll
+      for (int k = 0; k < PFR; k++) fetch(r0 + k, ring[k]);
+    }
+  }
 
   if constexpr (kGroup) reduce_range<NVG, LG, LPR>(acc);
   else reduce_range<ROWS, 1, LPR>(acc);
@@ -254,9 +272,15 @@ int lean_launch_lpr(const LeanParams& P, int slots, hipStream_t st, const char* 
   const int64_t waves = ((int64_t)P.rows + per_wave - 1) / per_wave;
   const dim3 grid((unsigned)((waves + 3) / 4), (unsigned)slots);
   const size_t lds = xm == 1 ? 0 : (size_t)P.cols * 2;
+  // dense rows of two rounds, up to two rows per wave: both rounds requested at once
+  constexpr bool kDense2 = SM == SMode::kNone;
+  const bool two = kDense2 && rpw <= 2 && (P.cols / 32 + LPR - 1) / LPR == 2;
 #define TT_LEAN(R, M)                                                                                     \
   if (P.experts != nullptr)                                                                               \
     hipLaunchKernelGGL((lean_gemv_kernel<F, SM, XT, OT, ST, LPR, R, L, M, true>), grid, dim3(256), lds, st, P); \
+  else if (two)                                                                                           \
+    hipLaunchKernelGGL((lean_gemv_kernel<F, SM, XT, OT, ST, LPR, R, L, M, false, kDense2 ? 2 : 1>), grid,  \
+                       dim3(256), lds, st, P);                                                            \
   else                                                                                                    \
     hipLaunchKernelGGL((lean_gemv_kernel<F, SM, XT, OT, ST, LPR, R, L, M, false>), grid, dim3(256), lds, st, P)
 #define TT_LEAN_X(R) \
