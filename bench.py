@@ -46,6 +46,7 @@ def _parse() -> argparse.Namespace:
     p.add_argument("--unfused", action="store_true", help="decode with one launch per reference operator")
     p.add_argument("--roofline-only", action="store_true",
                    help="only the int4 roofline phase (used for hardware-counter runs)")
+    p.add_argument("--ternary-only", action="store_true", help="only the ternary expert GEMV phase")
     p.add_argument("--batched-only", action="store_true",
                    help="only the batched small-M GEMM phase (used for MFMA counter runs)")
     return p.parse_args()
@@ -153,6 +154,34 @@ def affine_lowbit_phase(be, bits: int, rows: int, cols: int, copies: int, seed: 
     del W, sz
     return {"bits": bits, "shape": [rows, cols], "group": group, "us_per_call": t * 1e6, "bytes_per_call": nbytes,
             "GB_s": nbytes / t / 1e9, "frac_of_hbm_peak": nbytes / t / 1e9 / HBM_PEAK_GBS, "rotated_copies": copies}
+
+
+def ternary_phase(be, seed: int) -> dict:
+    """Ternary selected-expert GEMV at the gpt-oss-20B expert shapes: 32 experts,
+    four selected per call, gate/up 5760 x 2880 and down 2880 x 2880 (rows of
+    ceil(K/5) digit bytes + 3-bit selectors, E8M0 scales); 8 rotated copies."""
+    import torch
+
+    dev = be.device
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    res = {}
+    experts, sel, cols, copies = 32, 4, 2880, 8
+    groups = cols // 32
+    row_bytes = (cols + 4) // 5 + (groups * 3 + 7) // 8
+    ids = torch.randperm(experts, generator=g, device=dev)[:sel].to(torch.int32)
+    x = torch.randn(cols, generator=g, device=dev).to(torch.float16)
+    for name, rows in (("gate_up_5760x2880", 5760), ("down_2880x2880", 2880)):
+        W = torch.randint(0, 256, (copies, experts, rows, row_bytes), generator=g, device=dev, dtype=torch.uint8)
+        S = torch.randint(118, 128, (copies, experts, rows, groups), generator=g, device=dev, dtype=torch.uint8)
+        out = torch.empty((sel, rows), device=dev, dtype=torch.float16)
+        t = _time_rotated(lambda i: be.mxfp_ternary_selected_tensorcore_matvec(W[i], S[i], x, ids, out), copies)
+        nbytes = sel * rows * (row_bytes + groups) + cols * 2 + sel * rows * 2
+        res[name] = {"us": t * 1e6, "bytes_per_call": nbytes, "GB_s": nbytes / t / 1e9,
+                     "frac_of_hbm_peak": nbytes / t / 1e9 / HBM_PEAK_GBS}
+        del W, S
+    torch.cuda.empty_cache()
+    return res
 
 
 def batched_phase(be, seed: int) -> dict:
@@ -356,6 +385,11 @@ def main() -> int:
 
     _lib.load()  # fails loudly when the HIP library is missing
 
+    if args.ternary_only:
+        from thintensor_amd.backend import HipDecodeBackend
+        be = HipDecodeBackend(torch.device("cuda:0"), torch.float16, 2880, 4096, 512, 2880)
+        print(json.dumps({"ternary_experts_gptoss": ternary_phase(be, args.seed + 7)}), flush=True)
+        return 0
     if args.batched_only:
         from thintensor_amd.backend import HipDecodeBackend
         be = HipDecodeBackend(torch.device("cuda:0"), torch.float16, 5120, 5120, 1024, 17920)
@@ -393,6 +427,7 @@ def main() -> int:
         extra["lm_head_argmax_128256x2048"] = lm_head_phase(be, 128256, 2048, 2, args.seed + 3)
         extra["q2_affine_g64_17920x5120"] = affine_lowbit_phase(be, 2, 17920, 5120, 24, args.seed + 4)
         extra["q1_affine_g64_5120x5120"] = affine_lowbit_phase(be, 1, 5120, 5120, 64, args.seed + 5)
+        extra["ternary_experts_gptoss"] = ternary_phase(be, args.seed + 7)
         torch.cuda.empty_cache()
         _log("batched small-M GEMM (hidden 5120)")
         extra["batched_5120"] = batched_phase(be, args.seed + 6)

@@ -407,6 +407,57 @@ class HipDecodeBackend:
         """Same sum as the scalar variant (triton_kernels.py:3978-4055)."""
         return self.mxfp_lowbit_selected_matvec(packed_weight, scales, x, expert_indices, out, bits=bits)
 
+    def mxfp_ternary_selected_tensorcore_matvec(
+        self,
+        packed_weight: torch.Tensor,
+        scales: torch.Tensor,
+        x: torch.Tensor,
+        expert_indices: torch.Tensor,
+        out: torch.Tensor,
+        *,
+        block_m: int = 0,
+        block_n: int = 0,
+    ) -> torch.Tensor:
+        """Ternary selected-expert GEMV (triton_kernels.py:4057-4130, kernel :1022-1133).
+
+        ``packed_weight`` uint8 [E, rows, ceil(cols/5) + ceil(3*cols/32/8)] (base-3 digits,
+        then 3-bit magnitude selectors), ``scales`` E8M0 uint8 [E, rows, cols/32]; the
+        tile arguments of the reference are accepted and ignored."""
+        if packed_weight.ndim != 3 or scales.ndim != 3:
+            raise ValueError("ternary expert weights/scales must be rank 3/rank 3")
+        experts, rows, groups = map(int, scales.shape)
+        cols = groups * 32
+        ternary_bytes = (cols + 4) // 5
+        magnitude_bytes = (groups * 3 + 7) // 8
+        if tuple(packed_weight.shape) != (experts, rows, ternary_bytes + magnitude_bytes):
+            raise ValueError(
+                "ternary weight shape mismatch: "
+                f"got {tuple(packed_weight.shape)}, expected {(experts, rows, ternary_bytes + magnitude_bytes)}"
+            )
+        selected = int(expert_indices.numel())
+        if x.ndim == 1 and int(x.numel()) == cols:
+            stride_xe = 0
+        elif x.ndim == 2 and tuple(x.shape) == (selected, cols) and x.stride(1) == 1:
+            stride_xe = int(x.stride(0))
+        else:
+            raise ValueError(f"ternary input must be {(cols,)} or {(selected, cols)}, got {tuple(x.shape)}")
+        if tuple(out.shape) != (selected, rows):
+            raise ValueError(f"ternary output must be {(selected, rows)}, got {tuple(out.shape)}")
+        if packed_weight.dtype != torch.uint8 or scales.dtype != torch.uint8:
+            raise ValueError("ternary weights and scales must be uint8")
+        if not packed_weight.is_contiguous() or not scales.is_contiguous() or out.stride(1) != 1:
+            raise ValueError("ternary weights, scales and output rows must be contiguous")
+        self._check_indices(expert_indices)
+        _require_cuda(packed_weight, scales, x, out)
+        rc = self.lib.tt_mxfp_ternary_selected_matvec(
+            packed_weight.data_ptr(), packed_weight.stride(0), packed_weight.stride(1), packed_weight.numel(),
+            scales.data_ptr(), scales.stride(0), scales.stride(1), scales.numel(), experts, x.data_ptr(),
+            _code(x, "mxfp_ternary_selected_matvec"), stride_xe, expert_indices.data_ptr(), selected,
+            out.data_ptr(), _code(out, "mxfp_ternary_selected_matvec"), out.stride(0), rows, cols, _stream(out),
+        )
+        _lib.check(rc, "mxfp_ternary_selected_matvec")
+        return out
+
     def mxfp_lowbit_selected_swiglu(
         self,
         packed_weight: torch.Tensor,
