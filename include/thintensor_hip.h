@@ -121,9 +121,9 @@ int tt_mxfp_lowbit_selected_matvec(const void* packed, int64_t w_expert_bytes, i
  * ceil(3*cols/32/8) bytes hold a 3-bit selector m per group at bit 3g, |w| =
  * e2m1(m + 1); scales are E8M0 [E, rows, cols/32] (w = (digit-1)*|w|*2^(e-127)).
  * `experts` = E; w_total_bytes / s_total_bytes bound every read.  Selected ids
- * outside [0, E) produce NaN rows.  Summation order: per group in column order,
- * groups of a 160-column chunk in order, chunks j, j+L, ... per lane, butterfly
- * over L = tt_ternary_lanes_per_row(cols) lanes.
+ * outside [0, E) produce NaN rows.  Summation order (binary32): per group, the
+ * column-order fma chain of digit*x minus the column-order sum of x; per 160-column
+ * chunk, the groups' scaled sums in order; per row, the chunks in order.
  * Replaces TritonDecodeBackend.mxfp_ternary_selected_tensorcore_matvec
  * (triton_kernels.py:4057-4130; kernel :1022-1133; packer gpu_runtime.py:494-583). */
 int tt_mxfp_ternary_selected_matvec(const void* packed, int64_t w_expert_bytes, int64_t w_row_bytes,
@@ -133,10 +133,6 @@ int tt_mxfp_ternary_selected_matvec(const void* packed, int64_t w_expert_bytes, 
                                     const int32_t* expert_indices, int64_t selected,
                                     void* out, int out_dtype, int64_t out_slot,
                                     int64_t rows, int64_t cols, void* stream);
-
-/* Lanes sharing one output row in tt_mxfp_ternary_selected_matvec (part of its
- * documented summation order). */
-int tt_ternary_lanes_per_row(int64_t cols);
 
 /* Fused gate/up GEMV on interleaved rows (2i gate, 2i+1 up) + gpt-oss SwiGLU;
  * bits 1/2 = E8M0 low-bit experts (bf16 rounding), bits 4 = MXFP4 blocks (rounding

@@ -14,8 +14,8 @@ kernel (tests) and never by the product:
   LUT digits, selector bits (crossing bytes), nibble = 0 for digit 1, else
   (m + 1) | 8 * (digit == 0), value e2m1(nibble) * 2^(e - 127);
 * ``ternary_selected_gemv`` -- the HIP kernel's documented summation order in binary32
-  (per-group column-order sums, groups in order per 160-column chunk, chunks j, j+L,
-  ... per lane, butterfly over L lanes), so GPU results can be compared bit for bit.
+  (per-group digit*x chain minus the group's x sum, groups in order per 160-column
+  chunk, chunks in order), so GPU results can be compared bit for bit.
 """
 
 from __future__ import annotations
@@ -110,14 +110,6 @@ def ternary_dequant(packed: np.ndarray, scales: np.ndarray) -> np.ndarray:
     return E2M1[nibble] * np.exp2(s[..., g].astype(np.float64) - 127.0)
 
 
-def ternary_lanes_per_row(cols: int) -> int:
-    chunks = -(-cols // 160)
-    lanes = 1
-    while lanes < chunks and lanes < 64:
-        lanes <<= 1
-    return lanes
-
-
 def _digits(packed_rows: np.ndarray, cols: int) -> np.ndarray:
     k = np.arange(cols)
     b = packed_rows[:, k // 5].astype(np.int64)
@@ -126,14 +118,16 @@ def _digits(packed_rows: np.ndarray, cols: int) -> np.ndarray:
 
 def ternary_selected_gemv(packed: np.ndarray, scales: np.ndarray, x: np.ndarray, experts: np.ndarray) -> np.ndarray:
     """float32 [selected, rows] in the HIP kernel's order; x is [cols] or [selected, cols]
-    (values as float32); ids outside [0, E) give NaN rows."""
+    (values as float32); ids outside [0, E) give NaN rows.  Order, all binary32:
+    A_g = column-order chain of A + digit * x (exact products), B_g = column-order sum
+    of x, p_g = A_g - B_g; chunk = sum over the 160-column chunk's groups in order of
+    v_g * p_g with v_g = |w|_g * 2^(e_g - 127); row = sum of the chunks in order."""
     packed = np.asarray(packed, dtype=np.uint8)
     n_exp, rows, _ = packed.shape
     groups = scales.shape[-1]
     cols = groups * 32
     _, tbytes, _ = ternary_geometry(cols)
     chunks = -(-cols // 160)
-    lanes = ternary_lanes_per_row(cols)
     sel = len(experts)
     xs = np.asarray(x, dtype=np.float32)
     if xs.ndim == 1:
@@ -143,7 +137,7 @@ def ternary_selected_gemv(packed: np.ndarray, scales: np.ndarray, x: np.ndarray,
         if not 0 <= int(e) < n_exp:
             continue
         pr = packed[int(e)]
-        tern = (_digits(pr, cols) - 1).astype(np.float32)
+        digit = _digits(pr, cols).astype(np.float32)
         mbits = np.arange(groups) * 3
         mb = tbytes + mbits // 8
         word = pr[:, mb].astype(np.int64) | (pr[:, np.minimum(mb + 1, pr.shape[1] - 1)].astype(np.int64) << 8)
@@ -151,16 +145,18 @@ def ternary_selected_gemv(packed: np.ndarray, scales: np.ndarray, x: np.ndarray,
         mcode = (word >> (mbits % 8)) & 7
         mag = np.where(mcode == 7, 0.0, MAGNITUDES[np.minimum(mcode, 6)])
         v = mag.astype(np.float32) * np.exp2(np.asarray(scales[int(e)], dtype=np.float64) - 127.0).astype(np.float32)
-        part = np.zeros((rows, groups), dtype=np.float32)
         xrow = xs[si]
+        A = np.zeros((rows, groups), dtype=np.float32)
+        B = np.zeros(groups, dtype=np.float32)
         for k in range(cols):
-            part[:, k // 32] = part[:, k // 32] + tern[:, k] * xrow[k]
-        lane_acc = np.zeros((rows, lanes), dtype=np.float32)
+            A[:, k // 32] = A[:, k // 32] + digit[:, k] * xrow[k]
+            B[k // 32] = B[k // 32] + xrow[k]
+        p = A - B[None, :]
+        row = np.zeros(rows, dtype=np.float32)
         for c in range(chunks):
-            j = c % lanes
+            chunk = np.zeros(rows, dtype=np.float32)
             for g in range(5 * c, min(5 * c + 5, groups)):
-                lane_acc[:, j] = lane_acc[:, j] + v[:, g] * part[:, g]
-        while lane_acc.shape[1] > 1:
-            lane_acc = lane_acc[:, 0::2] + lane_acc[:, 1::2]
-        out[si] = lane_acc[:, 0]
+                chunk = chunk + v[:, g] * p[:, g]
+            row = row + chunk
+        out[si] = row
     return out

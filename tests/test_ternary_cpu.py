@@ -17,7 +17,6 @@ fixes, chosen so that a digit-order, power, sign or bit-position mistake fails i
 
 from __future__ import annotations
 
-import ctypes
 
 import numpy as np
 import pytest
@@ -146,11 +145,3 @@ def test_planted_selector_mistake_is_caught():
     sel = shifted[..., tb:].astype(np.uint32)
     shifted[..., tb:] = ((sel << 1) & 0xFF).astype(np.uint8)
     assert not np.array_equal(T.ternary_dequant(shifted, scales), ref.mxfp4_dequant(blocks, scales))
-
-
-def test_lanes_rule_matches_library_export():
-    from thintensor_amd import _lib
-
-    lib = _lib.load()
-    for cols in (32, 160, 192, 1056, 2880, 5120, 8192, 10240, 12000):
-        assert lib.tt_ternary_lanes_per_row(cols) == T.ternary_lanes_per_row(cols), cols

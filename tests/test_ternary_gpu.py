@@ -5,7 +5,7 @@ Bit-exact against the oracle's restatement of the kernel's summation order
 of the reference's dequantise-then-matmul in float64.  Cases: the gpt-oss expert
 shapes (gate/up 5760 x 2880, down 2880 x 2880), one 32-column group (rows of eight
 bytes, reads clamped at the buffer end), a partial last 160-column chunk, K = 5120
-and 8192 (64 lanes per row), per-slot activations, bf16 inputs, fp16/bf16/fp32
+and 8192 (52 chunks per row), per-slot activations, bf16 inputs, fp16/bf16/fp32
 outputs, weights packed from MXFP4 by the reference's packer, and ids outside the
 expert range (NaN rows).
 """
@@ -75,7 +75,7 @@ def _check_tolerance(got, packed, scales, x32, idx):
         (2, 3, 32, 2, False, False, "f32"),          # one group, eight-byte rows
         (3, 77, 1056, 3, True, True, "f32"),         # partial last chunk, bf16 x
         (2, 300, 5120, 2, False, True, "bf16"),      # 32 chunks
-        (2, 64, 8192, 2, True, False, "f16"),        # 52 chunks, 64 lanes per row
+        (2, 64, 8192, 2, True, False, "f16"),        # 52 chunks per row
     ],
 )
 def test_ternary_selected_matches_oracle(backend, device, experts, rows, cols, sel, per_slot, x_bf16, out_dtype):

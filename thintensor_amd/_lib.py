@@ -64,7 +64,6 @@ SIGNATURES: dict[str, list] = {
     "tt_mxfp4_selected_matvec": [_P, _L, _L, _P, _L, _L, _P, _I, _L, _P, _L, _P, _I, _L, _L, _L, _P],
     "tt_mxfp_lowbit_selected_matvec": [_P, _L, _L, _P, _L, _L, _I, _P, _I, _L, _P, _L, _P, _I, _L, _L, _L, _P],
     "tt_mxfp_ternary_selected_matvec": [_P, _L, _L, _L, _P, _L, _L, _L, _L, _P, _I, _L, _P, _L, _P, _I, _L, _L, _L, _P],
-    "tt_ternary_lanes_per_row": [_L],
     "tt_mxfp_lowbit_selected_swiglu": [_P, _L, _L, _P, _L, _L, _I, _P, _I, _L, _P, _L, _P, _I, _L, _F, _F, _P, _I,
                                        _L, _L, _L, _P],
     "tt_mxfp_lowbit_weighted_down": [_P, _L, _L, _P, _L, _L, _I, _P, _I, _L, _P, _P, _I, _L, _P, _I, _L, _P, _I, _L,

@@ -10,21 +10,23 @@
 //     {0.5, 1, 1.5, 2, 3, 4, 6} for m = 0..6 and 0 for m = 7 (e2m1 code 8 is -0);
 //   * E8M0 scales [E, rows, G] as a separate tensor: w = (digit - 1) * |w| * 2^(e - 127).
 //
-// Work split.  Five groups are exactly 32 digit bytes (lcm(5, 32) = 160 columns), so a
-// lane owns whole 160-column chunks: 32 digit bytes, a 15-bit field of magnitude
-// selectors and five scale bytes.  L lanes share a row (L = the smallest power of two
-// >= chunks, at most 64; lanes loop over chunks j, j + L, ...), 64 / L rows per wave,
-// and a workgroup walks kIter row sets per wave so the activation vector staged in
-// LDS (as fp32) is reused over 4 * kIter * 64 / L rows.  Rows are not 4-byte aligned
-// (row_bytes is arbitrary), so each lane reads aligned dwords that cover its bytes and
-// shifts them into place; dwords that would cross the end of a buffer are assembled
-// from byte loads instead.
+// Work split.  Five groups are exactly 32 digit bytes (lcm(5, 32) = 160 columns), so
+// the unit of work is an item = (row, 160-column chunk): 32 digit bytes, a 15-bit
+// field of magnitude selectors and five scale bytes.  A workgroup of 128 threads owns
+// `rpw` rows of one selected slot and hands its rpw * chunks items to its threads in
+// turn, two items' loads in flight per thread before either is used.  The slot's
+// activations are staged once per workgroup in LDS as fp32, together with the group
+// sums of x and a 256-entry table that expands a digit byte into its five digits as
+// bytes (read back with v_cvt_f32_ubyte).  Rows are not 4-byte aligned (row_bytes is
+// arbitrary), so each item reads aligned dwords that cover its bytes and shifts them
+// into place (reads are clamped to each buffer's last aligned dword).
 //
-// Fixed summation order (a CPU restatement reproduces every bit):
-//   p_g = sum over the group's 32 columns in column order of (digit - 1) * x   (fp32);
-//   acc = acc + (|w|_g * 2^(e_g - 127)) * p_g over the lane's groups in column order;
-//   row = butterfly over the L lanes (lane bits in increasing order), stored rounded
-//   to the output dtype.
+// Fixed summation order (a CPU restatement reproduces every bit), all binary32:
+//   A_g = sum over the group's 32 columns in order of digit * x   (fma chain, exact
+//         products), B_g = sum of the group's x in order, p_g = A_g - B_g
+//         (so p_g sums (digit - 1) * x);
+//   chunk = sum over the chunk's groups in order of (|w|_g * 2^(e_g - 127)) * p_g;
+//   row = sum of the row's chunks in order, stored rounded to the output dtype.
 // The reference contracts the same products on tensor cores in hardware order; this
 // order is held to the dequantise-then-matmul tolerance against it.
 #include "tt_abi_internal.h"
@@ -33,10 +35,10 @@
 namespace tt {
 namespace {
 
-constexpr int kChunk = 160;                   // columns per lane step
+constexpr int kChunk = 160;                   // columns per item
 constexpr int kMaxCols = 8192;
-constexpr int kMaxChunks = (kMaxCols + kChunk - 1) / kChunk;
-constexpr int kIter = 4;                      // row sets per wave
+constexpr int kThreads = 128;
+constexpr int kBatch = 2;                     // items whose loads are in flight together
 
 struct TernParams {
   const uint8_t* w;         // [E, rows, row_bytes]
@@ -50,115 +52,195 @@ struct TernParams {
   int64_t s_expert, s_row;  // bytes
   int64_t x_slot, out_slot; // elements
   int64_t n_experts;
-  int rows, cols, tbytes, groups, chunks, L;
+  int rows, cols, tbytes, groups, chunks, rpw;
 };
 
-// Dword at a 4-byte aligned address; bytes at or past `end` read as zero.
-__device__ __forceinline__ uint32_t ld_u32(const uint8_t* a4, const uint8_t* end) {
-  if (a4 + 4 <= end) return *reinterpret_cast<const uint32_t*>(a4);
-  uint32_t v = 0;
-#pragma unroll
-  for (int i = 0; i < 4; i++)
-    if (a4 + i < end) v |= (uint32_t)a4[i] << (8 * i);
-  return v;
+// Aligned dword at a4, or the buffer's last aligned dword if a4 lies past it.  An
+// aligned dword that holds at least one byte of the buffer lies in the same memory
+// page as that byte, so this read cannot fault; its bytes past the buffer's end only
+// feed groups past `groups`, whose sums are never used.
+__device__ __forceinline__ uint32_t ld_u32(const uint8_t* a4, const uint8_t* last4) {
+  return *reinterpret_cast<const uint32_t*>(a4 < last4 ? a4 : last4);
 }
 
-// 64 bits starting at byte address a (any alignment; at most 3 + 8 bytes are touched).
-__device__ __forceinline__ uint64_t ld_u64_at(const uint8_t* a, const uint8_t* end) {
-  const uint8_t* a4 = reinterpret_cast<const uint8_t*>(reinterpret_cast<uintptr_t>(a) & ~(uintptr_t)3);
-  const uint32_t sh = (uint32_t)(a - a4);
-  const uint32_t d0 = ld_u32(a4, end), d1 = ld_u32(a4 + 4, end), d2 = ld_u32(a4 + 8, end);
-  const uint32_t lo = __builtin_amdgcn_alignbyte(d1, d0, sh);
-  const uint32_t hi = __builtin_amdgcn_alignbyte(d2, d1, sh);
-  return (uint64_t)lo | ((uint64_t)hi << 32);
+// Round down to 4 bytes by pointer arithmetic (keeps the global address space).
+__device__ __forceinline__ const uint8_t* align4(const uint8_t* a) {
+  return a - (reinterpret_cast<uintptr_t>(a) & 3u);
 }
 
 // |w| * 2 for selector m: {1, 2, 3, 4, 6, 8, 12, 0}.
 __device__ __forceinline__ float magnitude(uint32_t m) { return (float)((0x0C864321u >> (4 * m)) & 15u) * 0.5f; }
 
-template <typename XT, typename OT>
-__global__ __launch_bounds__(256) void ternary_selected_kernel(TernParams P) {
-  __shared__ __attribute__((aligned(16))) float xs[kMaxChunks * kChunk];
-  const int slot = blockIdx.y;
-  const int64_t e = P.experts[slot];
-  const bool valid_expert = e >= 0 && e < P.n_experts;
-  // stage the slot's activations as fp32 (zero past cols, up to whole chunks)
-  const XT* xv = reinterpret_cast<const XT*>(P.x) + (int64_t)slot * P.x_slot;
-  const int padded = P.chunks * kChunk;
-  for (int i = threadIdx.x; i < padded; i += 256) xs[i] = i < P.cols ? to_f32(xv[i]) : 0.0f;
-  __syncthreads();
+struct Item {
+  uint32_t d[9];   // dwords covering the 32 digit bytes
+  uint32_t m[3];   // dwords covering the selector field
+  uint32_t s[3];   // dwords covering the five scale bytes
+  uint32_t shd, shm, shs;
+  int mbit;
+};
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int L = P.L;
-  const int per_wave = 64 / L;
-  const int r_in = lane / L, j0 = lane % L;
-  OT* out = reinterpret_cast<OT*>(P.out) + (int64_t)slot * P.out_slot;
-  const int wg_rows = 4 * kIter * per_wave;
-  for (int it = 0; it < kIter; it++) {
-    const int row = blockIdx.x * wg_rows + (it * 4 + wave) * per_wave + r_in;
-    const int lrow = row < P.rows ? row : P.rows - 1;
-    float acc = 0.0f;
-    if (valid_expert) {
-      const uint8_t* wrow = P.w + e * P.w_expert + (int64_t)lrow * P.w_row;
-      const uint8_t* srow = P.s + e * P.s_expert + (int64_t)lrow * P.s_row;
-      for (int c = j0; c < P.chunks; c += L) {
-        // 32 digit bytes at wrow + 32 c: nine aligned dwords, shifted into eight words
-        const uint8_t* a = wrow + 32 * c;
-        const uint8_t* a4 = reinterpret_cast<const uint8_t*>(reinterpret_cast<uintptr_t>(a) & ~(uintptr_t)3);
-        const uint32_t sh = (uint32_t)(a - a4);
-        uint32_t d[9];
+template <typename XT, typename OT>
+__global__ __launch_bounds__(kThreads) void ternary_selected_kernel(TernParams P) {
+  extern __shared__ __attribute__((aligned(16))) float smem[];
+  float* xs = smem;                                     // chunks * 160 (zero past cols)
+  float* bsum = xs + P.chunks * kChunk;                 // chunks * 5 group sums
+  float* part = bsum + P.chunks * 5 + ((P.chunks * 5) & 1);   // rpw * chunks item sums (8-byte aligned end)
+  uint2* dlut = reinterpret_cast<uint2*>(part + P.rpw * P.chunks + ((P.rpw * P.chunks) & 1));
+  const int slot = blockIdx.y;
+  const int row0 = blockIdx.x * P.rpw;
+  const int nrows = P.rows - row0 < P.rpw ? P.rows - row0 : P.rpw;
+  OT* out = reinterpret_cast<OT*>(P.out) + (int64_t)slot * P.out_slot + row0;
+  const int64_t e = P.experts[slot];
+  if (e < 0 || e >= P.n_experts) {                      // uniform over the workgroup
+    for (int r = threadIdx.x; r < nrows; r += kThreads) store(out + r, __builtin_nanf(""));
+    return;
+  }
+  const XT* xv = reinterpret_cast<const XT*>(P.x) + (int64_t)slot * P.x_slot;
+  // 16-byte activation loads, four per thread in flight (cols is a multiple of 32 and
+  // the slot's row is 16-byte aligned), then zeros up to whole chunks
+  const int nvec = P.cols / 8;
+  for (int v0 = threadIdx.x; v0 < nvec; v0 += 4 * kThreads) {
+    uint4 t[4];
 #pragma unroll
-        for (int i = 0; i < 9; i++) d[i] = ld_u32(a4 + 4 * i, P.w_end);
-        uint32_t wd[8];
+    for (int u = 0; u < 4; u++) {
+      const int v = v0 + u * kThreads < nvec ? v0 + u * kThreads : nvec - 1;
+      t[u] = reinterpret_cast<const uint4*>(xv)[v];
+    }
 #pragma unroll
-        for (int i = 0; i < 8; i++) wd[i] = __builtin_amdgcn_alignbyte(d[i + 1], d[i], sh);
-        // magnitude selectors of groups 5c .. 5c+4: bits 15 c .. 15 c + 14 of the sidecar
-        const int mbit = 15 * c;
-        const uint64_t mw = ld_u64_at(wrow + P.tbytes + (mbit >> 3), P.w_end);
-        const uint32_t mfield = (uint32_t)(mw >> (mbit & 7)) & 0x7fffu;
-        const uint64_t sw = ld_u64_at(srow + 5 * c, P.s_end);
-        const float* xc = xs + kChunk * c;
-        float p[5] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    for (int u = 0; u < 4; u++) {
+      const int v = v0 + u * kThreads;
+      if (v < nvec) {
+        const uint32_t wv[4] = {t[u].x, t[u].y, t[u].z, t[u].w};
 #pragma unroll
-        for (int b = 0; b < 32; b++) {
-          uint32_t q = (wd[b >> 2] >> (8 * (b & 3))) & 0xffu;
-#pragma unroll
-          for (int i = 0; i < 5; i++) {
-            const uint32_t q3 = (q * 171u) >> 9;   // q / 3 for q < 256
-            const int digit = (int)(q - 3u * q3);
-            q = q3;
-            const int t = 5 * b + i;
-            p[t / 32] = p[t / 32] + (float)(digit - 1) * xc[t];
-          }
-        }
-#pragma unroll
-        for (int g = 0; g < 5; g++) {
-          if (5 * c + g < P.groups) {
-            const uint32_t m = (mfield >> (3 * g)) & 7u;
-            const int ex = (int)((sw >> (8 * g)) & 0xffu);
-            const float v = magnitude(m) * pow2i(ex - 127);
-            acc = acc + v * p[g];
-          }
+        for (int j = 0; j < 4; j++) {
+          xs[8 * v + 2 * j] = lo_f32<XT>(wv[j]);
+          xs[8 * v + 2 * j + 1] = hi_f32<XT>(wv[j]);
         }
       }
     }
-    acc = xor_sum(acc, 1, L);
-    if (j0 == 0 && row < P.rows) store(out + row, valid_expert ? acc : __builtin_nanf(""));
+  }
+  const int padded = P.chunks * kChunk;
+  for (int i = P.cols + threadIdx.x; i < padded; i += kThreads) xs[i] = 0.0f;
+  for (int b = threadIdx.x; b < 256; b += kThreads) {
+    uint32_t q = (uint32_t)b, lo = 0, hi = 0;
+    for (int i = 0; i < 5; i++) {
+      const uint32_t q3 = q / 3u, dg = q - 3u * q3;
+      if (i < 4) lo |= dg << (8 * i);
+      else hi = dg;
+      q = q3;
+    }
+    dlut[b] = make_uint2(lo, hi);
+  }
+  __syncthreads();
+  for (int g = threadIdx.x; g < P.chunks * 5; g += kThreads) {
+    float b = 0.0f;
+    for (int k = 0; k < 32; k++) b = b + xs[32 * g + k];
+    bsum[g] = b;
+  }
+  __syncthreads();
+
+  const uint8_t* wlast = align4(P.w_end - 1);
+  const uint8_t* slast = align4(P.s_end - 1);
+  const uint8_t* wexp = P.w + e * P.w_expert;
+  const uint8_t* sexp = P.s + e * P.s_expert;
+  const int items = nrows * P.chunks;
+  for (int base = threadIdx.x; base < items; base += kThreads * kBatch) {
+    Item it[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; u++) {
+      int item = base + u * kThreads;
+      item = item < items ? item : items - 1;
+      const int r = item / P.chunks, c = item - r * P.chunks;
+      const uint8_t* wrow = wexp + (int64_t)(row0 + r) * P.w_row;
+      const uint8_t* a = wrow + 32 * c;
+      const uint8_t* a4 = align4(a);
+      it[u].shd = (uint32_t)(a - a4);
+#pragma unroll
+      for (int i = 0; i < 9; i++) it[u].d[i] = ld_u32(a4 + 4 * i, wlast);
+      const int mbit = 15 * c;
+      const uint8_t* ma = wrow + P.tbytes + (mbit >> 3);
+      const uint8_t* ma4 = align4(ma);
+      it[u].shm = (uint32_t)(ma - ma4);
+      it[u].mbit = mbit & 7;
+#pragma unroll
+      for (int i = 0; i < 3; i++) it[u].m[i] = ld_u32(ma4 + 4 * i, wlast);
+      const uint8_t* sa = sexp + (int64_t)(row0 + r) * P.s_row + 5 * c;
+      const uint8_t* sa4 = align4(sa);
+      it[u].shs = (uint32_t)(sa - sa4);
+#pragma unroll
+      for (int i = 0; i < 3; i++) it[u].s[i] = ld_u32(sa4 + 4 * i, slast);
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; u++) {
+      const int item = base + u * kThreads;
+      if (item >= items) break;
+      const int r = item / P.chunks, c = item - r * P.chunks;
+      const float* xc = xs + kChunk * c;
+      float A[5] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int wi = 0; wi < 8; wi++) {
+        const uint32_t word = __builtin_amdgcn_alignbyte(it[u].d[wi + 1], it[u].d[wi], it[u].shd);
+#pragma unroll
+        for (int bi = 0; bi < 4; bi++) {
+          const int b = 4 * wi + bi;
+          const uint2 ent = dlut[(word >> (8 * bi)) & 0xffu];
+#pragma unroll
+          for (int i = 0; i < 5; i++) {
+            const int t = 5 * b + i;
+            const uint32_t src = i < 4 ? ent.x : ent.y;
+            const float dg = (float)((src >> (8 * (i & 3))) & 0xffu);
+            A[t / 32] = __builtin_fmaf(dg, xc[t], A[t / 32]);
+          }
+        }
+        // finish each word's fma chains before the next word's table and activation
+        // reads (bounds the registers that hold LDS results; without it the compiler
+        // issues every read of the item first and keeps all 160 activations live)
+        asm volatile("" : "+v"(A[0]), "+v"(A[1]), "+v"(A[2]), "+v"(A[3]), "+v"(A[4])::"memory");
+      }
+      const uint32_t mlo = __builtin_amdgcn_alignbyte(it[u].m[1], it[u].m[0], it[u].shm);
+      const uint32_t mhi = __builtin_amdgcn_alignbyte(it[u].m[2], it[u].m[1], it[u].shm);
+      const uint32_t mfield = (uint32_t)((((uint64_t)mhi << 32) | mlo) >> it[u].mbit) & 0x7fffu;
+      const uint32_t slo = __builtin_amdgcn_alignbyte(it[u].s[1], it[u].s[0], it[u].shs);
+      const uint32_t shi = __builtin_amdgcn_alignbyte(it[u].s[2], it[u].s[1], it[u].shs);
+      float chunk = 0.0f;
+#pragma unroll
+      for (int g = 0; g < 5; g++) {
+        if (5 * c + g < P.groups) {
+          const uint32_t m = (mfield >> (3 * g)) & 7u;
+          const int ex = (int)(((g < 4 ? slo : shi) >> (8 * (g & 3))) & 0xffu);
+          const float v = magnitude(m) * pow2i(ex - 127);
+          const float p = A[g] - bsum[5 * c + g];
+          chunk = chunk + v * p;
+        }
+      }
+      part[r * P.chunks + c] = chunk;
+    }
+  }
+  __syncthreads();
+  for (int r = threadIdx.x; r < nrows; r += kThreads) {
+    float acc = 0.0f;
+    for (int c = 0; c < P.chunks; c++) acc = acc + part[r * P.chunks + c];
+    store(out + r, acc);
   }
 }
 
-int lanes_for(int chunks) {
-  int L = 1;
-  while (L < chunks && L < 64) L <<= 1;
-  return L;
+int rows_per_wg(int64_t rows, int64_t selected) {
+  int rpw = 32;
+  while (rpw > 8 && ((rows + rpw - 1) / rpw) * selected < 1024) rpw >>= 1;
+  return rpw;
+}
+
+size_t lds_bytes(int chunks, int rpw) {
+  const int a = chunks * 5, b = rpw * chunks;
+  return sizeof(float) * ((size_t)chunks * kChunk + a + (a & 1) + b + (b & 1)) + 256 * sizeof(uint2);
 }
 
 template <typename XT>
-int launch_out(int out_dtype, const TernParams& P, dim3 grid, hipStream_t st) {
+int launch_out(int out_dtype, const TernParams& P, dim3 grid, size_t lds, hipStream_t st) {
   switch (out_dtype) {
-    case TT_F16: hipLaunchKernelGGL((ternary_selected_kernel<XT, f16_t>), grid, dim3(256), 0, st, P); break;
-    case TT_BF16: hipLaunchKernelGGL((ternary_selected_kernel<XT, bf16_t>), grid, dim3(256), 0, st, P); break;
-    default: hipLaunchKernelGGL((ternary_selected_kernel<XT, float>), grid, dim3(256), 0, st, P); break;
+    case TT_F16: hipLaunchKernelGGL((ternary_selected_kernel<XT, f16_t>), grid, dim3(kThreads), lds, st, P); break;
+    case TT_BF16: hipLaunchKernelGGL((ternary_selected_kernel<XT, bf16_t>), grid, dim3(kThreads), lds, st, P); break;
+    default: hipLaunchKernelGGL((ternary_selected_kernel<XT, float>), grid, dim3(kThreads), lds, st, P); break;
   }
   return check_launch("mxfp_ternary_selected_matvec");
 }
@@ -167,11 +249,6 @@ int launch_out(int out_dtype, const TernParams& P, dim3 grid, hipStream_t st) {
 }  // namespace tt
 
 using namespace tt;
-
-extern "C" int tt_ternary_lanes_per_row(int64_t cols) {
-  if (cols <= 0) return 1;
-  return lanes_for((int)((cols + kChunk - 1) / kChunk));
-}
 
 extern "C" int tt_mxfp_ternary_selected_matvec(const void* packed, int64_t w_expert_bytes, int64_t w_row_bytes,
                                                int64_t w_total_bytes, const void* scales, int64_t s_expert,
@@ -193,9 +270,11 @@ extern "C" int tt_mxfp_ternary_selected_matvec(const void* packed, int64_t w_exp
              (long long)mbytes);
   TT_REQUIRE(s_row >= groups && s_expert >= rows * s_row && s_total_bytes >= (experts - 1) * s_expert + rows * s_row,
              "%s: scale rows must hold %lld groups", what, (long long)groups);
+  TT_REQUIRE(w_total_bytes >= 4 && s_total_bytes >= 4, "%s: weight and scale buffers must hold 4 bytes or more", what);
   TT_REQUIRE(packed && scales && aligned(packed, 4) && aligned(scales, 4),
              "%s: packed weights and scales must be 4-byte aligned", what);
-  TT_REQUIRE(x && out && x_slot >= 0 && (selected == 1 || out_slot >= rows), "%s: null pointer or bad strides", what);
+  TT_REQUIRE(x && out && aligned(x, 16) && x_slot >= 0 && x_slot % 8 == 0 && (selected == 1 || out_slot >= rows),
+             "%s: null or misaligned pointer / bad strides", what);
   TernParams P{};
   P.w = static_cast<const uint8_t*>(packed);
   P.w_end = P.w + w_total_bytes;
@@ -216,9 +295,10 @@ extern "C" int tt_mxfp_ternary_selected_matvec(const void* packed, int64_t w_exp
   P.tbytes = (int)tbytes;
   P.groups = (int)groups;
   P.chunks = (int)((cols + kChunk - 1) / kChunk);
-  P.L = lanes_for(P.chunks);
-  const int wg_rows = 4 * kIter * (64 / P.L);
-  const dim3 grid((unsigned)((rows + wg_rows - 1) / wg_rows), (unsigned)selected);
+  P.rpw = rows_per_wg(rows, selected);
+  const size_t lds = lds_bytes(P.chunks, P.rpw);
+  const dim3 grid((unsigned)((rows + P.rpw - 1) / P.rpw), (unsigned)selected);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  return x_dtype == TT_F16 ? launch_out<f16_t>(out_dtype, P, grid, st) : launch_out<bf16_t>(out_dtype, P, grid, st);
+  return x_dtype == TT_F16 ? launch_out<f16_t>(out_dtype, P, grid, lds, st)
+                           : launch_out<bf16_t>(out_dtype, P, grid, lds, st);
 }
