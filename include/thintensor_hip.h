@@ -134,6 +134,28 @@ int tt_mxfp_ternary_selected_matvec(const void* packed, int64_t w_expert_bytes, 
                                     void* out, int out_dtype, int64_t out_slot,
                                     int64_t rows, int64_t cols, void* stream);
 
+/* Sparse residual sidecar: out[m] = out[m] + sum_k values[m,k] * x[indices[m,k]]
+ * (values fp16/bf16/fp32 with element strides vm, vk; indices int32 or int64,
+ * index_bytes 4 or 8, strides im, ik).  One wave per row: lane l sums terms l, l+64,
+ * ... in order, then a butterfly over 64 lanes; an index outside [0, cols) makes the
+ * row's correction NaN.
+ * Replaces TritonDecodeBackend.sparse_residual_matvec (triton_kernels.py:5429-5456;
+ * kernel :2335-2374). */
+int tt_sparse_residual_matvec(const void* values, int value_dtype, int64_t vm, int64_t vk,
+                              const void* indices, int index_bytes, int64_t im, int64_t ik,
+                              const void* x, int x_dtype, void* out, int out_dtype,
+                              int64_t rows, int64_t terms, int64_t cols, void* stream);
+
+/* Binary residual sidecar: out[m] = out[m] + sum_k (bit ? +1 : -1) * scale[m, k/32] * x[k],
+ * sign bit k at byte k/8 (row stride bm bytes), bit k%8.  One wave per row: lane l
+ * owns 32-column groups l, l+64, ...; per group the column-order sum of +-x times
+ * the scale, then a butterfly over 64 lanes.
+ * Replaces TritonDecodeBackend.binary_residual_matvec (triton_kernels.py:5458-5487;
+ * kernel :2377-2419). */
+int tt_binary_residual_matvec(const void* packed_signs, int64_t bm, const void* scales, int scale_dtype,
+                              int64_t sm, const void* x, int x_dtype, void* out, int out_dtype,
+                              int64_t rows, int64_t cols, void* stream);
+
 /* Fused gate/up GEMV on interleaved rows (2i gate, 2i+1 up) + gpt-oss SwiGLU;
  * bits 1/2 = E8M0 low-bit experts (bf16 rounding), bits 4 = MXFP4 blocks (rounding
  * in the activation dtype, the reference's unfused MXFP4 chain):

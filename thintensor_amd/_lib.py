@@ -63,6 +63,8 @@ SIGNATURES: dict[str, list] = {
     "tt_multi_matvec": [_I, _PP, _I, _LP, _LP, _P, _I, _P, _I, _L, _P],
     "tt_mxfp4_selected_matvec": [_P, _L, _L, _P, _L, _L, _P, _I, _L, _P, _L, _P, _I, _L, _L, _L, _P],
     "tt_mxfp_lowbit_selected_matvec": [_P, _L, _L, _P, _L, _L, _I, _P, _I, _L, _P, _L, _P, _I, _L, _L, _L, _P],
+    "tt_sparse_residual_matvec": [_P, _I, _L, _L, _P, _I, _L, _L, _P, _I, _P, _I, _L, _L, _L, _P],
+    "tt_binary_residual_matvec": [_P, _L, _P, _I, _L, _P, _I, _P, _I, _L, _L, _P],
     "tt_mxfp_ternary_selected_matvec": [_P, _L, _L, _L, _P, _L, _L, _L, _L, _P, _I, _L, _P, _L, _P, _I, _L, _L, _L, _P],
     "tt_mxfp_lowbit_selected_swiglu": [_P, _L, _L, _P, _L, _L, _I, _P, _I, _L, _P, _L, _P, _I, _L, _F, _F, _P, _I,
                                        _L, _L, _L, _P],

@@ -407,6 +407,57 @@ class HipDecodeBackend:
         """Same sum as the scalar variant (triton_kernels.py:3978-4055)."""
         return self.mxfp_lowbit_selected_matvec(packed_weight, scales, x, expert_indices, out, bits=bits)
 
+    def sparse_residual_matvec(
+        self,
+        residual_values: torch.Tensor,
+        residual_indices: torch.Tensor,
+        x: torch.Tensor,
+        out: torch.Tensor,
+    ) -> torch.Tensor:
+        """out += sum_k values[:, k] * x[indices[:, k]] (triton_kernels.py:5429-5456)."""
+        if residual_values.shape != residual_indices.shape:
+            raise ValueError("sparse residual values/indices shape mismatch")
+        rows = int(residual_values.shape[0])
+        terms = int(residual_values.shape[1])
+        if residual_indices.dtype not in (torch.int32, torch.int64):
+            raise ValueError("sparse residual indices must be int32 or int64")
+        if out.numel() != rows or not out.is_contiguous() or not x.is_contiguous():
+            raise ValueError("sparse residual output/input layout mismatch")
+        _require_cuda(residual_values, residual_indices, x, out)
+        rc = self.lib.tt_sparse_residual_matvec(
+            residual_values.data_ptr(), _code(residual_values, "sparse residual values"), residual_values.stride(0),
+            residual_values.stride(1), residual_indices.data_ptr(), residual_indices.element_size(),
+            residual_indices.stride(0), residual_indices.stride(1), x.data_ptr(), _code(x, "sparse_residual_matvec"),
+            out.data_ptr(), _code(out, "sparse_residual_matvec"), rows, terms, int(x.numel()), _stream(out),
+        )
+        _lib.check(rc, "sparse_residual_matvec")
+        return out
+
+    def binary_residual_matvec(
+        self,
+        packed_signs: torch.Tensor,
+        scales: torch.Tensor,
+        x: torch.Tensor,
+        out: torch.Tensor,
+    ) -> torch.Tensor:
+        """out += sum_k sign_k * scale[:, k/32] * x[k] (triton_kernels.py:5458-5487)."""
+        rows = int(packed_signs.shape[0])
+        cols = int(x.numel())
+        if tuple(packed_signs.shape) != (rows, cols // 8):
+            raise ValueError("binary residual sign plane shape mismatch")
+        if tuple(scales.shape) != (rows, cols // 32):
+            raise ValueError("binary residual scale shape mismatch")
+        if packed_signs.stride(1) != 1 or scales.stride(1) != 1 or out.numel() != rows or not out.is_contiguous():
+            raise ValueError("binary residual sign plane, scales and output rows must be contiguous")
+        _require_cuda(packed_signs, scales, x, out)
+        rc = self.lib.tt_binary_residual_matvec(
+            packed_signs.data_ptr(), packed_signs.stride(0), scales.data_ptr(), _code(scales, "binary residual scales"),
+            scales.stride(0), x.data_ptr(), _code(x, "binary_residual_matvec"), out.data_ptr(),
+            _code(out, "binary_residual_matvec"), rows, cols, _stream(out),
+        )
+        _lib.check(rc, "binary_residual_matvec")
+        return out
+
     def mxfp_ternary_selected_tensorcore_matvec(
         self,
         packed_weight: torch.Tensor,
