@@ -135,10 +135,11 @@ int tt_mxfp_ternary_selected_matvec(const void* packed, int64_t w_expert_bytes, 
                                     int64_t rows, int64_t cols, void* stream);
 
 /* Sparse residual sidecar: out[m] = out[m] + sum_k values[m,k] * x[indices[m,k]]
- * (values fp16/bf16/fp32 with element strides vm, vk; indices int32 or int64,
- * index_bytes 4 or 8, strides im, ik).  One wave per row: lane l sums terms l, l+64,
- * ... in order, then a butterfly over 64 lanes; an index outside [0, cols) makes the
- * row's correction NaN.
+ * (values fp16/bf16/fp32 with element strides vm, vk; indices int16, int32 or int64,
+ * index_bytes 2, 4 or 8, strides im, ik; int16 is the reference runtime's sidecar
+ * layout, gpu_runtime.py:6468, and is sign-extended).  One wave per row: lane l sums
+ * terms l, l+64, ... in order, then a butterfly over 64 lanes; an index outside
+ * [0, cols) makes the row's correction NaN.
  * Replaces TritonDecodeBackend.sparse_residual_matvec (triton_kernels.py:5429-5456;
  * kernel :2335-2374). */
 int tt_sparse_residual_matvec(const void* values, int value_dtype, int64_t vm, int64_t vk,

@@ -124,3 +124,126 @@ def f32_to_f16_bits(v: float) -> int:
 
 def exp_f32(v: float) -> float:
     return float(lib().tto_exp_f32(v))
+
+
+# ---------------------------------------------------------------- operator wrappers
+# Convenience wrappers over the binary32 restatement (fp16 activations unless noted);
+# each returns fresh numpy arrays.
+
+def _c(a):
+    return np.ascontiguousarray(a)
+
+
+def rms_norm(x, w, eps: float, offset: float = 0.0) -> np.ndarray:
+    x, w = _c(x), _c(w)
+    out = np.empty(x.shape[0], dtype=np.float16)
+    lib().tto_rms_norm(_ptr(x), dtype_code(x), _ptr(w), dtype_code(w), _ptr(out), F16, x.shape[0], eps, offset)
+    return out
+
+
+def add_rms_norm(left, right, w, eps: float):
+    left, right, w = _c(left), _c(right), _c(w)
+    n = left.shape[0]
+    res = np.empty(n, dtype=left.dtype)
+    out = np.empty(n, dtype=np.float16)
+    lib().tto_add_rms_norm(_ptr(left), _ptr(right), _ptr(res), dtype_code(left), _ptr(w), dtype_code(w), _ptr(out),
+                           F16, n, eps)
+    return res, out
+
+
+def silu_mul(gate, up) -> np.ndarray:
+    gate, up = _c(gate), _c(up)
+    out = np.empty_like(gate)
+    lib().tto_silu_mul(_ptr(gate), _ptr(up), _ptr(out), dtype_code(gate), gate.shape[0])
+    return out
+
+
+def interleaved_swiglu(gate_up, alpha: float, limit: float) -> np.ndarray:
+    gu = _c(gate_up)
+    rows, n2 = gu.reshape(-1, gu.shape[-1]).shape
+    out = np.empty((rows, n2 // 2), dtype=gu.dtype)
+    lib().tto_interleaved_swiglu(_ptr(gu), _ptr(out), dtype_code(gu), rows, n2 // 2, alpha, limit)
+    return out
+
+
+def weighted_expert_sum(experts, scores) -> np.ndarray:
+    ex, sc = _c(experts), _c(scores)
+    out = np.empty(ex.shape[1], dtype=ex.dtype)
+    lib().tto_weighted_expert_sum(_ptr(ex), dtype_code(ex), _ptr(sc), dtype_code(sc), _ptr(out), ex.shape[1],
+                                  ex.shape[0])
+    return out
+
+
+def rope(q, k, cos_row, sin_row, heads: int, kv_heads: int, head_dim: int):
+    q, k = _c(q).copy(), _c(k).copy()
+    c, s = _c(cos_row), _c(sin_row)
+    lib().tto_rope(_ptr(q), _ptr(k), dtype_code(q), _ptr(c), _ptr(s), heads, kv_heads, head_dim)
+    return q, k
+
+
+def attention(q, keys, values, tokens: int, heads: int, kv_heads: int, head_dim: int, sinks=None) -> np.ndarray:
+    """keys/values [kv_heads, capacity, head_dim] (contiguous); q [heads * head_dim]."""
+    q, keys, values = _c(q), _c(keys), _c(values)
+    cap = keys.shape[1]
+    sk = None if sinks is None else _c(sinks)
+    out = np.empty(heads * head_dim, dtype=q.dtype)
+    lib().tto_attention(_ptr(q), _ptr(keys), _ptr(values), dtype_code(q), cap * head_dim, head_dim, cap * head_dim,
+                        head_dim, _ptr(sk), F16 if sk is None else dtype_code(sk), tokens, heads, kv_heads, head_dim,
+                        _ptr(out))
+    return out
+
+
+def router(weight, hidden, bias, k: int, renormalize: bool):
+    w, x = _c(weight), _c(hidden)
+    b = None if bias is None else _c(bias)
+    idx = np.empty(k, dtype=np.int32)
+    sc = np.empty(k, dtype=np.float16)
+    lib().tto_router(_ptr(w), dtype_code(w), w.shape[1], _ptr(x), dtype_code(x), x.shape[0], _ptr(b),
+                     F16 if b is None else dtype_code(b), w.shape[0], k, int(renormalize), _ptr(idx), _ptr(sc), F16)
+    return idx, sc
+
+
+def topk(logits, k: int, renormalize: bool):
+    lg = _c(logits)
+    idx = np.empty(k, dtype=np.int32)
+    sc = np.empty(k, dtype=np.float16)
+    lib().tto_topk(_ptr(lg), dtype_code(lg), lg.shape[0], k, int(renormalize), _ptr(idx), _ptr(sc), F16)
+    return idx, sc
+
+
+def expert_swiglu(fmt: str, packed, scales, x, experts, bias, alpha: float, limit: float, *, lpr: int,
+                  x_per_slot: bool = False) -> np.ndarray:
+    """Fused selected-expert gate/up GEMV + SwiGLU.  packed [E, 2I, K*b/8 ...], scales
+    E8M0 [E, 2I, K/32]; q2/q1 round through bf16, MXFP4 through the activation dtype."""
+    pw, sw, x, ex = _c(packed), _c(scales), _c(x), _c(np.asarray(experts, dtype=np.int32))
+    rows2 = pw.shape[1]
+    cols = sw.shape[2] * 32
+    inter = rows2 // 2
+    top_k = ex.shape[0]
+    rt = F16 if fmt == "mxfp4" else BF16
+    b = None if bias is None else _c(bias)
+    out = np.empty((top_k, inter), dtype=np.float16)
+    rc = lib().tto_swiglu(FMT[fmt], rt, _ptr(pw), pw.strides[0], pw.strides[1], _ptr(sw), sw.strides[0],
+                          sw.strides[1], _ptr(x), dtype_code(x), cols if x_per_slot else 0, _ptr(ex), top_k, _ptr(b),
+                          F16 if b is None else dtype_code(b), rows2, alpha, limit, _ptr(out), F16, inter, inter, cols,
+                          lpr)
+    if rc != 0:
+        raise ValueError("oracle swiglu rejected the configuration")
+    return out
+
+
+def weighted_down(fmt: str, packed, scales, x, experts, scores, bias, *, lpr: int) -> np.ndarray:
+    """Fused selected-expert down GEMV + router-weighted sum in slot order."""
+    pw, sw, x, ex, sc = _c(packed), _c(scales), _c(x), _c(np.asarray(experts, dtype=np.int32)), _c(scores)
+    rows = pw.shape[1]
+    cols = sw.shape[2] * 32
+    rt = F16 if fmt == "mxfp4" else BF16
+    b = None if bias is None else _c(bias)
+    out = np.empty(rows, dtype=np.float16)
+    rc = lib().tto_weighted_down(FMT[fmt], rt, _ptr(pw), pw.strides[0], pw.strides[1], _ptr(sw), sw.strides[0],
+                                 sw.strides[1], _ptr(x), dtype_code(x), cols, _ptr(ex), _ptr(sc), dtype_code(sc),
+                                 ex.shape[0], _ptr(b), F16 if b is None else dtype_code(b), rows, _ptr(out), F16,
+                                 rows, cols, lpr)
+    if rc != 0:
+        raise ValueError("oracle weighted_down rejected the configuration")
+    return out

@@ -252,6 +252,10 @@ def test_fused_swiglu(backend, device, bits, with_bias):
                       oracle.F16, inter, inter, cols, lanes(cols))
     assert rc == 0
     assert_bits_equal(from_torch_bits(out).reshape(-1), want.reshape(-1), f"swiglu q{bits}")
+    rnd = ref.f16_round64 if bits == 4 else ref.bf16_round64
+    dq = ref.mxfp4_dequant(packed, scales) if bits == 4 else ref.lowbit_e8_dequant(packed, scales, bits)
+    want64 = np.stack([ref.expert_swiglu64(dq[e], x, bias[e] if with_bias else None, 1.702, 7.0, rnd) for e in idx])
+    assert ref.max_rel_err(from_torch_bits(out), want64) < TOL
 
 
 @pytest.mark.parametrize("bits", [2, 4])
@@ -282,6 +286,10 @@ def test_fused_weighted_down(backend, device, bits):
                                         want.ctypes.data, oracle.F16, rows, cols, lanes(cols))
     assert rc == 0
     assert_bits_equal(from_torch_bits(out), want, f"weighted down bits={bits}")
+    rnd = ref.f16_round64 if bits == 4 else ref.bf16_round64
+    dq = ref.mxfp4_dequant(packed, scales) if bits == 4 else ref.lowbit_e8_dequant(packed, scales, 2)
+    want64 = ref.weighted_down64([dq[e] for e in idx], x, scores, [bias[e] for e in idx], rnd)
+    assert ref.max_rel_err(from_torch_bits(out), want64) < TOL
 
 
 @pytest.mark.parametrize("m,rows,cols,wdt", [(8, 2880, 4096, "f16"), (3, 1000, 2048, "bf16"), (5, 300, 5120, "f16")])
@@ -362,12 +370,14 @@ def test_lowbit_affine_matvec(backend, device, bits, rows):
     assert ref.max_rel_err(got, y64) < TOL
 
 
-def test_int4_selected_matvec(backend, device):
+@pytest.mark.parametrize("scale_dtype", [np.float16, np.float32])
+def test_int4_selected_matvec(backend, device, scale_dtype):
+    """The reference's int4 expert packs carry fp32 group scales (gpu_runtime.py:2613-2615)."""
     experts, rows, cols, group = 5, 1024, 2048, 128
     g = rng(71)
     codes = g.integers(0, 16, size=(experts, rows, cols), dtype=np.uint8)
     packed = layouts.pack_int4(codes)
-    scales = (np.abs(g.standard_normal((experts, rows, cols // group))) * 0.02).astype(np.float16)
+    scales = (np.abs(g.standard_normal((experts, rows, cols // group))) * 0.02).astype(scale_dtype)
     idx = np.array([4, 1, 1], dtype=np.int32)
     x = f16_normal(g, (3, cols))
     out = torch.empty((3, rows), device=device, dtype=torch.float16)
@@ -378,3 +388,4 @@ def test_int4_selected_matvec(backend, device):
         want = oracle.gemv("int4_sym", "group", packed[e], scales[e], x[s], cols=cols, lpr=lanes(cols, 4), L=4,
                            s_row=cols // group, s_grp=1)
         assert_bits_equal(got[s], want, f"int4 selected slot {s}")
+        assert ref.max_rel_err(got[s], ref.gemv64(ref.int4_dequant(packed[e], scales[e], group), x[s])) < TOL

@@ -1,5 +1,6 @@
 """GPU parity of norms, elementwise ops, RoPE, attention, router and lm_head argmax
-against the CPU oracle (bit for bit) and the float64 closed forms (tolerance)."""
+against the CPU oracle (bit for bit) and the float64 closed forms of oracle/ref.py
+(max relative error below the north-star tolerance TOL = 1e-2; router indices exact)."""
 
 from __future__ import annotations
 
@@ -8,10 +9,18 @@ import pytest
 import torch
 
 import oracle
+from oracle import ref
 from tests.helpers import bf16_bits, f16_normal, from_torch_bits, rng, to_torch
 from tests.test_gemv_gpu import assert_bits_equal, lanes
 
 pytestmark = pytest.mark.gpu
+
+TOL = 1e-2  # max |got - want| / max |want| against the float64 closed form
+
+
+def assert_f64(got, want64, what: str) -> None:
+    err = ref.max_rel_err(ref.f64(got).reshape(-1), np.asarray(want64, dtype=np.float64).reshape(-1))
+    assert err < TOL, f"{what}: max relative error {err:.3g} against float64"
 
 
 def P(a):
@@ -28,6 +37,7 @@ def test_rms_norm(backend, device, n, offset):
     want = np.empty(n, dtype=np.float16)
     oracle.lib().tto_rms_norm(P(x), oracle.F16, P(w), oracle.F16, P(want), oracle.F16, n, 1e-5, offset)
     assert_bits_equal(from_torch_bits(out), want, "rms_norm")
+    assert_f64(from_torch_bits(out), ref.rms_norm64(x, w, 1e-5, offset), "rms_norm")
 
 
 @pytest.mark.parametrize("n,seed", [(2048, 0), (2880, 0), (4096, 1), (5120, 0), (5120, 2), (8192, 3)])
@@ -46,6 +56,9 @@ def test_add_rms_norm(backend, device, n, seed):
     oracle.lib().tto_add_rms_norm(P(a), P(b), P(want_res), oracle.F16, P(w), oracle.F16, P(want), oracle.F16, n, 1e-5)
     assert_bits_equal(from_torch_bits(res), want_res, "residual")
     assert_bits_equal(from_torch_bits(out), want, "normed")
+    want_res64, want64 = ref.add_rms_norm64(a, b, w, 1e-5)
+    assert np.array_equal(from_torch_bits(res).astype(np.float64), want_res64)
+    assert_f64(from_torch_bits(out), want64, "add_rms_norm")
 
 
 def test_silu_swiglu_weighted_sum_add(backend, device):
@@ -57,6 +70,7 @@ def test_silu_swiglu_weighted_sum_add(backend, device):
     want = np.empty(n, dtype=np.float16)
     oracle.lib().tto_silu_mul(P(gt), P(up), P(want), oracle.F16, n)
     assert_bits_equal(from_torch_bits(out), want, "silu_mul")
+    assert_f64(from_torch_bits(out), ref.silu_mul64(gt, up), "silu_mul")
 
     gu = f16_normal(g, (4, 2 * 2880), 6.0)
     out2 = torch.empty((4, 2880), device=device, dtype=torch.float16)
@@ -64,6 +78,7 @@ def test_silu_swiglu_weighted_sum_add(backend, device):
     want2 = np.empty((4, 2880), dtype=np.float16)
     oracle.lib().tto_interleaved_swiglu(P(gu), P(want2), oracle.F16, 4, 2880, 1.702, 7.0)
     assert_bits_equal(from_torch_bits(out2).reshape(-1), want2.reshape(-1), "interleaved_swiglu")
+    assert_f64(from_torch_bits(out2), ref.interleaved_swiglu64(gu, 1.702, 7.0), "interleaved_swiglu")
 
     ex = f16_normal(g, (4, 2880))
     sc = np.array([0.5, 0.25, 0.125, 0.125], dtype=np.float16)
@@ -72,6 +87,7 @@ def test_silu_swiglu_weighted_sum_add(backend, device):
     want3 = np.empty(2880, dtype=np.float16)
     oracle.lib().tto_weighted_expert_sum(P(ex), oracle.F16, P(sc), oracle.F16, P(want3), 2880, 4)
     assert_bits_equal(from_torch_bits(out3), want3, "weighted_expert_sum")
+    assert_f64(from_torch_bits(out3), ref.weighted_expert_sum64(ex, sc), "weighted_expert_sum")
 
     out4 = torch.empty(n, device=device, dtype=torch.float16)
     backend.add(to_torch(gt, device), to_torch(up, device), out4)
@@ -95,6 +111,10 @@ def test_rope_table_and_device_position(backend, device):
     oracle.lib().tto_rope(P(qw), P(kw), oracle.F16, P(cos[517]), P(sin[517]), heads, kv_heads, D)
     assert_bits_equal(from_torch_bits(q_t), qw, "rope q")
     assert_bits_equal(from_torch_bits(k_t), kw, "rope k")
+    for src, got in ((q, q_t), (k, k_t)):
+        h = src.reshape(-1, D)
+        first, second = ref.rope64(h[:, :D // 2], h[:, D // 2:], cos[517], sin[517])
+        assert_f64(from_torch_bits(got), np.concatenate([first, second], axis=1), "rope")
 
 
 @pytest.mark.parametrize("cap", [1100, 1152])  # 1152: whole chunks, contiguous rows -> vector-load kernel
@@ -119,6 +139,8 @@ def test_gqa_attention(backend, device, heads, kv_heads, tokens, sinks, cap):
         oracle.lib().tto_attention(P(q), P(keys), P(vals), oracle.F16, cap * D, D, cap * D, D, P(sk) if sinks else None,
                                    oracle.F16, n, heads, kv_heads, D, P(want))
         assert_bits_equal(from_torch_bits(out), want, f"attention ({n} tokens)")
+        want64 = ref.attention64(q.reshape(heads, D), keys[:, :n], vals[:, :n], kv_heads, sinks=sk)
+        assert_f64(from_torch_bits(out), want64, f"attention ({n} tokens)")
 
 
 @pytest.mark.parametrize("renorm,with_bias", [(True, True), (False, False)])
@@ -138,6 +160,9 @@ def test_router(backend, device, renorm, with_bias):
                             int(renorm), P(widx), P(wsc), oracle.F16)
     assert np.array_equal(idx.cpu().numpy(), widx)
     assert_bits_equal(from_torch_bits(sc), wsc, "router scores")
+    idx64, sc64 = ref.router64(w, x, b, k, renorm)
+    assert np.array_equal(idx.cpu().numpy(), idx64)
+    assert_f64(from_torch_bits(sc), sc64, "router scores")
 
 
 @pytest.mark.parametrize("E,H,k,renorm,bias_dtype,wbf16", [
@@ -183,6 +208,10 @@ def test_add_rms_norm_router(backend, device, E, H, k, renorm, bias_dtype, wbf16
     assert_bits_equal(from_torch_bits(normed), want_n, "normed")
     assert np.array_equal(idx.cpu().numpy(), widx), (idx.cpu().numpy(), widx)
     assert_bits_equal(from_torch_bits(sc), wsc, "router scores")
+    assert_f64(from_torch_bits(normed), ref.add_rms_norm64(a, b, nw, 1e-5)[1], "normed")
+    idx64, sc64 = ref.router64(w, want_n, bias, k, renorm)
+    assert np.array_equal(idx.cpu().numpy(), idx64)
+    assert_f64(from_torch_bits(sc), sc64, "router scores")
 
 
 @pytest.mark.parametrize("tokens,H", [(8, 2880), (3, 5120)])
@@ -221,6 +250,7 @@ def test_router_topk_on_logits_with_ties(backend, device):
     wsc = np.empty(4, dtype=np.float16)
     oracle.lib().tto_topk(P(lg), oracle.F16, 8, 4, 1, P(widx), P(wsc), oracle.F16)
     assert_bits_equal(from_torch_bits(sc), wsc, "topk scores")
+    assert_f64(from_torch_bits(sc), ref.topk_softmax64(lg, 4, True)[1], "topk scores")
 
 
 @pytest.mark.parametrize("E,k,renorm,special", [(128, 128, True, False), (128, 100, False, True), (65, 64, True, True),
@@ -243,6 +273,10 @@ def test_router_topk_wave_selection(backend, device, E, k, renorm, special):
     oracle.lib().tto_topk(P(lg), oracle.F16, E, k, int(renorm), P(widx), P(wsc), oracle.F16)
     assert np.array_equal(idx.cpu().numpy(), widx)
     assert_bits_equal(from_torch_bits(sc), wsc, "topk scores")
+    if not special:  # NaN-free logits: stable-sort brute force and float64 softmax
+        idx64, sc64 = ref.topk_softmax64(lg, k, renorm)
+        assert np.array_equal(idx.cpu().numpy(), idx64)
+        assert_f64(from_torch_bits(sc), sc64, "topk scores")
 
 
 @pytest.mark.parametrize("rows,cols", [(128256, 2048), (201088, 2880), (4099, 5120)])
@@ -255,6 +289,7 @@ def test_lm_head_argmax(backend, device, rows, cols):
     logits = from_torch_bits(backend.logits_buffer(rows, torch.float16))
     want_logits = oracle.gemv("f16w", "none", w.view(np.uint8).reshape(rows, -1), None, x, cols=cols, lpr=lanes(cols))
     assert_bits_equal(logits, want_logits, "lm_head logits")
+    assert_f64(logits, ref.gemv64(w, x), "lm_head logits")
     want = int(np.argmax(want_logits.astype(np.float32)))
     assert int(tok.item()) == want == int(oracle.lib().tto_argmax(P(want_logits), oracle.F16, rows))
 
@@ -267,3 +302,38 @@ def test_argmax_ties_pick_lowest_index(backend, device):
     x[0] = 2.0
     tok = backend.matvec_argmax_tensor(to_torch(w, device), to_torch(x, device))
     assert int(tok.item()) == 17
+
+
+def test_argmax_modes_rounded_vs_unrounded(device):
+    """Rows 17 and 3001 tie after rounding to fp16 (1.0 and 1 + 2^-13) but not in
+    binary32: the default mode picks the lower index of the rounded tie, the two-stage
+    and persistent modes the larger binary32 value (triton_kernels.py:2245-2250,
+    2524-2537), and argmax_mode="triton_two_stage" routes matvec_argmax_tensor there."""
+    from thintensor_amd.backend import HipDecodeBackend
+
+    rows, cols = 5000, 64
+    w = np.zeros((rows, cols), dtype=np.float16)
+    w[17, 0] = 1.0
+    w[3001, 0] = 1.0
+    w[3001, 1] = 1.0
+    x = np.zeros(cols, dtype=np.float16)
+    x[0], x[1] = 1.0, 2.0 ** -13
+    be = HipDecodeBackend(device, torch.float16, cols, cols, cols, cols)
+    wt, xt = to_torch(w, device), to_torch(x, device)
+    assert int(be.matvec_argmax_tensor(wt, xt).item()) == 17
+    assert int(be._matvec_argmax_tensor_triton_two_stage(wt, xt).item()) == 3001
+    assert int(be.persistent_vocab_block_matvec_argmax_tensor(wt, xt).item()) == 3001
+    be2 = HipDecodeBackend(device, torch.float16, cols, cols, cols, cols, argmax_mode="triton_two_stage")
+    assert int(be2.matvec_argmax_tensor(wt, xt).item()) == 3001
+
+
+@pytest.mark.parametrize("rows,cols", [(128256, 2048), (4099, 5120)])
+def test_unrounded_argmax_matches_binary32_logits(backend, device, rows, cols):
+    g = rng(rows + 5)
+    w = f16_normal(g, (rows, cols), 0.02)
+    x = f16_normal(g, cols)
+    tok = backend.persistent_vocab_block_matvec_argmax_tensor(to_torch(w, device), to_torch(x, device))
+    lg32 = oracle.gemv("f16w", "none", w.view(np.uint8).reshape(rows, -1), None, x, cols=cols, lpr=lanes(cols),
+                       odtype=oracle.F32)
+    assert int(tok.item()) == int(np.argmax(lg32))
+    assert int(np.argmax(lg32)) == int(np.argmax(ref.gemv64(w, x)))

@@ -45,6 +45,8 @@ def _check(out_t, base32, corr32, out_dtype):
     (2880, 16, 2880, "int64", "f16", "f16", False),
     (77, 150, 5120, "int32", "f32", "f32", True),
     (5, 1, 32, "int64", "bf16", "bf16", False),
+    (5120, 32, 17920, "int16", "f16", "f16", False),  # the reference runtime's int16 sidecar indices
+    (300, 70, 2880, "int16", "bf16", "f32", True),
 ])
 def test_sparse_residual_matches_oracle(backend, device, rows, terms, cols, idx_dtype, vdt, out_dtype, strided):
     import torch
@@ -65,7 +67,7 @@ def test_sparse_residual_matches_oracle(backend, device, rows, terms, cols, idx_
         big = torch.zeros((rows, 2 * terms), device=device, dtype=vt.dtype)
         big[:, ::2] = vt
         vt = big[:, ::2]
-    it = torch.from_numpy(idx.astype(np.int32 if idx_dtype == "int32" else np.int64)).to(device)
+    it = torch.from_numpy(idx.astype({"int16": np.int16, "int32": np.int32, "int64": np.int64}[idx_dtype])).to(device)
     out_t, base = _out(device, g.standard_normal(rows).astype(np.float32), out_dtype)
     print(f"sparse residual rows={rows} terms={terms} cols={cols}", flush=True)
     backend.sparse_residual_matvec(vt, it, to_torch(x, device), out_t)

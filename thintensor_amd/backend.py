@@ -357,6 +357,22 @@ class HipDecodeBackend:
         _lib.check(rc, "mxfp4_selected_matvec")
         return out
 
+    def mxfp4_selected_tensorcore_matvec(
+        self,
+        blocks: torch.Tensor,
+        scales: torch.Tensor,
+        x: torch.Tensor,
+        expert_indices: torch.Tensor,
+        out: torch.Tensor,
+        *,
+        block_m: int = 64,
+        block_n: int = 8,
+    ) -> torch.Tensor:
+        """Same sum as ``mxfp4_selected_matvec`` (triton_kernels.py:3913-3976; the
+        reference's Blackwell tensor-core twin of :416-481).  Tile arguments are
+        accepted and ignored."""
+        return self.mxfp4_selected_matvec(blocks, scales, x, expert_indices, out)
+
     # The reference's Blackwell tensor-core variant computes the same sum
     # (triton_kernels.py:865-930, 3913-3976); on gfx950 it is the same kernel.
     mxfp4_selected_tensorcore_matvec = mxfp4_selected_matvec
@@ -419,8 +435,8 @@ class HipDecodeBackend:
             raise ValueError("sparse residual values/indices shape mismatch")
         rows = int(residual_values.shape[0])
         terms = int(residual_values.shape[1])
-        if residual_indices.dtype not in (torch.int32, torch.int64):
-            raise ValueError("sparse residual indices must be int32 or int64")
+        if residual_indices.dtype not in (torch.int16, torch.int32, torch.int64):
+            raise ValueError("sparse residual indices must be int16, int32 or int64")
         if out.numel() != rows or not out.is_contiguous() or not x.is_contiguous():
             raise ValueError("sparse residual output/input layout mismatch")
         _require_cuda(residual_values, residual_indices, x, out)
@@ -449,6 +465,8 @@ class HipDecodeBackend:
             raise ValueError("binary residual scale shape mismatch")
         if packed_signs.stride(1) != 1 or scales.stride(1) != 1 or out.numel() != rows or not out.is_contiguous():
             raise ValueError("binary residual sign plane, scales and output rows must be contiguous")
+        if not x.is_contiguous():
+            raise ValueError("binary residual input must be contiguous")
         _require_cuda(packed_signs, scales, x, out)
         rc = self.lib.tt_binary_residual_matvec(
             packed_signs.data_ptr(), packed_signs.stride(0), scales.data_ptr(), _code(scales, "binary residual scales"),
@@ -486,7 +504,7 @@ class HipDecodeBackend:
                 f"got {tuple(packed_weight.shape)}, expected {(experts, rows, ternary_bytes + magnitude_bytes)}"
             )
         selected = int(expert_indices.numel())
-        if x.ndim == 1 and int(x.numel()) == cols:
+        if x.ndim == 1 and int(x.numel()) == cols and x.stride(0) == 1:
             stride_xe = 0
         elif x.ndim == 2 and tuple(x.shape) == (selected, cols) and x.stride(1) == 1:
             stride_xe = int(x.stride(0))
@@ -705,15 +723,26 @@ class HipDecodeBackend:
             self._argmax_partials = torch.empty(need, device=self.device, dtype=torch.int64)
         return self._argmax_partials
 
-    def _matvec_argmax(self, weight: torch.Tensor, x: torch.Tensor, logits: torch.Tensor | None) -> torch.Tensor:
+    def _matvec_argmax(self, weight: torch.Tensor, x: torch.Tensor, logits: torch.Tensor | None,
+                       unrounded: bool = False) -> torch.Tensor:
+        """Shared lm_head launch.  The argmax key is taken from each logit rounded to the
+        logits dtype (x's dtype without a logits buffer), or from the binary32 dot
+        product itself when ``unrounded`` (the reference's two-stage and persistent
+        modes, triton_kernels.py:2245-2250, 2524-2537)."""
         _require_cuda(weight, x)
         rows, cols = int(weight.shape[0]), int(weight.shape[1])
         if weight.stride(1) != 1 or x.numel() != cols:
             raise ValueError("matvec_argmax shape mismatch")
         partials = self._argmax_scratch(rows, cols)
+        if unrounded:
+            if logits is not None:
+                raise ValueError("unrounded argmax writes no logits")
+            key_code = _lib.F32
+        else:
+            key_code = _code(logits, "logits") if logits is not None else _code(x, "x")
         rc = self.lib.tt_matvec_argmax(
             weight.data_ptr(), _code(weight, "matvec_argmax"), weight.stride(0), x.data_ptr(), _code(x, "matvec_argmax"),
-            logits.data_ptr() if logits is not None else None, _code(logits, "logits") if logits is not None else _code(x, "x"),
+            logits.data_ptr() if logits is not None else None, key_code,
             rows, cols, partials.data_ptr(), partials.numel(), self._argmax_out_idx.data_ptr(),
             self._argmax_out_val.data_ptr(), _stream(x),
         )
@@ -731,17 +760,25 @@ class HipDecodeBackend:
     ) -> torch.Tensor:
         """Greedy lm_head: first index of the maximum logit rounded to x's dtype
         (triton_kernels.py:5365-5398).  Logits are also written to ``logits_buffer``.
-        Returns a 0-d int64 device tensor that later calls overwrite."""
+        Returns a 0-d int64 device tensor that later calls overwrite.  With
+        ``argmax_mode="triton_two_stage"`` it takes the two-stage path instead, as the
+        reference does (:5381-5382)."""
+        if self.argmax_mode == "triton_two_stage":
+            return self._matvec_argmax_tensor_triton_two_stage(weight, x)
         logits = self.logits_buffer(int(weight.shape[0]), x.dtype)
         return self._matvec_argmax(weight, x, logits)
 
     def _matvec_argmax_tensor_triton_two_stage(self, weight: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
-        """The reference's two-stage mode argmaxes unrounded fp32 logits; this backend
-        keeps one semantic (rounded logits, first index) for every mode."""
-        return self._matvec_argmax(weight, x, None)
+        """Two-stage greedy lm_head (triton_kernels.py:5564-5625, kernels :2222-2285 and
+        :2456-2473): first index of the maximum of the *unrounded* binary32 logits; no
+        logits are stored.  At a tie of rounded logits it can pick a different token
+        than ``matvec_argmax_tensor``, exactly as the reference's modes differ."""
+        return self._matvec_argmax(weight, x, None, unrounded=True)
 
     def persistent_vocab_block_matvec_argmax_tensor(self, weight: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
-        return self._matvec_argmax(weight, x, None)
+        """Persistent vocab-block mode (triton_kernels.py:5516-5562, kernel :2477-2558):
+        the same unrounded binary32 argmax as the two-stage mode."""
+        return self._matvec_argmax(weight, x, None, unrounded=True)
 
     def matvec_argmax(self, weight: torch.Tensor, x: torch.Tensor) -> int:
         raise RuntimeError("matvec_argmax() synchronizes CUDA; use matvec_argmax_tensor()")

@@ -20,7 +20,7 @@ namespace {
 
 struct SparseParams {
   const void* values;       // [rows, terms] (vm, vk element strides)
-  const void* indices;      // [rows, terms] int32 or int64 (im, ik element strides)
+  const void* indices;      // [rows, terms] int16, int32 or int64 (im, ik element strides)
   const void* x;            // [cols]
   void* out;                // [rows], read and written
   int64_t vm, vk, im, ik;
@@ -122,7 +122,8 @@ extern "C" int tt_sparse_residual_matvec(const void* values, int value_dtype, in
   const char* what = "sparse_residual_matvec";
   TT_REQUIRE(valid_out_dtype(value_dtype) && valid_act_dtype(x_dtype) && valid_out_dtype(out_dtype),
              "%s: bad dtype codes", what);
-  TT_REQUIRE(index_bytes == 4 || index_bytes == 8, "%s: indices must be int32 or int64", what);
+  TT_REQUIRE(index_bytes == 2 || index_bytes == 4 || index_bytes == 8, "%s: indices must be int16, int32 or int64",
+             what);
   TT_REQUIRE(rows >= 0 && rows < (1LL << 31) && terms >= 0 && terms < (1LL << 31) && cols > 0 && cols < (1LL << 31),
              "%s: bad shape", what);
   TT_REQUIRE(values && indices && x && out, "%s: null pointer", what);
@@ -139,7 +140,12 @@ extern "C" int tt_sparse_residual_matvec(const void* values, int value_dtype, in
     return x_dtype == TT_F16 ? with_out<decltype(vt), decltype(it), f16_t>(out_dtype, go)
                              : with_out<decltype(vt), decltype(it), bf16_t>(out_dtype, go);
   };
-  auto by_i = [&](auto vt) { return index_bytes == 4 ? by_x(vt, int32_t{}) : by_x(vt, int64_t{}); };
+  // int16 indices (the reference runtime's sidecar layout, gpu_runtime.py:6468) are
+  // sign-extended, so a negative stored index takes the out-of-range NaN rule
+  auto by_i = [&](auto vt) {
+    if (index_bytes == 2) return by_x(vt, int16_t{});
+    return index_bytes == 4 ? by_x(vt, int32_t{}) : by_x(vt, int64_t{});
+  };
   switch (value_dtype) {
     case TT_F16: return by_i(f16_t{});
     case TT_BF16: return by_i(bf16_t{});
