@@ -48,16 +48,33 @@ def _compile(src: Path, obj: Path) -> tuple[Path, str]:
     return obj, proc.stderr
 
 
-def build(verbose: bool = False, jobs: int | None = None) -> Path:
-    """Compile every source under csrc/ and link the shared library."""
+def _stale(src: Path, obj: Path, headers_mtime: float) -> bool:
+    if not obj.exists():
+        return True
+    t = obj.stat().st_mtime
+    return src.stat().st_mtime > t or headers_mtime > t
+
+
+def build(verbose: bool = False, jobs: int | None = None, incremental: bool = False) -> Path:
+    """Compile every source under csrc/ and link the shared library.  With
+    ``incremental`` only sources newer than their object (or older than a changed
+    header) are recompiled."""
     BUILD_DIR.mkdir(exist_ok=True)
     sources = sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.cpp")))
     if not sources:
         raise RuntimeError("no kernel sources found")
     jobs = jobs or min(8, os.cpu_count() or 4)
+    headers = list(CSRC.glob("*.h")) + list((PKG_DIR.parent / "include").glob("*.h"))
+    headers_mtime = max((h.stat().st_mtime for h in headers), default=0.0)
     objs: list[Path] = []
     with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
-        futs = [pool.submit(_compile, s, BUILD_DIR / (s.stem + ".o")) for s in sources]
+        futs = []
+        for s in sources:
+            obj = BUILD_DIR / (s.stem + ".o")
+            if incremental and not _stale(s, obj, headers_mtime):
+                objs.append(obj)
+                continue
+            futs.append(pool.submit(_compile, s, obj))
         for fut in futs:
             obj, log = fut.result()
             objs.append(obj)
@@ -75,5 +92,5 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
 
 
 if __name__ == "__main__":
-    path = build(verbose="-v" in sys.argv)
+    path = build(verbose="-v" in sys.argv, incremental="--incremental" in sys.argv)
     print(path)
