@@ -249,6 +249,18 @@ int tt_matvec_argmax(const void* weight, int w_dtype, int64_t w_row, const void*
                      void* logits, int logits_dtype, int64_t rows, int64_t cols, uint64_t* partials,
                      int64_t partials_capacity, int64_t* out_idx, float* out_val, void* stream);
 
+/* No-allocation greedy lm_head: tt_matvec_argmax with its argmax partials in a
+ * library-owned device array of TT_NOALLOC_ARGMAX_KEYS uint64 keys (64 KiB per GPU,
+ * held until the process ends) instead of caller scratch; it calls no hipMalloc or
+ * hipFree.  Every shape tt_matvec_argmax accepts fits.  Calls that overlap on one GPU
+ * share the array and race; serialize them (one stream, or events).
+ * No counterpart in the reference: it is for callers that cannot allocate device
+ * memory (HIP graph capture, tight serving loops, harnesses that forbid allocation). */
+#define TT_NOALLOC_ARGMAX_KEYS 8192
+int tt_matvec_argmax_noalloc(const void* weight, int w_dtype, int64_t w_row, const void* x, int x_dtype,
+                             void* logits, int logits_dtype, int64_t rows, int64_t cols, int64_t* out_idx,
+                             float* out_val, void* stream);
+
 /* tt_multi_matvec with a per-matrix bias (nullable entries) fused into the
  * epilogue: out = round(round(dot) + bias), identical to the runtime's GEMV followed
  * by its in-place bias add (gpu_runtime.py:9100-9114, 9213-9221). */

@@ -76,6 +76,7 @@ SIGNATURES: dict[str, list] = {
     "tt_record_token": [_P, _P, _P, _P, ctypes.c_int32, _P],
     "tt_matvec_argmax_partials": [_L, _L],
     "tt_matvec_argmax": [_P, _I, _L, _P, _I, _P, _I, _L, _L, _P, _L, _P, _P, _P],
+    "tt_matvec_argmax_noalloc": [_P, _I, _L, _P, _I, _P, _I, _L, _L, _P, _P, _P],
     "tt_rms_norm": [_P, _I, _P, _I, _P, _I, _L, _F, _F, _P],
     "tt_add_rms_norm": [_P, _P, _P, _I, _P, _I, _P, _I, _L, _F, _P],
     "tt_add": [_P, _P, _P, _I, _L, _P],

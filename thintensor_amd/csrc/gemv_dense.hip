@@ -1,4 +1,6 @@
 // fp16/bf16 and fp8 GEMV entry points.
+#include <mutex>
+
 #include "gemv_lean.h"
 
 using namespace tt;
@@ -202,4 +204,61 @@ extern "C" int tt_matvec_argmax(const void* weight, int w_dtype, int64_t w_row, 
   if (rc) return rc;
   hipLaunchKernelGGL(argmax_finish_kernel, dim3(1), dim3(256), 0, st, partials, (int)need, out_idx, out_val);
   return check_launch(what);
+}
+
+// ------------------------------------------------------------------ no-allocation lm_head
+//
+// tt_matvec_argmax with its argmax partials in a file-scope device array instead of a
+// caller workspace, for callers that cannot allocate device memory.  The array holds
+// kNoAllocArgmaxKeys keys (64 KiB), the most any shape can ask for: the grid is capped at
+// kMaxGemvBlocks workgroups of four waves and every wave writes its key in each call, so
+// nothing needs clearing between calls.  Each GPU holds its own copy until the process
+// ends; calls that overlap on one GPU share it and race.
+
+namespace {
+
+constexpr int kNoAllocArgmaxKeys = TT_NOALLOC_ARGMAX_KEYS;
+static_assert(kNoAllocArgmaxKeys >= kMaxGemvWaves, "argmax scratch must hold one key per wave of the largest grid");
+
+static __device__ __align__(256) uint64_t scratch[kNoAllocArgmaxKeys];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+uint64_t* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// Device address of `scratch` on the current device, resolved once per device with that
+// device current (each GPU holds its own copy at its own address).
+int scratch_for_current_device(const char* what, uint64_t** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  TT_REQUIRE(e == hipSuccess && dev >= 0 && dev < kMaxScratchDevices, "%s: no usable current device", what);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      set_error("%s: hipGetSymbolAddress(scratch) failed on device %d: %s", what, dev, hipGetErrorString(e));
+      return TT_ERR_HIP;
+    }
+    g_scratch_ptr[dev] = static_cast<uint64_t*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return TT_OK;
+}
+
+}  // namespace
+
+extern "C" int tt_matvec_argmax_noalloc(const void* weight, int w_dtype, int64_t w_row, const void* x, int x_dtype,
+                                        void* logits, int logits_dtype, int64_t rows, int64_t cols, int64_t* out_idx,
+                                        float* out_val, void* stream) {
+  const char* what = "matvec_argmax_noalloc";
+  TT_REQUIRE(rows > 0 && rows < (1LL << 31) && cols > 0, "%s: bad shape", what);
+  const int64_t need = tt_matvec_argmax_partials(rows, cols);
+  TT_REQUIRE(need <= kNoAllocArgmaxKeys, "%s: %lld argmax partials exceed the %d-key scratch", what, (long long)need,
+             kNoAllocArgmaxKeys);
+  uint64_t* ptr = nullptr;
+  int rc = scratch_for_current_device(what, &ptr);
+  if (rc) return rc;
+  return tt_matvec_argmax(weight, w_dtype, w_row, x, x_dtype, logits, logits_dtype, rows, cols, ptr,
+                          kNoAllocArgmaxKeys, out_idx, out_val, stream);
 }
