@@ -128,11 +128,17 @@ class DenseRef:
             final = normed
         return lm_head_argmax(self.lm_head, final)
 
-    def generate(self, token: int, pos: int, steps: int) -> list[int]:
+    def generate(self, token: int, pos: int, steps: int, margins: list | None = None) -> list[int]:
+        """Greedy tokens; ``margins`` (if given) receives each step's gap between the two
+        largest logits, and ``self.last_logits`` holds the final step's logits."""
         out = []
         for i in range(steps):
-            token, _ = self.step(token, pos + i)
+            token, logits = self.step(token, pos + i)
             out.append(token)
+            if margins is not None:
+                top2 = np.partition(logits.astype(np.float32), -2)[-2:]
+                margins.append(float(top2[1] - top2[0]))
+        self.last_logits = logits if steps else None
         return out
 
 
@@ -189,9 +195,15 @@ class MoERef:
                 final = rms_norm(h, self.final_norm, s.eps)
         return lm_head_argmax(self.lm_head, final)
 
-    def generate(self, token: int, pos: int, steps: int) -> list[int]:
+    def generate(self, token: int, pos: int, steps: int, margins: list | None = None) -> list[int]:
+        """Greedy tokens; ``margins`` (if given) receives each step's gap between the two
+        largest logits, and ``self.last_logits`` holds the final step's logits."""
         out = []
         for i in range(steps):
-            token, _ = self.step(token, pos + i)
+            token, logits = self.step(token, pos + i)
             out.append(token)
+            if margins is not None:
+                top2 = np.partition(logits.astype(np.float32), -2)[-2:]
+                margins.append(float(top2[1] - top2[0]))
+        self.last_logits = logits if steps else None
         return out

@@ -98,25 +98,85 @@ def test_small_moe_32_tokens(device, fused):
     assert np.array_equal(_final_logits(dec).view(np.uint16), logits.view(np.uint16))
 
 
+@pytest.fixture(scope="module")
+def llama_case(device):
+    """Llama-3.2-1B-shaped model with centered int4 codes (q in [-7, 7]), 64 oracle
+    tokens from start token 1 at position 512, the per-step top-2 logit margins and the
+    final step's logits.  The oracle copies the weights and cache before any GPU run."""
+    s = LLAMA_1B
+    w = make_dense(s, device=device, seed=0, centered_codes=True)
+    ref = DenseRef(w)
+    margins: list[float] = []
+    want = ref.generate(1, s.prior_tokens, 64, margins=margins)
+    print(f"llama-1b oracle stream: {len(set(want))} distinct of 64, min top-2 margin {min(margins):.4g}", flush=True)
+    return w, want, ref.last_logits, margins
+
+
 @pytest.mark.parametrize("fused", [False, True])
-def test_llama_1b_shaped_tokens(device, fused):
+def test_llama_1b_shaped_64_tokens(device, llama_case, fused):
+    """64 graph-replayed tokens at the full 1B shape equal the oracle's, and the last
+    step's 128256 logits are bit-identical."""
+    w, want, logits, margins = llama_case
+    s = LLAMA_1B
+    dec = DenseDecoder(_backend(device, s), w, fused=fused)
+    got = dec.generate(1, s.prior_tokens, 64)
+    assert got == want
+    assert len(set(want)) >= 8, f"degenerate stream {want}"
+    assert np.array_equal(_final_logits(dec).view(np.uint16), logits.view(np.uint16))
+    assert all(np.isfinite(margins))
+
+
+def test_llama_1b_baseline_init_tokens(device):
+    """The benchmark's own init (q in [-8, 7]): the fp16 residual overflows, so the
+    stream is that of non-finite logits; it and the final logits still match the
+    oracle bit for bit (NaN and inf propagate the same way)."""
     s = LLAMA_1B
     w = make_dense(s, device=device, seed=0)
-    dec = DenseDecoder(_backend(device, s), w, fused=fused)
     ref = DenseRef(w)
-    start, pos, n = 1, s.prior_tokens, 6
-    got = dec.generate(start, pos, n)
-    want = ref.generate(start, pos, n)
-    assert got == want
+    want = ref.generate(1, s.prior_tokens, 16)
+    dec = DenseDecoder(_backend(device, s), w, fused=True)
+    assert dec.generate(1, s.prior_tokens, 16) == want
+    assert np.array_equal(_final_logits(dec).view(np.uint16), ref.last_logits.view(np.uint16))
+
+
+@pytest.fixture(scope="module")
+def gptoss_case(device):
+    s = GPT_OSS_20B
+    w = make_moe(s, device=device, seed=0)
+    ref = MoERef(w)
+    margins: list[float] = []
+    want = ref.generate(1, s.prior_tokens, 8, margins=margins)
+    print(f"gpt-oss oracle stream: {want}, min top-2 margin {min(margins):.4g}", flush=True)
+    return w, want, ref.last_logits, margins
 
 
 @pytest.mark.parametrize("fused", [False, True])
-def test_gpt_oss_20b_shaped_tokens(device, fused):
+def test_gpt_oss_20b_shaped_tokens(device, gptoss_case, fused):
+    """8 graph-replayed tokens at the full gpt-oss-20B shape equal the oracle's, and the
+    last step's 201088 logits are bit-identical."""
+    w, want, logits, margins = gptoss_case
     s = GPT_OSS_20B
-    w = make_moe(s, device=device, seed=0)
     dec = MoEDecoder(_backend(device, s), w, fused=fused)
-    ref = MoERef(w)
-    start, pos, n = 1, s.prior_tokens, 3
-    got = dec.generate(start, pos, n)
-    want = ref.generate(start, pos, n)
+    got = dec.generate(1, s.prior_tokens, 8)
     assert got == want
+    assert len(set(want)) >= 4, f"degenerate stream {want}"
+    assert np.array_equal(_final_logits(dec).view(np.uint16), logits.view(np.uint16))
+
+
+def test_gpt_oss_20b_shaped_batch8(device, gptoss_case):
+    """Eight sequences in lockstep at the full gpt-oss shape (one attention launch and
+    one 8-row lm_head per step): every stream equals that sequence decoded alone by
+    the bs=1 decoder (gpu_runtime.py:11130-11209 semantics, 8 independent routings)."""
+    s = GPT_OSS_20B
+    w = gptoss_case[0]
+    batch, steps = 8, 4
+    kc, vc = _batch_caches(s, w, batch, device, seed=11)
+    starts = [(7919 * b + 3) % s.vocab for b in range(batch)]
+    want = []
+    for b in range(batch):
+        wb = _sequence_weights(w, kc, vc, b, s.kv_heads)
+        want.append(MoEDecoder(_backend(device, s), wb, fused=True).generate(starts[b], s.prior_tokens, steps))
+        del wb
+    got = MoEBatchDecoder(_backend(device, s), w, batch, kc, vc).generate(starts, s.prior_tokens, steps)
+    assert got == want
+    assert len({t for seq in want for t in seq}) >= 8

@@ -83,8 +83,18 @@ def _normal(g: torch.Generator, shape, std: float, device) -> torch.Tensor:
     return (torch.randn(shape, generator=g, device=device, dtype=torch.float32) * std).to(torch.float16)
 
 
-def _int4(g: torch.Generator, rows: int, cols: int, group: int, device) -> tuple[torch.Tensor, torch.Tensor]:
-    packed = torch.randint(0, 256, (rows, cols // 2), generator=g, device=device, dtype=torch.uint8)
+def _int4(g: torch.Generator, rows: int, cols: int, group: int, device,
+          centered: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
+    """Packed int4 codes and fp16 group scales |N(0,1)| * 0.02.  Codes are uniform over
+    q in [-8, 7] (the benchmark definition) or, when ``centered``, over q in [-7, 7]
+    (the clamp of the reference's _quantize_int4_rows, gpu_runtime.py:6668), which has
+    no mean and so no row bias common to every output."""
+    if centered:
+        lo = torch.randint(1, 16, (rows, cols // 2), generator=g, device=device, dtype=torch.uint8)
+        hi = torch.randint(1, 16, (rows, cols // 2), generator=g, device=device, dtype=torch.uint8)
+        packed = lo | (hi << 4)
+    else:
+        packed = torch.randint(0, 256, (rows, cols // 2), generator=g, device=device, dtype=torch.uint8)
     scales = (torch.randn((rows, cols // group), generator=g, device=device).abs() * 0.02).to(torch.float16)
     return packed, scales
 
@@ -125,7 +135,13 @@ def rope_tables(head_dim: int, theta: float, positions: int, device) -> tuple[to
     return ang.cos().to(torch.float16).to(device), ang.sin().to(torch.float16).to(device)
 
 
-def make_dense(shape: DenseShape = LLAMA_1B, device="cuda", seed: int = 0, capacity: int | None = None) -> DenseWeights:
+def make_dense(shape: DenseShape = LLAMA_1B, device="cuda", seed: int = 0, capacity: int | None = None,
+               centered_codes: bool = False) -> DenseWeights:
+    """Seeded random weights of a dense int4 model.  With the benchmark's codes
+    (q in [-8, 7], mean -0.5) every row of a layer carries the same sign of bias, the
+    MLP output grows about sixteenfold per layer at the Llama-1B shape and the fp16
+    residual overflows after four layers, so the token stream is that of NaN logits;
+    ``centered_codes`` draws q in [-7, 7] and keeps the activations finite."""
     g = torch.Generator(device=device)
     g.manual_seed(seed)
     H, I, G = shape.hidden, shape.intermediate, shape.group
@@ -137,9 +153,10 @@ def make_dense(shape: DenseShape = LLAMA_1B, device="cuda", seed: int = 0, capac
     )
     for _ in range(shape.layers):
         w.layers.append(DenseLayer(
-            q=_int4(g, shape.q_dim, H, G, device), k=_int4(g, shape.kv_dim, H, G, device),
-            v=_int4(g, shape.kv_dim, H, G, device), o=_int4(g, H, shape.q_dim, G, device),
-            gate=_int4(g, I, H, G, device), up=_int4(g, I, H, G, device), down=_int4(g, H, I, G, device),
+            q=_int4(g, shape.q_dim, H, G, device, centered_codes), k=_int4(g, shape.kv_dim, H, G, device, centered_codes),
+            v=_int4(g, shape.kv_dim, H, G, device, centered_codes), o=_int4(g, H, shape.q_dim, G, device, centered_codes),
+            gate=_int4(g, I, H, G, device, centered_codes), up=_int4(g, I, H, G, device, centered_codes),
+            down=_int4(g, H, I, G, device, centered_codes),
             ln1=torch.ones(H, device=device, dtype=torch.float16), ln2=torch.ones(H, device=device, dtype=torch.float16),
         ))
     cap = capacity or (shape.prior_tokens + shape.max_new_tokens)
