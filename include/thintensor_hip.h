@@ -35,6 +35,7 @@ extern "C" {
 #define TT_F16 0
 #define TT_BF16 1
 #define TT_F32 2
+#define TT_W_FP8 3   /* weight format code: float8_e4m3fn (tt_split_k_matvec) */
 
 /* Library version and last error (thread-local message of the last failing call). */
 int tt_version(void);
@@ -238,6 +239,43 @@ int tt_int4_selected_matvec(const void* packed, int64_t w_expert_bytes, int64_t 
                             void* out, int out_dtype, int64_t out_slot,
                             int64_t rows, int64_t cols, int64_t group_size, void* stream);
 
+/* fp8 GEMV with per-block scales: y[m] = sum_b s[m*s_row + b*s_block] * sum_{k in block b}
+ * w[m,k] x[k], blocks of `block` columns (a power of two; the last may be partial; a
+ * block as wide as the row is the per-row-scale GEMV).  Blocks of 32 to 2048 columns.
+ * Replaces the block-scaled branch of TritonDecodeBackend.scaled_matvec
+ * (triton_kernels.py:4465-4497; kernel :3113-3152). */
+int tt_block_scaled_matvec(const void* weight, int64_t w_row_bytes, const void* scales, int scale_dtype,
+                           int64_t s_row, int64_t s_block, int64_t block, const void* x, int x_dtype,
+                           void* out, int out_dtype, int64_t rows, int64_t cols, void* stream);
+
+/* One to three fp8 matrices with per-row scales (scale i of matrix j at
+ * scales[j][i * s_stride[j]]) over one activation vector; outputs concatenated in
+ * matrix order.  Replaces TritonDecodeBackend.multi_scaled_tensorcore_matvec
+ * (triton_kernels.py:5119-5180; kernel :1958-2071). */
+int tt_multi_scaled_matvec(int count, const void* const* weights, const int64_t* w_row_bytes,
+                           const void* const* scales, int scale_dtype, const int64_t* s_stride,
+                           const int64_t* rows, const void* x, int x_dtype, void* out, int out_dtype,
+                           int64_t cols, void* stream);
+
+/* Split-K GEMV: K cut into split_k (2, 4 or 8) slices of whole 32-column chunks; binary32
+ * row sums of each slice go to partials[s * rows + m] (caller scratch of split_k * rows
+ * floats), then y = ((0 + p_0) + p_1 + ...) * scale (scales nullable).  w_format TT_F16,
+ * TT_BF16 or TT_W_FP8.  Replaces TritonDecodeBackend.split_k_matvec
+ * (triton_kernels.py:3773-3845; kernels :3023-3100). */
+int tt_split_k_matvec(const void* weight, int w_format, int64_t w_row_bytes, const void* scales, int scale_dtype,
+                      const void* x, int x_dtype, void* out, int out_dtype, int64_t rows, int64_t cols,
+                      int split_k, float* partials, int64_t partials_capacity, void* stream);
+
+/* Fused fp8 gate/up GEMV + SiLU: out[m] = silu(g) * u with g = bf16((W_g[m] . x) * s_g[m])
+ * and u = bf16((W_u[m] . x) * s_u[m]) (bfloat16 rounding whatever the activation dtype).
+ * Each dot product has the reduction order of tt_scaled_matvec.  Replaces
+ * TritonDecodeBackend.fused_scaled_gate_up_silu (triton_kernels.py:4346-4436; kernels
+ * :3243-3350). */
+int tt_scaled_gate_up_silu(const void* gate_weight, int64_t wg_row_bytes, const void* gate_scales,
+                           int64_t sg_stride, const void* up_weight, int64_t wu_row_bytes, const void* up_scales,
+                           int64_t su_stride, int scale_dtype, const void* x, int x_dtype, void* out,
+                           int out_dtype, int64_t rows, int64_t cols, void* stream);
+
 /* Greedy lm_head: logits = round(W x) (stored when `logits` is non-null), token =
  * first index of the maximum rounded logit (NaN counts as the maximum, +0 == -0),
  * written as int64 to out_idx and the value to out_val (nullable).  `partials` is
@@ -304,6 +342,22 @@ int tt_weighted_expert_sum(const void* experts, int dtype, int64_t stride, int64
 int tt_rope_qk_inplace(void* q, void* k, int dtype, const void* cos_table, const void* sin_table,
                        int64_t table_row, int64_t table_rows, const int32_t* position_dev, int64_t position,
                        int64_t heads, int64_t kv_heads, int64_t head_dim, void* stream);
+
+/* Per-head RMSNorm: out[h*D + i] = (x * (1 / sqrt(mean_h(x^2) + eps))) * w[i], heads of
+ * head_dim <= 512.  Replaces TritonDecodeBackend.head_rms_norm (triton_kernels.py:
+ * 5669-5687; kernel :2618-2634). */
+int tt_head_rms_norm(const void* x, int dtype, const void* weight, int w_dtype, void* out, int64_t heads,
+                     int64_t head_dim, float eps, void* stream);
+
+/* Per-head RMSNorm then RoPE in place on q heads and k heads: a' = a * (inv * w[i]),
+ * b' = b * (inv * w[i + half]), then (a' c - b' s, b' c + a' s) in binary32 with cos/sin
+ * taken from a table row (device or host position, as tt_rope_qk_inplace); head_dim <= 512.
+ * Replaces TritonDecodeBackend.qk_head_rmsnorm_rope_inplace (triton_kernels.py:5716-5749;
+ * kernel :2691-2757). */
+int tt_qk_head_rmsnorm_rope_inplace(void* q, void* k, int dtype, const void* q_weight, const void* k_weight,
+                                    int w_dtype, const void* cos_table, const void* sin_table, int64_t table_row,
+                                    int64_t table_rows, const int32_t* position_dev, int64_t position, int64_t heads,
+                                    int64_t kv_heads, int64_t head_dim, float eps, void* stream);
 
 /* out = embed[token] with the token read from token_dev (int64) if non-null; a device
  * token outside [0, vocab) leaves out unchanged.

@@ -64,6 +64,8 @@ EXTRA_SIGNATURES: dict[str, list] = {
     "tto_interleaved_swiglu": [_P, _P, _I, _I, _I, ctypes.c_float, ctypes.c_float],
     "tto_weighted_expert_sum": [_P, _I, _P, _I, _P, _I, _I],
     "tto_rope": [_P, _P, _I, _P, _P, _I, _I, _I],
+    "tto_head_rms_norm": [_P, _I, _P, _I, _P, _I, _I, ctypes.c_float],
+    "tto_qk_head_rope": [_P, _P, _I, _P, _P, _I, _P, _P, _I, _I, _I, ctypes.c_float],
     "tto_attention": [_P, _P, _P, _I, _L, _L, _L, _L, _P, _I, _I, _I, _I, _I, _P],
     "tto_router": [_P, _I, _L, _P, _I, _I, _P, _I, _I, _I, _I, _P, _P, _I],
     "tto_topk": [_P, _I, _I, _I, _I, _P, _P, _I],
@@ -247,3 +249,49 @@ def weighted_down(fmt: str, packed, scales, x, experts, scores, bias, *, lpr: in
     if rc != 0:
         raise ValueError("oracle weighted_down rejected the configuration")
     return out
+
+
+def head_rms_norm(x, w, heads: int, head_dim: int, eps: float) -> np.ndarray:
+    x, w = _c(x), _c(w)
+    out = np.empty_like(x)
+    lib().tto_head_rms_norm(_ptr(x), dtype_code(x), _ptr(w), dtype_code(w), _ptr(out), heads, head_dim, eps)
+    return out
+
+
+def qk_head_rmsnorm_rope(q, k, q_weight, k_weight, cos_row, sin_row, heads: int, kv_heads: int, head_dim: int,
+                         eps: float):
+    q, k = _c(q).copy(), _c(k).copy()
+    qw, kw = _c(q_weight), _c(k_weight)
+    c, s = _c(cos_row), _c(sin_row)
+    lib().tto_qk_head_rope(_ptr(q), _ptr(k), dtype_code(q), _ptr(qw), _ptr(kw), dtype_code(qw), _ptr(c), _ptr(s),
+                           heads, kv_heads, head_dim, eps)
+    return q, k
+
+
+def split_k_gemv(fmt: str, w: np.ndarray, x: np.ndarray, split_k: int, scales=None, odtype: int = F16) -> np.ndarray:
+    """Split-K GEMV restated: slices of q = ceil(K/32/split_k) whole chunks (last one
+    shorter or absent), each the single-matrix binary32 row sum of its width, added in
+    slice order from +0, times the per-row scale, rounded once.  ``w`` is uint8
+    [rows, row_bytes] of dense fp16/bf16 or fp8 weights."""
+    from .decode_ref import lanes
+
+    esz = 1 if fmt == "fp8" else 2
+    wb = np.ascontiguousarray(w).view(np.uint8).reshape(w.shape[0], -1)
+    cols = x.shape[0]
+    nchunks = cols // 32
+    q = -(-nchunks // split_k)
+    acc = np.zeros(wb.shape[0], dtype=np.float32)
+    for c0 in range(0, nchunks, q):
+        c1 = min(nchunks, c0 + q)
+        width = (c1 - c0) * 32
+        part = gemv(fmt, "none", wb[:, c0 * 32 * esz:c1 * 32 * esz], None, np.ascontiguousarray(x[c0 * 32:c1 * 32]),
+                    cols=width, lpr=lanes(width), odtype=F32)
+        acc = (acc + part).astype(np.float32)
+    if scales is not None:
+        acc = (acc * np.asarray(scales, dtype=np.float32)).astype(np.float32)
+    if odtype == F16:
+        return acc.astype(np.float16)
+    if odtype == BF16:
+        u = acc.view(np.uint32).astype(np.uint64)
+        return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    return acc

@@ -469,6 +469,61 @@ int tto_rope(void* q, void* k, int dt, const void* cos_row, const void* sin_row,
   return 0;
 }
 
+/* Per-head RMSNorm (triton_kernels.py:2618-2634) in the kernel's order: lane l sums the
+ * squares of elements l, l + 64, ... as an fma chain, then the 64-lane butterfly. */
+int tto_head_rms_norm(const void* x, int dt, const void* w, int wdt, void* out, int heads, int D, float eps) {
+  for (int h = 0; h < heads; h++) {
+    float s[64];
+    for (int l = 0; l < 64; l++) {
+      float a = 0.0f;
+      for (int i = l; i < D; i += 64) {
+        const float v = act_get(x, dt, (int64_t)h * D + i);
+        a = fmaf(v, v, a);
+      }
+      s[l] = a;
+    }
+    xor_sum(s, 64, 1, 64);
+    const float inv = 1.0f / sqrtf(s[0] / (float)D + eps);
+    for (int i = 0; i < D; i++)
+      act_put(out, dt, (int64_t)h * D + i, (act_get(x, dt, (int64_t)h * D + i) * inv) * act_get(w, wdt, i));
+  }
+  return 0;
+}
+
+/* Per-head RMSNorm + RoPE in place (triton_kernels.py:2691-2757) in the kernel's order:
+ * lane l takes pairs (i, i + half), i = l, l + 64, ...: s = fma(a, a, s), s = fma(b, b, s);
+ * 64-lane butterfly; a' = a * (inv * w[i]), b' = b * (inv * w[i + half]); binary32
+ * rotation with cos/sin from the activation-dtype table row, rounded once. */
+int tto_qk_head_rope(void* q, void* k, int dt, const void* qw, const void* kw, int wdt, const void* cos_row,
+                     const void* sin_row, int heads, int kv_heads, int D, float eps) {
+  const int half = D / 2;
+  for (int hh = 0; hh < heads + kv_heads; hh++) {
+    void* base = hh < heads ? q : k;
+    const void* w = hh < heads ? qw : kw;
+    const int64_t off = (int64_t)(hh < heads ? hh : hh - heads) * D;
+    float s[64];
+    for (int l = 0; l < 64; l++) {
+      float a = 0.0f;
+      for (int i = l; i < half; i += 64) {
+        const float x1 = act_get(base, dt, off + i), x2 = act_get(base, dt, off + i + half);
+        a = fmaf(x1, x1, a);
+        a = fmaf(x2, x2, a);
+      }
+      s[l] = a;
+    }
+    xor_sum(s, 64, 1, 64);
+    const float inv = 1.0f / sqrtf(s[0] / (float)D + eps);
+    for (int i = 0; i < half; i++) {
+      const float an = act_get(base, dt, off + i) * (inv * act_get(w, wdt, i));
+      const float bn = act_get(base, dt, off + i + half) * (inv * act_get(w, wdt, i + half));
+      const float c = act_get(cos_row, dt, i), sn = act_get(sin_row, dt, i);
+      act_put(base, dt, off + i, an * c - bn * sn);
+      act_put(base, dt, off + i + half, bn * c + an * sn);
+    }
+  }
+  return 0;
+}
+
 /* ------------------------------------------------------------ attention */
 
 /*

@@ -345,3 +345,70 @@ def test_weighted_down_exact_and_slot_order_caught(fmt):
     # planted: router scores applied in reverse slot order
     bad = oracle.weighted_down(fmt, packed, scales, x, experts, scores[::-1].copy(), bias, lpr=lanes(cols))
     assert not np.array_equal(bad.astype(np.float64), ref.f16_round64(want))
+
+
+# ---------------------------------------------------------------- per-head RMSNorm and QK norm + RoPE
+
+
+@pytest.mark.parametrize("heads,D", [(32, 128), (8, 64), (4, 256)])
+def test_head_rms_norm_vs_float64(heads, D):
+    g = rng(1000 + heads + D)
+    x, w = f16_normal(g, heads * D, 2.0), f16_normal(g, D, 0.5)
+    got = oracle.head_rms_norm(x, w, heads, D, 1e-6)
+    want = np.concatenate([ref.rms_norm64(x[h * D:(h + 1) * D], w, 1e-6) for h in range(heads)])
+    assert within_ulp(got, want)
+    # planted: one norm over all heads instead of one per head
+    assert not within_ulp(got, ref.rms_norm64(x, np.tile(w, heads), 1e-6))
+
+
+def _qk_norm_rope64(x, w, heads, D, c, s, eps):
+    out = []
+    for h in range(heads):
+        n = ref.rms_norm64(x[h * D:(h + 1) * D], w, eps)
+        first, second = ref.rope64(n[:D // 2], n[D // 2:], c, s)
+        out.append(np.concatenate([first, second]))
+    return np.concatenate(out)
+
+
+def test_qk_head_rmsnorm_rope_vs_float64_and_planted_sign():
+    heads, kv_heads, D = 16, 4, 128
+    g = rng(1100)
+    cos, sin = _rope_table(700, D, 1000000.0)
+    q, k = f16_normal(g, heads * D, 2.0), f16_normal(g, kv_heads * D)
+    qw, kw = f16_normal(g, D, 0.5), f16_normal(g, D, 0.5)
+    p = 613
+    qo, ko = oracle.qk_head_rmsnorm_rope(q, k, qw, kw, cos[p], sin[p], heads, kv_heads, D, 1e-6)
+    for x, w, n, got in ((q, qw, heads, qo), (k, kw, kv_heads, ko)):
+        want = _qk_norm_rope64(x, w, n, D, cos[p], sin[p], 1e-6)
+        # binary32 rotation rounded once: within one binary16 ulp of the operands' scale
+        norm = np.concatenate([np.abs(ref.rms_norm64(x[h * D:(h + 1) * D], w, 1e-6)) for h in range(n)])
+        scale = ref.ulp16(np.maximum(norm, np.roll(norm.reshape(n, 2, D // 2), 1, axis=1).reshape(-1)))
+        assert np.max(np.abs(ref.f64(got) - want) / scale) <= 1.0
+    # position 0 is the per-head RMSNorm alone (cos 1, sin 0)
+    q0, _ = oracle.qk_head_rmsnorm_rope(q, k, qw, kw, cos[0], sin[0], heads, kv_heads, D, 1e-6)
+    assert within_ulp(q0, np.concatenate([ref.rms_norm64(q[h * D:(h + 1) * D], qw, 1e-6) for h in range(heads)]))
+    # planted: rotation the wrong way
+    qb, _ = oracle.qk_head_rmsnorm_rope(q, k, qw, kw, cos[p], (-sin[p]).astype(np.float16), heads, kv_heads, D, 1e-6)
+    assert np.max(np.abs(ref.f64(qb) - _qk_norm_rope64(q, qw, heads, D, cos[p], sin[p], 1e-6))) > 0.1
+
+
+def test_split_k_restatement_vs_float64_and_exact():
+    """Split-K composition of the GEMV restatement: exact on integer inputs whatever
+    the split, close to float64 otherwise, and a dropped slice is caught."""
+    g = rng(1200)
+    rows, cols = 64, 2880
+    w_int = g.integers(-4, 5, size=(rows, cols)).astype(np.float16)
+    x_int = g.integers(-3, 4, size=cols).astype(np.float16)
+    for sk in (2, 4, 8):
+        got = oracle.split_k_gemv("f16w", w_int, x_int, sk, odtype=oracle.F32)
+        assert np.array_equal(got.astype(np.float64), ref.gemv64(w_int, x_int))
+    w, x = f16_normal(g, (rows, cols), 0.05), f16_normal(g, cols)
+    sc = np.abs(g.standard_normal(rows)).astype(np.float32)
+    got = oracle.split_k_gemv("f16w", w, x, 8, scales=sc)
+    want = ref.gemv64(w, x) * sc
+    assert within_ulp(got, want, ulps=1.0, exact_frac=0.9)
+    # planted: the last (shorter) slice left out
+    nchunks, q = cols // 32, -(-(cols // 32) // 8)
+    last = (nchunks // q) * q * 32
+    bad = oracle.split_k_gemv("f16w", w[:, :last], x[:last], 8, scales=sc)
+    assert not within_ulp(bad, want, ulps=1.0, exact_frac=0.9)

@@ -15,6 +15,7 @@ from pathlib import Path
 from . import build as _build
 
 F16, BF16, F32 = 0, 1, 2
+W_FP8 = 3   # weight format code of float8_e4m3fn (tt_split_k_matvec)
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -59,6 +60,12 @@ SIGNATURES: dict[str, list] = {
     "tt_int4_scaled_matvec": [_P, _L, _P, _I, _L, _L, _L, _I, _P, _I, _P, _I, _L, _L, _L, _P],
     "tt_multi_int4_scaled_matvec": [_I, _PP, _LP, _PP, _I, _LP, _LP, _L, _I, _LP, _P, _I, _P, _I, _L, _L, _P],
     "tt_scaled_matvec": [_P, _L, _P, _I, _P, _I, _P, _I, _L, _L, _P],
+    "tt_block_scaled_matvec": [_P, _L, _P, _I, _L, _L, _L, _P, _I, _P, _I, _L, _L, _P],
+    "tt_multi_scaled_matvec": [_I, _PP, _LP, _PP, _I, _LP, _LP, _P, _I, _P, _I, _L, _P],
+    "tt_split_k_matvec": [_P, _I, _L, _P, _I, _P, _I, _P, _I, _L, _L, _I, _P, _L, _P],
+    "tt_scaled_gate_up_silu": [_P, _L, _P, _L, _P, _L, _P, _L, _I, _P, _I, _P, _I, _L, _L, _P],
+    "tt_head_rms_norm": [_P, _I, _P, _I, _P, _L, _L, _F, _P],
+    "tt_qk_head_rmsnorm_rope_inplace": [_P, _P, _I, _P, _P, _I, _P, _P, _L, _L, _P, _L, _L, _L, _L, _F, _P],
     "tt_matvec": [_P, _I, _L, _P, _I, _P, _I, _L, _L, _P],
     "tt_multi_matvec": [_I, _PP, _I, _LP, _LP, _P, _I, _P, _I, _L, _P],
     "tt_mxfp4_selected_matvec": [_P, _L, _L, _P, _L, _L, _P, _I, _L, _P, _L, _P, _I, _L, _L, _L, _P],

@@ -105,6 +105,7 @@ class HipDecodeBackend:
         self._argmax_partials: torch.Tensor | None = None
         self._attention_partials: torch.Tensor | None = None
         self._batched_partials: torch.Tensor | None = None
+        self._split_k_partials: torch.Tensor | None = None   # split-K scratch (triton_kernels.py:3797-3805)
 
     # ------------------------------------------------------------ helpers
     @staticmethod
@@ -295,9 +296,23 @@ class HipDecodeBackend:
         _require_cuda(weight, scales, x, out)
         if weight.dtype != torch.float8_e4m3fn:
             raise ValueError(f"scaled_matvec supports float8_e4m3fn weights on this backend, got {weight.dtype}")
-        if scales.dim() != 1:
-            raise ValueError("scaled_matvec: block-scaled (2-D) scales are not supported by the HIP backend")
         rows, cols = int(weight.shape[0]), int(weight.shape[1])
+        if scales.dim() == 2:
+            # block-scaled branch (triton_kernels.py:4465-4497): blocks of
+            # next_pow2(ceil(cols / blocks)) columns, scale [row, block]
+            blocks = int(scales.shape[1])
+            if int(scales.shape[0]) != rows or blocks < 1 or x.numel() != cols or out.numel() != rows or \
+                    weight.stride(1) != 1:
+                raise ValueError("scaled_matvec shape mismatch")
+            block = 1 << max(0, (-(-cols // blocks) - 1).bit_length())
+            _require_cuda(weight, scales, x, out)
+            rc = self.lib.tt_block_scaled_matvec(
+                weight.data_ptr(), weight.stride(0), scales.data_ptr(), _code(scales, "fp8 scales"), scales.stride(0),
+                scales.stride(1), block, x.data_ptr(), _code(x, "scaled_matvec"), out.data_ptr(),
+                _code(out, "scaled_matvec"), rows, cols, _stream(out),
+            )
+            _lib.check(rc, "scaled_matvec")
+            return out
         if scales.numel() != rows or x.numel() != cols or out.numel() != rows or weight.stride(1) != 1:
             raise ValueError("scaled_matvec shape mismatch")
         rc = self.lib.tt_scaled_matvec(
@@ -305,6 +320,132 @@ class HipDecodeBackend:
             _code(x, "scaled_matvec"), out.data_ptr(), _code(out, "scaled_matvec"), rows, cols, _stream(out),
         )
         _lib.check(rc, "scaled_matvec")
+        return out
+
+    def multi_scaled_tensorcore_matvec(
+        self,
+        weights: tuple[torch.Tensor, ...],
+        scales: tuple[torch.Tensor, ...],
+        rows: tuple[int, ...],
+        cols: int,
+        x: torch.Tensor,
+        out: torch.Tensor,
+    ) -> torch.Tensor:
+        """Two or three fp8 matrices with per-row scales, outputs concatenated
+        (triton_kernels.py:5119-5180, kernel :1958-2071).  The reference's int8 weights are
+        not provided by this backend."""
+        if len(weights) not in {2, 3} or len(scales) != len(weights):
+            raise ValueError("multi scaled tensor-core matvec supports two or three matrices")
+        if cols % 256:
+            raise ValueError("tensor-core matvec columns must be divisible by 256")
+        dtype = weights[0].dtype
+        if dtype not in {torch.float8_e4m3fn, torch.int8}:
+            raise ValueError("tensor-core matvec requires E4M3 or INT8 weights")
+        if any(weight.dtype != dtype for weight in weights):
+            raise ValueError("multi tensor-core weights must share one dtype")
+        if dtype == torch.int8:
+            raise ValueError("multi_scaled_tensorcore_matvec: int8 weights are not supported by the HIP backend")
+        rows = tuple(int(r) for r in rows)[: len(weights)]
+        if len(rows) != len(weights) or any(int(w.shape[0]) != r or int(w.shape[1]) != cols or w.stride(1) != 1
+                                            for w, r in zip(weights, rows)):
+            raise ValueError("multi scaled matvec shape mismatch")
+        if any(sc.ndim != 1 or sc.numel() != r for sc, r in zip(scales, rows)):
+            raise ValueError("multi scaled matvec requires one scale per output row")
+        if len({sc.dtype for sc in scales}) != 1 or x.numel() != cols or out.numel() < sum(rows):
+            raise ValueError("multi scaled matvec scale/input/output mismatch")
+        _require_cuda(*weights, *scales, x, out)
+        rc = self.lib.tt_multi_scaled_matvec(
+            len(weights), _lib.ptr_array([w.data_ptr() for w in weights]), _lib.i64_array([w.stride(0) for w in weights]),
+            _lib.ptr_array([sc.data_ptr() for sc in scales]), _code(scales[0], "fp8 scales"),
+            _lib.i64_array([sc.stride(0) for sc in scales]), _lib.i64_array(rows), x.data_ptr(),
+            _code(x, "multi_scaled_tensorcore_matvec"), out.data_ptr(), _code(out, "multi_scaled_tensorcore_matvec"),
+            cols, _stream(out),
+        )
+        _lib.check(rc, "multi_scaled_tensorcore_matvec")
+        return out
+
+    def split_k_matvec(
+        self,
+        weight: torch.Tensor,
+        x: torch.Tensor,
+        out: torch.Tensor,
+        *,
+        scales: torch.Tensor | None = None,
+        split_k: int = 4,
+        block_m: int = 32,
+        block_n: int = 256,
+        num_warps: int = 4,
+    ) -> torch.Tensor:
+        """Split-K GEMV with binary32 partials and an in-order reduce
+        (triton_kernels.py:3773-3845, kernels :3023-3100).  Slices are whole 32-column
+        chunks; the tile arguments are accepted and ignored."""
+        if split_k not in {2, 4, 8}:
+            raise ValueError("split_k must be 2, 4, or 8")
+        rows = int(weight.shape[0])
+        cols = int(weight.shape[1])
+        if scales is not None and (scales.ndim != 1 or scales.numel() != rows):
+            raise ValueError("split-K scaled matvec requires one scale per output row")
+        if weight.dtype == torch.float16:
+            fmt = _lib.F16
+        elif weight.dtype == torch.bfloat16:
+            fmt = _lib.BF16
+        elif weight.dtype == torch.float8_e4m3fn:
+            fmt = _lib.W_FP8
+        else:
+            raise ValueError(f"split_k_matvec supports fp16, bf16 and float8_e4m3fn weights, got {weight.dtype}")
+        if weight.stride(1) != 1 or x.numel() != cols or out.numel() != rows or not out.is_contiguous():
+            raise ValueError("split_k_matvec shape mismatch")
+        count = split_k * rows
+        if self._split_k_partials is None or self._split_k_partials.numel() < count:
+            self._split_k_partials = torch.empty(count, device=self.device, dtype=torch.float32)
+        partials = self._split_k_partials
+        _require_cuda(weight, x, out)
+        rc = self.lib.tt_split_k_matvec(
+            weight.data_ptr(), fmt, weight.stride(0) * weight.element_size(),
+            scales.data_ptr() if scales is not None else None,
+            _code(scales, "split-K scales") if scales is not None else _lib.F32, x.data_ptr(),
+            _code(x, "split_k_matvec"), out.data_ptr(), _code(out, "split_k_matvec"), rows, cols, split_k,
+            partials.data_ptr(), partials.numel(), _stream(out),
+        )
+        _lib.check(rc, "split_k_matvec")
+        return out
+
+    def fused_scaled_gate_up_silu(
+        self,
+        gate_weight: torch.Tensor,
+        gate_scales: torch.Tensor,
+        up_weight: torch.Tensor,
+        up_scales: torch.Tensor,
+        x: torch.Tensor,
+        out: torch.Tensor,
+        *,
+        block_m: int | None = None,
+        num_warps: int | None = None,
+    ) -> torch.Tensor:
+        """silu(bf16(W_g x * s_g)) * bf16(W_u x * s_u) in one launch
+        (triton_kernels.py:4346-4436, kernels :3243-3350)."""
+        if gate_scales.ndim != 1 or up_scales.ndim != 1:
+            raise ValueError("fused scaled gate/up requires one scale per output row")
+        rows = int(gate_weight.shape[0])
+        cols = int(gate_weight.shape[1])
+        if tuple(up_weight.shape) != tuple(gate_weight.shape):
+            raise ValueError("fused scaled gate/up matrices must have equal shapes")
+        if gate_scales.numel() != rows or up_scales.numel() != rows:
+            raise ValueError("fused scaled gate/up scales must match matrix rows")
+        if gate_weight.dtype != torch.float8_e4m3fn or up_weight.dtype != torch.float8_e4m3fn:
+            raise ValueError("fused_scaled_gate_up_silu supports float8_e4m3fn weights on this backend")
+        if gate_scales.dtype != up_scales.dtype:
+            raise ValueError("fused scaled gate/up scales must share a dtype")
+        if gate_weight.stride(1) != 1 or up_weight.stride(1) != 1 or x.numel() != cols or out.numel() != rows:
+            raise ValueError("fused_scaled_gate_up_silu shape mismatch")
+        _require_cuda(gate_weight, gate_scales, up_weight, up_scales, x, out)
+        rc = self.lib.tt_scaled_gate_up_silu(
+            gate_weight.data_ptr(), gate_weight.stride(0), gate_scales.data_ptr(), gate_scales.stride(0),
+            up_weight.data_ptr(), up_weight.stride(0), up_scales.data_ptr(), up_scales.stride(0),
+            _code(gate_scales, "gate/up scales"), x.data_ptr(), _code(x, "fused_scaled_gate_up_silu"), out.data_ptr(),
+            _code(out, "fused_scaled_gate_up_silu"), rows, cols, _stream(out),
+        )
+        _lib.check(rc, "fused_scaled_gate_up_silu")
         return out
 
     # ------------------------------------------------------------ MoE experts
@@ -866,6 +1007,52 @@ class HipDecodeBackend:
         rc = self.lib.tt_rope_qk_inplace(q.data_ptr(), k.data_ptr(), _code(q, "rope"), cos.data_ptr(), sin.data_ptr(),
                                          table_row, table_rows, pos_dev, pos, heads, kv_heads, head_dim, _stream(q))
         _lib.check(rc, "rope_qk_inplace")
+        return q, k
+
+    def head_rms_norm(self, x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor, heads: int, head_dim: int,
+                      eps: float) -> torch.Tensor:
+        """Per-head RMSNorm (triton_kernels.py:5669-5687, kernel :2618-2634)."""
+        _require_cuda(x, weight, out)
+        if x.numel() < heads * head_dim or out.numel() < heads * head_dim or weight.numel() < head_dim:
+            raise ValueError("head_rms_norm size mismatch")
+        if not (x.is_contiguous() and out.is_contiguous() and weight.is_contiguous()):
+            raise ValueError("head_rms_norm tensors must be contiguous")
+        rc = self.lib.tt_head_rms_norm(x.data_ptr(), _code(x, "head_rms_norm"), weight.data_ptr(),
+                                       _code(weight, "head_rms_norm"), out.data_ptr(), heads, head_dim, float(eps),
+                                       _stream(x))
+        _lib.check(rc, "head_rms_norm")
+        return out
+
+    def qk_head_rmsnorm_rope_inplace(self, q: torch.Tensor, k: torch.Tensor, q_weight: torch.Tensor,
+                                     k_weight: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, heads: int,
+                                     kv_heads: int, head_dim: int, eps: float, *,
+                                     position: torch.Tensor | int | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+        """Per-head RMSNorm of q and k followed by RoPE, in place (triton_kernels.py:
+        5716-5749, kernel :2691-2757).  ``cos``/``sin`` are the current row or a table
+        indexed by ``position``, as in ``rope_qk_inplace``."""
+        if head_dim % 2:
+            raise ValueError(f"RoPE head_dim must be even, got {head_dim}")
+        if q_weight.numel() != head_dim or k_weight.numel() != head_dim:
+            raise ValueError("fused Q/K RMSNorm requires one weight per head channel")
+        if q_weight.dtype != k_weight.dtype:
+            raise ValueError("fused Q/K RMSNorm weights must share a dtype")
+        _require_cuda(q, k, q_weight, k_weight, cos, sin)
+        if cos.ndim == 1:
+            table_row, table_rows, pos_dev, pos = 0, 1, None, 0
+        else:
+            table_row, table_rows = cos.stride(0), int(cos.shape[0])
+            if isinstance(position, torch.Tensor):
+                if position.dtype != torch.int32:
+                    raise ValueError("device position must be int32")
+                pos_dev, pos = position.data_ptr(), 0
+            else:
+                pos_dev, pos = None, int(position or 0)
+        rc = self.lib.tt_qk_head_rmsnorm_rope_inplace(
+            q.data_ptr(), k.data_ptr(), _code(q, "qk_head_rmsnorm_rope_inplace"), q_weight.data_ptr(),
+            k_weight.data_ptr(), _code(q_weight, "qk norm weights"), cos.data_ptr(), sin.data_ptr(), table_row,
+            table_rows, pos_dev, pos, heads, kv_heads, head_dim, float(eps), _stream(q),
+        )
+        _lib.check(rc, "qk_head_rmsnorm_rope_inplace")
         return q, k
 
     # ------------------------------------------------------------ attention

@@ -80,6 +80,7 @@ struct GemvParams {
   int64_t w_expert;        // bytes between experts
   int64_t s_expert;        // scale elements between experts
   int64_t out_slot;        // output elements between slots
+  int64_t w_slot;          // bytes between slots without expert ids (split-K column slices)
   int64_t s_pair;          // affine: element offset of the second scale value
   int aff_zero;            // affine pair holds (s, z) instead of (s, m)
   int cols;
@@ -188,7 +189,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
   using Data = GemvData<F, ST, ROWS, NVG>;
 
   const int slot = blockIdx.y;
-  int64_t woff = 0, soff = 0;
+  int64_t woff = (int64_t)slot * P.w_slot, soff = 0;
   if (P.experts != nullptr) {
     const int64_t e = P.experts[slot];
     woff = e * P.w_expert;
@@ -477,7 +478,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
           } else {
             t = p[k] * sk;
           }
-          const bool ok = cv && (bt.lr0 + grow[k] < bt.rows);
+          // a group counts when its first chunk is in range (ragged last group)
+          const bool ok = ((j & ~(LG - 1)) < nchunks) && (bt.lr0 + grow[k] < bt.rows);
           acc[k] = acc[k] + (ok ? t : 0.0f);
         }
       }

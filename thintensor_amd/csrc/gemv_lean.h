@@ -206,7 +206,10 @@ __global__ __launch_bounds__(256) void lean_gemv_kernel(const LeanParams P) {
         } else {
           t = p[k] * sk;
         }
-        acc[k] = acc[k] + ((cv && sv[k]) ? t : 0.0f);
+        // a group counts when its first chunk is in range (a ragged last group of a
+        // block-scaled matrix keeps its partial sum on every lane of the group)
+        const bool gv = (j & ~(LG - 1)) < nchunks;
+        acc[k] = acc[k] + ((gv && sv[k]) ? t : 0.0f);
       }
     }
   };

@@ -179,6 +179,88 @@ __global__ void rope_kernel(void* q, void* k, const void* cos_t, const void* sin
   store<T>(base + i + half, o2);
 }
 
+// ---------------------------------------------------------------- per-head RMSNorm
+// One wave per head (head_dim <= 512): lane l holds elements l, l + 64, ...; the sum of
+// squares is an fma chain per lane in that order, then the 64-lane xor butterfly;
+// out = (x * (1 / sqrt(sum / head_dim + eps))) * w (triton_kernels.py:2618-2634).
+constexpr int kHeadHeld = 8;
+
+template <typename T, typename WT>
+__global__ __launch_bounds__(256) void head_rms_norm_kernel(const void* x, const void* w, void* out, int heads, int D,
+                                                            float eps) {
+  const int head = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (head >= heads) return;   // whole waves
+  const T* xh = reinterpret_cast<const T*>(x) + (int64_t)head * D;
+  float v[kHeadHeld];
+  float s = 0.0f;
+#pragma unroll
+  for (int k = 0; k < kHeadHeld; k++) {
+    const int i = lane + 64 * k;
+    v[k] = i < D ? to_f32(xh[i]) : 0.0f;
+    if (i < D) s = __builtin_fmaf(v[k], v[k], s);
+  }
+  s = xor_sum(s, 1, 64);
+  const float inv = 1.0f / __builtin_sqrtf(s / (float)D + eps);
+  T* oh = reinterpret_cast<T*>(out) + (int64_t)head * D;
+#pragma unroll
+  for (int k = 0; k < kHeadHeld; k++) {
+    const int i = lane + 64 * k;
+    if (i < D) store<T>(oh + i, (v[k] * inv) * ld<WT>(w, i));
+  }
+}
+
+// Per-head RMSNorm then RoPE, in place on q heads then k heads (triton_kernels.py:
+// 2691-2757): one wave per head, lane l holds the pairs (i, i + half) for i = l, l + 64,
+// ...; sum of squares per lane: fma(a, a, .) then fma(b, b, .) per pair, then the 64-lane
+// butterfly; a' = a * (inv * w[i]), b' = b * (inv * w[i + half]); the rotation is binary32
+// (a' c - b' s, b' c + a' s, cos/sin read from the activation-dtype table), rounded once
+// by the store.
+constexpr int kPairHeld = 4;
+
+template <typename T, typename WT>
+__global__ __launch_bounds__(256) void qk_head_norm_rope_kernel(void* q, void* k, const void* qw, const void* kw,
+                                                                const void* cos_t, const void* sin_t,
+                                                                int64_t table_row, int64_t table_rows,
+                                                                const int32_t* pos_dev, int pos, int heads,
+                                                                int kv_heads, int D, float eps) {
+  const int hh = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (hh >= heads + kv_heads) return;   // whole waves
+  const int64_t p = pos_dev ? (int64_t)pos_dev[0] : (int64_t)pos;
+  if (p < 0 || p >= table_rows) return;
+  const bool is_q = hh < heads;
+  T* base = is_q ? reinterpret_cast<T*>(q) + (int64_t)hh * D : reinterpret_cast<T*>(k) + (int64_t)(hh - heads) * D;
+  const void* w = is_q ? qw : kw;
+  const int half = D >> 1;
+  float a[kPairHeld], b[kPairHeld];
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < kPairHeld; j++) {
+    const int i = lane + 64 * j;
+    const bool ok = i < half;
+    a[j] = ok ? to_f32(base[i]) : 0.0f;
+    b[j] = ok ? to_f32(base[i + half]) : 0.0f;
+    if (ok) {
+      s = __builtin_fmaf(a[j], a[j], s);
+      s = __builtin_fmaf(b[j], b[j], s);
+    }
+  }
+  s = xor_sum(s, 1, 64);
+  const float inv = 1.0f / __builtin_sqrtf(s / (float)D + eps);
+#pragma unroll
+  for (int j = 0; j < kPairHeld; j++) {
+    const int i = lane + 64 * j;
+    if (i < half) {
+      const float an = a[j] * (inv * ld<WT>(w, i));
+      const float bn = b[j] * (inv * ld<WT>(w, i + half));
+      const float c = ld<T>(cos_t, p * table_row + i), sn = ld<T>(sin_t, p * table_row + i);
+      store<T>(base + i, an * c - bn * sn);
+      store<T>(base + i + half, bn * c + an * sn);
+    }
+  }
+}
+
 // ---------------------------------------------------------------- embedding / KV
 // out = embed[token] (row copy), token read from device memory when token_dev is set.
 __global__ void embed_kernel(const uint16_t* embed, int64_t row, int64_t vocab, const int64_t* token_dev, int64_t token,
@@ -326,6 +408,45 @@ extern "C" int tt_rope_qk_inplace(void* q, void* k, int dtype, const void* cos_t
                        cos_table, sin_table, table_row, table_rows, position_dev, (int)position, (int)heads, (int)kv_heads,
                        (int)head_dim);
     return check_launch("rope_qk_inplace");
+  });
+}
+
+extern "C" int tt_head_rms_norm(const void* x, int dtype, const void* weight, int w_dtype, void* out, int64_t heads,
+                                int64_t head_dim, float eps, void* stream) {
+  TT_REQUIRE(x && weight && out && heads > 0, "head_rms_norm: bad arguments");
+  TT_UNSUPPORTED(head_dim > 0 && head_dim <= 64 * kHeadHeld, "head_rms_norm: head_dim up to %d", 64 * kHeadHeld);
+  return with_act(dtype, [&](auto t) {
+    using T = decltype(t);
+    return with_any(w_dtype, [&](auto wt) {
+      using WT = decltype(wt);
+      hipLaunchKernelGGL((head_rms_norm_kernel<T, WT>), dim3((unsigned)((heads + 3) / 4)), dim3(256), 0,
+                         static_cast<hipStream_t>(stream), x, weight, out, (int)heads, (int)head_dim, eps);
+      return check_launch("head_rms_norm");
+    });
+  });
+}
+
+extern "C" int tt_qk_head_rmsnorm_rope_inplace(void* q, void* k, int dtype, const void* q_weight, const void* k_weight,
+                                               int w_dtype, const void* cos_table, const void* sin_table,
+                                               int64_t table_row, int64_t table_rows, const int32_t* position_dev,
+                                               int64_t position, int64_t heads, int64_t kv_heads, int64_t head_dim,
+                                               float eps, void* stream) {
+  const char* what = "qk_head_rmsnorm_rope_inplace";
+  TT_REQUIRE(q && k && q_weight && k_weight && cos_table && sin_table, "%s: null pointer", what);
+  TT_REQUIRE(head_dim > 0 && head_dim % 2 == 0, "%s: RoPE head_dim must be even, got %lld", what, (long long)head_dim);
+  TT_UNSUPPORTED(head_dim <= 128 * kPairHeld, "%s: head_dim up to %d", what, 128 * kPairHeld);
+  TT_REQUIRE(heads > 0 && kv_heads >= 0, "%s: bad head counts", what);
+  TT_REQUIRE(table_rows > 0 && (position_dev != nullptr || (position >= 0 && position < table_rows)),
+             "%s: position outside the cos/sin table", what);
+  return with_act(dtype, [&](auto t) {
+    using T = decltype(t);
+    return with_any(w_dtype, [&](auto wt) {
+      using WT = decltype(wt);
+      hipLaunchKernelGGL((qk_head_norm_rope_kernel<T, WT>), dim3((unsigned)((heads + kv_heads + 3) / 4)), dim3(256), 0,
+                         static_cast<hipStream_t>(stream), q, k, q_weight, k_weight, cos_table, sin_table, table_row,
+                         table_rows, position_dev, (int)position, (int)heads, (int)kv_heads, (int)head_dim, eps);
+      return check_launch(what);
+    });
   });
 }
 
