@@ -557,6 +557,15 @@ int tt_fused_lm_head_argmax(const tt_fused_gemv* desc, uint64_t* partials, int64
                             int64_t* out_idx, float* out_val, int32_t* position, const int32_t* base,
                             int64_t* history, int32_t history_len, void* stream);
 
+/* Memory-floor reference (measurement utility; no counterpart in the reference): a
+ * pure streaming read of `bytes` (a multiple of 16) in contiguous spans of bytes_per_wave
+ * (a multiple of 2048) per wave, one 32-bit word stored per wave into `out`
+ * (tt_stream_read_waves(bytes, bytes_per_wave) words).  Used to time the fastest
+ * single launch that moves a given number of bytes. */
+int64_t tt_stream_read_waves(int64_t bytes, int64_t bytes_per_wave);
+int tt_stream_read(const void* data, int64_t bytes, int64_t bytes_per_wave, void* out, int64_t out_words,
+                   void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -113,8 +113,11 @@ SIGNATURES: dict[str, list] = {
     "tt_fused_struct_sizes": [_LP, _LP],
     "tt_fused_gemv_run": [_FGP, _P],
     "tt_fused_lm_head_argmax": [_FGP, _P, _L, _P, _P, _P, _P, _P, ctypes.c_int32, _P],
+    "tt_stream_read_waves": [_L, _L],
+    "tt_stream_read": [_P, _L, _L, _P, _L, _P],
 }
 _RESTYPES = {"tt_last_error": ctypes.c_char_p, "tt_matvec_argmax_partials": ctypes.c_int64,
+             "tt_stream_read_waves": ctypes.c_int64,
              "tt_matvec_argmax_batched_partials": ctypes.c_int64}
 
 _lock = threading.Lock()
