@@ -382,16 +382,17 @@ static float block_sum256(const float* part) {
   return (w[0] + w[1]) + (w[2] + w[3]);
 }
 
+/* The kernels' RMSNorm partition: pieces of 8 elements, piece p to thread p % 256; a
+ * thread's sum of squares is an fma chain over its elements in increasing index order. */
+#define TTO_PIECE_OWNER(i) ((int)(((i) / 8) % 256))
+
 /* RMSNorm (triton_kernels.py:2562-2577): out = (x * inv) * (w + offset). */
 int tto_rms_norm(const void* x, int xdt, const void* w, int wdt, void* out, int odt, int n, float eps, float offset) {
   float part[256];
-  for (int t = 0; t < 256; t++) {
-    float s = 0.0f;
-    for (int i = t; i < n; i += 256) {
-      const float v = act_get(x, xdt, i);
-      s = fmaf(v, v, s);
-    }
-    part[t] = s;
+  for (int t = 0; t < 256; t++) part[t] = 0.0f;
+  for (int i = 0; i < n; i++) {
+    const float v = act_get(x, xdt, i);
+    part[TTO_PIECE_OWNER(i)] = fmaf(v, v, part[TTO_PIECE_OWNER(i)]);
   }
   const float total = block_sum256(part);
   const float inv = 1.0f / sqrtf(total / (float)n + eps);
@@ -403,13 +404,10 @@ int tto_rms_norm(const void* x, int xdt, const void* w, int wdt, void* out, int 
 int tto_add_rms_norm(const void* l, const void* r, void* res_out, int xdt, const void* w, int wdt, void* out, int odt,
                      int n, float eps) {
   float part[256];
-  for (int t = 0; t < 256; t++) {
-    float s = 0.0f;
-    for (int i = t; i < n; i += 256) {
-      const float v = tto_round_bf16(act_get(l, xdt, i) + act_get(r, xdt, i));
-      s = fmaf(v, v, s);
-    }
-    part[t] = s;
+  for (int t = 0; t < 256; t++) part[t] = 0.0f;
+  for (int i = 0; i < n; i++) {
+    const float v = tto_round_bf16(act_get(l, xdt, i) + act_get(r, xdt, i));
+    part[TTO_PIECE_OWNER(i)] = fmaf(v, v, part[TTO_PIECE_OWNER(i)]);
   }
   const float total = block_sum256(part);
   const float inv = 1.0f / sqrtf(total / (float)n + eps);

@@ -127,11 +127,12 @@ __global__ __launch_bounds__(256) void fused_lean_kernel(const LeanFused P) {
     }
   };
   // ---- the prologue's inputs are requested before round 0 of the weights, so that
-  // waiting for them never waits for the weight stream
+  // waiting for them never waits for the weight stream: one 16-byte piece of each vector
+  // per held piece (cols <= 4096, a multiple of 32; indices past the last piece repeat it)
   __shared__ float red[4];
   const int n = cols;
-  constexpr int kHeld = 16;   // prologue elements per thread (cols <= 4096)
-  uint16_t ra[kHeld], rb[kHeld], rw[kHeld];
+  const int np = n >> 3;
+  uint4 qa[kNormPieces], qb[kNormPieces], qw[kNormPieces];
   if constexpr (PRO != Pro::kLoad) {
     const uint16_t* pa;
     if constexpr (PRO == Pro::kEmbedNorm) {
@@ -142,14 +143,13 @@ __global__ __launch_bounds__(256) void fused_lean_kernel(const LeanFused P) {
       pa = reinterpret_cast<const uint16_t*>(P.left) + tok * P.token_x;
     }
     const uint16_t* pb = reinterpret_cast<const uint16_t*>(P.right) + tok * P.token_x;
-    const uint16_t* pw = reinterpret_cast<const uint16_t*>(P.norm_w);
 #pragma unroll
-    for (int k = 0; k < kHeld; k++) {
-      const int i = threadIdx.x + 256 * k;
-      const int ic = i < n ? i : n - 1;
-      ra[k] = pa[ic];
-      if constexpr (PRO != Pro::kEmbedNorm) rb[k] = pb[ic];
-      rw[k] = pw[ic];
+    for (int k = 0; k < kNormPieces; k++) {
+      const int pi = (int)threadIdx.x + 256 * k;
+      const int pc = pi < np ? pi : np - 1;
+      qa[k] = reinterpret_cast<const uint4*>(pa)[pc];
+      if constexpr (PRO != Pro::kEmbedNorm) qb[k] = reinterpret_cast<const uint4*>(pb)[pc];
+      qw[k] = reinterpret_cast<const uint4*>(P.norm_w)[pc];
     }
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -164,32 +164,40 @@ __global__ __launch_bounds__(256) void fused_lean_kernel(const LeanFused P) {
       reinterpret_cast<uint4*>(xs_lds)[idx] = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(P.x) +
                                                                              tok * P.token_x)[idx];
   } else {
-    // RMSNorm of the residual stream with the thread partition, reduction order and
+    // RMSNorm of the residual stream in the piece partition, reduction order and
     // rounding points of the standalone rms_norm / add_rms_norm kernels; workgroup 0
     // stores the residual.
     const bool writer = blockIdx.x == 0 && P.residual_out != nullptr;
-    XT* xl = reinterpret_cast<XT*>(xs_lds);
-    float rr[kHeld];
+    const int t = threadIdx.x;
+    float rr[kNormPieces][8];
     float ss = 0.0f;
 #pragma unroll
-    for (int k = 0; k < kHeld; k++) {
-      const float a = to_f32(XT{ra[k]});
-      float r;
-      if constexpr (PRO == Pro::kAddNorm) r = round_bf16(a + to_f32(XT{rb[k]}));
-      else if constexpr (PRO == Pro::kAddRmsNorm) r = round_to<XT>(a + to_f32(XT{rb[k]}));
-      else r = a;
-      rr[k] = r;
-      if (threadIdx.x + 256 * k < n) ss = __builtin_fmaf(r, r, ss);
-    }
+    for (int k = 0; k < kNormPieces; k++)
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const float a = piece_f32<XT>(qa[k], e);
+        float r;
+        if constexpr (PRO == Pro::kAddNorm) r = round_bf16(a + piece_f32<XT>(qb[k], e));
+        else if constexpr (PRO == Pro::kAddRmsNorm) r = round_to<XT>(a + piece_f32<XT>(qb[k], e));
+        else r = a;
+        rr[k][e] = r;
+        if (8 * (t + 256 * k) + e < n) ss = __builtin_fmaf(r, r, ss);
+      }
     const float total = block_sum256(ss, red);
     const float inv = 1.0f / __builtin_sqrtf(total / (float)n + P.eps);
 #pragma unroll
-    for (int k = 0; k < kHeld; k++) {
-      const int i = threadIdx.x + 256 * k;
-      if (i < n) {
-        const float w = to_f32(XT{rw[k]});
-        if (writer) store<XT>(reinterpret_cast<XT*>(P.residual_out) + tok * P.token_x + i, rr[k]);
-        store<XT>(xl + i, PRO == Pro::kAddNorm ? (rr[k] * inv) * w : (rr[k] * inv) * (w + 0.0f));
+    for (int k = 0; k < kNormPieces; k++) {
+      const int pi = t + 256 * k;
+      if (pi < np) {
+        float o[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          const float w = piece_f32<XT>(qw[k], e);
+          o[e] = PRO == Pro::kAddNorm ? (rr[k][e] * inv) * w : (rr[k][e] * inv) * (w + 0.0f);
+        }
+        if (writer)
+          reinterpret_cast<uint4*>(reinterpret_cast<XT*>(P.residual_out) + tok * P.token_x)[pi] = pack_piece<XT>(rr[k]);
+        reinterpret_cast<uint4*>(xs_lds)[pi] = pack_piece<XT>(o);
       }
     }
   }
@@ -431,10 +439,16 @@ int validate(const tt_fused_gemv* d, bool lm_head) {
     case TT_PRO_ADD_RMS_NORM:
       TT_REQUIRE(d->left && d->right && d->norm_weight, "%s: add+norm prologue needs left, right and the weight",
                  kWhat);
+      TT_REQUIRE(aligned(d->left, 16) && aligned(d->right, 16) && aligned(d->norm_weight, 16),
+                 "%s: the norm prologue reads 16-byte pieces: left, right and the weight must be 16-byte aligned",
+                 kWhat);
       break;
     case TT_PRO_EMBED_NORM:
       TT_REQUIRE(d->embed && d->token && d->norm_weight && d->vocab > 0 && d->embed_row >= d->cols,
                  "%s: embedding prologue needs the table, the device token and the weight", kWhat);
+      TT_REQUIRE(aligned(d->embed, 16) && d->embed_row % 8 == 0 && aligned(d->norm_weight, 16),
+                 "%s: the norm prologue reads 16-byte pieces: embedding rows and the weight must be 16-byte aligned",
+                 kWhat);
       break;
     default:
       TT_REQUIRE(false, "%s: unknown prologue %d", kWhat, d->prologue);

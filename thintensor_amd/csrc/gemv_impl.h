@@ -305,13 +305,13 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
     }
   }
 
-  // The RMSNorm prologue's inputs (cols <= 256 * kHeld) are requested here too, ahead of
-  // the weights, as raw bits: indices past cols clamp to cols - 1 (values discarded), so
-  // no branch separates the loads and waiting for them never waits for the weight stream.
-  constexpr int kHeld = 16;   // prologue elements per thread kept in registers
-  uint16_t ra[kHeld], rb[kHeld], rw[kHeld];
+  // The RMSNorm prologue's inputs (cols <= 4096, in the piece partition of tt_common.h)
+  // are requested here too, ahead of the weights, as raw 16-byte pieces: indices past the
+  // last piece repeat it (values discarded), so no branch separates the loads and waiting
+  // for them never waits for the weight stream.
+  uint4 qa[kNormPieces], qb[kNormPieces], qw[kNormPieces];
   if constexpr (PRO != Pro::kLoad) {
-    const int n = P.cols;
+    const int np = P.cols >> 3;
     const uint16_t* pa;
     if constexpr (PRO == Pro::kEmbedNorm) {
       int64_t t = P.f.token[0];
@@ -320,15 +320,13 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
     } else {
       pa = reinterpret_cast<const uint16_t*>(P.f.left);
     }
-    const uint16_t* pb = reinterpret_cast<const uint16_t*>(P.f.right);
-    const uint16_t* pw = reinterpret_cast<const uint16_t*>(P.f.norm_w);
 #pragma unroll
-    for (int k = 0; k < kHeld; k++) {
-      const int i = threadIdx.x + 256 * k;
-      const int ic = i < n ? i : n - 1;
-      ra[k] = pa[ic];
-      if constexpr (PRO != Pro::kEmbedNorm) rb[k] = pb[ic];
-      rw[k] = pw[ic];
+    for (int k = 0; k < kNormPieces; k++) {
+      const int pi = (int)threadIdx.x + 256 * k;
+      const int pc = pi < np ? pi : np - 1;
+      qa[k] = reinterpret_cast<const uint4*>(pa)[pc];
+      if constexpr (PRO != Pro::kEmbedNorm) qb[k] = reinterpret_cast<const uint4*>(P.f.right)[pc];
+      qw[k] = reinterpret_cast<const uint4*>(P.f.norm_w)[pc];
     }
     __builtin_amdgcn_sched_barrier(0);   // raw bits only above: no use between the loads
   }
@@ -381,47 +379,52 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
       if constexpr (PRO == Pro::kAddNorm) return (r * inv) * w;
       else return (r * inv) * (w + 0.0f);
     };
-    if (n <= 256 * kHeld) {
-      // one pass over memory: the raw bits requested before the weights
-      float rr[kHeld], wn[kHeld];
-#pragma unroll
-      for (int k = 0; k < kHeld; k++) {
-        const bool in = threadIdx.x + 256 * k < n;
-        const float a = to_f32(XT{ra[k]});
-        float r;
-        if constexpr (PRO == Pro::kAddNorm) r = round_bf16(a + to_f32(XT{rb[k]}));
-        else if constexpr (PRO == Pro::kAddRmsNorm) r = round_to<XT>(a + to_f32(XT{rb[k]}));
-        else r = a;
-        rr[k] = in ? r : 0.0f;
-        wn[k] = in ? to_f32(XT{rw[k]}) : 0.0f;
-      }
+    const int np = n >> 3;
+    const int t = threadIdx.x;
+    if (np <= 256 * kNormPieces) {
+      // one pass over memory: the raw pieces requested before the weights
+      float rr[kNormPieces][8];
       float ss = 0.0f;
 #pragma unroll
-      for (int k = 0; k < kHeld; k++)
-        if (threadIdx.x + 256 * k < n) ss = __builtin_fmaf(rr[k], rr[k], ss);
+      for (int k = 0; k < kNormPieces; k++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          const float a = piece_f32<XT>(qa[k], e);
+          float r;
+          if constexpr (PRO == Pro::kAddNorm) r = round_bf16(a + piece_f32<XT>(qb[k], e));
+          else if constexpr (PRO == Pro::kAddRmsNorm) r = round_to<XT>(a + piece_f32<XT>(qb[k], e));
+          else r = a;
+          rr[k][e] = r;
+          if (8 * (t + 256 * k) + e < n) ss = __builtin_fmaf(r, r, ss);
+        }
       const float total = block_sum256(ss, red);
       const float inv = 1.0f / __builtin_sqrtf(total / (float)n + P.f.eps);
 #pragma unroll
-      for (int k = 0; k < kHeld; k++) {
-        const int i = threadIdx.x + 256 * k;
-        if (i < n) {
-          if (writer) store<XT>(reinterpret_cast<XT*>(P.f.residual_out) + i, rr[k]);
-          store<XT>(xl + i, normed(rr[k], inv, wn[k]));
+      for (int k = 0; k < kNormPieces; k++) {
+        const int pi = t + 256 * k;
+        if (pi < np) {
+          float o[8];
+#pragma unroll
+          for (int e = 0; e < 8; e++) o[e] = normed(rr[k][e], inv, piece_f32<XT>(qw[k], e));
+          if (writer) reinterpret_cast<uint4*>(P.f.residual_out)[pi] = pack_piece<XT>(rr[k]);
+          reinterpret_cast<uint4*>(xs_lds)[pi] = pack_piece<XT>(o);
         }
       }
     } else {
       float ss = 0.0f;
-      for (int i = threadIdx.x; i < n; i += 256) {
-        const float r = resid(i);
-        ss = __builtin_fmaf(r, r, ss);
-      }
+      for (int pi = t; pi < np; pi += 256)
+        for (int i = 8 * pi; i < 8 * pi + 8; i++) {
+          const float r = resid(i);
+          ss = __builtin_fmaf(r, r, ss);
+        }
       const float total = block_sum256(ss, red);
       const float inv = 1.0f / __builtin_sqrtf(total / (float)n + P.f.eps);
-      for (int i = threadIdx.x; i < n; i += 256) {
-        const float r = resid(i);
-        if (writer) store<XT>(reinterpret_cast<XT*>(P.f.residual_out) + i, r);
-        store<XT>(xl + i, normed(r, inv, ld<XT>(P.f.norm_w, i)));
-      }
+      for (int pi = t; pi < np; pi += 256)
+        for (int i = 8 * pi; i < 8 * pi + 8; i++) {
+          const float r = resid(i);
+          if (writer) store<XT>(reinterpret_cast<XT*>(P.f.residual_out) + i, r);
+          store<XT>(xl + i, normed(r, inv, ld<XT>(P.f.norm_w, i)));
+        }
     }
     __syncthreads();
   }

@@ -11,103 +11,122 @@
 namespace tt {
 
 // ---------------------------------------------------------------- RMSNorm
-// out_i = (x_i * (1 / sqrt(mean(x^2) + eps))) * (w_i + offset); sum of squares per
-// thread is an fma chain over elements t, t+256, ... (triton_kernels.py:2562-2577).
-// Vectors of up to kNormHeld * 256 elements are held in registers: every load is issued
-// before the first one is used (indices past n clamp to n - 1, their values discarded),
-// so the kernel waits for memory once instead of once per element.
-constexpr int kNormHeld = 16;
+// out_i = (x_i * (1 / sqrt(mean(x^2) + eps))) * (w_i + offset) (triton_kernels.py:
+// 2562-2577), add_rms_norm with the residual rounded through bfloat16 (:2581-2614).  The
+// sum of squares follows the piece partition of tt_common.h (8-element pieces, piece p to
+// thread p % 256).  With whole aligned pieces (vec) a thread holds its pieces in
+// registers, every load issued before the first use; otherwise it reads element by
+// element in the same partition.
 
 template <typename XT, typename WT, typename OT>
 __global__ __launch_bounds__(256) void rms_norm_kernel(const void* x, const void* w, void* out, int n, float eps,
-                                                       float offset) {
+                                                       float offset, int vec) {
   __shared__ float red[4];
-  if (n <= 256 * kNormHeld) {
-    XT xr[kNormHeld];
-    WT wr[kNormHeld];
+  const int np = (n + 7) >> 3;
+  const int t = threadIdx.x;
+  if (vec && np <= 256 * kNormPieces) {
+    uint4 xr[kNormPieces];
 #pragma unroll
-    for (int k = 0; k < kNormHeld; k++) {
-      const int i = threadIdx.x + 256 * k;
-      const int ic = i < n ? i : n - 1;
-      xr[k] = reinterpret_cast<const XT*>(x)[ic];
-      wr[k] = reinterpret_cast<const WT*>(w)[ic];
+    for (int k = 0; k < kNormPieces; k++) {
+      const int p = t + 256 * k;
+      xr[k] = reinterpret_cast<const uint4*>(x)[p < np ? p : np - 1];
     }
     __builtin_amdgcn_sched_barrier(0);
     float s = 0.0f;
 #pragma unroll
-    for (int k = 0; k < kNormHeld; k++) {
-      const float v = to_f32(xr[k]);
-      if (threadIdx.x + 256 * k < n) s = __builtin_fmaf(v, v, s);
-    }
+    for (int k = 0; k < kNormPieces; k++)
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const float v = piece_f32<XT>(xr[k], e);
+        if (8 * (t + 256 * k) + e < n) s = __builtin_fmaf(v, v, s);
+      }
     const float total = block_sum256(s, red);
     const float inv = 1.0f / __builtin_sqrtf(total / (float)n + eps);
 #pragma unroll
-    for (int k = 0; k < kNormHeld; k++) {
-      const int i = threadIdx.x + 256 * k;
-      if (i < n) store<OT>(reinterpret_cast<OT*>(out) + i, (to_f32(xr[k]) * inv) * (to_f32(wr[k]) + offset));
-    }
-    return;
-  }
-  float s = 0.0f;
-  for (int i = threadIdx.x; i < n; i += 256) {
-    const float v = ld<XT>(x, i);
-    s = __builtin_fmaf(v, v, s);
-  }
-  const float total = block_sum256(s, red);
-  const float inv = 1.0f / __builtin_sqrtf(total / (float)n + eps);
-  for (int i = threadIdx.x; i < n; i += 256)
-    store<OT>(reinterpret_cast<OT*>(out) + i, (ld<XT>(x, i) * inv) * (ld<WT>(w, i) + offset));
-}
-
-// residual = bf16(left + right) stored to residual_out; out = (r * inv) * w with the
-// RMS taken over the rounded residual (triton_kernels.py:2581-2614).
-template <typename XT, typename WT, typename OT>
-__global__ __launch_bounds__(256) void add_rms_norm_kernel(const void* left, const void* right, void* residual_out,
-                                                           const void* w, void* out, int n, float eps) {
-  __shared__ float red[4];
-  if (n <= 256 * kNormHeld) {
-    XT lr[kNormHeld], rr[kNormHeld];
-    WT wr[kNormHeld];
+    for (int k = 0; k < kNormPieces; k++) {
+      const int p = t + 256 * k;
+      if (p < np) {
 #pragma unroll
-    for (int k = 0; k < kNormHeld; k++) {
-      const int i = threadIdx.x + 256 * k;
-      const int ic = i < n ? i : n - 1;
-      lr[k] = reinterpret_cast<const XT*>(left)[ic];
-      rr[k] = reinterpret_cast<const XT*>(right)[ic];
-      wr[k] = reinterpret_cast<const WT*>(w)[ic];
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    float res[kNormHeld];
-    float s = 0.0f;
-#pragma unroll
-    for (int k = 0; k < kNormHeld; k++) {
-      res[k] = round_bf16(to_f32(lr[k]) + to_f32(rr[k]));
-      if (threadIdx.x + 256 * k < n) s = __builtin_fmaf(res[k], res[k], s);
-    }
-    const float total = block_sum256(s, red);
-    const float inv = 1.0f / __builtin_sqrtf(total / (float)n + eps);
-#pragma unroll
-    for (int k = 0; k < kNormHeld; k++) {
-      const int i = threadIdx.x + 256 * k;
-      if (i < n) {
-        store<XT>(reinterpret_cast<XT*>(residual_out) + i, res[k]);
-        store<OT>(reinterpret_cast<OT*>(out) + i, (res[k] * inv) * to_f32(wr[k]));
+        for (int e = 0; e < 8; e++) {
+          const int i = 8 * p + e;
+          if (i < n) store<OT>(reinterpret_cast<OT*>(out) + i, (piece_f32<XT>(xr[k], e) * inv) * (ld<WT>(w, i) + offset));
+        }
       }
     }
     return;
   }
   float s = 0.0f;
-  for (int i = threadIdx.x; i < n; i += 256) {
-    const float r = norm_residual<XT>(left, right, i);
-    s = __builtin_fmaf(r, r, s);
-  }
+  for (int p = t; p < np; p += 256)
+    for (int i = 8 * p; i < 8 * p + 8 && i < n; i++) {
+      const float v = ld<XT>(x, i);
+      s = __builtin_fmaf(v, v, s);
+    }
   const float total = block_sum256(s, red);
   const float inv = 1.0f / __builtin_sqrtf(total / (float)n + eps);
-  for (int i = threadIdx.x; i < n; i += 256) {
-    const float r = norm_residual<XT>(left, right, i);
-    store<XT>(reinterpret_cast<XT*>(residual_out) + i, r);
-    store<OT>(reinterpret_cast<OT*>(out) + i, (r * inv) * ld<WT>(w, i));
+  for (int p = t; p < np; p += 256)
+    for (int i = 8 * p; i < 8 * p + 8 && i < n; i++)
+      store<OT>(reinterpret_cast<OT*>(out) + i, (ld<XT>(x, i) * inv) * (ld<WT>(w, i) + offset));
+}
+
+// residual = bf16(left + right) (stored in the activation dtype); the RMS is taken over
+// the rounded residual.
+template <typename XT, typename WT, typename OT>
+__global__ __launch_bounds__(256) void add_rms_norm_kernel(const void* left, const void* right, void* residual_out,
+                                                           const void* w, void* out, int n, float eps, int vec) {
+  __shared__ float red[4];
+  const int np = (n + 7) >> 3;
+  const int t = threadIdx.x;
+  if (vec && np <= 256 * kNormPieces) {
+    uint4 lr[kNormPieces], rr[kNormPieces];
+#pragma unroll
+    for (int k = 0; k < kNormPieces; k++) {
+      const int p = t + 256 * k;
+      const int pc = p < np ? p : np - 1;
+      lr[k] = reinterpret_cast<const uint4*>(left)[pc];
+      rr[k] = reinterpret_cast<const uint4*>(right)[pc];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float res[kNormPieces][8];
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kNormPieces; k++)
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        res[k][e] = round_bf16(piece_f32<XT>(lr[k], e) + piece_f32<XT>(rr[k], e));
+        if (8 * (t + 256 * k) + e < n) s = __builtin_fmaf(res[k][e], res[k][e], s);
+      }
+    const float total = block_sum256(s, red);
+    const float inv = 1.0f / __builtin_sqrtf(total / (float)n + eps);
+#pragma unroll
+    for (int k = 0; k < kNormPieces; k++) {
+      const int p = t + 256 * k;
+      if (p < np) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          const int i = 8 * p + e;
+          if (i < n) {
+            store<XT>(reinterpret_cast<XT*>(residual_out) + i, res[k][e]);
+            store<OT>(reinterpret_cast<OT*>(out) + i, (res[k][e] * inv) * ld<WT>(w, i));
+          }
+        }
+      }
+    }
+    return;
   }
+  float s = 0.0f;
+  for (int p = t; p < np; p += 256)
+    for (int i = 8 * p; i < 8 * p + 8 && i < n; i++) {
+      const float r = round_bf16(ld<XT>(left, i) + ld<XT>(right, i));
+      s = __builtin_fmaf(r, r, s);
+    }
+  const float total = block_sum256(s, red);
+  const float inv = 1.0f / __builtin_sqrtf(total / (float)n + eps);
+  for (int p = t; p < np; p += 256)
+    for (int i = 8 * p; i < 8 * p + 8 && i < n; i++) {
+      const float r = round_bf16(ld<XT>(left, i) + ld<XT>(right, i));
+      store<XT>(reinterpret_cast<XT*>(residual_out) + i, r);
+      store<OT>(reinterpret_cast<OT*>(out) + i, (r * inv) * ld<WT>(w, i));
+    }
 }
 
 // ---------------------------------------------------------------- elementwise
@@ -323,8 +342,9 @@ extern "C" int tt_rms_norm(const void* x, int x_dtype, const void* weight, int w
       using WT = decltype(wt);
       return with_any(out_dtype, [&](auto ot) {
         using OT = decltype(ot);
+        const int vec = n % 8 == 0 && aligned(x, 16);
         hipLaunchKernelGGL((rms_norm_kernel<XT, WT, OT>), dim3(1), dim3(256), 0, static_cast<hipStream_t>(stream), x,
-                           weight, out, (int)n, eps, weight_offset);
+                           weight, out, (int)n, eps, weight_offset, vec);
         return check_launch("rms_norm");
       });
     });
@@ -341,8 +361,9 @@ extern "C" int tt_add_rms_norm(const void* left, const void* right, void* residu
       using WT = decltype(wt);
       return with_any(out_dtype, [&](auto ot) {
         using OT = decltype(ot);
+        const int vec = n % 8 == 0 && aligned(left, 16) && aligned(right, 16);
         hipLaunchKernelGGL((add_rms_norm_kernel<XT, WT, OT>), dim3(1), dim3(256), 0, static_cast<hipStream_t>(stream),
-                           left, right, residual_out, weight, out, (int)n, eps);
+                           left, right, residual_out, weight, out, (int)n, eps, vec);
         return check_launch("add_rms_norm");
       });
     });

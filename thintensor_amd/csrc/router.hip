@@ -241,7 +241,6 @@ constexpr int kNormRouterExperts = 32;   // 16 waves x 2 experts
 template <typename WT, typename XT, typename BT, typename OT>
 __global__ __launch_bounds__(1024) void norm_router_kernel(const NormRouterParams P) {
   constexpr Fmt F = std::is_same_v<WT, bf16_t> ? Fmt::kBF16W : Fmt::kF16W;
-  constexpr int kHeld = 16;   // norm elements per thread of waves 0-3 (H <= 4096)
   __shared__ float red[4];
   __shared__ float logits[kNormRouterExperts];
   __shared__ uint4 xs[4096 / 8];   // normalized vector, XT bits
@@ -262,7 +261,7 @@ __global__ __launch_bounds__(1024) void norm_router_kernel(const NormRouterParam
   // ---- every load before the first wait: the norm inputs as 16-byte pieces (threads
   // 0-511, one piece of each vector; n <= 4096), then this wave's router rows and bias
   __shared__ uint4 raw_a[512], raw_b[512], raw_w[512];   // left, right, norm weight (raw bits)
-  static_assert(kHeld * 256 == 512 * 8, "the staging buffers hold whole vectors");
+  static_assert(kNormPieces * 256 == 512, "the staging buffers hold whole vectors");
   const int nq = n >> 3;
   // every thread loads (threads past the vector repeat its last piece), so no branch
   // separates these loads from the weight loads below
@@ -299,28 +298,29 @@ __global__ __launch_bounds__(1024) void norm_router_kernel(const NormRouterParam
   }
   __syncthreads();
 
-  // ---- add + RMSNorm in add_rms_norm_kernel's partition and order: thread t of waves
-  // 0-3 takes elements t + 256k, fma chain over k, wave butterfly, (w0 + w1) + (w2 + w3)
-  const XT* la = reinterpret_cast<const XT*>(raw_a);
-  const XT* lb = reinterpret_cast<const XT*>(raw_b);
-  const XT* lw = reinterpret_cast<const XT*>(raw_w);
-  float res[kHeld];
+  // ---- add + RMSNorm in add_rms_norm_kernel's piece partition and order: thread t of
+  // waves 0-3 takes pieces t, t + 256 of 8 elements, fma chain in element order, wave
+  // butterfly, (w0 + w1) + (w2 + w3)
+  const int t = threadIdx.x;
+  float res[kNormPieces][8];
   if (norm_wave) {
-    XT va[kHeld], vb[kHeld];
+    uint4 pa[kNormPieces], pb[kNormPieces];
 #pragma unroll
-    for (int k = 0; k < kHeld; k++) {
-      const int i = threadIdx.x + 256 * k;
-      const int ic = i < n ? i : n - 1;
-      va[k] = la[ic];
-      vb[k] = lb[ic];
+    for (int k = 0; k < kNormPieces; k++) {
+      const int pi = t + 256 * k;
+      const int pc = pi < nq ? pi : nq - 1;
+      pa[k] = raw_a[pc];
+      pb[k] = raw_b[pc];
     }
     __builtin_amdgcn_sched_barrier(0);   // every LDS read issued before the first use
     float ss = 0.0f;
 #pragma unroll
-    for (int k = 0; k < kHeld; k++) {
-      res[k] = round_bf16(to_f32(va[k]) + to_f32(vb[k]));
-      if (threadIdx.x + 256 * k < n) ss = __builtin_fmaf(res[k], res[k], ss);
-    }
+    for (int k = 0; k < kNormPieces; k++)
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        res[k][e] = round_bf16(piece_f32<XT>(pa[k], e) + piece_f32<XT>(pb[k], e));
+        if (8 * (t + 256 * k) + e < n) ss = __builtin_fmaf(res[k][e], res[k][e], ss);
+      }
     ss = xor_sum(ss, 1, 64);
     if (lane == 0) red[wave] = ss;
   }
@@ -328,15 +328,18 @@ __global__ __launch_bounds__(1024) void norm_router_kernel(const NormRouterParam
   if (norm_wave) {
     const float total = (red[0] + red[1]) + (red[2] + red[3]);
     const float inv = 1.0f / __builtin_sqrtf(total / (float)n + P.eps);
-    XT* xl = reinterpret_cast<XT*>(xs);
 #pragma unroll
-    for (int k = 0; k < kHeld; k++) {
-      const int i = threadIdx.x + 256 * k;
-      if (i < n) {
-        const float v = (res[k] * inv) * to_f32(lw[i]);
-        store<XT>(residual_out + i, res[k]);
-        store<XT>(norm_out + i, v);
-        store<XT>(xl + i, v);
+    for (int k = 0; k < kNormPieces; k++) {
+      const int pi = t + 256 * k;
+      if (pi < nq) {
+        const uint4 wv = raw_w[pi];
+        float o[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) o[e] = (res[k][e] * inv) * piece_f32<XT>(wv, e);
+        const uint4 op = pack_piece<XT>(o);
+        reinterpret_cast<uint4*>(residual_out)[pi] = pack_piece<XT>(res[k]);
+        reinterpret_cast<uint4*>(norm_out)[pi] = op;
+        xs[pi] = op;
       }
     }
   }
@@ -462,7 +465,9 @@ extern "C" int tt_add_rms_norm_router_topk(const void* left, const void* right, 
   const bool one_launch = experts <= kNormRouterExperts && hidden_size <= 4096 && hidden_size % 32 == 0 && hidden_size > 0 &&
                           x_dtype != TT_F32 && norm_w_dtype == x_dtype && norm_dtype == x_dtype &&
                           (w_dtype == TT_F16 || w_dtype == TT_BF16) && weight && indices_out && scores_out &&
-                          aligned(weight, 16) && w_row % 8 == 0 && experts > 0 && top_k > 0 && top_k <= experts;
+                          aligned(weight, 16) && w_row % 8 == 0 && experts > 0 && top_k > 0 && top_k <= experts &&
+                          aligned(left, 16) && aligned(right, 16) && aligned(residual_out, 16) &&
+                          aligned(norm_weight, 16) && aligned(norm_out, 16);
   if (!one_launch) {
     // the two operators per token, each with its own checks
     const int64_t xs = hidden_size * (x_dtype == TT_F32 ? 4 : 2), ns = hidden_size * (norm_dtype == TT_F32 ? 4 : 2);

@@ -257,6 +257,37 @@ __device__ __forceinline__ void rope_pair(float a, float b, float c, float s, fl
   o2 = bc + as;
 }
 
+// ---------------------------------------------------------------- RMSNorm partition
+// Every RMSNorm in the library (the standalone kernels and the fused prologues) cuts the
+// vector into pieces of 8 elements (16 bytes of a 16-bit type); piece p belongs to thread
+// p % 256 of the normalizing threads, and a thread's sum of squares is an fma chain over
+// its elements in increasing index order, followed by block_sum256.  One 16-byte load
+// brings a whole piece, and all implementations give the same bits.
+constexpr int kNormPieces = 2;   // pieces per thread held in registers: vectors up to 4096
+
+// element e (0..7) of a piece of a 16-bit type, as binary32
+template <typename T>
+__device__ __forceinline__ float piece_f32(const uint4& v, int e) {
+  const uint32_t w = e < 2 ? v.x : (e < 4 ? v.y : (e < 6 ? v.z : v.w));
+  return (e & 1) ? hi_f32<T>(w) : lo_f32<T>(w);
+}
+
+template <typename T> __device__ __forceinline__ uint32_t bits16(float v);
+template <> __device__ __forceinline__ uint32_t bits16<f16_t>(float v) { return f32_to_f16_bits(v); }
+template <> __device__ __forceinline__ uint32_t bits16<bf16_t>(float v) { return f32_to_bf16_bits(v); }
+
+// eight binary32 values rounded to a 16-bit type and packed as one piece (as store<T>
+// rounds them one at a time)
+template <typename T>
+__device__ __forceinline__ uint4 pack_piece(const float* v) {
+  uint4 r;
+  r.x = bits16<T>(v[0]) | (bits16<T>(v[1]) << 16);
+  r.y = bits16<T>(v[2]) | (bits16<T>(v[3]) << 16);
+  r.z = bits16<T>(v[4]) | (bits16<T>(v[5]) << 16);
+  r.w = bits16<T>(v[6]) | (bits16<T>(v[7]) << 16);
+  return r;
+}
+
 // silu(g) * u = (g / (1 + exp(-g))) * u in binary32 (triton_kernels.py:2761-2774).
 __device__ __forceinline__ float silu_mul_val(float g, float u) { return (g / (1.0f + exp_f32(-g))) * u; }
 
