@@ -130,8 +130,8 @@ def test_gqa_attention(backend, device, heads, kv_heads, tokens, sinks, cap):
     out = torch.empty(heads * D, device=device, dtype=torch.float16)
     qd, kd, vd = to_torch(q, device), to_torch(keys, device), to_torch(vals, device)
     skd = to_torch(sk, device) if sinks else None
-    # two calls in a row (the single-launch path counts chunk arrivals in the scratch and
-    # must leave the counters ready for the next call), the second with fewer tokens
+    # two calls in a row on the same scratch and output, the second with fewer tokens
+    # (stale partials of the first call must not leak into the second)
     for n in (tokens, max(1, tokens // 2 - 3)):
         tok = torch.tensor([n], dtype=torch.int32, device=device)
         backend.single_token_gqa_attention(qd, kd, vd, out, heads, kv_heads, D, sinks=skd, active_tokens=tok)

@@ -374,67 +374,86 @@ __global__ __launch_bounds__(64) void attn_combine64_kernel(AttnParams P) {
   store<T>(reinterpret_cast<T*>(P.out) + (int64_t)h * D + lane, acc / den);
 }
 
-// One workgroup per query head (contiguous head_dim-64 caches, whole-chunk capacity,
-// groups of at least eight query heads per KV head -- measured faster than the two
-// launches there, slower for smaller groups):
-// its 16 waves compute the head's chunk partials (chunk c on wave c mod 16) into LDS with
-// the arithmetic of attn_partial64_kernel, and after one barrier wave 0 combines them
-// in chunk order with the arithmetic of attn_combine64_kernel -- one launch, no
-// communication between workgroups.  The query heads of a KV head read the same K/V
-// rows, which the L2 serves after the first.
-constexpr int kHeadWaves = 16;
-constexpr int kHeadMaxChunks = 256;   // LDS partials: 66 floats per chunk
+// One workgroup per query head (contiguous head_dim-64 caches, whole-chunk capacity):
+// its kHeadWaves waves compute the head's chunk partials (chunk c on wave c mod
+// kHeadWaves) into LDS with the arithmetic of attn_partial64_kernel, and after one
+// barrier wave 0 combines them in chunk order with the arithmetic of
+// attn_combine64_kernel -- one launch, no communication between workgroups.
+//
+// Memory path: a wave requests its chunk as sixteen 16-byte loads per lane (K row of
+// the lane's token; V block pieces i * 64 + lane, i.e. token 8i + lane / 8), so the
+// address unit handles 16 instructions per chunk instead of one per V column element;
+// the V block is transposed through the wave's LDS slice for the weighted sum, and the
+// next chunk's rows are requested before the softmax so the value phase hides them.
+// Workgroups are dealt to the XCDs round-robin by id, so the query heads of one KV head
+// get ids congruent mod 8 (when the head counts allow it) and read its K/V rows through
+// one L2.
+constexpr int kHeadWaves = 12;
+constexpr int kHeadMaxChunks = 192;   // LDS partials: 66 floats per chunk
+constexpr int kXcds = 8;
+
+template <typename T>
+__device__ __forceinline__ void load_chunk(const T* kbase, const uint4* vbase, int c, int lane, uint4 (&kr)[8],
+                                           uint4 (&vr)[8]) {
+  const uint4* krow = reinterpret_cast<const uint4*>(kbase + (int64_t)(c * kChunk + lane) * 64);
+#pragma unroll
+  for (int i = 0; i < 8; i++) kr[i] = krow[i];
+  const uint4* vblk = vbase + (int64_t)c * (kChunk * 64 / 8);
+#pragma unroll
+  for (int i = 0; i < 8; i++) vr[i] = vblk[i * 64 + lane];
+}
 
 template <typename T, typename SKT>
-__global__ __launch_bounds__(1024) void attn_head_kernel(AttnParams P) {
+__global__ __launch_bounds__(64 * kHeadWaves) void attn_head_kernel(AttnParams P) {
   constexpr int D = 64;
-  const int h = blockIdx.x;
   const int G = P.heads / P.kv_heads;
+  int h = blockIdx.x;
+  if (P.heads % kXcds == 0 && P.kv_heads % kXcds == 0) {
+    // workgroup w runs on XCD w mod 8; its slot j = w / 8 on that XCD names
+    // (KV head 8 * (j / G) + w mod 8, query head j mod G of that group)
+    const int x = h % kXcds, j = h / kXcds;
+    h = ((j / G) * kXcds + x) * G + j % G;
+  }
   const int kvh = h / G;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   __shared__ float q_s[D];
   __shared__ float p_s[kHeadWaves][kChunk];
+  __shared__ uint4 v_s[kHeadWaves][kChunk * D / 8];
   __shared__ float pm_s[kHeadMaxChunks], pl_s[kHeadMaxChunks];
   __shared__ float po_s[kHeadMaxChunks][D];
   const float ninf = __builtin_bit_cast(float, 0xff800000u);
   const T* kbase = reinterpret_cast<const T*>(P.keys) + kvh * P.k_head;
-  const T* vbase = reinterpret_cast<const T*>(P.values) + kvh * P.v_head;
+  const uint4* vbase = reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(P.values) + kvh * P.v_head);
   // first chunk of this wave: every load is issued before the active count is known
   // (chunks below max_chunks are inside the capacity)
   const int c_first = wave;
-  uint4 kr[D / 8];
-  T vraw[kChunk];
-  if (c_first < P.max_chunks) {
-    const uint4* krow = reinterpret_cast<const uint4*>(kbase + (int64_t)(c_first * kChunk + lane) * D);
-#pragma unroll
-    for (int i = 0; i < D / 8; i++) kr[i] = krow[i];
-    const T* vcol = vbase + (int64_t)(c_first * kChunk) * D + lane;
-#pragma unroll
-    for (int tt = 0; tt < kChunk; tt++) vraw[tt] = vcol[tt * D];
-  }
+  uint4 kr[8], vr[8];
+  if (c_first < P.max_chunks) load_chunk<T>(kbase, vbase, c_first, lane, kr, vr);
   const T qraw = reinterpret_cast<const T*>(P.q)[(int64_t)h * D + lane];
   const int T_act = min(P.tokens_dev ? P.tokens_dev[0] + P.tokens : P.tokens, P.max_tokens);
   const int nc = T_act > 0 ? (T_act + kChunk - 1) / kChunk : 0;
   if (wave == 0) q_s[lane] = to_f32(qraw);
   __syncthreads();
 
+  float* p_w = p_s[wave];
+  uint4* v_w = v_s[wave];
   for (int c = c_first; c < nc; c += kHeadWaves) {
-    if (c != c_first) {
-      const uint4* krow = reinterpret_cast<const uint4*>(kbase + (int64_t)(c * kChunk + lane) * D);
-#pragma unroll
-      for (int i = 0; i < D / 8; i++) kr[i] = krow[i];
-      const T* vcol = vbase + (int64_t)(c * kChunk) * D + lane;
-#pragma unroll
-      for (int tt = 0; tt < kChunk; tt++) vraw[tt] = vcol[tt * D];
-    }
     const int t = c * kChunk + lane;
     const bool valid = t < T_act;
     const int nt = min(kChunk, T_act - c * kChunk);
+    // V pieces of tokens past the count are staged as zeros: the weighted sum then adds
+    // fma(0, 0, o) == o for them (p is 0 there and o is never -0)
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const uint32_t keep = i * 8 + (lane >> 3) < nt ? ~0u : 0u;
+      v_w[i * 64 + lane] = uint4{vr[i].x & keep, vr[i].y & keep, vr[i].z & keep, vr[i].w & keep};
+    }
     // score: fma chain over d ascending, lane = token
     float sc = 0.0f;
 #pragma unroll
     for (int i = 0; i < D / 8; i++) {
+      asm volatile("" : "+v"(sc)::"memory");   // eight query values live per step
       const uint32_t kw[4] = {kr[i].x, kr[i].y, kr[i].z, kr[i].w};
 #pragma unroll
       for (int e = 0; e < 8; e++) {
@@ -442,6 +461,8 @@ __global__ __launch_bounds__(1024) void attn_head_kernel(AttnParams P) {
         sc = __builtin_fmaf(q_s[8 * i + e], kv, sc);
       }
     }
+    // the next chunk of this wave is requested while this one finishes
+    if (c + kHeadWaves < nc) load_chunk<T>(kbase, vbase, c + kHeadWaves, lane, kr, vr);
     const float s = valid ? sc * P.scale : ninf;
     float m = s;
     m = fmaxf(m, xor_partner<1>(m));
@@ -452,21 +473,23 @@ __global__ __launch_bounds__(1024) void attn_head_kernel(AttnParams P) {
     m = fmaxf(m, xor_partner<32>(m));
     const float p = valid ? exp_f32(s - m) : 0.0f;
     const float l = xor_sum(p, 1, 64);
-    p_s[wave][lane] = p;
+    p_w[lane] = p;
     if (lane == 0) {
       pm_s[c] = m;
       pl_s[c] = l;
     }
-    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's p_s stores done
+    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's p and V stores done
     __builtin_amdgcn_wave_barrier();
     // weighted values: lane = dimension, fma chain over the chunk's tokens ascending
+    const T* vs = reinterpret_cast<const T*>(v_w);
     float o = 0.0f;
 #pragma unroll
     for (int tt = 0; tt < kChunk; tt++) {
-      const float v = tt < nt ? to_f32(vraw[tt]) : 0.0f;
-      o = __builtin_fmaf(p_s[wave][tt], v, o);
+      if ((tt & 7) == 0) asm volatile("" : "+v"(o)::"memory");   // eight tokens live per step
+      o = __builtin_fmaf(p_w[tt], to_f32(vs[tt * D + lane]), o);
     }
     po_s[c][lane] = o;
+    __builtin_amdgcn_s_waitcnt(0xc07f);   // reads of the wave's LDS slices done before reuse
     __builtin_amdgcn_wave_barrier();
   }
   __syncthreads();
@@ -504,11 +527,11 @@ __global__ __launch_bounds__(1024) void attn_head_kernel(AttnParams P) {
 
 template <typename T, int G>
 static int launch_attn(const AttnParams& P, int sink_dtype, bool contiguous64, hipStream_t st) {
-  if (contiguous64 && G >= 8 && P.max_chunks <= kHeadMaxChunks) {
+  if (contiguous64 && P.max_chunks <= kHeadMaxChunks) {
     switch (sink_dtype) {
-      case TT_BF16: hipLaunchKernelGGL((attn_head_kernel<T, bf16_t>), dim3(P.heads), dim3(1024), 0, st, P); break;
-      case TT_F32: hipLaunchKernelGGL((attn_head_kernel<T, float>), dim3(P.heads), dim3(1024), 0, st, P); break;
-      default: hipLaunchKernelGGL((attn_head_kernel<T, f16_t>), dim3(P.heads), dim3(1024), 0, st, P); break;
+      case TT_BF16: hipLaunchKernelGGL((attn_head_kernel<T, bf16_t>), dim3(P.heads), dim3(64 * kHeadWaves), 0, st, P); break;
+      case TT_F32: hipLaunchKernelGGL((attn_head_kernel<T, float>), dim3(P.heads), dim3(64 * kHeadWaves), 0, st, P); break;
+      default: hipLaunchKernelGGL((attn_head_kernel<T, f16_t>), dim3(P.heads), dim3(64 * kHeadWaves), 0, st, P); break;
     }
     return check_launch("gqa_attention");
   }
