@@ -380,11 +380,12 @@ __global__ __launch_bounds__(64) void attn_combine64_kernel(AttnParams P) {
 // barrier wave 0 combines them in chunk order with the arithmetic of
 // attn_combine64_kernel -- one launch, no communication between workgroups.
 //
-// Memory path: a wave requests its chunk as sixteen 16-byte loads per lane (K row of
-// the lane's token; V block pieces i * 64 + lane, i.e. token 8i + lane / 8), so the
-// address unit handles 16 instructions per chunk instead of one per V column element;
-// the V block is transposed through the wave's LDS slice for the weighted sum, and the
-// next chunk's rows are requested before the softmax so the value phase hides them.
+// Memory path: a wave requests its chunk's K and V blocks as sixteen fully coalesced
+// 16-byte loads per lane (each instruction covers 1 KB of consecutive bytes) and
+// transposes them through its own 8 KB LDS slice: K first (token r's piece d at slot
+// 8r + (d xor (r mod 8)), so the row reads of the score phase are free of bank
+// conflicts), then V in the same slice for the weighted sum.  The next chunk's blocks
+// are requested before the softmax so the value phase hides them.
 // Workgroups are dealt to the XCDs round-robin by id, so the query heads of one KV head
 // get ids congruent mod 8 (when the head counts allow it) and read its K/V rows through
 // one L2.
@@ -392,15 +393,21 @@ constexpr int kHeadWaves = 12;
 constexpr int kHeadMaxChunks = 192;   // LDS partials: 66 floats per chunk
 constexpr int kXcds = 8;
 
-template <typename T>
-__device__ __forceinline__ void load_chunk(const T* kbase, const uint4* vbase, int c, int lane, uint4 (&kr)[8],
-                                           uint4 (&vr)[8]) {
-  const uint4* krow = reinterpret_cast<const uint4*>(kbase + (int64_t)(c * kChunk + lane) * 64);
-#pragma unroll
-  for (int i = 0; i < 8; i++) kr[i] = krow[i];
+// A chunk's K and V blocks (64 tokens x 64 dims, 8 KB each) as 16-byte pieces
+// i * 64 + lane: token 8i + lane / 8, dimensions 8 (lane mod 8) .. +7.
+struct ChunkPieces {
+  uint4 k[8], v[8];
+};
+
+__device__ __forceinline__ ChunkPieces load_chunk(const uint4* kbase, const uint4* vbase, int c, int lane) {
+  const uint4* kblk = kbase + (int64_t)c * (kChunk * 64 / 8);
   const uint4* vblk = vbase + (int64_t)c * (kChunk * 64 / 8);
+  ChunkPieces r;
 #pragma unroll
-  for (int i = 0; i < 8; i++) vr[i] = vblk[i * 64 + lane];
+  for (int i = 0; i < 8; i++) r.k[i] = kblk[i * 64 + lane];
+#pragma unroll
+  for (int i = 0; i < 8; i++) r.v[i] = vblk[i * 64 + lane];
+  return r;
 }
 
 template <typename T, typename SKT>
@@ -419,17 +426,17 @@ __global__ __launch_bounds__(64 * kHeadWaves) void attn_head_kernel(AttnParams P
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   __shared__ float q_s[D];
   __shared__ float p_s[kHeadWaves][kChunk];
-  __shared__ uint4 v_s[kHeadWaves][kChunk * D / 8];
+  __shared__ uint4 kv_s[kHeadWaves][kChunk * D / 8];
   __shared__ float pm_s[kHeadMaxChunks], pl_s[kHeadMaxChunks];
   __shared__ float po_s[kHeadMaxChunks][D];
   const float ninf = __builtin_bit_cast(float, 0xff800000u);
-  const T* kbase = reinterpret_cast<const T*>(P.keys) + kvh * P.k_head;
+  const uint4* kbase = reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(P.keys) + kvh * P.k_head);
   const uint4* vbase = reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(P.values) + kvh * P.v_head);
   // first chunk of this wave: every load is issued before the active count is known
   // (chunks below max_chunks are inside the capacity)
   const int c_first = wave;
-  uint4 kr[8], vr[8];
-  if (c_first < P.max_chunks) load_chunk<T>(kbase, vbase, c_first, lane, kr, vr);
+  ChunkPieces cur;
+  if (c_first < P.max_chunks) cur = load_chunk(kbase, vbase, c_first, lane);
   const T qraw = reinterpret_cast<const T*>(P.q)[(int64_t)h * D + lane];
   const int T_act = min(P.tokens_dev ? P.tokens_dev[0] + P.tokens : P.tokens, P.max_tokens);
   const int nc = T_act > 0 ? (T_act + kChunk - 1) / kChunk : 0;
@@ -437,24 +444,40 @@ __global__ __launch_bounds__(64 * kHeadWaves) void attn_head_kernel(AttnParams P
   __syncthreads();
 
   float* p_w = p_s[wave];
-  uint4* v_w = v_s[wave];
+  uint4* kv_w = kv_s[wave];
   for (int c = c_first; c < nc; c += kHeadWaves) {
     const int t = c * kChunk + lane;
     const bool valid = t < T_act;
     const int nt = min(kChunk, T_act - c * kChunk);
+    // K block into the slice, then this lane's token row back out of it
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const int r = i * 8 + (lane >> 3);
+      const uint4 k = cur.k[i];
+      kv_w[r * 8 + ((lane & 7) ^ (r & 7))] = uint4{k.x, k.y, k.z, k.w};
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): the K stores are done
+    __builtin_amdgcn_wave_barrier();
+    uint32_t krow[8][4];
+#pragma unroll
+    for (int d = 0; d < 8; d++) {
+      const uint4 k = kv_w[lane * 8 + (d ^ (lane & 7))];
+      krow[d][0] = k.x; krow[d][1] = k.y; krow[d][2] = k.z; krow[d][3] = k.w;
+    }
     // V pieces of tokens past the count are staged as zeros: the weighted sum then adds
-    // fma(0, 0, o) == o for them (p is 0 there and o is never -0)
+    // fma(0, 0, o) == o for them (p is 0 there and o is never -0).  The wave's LDS
+    // operations complete in order, so these stores follow the row reads above.
 #pragma unroll
     for (int i = 0; i < 8; i++) {
       const uint32_t keep = i * 8 + (lane >> 3) < nt ? ~0u : 0u;
-      v_w[i * 64 + lane] = uint4{vr[i].x & keep, vr[i].y & keep, vr[i].z & keep, vr[i].w & keep};
+      kv_w[i * 64 + lane] = uint4{cur.v[i].x & keep, cur.v[i].y & keep, cur.v[i].z & keep, cur.v[i].w & keep};
     }
     // score: fma chain over d ascending, lane = token
     float sc = 0.0f;
 #pragma unroll
     for (int i = 0; i < D / 8; i++) {
-      asm volatile("" : "+v"(sc)::"memory");   // eight query values live per step
-      const uint32_t kw[4] = {kr[i].x, kr[i].y, kr[i].z, kr[i].w};
+      if ((i & 3) == 0) asm volatile("" : "+v"(sc)::"memory");   // 32 query values live per step
+      const uint32_t* kw = krow[i];
 #pragma unroll
       for (int e = 0; e < 8; e++) {
         const float kv = (e & 1) ? hi_f32<T>(kw[e >> 1]) : lo_f32<T>(kw[e >> 1]);
@@ -462,7 +485,7 @@ __global__ __launch_bounds__(64 * kHeadWaves) void attn_head_kernel(AttnParams P
       }
     }
     // the next chunk of this wave is requested while this one finishes
-    if (c + kHeadWaves < nc) load_chunk<T>(kbase, vbase, c + kHeadWaves, lane, kr, vr);
+    if (c + kHeadWaves < nc) cur = load_chunk(kbase, vbase, c + kHeadWaves, lane);
     const float s = valid ? sc * P.scale : ninf;
     float m = s;
     m = fmaxf(m, xor_partner<1>(m));
@@ -481,11 +504,11 @@ __global__ __launch_bounds__(64 * kHeadWaves) void attn_head_kernel(AttnParams P
     __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's p and V stores done
     __builtin_amdgcn_wave_barrier();
     // weighted values: lane = dimension, fma chain over the chunk's tokens ascending
-    const T* vs = reinterpret_cast<const T*>(v_w);
+    const T* vs = reinterpret_cast<const T*>(kv_w);
     float o = 0.0f;
 #pragma unroll
     for (int tt = 0; tt < kChunk; tt++) {
-      if ((tt & 7) == 0) asm volatile("" : "+v"(o)::"memory");   // eight tokens live per step
+      if ((tt & 31) == 0) asm volatile("" : "+v"(o)::"memory");   // 32 tokens live per step
       o = __builtin_fmaf(p_w[tt], to_f32(vs[tt * D + lane]), o);
     }
     po_s[c][lane] = o;
