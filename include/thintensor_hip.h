@@ -566,6 +566,60 @@ int64_t tt_stream_read_waves(int64_t bytes, int64_t bytes_per_wave);
 int tt_stream_read(const void* data, int64_t bytes, int64_t bytes_per_wave, void* out, int64_t out_words,
                    void* stream);
 
+/* ---------------------------------------------------------------- load-time quantizers
+ * Device-side packers of the layouts the GEMV kernels read.  Sources are row-major
+ * [rows, cols] fp16/bf16/fp32 (src_row elements between rows); outputs are contiguous.
+ * Group sums are taken in binary64 in a fixed lane order and rounded once, so results
+ * agree with the reference's binary32 torch sums except at near-ties that the
+ * reference's own summation order decides. */
+
+#define TT_Q4_LSQ 0          /* quantize_to_int4_cpu: amax/7, one least-squares refit, codes [-8,7]+8, fp16 scales [rows, groups] */
+#define TT_Q4_LSQ_AFFINE 1   /* quantize_to_int4_cpu, THINTENSOR_AFFINE_INT4=1: min/max line, 2 refits + final refit, codes [0,15], fp16 [rows, groups, 2] */
+#define TT_Q4_ROWS 2         /* _quantize_int4_rows: amax/7, codes [-7,7]+8, fp32 scales [rows, groups] */
+#define TT_Q4_ROWS_AFFINE 3  /* _quantize_int4_rows affine: min/max line, codes [0,15], fp32 [rows, groups, 2] */
+
+/* Grouped INT4 (two codes per byte, even column in the low nibble) for group sizes
+ * 32..512 (powers of two); importance [cols] (binary32 max(rms^2, 1e-8)) only with
+ * TT_Q4_LSQ_AFFINE.  Replaces quantize_to_int4_cpu (gpu_runtime.py:91-304, without the
+ * GPTQ covariance refinement) and ThinGpuCausalLMRuntime._quantize_int4_rows
+ * (gpu_runtime.py:6609-6700). */
+int tt_quantize_int4(const void* src, int src_dtype, int64_t rows, int64_t cols, int64_t src_row,
+                     int64_t group_size, int mode, const float* importance, uint8_t* packed, void* scales,
+                     void* stream);
+
+/* float8_e4m3fn rows with fp32 scales max(amax, 1e-12)/448 per row (block == 0, scales
+ * [rows]) or per block of columns (scales [rows, ceil(cols/block)]).  via_bf16 rounds the
+ * source and x/scale through bfloat16 first.  Replaces
+ * ThinGpuCausalLMRuntime._quantize_fp8_rows (gpu_runtime.py:6551-6607) and
+ * quantize_to_fp8_via_gpu (:40-88). */
+int tt_quantize_fp8_rows(const void* src, int src_dtype, int64_t rows, int64_t cols, int64_t src_row,
+                         int64_t block, int via_bf16, uint8_t* out, float* scales, void* stream);
+
+/* Native MXFP4 rows: packed [rows, cols/2] nibbles and E8M0 scales [rows, cols/32];
+ * optional Walsh-Hadamard blocks of `transform` (0 or 32..512) with sign flips `signs`
+ * [cols] (source dtype), and the binary-residual error criterion.  Replaces
+ * ThinGpuCausalLMRuntime._quantize_mxfp4_rows (gpu_runtime.py:6702-6812). */
+int tt_quantize_mxfp4_rows(const void* src, int src_dtype, int64_t rows, int64_t cols, int64_t src_row,
+                           int64_t transform, const void* signs, int binary_residual, uint8_t* packed,
+                           uint8_t* scales, void* stream);
+
+/* MXFP4 groups (blocks [n, 16] bytes, E8M0 scales [n]) to Q2 ([n, 8]) or Q1 ([n, 4])
+ * groups with the MSE-chosen exponent offset.  Replaces quantize_mxfp4_to_lowbit_cpu
+ * (gpu_runtime.py:306-395). */
+int tt_requantize_mxfp4_lowbit(const uint8_t* blocks, const uint8_t* scales, int64_t n_groups, int bits,
+                               uint8_t* out, uint8_t* out_scales, void* stream);
+
+/* Dense rows to Q2/Q1 E8M0 groups: out [rows, cols/32, 8 or 4], scales [rows, cols/32].
+ * Replaces quantize_dense_to_mxfp_lowbit_cpu (gpu_runtime.py:398-491). */
+int tt_quantize_dense_lowbit(const void* src, int src_dtype, int64_t rows, int64_t cols, int64_t src_row,
+                             int bits, uint8_t* out, uint8_t* out_scales, void* stream);
+
+/* MXFP4 rows (blocks [rows, groups, 16]) to the ternary layout [rows, ceil(32 groups/5)
+ * + ceil(3 groups/8)] (five base-3 digits per byte, then 3-bit magnitude selectors);
+ * the E8M0 scales are kept as they are.  Rows up to 16384 columns.  Replaces
+ * quantize_mxfp4_to_ternary_cpu (gpu_runtime.py:494-583). */
+int tt_pack_mxfp4_ternary(const uint8_t* blocks, int64_t rows, int64_t groups, uint8_t* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

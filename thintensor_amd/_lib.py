@@ -16,6 +16,7 @@ from . import build as _build
 
 F16, BF16, F32 = 0, 1, 2
 W_FP8 = 3   # weight format code of float8_e4m3fn (tt_split_k_matvec)
+Q4_LSQ, Q4_LSQ_AFFINE, Q4_ROWS, Q4_ROWS_AFFINE = 0, 1, 2, 3   # tt_quantize_int4 modes
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -115,6 +116,12 @@ SIGNATURES: dict[str, list] = {
     "tt_fused_lm_head_argmax": [_FGP, _P, _L, _P, _P, _P, _P, _P, ctypes.c_int32, _P],
     "tt_stream_read_waves": [_L, _L],
     "tt_stream_read": [_P, _L, _L, _P, _L, _P],
+    "tt_quantize_int4": [_P, _I, _L, _L, _L, _L, _I, _P, _P, _P, _P],
+    "tt_quantize_fp8_rows": [_P, _I, _L, _L, _L, _L, _I, _P, _P, _P],
+    "tt_quantize_mxfp4_rows": [_P, _I, _L, _L, _L, _L, _P, _I, _P, _P, _P],
+    "tt_requantize_mxfp4_lowbit": [_P, _P, _L, _I, _P, _P, _P],
+    "tt_quantize_dense_lowbit": [_P, _I, _L, _L, _L, _I, _P, _P, _P],
+    "tt_pack_mxfp4_ternary": [_P, _L, _L, _P, _P],
 }
 _RESTYPES = {"tt_last_error": ctypes.c_char_p, "tt_matvec_argmax_partials": ctypes.c_int64,
              "tt_stream_read_waves": ctypes.c_int64,
