@@ -620,6 +620,46 @@ int tt_quantize_dense_lowbit(const void* src, int src_dtype, int64_t rows, int64
  * quantize_mxfp4_to_ternary_cpu (gpu_runtime.py:494-583). */
 int tt_pack_mxfp4_ternary(const uint8_t* blocks, int64_t rows, int64_t groups, uint8_t* out, void* stream);
 
+/* ---------------------------------------------------------------- .thin archives
+ * Memory-mapped reader of ThinTensor v0 archives (header, JSON manifest, page table,
+ * payload).  Replaces the binary parsing and checks of ThinArchive
+ * (thinruntime/archive.py:99-208, 248-254; format src/archive.rs:14-41, 583-662) with
+ * the same messages; the manifest JSON and its page index stay with the caller.  The
+ * validation comes in the reference's order: tt_archive_open (header),
+ * tt_archive_parse_pages (page table, data_off), tt_archive_check_overlaps. */
+typedef struct tt_archive tt_archive;
+
+typedef struct {
+  uint32_t header_len, version;
+  uint64_t manifest_off, manifest_len, page_table_off, page_count, data_off;
+  uint8_t archive_hash[32];
+  uint64_t file_size;
+  const uint8_t* manifest; /* manifest_len bytes inside the mapping */
+} tt_archive_info;
+
+typedef struct {
+  const char* id; /* id_len bytes of UTF-8 inside the mapping (not terminated) */
+  int64_t id_len;
+  uint64_t offset, stored_size, raw_size;
+  uint32_t flags;
+  uint8_t checksum[32];
+} tt_archive_record;
+
+int tt_archive_open(const char* path, tt_archive** out);
+int tt_archive_parse_pages(tt_archive* archive);
+int tt_archive_check_overlaps(const tt_archive* archive);
+int tt_archive_get_info(const tt_archive* archive, tt_archive_info* out);
+int tt_archive_get_record(const tt_archive* archive, int64_t index, tt_archive_record* out);
+/* Index of the page table record named id, or -1. */
+int64_t tt_archive_find(const tt_archive* archive, const char* id, int64_t id_len);
+/* Base address of the read-only mapping (file offset 0); valid until tt_archive_close. */
+const uint8_t* tt_archive_data(const tt_archive* archive);
+/* Copy file bytes [offset, offset + nbytes) to device memory `dst` on `stream` through
+ * two 32 MiB pinned staging buffers (allocated on first use for the current device).
+ * Returns once the last chunk is queued; calls on one archive are serialized. */
+int tt_archive_upload(tt_archive* archive, int64_t offset, int64_t nbytes, void* dst, void* stream);
+int tt_archive_close(tt_archive* archive);
+
 #ifdef __cplusplus
 }
 #endif

@@ -41,3 +41,60 @@ def from_torch_bits(t) -> np.ndarray:
     if c.dtype == torch.bfloat16:
         return c.view(torch.int16).numpy().view(np.uint16)
     return c.numpy()
+
+
+# ------------------------------------------------------------------ .thin archives
+THIN_MAGIC = b"THINv0\0\0"
+
+
+def page_spec(page_id: str, dtype: str, shape, size: int, kind: str = "weight", layer=None, op: str = "weight",
+              **extra) -> dict:
+    """A manifest page entry (fields of PageSpec, src/manifest.rs:160-184)."""
+    spec = {"id": page_id, "kind": kind, "op": op, "dtype": dtype, "shape": list(shape),
+            "backend_layout": "row_major", "size": int(size), "checksum": "0" * 64}
+    if layer is not None:
+        spec["layer"] = layer
+    spec.update(extra)
+    return spec
+
+
+def write_thin_archive(path, manifest: dict, pages: dict) -> None:
+    """Write a .thin v0 file laid out as the reference's writer does (src/archive.rs:
+    457-520): 88-byte header, JSON manifest, page table (u16 id length, id, u64 offset,
+    u64 stored size, u64 raw size, u32 flags, 32-byte checksum), then the payloads back
+    to back.  Checksums are left zero (the readers do not check them)."""
+    import json
+    import struct
+
+    manifest_bytes = json.dumps(manifest, indent=2).encode()
+    ids = list(pages)
+    table_len = sum(2 + len(i.encode()) + 60 for i in ids)
+    manifest_off = 88
+    page_table_off = manifest_off + len(manifest_bytes)
+    data_off = page_table_off + table_len
+    table = b""
+    offset = data_off
+    for pid in ids:
+        data = bytes(pages[pid])
+        b = pid.encode()
+        table += struct.pack("<H", len(b)) + b + struct.pack("<QQQI", offset, len(data), len(data), 0) + bytes(32)
+        offset += len(data)
+    header = struct.pack("<8sIIQQQQQ32s", THIN_MAGIC, 88, 0, manifest_off, len(manifest_bytes), page_table_off,
+                         len(ids), data_off, bytes(32))
+    with open(path, "wb") as f:
+        f.write(header)
+        f.write(manifest_bytes)
+        f.write(table)
+        for pid in ids:
+            f.write(bytes(pages[pid]))
+
+
+def minimal_manifest(pages: list, layers: int = 1) -> dict:
+    return {
+        "format": "thintensor", "version": 0,
+        "model": {"arch": "llama", "hidden_size": 64, "layers": layers, "heads": 1, "kv_heads": 1, "dtype": "bf16"},
+        "execution_tape": [{"stage": "embed", "operator": "embedding", "page_refs": []}],
+        "pages": pages,
+        "memory_plan": {"scratch_bytes": 0, "min_vram_bytes": 0, "recommended_vram_bytes": 0,
+                        "kv_cache": {"policy": "none", "recent_tokens_high_precision": 0, "old_tokens_codec": "none"}},
+    }

@@ -53,6 +53,25 @@ class FusedGemv(ctypes.Structure):
 
 _FGP = ctypes.POINTER(FusedGemv)
 
+
+class ArchiveInfo(ctypes.Structure):
+    """tt_archive_info: header fields of a .thin archive and its manifest bytes."""
+    _fields_ = [
+        ("header_len", ctypes.c_uint32), ("version", ctypes.c_uint32), ("manifest_off", ctypes.c_uint64),
+        ("manifest_len", ctypes.c_uint64), ("page_table_off", ctypes.c_uint64), ("page_count", ctypes.c_uint64),
+        ("data_off", ctypes.c_uint64), ("archive_hash", ctypes.c_uint8 * 32), ("file_size", ctypes.c_uint64),
+        ("manifest", ctypes.c_void_p),
+    ]
+
+
+class ArchiveRecord(ctypes.Structure):
+    """tt_archive_record: one page table record."""
+    _fields_ = [
+        ("id", ctypes.c_void_p), ("id_len", ctypes.c_int64), ("offset", ctypes.c_uint64),
+        ("stored_size", ctypes.c_uint64), ("raw_size", ctypes.c_uint64), ("flags", ctypes.c_uint32),
+        ("checksum", ctypes.c_uint8 * 32),
+    ]
+
 # name -> argtypes (restype is int unless listed in _RESTYPES)
 SIGNATURES: dict[str, list] = {
     "tt_version": [],
@@ -122,10 +141,20 @@ SIGNATURES: dict[str, list] = {
     "tt_requantize_mxfp4_lowbit": [_P, _P, _L, _I, _P, _P, _P],
     "tt_quantize_dense_lowbit": [_P, _I, _L, _L, _L, _I, _P, _P, _P],
     "tt_pack_mxfp4_ternary": [_P, _L, _L, _P, _P],
+    "tt_archive_open": [ctypes.c_char_p, ctypes.POINTER(_P)],
+    "tt_archive_parse_pages": [_P],
+    "tt_archive_check_overlaps": [_P],
+    "tt_archive_get_info": [_P, ctypes.POINTER(ArchiveInfo)],
+    "tt_archive_get_record": [_P, _L, ctypes.POINTER(ArchiveRecord)],
+    "tt_archive_find": [_P, ctypes.c_char_p, _L],
+    "tt_archive_data": [_P],
+    "tt_archive_upload": [_P, _L, _L, _P, _P],
+    "tt_archive_close": [_P],
 }
 _RESTYPES = {"tt_last_error": ctypes.c_char_p, "tt_matvec_argmax_partials": ctypes.c_int64,
              "tt_stream_read_waves": ctypes.c_int64,
-             "tt_matvec_argmax_batched_partials": ctypes.c_int64}
+             "tt_matvec_argmax_batched_partials": ctypes.c_int64, "tt_archive_find": ctypes.c_int64,
+             "tt_archive_data": ctypes.c_void_p}
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
