@@ -350,24 +350,34 @@ def test_expert_kernels_token_batched(backend, device, bits, tokens):
         assert_bits_equal(from_torch_bits(out[t]), from_torch_bits(o1), f"weighted down token {t}")
 
 
-@pytest.mark.parametrize("bits,rows", [(2, 17920), (1, 5120)])
-def test_lowbit_affine_matvec(backend, device, bits, rows):
-    cols, group = 5120, 64
-    g = rng(61 + bits)
+# cfg2 shapes (17920 x 5120 q2, 5120 x 5120 q1), every lanes-per-row choice, odd group
+# counts (q1 falls back to the generic kernel), rows not a multiple of a wave's rows, bf16
+@pytest.mark.parametrize("bits,rows,cols,bf16", [(2, 17920, 5120, False), (1, 5120, 5120, False),
+                                                 (2, 1000, 2048, True), (1, 999, 2048, True),
+                                                 (2, 77, 960, False), (1, 77, 960, False),
+                                                 (1, 300, 4096, False), (2, 64, 192, True), (1, 130, 128, False)])
+def test_lowbit_affine_matvec(backend, device, bits, rows, cols, bf16):
+    group = 64
+    g = rng(61 + bits + cols)
     codes = g.integers(0, 1 << bits, size=(rows, cols), dtype=np.uint8)
     packed = layouts.pack_bits(codes, bits)
     sz = np.stack([np.abs(g.standard_normal((rows, cols // group))) * 0.05,
                    g.uniform(0, (1 << bits) - 1, size=(rows, cols // group))], axis=-1).astype(np.float16)
-    x = f16_normal(g, cols)
-    out = torch.empty(rows, device=device, dtype=torch.float16)
-    backend.lowbit_affine_matvec(to_torch(packed, device), to_torch(sz, device), to_torch(x, device), out, bits=bits,
-                                 rows=rows, cols=cols, group_size=group)
+    xf = g.standard_normal(cols).astype(np.float32)
+    x = bf16_bits(xf) if bf16 else xf.astype(np.float16)
+    odt = torch.bfloat16 if bf16 else torch.float16
+    out = torch.empty(rows, device=device, dtype=odt)
+    backend.lowbit_affine_matvec(to_torch(packed, device), to_torch(sz, device), to_torch(x, device, bf16=bf16), out,
+                                 bits=bits, rows=rows, cols=cols, group_size=group)
     got = from_torch_bits(out)
     want = oracle.gemv("q2aff" if bits == 2 else "q1aff", "group_aff", packed, sz, x, cols=cols, lpr=lanes(cols, 2),
-                       L=2, s_row=sz.shape[1] * 2, s_grp=2, s_pair=1, aff_zero=1)
-    assert_bits_equal(got, want, f"affine q{bits}")
-    y64 = ref.gemv64(ref.lowbit_affine_dequant(packed, sz, bits, group, cols), x)
-    assert ref.max_rel_err(got, y64) < TOL
+                       L=2, s_row=sz.shape[1] * 2, s_grp=2, s_pair=1, aff_zero=1,
+                       odtype=oracle.BF16 if bf16 else oracle.F16)
+    assert_bits_equal(got, want, f"affine q{bits} {rows}x{cols}")
+    xd = bf16_to_f32(x) if bf16 else x
+    y64 = ref.gemv64(ref.lowbit_affine_dequant(packed, sz, bits, group, cols), xd)
+    gotf = bf16_to_f32(got) if bf16 else got
+    assert ref.max_rel_err(gotf, y64) < TOL
 
 
 @pytest.mark.parametrize("scale_dtype", [np.float16, np.float32])

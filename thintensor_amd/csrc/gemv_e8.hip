@@ -66,6 +66,198 @@ int selected_e8(const char* what, Fmt fmt, const void* packed, int64_t w_expert_
   return TT_ERR_INVALID;
 }
 
+// Grouped affine Q2 / Q1 with 64-element groups, whole groups per lane load.
+//
+// Same arithmetic as the documented GEMV order (tt_gemv.h) with LPR lanes per row and
+// L = 2 chunks per group: the two chunks of group g sit in lanes 2(g mod P), +1 of the
+// contract (P = LPR / 2 "pair lanes") in round g div P, so S_g = p_2g + p_2g+1,
+// X_g = x_2g + x_2g+1, t_g = fmaf(X_g, -(z_g s_g), S_g s_g) and pair lane p keeps
+// A_p = ((+0 + t_round0) + t_round1) + ...; the row is the lane-index tree over the A_p.
+// Here one lane holds VP adjacent pair lanes (one group is 16 bytes of Q2, 8 of Q1)
+// with one accumulator each; the first tree level over them is taken in
+// the lane and the rest over the row's Q = P / VP lanes, so the bits are those of the
+// contract.  Chunk x sums (sequential from +0) are computed once per workgroup; x sits
+// in LDS with 16-byte piece k of group g at slot 8g + (k xor g mod 8), so the row's
+// lanes, which read consecutive groups, spread over the banks.
+struct Aff16Params {
+  const uint8_t* w;
+  const uint16_t* s;      // fp16 (scale, zero) pairs
+  const void* x;
+  void* out;
+  uint32_t w_row, s_row, s_grp;
+  int rows, cols;
+};
+
+// RPL rows per lane (rows lane / Q and lane / Q + 64 / (Q * RPL) ... of the wave's block
+// share each activation read and give the lane RPL * 2 independent fma chains per group).
+template <int BITS, typename XT, typename OT, int P, int VP, int RPL, int PF>
+__global__ __launch_bounds__(256) void affine16_kernel(const Aff16Params A) {
+  constexpr int Q = P / VP;                 // lanes per row
+  constexpr int RG = 64 / Q;                // row groups per wave
+  constexpr int RPW = RG * RPL;             // rows per wave
+  constexpr int GB = 8 * BITS;              // bytes per 64-element group
+  constexpr int LB = GB * VP;               // bytes per lane per round (16 or 8)
+  constexpr Fmt F = BITS == 2 ? Fmt::kQ2Aff : Fmt::kQ1Aff;
+  constexpr int CB = FmtInfo<F>::kBytes;    // bytes per 32-element chunk
+  extern __shared__ uint4 x_lds[];          // cols / 8 pieces, then cols / 32 floats
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int q = lane % Q;
+  const int row0 = (int)(blockIdx.x * 4 + wave) * RPW + lane / Q;
+  int row[RPL], rc[RPL];
+  bool live[RPL];
+#pragma unroll
+  for (int i = 0; i < RPL; i++) {
+    row[i] = row0 + i * RG;
+    live[i] = row[i] < A.rows;
+    rc[i] = live[i] ? row[i] : A.rows - 1;
+  }
+  const int G = A.cols >> 6;
+  const int rounds = (G + P - 1) / P;
+
+  struct Rnd {
+    uint32_t w[RPL][LB / 4];
+    uint16_t s[RPL][VP], z[RPL][VP];
+  };
+  auto fetch = [&](int r, Rnd& d) {
+    int g0 = r * P + q * VP;
+    g0 = g0 < G ? g0 : G - VP;              // past the last group: re-read it (unused)
+#pragma unroll
+    for (int i = 0; i < RPL; i++) {
+      const uint8_t* wp = A.w + (size_t)rc[i] * A.w_row + (uint32_t)g0 * GB;
+      if constexpr (LB == 16) {
+        const uint4 v = *reinterpret_cast<const uint4*>(wp);
+        d.w[i][0] = v.x; d.w[i][1] = v.y; d.w[i][2] = v.z; d.w[i][3] = v.w;
+      } else {
+        const uint2 v = *reinterpret_cast<const uint2*>(wp);
+        d.w[i][0] = v.x; d.w[i][1] = v.y;
+      }
+      const uint16_t* sp = A.s + (size_t)rc[i] * A.s_row;
+#pragma unroll
+      for (int v = 0; v < VP; v++) {
+        const uint32_t o = (uint32_t)(g0 + v) * A.s_grp;
+        d.s[i][v] = sp[o];
+        d.z[i][v] = sp[o + 1];
+      }
+    }
+  };
+  Rnd ring[PF];
+#pragma unroll
+  for (int k = 0; k < PF; k++) fetch(k, ring[k]);
+
+  // x into LDS (swizzled pieces), then the chunk sums
+  const int xn = A.cols >> 3;
+  const uint4* xg = reinterpret_cast<const uint4*>(A.x);
+  for (int i = threadIdx.x; i < xn; i += 256) {
+    const int g = i >> 3, k = i & 7;
+    x_lds[8 * g + (k ^ (g & 7))] = xg[i];
+  }
+  __syncthreads();
+  float* xsum = reinterpret_cast<float*>(x_lds + xn);
+  for (int c = threadIdx.x; c < (A.cols >> 5); c += 256) {
+    const int g = c >> 1;
+    float t = 0.0f;
+#pragma unroll
+    for (int k4 = 0; k4 < 4; k4++) {
+      const int k = 4 * (c & 1) + k4;
+      const uint4 v = x_lds[8 * g + (k ^ (g & 7))];
+      const uint32_t wd[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int e = 0; e < 8; e++) t = t + ((e & 1) ? hi_f32<XT>(wd[e >> 1]) : lo_f32<XT>(wd[e >> 1]));
+    }
+    xsum[c] = t;
+  }
+  __syncthreads();
+
+  float acc[RPL][VP];
+#pragma unroll
+  for (int i = 0; i < RPL; i++)
+#pragma unroll
+    for (int v = 0; v < VP; v++) acc[i][v] = 0.0f;
+  auto consume = [&](const Rnd& c, int r) {
+#pragma unroll
+    for (int v = 0; v < VP; v++) {
+      const int g = r * P + q * VP + v;
+      const bool gv = g < G;
+      const int gc = gv ? g : G - 1;
+      float pch[RPL][2];
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        // chunk 2g + h: its 32 activations (pieces 4h .. 4h+3 of the group), then the
+        // weight bytes of each row
+        uint32_t xw[16];
+#pragma unroll
+        for (int k4 = 0; k4 < 4; k4++) {
+          const int k = 4 * h + k4;
+          const uint4 xv4 = x_lds[8 * gc + (k ^ (gc & 7))];
+          xw[4 * k4] = xv4.x; xw[4 * k4 + 1] = xv4.y; xw[4 * k4 + 2] = xv4.z; xw[4 * k4 + 3] = xv4.w;
+        }
+        Raw<CB> raw[RPL];
+#pragma unroll
+        for (int i = 0; i < RPL; i++)
+#pragma unroll
+          for (int u = 0; u < CB / 4; u++) raw[i].w[u] = c.w[i][(v * 2 + h) * (CB / 4) + u];
+        float p[RPL];
+        chunk_dot_rows<F, XT, RPL>(raw, xw, p);
+#pragma unroll
+        for (int i = 0; i < RPL; i++) pch[i][h] = p[i];
+      }
+      const float X = xsum[2 * gc] + xsum[2 * gc + 1];
+#pragma unroll
+      for (int i = 0; i < RPL; i++) {
+        const float S = pch[i][0] + pch[i][1];
+        const float sk = (float)__builtin_bit_cast(_Float16, c.s[i][v]);
+        const float m = -((float)__builtin_bit_cast(_Float16, c.z[i][v]) * sk);
+        const float t = __builtin_fmaf(X, m, S * sk);
+        acc[i][v] = acc[i][v] + (gv ? t : 0.0f);
+      }
+    }
+  };
+  for (int r0 = 0; r0 < rounds; r0 += PF) {
+#pragma unroll
+    for (int k = 0; k < PF; k++) {
+      if (r0 + k < rounds) {
+        consume(ring[k], r0 + k);
+        if (r0 + k + PF < rounds) fetch(r0 + k + PF, ring[k]);
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < RPL; i++) {
+    float a = acc[i][0];
+    if constexpr (VP == 2) a = acc[i][0] + acc[i][1];
+    a = xor_sum(a, 1, Q);
+    if (live[i] && q == 0) store<OT>(reinterpret_cast<OT*>(A.out) + row[i], a);
+  }
+}
+
+// Measured at the cfg2 shapes: one group and one row per lane with two rounds in flight
+// was the fastest of {VP 1, 2} x {rows per lane 1, 2} x {2, 4 rounds in flight} for
+// both formats (q2 17920 x 5120 14.1 us, q1 5120 x 5120 6.6 us); the kernel is bound by
+// its VALU issue (v_fma_mix_f32 issues at half the rate of v_fma_f32 on this part).
+constexpr int kAffVP = 1, kAffRPL = 1, kAffPF = 2;
+
+template <int BITS, typename XT, int P, int VP, int RPL>
+int launch_affine16(const Aff16Params& A, hipStream_t st, const char* what) {
+  constexpr int RPW = 64 / (P / VP) * RPL;
+  const int64_t waves = ((int64_t)A.rows + RPW - 1) / RPW;
+  const dim3 grid((unsigned)((waves + 3) / 4));
+  const size_t lds = (size_t)A.cols * 2 + (size_t)(A.cols / 32) * 4;
+  hipLaunchKernelGGL((affine16_kernel<BITS, XT, XT, P, VP, RPL, kAffPF>), grid, dim3(256), lds, st, A);
+  return check_launch(what);
+}
+
+template <int BITS, typename XT>
+int affine16_by_lpr(int lpr, const Aff16Params& A, hipStream_t st, const char* what) {
+  constexpr int VP = kAffVP;
+  constexpr int RPL = kAffRPL;
+  switch (lpr) {
+    case 64: return launch_affine16<BITS, XT, 32, VP, RPL>(A, st, what);
+    case 32: return launch_affine16<BITS, XT, 16, VP, RPL>(A, st, what);
+    default: return launch_affine16<BITS, XT, 8, VP, RPL>(A, st, what);
+  }
+}
+
 }  // namespace
 
 extern "C" int tt_mxfp4_selected_matvec(const void* blocks, int64_t b_expert_bytes, int64_t b_row_bytes,
@@ -118,6 +310,17 @@ extern "C" int tt_lowbit_affine_matvec(const void* packed, int64_t w_row_bytes, 
   P.aff_zero = 1;
   const int lpr = tt_gemv_lanes_per_row(cols / 32, L);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  // 64-element groups, 16-byte rows, every lane's share a whole number of 16-byte loads
+  const int vp = kAffVP;
+  if (x_dtype == out_dtype && Lg == 2 && aligned(packed, 16) && w_row_bytes % 16 == 0 &&
+      (cols / 64) % vp == 0 && lpr / 2 >= vp && lean_fits(rows, w_row_bytes, 2 * s_row, cols) && s_group >= 2 &&
+      s_group * (cols / group_size) < (1LL << 30)) {
+    Aff16Params A{static_cast<const uint8_t*>(packed), static_cast<const uint16_t*>(scale_zero), x, out,
+                  (uint32_t)w_row_bytes, (uint32_t)s_row, (uint32_t)s_group, (int)rows, (int)cols};
+    if (bits == 2)
+      return x_dtype == TT_F16 ? affine16_by_lpr<2, f16_t>(lpr, A, st, what) : affine16_by_lpr<2, bf16_t>(lpr, A, st, what);
+    return x_dtype == TT_F16 ? affine16_by_lpr<1, f16_t>(lpr, A, st, what) : affine16_by_lpr<1, bf16_t>(lpr, A, st, what);
+  }
   if (x_dtype == out_dtype && lean_group_ok(Lg) && lean_fits(rows, w_row_bytes, 2 * s_row, cols) && s_group >= 0 &&
       s_group * (cols / group_size) < (1LL << 30)) {
     LeanParams Q{};
