@@ -436,14 +436,23 @@ int tt_moe_router_topk(const void* logits, int logits_dtype, int64_t experts, in
  * to M rows.  M < 16 runs the GEMV engine on up to four rows per launch (row m equals
  * the single-row operator bit for bit); M >= 16 (up to 64) runs an MFMA kernel
  * whose fp32 sums follow the hardware's order (tolerance parity).  cols must be a
- * multiple of 256 up to 8192. */
+ * multiple of 256 up to 8192.  The MFMA path (m >= 16) needs a workspace of
+ * tt_batched_workspace_floats(m, rows, cols) floats (0 for m < 16): it splits the
+ * (64-row block, 256-column slice) units evenly over one grid of the workgroups the
+ * chip holds at once; a block shared by several workgroups leaves their fp32 partial
+ * tiles in the workspace and a second kernel sums them in workgroup order, so the
+ * result is the same from run to run.  Calls sharing one workspace must be ordered
+ * (same stream).  int4 scales must be 4-byte aligned with an even row stride for
+ * m >= 16 (the kernel reads the two group scales of a slice at once). */
+int64_t tt_batched_workspace_floats(int64_t m, int64_t rows, int64_t cols);
 int tt_int4_batched_matvec(const void* packed, int64_t w_row_bytes, const void* scales_f16, int64_t s_row,
                            const void* x, int64_t x_row, void* out, int64_t out_row, int64_t m, int64_t rows,
-                           int64_t cols, int64_t group_size, void* stream);
-/* fp8-e4m3 rows with an fp32 scale per output row. */
+                           int64_t cols, int64_t group_size, float* workspace, int64_t workspace_floats,
+                           void* stream);
+/* fp8-e4m3 rows with an fp32 scale per output row (applied to the fp32 sum). */
 int tt_scaled_batched_matvec(const void* weight, int64_t w_row_bytes, const float* scales, const void* x,
                              int64_t x_row, void* out, int64_t out_row, int64_t m, int64_t rows, int64_t cols,
-                             void* stream);
+                             float* workspace, int64_t workspace_floats, void* stream);
 
 /* Greedy lm_head for M activation rows: out_idx[m] = first index of the maximum of
  * round(W x[m]) (the tt_matvec_argmax semantics per row), logits [M, logits_row]

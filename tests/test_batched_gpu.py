@@ -66,6 +66,40 @@ def test_int4_batched_decode_shape_mfma(backend, device):
     assert diff.max() / np.abs(from_torch_bits(one).astype(np.float64)).max() < 2e-3
 
 
+@pytest.mark.parametrize("fmt,rows,cols,m", [
+    ("int4", 64, 256, 16),        # one unit: one workgroup, no shared block
+    ("int4", 100, 768, 20),       # six units over six workgroups: every block shared, ragged last block
+    ("int4", 4000, 2048, 48),     # one unit per workgroup: eight partial tiles per block
+    ("int4", 17920, 5120, 16),    # whole blocks inside a range and blocks shared at range ends
+    ("fp8", 100, 768, 17),
+    ("fp8", 9000, 4096, 64),
+])
+def test_batched_mfma_stream_k(backend, device, fmt, rows, cols, m):
+    """The MFMA path splits (64-row block, 256-column slice) units evenly over the
+    grid; blocks shared by several workgroups are summed from partial tiles.  Every
+    output row is checked against float64, and a second call with fewer activation
+    rows reuses the workspace."""
+    g = rng(rows + cols + m)
+    if fmt == "int4":
+        packed, scales = _int4_case(g, rows, cols)
+        w64 = ref.int4_dequant(packed, scales, 128)
+        wd, sd = to_torch(packed, device), to_torch(scales, device)
+        call = backend.int4_batched_matvec
+    else:
+        bits, scales = _fp8_case(g, rows, cols)
+        w64 = ref.fp8_e4m3fn(bits) * scales[:, None].astype(np.float64)
+        wd, sd = torch.from_numpy(bits).to(device).view(torch.float8_e4m3fn), to_torch(scales, device)
+        call = backend.scaled_batched_matvec
+    for mm in (m, 16):
+        x = f16_normal(g, (mm, cols))
+        out = torch.empty((mm, rows), device=device, dtype=torch.float16)
+        call(wd, sd, to_torch(x, device), out)
+        got = from_torch_bits(out)
+        y64 = x.astype(np.float64) @ w64.T
+        for r in range(mm):
+            assert ref.max_rel_err(got[r], y64[r]) < TOL, f"{fmt} {rows}x{cols} m={mm} row {r}"
+
+
 def _fp8_case(g, rows, cols):
     bits = g.integers(0, 256, size=(rows, cols), dtype=np.uint8)
     bits[(bits & 0x7F) == 0x7F] = 0x3C          # no NaN encodings

@@ -126,8 +126,9 @@ SIGNATURES: dict[str, list] = {
                                               _I, _L, _L, _L, _L, _P],
     "tt_mxfp_lowbit_weighted_down_tokens": [_P, _L, _L, _P, _L, _L, _I, _P, _I, _L, _P, _P, _I, _L, _P, _I, _L, _P, _I,
                                             _L, _L, _L, _L, _P],
-    "tt_int4_batched_matvec": [_P, _L, _P, _L, _P, _L, _P, _L, _L, _L, _L, _L, _P],
-    "tt_scaled_batched_matvec": [_P, _L, _P, _P, _L, _P, _L, _L, _L, _L, _P],
+    "tt_batched_workspace_floats": [_L, _L, _L],
+    "tt_int4_batched_matvec": [_P, _L, _P, _L, _P, _L, _P, _L, _L, _L, _L, _L, _P, _L, _P],
+    "tt_scaled_batched_matvec": [_P, _L, _P, _P, _L, _P, _L, _L, _L, _L, _P, _L, _P],
     "tt_matvec_argmax_batched_partials": [_L, _L, _L],
     "tt_matvec_argmax_batched": [_P, _L, _P, _L, _L, _P, _L, _L, _L, _P, _L, _P, _P, _P],
     "tt_fused_struct_sizes": [_LP, _LP],
@@ -152,6 +153,7 @@ SIGNATURES: dict[str, list] = {
     "tt_archive_close": [_P],
 }
 _RESTYPES = {"tt_last_error": ctypes.c_char_p, "tt_matvec_argmax_partials": ctypes.c_int64,
+             "tt_batched_workspace_floats": ctypes.c_int64,
              "tt_stream_read_waves": ctypes.c_int64,
              "tt_matvec_argmax_batched_partials": ctypes.c_int64, "tt_archive_find": ctypes.c_int64,
              "tt_archive_data": ctypes.c_void_p}

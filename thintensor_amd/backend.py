@@ -1217,10 +1217,11 @@ class HipDecodeBackend:
         rows, cols = int(packed_weight.shape[0]), int(x.shape[1])
         if packed_weight.shape[1] * packed_weight.element_size() * 2 != cols or out.shape[1] != rows:
             raise ValueError("batched int4 matvec shape mismatch")
+        ws = self._batched_workspace(int(x.shape[0]), rows, cols)
         rc = self.lib.tt_int4_batched_matvec(
             packed_weight.data_ptr(), packed_weight.stride(0) * packed_weight.element_size(), scales.data_ptr(),
             scales.stride(0), x.data_ptr(), x.stride(0), out.data_ptr(), out.stride(0), int(x.shape[0]), rows, cols,
-            group_size, _stream(out))
+            group_size, ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0, _stream(out))
         _lib.check(rc, "int4_batched_matvec")
         return out
 
@@ -1233,11 +1234,25 @@ class HipDecodeBackend:
         if x.dtype != torch.float16 or out.dtype != torch.float16:
             raise ValueError("batched scaled matvec takes fp16 activations and outputs")
         rows, cols = int(weight.shape[0]), int(weight.shape[1])
+        ws = self._batched_workspace(int(x.shape[0]), rows, cols)
         rc = self.lib.tt_scaled_batched_matvec(
             weight.data_ptr(), weight.stride(0) * weight.element_size(), scales.data_ptr(), x.data_ptr(), x.stride(0),
-            out.data_ptr(), out.stride(0), int(x.shape[0]), rows, cols, _stream(out))
+            out.data_ptr(), out.stride(0), int(x.shape[0]), rows, cols, ws.data_ptr() if ws is not None else None,
+            ws.numel() if ws is not None else 0, _stream(out))
         _lib.check(rc, "scaled_batched_matvec")
         return out
+
+    def _batched_workspace(self, m: int, rows: int, cols: int) -> torch.Tensor | None:
+        """Workspace of the MFMA path (fp32 partial tiles of row blocks shared
+        between workgroups), reused between calls on this backend's stream."""
+        need = int(self.lib.tt_batched_workspace_floats(m, rows, cols))
+        if need == 0:
+            return None
+        ws = getattr(self, "_batched_ws", None)
+        if ws is None or ws.numel() < need:
+            ws = torch.empty(need, device=self.device, dtype=torch.float32)
+            self._batched_ws = ws
+        return ws
 
     def _batched_argmax_scratch(self, m: int, rows: int, cols: int) -> torch.Tensor:
         need = int(self.lib.tt_matvec_argmax_batched_partials(m, rows, cols))

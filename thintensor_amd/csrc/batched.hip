@@ -3,13 +3,16 @@
 //   * M < 16: the GEMV engine with up to four activation rows per wave (every
 //     weight word decoded once, one fma chain per activation row), so row m equals
 //     the single-row GEMV bit for bit;
-//   * M >= 16: MFMA.  Each wave owns 16 output rows and all M (<= 64, in tiles of
-//     16) activation rows; per quantisation group of 128 columns it issues four
-//     v_mfma_f32_16x16x32_f16 with the dequantised weights as the A operand and the
-//     activations (staged in LDS per 256-column slice) as the B operand, then scales
-//     the group's fp32 tile (int4) or accumulates it (fp8, row scale at the end).
-//     MFMA sums products in a hardware-defined order, so this path matches the
-//     dequantise-then-matmul reference to the stated tolerance, not bit for bit.
+//   * M >= 16: MFMA.  The four waves of a workgroup own a 64-row block (16 rows
+//     each) and all M (<= 64, in tiles of 16) activation rows; per quantisation
+//     group of 128 columns each wave issues four v_mfma_f32_16x16x32_f16 with the
+//     dequantised weights as the A operand (int4: code times group scale, rounded
+//     to fp16; fp8: exact) and the activations (staged in LDS per 256-column slice)
+//     as the B operand; fp8's row scale multiplies the fp32 sum.  The (block, slice)
+//     units are split evenly over a grid of two workgroups per CU (stream-K), and
+//     blocks split between workgroups are summed in a fixed order by a second
+//     kernel.  MFMA sums products in a hardware-defined order, so this path matches
+//     the dequantise-then-matmul reference to the stated tolerance, not bit for bit.
 //   * the M-row lm_head argmax runs the GEMV engine with four activation rows per
 //     launch and one argmax key per (wave, row); a finishing kernel picks each row's
 //     token, as tt_matvec_argmax does for one row.
@@ -25,10 +28,16 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
 constexpr int kSlice = 256;   // columns of x staged in LDS per step (two int4 groups)
-// LDS row pitch of a staged slice, in halves: 16 bytes of padding per row put the 16
-// rows that one B-operand read touches in 16 different 4-bank groups (an unpadded
-// 512-byte pitch maps them all to the same banks).
-constexpr int kPitch = kSlice + 8;
+constexpr int kMaxSlices = 8192 / kSlice;
+
+// LDS position (in 16-byte pieces) of activation row 16 t + i, columns 128 gs +
+// 32 g + 8 q + [0, 8) of a staged slice.  The B operand of (gs, q, t) is one read of
+// 64 consecutive pieces, lane 16 g + i taking piece i ^ (4 q + g) of its 16: any
+// group of lanes the LDS serves together reads distinct banks, and so do the 16
+// consecutive lanes of a store (one row, 16 pieces = 16 distinct (q, g)).
+__device__ __forceinline__ int x_piece(int t, int gs, int q, int g, int i) {
+  return ((t * (kSlice / 128) + gs) * 4 + q) * 64 + g * 16 + (i ^ (4 * q + g));
+}
 
 enum class WFmt : int { kInt4G128 = 0, kFp8Row = 1 };
 
@@ -41,7 +50,12 @@ struct MfmaParams {
   int64_t x_row;
   uint16_t* out;        // fp16 [M, out_row]
   int64_t out_row;
+  float* ws;            // fp32 partial tiles [2 * grid][16 MT][64] of blocks shared by workgroups
   int m, n, k;
+  int spb;              // 256-column slices per 64-row block
+  int64_t units;        // blocks * spb
+  int grid;             // workgroups
+  int ws_row_scale;     // fold: multiply by the fp8 row scale
 };
 
 // Weights of one 128-column group for this lane: row n0 + lane % 16, columns
@@ -51,15 +65,15 @@ struct WChunk {
   uint32_t w[W == WFmt::kInt4G128 ? 4 : 8];
 };
 
+// p: this lane's 32 columns of the group (int4: 16 bytes, fp8: 32 bytes).
 template <WFmt W>
-__device__ __forceinline__ WChunk<W> load_chunk(const MfmaParams& P, int row, int grp, int lane) {
+__device__ __forceinline__ WChunk<W> load_chunk(const uint8_t* p) {
   WChunk<W> c;
   if constexpr (W == WFmt::kInt4G128) {
-    const uint4 v = *reinterpret_cast<const uint4*>(P.w + (int64_t)row * P.w_row + (int64_t)grp * 64 + 16 * (lane >> 4));
+    const uint4 v = *reinterpret_cast<const uint4*>(p);
     c.w[0] = v.x; c.w[1] = v.y; c.w[2] = v.z; c.w[3] = v.w;
   } else {
-    const uint4* p = reinterpret_cast<const uint4*>(P.w + (int64_t)row * P.w_row + (int64_t)grp * 128 + 32 * (lane >> 4));
-    const uint4 a = p[0], b = p[1];
+    const uint4 a = reinterpret_cast<const uint4*>(p)[0], b = reinterpret_cast<const uint4*>(p)[1];
     c.w[0] = a.x; c.w[1] = a.y; c.w[2] = a.z; c.w[3] = a.w;
     c.w[4] = b.x; c.w[5] = b.y; c.w[6] = b.z; c.w[7] = b.w;
   }
@@ -98,8 +112,6 @@ __device__ __forceinline__ uint4 nib_order(uint4 v) {
                  __builtin_amdgcn_perm(v.w, v.y, 0x05040100u), __builtin_amdgcn_perm(v.w, v.y, 0x07060302u)};
 }
 
-constexpr int kMaxGroups = 8192 / 128;   // int4 scale groups per row (cols <= 8192)
-
 // f(integral_constant<I>) for I = B .. E-1, unrolled at compile time.
 template <int B, int E, typename F>
 __device__ __forceinline__ void static_for(F&& f) {
@@ -109,55 +121,107 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
-// Pipeline depth (slices in flight) per activation tile count: as deep as two
-// workgroups per CU (256 registers per wave) allow.
-template <bool I4, int MT> constexpr int mfma_depth() { return MT == 1 ? 8 : (MT == 2 ? 4 : (I4 ? 4 : 2)); }
+// Workgroups per CU (one wave per SIMD each) and pipeline depth (units in flight)
+// per activation tile count.  Two units in flight per workgroup already keep ~16 MB
+// of loads in flight over the chip; deeper pipelines only lengthen the start, when
+// every workgroup's first unit waits behind the whole initial burst (measured at
+// 17920 x 5120, M = 16: depth 8 -> 2 takes 28.0 -> 23.9 us).
+#ifndef TT_MFMA_TUNE
+template <int MT> constexpr int mfma_per_cu() { return 2; }
+template <bool I4, int MT> constexpr int mfma_depth() { return MT <= 3 ? 2 : (I4 ? 3 : 2); }
+#endif
+
+// Stream-K over (64-row block, 256-column slice) units: unit u is block u / spb,
+// slice u % spb; workgroup w owns units [w T / G, (w + 1) T / G) of T, so every
+// workgroup gets the same work (within one unit) whatever the block count, and the
+// grid is exactly the workgroups the chip holds at once.
+__device__ __host__ __forceinline__ int64_t unit_begin(int64_t w, int64_t units, int64_t grid) {
+  return w * units / grid;
+}
+// The workgroup whose range holds unit u.
+__device__ __forceinline__ int64_t unit_owner(int64_t u, int64_t units, int64_t grid) {
+  return ((u + 1) * grid - 1) / units;
+}
 
 template <WFmt W, int MT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void mfma_gemm_kernel(MfmaParams P) {
-  // Software pipeline of depth D slices, held in registers:
-  //   * the weights and the activations of slice s are both requested D slices
-  //     before s computes (vector loads complete in issue order, so a load issued
-  //     later than another can never be waited for earlier: both streams get the same
-  //     lead);
-  //   * the activations of slice s + 1 go from registers to one of two LDS buffers at
-  //     the end of slice s;
-  //   * the workgroup's int4 group scales are staged in LDS once ([row][group]);
-  //   * barriers order LDS only, so the global loads stay in flight across them.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(mfma_per_cu<MT>()))) void mfma_gemm_kernel(MfmaParams P) {
+  // Software pipeline of depth D units, held in registers:
+  //   * the weights (and int4 group scales) and the activations of unit i are both
+  //     requested D units before i computes (vector loads complete in issue order,
+  //     so a load issued later than another can never be waited for earlier: both
+  //     streams get the same lead);
+  //   * the activations of unit i + 1 go from registers to one of two LDS buffers at
+  //     the end of unit i;
+  //   * barriers order LDS only, so the global loads stay in flight across them;
+  //   * the pipeline runs on across block boundaries: at the last unit of a block
+  //     (or of the workgroup's range) the tile is written out and the accumulators
+  //     restart.  A block that lies inside one workgroup's range is stored as fp16;
+  //     a block shared by several workgroups leaves one fp32 partial tile per
+  //     workgroup, summed in workgroup order by mfma_fold_kernel.
   // int4 weights enter the MFMA already scaled (fp16), so every product of a row
   // accumulates into one fp32 tile; with a single activation tile the accumulation
   // alternates between two tiles (summed at the end) to halve the dependency chain.
   constexpr bool kI4 = W == WFmt::kInt4G128;
   constexpr int kAhead = mfma_depth<kI4, MT>();
   constexpr int NA = MT == 1 ? 2 : 1;                  // accumulator tiles per activation tile
-  constexpr int XS = MT * 16 * kPitch;                 // halves per buffer
+  constexpr int XS = MT * 16 * kSlice;                 // halves per buffer
   constexpr int XV = MT * 16 * kSlice / 8 / 256;       // 16-byte pieces per thread per slice
   constexpr int GPS = kSlice / 128;                    // quantisation groups per slice
   __shared__ __attribute__((aligned(16))) uint16_t xs[2 * XS];
-  __shared__ __attribute__((aligned(16))) uint16_t scl[kI4 ? kMaxGroups * 64 : 4];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int nb = blockIdx.x * 64;
-  const int n0 = nb + wave * 16;
-  const int arow = n0 + (lane & 15);                 // weight row this lane loads (A operand)
-  const int lrow = arow < P.n ? arow : P.n - 1;
   const int g = lane >> 4;
-  const int slices = P.k / kSlice;
-  const int groups = P.k / 128;
-  // Every load below is unconditional (indices are clamped) so the compiler keeps
-  // exact outstanding-load counts across the unrolled pipeline; rows of x past m and
-  // slices past the end are loaded again, and only feed outputs that are not stored.
+  const int spb = P.spb;
+  const int64_t u0 = unit_begin(blockIdx.x, P.units, P.grid);
+  const int count = (int)(unit_begin(blockIdx.x + 1, P.units, P.grid) - u0);
+  const int first_block = (int)(u0 / spb);
+  // cursors: the unit computed (cb, cs) and the unit loaded next (lb, ls, li);
+  // loads past the range repeat its last unit, so every load is unconditional and
+  // the compiler keeps exact outstanding-load counts across the unrolled pipeline
+  int cb = first_block, cs = (int)(u0 - (int64_t)first_block * spb);
+  int lb = cb, ls = cs, li = 0;
+  // load pointers of the lane: weight row of block lb at slice ls (and its group
+  // scales); stepped by one slice per unit, recomputed at block changes
+  constexpr int kSliceBytes = kI4 ? kSlice / 2 : kSlice;
+  const int lane_col = (kI4 ? 16 : 32) * g;
+  const uint8_t* wp;
+  const uint16_t* sp;
+  auto row_ptrs = [&]() __attribute__((always_inline)) {
+    int row = lb * 64 + wave * 16 + (lane & 15);
+    row = row < P.n ? row : P.n - 1;
+    wp = P.w + (int64_t)row * P.w_row + ls * kSliceBytes + lane_col;
+    if constexpr (kI4) sp = static_cast<const uint16_t*>(P.s) + (int64_t)row * P.s_row + ls * GPS;
+  };
+  row_ptrs();
+  auto advance_load = [&]() __attribute__((always_inline)) {
+    if (li < count - 1) {
+      li++;
+      if (++ls == spb) {
+        ls = 0;
+        lb++;
+        row_ptrs();
+      } else {
+        wp += kSliceBytes;
+        if constexpr (kI4) sp += GPS;
+      }
+    }
+  };
   // activation slot u: xq_even / xq_odd[(u / 2) * XV + v] (two arrays: smaller
   // private arrays are the ones the compiler keeps in registers)
-  uint4 xq_even[kAhead / 2 * XV], xq_odd[kAhead / 2 * XV];
+  uint4 xq_even[(kAhead + 1) / 2 * XV], xq_odd[(kAhead + 1) / 2 * XV];
+  const uint16_t* xb[XV];                              // row min(r, m - 1), columns 8 c8 .. of slice 0
+#pragma unroll
+  for (int v = 0; v < XV; v++) {
+    const int i = threadIdx.x + 256 * v;
+    int r = i / (kSlice / 8);
+    const int c8 = i - r * (kSlice / 8);
+    r = r < P.m ? r : P.m - 1;
+    xb[v] = P.x + (int64_t)r * P.x_row + 8 * c8;
+  }
   auto load_x = [&](int sl, auto uc) __attribute__((always_inline)) {
     constexpr int u = decltype(uc)::value;
 #pragma unroll
     for (int v = 0; v < XV; v++) {
-      const int i = threadIdx.x + 256 * v;
-      int r = i / (kSlice / 8);
-      const int c8 = i - r * (kSlice / 8);
-      r = r < P.m ? r : P.m - 1;
-      const uint4 t = *reinterpret_cast<const uint4*>(P.x + (int64_t)r * P.x_row + (int64_t)sl * kSlice + 8 * c8);
+      const uint4 t = *reinterpret_cast<const uint4*>(xb[v] + sl * kSlice);
       if constexpr ((u & 1) == 0) xq_even[u / 2 * XV + v] = t;
       else xq_odd[u / 2 * XV + v] = t;
     }
@@ -170,64 +234,92 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
       const int r = i / (kSlice / 8), c8 = i - r * (kSlice / 8);
       uint4 t = (u & 1) == 0 ? xq_even[u / 2 * XV + v] : xq_odd[u / 2 * XV + v];
       if constexpr (kI4) t = nib_order(t);
-      *reinterpret_cast<uint4*>(xs + buf * XS + r * kPitch + 8 * c8) = t;
+      const int cc = c8 & 15;
+      *reinterpret_cast<uint4*>(xs + buf * XS + 8 * x_piece(r >> 4, c8 >> 4, cc & 3, cc >> 2, r & 15)) = t;
     }
+  };
+  WChunk<W> ring[kAhead][GPS];
+  uint32_t sring[kI4 ? kAhead : 1];                    // int4: the row's two group scales (fp16 pair)
+  auto load_unit = [&](auto uc) __attribute__((always_inline)) {
+    constexpr int u = decltype(uc)::value;
+#pragma unroll
+    for (int gs = 0; gs < GPS; gs++) ring[u][gs] = load_chunk<W>(wp + gs * (kSliceBytes / GPS));
+    if constexpr (kI4) sring[u] = *reinterpret_cast<const uint32_t*>(sp);
+    load_x(ls, uc);
   };
   f4 acc[NA][MT];
 #pragma unroll
   for (int j = 0; j < NA; j++)
 #pragma unroll
     for (int t = 0; t < MT; t++) acc[j][t] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
-  WChunk<W> ring[kAhead][GPS];
-#pragma unroll
-  for (int u = 0; u < kAhead; u++)
-#pragma unroll
-    for (int gs = 0; gs < GPS; gs++) ring[u][gs] = load_chunk<W>(P, lrow, (u < slices ? u : slices - 1) * GPS + gs, lane);
+  // prologue: units 0 .. kAhead - 1 in the order every step issues its loads (the
+  // wait for unit i + 1's activations is then as shallow in the first loop
+  // iteration as in later ones, and the first store waits for unit 0 only)
   static_for<0, kAhead>([&](auto uc) __attribute__((always_inline)) {
-    load_x(decltype(uc)::value < slices ? decltype(uc)::value : slices - 1, uc);
+    load_unit(uc);
+    advance_load();
   });
-  if constexpr (kI4) {
-    // thread t stages row t / 4, groups t % 4 + 4 j, into scl[row * groups + group]
-    const int r = threadIdx.x >> 2;
-    const int row = nb + r < P.n ? nb + r : P.n - 1;
-    const uint16_t* sg = reinterpret_cast<const uint16_t*>(P.s) + (int64_t)row * P.s_row;
-    uint16_t sv[kMaxGroups / 4];
-#pragma unroll
-    for (int j = 0; j < kMaxGroups / 4; j++) {
-      const int gi = (threadIdx.x & 3) + 4 * j;
-      sv[j] = sg[gi < groups ? gi : groups - 1];
-    }
-#pragma unroll
-    for (int j = 0; j < kMaxGroups / 4; j++) {
-      const int gi = (threadIdx.x & 3) + 4 * j;
-      if (gi < groups) scl[r * groups + gi] = sv[j];
-    }
-  }
   store_x(0, std::integral_constant<int, 0>{});
   lds_barrier();
 
-  const uint16_t* my_scl = scl + (wave * 16 + (lane & 15)) * groups;
-  auto step = [&](int sl, auto uc) __attribute__((always_inline)) {
-    constexpr int u = decltype(uc)::value;
-    const uint16_t* xl = xs + (u & 1) * XS;
-    // this lane's row scales of the slice's two groups, as (s, s) pairs
-    h2 s2[GPS];
-    if constexpr (kI4) {
+  // lane holds output rows b * 64 + wave * 16 + 4 g + i of activation row 16 t + lane % 16
+  auto flush = [&](int b) __attribute__((always_inline)) {
+    if constexpr (NA == 2) {
 #pragma unroll
-      for (int gs = 0; gs < GPS; gs++) {
-        const _Float16 sc = __builtin_bit_cast(_Float16, my_scl[sl * GPS + gs]);
-        s2[gs] = (h2){sc, sc};
+      for (int i = 0; i < 4; i++) {
+        acc[0][0][i] = acc[0][0][i] + acc[1][0][i];
+        acc[1][0][i] = 0.0f;
       }
     }
+    const int64_t bu = (int64_t)b * spb;
+    const int r0 = b * 64 + wave * 16 + 4 * g;
+    if (bu >= u0 && bu + spb <= u0 + count) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int r = r0 + i;
+        if (r >= P.n) continue;
+        float rs = 1.0f;
+        if constexpr (W == WFmt::kFp8Row) rs = reinterpret_cast<const float*>(P.s)[r];
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+          const int m = 16 * t + (lane & 15);
+          if (m < P.m) {
+            const float v = W == WFmt::kFp8Row ? acc[0][t][i] * rs : acc[0][t][i];
+            P.out[(int64_t)m * P.out_row + r] = f32_to_f16_bits(v);
+          }
+        }
+      }
+    } else {
+      // partial tile [16 MT][64] in slot 2 w + (0: the range's first block, 1: its last)
+      float* tile = P.ws + (int64_t)(2 * blockIdx.x + (b == first_block ? 0 : 1)) * (16 * MT * 64);
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int t = 0; t < MT; t++) tile[(16 * t + (lane & 15)) * 64 + wave * 16 + 4 * g + i] = acc[0][t][i];
+    }
+#pragma unroll
+    for (int t = 0; t < MT; t++) acc[0][t] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
+  };
+
+  auto step = [&](int i, auto uc) __attribute__((always_inline)) {
+    constexpr int u = decltype(uc)::value;
+    const uint16_t* xl = xs + (i & 1) * XS;
+    // this lane's row scales of the unit's two groups, as (s, s) pairs
+    h2 s2[GPS];
+    if constexpr (kI4) {
+      const h2 sp = __builtin_bit_cast(h2, sring[u]);
+#pragma unroll
+      for (int gs = 0; gs < GPS; gs++) s2[gs] = (h2){sp[gs], sp[gs]};
+    }
     // B operands of a group are read from LDS together, the next group's while the
-    // current one's MFMAs run (with one wave per SIMD nothing else hides LDS latency)
+    // current one's MFMAs run
     h8 bb[GPS][4][MT];
     auto read_b = [&](int gs) __attribute__((always_inline)) {
 #pragma unroll
       for (int q = 0; q < 4; q++)
 #pragma unroll
         for (int t = 0; t < MT; t++)
-          bb[gs][q][t] = *reinterpret_cast<const h8*>(xl + (16 * t + (lane & 15)) * kPitch + 128 * gs + 32 * g + 8 * q);
+          bb[gs][q][t] = *reinterpret_cast<const h8*>(xl + 8 * x_piece(t, gs, q, g, lane & 15));
     };
     read_b(0);
     __builtin_amdgcn_sched_barrier(0);
@@ -245,52 +337,98 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    const int nx = sl + kAhead < slices ? sl + kAhead : slices - 1;
-#pragma unroll
-    for (int gs = 0; gs < GPS; gs++) ring[u][gs] = load_chunk<W>(P, lrow, nx * GPS + gs, lane);
-    load_x(nx, uc);                                                  // slot u held slice sl, stored a step ago
-    store_x((u + 1) & 1, std::integral_constant<int, (u + 1) % kAhead>{});  // slice sl + 1
+    if (cs == spb - 1 || i == count - 1) flush(cb);
+    if (++cs == spb) { cs = 0; cb++; }
+    load_unit(uc);                                                   // slot u held unit i, stored a step ago
+    advance_load();
+    store_x((i + 1) & 1, std::integral_constant<int, (u + 1) % kAhead>{});  // unit i + 1
     lds_barrier();
   };
-  int s0 = 0;
-  for (; s0 + kAhead <= slices; s0 += kAhead)
-    static_for<0, kAhead>([&](auto uc) __attribute__((always_inline)) { step(s0 + decltype(uc)::value, uc); });
-  // tail: fewer than kAhead slices, still with static ring slots
+  int i0 = 0;
+  for (; i0 + kAhead <= count; i0 += kAhead)
+    static_for<0, kAhead>([&](auto uc) __attribute__((always_inline)) { step(i0 + decltype(uc)::value, uc); });
+  // tail: fewer than kAhead units, still with static ring slots
   static_for<0, kAhead - 1>([&](auto uc) __attribute__((always_inline)) {
-    if (s0 + decltype(uc)::value < slices) step(s0 + decltype(uc)::value, uc);
+    if (i0 + decltype(uc)::value < count) step(i0 + decltype(uc)::value, uc);
   });
-  if constexpr (NA == 2) {
-#pragma unroll
-    for (int i = 0; i < 4; i++) acc[0][0][i] = acc[0][0][i] + acc[1][0][i];
+}
+
+// out[m][n] of the blocks that several workgroups share: the partial tiles summed in
+// workgroup order (((+0 + first) + second) + ...) [times the fp8 row scale], so the
+// result does not depend on which workgroup finished first.  Workgroup w of this
+// kernel takes the block holding unit_begin(w) when w is the first range boundary
+// inside that block.
+__global__ __launch_bounds__(256) void mfma_fold_kernel(MfmaParams P, int mp) {
+  const int64_t w = (int64_t)blockIdx.x + 1;
+  const int spb = P.spb;
+  const int64_t uw = unit_begin(w, P.units, P.grid);
+  const int64_t b = uw / spb, bu = b * spb;
+  if (uw == bu || unit_begin(w - 1, P.units, P.grid) > bu) return;
+  // partial tiles of the block in workgroup order: workgroups w - 1 .. last
+  __shared__ int slot[kMaxSlices + 1];
+  const int n_slots = (int)(unit_owner(bu + spb - 1, P.units, P.grid) - (w - 1) + 1);
+  if (threadIdx.x < n_slots) {
+    const int64_t o = w - 1 + threadIdx.x;
+    slot[threadIdx.x] = (int)(2 * o + (b == unit_begin(o, P.units, P.grid) / spb ? 0 : 1));
   }
-  // out[m][n]: lane holds rows n0 + 4g + i of activation row 16t + lane % 16
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int r = n0 + 4 * g + i;
-    if (r >= P.n) continue;
-    float rs = 1.0f;
-    if constexpr (W == WFmt::kFp8Row) rs = reinterpret_cast<const float*>(P.s)[r];
-#pragma unroll
-    for (int t = 0; t < MT; t++) {
-      const int m = 16 * t + (lane & 15);
-      if (m < P.m) {
-        const float v = W == WFmt::kFp8Row ? acc[0][t][i] * rs : acc[0][t][i];
-        P.out[(int64_t)m * P.out_row + r] = f32_to_f16_bits(v);
-      }
-    }
+  __syncthreads();
+  const float* rsc = P.ws_row_scale ? reinterpret_cast<const float*>(P.s) : nullptr;
+  for (int e = threadIdx.x; e < mp * 64; e += 256) {
+    const int mi = e >> 6, c = e & 63;
+    const int64_t r = b * 64 + c;
+    if (mi >= P.m || r >= P.n) continue;
+    float v = 0.0f;
+    for (int j = 0; j < n_slots; j++) v = v + P.ws[((int64_t)slot[j] * mp + mi) * 64 + c];
+    if (rsc) v = v * rsc[r];
+    P.out[(int64_t)mi * P.out_row + r] = f32_to_f16_bits(v);
   }
 }
 
-template <WFmt W>
-int launch_mfma(const MfmaParams& P, hipStream_t st, const char* what) {
-  const int blocks = (P.n + 63) / 64;
-  const int mt = (P.m + 15) / 16;
-  switch (mt) {
-    case 1: hipLaunchKernelGGL((mfma_gemm_kernel<W, 1>), dim3(blocks), dim3(256), 0, st, P); break;
-    case 2: hipLaunchKernelGGL((mfma_gemm_kernel<W, 2>), dim3(blocks), dim3(256), 0, st, P); break;
-    case 3: hipLaunchKernelGGL((mfma_gemm_kernel<W, 3>), dim3(blocks), dim3(256), 0, st, P); break;
-    default: hipLaunchKernelGGL((mfma_gemm_kernel<W, 4>), dim3(blocks), dim3(256), 0, st, P); break;
+inline int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (cus[dev] == 0) {
+    int c = 0;
+    cus[dev] = hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && c > 0 ? c : 256;
   }
+  return cus[dev];
+}
+
+// Workgroups of the stream-K grid: the workgroups the chip holds at once, at most
+// one per unit.
+inline int64_t mfma_grid(int64_t units, int mt) {
+  static constexpr int per_cu[4] = {mfma_per_cu<1>(), mfma_per_cu<2>(), mfma_per_cu<3>(), mfma_per_cu<4>()};
+  return std::min<int64_t>((int64_t)per_cu[mt - 1] * device_cus(), units);
+}
+
+inline int64_t mfma_ws_floats(int64_t m, int64_t rows, int64_t cols) {
+  const int mt = (int)((m + 15) / 16);
+  const int64_t units = (rows + 63) / 64 * (cols / kSlice);
+  return 2 * mfma_grid(units, mt) * 16 * mt * 64;
+}
+
+template <WFmt W>
+int launch_mfma(MfmaParams P, float* ws, int64_t ws_floats, hipStream_t st, const char* what) {
+  const int mt = (P.m + 15) / 16;
+  P.spb = P.k / kSlice;
+  P.units = (int64_t)((P.n + 63) / 64) * P.spb;
+  P.grid = (int)mfma_grid(P.units, mt);
+  TT_REQUIRE(P.spb >= 1 && P.units >= 1 && P.grid >= 1, "%s: bad MFMA grid", what);
+  TT_REQUIRE(ws != nullptr && ws_floats >= mfma_ws_floats(P.m, P.n, P.k),
+             "%s: workspace of tt_batched_workspace_floats(m, rows, cols) floats required for m >= 16", what);
+  P.ws = ws;
+  P.ws_row_scale = W == WFmt::kFp8Row ? 1 : 0;
+  const dim3 grid((unsigned)P.grid);
+  switch (mt) {
+    case 1: hipLaunchKernelGGL((mfma_gemm_kernel<W, 1>), grid, dim3(256), 0, st, P); break;
+    case 2: hipLaunchKernelGGL((mfma_gemm_kernel<W, 2>), grid, dim3(256), 0, st, P); break;
+    case 3: hipLaunchKernelGGL((mfma_gemm_kernel<W, 3>), grid, dim3(256), 0, st, P); break;
+    default: hipLaunchKernelGGL((mfma_gemm_kernel<W, 4>), grid, dim3(256), 0, st, P); break;
+  }
+  int rc = check_launch(what);
+  if (rc || P.grid == 1) return rc;
+  hipLaunchKernelGGL(mfma_fold_kernel, dim3((unsigned)(P.grid - 1)), dim3(256), 0, st, P, 16 * mt);
   return check_launch(what);
 }
 
@@ -364,9 +502,15 @@ __global__ __launch_bounds__(256) void argmax_rows_kernel(const uint64_t* partia
 
 }  // namespace
 
+extern "C" int64_t tt_batched_workspace_floats(int64_t m, int64_t rows, int64_t cols) {
+  if (m < 16 || m > 64 || rows <= 0 || cols < kSlice) return 0;
+  return mfma_ws_floats(m, rows, cols);
+}
+
 extern "C" int tt_int4_batched_matvec(const void* packed, int64_t w_row_bytes, const void* scales, int64_t s_row,
                                       const void* x, int64_t x_row, void* out, int64_t out_row, int64_t m,
-                                      int64_t rows, int64_t cols, int64_t group_size, void* stream) {
+                                      int64_t rows, int64_t cols, int64_t group_size, float* workspace,
+                                      int64_t workspace_floats, void* stream) {
   const char* what = "int4_batched_matvec";
   TT_UNSUPPORTED(group_size == 128, "%s: batched int4 uses group size 128", what);
   TT_REQUIRE(cols > 0 && cols % 256 == 0 && cols <= 8192, "%s: cols must be a multiple of 256 up to 8192", what);
@@ -378,9 +522,11 @@ extern "C" int tt_int4_batched_matvec(const void* packed, int64_t w_row_bytes, c
              "%s: null or misaligned pointer / bad row strides", what);
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (m >= 16) {
+    TT_REQUIRE(aligned(scales, 4) && s_row % 2 == 0, "%s: m >= 16 reads scale pairs: 4-byte aligned scales, even row stride",
+               what);
     MfmaParams P{static_cast<const uint8_t*>(packed), w_row_bytes, scales, s_row, static_cast<const uint16_t*>(x),
-                 x_row, static_cast<uint16_t*>(out), out_row, (int)m, (int)rows, (int)cols};
-    return launch_mfma<WFmt::kInt4G128>(P, st, what);
+                 x_row, static_cast<uint16_t*>(out), out_row, nullptr, (int)m, (int)rows, (int)cols};
+    return launch_mfma<WFmt::kInt4G128>(P, workspace, workspace_floats, st, what);
   }
   GemvParams P{};
   P.nseg = 1;
@@ -393,7 +539,7 @@ extern "C" int tt_int4_batched_matvec(const void* packed, int64_t w_row_bytes, c
 
 extern "C" int tt_scaled_batched_matvec(const void* weight, int64_t w_row_bytes, const float* scales, const void* x,
                                         int64_t x_row, void* out, int64_t out_row, int64_t m, int64_t rows,
-                                        int64_t cols, void* stream) {
+                                        int64_t cols, float* workspace, int64_t workspace_floats, void* stream) {
   const char* what = "scaled_batched_matvec";
   TT_REQUIRE(cols > 0 && cols % 256 == 0 && cols <= 8192, "%s: cols must be a multiple of 256 up to 8192", what);
   TT_REQUIRE(m >= 1 && m <= 64, "%s: 1 to 64 activation rows", what);
@@ -405,8 +551,8 @@ extern "C" int tt_scaled_batched_matvec(const void* weight, int64_t w_row_bytes,
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (m >= 16) {
     MfmaParams P{static_cast<const uint8_t*>(weight), w_row_bytes, scales, 1, static_cast<const uint16_t*>(x), x_row,
-                 static_cast<uint16_t*>(out), out_row, (int)m, (int)rows, (int)cols};
-    return launch_mfma<WFmt::kFp8Row>(P, st, what);
+                 static_cast<uint16_t*>(out), out_row, nullptr, (int)m, (int)rows, (int)cols};
+    return launch_mfma<WFmt::kFp8Row>(P, workspace, workspace_floats, st, what);
   }
   GemvParams P{};
   P.nseg = 1;
