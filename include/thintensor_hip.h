@@ -411,16 +411,22 @@ int tt_moe_router_matvec_topk(const void* weight, int w_dtype, int64_t w_row, co
  * an fp16/bf16 dtype (otherwise the two operators run one after the other).  Outputs and
  * bits are those of tt_add_rms_norm then tt_moe_router_matvec_topk(hidden = norm_out).
  * `tokens` rows at once: left/right/residual_out/norm_out [tokens, hidden_size],
- * indices/scores [tokens, top_k], all contiguous (one workgroup per token).
+ * indices/scores [tokens, top_k], all contiguous.
  * Fuses the reference's add_rms_norm (triton_kernels.py:5646-5667) and
  * moe_router_matvec_topk (:5826-5860) as its MoE layer calls them back to back
- * (gpu_runtime.py:9465-9513); the reference has no single entry point for the pair. */
+ * (gpu_runtime.py:9465-9513); the reference has no single entry point for the pair.
+ * With a workspace of tt_norm_router_workspace_bytes(tokens) bytes, zero-filled before
+ * its first use, each token's router rows are spread over ceil(experts / 4)
+ * workgroups and the last one to finish takes the top-k (it leaves the workspace
+ * zeroed; calls sharing one workspace must be ordered); without one, a single
+ * workgroup per token does everything.  Same bits either way. */
+int64_t tt_norm_router_workspace_bytes(int64_t tokens);
 int tt_add_rms_norm_router_topk(const void* left, const void* right, void* residual_out, int x_dtype,
                                 const void* norm_weight, int norm_w_dtype, void* norm_out, int norm_dtype,
                                 int64_t hidden_size, float eps, const void* weight, int w_dtype, int64_t w_row,
                                 const void* bias, int bias_dtype, int64_t experts, int64_t top_k, int renormalize,
                                 int32_t* indices_out, void* scores_out, int score_dtype, int64_t tokens,
-                                void* stream);
+                                void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Top-k + softmax on given logits.  Replaces TritonDecodeBackend.moe_router_topk
  * (triton_kernels.py:5803-5824; kernel :2821-2851). */

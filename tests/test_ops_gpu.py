@@ -174,8 +174,10 @@ def test_router(backend, device, renorm, with_bias):
     (64, 2880, 4, True, "f16", False),    # more experts than one launch takes: two launches
     (32, 5120, 4, True, None, False),     # hidden above 4096: two launches
 ])
-def test_add_rms_norm_router(backend, device, E, H, k, renorm, bias_dtype, wbf16):
-    """The combined launch equals add_rms_norm followed by the router on its output."""
+@pytest.mark.parametrize("split", [True, False])
+def test_add_rms_norm_router(backend, device, E, H, k, renorm, bias_dtype, wbf16, split):
+    """The combined launch equals add_rms_norm followed by the router on its output,
+    with the router rows over ceil(E / 4) workgroups (split) or in one workgroup."""
     g = rng(E * 7 + H + k)
     a, b = f16_normal(g, H), f16_normal(g, H, 0.5)
     nw = f16_normal(g, H, 0.1)
@@ -196,7 +198,7 @@ def test_add_rms_norm_router(backend, device, E, H, k, renorm, bias_dtype, wbf16
     backend.add_rms_norm_router_topk(to_torch(a, device), to_torch(b, device), res, to_torch(nw, device), normed, 1e-5,
                                      to_torch(w, device, bf16=wbf16), idx, sc,
                                      bias=None if bias is None else to_torch(bias, device, bf16=bias_dtype == "bf16"),
-                                     renormalize=renorm)
+                                     renormalize=renorm, split=split)
     want_res = np.empty(H, dtype=np.float16)
     want_n = np.empty(H, dtype=np.float16)
     oracle.lib().tto_add_rms_norm(P(a), P(b), P(want_res), oracle.F16, P(nw), oracle.F16, P(want_n), oracle.F16, H, 1e-5)
@@ -216,8 +218,9 @@ def test_add_rms_norm_router(backend, device, E, H, k, renorm, bias_dtype, wbf16
 
 @pytest.mark.parametrize("tokens,H", [(8, 2880), (3, 5120)])
 def test_add_rms_norm_router_tokens(backend, device, tokens, H):
-    """Several tokens in one call (one workgroup each; above 4096 the per-token
-    operators) equal the single-token calls."""
+    """Several tokens in one call (above 4096 the per-token operators) equal the
+    single-token calls, and the split launch equals the one-workgroup launch on two
+    calls in a row (the arrival counters are left at zero)."""
     E, k = 32, 4
     g = rng(tokens + H)
     a, b = f16_normal(g, (tokens, H)), f16_normal(g, (tokens, H), 0.5)
@@ -238,6 +241,16 @@ def test_add_rms_norm_router_tokens(backend, device, tokens, H):
         assert_bits_equal(from_torch_bits(normed[t]), from_torch_bits(n1), f"normed {t}")
         assert torch.equal(idx[t], i1)
         assert_bits_equal(from_torch_bits(sc[t]), from_torch_bits(s1), f"scores {t}")
+    for _ in range(2):
+        r2, n2 = torch.empty_like(res), torch.empty_like(res)
+        i2, s2 = torch.empty_like(idx), torch.empty_like(sc)
+        backend.add_rms_norm_router_topk(T(a), T(b), r2, T(nw), n2, 1e-5, T(w), i2, s2, bias=T(bias), renormalize=True,
+                                         split=False)
+        assert torch.equal(res.view(torch.int16), r2.view(torch.int16))
+        assert torch.equal(normed.view(torch.int16), n2.view(torch.int16))
+        assert torch.equal(idx, i2) and torch.equal(sc.view(torch.int16), s2.view(torch.int16))
+        backend.add_rms_norm_router_topk(T(a), T(b), res, T(nw), normed, 1e-5, T(w), idx, sc, bias=T(bias),
+                                         renormalize=True)
 
 
 def test_router_topk_on_logits_with_ties(backend, device):

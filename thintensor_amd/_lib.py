@@ -120,7 +120,8 @@ SIGNATURES: dict[str, list] = {
     "tt_moe_router_matvec_topk": [_P, _I, _L, _P, _I, _L, _P, _I, _L, _L, _I, _P, _P, _I, _P],
     "tt_moe_router_topk": [_P, _I, _L, _L, _I, _P, _P, _I, _P],
     "tt_add_rms_norm_router_topk": [_P, _P, _P, _I, _P, _I, _P, _I, _L, _F, _P, _I, _L, _P, _I, _L, _L, _I, _P, _P,
-                                    _I, _L, _P],
+                                    _I, _L, _P, _L, _P],
+    "tt_norm_router_workspace_bytes": [_L],
     "tt_matvec_bias_rows": [_P, _I, _L, _P, _P, _I, _L, _P, _I, _L, _L, _L, _L, _P],
     "tt_mxfp_lowbit_selected_swiglu_tokens": [_P, _L, _L, _P, _L, _L, _I, _P, _I, _L, _P, _L, _P, _I, _L, _F, _F, _P,
                                               _I, _L, _L, _L, _L, _P],
@@ -154,6 +155,7 @@ SIGNATURES: dict[str, list] = {
 }
 _RESTYPES = {"tt_last_error": ctypes.c_char_p, "tt_matvec_argmax_partials": ctypes.c_int64,
              "tt_batched_workspace_floats": ctypes.c_int64,
+             "tt_norm_router_workspace_bytes": ctypes.c_int64,
              "tt_stream_read_waves": ctypes.c_int64,
              "tt_matvec_argmax_batched_partials": ctypes.c_int64, "tt_archive_find": ctypes.c_int64,
              "tt_archive_data": ctypes.c_void_p}

@@ -1153,6 +1153,7 @@ class HipDecodeBackend:
         *,
         bias: torch.Tensor | None = None,
         renormalize: bool,
+        split: bool = True,
     ) -> tuple[torch.Tensor, torch.Tensor]:
         """``add_rms_norm`` then ``moe_router_matvec_topk`` on its output, as one launch
         where the shapes allow (<= 32 experts, hidden <= 4096, one activation dtype).
@@ -1160,8 +1161,9 @@ class HipDecodeBackend:
         No single reference operator: the reference's MoE layer calls add_rms_norm
         (triton_kernels.py:5646-5667) and moe_router_matvec_topk (:5826-5860) back to
         back (gpu_runtime.py:9465-9513).  Outputs and bits equal that pair's.  The vectors
-        may hold several tokens ([tokens, hidden]; indices/scores [tokens, top_k]), one
-        workgroup each."""
+        may hold several tokens ([tokens, hidden]; indices/scores [tokens, top_k]).
+        ``split`` spreads each token's router rows over ceil(experts / 4) workgroups
+        (a zeroed workspace kept by the backend); otherwise one workgroup per token."""
         experts, hidden_size = map(int, router_weight.shape)
         n = hidden_size
         tokens = int(left.numel()) // n if n else 0
@@ -1180,6 +1182,14 @@ class HipDecodeBackend:
             raise ValueError("router bias does not match expert count")
         self._check_indices(indices_out)
         _require_cuda(left, right, residual_out, norm_weight, norm_out, router_weight, indices_out, scores_out)
+        ws = None
+        if split:
+            need = int(self.lib.tt_norm_router_workspace_bytes(tokens))
+            ws = getattr(self, "_norm_router_ws", None)
+            if ws is None or ws.numel() < need:
+                # arrival counters and logits; every call leaves the counters at zero
+                ws = torch.zeros(need, device=self.device, dtype=torch.uint8)
+                self._norm_router_ws = ws
         rc = self.lib.tt_add_rms_norm_router_topk(
             left.data_ptr(), right.data_ptr(), residual_out.data_ptr(), _code(left, "add_rms_norm"),
             norm_weight.data_ptr(), _code(norm_weight, "add_rms_norm"), norm_out.data_ptr(),
@@ -1187,7 +1197,7 @@ class HipDecodeBackend:
             router_weight.stride(0), bias.data_ptr() if bias is not None else None,
             _code(bias, "bias") if bias is not None else _lib.F32, experts, int(indices_out.numel()) // tokens,
             int(bool(renormalize)), indices_out.data_ptr(), scores_out.data_ptr(), _code(scores_out, "scores"),
-            tokens, _stream(left),
+            tokens, ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0, _stream(left),
         )
         _lib.check(rc, "add_rms_norm_router_topk")
         return indices_out, scores_out

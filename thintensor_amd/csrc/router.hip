@@ -382,6 +382,132 @@ __global__ __launch_bounds__(1024) void norm_router_kernel(const NormRouterParam
   }
 }
 
+// The same operator over ceil(E / 4) workgroups of four waves per token: every
+// workgroup forms the residual and the normalized vector itself (the norm inputs are a
+// few KB; same partition, order and rounding as add_rms_norm_kernel, so every copy has
+// the same bits) while its waves' router rows arrive, wave w of workgroup g computes
+// expert 4 g + w, and the workgroup stores its logits in the token's workspace slot
+// and counts itself in the slot's arrival counter.  The last workgroup to arrive reads
+// the E logits, takes the top-k and resets the counter to zero; no workgroup waits for
+// another.  Logits and counters use device-scope atomic loads and stores, coherent
+// across the XCDs' caches; a workgroup's logit stores have completed (vector memory
+// counter drained) before it counts itself.  Workgroup 0 stores residual_out and
+// norm_out.  Same bits as norm_router_kernel.
+constexpr int kNormRouterSlot = 64;   // ints per token: counter at 0, logits at 32 + e
+
+template <typename WT, typename XT, typename BT, typename OT>
+__global__ __launch_bounds__(256) void norm_router_split_kernel(const NormRouterParams P, int* ws) {
+  constexpr Fmt F = std::is_same_v<WT, bf16_t> ? Fmt::kBF16W : Fmt::kF16W;
+  __shared__ float red[4];
+  __shared__ int last;
+  __shared__ uint4 xs[4096 / 8];   // normalized vector, XT bits
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int n = P.H;
+  const int nchunks = n >> 5;
+  const int64_t tok = blockIdx.y;
+  const XT* const left = reinterpret_cast<const XT*>(P.left) + tok * n;
+  const XT* const right = reinterpret_cast<const XT*>(P.right) + tok * n;
+  int* const slot = ws + tok * kNormRouterSlot;
+
+  // ---- every load before the first wait: the norm inputs (kNormPieces 16-byte pieces
+  // of each vector per thread), then this wave's router row and bias
+  const int nq = n >> 3;
+  const int t = threadIdx.x;
+  uint4 pa[kNormPieces], pb[kNormPieces], pw[kNormPieces];
+#pragma unroll
+  for (int k = 0; k < kNormPieces; k++) {
+    const int pi = t + 256 * k;
+    const int pc = pi < nq ? pi : nq - 1;
+    pa[k] = reinterpret_cast<const uint4*>(left)[pc];
+    pb[k] = reinterpret_cast<const uint4*>(right)[pc];
+    pw[k] = reinterpret_cast<const uint4*>(P.norm_w)[pc];
+  }
+  const int e = 4 * blockIdx.x + wave;
+  const int er = e < P.E ? e : P.E - 1;
+  Raw<64> wr[2];
+#pragma unroll
+  for (int r = 0; r < 2; r++) {
+    int j = r * 64 + lane;
+    j = j < nchunks ? j : nchunks - 1;
+    wr[r] = load_raw<64>(reinterpret_cast<const uint8_t*>(P.w) + ((int64_t)er * P.w_row + 32 * j) * 2);
+  }
+  const BT* bsrc = reinterpret_cast<const BT*>(P.bias != nullptr ? P.bias : P.w);
+  const BT braw = bsrc[er];
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- add + RMSNorm in add_rms_norm_kernel's partition and order
+  float res[kNormPieces][8];
+  float ss = 0.0f;
+#pragma unroll
+  for (int k = 0; k < kNormPieces; k++)
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+      res[k][c] = round_bf16(piece_f32<XT>(pa[k], c) + piece_f32<XT>(pb[k], c));
+      if (8 * (t + 256 * k) + c < n) ss = __builtin_fmaf(res[k][c], res[k][c], ss);
+    }
+  ss = xor_sum(ss, 1, 64);
+  if (lane == 0) red[wave] = ss;
+  __syncthreads();
+  const float total = (red[0] + red[1]) + (red[2] + red[3]);
+  const float inv = 1.0f / __builtin_sqrtf(total / (float)n + P.eps);
+  XT* const residual_out = reinterpret_cast<XT*>(P.residual_out) + tok * n;
+  XT* const norm_out = reinterpret_cast<XT*>(P.norm_out) + tok * n;
+#pragma unroll
+  for (int k = 0; k < kNormPieces; k++) {
+    const int pi = t + 256 * k;
+    if (pi < nq) {
+      float o[8];
+#pragma unroll
+      for (int c = 0; c < 8; c++) o[c] = (res[k][c] * inv) * piece_f32<XT>(pw[k], c);
+      const uint4 op = pack_piece<XT>(o);
+      if (blockIdx.x == 0) {
+        reinterpret_cast<uint4*>(residual_out)[pi] = pack_piece<XT>(res[k]);
+        reinterpret_cast<uint4*>(norm_out)[pi] = op;
+      }
+      xs[pi] = op;
+    }
+  }
+  __syncthreads();
+
+  // ---- this wave's router row (router_rows_held's arithmetic) on the vector in LDS
+  float acc = 0.0f;
+#pragma unroll
+  for (int r = 0; r < 2; r++) {
+    int j = r * 64 + lane;
+    j = j < nchunks ? j : nchunks - 1;
+    Raw<64> xr;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const uint4 v = xs[j * 4 + q];
+      xr.w[4 * q] = v.x;
+      xr.w[4 * q + 1] = v.y;
+      xr.w[4 * q + 2] = v.z;
+      xr.w[4 * q + 3] = v.w;
+    }
+    const bool cv = r * 64 + lane < nchunks;
+    const float p = chunk_dot<F, XT>(wr[r], xr.w);
+    if (r == 0) acc = 0.0f + (cv ? p : 0.0f);
+    else if (nchunks > 64) acc = acc + (cv ? p : 0.0f);
+  }
+  float v = round_bf16(xor_sum(acc, 1, 64));
+  if (P.bias != nullptr) v = round_bf16(v + to_f32(braw));
+  if (e < P.E && lane == 0)
+    __hip_atomic_store(reinterpret_cast<float*>(slot) + 32 + e, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0)
+    last = __hip_atomic_fetch_add(slot, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (int)gridDim.x - 1;
+  __syncthreads();
+  if (!last || wave != 0) return;
+  const float l0 = lane < P.E
+                       ? __hip_atomic_load(reinterpret_cast<float*>(slot) + 32 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                       : 0.0f;
+  wave_topk<OT>(l0, 0.0f, P.E, P.top_k, P.renorm != 0, P.idx_out + tok * P.top_k,
+                reinterpret_cast<OT*>(P.score_out) + tok * P.top_k);
+  if (lane == 0) __hip_atomic_store(slot, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 template <typename LT, typename OT>
 __global__ __launch_bounds__(64) void topk_kernel(const void* logits_in, int E, int top_k, int renorm, int32_t* idx_out,
                                                   void* score_out) {
@@ -453,12 +579,17 @@ extern "C" int tt_moe_router_topk(const void* logits, int logits_dtype, int64_t 
   });
 }
 
+extern "C" int64_t tt_norm_router_workspace_bytes(int64_t tokens) {
+  return tokens > 0 ? tokens * kNormRouterSlot * (int64_t)sizeof(int) : 0;
+}
+
 extern "C" int tt_add_rms_norm_router_topk(const void* left, const void* right, void* residual_out, int x_dtype,
                                            const void* norm_weight, int norm_w_dtype, void* norm_out, int norm_dtype,
                                            int64_t hidden_size, float eps, const void* weight, int w_dtype,
                                            int64_t w_row, const void* bias, int bias_dtype, int64_t experts,
                                            int64_t top_k, int renormalize, int32_t* indices_out, void* scores_out,
-                                           int score_dtype, int64_t tokens, void* stream) {
+                                           int score_dtype, int64_t tokens, void* workspace, int64_t workspace_bytes,
+                                           void* stream) {
   const char* what = "add_rms_norm_router_topk";
   TT_REQUIRE(tokens >= 1 && tokens <= 65535, "%s: bad token count", what);
   TT_REQUIRE(left && right && residual_out && norm_weight && norm_out, "%s: null pointer", what);
@@ -501,8 +632,15 @@ extern "C" int tt_add_rms_norm_router_topk(const void* left, const void* right, 
             set_error("%s: unsupported dtypes", what);
             return TT_ERR_UNSUPPORTED;
           } else {
-            hipLaunchKernelGGL((norm_router_kernel<WT, XT, BT, OT>), dim3((unsigned)tokens), dim3(1024), 0,
-                               static_cast<hipStream_t>(stream), P);
+            if (workspace != nullptr && workspace_bytes >= tt_norm_router_workspace_bytes(tokens) &&
+                aligned(workspace, 4)) {
+              hipLaunchKernelGGL((norm_router_split_kernel<WT, XT, BT, OT>), dim3((unsigned)((experts + 3) / 4),
+                                 (unsigned)tokens), dim3(256), 0, static_cast<hipStream_t>(stream), P,
+                                 static_cast<int*>(workspace));
+            } else {
+              hipLaunchKernelGGL((norm_router_kernel<WT, XT, BT, OT>), dim3((unsigned)tokens), dim3(1024), 0,
+                                 static_cast<hipStream_t>(stream), P);
+            }
             return check_launch(what);
           }
         });
