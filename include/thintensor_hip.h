@@ -382,7 +382,9 @@ int tt_record_token(const int64_t* token_dev, const int32_t* position_dev, const
 
 /* ---------------------------------------------------------------- attention / router */
 
-/* Floats of scratch tt_single_token_gqa_attention needs. */
+/* Floats of scratch tt_single_token_gqa_attention needs.  The scratch must be
+ * zero-filled before its first use (its head holds arrival counters that every call
+ * leaves at zero); calls sharing one scratch must be ordered (same stream). */
 int tt_attention_scratch_floats(int64_t heads, int64_t max_tokens, int64_t head_dim);
 
 /* Single-token GQA attention over keys/values [kv_heads, tokens, D] (strides in

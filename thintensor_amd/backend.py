@@ -1059,7 +1059,8 @@ class HipDecodeBackend:
     def _attention_scratch(self, heads: int, max_tokens: int, head_dim: int) -> torch.Tensor:
         need = int(self.lib.tt_attention_scratch_floats(heads, max_tokens, head_dim))
         if self._attention_partials is None or self._attention_partials.numel() < need:
-            self._attention_partials = torch.empty(need, device=self.device, dtype=torch.float32)
+            # arrival counters at the head (zero-filled once; every call leaves them at zero)
+            self._attention_partials = torch.zeros(need, device=self.device, dtype=torch.float32)
         return self._attention_partials
 
     def single_token_gqa_attention(

@@ -548,8 +548,178 @@ __global__ __launch_bounds__(64 * kHeadWaves) void attn_head_kernel(AttnParams P
   store<T>(reinterpret_cast<T*>(P.out) + (int64_t)h * D + lane, acc / den);
 }
 
+// One workgroup per (KV head, chunk) with one wave per query head of that KV head
+// (contiguous head_dim-64 caches, whole-chunk capacity): the chunk's K and V blocks are
+// read once per KV head -- each CU moves 16 KB instead of a whole sequence -- staged in
+// LDS (K swizzled as in attn_head_kernel, V rows of tokens past the count zeroed), and
+// wave g computes the chunk partial of query head G kvh + g with the arithmetic of
+// attn_partial64_kernel.  The partials go to the scratch with device-scope atomic stores;
+// the workgroup counts itself in its KV head's arrival counter once its stores have
+// completed, and the last of the head's active chunks combines every query head of the
+// KV head in chunk order (the arithmetic of attn_combine64_kernel, partials read with
+// device-scope atomic loads) and resets the counter to zero.  No workgroup waits for
+// another.  Same bits as attn_head_kernel.
+__device__ __forceinline__ void st_dev(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ float ld_dev(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <typename T, typename SKT, int G>
+__global__ __launch_bounds__(64 * G) void attn_kvchunk_kernel(AttnParams P, int* counters) {
+  constexpr int D = 64;
+  const int c = blockIdx.x, kvh = blockIdx.y;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int h = kvh * G + wave;
+  constexpr int nthr = 64 * G;
+  __shared__ uint4 ks[kChunk * D / 8], vs_s[kChunk * D / 8];
+  __shared__ float q_s[G][D];
+  __shared__ float p_s[G][kChunk];
+  __shared__ int last;
+  const float ninf = __builtin_bit_cast(float, 0xff800000u);
+  // every load before the active count is known (chunks below max_chunks are inside
+  // the capacity): K and V pieces of the chunk, this wave's query row
+  const uint4* kblk = reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(P.keys) + kvh * P.k_head) +
+                      (int64_t)c * (kChunk * D / 8);
+  const uint4* vblk = reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(P.values) + kvh * P.v_head) +
+                      (int64_t)c * (kChunk * D / 8);
+  constexpr int kPer = kChunk * D / 8 / nthr;   // 16-byte pieces per thread
+  uint4 kr[kPer], vr[kPer];
+#pragma unroll
+  for (int j = 0; j < kPer; j++) {
+    kr[j] = kblk[(int)threadIdx.x + nthr * j];
+    vr[j] = vblk[(int)threadIdx.x + nthr * j];
+  }
+  const T qraw = reinterpret_cast<const T*>(P.q)[(int64_t)h * D + lane];
+  const int T_act = min(P.tokens_dev ? P.tokens_dev[0] + P.tokens : P.tokens, P.max_tokens);
+  const int nc = T_act > 0 ? (T_act + kChunk - 1) / kChunk : 0;
+  if (c >= nc) return;
+  const int nt = min(kChunk, T_act - c * kChunk);
+#pragma unroll
+  for (int j = 0; j < kPer; j++) {
+    const int pidx = (int)threadIdx.x + nthr * j;
+    const int r = pidx >> 3, col = pidx & 7;
+    ks[r * 8 + (col ^ (r & 7))] = kr[j];
+    const uint32_t keep = r < nt ? ~0u : 0u;
+    vs_s[pidx] = uint4{vr[j].x & keep, vr[j].y & keep, vr[j].z & keep, vr[j].w & keep};
+  }
+  q_s[wave][lane] = to_f32(qraw);
+  __syncthreads();
+
+  // ---- chunk partial of query head h (lane = token, then lane = dimension)
+  const int t = c * kChunk + lane;
+  const bool valid = t < T_act;
+  uint32_t krow[8][4];
+#pragma unroll
+  for (int d = 0; d < 8; d++) {
+    const uint4 k = ks[lane * 8 + (d ^ (lane & 7))];
+    krow[d][0] = k.x; krow[d][1] = k.y; krow[d][2] = k.z; krow[d][3] = k.w;
+  }
+  const float* qw = q_s[wave];
+  float sc = 0.0f;
+#pragma unroll
+  for (int i = 0; i < D / 8; i++) {
+    if ((i & 3) == 0) asm volatile("" : "+v"(sc)::"memory");
+    const uint32_t* kw = krow[i];
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      const float kv = (e & 1) ? hi_f32<T>(kw[e >> 1]) : lo_f32<T>(kw[e >> 1]);
+      sc = __builtin_fmaf(qw[8 * i + e], kv, sc);
+    }
+  }
+  const float s = valid ? sc * P.scale : ninf;
+  float m = s;
+  m = fmaxf(m, xor_partner<1>(m));
+  m = fmaxf(m, xor_partner<2>(m));
+  m = fmaxf(m, xor_partner<4>(m));
+  m = fmaxf(m, xor_partner<8>(m));
+  m = fmaxf(m, xor_partner<16>(m));
+  m = fmaxf(m, xor_partner<32>(m));
+  const float p = valid ? exp_f32(s - m) : 0.0f;
+  const float l = xor_sum(p, 1, 64);
+  float* p_w = p_s[wave];
+  p_w[lane] = p;
+  __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's p stores done
+  __builtin_amdgcn_wave_barrier();
+  const T* vsp = reinterpret_cast<const T*>(vs_s);
+  float o = 0.0f;
+#pragma unroll
+  for (int tt = 0; tt < kChunk; tt++) {
+    if ((tt & 31) == 0) asm volatile("" : "+v"(o)::"memory");
+    o = __builtin_fmaf(p_w[tt], to_f32(vsp[tt * D + lane]), o);
+  }
+  const int64_t slot = (int64_t)h * P.max_chunks + c;
+  if (lane == 0) {
+    st_dev(P.part_m + slot, m);
+    st_dev(P.part_l + slot, l);
+  }
+  st_dev(P.part_o + slot * D + lane, o);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0)
+    last = __hip_atomic_fetch_add(counters + kvh, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nc - 1;
+  __syncthreads();
+  if (!last) return;
+
+  // ---- combine of query head h in chunk order (attn_combine64_kernel's arithmetic)
+  const float* pm = P.part_m + (int64_t)h * P.max_chunks;
+  const float* pl = P.part_l + (int64_t)h * P.max_chunks;
+  const float* po = P.part_o + (int64_t)h * P.max_chunks * D + lane;
+  const bool has_sink = P.sinks != nullptr;
+  const float sink = has_sink ? to_f32(reinterpret_cast<const SKT*>(P.sinks)[h]) : 0.0f;
+  float M = has_sink ? sink : ninf;
+  for (int c0 = 0; c0 < nc; c0 += 64) {
+    float mm = c0 + lane < nc ? ld_dev(pm + c0 + lane) : ninf;
+    mm = fmaxf(mm, xor_partner<1>(mm));
+    mm = fmaxf(mm, xor_partner<2>(mm));
+    mm = fmaxf(mm, xor_partner<4>(mm));
+    mm = fmaxf(mm, xor_partner<8>(mm));
+    mm = fmaxf(mm, xor_partner<16>(mm));
+    mm = fmaxf(mm, xor_partner<32>(mm));
+    M = fmaxf(M, mm);
+  }
+  float den = has_sink ? exp_f32(sink - M) : 0.0f;
+  float acc = 0.0f;
+  constexpr int kBlk = 16;
+  for (int c0 = 0; c0 < nc; c0 += 64) {
+    const int n = min(64, nc - c0);
+    const float e = c0 + lane < nc ? exp_f32(ld_dev(pm + c0 + lane) - M) : 0.0f;
+    const float lv = c0 + lane < nc ? ld_dev(pl + c0 + lane) : 0.0f;
+    for (int c1 = 0; c1 < n; c1 += kBlk) {
+      float ov[kBlk];
+#pragma unroll
+      for (int u = 0; u < kBlk; u++) {
+        const int cc = c0 + c1 + u;
+        ov[u] = cc < nc ? ld_dev(po + (int64_t)cc * D) : 0.0f;
+      }
+#pragma unroll
+      for (int u = 0; u < kBlk; u++) {
+        if (c1 + u < n) {
+          const float ec = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e), c1 + u));
+          const float lc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lv), c1 + u));
+          den = __builtin_fmaf(lc, ec, den);
+          acc = __builtin_fmaf(ov[u], ec, acc);
+        }
+      }
+    }
+  }
+  store<T>(reinterpret_cast<T*>(P.out) + (int64_t)h * D + lane, acc / den);
+  if (threadIdx.x == 0) __hip_atomic_store(counters + kvh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 template <typename T, int G>
-static int launch_attn(const AttnParams& P, int sink_dtype, bool contiguous64, hipStream_t st) {
+static int launch_attn(const AttnParams& P, int sink_dtype, bool contiguous64, int* counters, hipStream_t st) {
+  if constexpr (G <= 8) {
+    if (contiguous64 && counters != nullptr) {
+      const dim3 grid((unsigned)P.max_chunks, (unsigned)P.kv_heads), block(64 * G);
+      switch (sink_dtype) {
+        case TT_BF16: hipLaunchKernelGGL((attn_kvchunk_kernel<T, bf16_t, G>), grid, block, 0, st, P, counters); break;
+        case TT_F32: hipLaunchKernelGGL((attn_kvchunk_kernel<T, float, G>), grid, block, 0, st, P, counters); break;
+        default: hipLaunchKernelGGL((attn_kvchunk_kernel<T, f16_t, G>), grid, block, 0, st, P, counters); break;
+      }
+      return check_launch("gqa_attention");
+    }
+  }
   if (contiguous64 && P.max_chunks <= kHeadMaxChunks) {
     switch (sink_dtype) {
       case TT_BF16: hipLaunchKernelGGL((attn_head_kernel<T, bf16_t>), dim3(P.heads), dim3(64 * kHeadWaves), 0, st, P); break;
@@ -587,9 +757,14 @@ static int launch_attn(const AttnParams& P, int sink_dtype, bool contiguous64, h
 
 using namespace tt;
 
+// Scratch: kAttnCounters arrival counters of the single-launch path (one per KV head,
+// at fixed offsets whatever the shape, left at zero by every call), then the chunk
+// partials (m, l, o) per query head.
+constexpr int kAttnCounters = 1024;
+
 extern "C" int tt_attention_scratch_floats(int64_t heads, int64_t max_tokens, int64_t head_dim) {
   const int64_t chunks = (max_tokens + kChunk - 1) / kChunk;
-  return (int)(heads * chunks * (2 + head_dim));
+  return (int)(kAttnCounters + heads * chunks * (2 + head_dim));
 }
 
 extern "C" int tt_single_token_gqa_attention(const void* q, const void* keys, const void* values, int dtype,
@@ -606,7 +781,9 @@ extern "C" int tt_single_token_gqa_attention(const void* q, const void* keys, co
   TT_REQUIRE(tokens_dev == nullptr || (tokens >= 0 && tokens <= 1), "%s: device token count offset must be 0 or 1", what);
   TT_REQUIRE(max_tokens > 0, "%s: bad max_tokens", what);
   const int64_t chunks = (max_tokens + kChunk - 1) / kChunk;
-  TT_REQUIRE(scratch_floats >= heads * chunks * (2 + head_dim), "%s: scratch too small", what);
+  TT_REQUIRE(scratch_floats >= kAttnCounters + heads * chunks * (2 + head_dim), "%s: scratch too small", what);
+  int* counters = kv_heads <= kAttnCounters ? reinterpret_cast<int*>(scratch) : nullptr;
+  scratch += kAttnCounters;
   TT_REQUIRE(chunks <= 65535 && kv_heads <= 65535, "%s: sequence too long", what);
   AttnParams P{};
   P.q = q; P.keys = keys; P.values = values;
@@ -628,11 +805,11 @@ extern "C" int tt_single_token_gqa_attention(const void* q, const void* keys, co
   auto by_g = [&](auto t) -> int {
     using T = decltype(t);
     switch (G) {
-      case 1: return launch_attn<T, 1>(P, sink_dtype, c64, st);
-      case 2: return launch_attn<T, 2>(P, sink_dtype, c64, st);
-      case 4: return launch_attn<T, 4>(P, sink_dtype, c64, st);
-      case 8: return launch_attn<T, 8>(P, sink_dtype, c64, st);
-      case 16: return launch_attn<T, 16>(P, sink_dtype, c64, st);
+      case 1: return launch_attn<T, 1>(P, sink_dtype, c64, counters, st);
+      case 2: return launch_attn<T, 2>(P, sink_dtype, c64, counters, st);
+      case 4: return launch_attn<T, 4>(P, sink_dtype, c64, counters, st);
+      case 8: return launch_attn<T, 8>(P, sink_dtype, c64, counters, st);
+      case 16: return launch_attn<T, 16>(P, sink_dtype, c64, counters, st);
     }
     set_error("%s: query heads per KV head must be 1, 2, 4, 8 or 16 (got %d)", what, G);
     return TT_ERR_UNSUPPORTED;
