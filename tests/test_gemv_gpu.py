@@ -52,6 +52,7 @@ INT4_CASES = [
     (7, 160, 32, np.float32, "f16", "f32"),        # 5 chunks on 16 lanes
     (96, 5632, 128, np.float16, "f16", "f16"),     # 16 lanes per row, 11 rounds: blocks of four and a tail
     (2048, 6144, 128, np.float16, "f16", "f16"),   # three rounds, requested together
+    (16400, 5120, 128, np.float16, "f16", "f16"),  # four rows per wave of five rounds, ragged last batch
 ]
 
 

@@ -227,10 +227,13 @@ int launch_int4g128_lpr(int rpw, const void* W, int64_t w_row, const void* S, in
 }
 
 // Rows per wave of the single-matrix path: enough waves to cover the chip several
-// times over before a wave takes more than one row.
-inline int int4g128_rows_per_wave(int64_t rows, int lpr) {
+// times over before a wave takes more than one row.  Rows of several rounds take four
+// rows per wave from half the lane groups (17920 x 5120: 15.5 -> 14.5 us; single-round
+// rows of 8192 x 2048 are faster at two).
+inline int int4g128_rows_per_wave(int64_t rows, int64_t cols, int lpr) {
   const int64_t groups = rows * lpr / 64;   // lane groups needed at one row each
-  if (groups >= 16384) return 4;
+  const bool multi_round = cols / 32 > lpr;
+  if (groups >= 16384 || (multi_round && groups >= 8192)) return 4;
   if (groups >= 2048) return 2;
   return 1;
 }
@@ -245,7 +248,7 @@ inline bool int4g128_fits(int64_t rows, int64_t w_row, int64_t s_row, int64_t s_
 template <typename XT>
 int launch_int4g128(int lpr, const void* W, int64_t w_row, const void* S, int64_t s_row, int64_t s_grp, const void* x,
                     void* y, int rows, int cols, hipStream_t st) {
-  const int rpw = int4g128_rows_per_wave(rows, lpr);
+  const int rpw = int4g128_rows_per_wave(rows, cols, lpr);
   if (lpr == 64) return launch_int4g128_lpr<XT, 64>(rpw, W, w_row, S, s_row, s_grp, x, y, rows, cols, st);
   if (lpr == 32) return launch_int4g128_lpr<XT, 32>(rpw, W, w_row, S, s_row, s_grp, x, y, rows, cols, st);
   return launch_int4g128_lpr<XT, 16>(rpw, W, w_row, S, s_row, s_grp, x, y, rows, cols, st);
