@@ -47,6 +47,7 @@ def _parse() -> argparse.Namespace:
     p.add_argument("--roofline-only", action="store_true",
                    help="only the int4 roofline phase (used for hardware-counter runs)")
     p.add_argument("--ternary-only", action="store_true", help="only the ternary expert GEMV phase")
+    p.add_argument("--cfg2-only", action="store_true", help="only the cfg2 q2/q1 affine GEMV phase")
     p.add_argument("--batched-only", action="store_true",
                    help="only the batched small-M GEMM phase (used for MFMA counter runs)")
     return p.parse_args()
@@ -182,6 +183,46 @@ def affine_lowbit_phase(be, bits: int, rows: int, cols: int, copies: int, seed: 
     del W, sz
     return {"bits": bits, "shape": [rows, cols], "group": group, "us_per_call": t * 1e6, "bytes_per_call": nbytes,
             "GB_s": nbytes / t / 1e9, "frac_of_hbm_peak": nbytes / t / 1e9 / HBM_PEAK_GBS, "rotated_copies": copies}
+
+
+def cfg2_phase(be, seed: int) -> dict:
+    """BASELINE cfg2 at Phi-4/14B shapes (K = 5120): q2 and q1 g64 affine GEMVs at N = 17920
+    (MLP) and N = 5120 (attention out), and the mixed run: per step an attention-out GEMV in
+    q1 (5120 x 5120) followed by an MLP GEMV in q2 (17920 x 5120), graph-replayed over 12
+    rotated weight copies of each."""
+    import torch
+
+    res = {}
+    for bits, rows, copies in ((2, 17920, 24), (2, 5120, 64), (1, 5120, 64), (1, 17920, 48)):
+        res[f"q{bits}_{rows}x5120"] = affine_lowbit_phase(be, bits, rows, 5120, copies, seed + bits * 7 + rows)
+    dev = be.device
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    cols, group, copies = 5120, 64, 12
+    mats = {}
+    for bits, rows in ((1, 5120), (2, 17920)):
+        W = torch.randint(0, 256, (copies, rows, cols * bits // 8), generator=g, device=dev, dtype=torch.uint8)
+        sz = torch.empty((copies, rows, cols // group, 2), device=dev, dtype=torch.float16)
+        sz[..., 0] = (torch.randn((copies, rows, cols // group), generator=g, device=dev).abs() * 0.05).to(torch.float16)
+        sz[..., 1] = (torch.rand((copies, rows, cols // group), generator=g, device=dev) * (2 ** bits - 1)).to(torch.float16)
+        mats[bits] = (W, sz, rows)
+    x = torch.randn(cols, generator=g, device=dev).to(torch.float16)
+    attn = torch.empty(5120, device=dev, dtype=torch.float16)
+    mlp = torch.empty(17920, device=dev, dtype=torch.float16)
+
+    def step(i):
+        W1, s1, r1 = mats[1]
+        W2, s2, r2 = mats[2]
+        be.lowbit_affine_matvec(W1[i], s1[i], x, attn, bits=1, rows=r1, cols=cols, group_size=group)
+        be.lowbit_affine_matvec(W2[i], s2[i], attn, mlp, bits=2, rows=r2, cols=cols, group_size=group)
+
+    t = _time_rotated(step, copies)
+    nbytes = sum(r * cols * b // 8 + r * (cols // group) * 4 + cols * 2 + r * 2 for b, (_, _, r) in mats.items())
+    res["mixed_q1_attn_q2_mlp"] = {"us_per_step": t * 1e6, "bytes_per_step": nbytes, "GB_s": nbytes / t / 1e9,
+                                   "launches_per_step": 2}
+    del mats
+    torch.cuda.empty_cache()
+    return res
 
 
 def ternary_phase(be, seed: int) -> dict:
@@ -417,6 +458,11 @@ def main() -> int:
         be = HipDecodeBackend(torch.device("cuda:0"), torch.float16, 2880, 4096, 512, 2880)
         print(json.dumps({"ternary_experts_gptoss": ternary_phase(be, args.seed + 7)}), flush=True)
         return 0
+    if args.cfg2_only:
+        from thintensor_amd.backend import HipDecodeBackend
+        be = HipDecodeBackend(torch.device("cuda:0"), torch.float16, 5120, 5120, 1024, 17920)
+        print(json.dumps({"cfg2_affine_lowbit_g64": cfg2_phase(be, args.seed + 4)}), flush=True)
+        return 0
     if args.batched_only:
         from thintensor_amd.backend import HipDecodeBackend
         be = HipDecodeBackend(torch.device("cuda:0"), torch.float16, 5120, 5120, 1024, 17920)
@@ -458,8 +504,7 @@ def main() -> int:
         extra["int4_gemv_17920x5120"]["single_launch_floor"] = memory_floor_phase(
             extra["int4_gemv_17920x5120"]["bytes_per_call"], 12)
         extra["lm_head_argmax_128256x2048"] = lm_head_phase(be, 128256, 2048, 2, args.seed + 3)
-        extra["q2_affine_g64_17920x5120"] = affine_lowbit_phase(be, 2, 17920, 5120, 24, args.seed + 4)
-        extra["q1_affine_g64_5120x5120"] = affine_lowbit_phase(be, 1, 5120, 5120, 64, args.seed + 5)
+        extra["cfg2_affine_lowbit_g64"] = cfg2_phase(be, args.seed + 4)
         extra["ternary_experts_gptoss"] = ternary_phase(be, args.seed + 7)
         torch.cuda.empty_cache()
         _log("batched small-M GEMM (hidden 5120)")
