@@ -51,6 +51,22 @@ struct LeanFused {
   int64_t token_x, token_out, token_cache;   // strides of token blockIdx.y
 };
 
+__device__ __forceinline__ LeanSeg pick_seg(const LeanSeg a, const LeanSeg b, const LeanSeg c, int si) {
+  LeanSeg r;
+  r.w = si == 0 ? a.w : (si == 1 ? b.w : c.w);
+  r.w2 = si == 0 ? a.w2 : (si == 1 ? b.w2 : c.w2);
+  r.s = si == 0 ? a.s : (si == 1 ? b.s : c.s);
+  r.s2 = si == 0 ? a.s2 : (si == 1 ? b.s2 : c.s2);
+  r.out = si == 0 ? a.out : (si == 1 ? b.out : c.out);
+  r.bias = si == 0 ? a.bias : (si == 1 ? b.bias : c.bias);
+  r.w_row = si == 0 ? a.w_row : (si == 1 ? b.w_row : c.w_row);
+  r.s_row = si == 0 ? a.s_row : (si == 1 ? b.s_row : c.s_row);
+  r.rows = si == 0 ? a.rows : (si == 1 ? b.rows : c.rows);
+  r.vbegin = si == 0 ? a.vbegin : (si == 1 ? b.vbegin : c.vbegin);
+  r.kind = si == 0 ? a.kind : (si == 1 ? b.kind : c.kind);
+  return r;
+}
+
 template <Fmt F, typename XT, int LPR, int ROWS, Pro PRO>
 __global__ __launch_bounds__(256) void fused_lean_kernel(const LeanFused P) {
   constexpr bool kInt4 = F == Fmt::kInt4Sym;
@@ -73,7 +89,10 @@ __global__ __launch_bounds__(256) void fused_lean_kernel(const LeanFused P) {
   const bool active = v0 < P.vtotal;
   const int64_t tok = blockIdx.y;   // token of a multi-token launch (0 otherwise)
   const int si = (P.nseg > 1 && v0 >= P.seg[1].vbegin ? 1 : 0) + (P.nseg > 2 && v0 >= P.seg[2].vbegin ? 1 : 0);
-  const LeanSeg& S = si == 0 ? P.seg[0] : (si == 1 ? P.seg[1] : P.seg[2]);
+  // every segment's fields are read from the kernel arguments unconditionally and the
+  // wave's segment is selected afterwards (scalar selects), so all argument loads go
+  // out in one batch instead of a second round trip behind the segment index
+  const LeanSeg S = pick_seg(P.seg[0], P.seg[1], P.seg[2], si);
   const int kind = S.kind;
   const int srows = S.rows;
   const int lr0 = v0 - S.vbegin;
