@@ -42,6 +42,26 @@ struct Seg {
   const void* s2;
 };
 
+// The segment of index si, every segment's fields read unconditionally first and the
+// wanted one selected afterwards (uniform selects): the kernel-argument loads then go out
+// in one batch instead of a second round trip behind the segment index.
+__device__ __forceinline__ Seg pick_seg(const Seg a, const Seg b, const Seg c, int si) {
+  Seg r;
+  r.w = si == 0 ? a.w : (si == 1 ? b.w : c.w);
+  r.w_row = si == 0 ? a.w_row : (si == 1 ? b.w_row : c.w_row);
+  r.s = si == 0 ? a.s : (si == 1 ? b.s : c.s);
+  r.s_row = si == 0 ? a.s_row : (si == 1 ? b.s_row : c.s_row);
+  r.s_grp = si == 0 ? a.s_grp : (si == 1 ? b.s_grp : c.s_grp);
+  r.out = si == 0 ? a.out : (si == 1 ? b.out : c.out);
+  r.rows = si == 0 ? a.rows : (si == 1 ? b.rows : c.rows);
+  r.vbegin = si == 0 ? a.vbegin : (si == 1 ? b.vbegin : c.vbegin);
+  r.bias = si == 0 ? a.bias : (si == 1 ? b.bias : c.bias);
+  r.kind = si == 0 ? a.kind : (si == 1 ? b.kind : c.kind);
+  r.w2 = si == 0 ? a.w2 : (si == 1 ? b.w2 : c.w2);
+  r.s2 = si == 0 ? a.s2 : (si == 1 ? b.s2 : c.s2);
+  return r;
+}
+
 // Context of the fused prologue (activation vector built in the kernel) and the
 // position-dependent epilogues.
 struct FuseParams {
@@ -219,7 +239,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
     if (P.nseg > 1 && v0 >= P.seg[1].vbegin) si = 1;
     if (P.nseg > 2 && v0 >= P.seg[2].vbegin) si = 2;
     si = __builtin_amdgcn_readfirstlane(si);
-    const Seg& S = si == 0 ? P.seg[0] : (si == 1 ? P.seg[1] : P.seg[2]);
+    const Seg S = pick_seg(P.seg[0], P.seg[1], P.seg[2], si);   // argument loads in one batch
     bt.lr0 = v0 - S.vbegin;
     bt.rows = S.rows;
     bt.kind = EPI ? S.kind : kSegPlain;
