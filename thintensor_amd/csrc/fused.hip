@@ -67,7 +67,7 @@ __device__ __forceinline__ LeanSeg pick_seg(const LeanSeg a, const LeanSeg b, co
   return r;
 }
 
-template <Fmt F, typename XT, int LPR, int ROWS, Pro PRO>
+template <Fmt F, typename XT, int LPR, int ROWS, Pro PRO, bool MULTI>
 __global__ __launch_bounds__(256) void fused_lean_kernel(const LeanFused P) {
   constexpr bool kInt4 = F == Fmt::kInt4Sym;
   constexpr int B = FmtInfo<F>::kBytes;
@@ -88,11 +88,43 @@ __global__ __launch_bounds__(256) void fused_lean_kernel(const LeanFused P) {
   const int v0 = (int)(blockIdx.x * 4 + wave) * (ROWS * SUBS);   // first virtual row (uniform)
   const bool active = v0 < P.vtotal;
   const int64_t tok = blockIdx.y;   // token of a multi-token launch (0 otherwise)
-  const int si = (P.nseg > 1 && v0 >= P.seg[1].vbegin ? 1 : 0) + (P.nseg > 2 && v0 >= P.seg[2].vbegin ? 1 : 0);
-  // every segment's fields are read from the kernel arguments unconditionally and the
-  // wave's segment is selected afterwards (scalar selects), so all argument loads go
-  // out in one batch instead of a second round trip behind the segment index
-  const LeanSeg S = pick_seg(P.seg[0], P.seg[1], P.seg[2], si);
+  // ---- the prologue's inputs are requested first -- before the row addressing, which
+  // is a few hundred scalar instructions for paired segments, and before round 0 of the
+  // weights, so that waiting for them never waits for the weight stream: one 16-byte
+  // piece of each vector per held piece (cols <= 4096, a multiple of 32; indices past the
+  // last piece repeat it)
+  __shared__ float red[4];
+  const int n = cols;
+  const int np = n >> 3;
+  uint4 qa[kNormPieces], qb[kNormPieces], qw[kNormPieces];
+  if constexpr (PRO != Pro::kLoad) {
+    const uint16_t* pa;
+    if constexpr (PRO == Pro::kEmbedNorm) {
+      int64_t t = P.token[tok];
+      t = t < 0 ? 0 : (t >= P.vocab ? P.vocab - 1 : t);
+      pa = reinterpret_cast<const uint16_t*>(P.embed) + t * P.embed_row;
+    } else {
+      pa = reinterpret_cast<const uint16_t*>(P.left) + tok * P.token_x;
+    }
+    const uint16_t* pb = reinterpret_cast<const uint16_t*>(P.right) + tok * P.token_x;
+#pragma unroll
+    for (int k = 0; k < kNormPieces; k++) {
+      const int pi = (int)threadIdx.x + 256 * k;
+      const int pc = pi < np ? pi : np - 1;
+      qa[k] = reinterpret_cast<const uint4*>(pa)[pc];
+      if constexpr (PRO != Pro::kEmbedNorm) qb[k] = reinterpret_cast<const uint4*>(pb)[pc];
+      qw[k] = reinterpret_cast<const uint4*>(P.norm_w)[pc];
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // MULTI: every segment's fields are read from the kernel arguments unconditionally and
+  // the wave's segment is selected afterwards (scalar selects), so the argument loads go
+  // out together instead of a second round trip behind the segment index; a
+  // one-segment launch reads segment 0 only (fewer argument loads, fewer scalar
+  // registers)
+  int si = 0;
+  if constexpr (MULTI) si = (P.nseg > 1 && v0 >= P.seg[1].vbegin ? 1 : 0) + (P.nseg > 2 && v0 >= P.seg[2].vbegin ? 1 : 0);
+  const LeanSeg S = MULTI ? pick_seg(P.seg[0], P.seg[1], P.seg[2], si) : P.seg[0];
   const int kind = S.kind;
   const int srows = S.rows;
   const int lr0 = v0 - S.vbegin;
@@ -145,32 +177,6 @@ __global__ __launch_bounds__(256) void fused_lean_kernel(const LeanFused P) {
       for (int k = 0; k < NS; k++) sc[k] = srow[k][j >> 2];
     }
   };
-  // ---- the prologue's inputs are requested before round 0 of the weights, so that
-  // waiting for them never waits for the weight stream: one 16-byte piece of each vector
-  // per held piece (cols <= 4096, a multiple of 32; indices past the last piece repeat it)
-  __shared__ float red[4];
-  const int n = cols;
-  const int np = n >> 3;
-  uint4 qa[kNormPieces], qb[kNormPieces], qw[kNormPieces];
-  if constexpr (PRO != Pro::kLoad) {
-    const uint16_t* pa;
-    if constexpr (PRO == Pro::kEmbedNorm) {
-      int64_t t = P.token[tok];
-      t = t < 0 ? 0 : (t >= P.vocab ? P.vocab - 1 : t);
-      pa = reinterpret_cast<const uint16_t*>(P.embed) + t * P.embed_row;
-    } else {
-      pa = reinterpret_cast<const uint16_t*>(P.left) + tok * P.token_x;
-    }
-    const uint16_t* pb = reinterpret_cast<const uint16_t*>(P.right) + tok * P.token_x;
-#pragma unroll
-    for (int k = 0; k < kNormPieces; k++) {
-      const int pi = (int)threadIdx.x + 256 * k;
-      const int pc = pi < np ? pi : np - 1;
-      qa[k] = reinterpret_cast<const uint4*>(pa)[pc];
-      if constexpr (PRO != Pro::kEmbedNorm) qb[k] = reinterpret_cast<const uint4*>(pb)[pc];
-      qw[k] = reinterpret_cast<const uint4*>(P.norm_w)[pc];
-    }
-  }
   __builtin_amdgcn_sched_barrier(0);
   Raw<B> wc[ROWS];
   f16_t sc[NS];
@@ -390,8 +396,13 @@ int launch_lean_lpr(const tt_fused_gemv* d, hipStream_t st) {
   const int64_t waves = P.vtotal / per_batch;
   const dim3 grid((unsigned)((waves + 3) / 4), (unsigned)(d->tokens > 1 ? d->tokens : 1));
   const size_t lds = (size_t)d->cols * 2;
-  if (rpw == 4) hipLaunchKernelGGL((fused_lean_kernel<F, XT, LPR, 4, PRO>), grid, dim3(256), lds, st, P);
-  else hipLaunchKernelGGL((fused_lean_kernel<F, XT, LPR, 2, PRO>), grid, dim3(256), lds, st, P);
+  if (d->count > 1) {
+    if (rpw == 4) hipLaunchKernelGGL((fused_lean_kernel<F, XT, LPR, 4, PRO, true>), grid, dim3(256), lds, st, P);
+    else hipLaunchKernelGGL((fused_lean_kernel<F, XT, LPR, 2, PRO, true>), grid, dim3(256), lds, st, P);
+  } else {
+    if (rpw == 4) hipLaunchKernelGGL((fused_lean_kernel<F, XT, LPR, 4, PRO, false>), grid, dim3(256), lds, st, P);
+    else hipLaunchKernelGGL((fused_lean_kernel<F, XT, LPR, 2, PRO, false>), grid, dim3(256), lds, st, P);
+  }
   return check_launch(kWhat);
 }
 
