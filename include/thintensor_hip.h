@@ -319,6 +319,16 @@ int tt_add_rms_norm(const void* left, const void* right, void* residual_out, int
                     const void* weight, int w_dtype, void* out, int out_dtype, int64_t n, float eps,
                     void* stream);
 
+/* For each of `rows` rows (row stride `row` for left/right/sum_out, `out_row` for out):
+ * sum_out = left + right rounded to x_dtype, then out = rms_norm(sum_out) * weight --
+ * tt_add followed by tt_rms_norm (weight offset 0) per row, bit for bit, in one launch.
+ * The batched form of TritonDecodeBackend.add + rms_norm (triton_kernels.py:5862-5873,
+ * 5632-5644) at the end of a batched decode step.  n a multiple of 8 up to 4096,
+ * 16-byte aligned rows. */
+int tt_add_then_rms_norm_rows(const void* left, const void* right, void* sum_out, int x_dtype, int64_t row,
+                              const void* weight, int w_dtype, void* out, int out_dtype, int64_t out_row, int64_t rows,
+                              int64_t n, float eps, void* stream);
+
 /* out = a + b.  Replaces TritonDecodeBackend.add (triton_kernels.py:5862-5873). */
 int tt_add(const void* a, const void* b, void* out, int dtype, int64_t n, void* stream);
 
@@ -379,6 +389,13 @@ int tt_advance_position(int32_t* position_dev, int32_t step, void* stream);
  * replays); indices outside [0, capacity) are skipped. */
 int tt_record_token(const int64_t* token_dev, const int32_t* position_dev, const int32_t* base_dev,
                     int64_t* history, int32_t capacity, void* stream);
+
+/* Batched token log of a decode batch: history[r * history_row + position - base] =
+ * tokens[r] for r < count (indices outside [0, capacity) skipped), then position +=
+ * step -- tt_record_token per row followed by tt_advance_position, in one launch.
+ * No reference counterpart (graph-replay helper of the batched decoder). */
+int tt_record_tokens_advance(const int64_t* tokens_dev, int32_t count, int32_t* position_dev, const int32_t* base_dev,
+                             int64_t* history, int64_t history_row, int32_t capacity, int32_t step, void* stream);
 
 /* ---------------------------------------------------------------- attention / router */
 

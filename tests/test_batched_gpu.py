@@ -125,7 +125,7 @@ def test_fp8_batched(backend, device, m):
             assert_bits_equal(got[r], want, f"fp8 batched row {r}")
 
 
-@pytest.mark.parametrize("m", [1, 4, 6, 9])
+@pytest.mark.parametrize("m", [1, 4, 6, 8, 9, 15])
 def test_lm_head_argmax_batched(backend, device, m):
     g = rng(300 + m)
     rows, cols = 20000, 5120

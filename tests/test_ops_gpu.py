@@ -61,6 +61,46 @@ def test_add_rms_norm(backend, device, n, seed):
     assert_f64(from_torch_bits(out), want64, "add_rms_norm")
 
 
+@pytest.mark.parametrize("rows,n", [(8, 2880), (3, 4096), (1, 2048)])
+def test_add_then_rms_norm_rows(backend, device, rows, n):
+    """The batched end-of-step launch equals add then rms_norm on each row, bit for bit,
+    and both equal the oracle."""
+    g = rng(rows * 31 + n)
+    a, b = f16_normal(g, (rows, n), 2.0), f16_normal(g, (rows, n), 0.5)
+    w = f16_normal(g, n, 0.1)
+    ad, bd, wd = to_torch(a, device), to_torch(b, device), to_torch(w, device)
+    sums = torch.empty((rows, n), device=device, dtype=torch.float16)
+    out = torch.empty((rows, n), device=device, dtype=torch.float16)
+    backend.add_then_rms_norm_rows(ad, bd, sums, wd, out, 1e-5)
+    got_sum, got = from_torch_bits(sums), from_torch_bits(out)
+    for r in range(rows):
+        want_sum = (a[r].astype(np.float32) + b[r].astype(np.float32)).astype(np.float16)
+        assert_bits_equal(got_sum[r], want_sum, f"sum row {r}")
+        want = np.empty(n, dtype=np.float16)
+        oracle.lib().tto_rms_norm(P(want_sum), oracle.F16, P(w), oracle.F16, P(want), oracle.F16, n, 1e-5, 0.0)
+        assert_bits_equal(got[r], want, f"normed row {r}")
+        one_sum = torch.empty(n, device=device, dtype=torch.float16)
+        one = torch.empty(n, device=device, dtype=torch.float16)
+        backend.add(ad[r], bd[r], one_sum)
+        backend.rms_norm(one_sum, wd, one, 1e-5)
+        assert_bits_equal(got[r], from_torch_bits(one), f"unbatched row {r}")
+
+
+def test_record_tokens_advance(backend, device):
+    tokens = torch.tensor([5, 7, 11], device=device, dtype=torch.int64)
+    history = torch.zeros((3, 4), device=device, dtype=torch.int64)
+    position = torch.tensor([10], device=device, dtype=torch.int32)
+    base = torch.tensor([9], device=device, dtype=torch.int32)
+    backend.record_tokens_advance(tokens, position, base, history)
+    backend.record_tokens_advance(tokens + 1, position, base, history)
+    assert history.cpu().tolist() == [[0, 5, 6, 0], [0, 7, 8, 0], [0, 11, 12, 0]]
+    assert int(position.item()) == 12
+    position.fill_(13)  # outside the log: skipped, the position still moves
+    backend.record_tokens_advance(tokens, position, base, history)
+    assert history.cpu().tolist() == [[0, 5, 6, 0], [0, 7, 8, 0], [0, 11, 12, 0]]
+    assert int(position.item()) == 14
+
+
 def test_silu_swiglu_weighted_sum_add(backend, device):
     g = rng(3)
     n = 8192

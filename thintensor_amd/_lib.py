@@ -101,6 +101,8 @@ SIGNATURES: dict[str, list] = {
     "tt_int4_selected_matvec": [_P, _L, _L, _P, _I, _L, _L, _L, _P, _I, _L, _P, _L, _P, _I, _L, _L, _L, _L, _P],
     "tt_multi_matvec_bias": [_I, _PP, _I, _LP, _LP, _PP, _P, _I, _P, _I, _L, _P],
     "tt_record_token": [_P, _P, _P, _P, ctypes.c_int32, _P],
+    "tt_record_tokens_advance": [_P, ctypes.c_int32, _P, _P, _P, _L, ctypes.c_int32, ctypes.c_int32, _P],
+    "tt_add_then_rms_norm_rows": [_P, _P, _P, _I, _L, _P, _I, _P, _I, _L, _L, _L, _F, _P],
     "tt_matvec_argmax_partials": [_L, _L],
     "tt_matvec_argmax": [_P, _I, _L, _P, _I, _P, _I, _L, _L, _P, _L, _P, _P, _P],
     "tt_matvec_argmax_noalloc": [_P, _I, _L, _P, _I, _P, _I, _L, _L, _P, _P, _P],

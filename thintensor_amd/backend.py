@@ -937,6 +937,26 @@ class HipDecodeBackend:
         _lib.check(rc, "rms_norm")
         return out
 
+    def add_then_rms_norm_rows(self, left: torch.Tensor, right: torch.Tensor, sum_out: torch.Tensor,
+                               weight: torch.Tensor, out: torch.Tensor, eps: float) -> torch.Tensor:
+        """Rows [B, n]: sum_out = left + right, out = rms_norm(sum_out) * weight, each row
+        bit-identical to add followed by rms_norm (triton_kernels.py:5862-5873, 5632-5644)."""
+        _require_cuda(left, right, sum_out, weight, out)
+        if left.ndim != 2 or any(t.shape != left.shape for t in (right, sum_out, out)):
+            raise ValueError("add_then_rms_norm_rows: [B, n] tensors of one shape")
+        if right.dtype != left.dtype or sum_out.dtype != left.dtype or weight.numel() != left.shape[1]:
+            raise ValueError("add_then_rms_norm_rows: dtype or weight size mismatch")
+        if any(t.stride(1) != 1 or t.stride(0) != left.stride(0) for t in (right, sum_out)) or out.stride(1) != 1:
+            raise ValueError("add_then_rms_norm_rows: rows must be contiguous with one row stride")
+        rows, n = int(left.shape[0]), int(left.shape[1])
+        rc = self.lib.tt_add_then_rms_norm_rows(left.data_ptr(), right.data_ptr(), sum_out.data_ptr(),
+                                                _code(left, "add_then_rms_norm_rows"), left.stride(0),
+                                                weight.data_ptr(), _code(weight, "add_then_rms_norm_rows"),
+                                                out.data_ptr(), _code(out, "add_then_rms_norm_rows"), out.stride(0),
+                                                rows, n, float(eps), _stream(left))
+        _lib.check(rc, "add_then_rms_norm_rows")
+        return out
+
     def add_rms_norm(self, left: torch.Tensor, right: torch.Tensor, residual_out: torch.Tensor, weight: torch.Tensor,
                      norm_out: torch.Tensor, eps: float) -> tuple[torch.Tensor, torch.Tensor]:
         """(triton_kernels.py:5646-5667)"""
@@ -1354,6 +1374,19 @@ class HipDecodeBackend:
         rc = self.lib.tt_record_token(token.data_ptr(), position.data_ptr(), base.data_ptr(), history.data_ptr(),
                                       int(history.numel()), _stream(token))
         _lib.check(rc, "record_token")
+
+    def record_tokens_advance(self, tokens: torch.Tensor, position: torch.Tensor, base: torch.Tensor,
+                              history: torch.Tensor, step: int = 1) -> None:
+        """history[r, position - base] = tokens[r] for every row, then position += step
+        (record_token per row + advance_position in one launch)."""
+        if tokens.dtype != torch.int64 or history.dtype != torch.int64 or history.ndim != 2:
+            raise ValueError("record_tokens_advance: int64 tokens [B] and history [B, T]")
+        if tokens.numel() != history.shape[0] or not tokens.is_contiguous() or history.stride(1) != 1:
+            raise ValueError("record_tokens_advance: one token per history row, contiguous rows")
+        rc = self.lib.tt_record_tokens_advance(tokens.data_ptr(), int(tokens.numel()), position.data_ptr(),
+                                               base.data_ptr(), history.data_ptr(), history.stride(0),
+                                               int(history.shape[1]), int(step), _stream(tokens))
+        _lib.check(rc, "record_tokens_advance")
 
     def multi_matvec_bias(self, weights: tuple[torch.Tensor, ...], biases: tuple[torch.Tensor | None, ...],
                           x: torch.Tensor, out: torch.Tensor) -> torch.Tensor:

@@ -432,7 +432,8 @@ int launch_mfma(MfmaParams P, float* ws, int64_t ws_floats, hipStream_t st, cons
   return check_launch(what);
 }
 
-// Up to four activation rows per GEMV launch (VALU, bit-exact per row).
+// Up to four activation rows per GEMV launch (eight for the argmax lm_head, whose
+// weights are the largest read of a batched decode step; VALU, bit-exact per row).
 template <Fmt F, SMode SM, typename ST, int ROWS, int L, bool AM>
 int launch_rows(GemvParams P, int64_t m_total, int64_t x_row, int64_t out_row, int lpr, hipStream_t st,
                 const char* what, int64_t partial_stride) {
@@ -443,13 +444,17 @@ int launch_rows(GemvParams P, int64_t m_total, int64_t x_row, int64_t out_row, i
   uint64_t* part0 = P.am_partials;
   for (int64_t m0 = 0; m0 < m_total;) {
     const int64_t left = m_total - m0;
-    const int mr = left >= 4 ? 4 : (left >= 2 ? 2 : 1);
+    const int mr = (AM && left >= 8) ? 8 : (left >= 4 ? 4 : (left >= 2 ? 2 : 1));
     GemvParams Q = P;
     Q.x = x0 + m0 * x_row;
     if (out0) Q.seg[0].out = out0 + m0 * out_row * 2;
     if (AM) Q.am_partials = part0 + m0 * partial_stride;
     int rc;
     switch (mr) {
+      case 8:
+        if constexpr (AM) rc = launch_lpr<F, SM, f16_t, f16_t, ST, ROWS, L, Pro::kLoad, false, 1, 8>(lpr, Q, 1, st, what);
+        else rc = TT_ERR_INVALID;
+        break;
       case 4: rc = launch_lpr<F, SM, f16_t, f16_t, ST, ROWS, L, Pro::kLoad, false, 1, 4>(lpr, Q, 1, st, what); break;
       case 2: rc = launch_lpr<F, SM, f16_t, f16_t, ST, ROWS, L, Pro::kLoad, false, 1, 2>(lpr, Q, 1, st, what); break;
       default: rc = launch_lpr<F, SM, f16_t, f16_t, ST, ROWS, L, Pro::kLoad, false, 1, 1>(lpr, Q, 1, st, what); break;
@@ -460,23 +465,32 @@ int launch_rows(GemvParams P, int64_t m_total, int64_t x_row, int64_t out_row, i
   return TT_OK;
 }
 
-// Token of each activation row.  Rows go to GEMV launches of four (then two, then
-// one for the tail); the launch holding rows m0 .. m0 + mr - 1 writes the key of
+// Token of each activation row.  Rows go to GEMV launches of eight (then four, two
+// and one for the tail); the launch holding rows m0 .. m0 + mr - 1 writes the key of
 // (wave w, row r) at partials[m0 * per + w * mr + r].
 __global__ __launch_bounds__(256) void argmax_rows_kernel(const uint64_t* partials, int64_t per, int64_t m_total,
                                                           int64_t* out_idx, float* out_val) {
   const int64_t m = blockIdx.x;
-  const int64_t full = m_total / 4 * 4;
+  int64_t b = m_total / 8 * 8, rem = m_total - b;
   int64_t m0, mr;
-  if (m < full) {
-    m0 = m / 4 * 4;
-    mr = 4;
-  } else if (m_total - full >= 2 && m < full + 2) {
-    m0 = full;
-    mr = 2;
+  if (m < b) {
+    m0 = m / 8 * 8;
+    mr = 8;
   } else {
-    m0 = m;
-    mr = 1;
+    if (rem >= 4 && m >= b + 4) {
+      b += 4;
+      rem -= 4;
+    }
+    if (rem >= 4) {
+      m0 = b;
+      mr = 4;
+    } else if (rem >= 2 && m < b + 2) {
+      m0 = b;
+      mr = 2;
+    } else {
+      m0 = m;
+      mr = 1;
+    }
   }
   const uint64_t* base = partials + m0 * per + (m - m0);
   __shared__ uint64_t red[256];

@@ -129,6 +129,55 @@ __global__ __launch_bounds__(256) void add_rms_norm_kernel(const void* left, con
     }
 }
 
+// Rows of a decode batch, one workgroup per row: sum_r = a_r + b_r rounded to the
+// activation dtype (add_kernel's rounding), out_r = rms_norm(sum_r) * w (rms_norm_kernel's
+// piece partition and reduction, weight offset 0).  Whole aligned pieces only.
+template <typename XT, typename WT, typename OT>
+__global__ __launch_bounds__(256) void add_then_rms_norm_rows_kernel(const void* a, const void* b, void* sum,
+                                                                     const void* w, void* out, int n, int64_t row,
+                                                                     int64_t out_row, float eps) {
+  __shared__ float red[4];
+  const int np = n >> 3;
+  const int t = threadIdx.x;
+  const int64_t off = (int64_t)blockIdx.x * row;
+  const uint4* ap = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a) + off);
+  const uint4* bp = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(b) + off);
+  uint4 ar[kNormPieces], br[kNormPieces];
+#pragma unroll
+  for (int k = 0; k < kNormPieces; k++) {
+    const int p = t + 256 * k;
+    const int pc = p < np ? p : np - 1;
+    ar[k] = ap[pc];
+    br[k] = bp[pc];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  float r[kNormPieces][8];
+  float s = 0.0f;
+#pragma unroll
+  for (int k = 0; k < kNormPieces; k++)
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      r[k][e] = round_to<XT>(piece_f32<XT>(ar[k], e) + piece_f32<XT>(br[k], e));
+      if (t + 256 * k < np) s = __builtin_fmaf(r[k][e], r[k][e], s);
+    }
+  const float total = block_sum256(s, red);
+  const float inv = 1.0f / __builtin_sqrtf(total / (float)n + eps);
+  XT* so = reinterpret_cast<XT*>(sum) + off;
+  OT* oo = reinterpret_cast<OT*>(out) + (int64_t)blockIdx.x * out_row;
+#pragma unroll
+  for (int k = 0; k < kNormPieces; k++) {
+    const int p = t + 256 * k;
+    if (p < np) {
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const int i = 8 * p + e;
+        store<XT>(so + i, r[k][e]);
+        store<OT>(oo + i, (r[k][e] * inv) * ld<WT>(w, i));
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------------- elementwise
 template <typename T>
 __global__ void add_kernel(const void* a, const void* b, void* out, int n) {
@@ -315,6 +364,17 @@ __global__ void record_token_kernel(const int64_t* token, const int32_t* pos, co
   }
 }
 
+// history[r * history_row + pos - base] = tokens[r] for the rows of a batch, then
+// pos += step once every row has read it.
+__global__ void record_tokens_advance_kernel(const int64_t* tokens, int32_t count, int32_t* pos, const int32_t* base,
+                                             int64_t* history, int64_t history_row, int32_t capacity, int32_t step) {
+  const int32_t i = pos[0] - base[0];
+  for (int r = threadIdx.x; r < count; r += blockDim.x)
+    if (i >= 0 && i < capacity) history[(int64_t)r * history_row + i] = tokens[r];
+  __syncthreads();
+  if (threadIdx.x == 0) pos[0] = pos[0] + step;
+}
+
 template <typename Fn> static int with_act(int code, Fn&& f) {
   if (code == TT_F16) return f(f16_t{});
   if (code == TT_BF16) return f(bf16_t{});
@@ -365,6 +425,31 @@ extern "C" int tt_add_rms_norm(const void* left, const void* right, void* residu
         hipLaunchKernelGGL((add_rms_norm_kernel<XT, WT, OT>), dim3(1), dim3(256), 0, static_cast<hipStream_t>(stream),
                            left, right, residual_out, weight, out, (int)n, eps, vec);
         return check_launch("add_rms_norm");
+      });
+    });
+  });
+}
+
+extern "C" int tt_add_then_rms_norm_rows(const void* left, const void* right, void* sum_out, int x_dtype, int64_t row,
+                                         const void* weight, int w_dtype, void* out, int out_dtype, int64_t out_row,
+                                         int64_t rows, int64_t n, float eps, void* stream) {
+  const char* what = "add_then_rms_norm_rows";
+  TT_REQUIRE(left && right && sum_out && weight && out && rows >= 1 && rows <= 65535, "%s: bad arguments", what);
+  TT_REQUIRE(n > 0 && n % 8 == 0 && n <= 8 * 256 * kNormPieces, "%s: n must be a multiple of 8 up to %d", what,
+             8 * 256 * kNormPieces);
+  TT_REQUIRE(aligned(left, 16) && aligned(right, 16) && aligned(sum_out, 16) && row % 8 == 0 && row >= n &&
+                 out_row >= n,
+             "%s: 16-byte aligned rows required", what);
+  return with_act(x_dtype, [&](auto xt) {
+    using XT = decltype(xt);
+    return with_any(w_dtype, [&](auto wt) {
+      using WT = decltype(wt);
+      return with_any(out_dtype, [&](auto ot) {
+        using OT = decltype(ot);
+        hipLaunchKernelGGL((add_then_rms_norm_rows_kernel<XT, WT, OT>), dim3((unsigned)rows), dim3(256), 0,
+                           static_cast<hipStream_t>(stream), left, right, sum_out, weight, out, (int)n, row, out_row,
+                           eps);
+        return check_launch(what);
       });
     });
   });
@@ -506,4 +591,14 @@ extern "C" int tt_record_token(const int64_t* token_dev, const int32_t* position
   hipLaunchKernelGGL(record_token_kernel, dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream), token_dev, position_dev,
                      base_dev, history, capacity);
   return check_launch("record_token");
+}
+
+extern "C" int tt_record_tokens_advance(const int64_t* tokens_dev, int32_t count, int32_t* position_dev,
+                                        const int32_t* base_dev, int64_t* history, int64_t history_row,
+                                        int32_t capacity, int32_t step, void* stream) {
+  TT_REQUIRE(tokens_dev && position_dev && base_dev && history && count >= 1 && capacity > 0 && history_row >= capacity,
+             "record_tokens_advance: bad arguments");
+  hipLaunchKernelGGL(record_tokens_advance_kernel, dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream), tokens_dev,
+                     count, position_dev, base_dev, history, history_row, capacity, step);
+  return check_launch("record_tokens_advance");
 }

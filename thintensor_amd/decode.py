@@ -470,13 +470,9 @@ class MoEBatchDecoder:
                                                   bias=L.gate_up_bias)
             be.mxfp_lowbit_weighted_down_tokens(L.down_blocks, L.down_scales, self.act, self.router_idx,
                                                 self.router_scores, self.moe, bits=4, bias=L.down_bias)
-        for b in range(B):
-            be.add(self.hidden_b[b], self.moe[b], self.hidden_a[b])
-            be.rms_norm(self.hidden_a[b], w.final_norm, self.final_all[b], s.eps)
+        be.add_then_rms_norm_rows(self.hidden_b, self.moe, self.hidden_a, w.final_norm, self.final_all, s.eps)
         be.matvec_argmax_batched(w.lm_head, self.final_all, out=self.tokens)
-        for b in range(B):
-            be.record_token(self.tokens[b], self.position, self.base, self.history[b])
-        be.advance_position(self.position)
+        be.record_tokens_advance(self.tokens, self.position, self.base, self.history)
 
     def capture(self) -> None:
         """Record one batched step into a HIP graph (scratch reserved first)."""
