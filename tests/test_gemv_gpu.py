@@ -293,7 +293,8 @@ def test_fused_weighted_down(backend, device, bits):
     assert ref.max_rel_err(from_torch_bits(out), want64) < TOL
 
 
-@pytest.mark.parametrize("m,rows,cols,wdt", [(8, 2880, 4096, "f16"), (3, 1000, 2048, "bf16"), (5, 300, 5120, "f16")])
+@pytest.mark.parametrize("m,rows,cols,wdt", [(8, 2880, 4096, "f16"), (3, 1000, 2048, "bf16"), (5, 300, 5120, "f16"),
+                                            (13, 2880, 4096, "f16"), (2, 77, 96, "f16")])
 def test_matvec_bias_rows(backend, device, m, rows, cols, wdt):
     """M activation rows in one launch (or one per row past 4096 columns) equal the
     single-row GEMV with bias row by row."""
@@ -315,12 +316,14 @@ def test_matvec_bias_rows(backend, device, m, rows, cols, wdt):
         assert_bits_equal(from_torch_bits(out[t]), from_torch_bits(o1), f"row {t}")
 
 
-@pytest.mark.parametrize("bits,tokens", [(4, 8), (2, 3)])
-def test_expert_kernels_token_batched(backend, device, bits, tokens):
+@pytest.mark.parametrize("bits,tokens,same", [(4, 8, False), (2, 3, False), (4, 16, True), (1, 5, False),
+                                              (4, 17, False)])
+def test_expert_kernels_token_batched(backend, device, bits, tokens, same):
     """SwiGLU and weighted down over several tokens (each with its own activation
-    vector, experts and scores) equal the single-token operators token by token."""
+    vector, experts and scores) equal the single-token operators token by token.  Six
+    experts, so slots share experts (`same`: every token picks the same experts)."""
     experts, inter, cols, top_k = 6, 2880, 2880, 4
-    g = rng(71 + bits)
+    g = rng(71 + bits + tokens)
     if bits == 4:
         gu, gus = _mxfp4_expert_weights(g, experts, 2 * inter, cols)
         dw, dws = _mxfp4_expert_weights(g, experts, cols, inter)
@@ -330,7 +333,10 @@ def test_expert_kernels_token_batched(backend, device, bits, tokens):
         dw = layouts.pack_lowbit_blocks(g.integers(0, 4, size=(experts, cols, inter), dtype=np.uint8), 2)
         dws = g.integers(118, 123, size=(experts, cols, inter // 32), dtype=np.uint8)
     gub, db = f16_normal(g, (experts, 2 * inter), 0.5), f16_normal(g, (experts, cols), 0.5)
-    idx = np.stack([g.permutation(experts)[:top_k] for _ in range(tokens)]).astype(np.int32)
+    if same:
+        idx = np.tile(g.permutation(experts)[:top_k], (tokens, 1)).astype(np.int32)
+    else:
+        idx = np.stack([g.permutation(experts)[:top_k] for _ in range(tokens)]).astype(np.int32)
     sc = g.dirichlet(np.ones(top_k), size=tokens).astype(np.float16)
     x = f16_normal(g, (tokens, cols))
     T = lambda a: to_torch(a, device)

@@ -799,6 +799,23 @@ class HipDecodeBackend:
         _lib.check(rc, "mxfp_lowbit_selected_swiglu_tokens")
         return out
 
+    def _zeroed_workspace(self, name: str, need: int) -> torch.Tensor:
+        """A byte workspace kept by the backend under `name`, zero-filled when it is
+        (re)allocated: arrival counters at its head, which every call leaves at zero.
+        Reserve it before graph capture so the capture records no allocation."""
+        ws = getattr(self, name, None)
+        if ws is None or ws.numel() < need:
+            ws = torch.zeros(max(need, 1), device=self.device, dtype=torch.uint8)
+            setattr(self, name, ws)
+        return ws
+
+    def reserve_batch_workspaces(self, tokens: int) -> None:
+        """Allocate the router workspace of a `tokens`-row batched decode step ahead of
+        graph capture."""
+        need = int(self.lib.tt_norm_router_workspace_bytes(tokens))
+        if need > 0:
+            self._zeroed_workspace("_norm_router_ws", need)
+
     def mxfp_lowbit_weighted_down_tokens(self, packed_weight: torch.Tensor, scales: torch.Tensor, x: torch.Tensor,
                                          expert_indices: torch.Tensor, router_scores: torch.Tensor,
                                          out: torch.Tensor, *, bits: int,
@@ -1206,11 +1223,7 @@ class HipDecodeBackend:
         ws = None
         if split:
             need = int(self.lib.tt_norm_router_workspace_bytes(tokens))
-            ws = getattr(self, "_norm_router_ws", None)
-            if ws is None or ws.numel() < need:
-                # arrival counters and logits; every call leaves the counters at zero
-                ws = torch.zeros(need, device=self.device, dtype=torch.uint8)
-                self._norm_router_ws = ws
+            ws = self._zeroed_workspace("_norm_router_ws", need)
         rc = self.lib.tt_add_rms_norm_router_topk(
             left.data_ptr(), right.data_ptr(), residual_out.data_ptr(), _code(left, "add_rms_norm"),
             norm_weight.data_ptr(), _code(norm_weight, "add_rms_norm"), norm_out.data_ptr(),

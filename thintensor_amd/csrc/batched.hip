@@ -13,9 +13,12 @@
 //     blocks split between workgroups are summed in a fixed order by a second
 //     kernel.  MFMA sums products in a hardware-defined order, so this path matches
 //     the dequantise-then-matmul reference to the stated tolerance, not bit for bit.
-//   * the M-row lm_head argmax runs the GEMV engine with four activation rows per
+//   * the M-row lm_head argmax runs the GEMV engine with eight activation rows per
 //     launch and one argmax key per (wave, row); a finishing kernel picks each row's
-//     token, as tt_matvec_argmax does for one row.
+//     token, as tt_matvec_argmax does for one row;
+//   * the M-row dense GEMV + bias of a batched decode step (tt_matvec_bias_rows, fp16)
+//     runs the same engine with eight rows per launch: each weight load feeds every
+//     row's fma chain, the bits per row those of the single-row operator.
 #include "gemv_impl.h"
 
 #include <type_traits>
@@ -432,9 +435,10 @@ int launch_mfma(MfmaParams P, float* ws, int64_t ws_floats, hipStream_t st, cons
   return check_launch(what);
 }
 
-// Up to four activation rows per GEMV launch (eight for the argmax lm_head, whose
-// weights are the largest read of a batched decode step; VALU, bit-exact per row).
-template <Fmt F, SMode SM, typename ST, int ROWS, int L, bool AM>
+// Up to four activation rows per GEMV launch, eight with M8 (the dense decode-step
+// GEMVs, whose fp16 weights are the largest reads of a batched step); VALU, bit-exact
+// per row.
+template <Fmt F, SMode SM, typename ST, int ROWS, int L, bool AM, bool M8 = AM>
 int launch_rows(GemvParams P, int64_t m_total, int64_t x_row, int64_t out_row, int lpr, hipStream_t st,
                 const char* what, int64_t partial_stride) {
   P.x_slot = x_row;
@@ -444,7 +448,7 @@ int launch_rows(GemvParams P, int64_t m_total, int64_t x_row, int64_t out_row, i
   uint64_t* part0 = P.am_partials;
   for (int64_t m0 = 0; m0 < m_total;) {
     const int64_t left = m_total - m0;
-    const int mr = (AM && left >= 8) ? 8 : (left >= 4 ? 4 : (left >= 2 ? 2 : 1));
+    const int mr = (M8 && left >= 8) ? 8 : (left >= 4 ? 4 : (left >= 2 ? 2 : 1));
     GemvParams Q = P;
     Q.x = x0 + m0 * x_row;
     if (out0) Q.seg[0].out = out0 + m0 * out_row * 2;
@@ -452,7 +456,7 @@ int launch_rows(GemvParams P, int64_t m_total, int64_t x_row, int64_t out_row, i
     int rc;
     switch (mr) {
       case 8:
-        if constexpr (AM) rc = launch_lpr<F, SM, f16_t, f16_t, ST, ROWS, L, Pro::kLoad, false, 1, 8>(lpr, Q, 1, st, what);
+        if constexpr (M8) rc = launch_lpr<F, SM, f16_t, f16_t, ST, ROWS, L, Pro::kLoad, false, 1, 8>(lpr, Q, 1, st, what);
         else rc = TT_ERR_INVALID;
         break;
       case 4: rc = launch_lpr<F, SM, f16_t, f16_t, ST, ROWS, L, Pro::kLoad, false, 1, 4>(lpr, Q, 1, st, what); break;
@@ -515,6 +519,21 @@ __global__ __launch_bounds__(256) void argmax_rows_kernel(const uint64_t* partia
 }
 
 }  // namespace
+
+namespace tt {
+int dense_bias_rows_f16(const void* weight, int64_t w_row, const void* bias, const void* x, int64_t x_row, void* out,
+                        int64_t out_row, int64_t m, int64_t rows, int64_t cols, hipStream_t st) {
+  GemvParams P{};
+  P.nseg = 1;
+  P.seg[0] = Seg{static_cast<const uint8_t*>(weight), w_row * 2, nullptr, 0, 0, out, (int)rows};
+  P.seg[0].bias = bias;
+  P.x = x;
+  P.cols = (int)cols;
+  const int lpr = tt_gemv_lanes_per_row(cols / 32, 1);
+  return launch_rows<Fmt::kF16W, SMode::kNone, float, 2, 1, false, true>(P, m, x_row, out_row, lpr, st,
+                                                                         "matvec_bias_rows", 0);
+}
+}  // namespace tt
 
 extern "C" int64_t tt_batched_workspace_floats(int64_t m, int64_t rows, int64_t cols) {
   if (m < 16 || m > 64 || rows <= 0 || cols < kSlice) return 0;

@@ -120,6 +120,9 @@ extern "C" int tt_matvec_bias_rows(const void* weight, int w_dtype, int64_t w_ro
     }
     return TT_OK;
   }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (w_dtype == TT_F16 && x_dtype == TT_F16 && cols <= 4096)   // eight activation rows in 64 KB of LDS
+    return dense_bias_rows_f16(weight, w_row, bias, x, x_row, out, out_row, m, rows, cols, st);
   // rows of the batch are slots of the lean kernel (blockIdx.y), each with its own
   // activation and output row; the arithmetic per row is the single-row kernel's
   LeanParams L{};
@@ -133,7 +136,6 @@ extern "C" int tt_matvec_bias_rows(const void* weight, int w_dtype, int64_t w_ro
   L.rows = (int)rows;
   L.cols = (int)cols;
   const int lpr = tt_gemv_lanes_per_row(cols / 32, 1);
-  hipStream_t st = static_cast<hipStream_t>(stream);
   if (w_dtype == TT_F16) return lean_launch<Fmt::kF16W, SMode::kNone, float, 1>(x_dtype, lpr, L, (int)m, st, what);
   return lean_launch<Fmt::kBF16W, SMode::kNone, float, 1>(x_dtype, lpr, L, (int)m, st, what);
 }

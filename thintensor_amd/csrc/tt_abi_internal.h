@@ -40,6 +40,12 @@ inline int check_launch(const char* what) {
 
 inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
+// y[r] = W x[r] + bias for m fp16 activation rows through the GEMV engine, several rows
+// per launch sharing every weight load; row r has the bits of the single-row GEMV + bias
+// (batched.hip).  Shapes and alignment checked by the caller.
+int dense_bias_rows_f16(const void* weight, int64_t w_row, const void* bias, const void* x, int64_t x_row, void* out,
+                        int64_t out_row, int64_t m, int64_t rows, int64_t cols, hipStream_t st);
+
 inline bool valid_act_dtype(int d) { return d == TT_F16 || d == TT_BF16; }
 inline bool valid_out_dtype(int d) { return d == TT_F16 || d == TT_BF16 || d == TT_F32; }
 

@@ -211,6 +211,19 @@ __device__ __forceinline__ void decode_word8(uint32_t w, _Float16* v) {
   }
 }
 
+// MXFP4 word q (elements 8q .. 8q+7) decoded straight to binary32: the exact values the
+// binary16 decode gives, so the fma chains below run as plain fp32 fmas (full issue
+// rate) instead of mixed-precision ones, with the same bits.
+__device__ __forceinline__ void decode_word8_mxfp4_f32(uint32_t w, float* v) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  const f2 p0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 0);
+  const f2 p1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 1);
+  const f2 p2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 2);
+  const f2 p3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 3);
+  v[0] = p0[0]; v[1] = p0[1]; v[2] = p1[0]; v[3] = p1[1];
+  v[4] = p2[0]; v[5] = p2[1]; v[6] = p3[0]; v[7] = p3[1];
+}
+
 // Chunk partials of NR rows: for each row an fma chain over the chunk's 32 elements
 // in ascending k, starting from +0.  The rows' chains are interleaved element by
 // element so no fma waits on the one issued just before it.  The 4-bit formats are
@@ -219,7 +232,20 @@ template <Fmt F, typename XT, int NR>
 __device__ __forceinline__ void chunk_dot_rows(const Raw<FmtInfo<F>::kBytes>* r, const uint32_t* xw, float* p) {
 #pragma unroll
   for (int i = 0; i < NR; i++) p[i] = 0.0f;
-  if constexpr (F == Fmt::kInt4Sym || F == Fmt::kInt4Aff || F == Fmt::kMxfp4) {
+  if constexpr (F == Fmt::kMxfp4) {
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      float wv[NR][8];
+#pragma unroll
+      for (int i = 0; i < NR; i++) decode_word8_mxfp4_f32(r[i].w[q], wv[i]);
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const float xe = xv<XT>(xw, 8 * q + e);
+#pragma unroll
+        for (int i = 0; i < NR; i++) p[i] = __builtin_fmaf(wv[i][e], xe, p[i]);
+      }
+    }
+  } else if constexpr (F == Fmt::kInt4Sym || F == Fmt::kInt4Aff) {
 #pragma unroll
     for (int q = 0; q < 4; q++) {
       _Float16 wv[NR][8];
@@ -258,7 +284,23 @@ __device__ __forceinline__ void chunk_dot_rows_multi(const Raw<FmtInfo<F>::kByte
     for (int m = 0; m < MR; m++)
 #pragma unroll
       for (int i = 0; i < NR; i++) p[m][i] = 0.0f;
-    if constexpr (F == Fmt::kInt4Sym || F == Fmt::kInt4Aff || F == Fmt::kMxfp4) {
+    if constexpr (F == Fmt::kMxfp4) {
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        float wv[NR][8];
+#pragma unroll
+        for (int i = 0; i < NR; i++) decode_word8_mxfp4_f32(r[i].w[q], wv[i]);
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+#pragma unroll
+          for (int m = 0; m < MR; m++) {
+            const float xe = xv<XT>(xw[m], 8 * q + e);
+#pragma unroll
+            for (int i = 0; i < NR; i++) p[m][i] = __builtin_fmaf(wv[i][e], xe, p[m][i]);
+          }
+        }
+      }
+    } else if constexpr (F == Fmt::kInt4Sym || F == Fmt::kInt4Aff) {
 #pragma unroll
       for (int q = 0; q < 4; q++) {
         _Float16 wv[NR][8];

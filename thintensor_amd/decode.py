@@ -294,6 +294,7 @@ class MoEDecoder(_GraphedDecoder):
         self.be._attention_scratch(s.heads, self.capacity, s.head_dim)
         self.be._argmax_scratch(int(self.w.lm_head.shape[0]), s.hidden)
         self.be.logits_buffer(int(self.w.lm_head.shape[0]), torch.float16)
+        self.be.reserve_batch_workspaces(1)
 
     def step(self) -> None:
         be, w, s = self.be, self.w, self.s
@@ -452,6 +453,7 @@ class MoEBatchDecoder:
         s = self.s
         self.be._attention_scratch(self.batch * s.heads, self.capacity, s.head_dim)
         self.be._batched_argmax_scratch(self.batch, int(self.w.lm_head.shape[0]), s.hidden)
+        self.be.reserve_batch_workspaces(self.batch)
 
     def step(self) -> None:
         """One token of every sequence, logged at history[:, position - base]; advances the position."""
