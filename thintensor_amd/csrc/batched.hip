@@ -499,9 +499,16 @@ __global__ __launch_bounds__(256) void argmax_rows_kernel(const uint64_t* partia
   const uint64_t* base = partials + m0 * per + (m - m0);
   __shared__ uint64_t red[256];
   uint64_t best = 0;
-  for (int64_t i = threadIdx.x; i < per; i += 256) {
-    const uint64_t k = base[i * mr];
-    best = k > best ? k : best;
+  // eight independent loads in flight per thread and step
+  for (int64_t i0 = threadIdx.x; i0 < per; i0 += 256 * 8) {
+    uint64_t k[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      const int64_t i = i0 + 256 * u;
+      k[u] = i < per ? base[i * mr] : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; u++) best = k[u] > best ? k[u] : best;
   }
   red[threadIdx.x] = best;
   __syncthreads();
