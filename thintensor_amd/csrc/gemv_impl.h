@@ -368,11 +368,20 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
     uint4* xl = reinterpret_cast<uint4*>(xs_lds);
 #pragma unroll
     for (int k = 0; k < kXR; k++) xl[xidx[k]] = xreg[k];
-    for (int idx = threadIdx.x + 256 * kXR; idx < xtotal; idx += 256) {
-      const int m = MR == 1 ? 0 : idx / xn;
-      const uint4* xg = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(P.x) +
-                                                       (int64_t)(slot + m) * P.x_slot);
-      xl[idx] = xg[idx - m * xn];
+    // the rest (several activation rows) in steps of kXR loads in flight per thread,
+    // indices clamped as above
+    for (int i0 = threadIdx.x + 256 * kXR; i0 < xtotal; i0 += 256 * kXR) {
+#pragma unroll
+      for (int k = 0; k < kXR; k++) {
+        const int idx = i0 + 256 * k;
+        xidx[k] = idx < xtotal ? idx : xtotal - 1;
+        const int m = MR == 1 ? 0 : xidx[k] / xn;
+        const uint4* xg = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(P.x) +
+                                                         (int64_t)(slot + m) * P.x_slot);
+        xreg[k] = xg[xidx[k] - m * xn];
+      }
+#pragma unroll
+      for (int k = 0; k < kXR; k++) xl[xidx[k]] = xreg[k];
     }
     __syncthreads();
   } else {
