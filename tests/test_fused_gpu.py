@@ -63,7 +63,8 @@ def _inputs(g, n, device):
 
 
 @pytest.mark.parametrize("cols,prologue", [(2048, _lib.PRO_ADD_NORM), (2048, _lib.PRO_EMBED_NORM),
-                                           (1536, _lib.PRO_ADD_NORM), (2816, _lib.PRO_ADD_RMS_NORM)])
+                                           (2048, _lib.PRO_ADD_RMS_NORM), (1536, _lib.PRO_ADD_NORM),
+                                           (2816, _lib.PRO_ADD_RMS_NORM)])
 def test_fused_int4_qkv_rope_cache(backend, device, cols, prologue):
     """cols 2048 / 1536 / 2816 give 64 / 16 / 32 lanes per row."""
     g = rng(cols + prologue)
