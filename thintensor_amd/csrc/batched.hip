@@ -376,14 +376,33 @@ __global__ __launch_bounds__(256) void mfma_fold_kernel(MfmaParams P, int mp) {
   }
   __syncthreads();
   const float* rsc = P.ws_row_scale ? reinterpret_cast<const float*>(P.s) : nullptr;
-  for (int e = threadIdx.x; e < mp * 64; e += 256) {
-    const int mi = e >> 6, c = e & 63;
-    const int64_t r = b * 64 + c;
-    if (mi >= P.m || r >= P.n) continue;
-    float v = 0.0f;
-    for (int j = 0; j < n_slots; j++) v = v + P.ws[((int64_t)slot[j] * mp + mi) * 64 + c];
-    if (rsc) v = v * rsc[r];
-    P.out[(int64_t)mi * P.out_row + r] = f32_to_f16_bits(v);
+  // kE elements per thread and step with every partial of up to kJ slots requested before
+  // the first sum (one memory round trip per step instead of one per element and slot);
+  // slots past kJ (blocks shared by more workgroups) are added one at a time after them
+  constexpr int kE = 4, kJ = 4;
+  for (int e0 = threadIdx.x; e0 < mp * 64; e0 += 256 * kE) {
+    float p[kJ][kE];
+#pragma unroll
+    for (int j = 0; j < kJ; j++)
+#pragma unroll
+      for (int u = 0; u < kE; u++) {
+        const int e = e0 + 256 * u;
+        p[j][u] = (j < n_slots && e < mp * 64) ? P.ws[((int64_t)slot[j] * mp + (e >> 6)) * 64 + (e & 63)] : 0.0f;
+      }
+#pragma unroll
+    for (int u = 0; u < kE; u++) {
+      const int e = e0 + 256 * u;
+      const int mi = e >> 6, c = e & 63;
+      const int64_t r = b * 64 + c;
+      if (e >= mp * 64 || mi >= P.m || r >= P.n) continue;
+      float v = 0.0f;
+#pragma unroll
+      for (int j = 0; j < kJ; j++)
+        if (j < n_slots) v = v + p[j][u];
+      for (int j = kJ; j < n_slots; j++) v = v + P.ws[((int64_t)slot[j] * mp + mi) * 64 + c];
+      if (rsc) v = v * rsc[r];
+      P.out[(int64_t)mi * P.out_row + r] = f32_to_f16_bits(v);
+    }
   }
 }
 
