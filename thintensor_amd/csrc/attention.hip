@@ -661,15 +661,23 @@ __global__ __launch_bounds__(64 * G) void attn_kvchunk_kernel(AttnParams P, int*
   __syncthreads();
   if (!last) return;
 
-  // ---- combine of query head h in chunk order (attn_combine64_kernel's arithmetic)
+  // ---- combine of query head h in chunk order (attn_combine64_kernel's arithmetic); the
+  // first 64 chunks' (m, l) and the first kBlk chunks' partial rows are requested together
+  // with the sink, one round trip, before the maximum is formed
+  constexpr int kBlk = 32;
   const float* pm = P.part_m + (int64_t)h * P.max_chunks;
   const float* pl = P.part_l + (int64_t)h * P.max_chunks;
   const float* po = P.part_o + (int64_t)h * P.max_chunks * D + lane;
   const bool has_sink = P.sinks != nullptr;
+  const float m0 = lane < nc ? ld_dev(pm + lane) : ninf;
+  const float l0 = lane < nc ? ld_dev(pl + lane) : 0.0f;
+  float ov0[kBlk];
+#pragma unroll
+  for (int u = 0; u < kBlk; u++) ov0[u] = u < nc ? ld_dev(po + (int64_t)u * D) : 0.0f;
   const float sink = has_sink ? to_f32(reinterpret_cast<const SKT*>(P.sinks)[h]) : 0.0f;
   float M = has_sink ? sink : ninf;
   for (int c0 = 0; c0 < nc; c0 += 64) {
-    float mm = c0 + lane < nc ? ld_dev(pm + c0 + lane) : ninf;
+    float mm = c0 == 0 ? m0 : (c0 + lane < nc ? ld_dev(pm + c0 + lane) : ninf);
     mm = fmaxf(mm, xor_partner<1>(mm));
     mm = fmaxf(mm, xor_partner<2>(mm));
     mm = fmaxf(mm, xor_partner<4>(mm));
@@ -680,17 +688,21 @@ __global__ __launch_bounds__(64 * G) void attn_kvchunk_kernel(AttnParams P, int*
   }
   float den = has_sink ? exp_f32(sink - M) : 0.0f;
   float acc = 0.0f;
-  constexpr int kBlk = 16;
   for (int c0 = 0; c0 < nc; c0 += 64) {
     const int n = min(64, nc - c0);
-    const float e = c0 + lane < nc ? exp_f32(ld_dev(pm + c0 + lane) - M) : 0.0f;
-    const float lv = c0 + lane < nc ? ld_dev(pl + c0 + lane) : 0.0f;
+    const float e = c0 + lane < nc ? exp_f32((c0 == 0 ? m0 : ld_dev(pm + c0 + lane)) - M) : 0.0f;
+    const float lv = c0 + lane < nc ? (c0 == 0 ? l0 : ld_dev(pl + c0 + lane)) : 0.0f;
     for (int c1 = 0; c1 < n; c1 += kBlk) {
       float ov[kBlk];
+      if (c0 == 0 && c1 == 0) {
 #pragma unroll
-      for (int u = 0; u < kBlk; u++) {
-        const int cc = c0 + c1 + u;
-        ov[u] = cc < nc ? ld_dev(po + (int64_t)cc * D) : 0.0f;
+        for (int u = 0; u < kBlk; u++) ov[u] = ov0[u];
+      } else {
+#pragma unroll
+        for (int u = 0; u < kBlk; u++) {
+          const int cc = c0 + c1 + u;
+          ov[u] = cc < nc ? ld_dev(po + (int64_t)cc * D) : 0.0f;
+        }
       }
 #pragma unroll
       for (int u = 0; u < kBlk; u++) {
