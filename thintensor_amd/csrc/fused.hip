@@ -116,6 +116,9 @@ __global__ __launch_bounds__(256) void fused_lean_kernel(const LeanFused P) {
       qw[k] = reinterpret_cast<const uint4*>(P.norm_w)[pc];
     }
   }
+  // the token position of the RoPE / cache epilogues, requested with the prologue's
+  // inputs so that the epilogue's table reads are its only dependent round trip
+  const int32_t pos_raw = P.pos != nullptr ? P.pos[0] : 0;
   __builtin_amdgcn_sched_barrier(0);
   // MULTI: every segment's fields are read from the kernel arguments unconditionally and
   // the wave's segment is selected afterwards (scalar selects), so the argument loads go
@@ -298,7 +301,7 @@ __global__ __launch_bounds__(256) void fused_lean_kernel(const LeanFused P) {
     if (ok && !odd) store<XT>(reinterpret_cast<XT*>(S.out) + tok * P.token_out + ph, silu_mul_val(val, pv));
     return;
   }
-  const int64_t pos = P.pos != nullptr ? (int64_t)P.pos[0] : 0;
+  const int64_t pos = (int64_t)__builtin_amdgcn_readfirstlane(pos_raw);
   const int D = P.head_dim;
   float o = val;
   if (kind != kSegCache && pos >= 0 && pos < P.table_rows) {
