@@ -587,6 +587,9 @@ extern "C" int tt_int4_batched_matvec(const void* packed, int64_t w_row_bytes, c
                  x_row, static_cast<uint16_t*>(out), out_row, nullptr, (int)m, (int)rows, (int)cols};
     return launch_mfma<WFmt::kInt4G128>(P, workspace, workspace_floats, st, what);
   }
+  if (m == 1)   // one row: the single-row GEMV itself (its lean int4 kernel)
+    return tt_int4_scaled_matvec(packed, w_row_bytes, scales, TT_F16, s_row, 1, 0, 0, x, TT_F16, out, TT_F16, rows, cols,
+                                 group_size, stream);
   GemvParams P{};
   P.nseg = 1;
   P.seg[0] = Seg{static_cast<const uint8_t*>(packed), w_row_bytes, scales, s_row, 1, out, (int)rows};
