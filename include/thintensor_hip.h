@@ -458,17 +458,17 @@ int tt_moe_router_topk(const void* logits, int logits_dtype, int64_t experts, in
  * The reference has no batched variant (its kernels take one activation vector and
  * its tensor-core variants broadcast it, triton_kernels.py:596-638); these extend
  * TritonDecodeBackend.int4_scaled_matvec (:4597-4743) and scaled_matvec (:4452-4595)
- * to M rows.  M < 16 runs the GEMV engine on up to four rows per launch (row m equals
- * the single-row operator bit for bit); M >= 16 (up to 64) runs an MFMA kernel
- * whose fp32 sums follow the hardware's order (tolerance parity).  cols must be a
- * multiple of 256 up to 8192.  The MFMA path (m >= 16) needs a workspace of
- * tt_batched_workspace_floats(m, rows, cols) floats (0 for m < 16): it splits the
+ * to M rows.  Small M (int4: M < 4, fp8: M < 16) runs the GEMV engine on up to four
+ * rows per launch (row m equals the single-row operator bit for bit); from there (up
+ * to 64) an MFMA kernel runs whose fp32 sums follow the hardware's order (tolerance
+ * parity).  cols must be a multiple of 256 up to 8192.  The MFMA path needs a
+ * workspace of tt_batched_workspace_floats(m, rows, cols) floats (0 for m < 4): it splits the
  * (64-row block, 256-column slice) units evenly over one grid of the workgroups the
  * chip holds at once; a block shared by several workgroups leaves their fp32 partial
  * tiles in the workspace and a second kernel sums them in workgroup order, so the
  * result is the same from run to run.  Calls sharing one workspace must be ordered
  * (same stream).  int4 scales must be 4-byte aligned with an even row stride for
- * m >= 16 (the kernel reads the two group scales of a slice at once). */
+ * m >= 4 (the kernel reads the two group scales of a slice at once). */
 int64_t tt_batched_workspace_floats(int64_t m, int64_t rows, int64_t cols);
 int tt_int4_batched_matvec(const void* packed, int64_t w_row_bytes, const void* scales_f16, int64_t s_row,
                            const void* x, int64_t x_row, void* out, int64_t out_row, int64_t m, int64_t rows,

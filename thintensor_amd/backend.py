@@ -1251,8 +1251,8 @@ class HipDecodeBackend:
     def int4_batched_matvec(self, packed_weight: torch.Tensor, scales: torch.Tensor, x: torch.Tensor,
                             out: torch.Tensor, *, group_size: int = 128) -> torch.Tensor:
         """out[m] = dequant(W) x[m] for x fp16 [M, cols], out fp16 [M, rows]; int4 group-128
-        weights with fp16 scales.  M < 16 is bit-identical to int4_scaled_matvec per row;
-        M >= 16 uses MFMA (tolerance parity)."""
+        weights with fp16 scales.  M < 4 is bit-identical to int4_scaled_matvec per row;
+        M >= 4 uses MFMA (tolerance parity)."""
         _require_cuda(packed_weight, scales, x, out)
         if x.ndim != 2 or out.ndim != 2 or x.shape[0] != out.shape[0]:
             raise ValueError("batched matvec takes x [M, cols] and out [M, rows]")

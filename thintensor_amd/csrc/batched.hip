@@ -1,10 +1,13 @@
 // Batched small-M dequant GEMM: y[m] = W x[m] for M activation rows.
 //
-//   * M < 16: the GEMV engine with up to four activation rows per wave (every
-//     weight word decoded once, one fma chain per activation row), so row m equals
-//     the single-row GEMV bit for bit;
-//   * M >= 16: MFMA.  The four waves of a workgroup own a 64-row block (16 rows
-//     each) and all M (<= 64, in tiles of 16) activation rows; per quantisation
+//   * M below the MFMA threshold (int4: 4, fp8: 16): the GEMV engine with up to four
+//     activation rows per wave (every weight word decoded once, one fma chain per
+//     activation row), so row m equals the single-row GEMV bit for bit (one int4 row
+//     goes to the single-row kernel itself);
+//   * from the threshold (int4 M >= 4, where the engine's per-row fma chains make it
+//     VALU-bound; fp8 M >= 16): MFMA, rows past M clamped to the last one.  The four
+//     waves of a workgroup own a 64-row block (16 rows each) and all M (<= 64, in
+//     tiles of 16) activation rows; per quantisation
 //     group of 128 columns each wave issues four v_mfma_f32_16x16x32_f16 with the
 //     dequantised weights as the A operand (int4: code times group scale, rounded
 //     to fp16; fp8: exact) and the activations (staged in LDS per 256-column slice)
@@ -438,7 +441,7 @@ int launch_mfma(MfmaParams P, float* ws, int64_t ws_floats, hipStream_t st, cons
   P.grid = (int)mfma_grid(P.units, mt);
   TT_REQUIRE(P.spb >= 1 && P.units >= 1 && P.grid >= 1, "%s: bad MFMA grid", what);
   TT_REQUIRE(ws != nullptr && ws_floats >= mfma_ws_floats(P.m, P.n, P.k),
-             "%s: workspace of tt_batched_workspace_floats(m, rows, cols) floats required for m >= 16", what);
+             "%s: workspace of tt_batched_workspace_floats(m, rows, cols) floats required on the MFMA path", what);
   P.ws = ws;
   P.ws_row_scale = W == WFmt::kFp8Row ? 1 : 0;
   const dim3 grid((unsigned)P.grid);
@@ -561,8 +564,12 @@ int dense_bias_rows_f16(const void* weight, int64_t w_row, const void* bias, con
 }
 }  // namespace tt
 
+// Smallest M that runs on MFMA (tolerance parity from there; bit-exact GEMV below).
+constexpr int kInt4MfmaMin = 4;
+constexpr int kFp8MfmaMin = 16;
+
 extern "C" int64_t tt_batched_workspace_floats(int64_t m, int64_t rows, int64_t cols) {
-  if (m < 16 || m > 64 || rows <= 0 || cols < kSlice) return 0;
+  if (m < kInt4MfmaMin || m > 64 || rows <= 0 || cols < kSlice) return 0;
   return mfma_ws_floats(m, rows, cols);
 }
 
@@ -580,8 +587,8 @@ extern "C" int tt_int4_batched_matvec(const void* packed, int64_t w_row_bytes, c
   TT_REQUIRE(scales && x && out && aligned(x, 16) && x_row % 8 == 0 && x_row >= cols && out_row >= rows,
              "%s: null or misaligned pointer / bad row strides", what);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (m >= 16) {
-    TT_REQUIRE(aligned(scales, 4) && s_row % 2 == 0, "%s: m >= 16 reads scale pairs: 4-byte aligned scales, even row stride",
+  if (m >= kInt4MfmaMin) {
+    TT_REQUIRE(aligned(scales, 4) && s_row % 2 == 0, "%s: m >= 4 reads scale pairs: 4-byte aligned scales, even row stride",
                what);
     MfmaParams P{static_cast<const uint8_t*>(packed), w_row_bytes, scales, s_row, static_cast<const uint16_t*>(x),
                  x_row, static_cast<uint16_t*>(out), out_row, nullptr, (int)m, (int)rows, (int)cols};
@@ -611,7 +618,7 @@ extern "C" int tt_scaled_batched_matvec(const void* weight, int64_t w_row_bytes,
   TT_REQUIRE(scales && x && out && aligned(x, 16) && x_row % 8 == 0 && x_row >= cols && out_row >= rows,
              "%s: null or misaligned pointer / bad row strides", what);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (m >= 16) {
+  if (m >= kFp8MfmaMin) {
     MfmaParams P{static_cast<const uint8_t*>(weight), w_row_bytes, scales, 1, static_cast<const uint16_t*>(x), x_row,
                  static_cast<uint16_t*>(out), out_row, nullptr, (int)m, (int)rows, (int)cols};
     return launch_mfma<WFmt::kFp8Row>(P, workspace, workspace_floats, st, what);
