@@ -191,13 +191,146 @@ __global__ __launch_bounds__(256) void swiglu_lean_kernel(const SwigluParams P) 
   store<OT>(reinterpret_cast<OT*>(P.out) + (int64_t)slot * P.out_slot + a, num / den);
 }
 
+// swiglu_lean_kernel with KB consecutive row blocks per workgroup (ROWS = 2, rows of at
+// most three rounds): the slot's activations are staged once, and block k + 1's weight
+// rounds are in flight while block k computes, so a workgroup waits for memory once per
+// launch rather than once per block and the grid has KB times fewer workgroups.  Each
+// row's arithmetic is swiglu_lean_kernel's (same chunk partition, fma order, reduction
+// and epilogue), so the bits are the same.
+template <Fmt F, typename XT, typename OT, typename RT, typename BT, int LPR, int KB>
+__global__ __launch_bounds__(256) void swiglu_lean_multi_kernel(const SwigluParams P, int nblocks) {
+  constexpr int ROWS = 2;
+  constexpr int B = FmtInfo<F>::kBytes;
+  constexpr int SUBS = 64 / LPR;
+  constexpr int R = 3;   // rounds per row (the host checks)
+  extern __shared__ uint32_t xs_lds[];
+  const int slot = blockIdx.y;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int sub = lane / LPR, l = lane % LPR;
+  const int nchunks = P.cols >> 5;
+  const int rounds = (nchunks + LPR - 1) / LPR;
+  const int xn = P.cols >> 3;
+  const uint4* xg = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(P.x) + (int64_t)(slot / P.x_div) * P.x_slot);
+  uint4 xreg[4];
+  int xidx[4];
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const int idx = threadIdx.x + 256 * k;
+    xidx[k] = idx < xn ? idx : xn - 1;
+    xreg[k] = xg[xidx[k]];
+  }
+  const int64_t e = P.experts[slot];
+  const uint8_t* wexp = P.w + e * P.w_expert;
+  const uint8_t* sexp = P.s + e * P.s_expert;
+  struct Round {
+    Raw<B> w[ROWS];
+    uint8_t ex[ROWS];
+  };
+  // activation row of block kb for this lane, clamped, and the block's rows
+  auto block_row = [&](int kb) -> int {
+    const int bx = (int)blockIdx.x * KB + kb;
+    return (bx * 4 + wave) * SUBS + sub;
+  };
+  auto fetch_block = [&](int kb, Round* d) {
+    const int a = block_row(kb);
+    const int ac = a < P.act_rows ? a : P.act_rows - 1;
+    const uint8_t* w0 = wexp + 2 * (int64_t)ac * P.w_row;
+    const uint8_t* s0 = sexp + 2 * (int64_t)ac * P.s_row;
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      uint32_t j = (uint32_t)(r * LPR + l);
+      j = j < (uint32_t)nchunks ? j : (uint32_t)nchunks - 1;
+#pragma unroll
+      for (int i = 0; i < ROWS; i++) {
+        d[r].w[i] = load_raw<B>(w0 + i * P.w_row + j * (uint32_t)B);
+        d[r].ex[i] = s0[i * P.s_row + j];
+      }
+    }
+  };
+  Round d[2][R];
+  fetch_block(0, d[0]);
+  uint4* xl = reinterpret_cast<uint4*>(xs_lds);
+#pragma unroll
+  for (int k = 0; k < 4; k++) xl[xidx[k]] = xreg[k];
+  for (int idx = threadIdx.x + 1024; idx < xn; idx += 256) xl[idx] = xg[idx];
+  lds_barrier();
+
+#pragma unroll
+  for (int kb = 0; kb < KB; kb++) {
+    if ((int)blockIdx.x * KB + kb >= nblocks) break;   // uniform: past the last row block
+    if (kb + 1 < KB && (int)blockIdx.x * KB + kb + 1 < nblocks) fetch_block(kb + 1, d[(kb + 1) & 1]);
+    const Round* c = d[kb & 1];
+    const int a = block_row(kb);
+    const bool av = a < P.act_rows;
+    float acc[ROWS];
+#pragma unroll
+    for (int i = 0; i < ROWS; i++) acc[i] = 0.0f;
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      if (r < rounds) {
+        const int j = r * LPR + l;
+        const bool cv = j < nchunks;
+        uint32_t xw[16];
+        const uint4* xp = reinterpret_cast<const uint4*>(xs_lds + (cv ? j : 0) * 16);
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const uint4 v = xp[q];
+          xw[4 * q] = v.x; xw[4 * q + 1] = v.y; xw[4 * q + 2] = v.z; xw[4 * q + 3] = v.w;
+        }
+        float p[ROWS];
+        chunk_dot_rows<F, XT, ROWS>(c[r].w, xw, p);
+#pragma unroll
+        for (int i = 0; i < ROWS; i++) {
+          const float t = p[i] * pow2i((int)c[r].ex[i] - 127);
+          acc[i] = acc[i] + ((cv && av) ? t : 0.0f);
+        }
+      }
+    }
+    reduce_range<ROWS, 1, LPR>(acc);
+    const float v = acc[0];
+    const float pv = xor_partner<ROWS / 2>(v);   // the other row of the gate/up pair
+    const int br = rs_row<ROWS>(l, log2c(ROWS), 0);
+    if ((l >> log2c(ROWS)) == 0 && (br & 1) == 0 && av) {
+      float g = round_to<RT>(v);
+      float u = round_to<RT>(pv);
+      if (P.bias != nullptr) {
+        const int64_t bb = e * P.bias_expert + 2 * (int64_t)a;
+        g = round_to<RT>(g + ld_bias<BT>(P.bias, bb));
+        u = round_to<RT>(u + ld_bias<BT>(P.bias, bb + 1));
+      }
+      g = fminf(g, P.limit);
+      u = fmaxf(fminf(u, P.limit), -P.limit);
+      const float num = (u + 1.0f) * g;
+      const float den = 1.0f + exp_f32(-g * P.alpha);
+      store<OT>(reinterpret_cast<OT*>(P.out) + (int64_t)slot * P.out_slot + a, num / den);
+    }
+  }
+}
+
 // ------------------------------------------------------------------ dispatch
+
+// Row blocks per workgroup of swiglu_lean_multi_kernel: 2 once the one-block grid would
+// be several generations of workgroups deep, 1 (swiglu_lean_kernel) otherwise.
+constexpr int kSwigluMultiBlocks = 2;
+constexpr int64_t kSwigluMultiMinWorkgroups = 4096;
 
 template <Fmt F, typename XT, typename OT, typename RT, typename BT, int LPR>
 static int launch_swiglu_lean(const SwigluParams& P, int slots, hipStream_t st) {
   constexpr int SUBS = 64 / LPR;
   const int per_wave = SUBS;   // one activation row (two weight rows) per lane group
   const int64_t waves = ((int64_t)P.act_rows + per_wave - 1) / per_wave;
+  const int64_t nblocks = (waves + 3) / 4;
+  const int rounds = (P.cols / 32 + LPR - 1) / LPR;
+  if (rounds <= 3 && nblocks * slots >= kSwigluMultiMinWorkgroups) {
+    constexpr int KB = kSwigluMultiBlocks;
+    // a multiple of 8 workgroups per slot, so that the workgroups of one row block for
+    // every slot sit on the same XCD (slots sharing an expert share its L2 lines)
+    const int64_t groups = ((nblocks + KB - 1) / KB + 7) / 8 * 8;
+    hipLaunchKernelGGL((swiglu_lean_multi_kernel<F, XT, OT, RT, BT, LPR, KB>), dim3((unsigned)groups, slots), dim3(256),
+                       (size_t)P.cols * 2, st, P, (int)nblocks);
+    return check_launch("mxfp_lowbit_selected_swiglu");
+  }
   hipLaunchKernelGGL((swiglu_lean_kernel<F, XT, OT, RT, BT, LPR, 2>), dim3((unsigned)((waves + 3) / 4), slots),
                      dim3(256), (size_t)P.cols * 2, st, P);
   return check_launch("mxfp_lowbit_selected_swiglu");
