@@ -159,7 +159,9 @@ def test_rope_table_and_device_position(backend, device):
 
 @pytest.mark.parametrize("cap", [1100, 1152])  # 1152: whole chunks, contiguous rows -> vector-load kernel
 @pytest.mark.parametrize("heads,kv_heads,tokens,sinks", [(32, 8, 513, False), (64, 8, 1025, True), (8, 8, 5, False),
-                                                         (32, 8, 64, True), (128, 8, 1100, False)])
+                                                         (32, 8, 64, True), (128, 8, 1100, False),
+                                                         # 64 KV heads x 18 chunks: two chunks per workgroup
+                                                         (256, 64, 1025, True), (512, 64, 705, False)])
 def test_gqa_attention(backend, device, heads, kv_heads, tokens, sinks, cap):
     D = 64
     g = rng(heads + tokens)

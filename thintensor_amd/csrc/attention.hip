@@ -564,10 +564,15 @@ __device__ __forceinline__ float ld_dev(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <typename T, typename SKT, int G>
+template <typename T, typename SKT, int G, int CPW = 1>
 __global__ __launch_bounds__(64 * G) void attn_kvchunk_kernel(AttnParams P, int* counters) {
+  // CPW chunks per workgroup (1 or 2): with 2, both chunks' K and V pieces are requested
+  // up front and the chunks are computed one after the other through the same LDS, which
+  // halves the grid when it is several generations of workgroups deep; every chunk's
+  // partial is computed exactly as with one chunk per workgroup
+  static_assert(CPW == 1 || CPW == 2, "one or two chunks per workgroup");
   constexpr int D = 64;
-  const int c = blockIdx.x, kvh = blockIdx.y;
+  const int c0 = blockIdx.x * CPW, kvh = blockIdx.y;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int h = kvh * G + wave;
@@ -578,86 +583,105 @@ __global__ __launch_bounds__(64 * G) void attn_kvchunk_kernel(AttnParams P, int*
   __shared__ int last;
   const float ninf = __builtin_bit_cast(float, 0xff800000u);
   // every load before the active count is known (chunks below max_chunks are inside
-  // the capacity): K and V pieces of the chunk, this wave's query row
-  const uint4* kblk = reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(P.keys) + kvh * P.k_head) +
-                      (int64_t)c * (kChunk * D / 8);
-  const uint4* vblk = reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(P.values) + kvh * P.v_head) +
-                      (int64_t)c * (kChunk * D / 8);
+  // the capacity; a second chunk past them is clamped to the last one, values unused):
+  // K and V pieces of the chunks, this wave's query row
   constexpr int kPer = kChunk * D / 8 / nthr;   // 16-byte pieces per thread
-  uint4 kr[kPer], vr[kPer];
+  // (native 4-vectors: arrays of the uint4 struct type are kept in scratch memory here)
+  typedef uint32_t piece_t __attribute__((ext_vector_type(4)));
+  piece_t kr[kPer], vr[kPer], kr1[kPer], vr1[kPer];
+  auto load_chunk = [&](int c, piece_t (&kk)[kPer], piece_t (&vv)[kPer]) {
+    const piece_t* kblk = reinterpret_cast<const piece_t*>(reinterpret_cast<const T*>(P.keys) + kvh * P.k_head) +
+                          (int64_t)c * (kChunk * D / 8);
+    const piece_t* vblk = reinterpret_cast<const piece_t*>(reinterpret_cast<const T*>(P.values) + kvh * P.v_head) +
+                          (int64_t)c * (kChunk * D / 8);
 #pragma unroll
-  for (int j = 0; j < kPer; j++) {
-    kr[j] = kblk[(int)threadIdx.x + nthr * j];
-    vr[j] = vblk[(int)threadIdx.x + nthr * j];
-  }
+    for (int j = 0; j < kPer; j++) {
+      kk[j] = kblk[(int)threadIdx.x + nthr * j];
+      vv[j] = vblk[(int)threadIdx.x + nthr * j];
+    }
+  };
+  load_chunk(c0, kr, vr);
+  if constexpr (CPW == 2) load_chunk(c0 + 1 < P.max_chunks ? c0 + 1 : P.max_chunks - 1, kr1, vr1);
   const T qraw = reinterpret_cast<const T*>(P.q)[(int64_t)h * D + lane];
   const int T_act = min(P.tokens_dev ? P.tokens_dev[0] + P.tokens : P.tokens, P.max_tokens);
   const int nc = T_act > 0 ? (T_act + kChunk - 1) / kChunk : 0;
-  if (c >= nc) return;
-  const int nt = min(kChunk, T_act - c * kChunk);
-#pragma unroll
-  for (int j = 0; j < kPer; j++) {
-    const int pidx = (int)threadIdx.x + nthr * j;
-    const int r = pidx >> 3, col = pidx & 7;
-    ks[r * 8 + (col ^ (r & 7))] = kr[j];
-    const uint32_t keep = r < nt ? ~0u : 0u;
-    vs_s[pidx] = uint4{vr[j].x & keep, vr[j].y & keep, vr[j].z & keep, vr[j].w & keep};
-  }
+  if (c0 >= nc) return;
+  const int done = min(CPW, nc - c0);   // active chunks of this workgroup
   q_s[wave][lane] = to_f32(qraw);
-  __syncthreads();
 
-  // ---- chunk partial of query head h (lane = token, then lane = dimension)
-  const int t = c * kChunk + lane;
-  const bool valid = t < T_act;
-  uint32_t krow[8][4];
 #pragma unroll
-  for (int d = 0; d < 8; d++) {
-    const uint4 k = ks[lane * 8 + (d ^ (lane & 7))];
-    krow[d][0] = k.x; krow[d][1] = k.y; krow[d][2] = k.z; krow[d][3] = k.w;
-  }
-  const float* qw = q_s[wave];
-  float sc = 0.0f;
+  for (int cc = 0; cc < CPW; cc++) {
+    if (cc >= done) break;   // uniform
+    const int c = c0 + cc;
+    if (cc > 0) __syncthreads();   // the previous chunk's LDS reads are done
+    const int nt = min(kChunk, T_act - c * kChunk);
+    auto stage = [&](const piece_t (&kk)[kPer], const piece_t (&vv)[kPer]) {
 #pragma unroll
-  for (int i = 0; i < D / 8; i++) {
-    if ((i & 3) == 0) asm volatile("" : "+v"(sc)::"memory");
-    const uint32_t* kw = krow[i];
+      for (int j = 0; j < kPer; j++) {
+        const int pidx = (int)threadIdx.x + nthr * j;
+        const int r = pidx >> 3, col = pidx & 7;
+        reinterpret_cast<piece_t*>(ks)[r * 8 + (col ^ (r & 7))] = kk[j];
+        const uint32_t keep = r < nt ? ~0u : 0u;
+        reinterpret_cast<piece_t*>(vs_s)[pidx] = vv[j] & keep;
+      }
+    };
+    if (cc == 0) stage(kr, vr);
+    else stage(kr1, vr1);
+    __syncthreads();
+
+    // ---- chunk partial of query head h (lane = token, then lane = dimension)
+    const int t = c * kChunk + lane;
+    const bool valid = t < T_act;
+    uint32_t krow[8][4];
 #pragma unroll
-    for (int e = 0; e < 8; e++) {
-      const float kv = (e & 1) ? hi_f32<T>(kw[e >> 1]) : lo_f32<T>(kw[e >> 1]);
-      sc = __builtin_fmaf(qw[8 * i + e], kv, sc);
+    for (int d = 0; d < 8; d++) {
+      const uint4 k = ks[lane * 8 + (d ^ (lane & 7))];
+      krow[d][0] = k.x; krow[d][1] = k.y; krow[d][2] = k.z; krow[d][3] = k.w;
     }
-  }
-  const float s = valid ? sc * P.scale : ninf;
-  float m = s;
-  m = fmaxf(m, xor_partner<1>(m));
-  m = fmaxf(m, xor_partner<2>(m));
-  m = fmaxf(m, xor_partner<4>(m));
-  m = fmaxf(m, xor_partner<8>(m));
-  m = fmaxf(m, xor_partner<16>(m));
-  m = fmaxf(m, xor_partner<32>(m));
-  const float p = valid ? exp_f32(s - m) : 0.0f;
-  const float l = xor_sum(p, 1, 64);
-  float* p_w = p_s[wave];
-  p_w[lane] = p;
-  __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's p stores done
-  __builtin_amdgcn_wave_barrier();
-  const T* vsp = reinterpret_cast<const T*>(vs_s);
-  float o = 0.0f;
+    const float* qw = q_s[wave];
+    float sc = 0.0f;
 #pragma unroll
-  for (int tt = 0; tt < kChunk; tt++) {
-    if ((tt & 31) == 0) asm volatile("" : "+v"(o)::"memory");
-    o = __builtin_fmaf(p_w[tt], to_f32(vsp[tt * D + lane]), o);
+    for (int i = 0; i < D / 8; i++) {
+      if ((i & 3) == 0) asm volatile("" : "+v"(sc)::"memory");
+      const uint32_t* kw = krow[i];
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const float kv = (e & 1) ? hi_f32<T>(kw[e >> 1]) : lo_f32<T>(kw[e >> 1]);
+        sc = __builtin_fmaf(qw[8 * i + e], kv, sc);
+      }
+    }
+    const float s = valid ? sc * P.scale : ninf;
+    float m = s;
+    m = fmaxf(m, xor_partner<1>(m));
+    m = fmaxf(m, xor_partner<2>(m));
+    m = fmaxf(m, xor_partner<4>(m));
+    m = fmaxf(m, xor_partner<8>(m));
+    m = fmaxf(m, xor_partner<16>(m));
+    m = fmaxf(m, xor_partner<32>(m));
+    const float p = valid ? exp_f32(s - m) : 0.0f;
+    const float l = xor_sum(p, 1, 64);
+    float* p_w = p_s[wave];
+    p_w[lane] = p;
+    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's p stores done
+    __builtin_amdgcn_wave_barrier();
+    const T* vsp = reinterpret_cast<const T*>(vs_s);
+    float o = 0.0f;
+#pragma unroll
+    for (int tt = 0; tt < kChunk; tt++) {
+      if ((tt & 31) == 0) asm volatile("" : "+v"(o)::"memory");
+      o = __builtin_fmaf(p_w[tt], to_f32(vsp[tt * D + lane]), o);
+    }
+    const int64_t slot = (int64_t)h * P.max_chunks + c;
+    if (lane == 0) {
+      st_dev(P.part_m + slot, m);
+      st_dev(P.part_l + slot, l);
+    }
+    st_dev(P.part_o + slot * D + lane, o);
   }
-  const int64_t slot = (int64_t)h * P.max_chunks + c;
-  if (lane == 0) {
-    st_dev(P.part_m + slot, m);
-    st_dev(P.part_l + slot, l);
-  }
-  st_dev(P.part_o + slot * D + lane, o);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (threadIdx.x == 0)
-    last = __hip_atomic_fetch_add(counters + kvh, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nc - 1;
+    last = __hip_atomic_fetch_add(counters + kvh, done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nc - done;
   __syncthreads();
   if (!last) return;
 
@@ -719,11 +743,24 @@ __global__ __launch_bounds__(64 * G) void attn_kvchunk_kernel(AttnParams P, int*
   if (threadIdx.x == 0) __hip_atomic_store(counters + kvh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Two chunks per workgroup once the one-chunk grid holds more workgroups than this.
+constexpr int64_t kAttnPairMinWorkgroups = 1024;
+
 template <typename T, int G>
 static int launch_attn(const AttnParams& P, int sink_dtype, bool contiguous64, int* counters, hipStream_t st) {
   if constexpr (G <= 8) {
     if (contiguous64 && counters != nullptr) {
-      const dim3 grid((unsigned)P.max_chunks, (unsigned)P.kv_heads), block(64 * G);
+      const dim3 block(64 * G);
+      if ((int64_t)P.max_chunks * P.kv_heads > kAttnPairMinWorkgroups) {
+        const dim3 grid((unsigned)((P.max_chunks + 1) / 2), (unsigned)P.kv_heads);
+        switch (sink_dtype) {
+          case TT_BF16: hipLaunchKernelGGL((attn_kvchunk_kernel<T, bf16_t, G, 2>), grid, block, 0, st, P, counters); break;
+          case TT_F32: hipLaunchKernelGGL((attn_kvchunk_kernel<T, float, G, 2>), grid, block, 0, st, P, counters); break;
+          default: hipLaunchKernelGGL((attn_kvchunk_kernel<T, f16_t, G, 2>), grid, block, 0, st, P, counters); break;
+        }
+        return check_launch("gqa_attention");
+      }
+      const dim3 grid((unsigned)P.max_chunks, (unsigned)P.kv_heads);
       switch (sink_dtype) {
         case TT_BF16: hipLaunchKernelGGL((attn_kvchunk_kernel<T, bf16_t, G>), grid, block, 0, st, P, counters); break;
         case TT_F32: hipLaunchKernelGGL((attn_kvchunk_kernel<T, float, G>), grid, block, 0, st, P, counters); break;
