@@ -16,8 +16,9 @@ constexpr const char* kWhat = "fused_gemv";
 // rows per wave (segments padded to whole batches, as in gemv_kernel), the RMSNorm
 // prologue and the RoPE / KV-cache / SiLU epilogues of gemv_kernel with the same
 // row pairing, rounding points and reduction order, without its persistent loop.
-// The weight and scale loads of round 0 are issued before the prologue's loads, so
-// the prologue's memory wait overlaps the weight stream.
+// The prologue's inputs (and the token position of the epilogues) are requested first,
+// then round 0's weights and scales, so the prologue's memory wait overlaps the weight
+// stream without waiting behind it.
 struct LeanSeg {
   const uint8_t* w;     // weights (kSegSilu: gate rows)
   const uint8_t* w2;    // kSegSilu: up rows
