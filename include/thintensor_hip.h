@@ -417,6 +417,26 @@ int tt_single_token_gqa_attention(const void* q, const void* keys, const void* v
                                   int64_t head_dim, float* scratch, int64_t scratch_floats, void* out,
                                   void* stream);
 
+/* Attention then o_proj in two launches, the decode step's single_token_gqa_attention
+ * followed by the o_proj int4_scaled_matvec (triton_kernels.py:5228-5278, then the
+ * o_proj matvec of gpu_runtime.py's layer loop).  The first call stores the chunk
+ * partials into the attention scratch only (head_dim-64 caches of whole 64-token
+ * chunks, 1/2/4/8 query heads per KV head, no sinks); the second combines them into the
+ * activation -- the bits tt_single_token_gqa_attention writes to `out` -- and runs the
+ * int4 group-128 GEMV (fp16 scales [rows, cols/128] with strides s_row, s_group) over it:
+ * out [rows] = W [rows, heads*64] x combined.  attn_out (optional) receives the
+ * combined activation.  At most 32 query heads; same scratch, token count and capacity
+ * in both calls, on one stream. */
+int tt_single_token_gqa_attention_partials(const void* q, const void* keys, const void* values, int dtype,
+                                           int64_t k_head, int64_t k_tok, int64_t v_head, int64_t v_tok,
+                                           const int32_t* tokens_dev, int64_t tokens, int64_t max_tokens,
+                                           int64_t heads, int64_t kv_heads, int64_t head_dim, float* scratch,
+                                           int64_t scratch_floats, void* stream);
+int tt_attention_combine_int4_matvec(const float* scratch, int64_t scratch_floats, const int32_t* tokens_dev,
+                                     int64_t tokens, int64_t max_tokens, int64_t heads, int64_t head_dim, int dtype,
+                                     const void* packed, int64_t w_row_bytes, const void* scales, int64_t s_row,
+                                     int64_t s_group, void* attn_out, void* out, int64_t rows, void* stream);
+
 /* Router GEMV + bias + top-k + softmax (E <= 128), logits rounded through bf16.
  * Replaces TritonDecodeBackend.moe_router_matvec_topk (triton_kernels.py:5826-5860;
  * kernel :2855-2921). */

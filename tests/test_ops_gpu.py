@@ -392,3 +392,60 @@ def test_unrounded_argmax_matches_binary32_logits(backend, device, rows, cols):
                        odtype=oracle.F32)
     assert int(tok.item()) == int(np.argmax(lg32))
     assert int(np.argmax(lg32)) == int(np.argmax(ref.gemv64(w, x)))
+
+
+@pytest.mark.parametrize("heads,kv_heads,tokens,cap", [
+    (32, 8, 577, 640),     # the 1B decode shape: ten active chunks, all from the first request
+    (32, 8, 1500, 1536),   # 24 chunks: past the 16 requested with the weights
+    (16, 16, 1, 64),       # one token, one query head per KV head
+    (32, 4, 130, 1024),    # eight query heads per KV head, most of the capacity unused
+    (8, 2, 200, 256),      # four heads of 64 (cols 512: 16 lanes per row)
+])
+def test_attention_then_int4_matvec(backend, device, heads, kv_heads, tokens, cap):
+    """o_proj that combines the attention chunk partials itself: the combined activation
+    equals single_token_gqa_attention's output bit for bit (and the oracle's), and the
+    GEMV equals int4_scaled_matvec over it (and the oracle's) bit for bit.  Two calls in
+    a row on one scratch, the second with fewer tokens."""
+    from thintensor_amd import layouts
+
+    D = 64
+    cols, rows = heads * D, 2048
+    g = rng(heads * 7 + tokens)
+    q = f16_normal(g, cols)
+    keys = f16_normal(g, (kv_heads, cap, D))
+    vals = f16_normal(g, (kv_heads, cap, D))
+    codes = g.integers(0, 16, size=(rows, cols), dtype=np.uint8)
+    packed = layouts.pack_int4(codes)
+    scales = (np.abs(g.standard_normal((rows, cols // 128))) * 0.02).astype(np.float16)
+    qd, kd, vd = to_torch(q, device), to_torch(keys, device), to_torch(vals, device)
+    pd, sd = to_torch(packed, device), to_torch(scales, device)
+    attn = torch.empty(cols, device=device, dtype=torch.float16)
+    attn_ref = torch.empty(cols, device=device, dtype=torch.float16)
+    out = torch.empty(rows, device=device, dtype=torch.float16)
+    out_ref = torch.empty(rows, device=device, dtype=torch.float16)
+    for n in (tokens, max(1, tokens // 2 - 3)):
+        pos = torch.tensor([n - 1], dtype=torch.int32, device=device)
+        backend.attention_then_int4_matvec(qd, kd, vd, heads, kv_heads, D, pd, sd, out, active_tokens=(pos, 1),
+                                           attn_out=attn)
+        backend.single_token_gqa_attention(qd, kd, vd, attn_ref, heads, kv_heads, D, active_tokens=(pos, 1))
+        backend.int4_scaled_matvec(pd, sd, attn_ref, out_ref, rows=rows, cols=cols, group_size=128)
+        assert_bits_equal(from_torch_bits(attn), from_torch_bits(attn_ref), f"combined activation ({n} tokens)")
+        assert_bits_equal(from_torch_bits(out), from_torch_bits(out_ref), f"o_proj ({n} tokens)")
+        want_attn = np.empty(cols, dtype=np.float16)
+        oracle.lib().tto_attention(P(q), P(keys), P(vals), oracle.F16, cap * D, D, cap * D, D, None, oracle.F16, n,
+                                   heads, kv_heads, D, P(want_attn))
+        assert_bits_equal(from_torch_bits(attn), want_attn, f"attention vs oracle ({n} tokens)")
+        want = oracle.gemv("int4_sym", "group", packed, scales, want_attn, cols=cols, lpr=lanes(cols, 4), L=4,
+                           s_row=cols // 128, s_grp=1)
+        assert_bits_equal(from_torch_bits(out), want, f"o_proj vs oracle ({n} tokens)")
+
+
+def test_attention_then_int4_matvec_rejects(backend, device):
+    D, heads = 64, 48   # more than 32 query heads
+    q = torch.zeros(heads * D, device=device, dtype=torch.float16)
+    kv = torch.zeros((heads, 64, D), device=device, dtype=torch.float16)
+    pk = torch.zeros((16, heads * D // 2), device=device, dtype=torch.uint8)
+    sc = torch.zeros((16, heads * D // 128), device=device, dtype=torch.float16)
+    out = torch.empty(16, device=device, dtype=torch.float16)
+    with pytest.raises((ValueError, NotImplementedError, RuntimeError)):
+        backend.attention_then_int4_matvec(q, kv, kv, heads, heads, D, pk, sc, out, active_tokens=10)

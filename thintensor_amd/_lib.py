@@ -119,6 +119,8 @@ SIGNATURES: dict[str, list] = {
     "tt_attention_scratch_floats": [_L, _L, _L],
     "tt_single_token_gqa_attention": [_P, _P, _P, _I, _L, _L, _L, _L, _P, _I, _P, _L, _L, _L, _L, _L, _P, _L, _P,
                                       _P],
+    "tt_single_token_gqa_attention_partials": [_P, _P, _P, _I, _L, _L, _L, _L, _P, _L, _L, _L, _L, _L, _P, _L, _P],
+    "tt_attention_combine_int4_matvec": [_P, _L, _P, _L, _L, _L, _L, _I, _P, _L, _P, _L, _L, _P, _P, _L, _P],
     "tt_moe_router_matvec_topk": [_P, _I, _L, _P, _I, _L, _P, _I, _L, _L, _I, _P, _P, _I, _P],
     "tt_moe_router_topk": [_P, _I, _L, _L, _I, _P, _P, _I, _P],
     "tt_add_rms_norm_router_topk": [_P, _P, _P, _I, _P, _I, _P, _I, _L, _F, _P, _I, _L, _P, _I, _L, _L, _I, _P, _P,

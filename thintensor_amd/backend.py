@@ -1142,6 +1142,66 @@ class HipDecodeBackend:
         _lib.check(rc, "single_token_gqa_attention")
         return out
 
+    def attention_then_int4_matvec(
+        self,
+        query: torch.Tensor,
+        keys: torch.Tensor,
+        values: torch.Tensor,
+        heads: int,
+        kv_heads: int,
+        head_dim: int,
+        packed_weight: torch.Tensor,
+        scales: torch.Tensor,
+        out: torch.Tensor,
+        active_tokens: torch.Tensor | int | tuple | None = None,
+        attn_out: torch.Tensor | None = None,
+    ) -> torch.Tensor:
+        """Decode attention followed by the int4 (group 128, fp16 scales) o_proj GEMV
+        (triton_kernels.py:5228-5278, then the o_proj matvec of gpu_runtime.py's layer
+        loop) in two launches: the attention kernel stores its chunk partials only, and the
+        GEMV combines them into its activation (the bits ``single_token_gqa_attention``
+        writes) before the product.  ``attn_out``, when given, receives that activation.
+        Head_dim-64 caches, at most 32 query heads, no sinks."""
+        capacity = int(keys.shape[1])
+        offset = 0
+        tokens = capacity if active_tokens is None else active_tokens
+        if isinstance(tokens, tuple):
+            tokens, offset = tokens
+        if isinstance(tokens, int) and tokens <= 0:
+            raise ValueError("attention requires at least one KV token")
+        _require_cuda(query, keys, values, packed_weight, scales, out)
+        rows, cols = int(out.shape[-1]), heads * head_dim
+        if int(packed_weight.shape[0]) != rows or packed_weight.shape[1] * packed_weight.element_size() * 2 != cols:
+            raise ValueError(f"int4 packed weight {tuple(packed_weight.shape)} does not match rows={rows} cols={cols}")
+        if scales.dtype != torch.float16 or tuple(scales.shape) != (rows, cols // 128):
+            raise ValueError("o_proj scales must be fp16 [rows, cols / 128]")
+        scratch = self._attention_scratch(heads, capacity, head_dim)
+        if isinstance(tokens, torch.Tensor):
+            if tokens.dtype != torch.int32:
+                raise ValueError("active_tokens device tensor must be int32")
+            tok_dev, tok = tokens.data_ptr(), int(offset)
+        else:
+            tok_dev, tok = None, int(tokens)
+        code = _code(keys, "attention")
+        rc = self.lib.tt_single_token_gqa_attention_partials(
+            query.data_ptr(), keys.data_ptr(), values.data_ptr(), code, keys.stride(0), keys.stride(1),
+            values.stride(0), values.stride(1), tok_dev, tok, capacity, heads, kv_heads, head_dim,
+            scratch.data_ptr(), scratch.numel(), _stream(out),
+        )
+        _lib.check(rc, "single_token_gqa_attention_partials")
+        if attn_out is not None:
+            _require_cuda(attn_out)
+            if attn_out.dtype != keys.dtype or attn_out.numel() != cols:
+                raise ValueError("attn_out must hold heads * head_dim values of the cache dtype")
+        rc = self.lib.tt_attention_combine_int4_matvec(
+            scratch.data_ptr(), scratch.numel(), tok_dev, tok, capacity, heads, head_dim, code,
+            packed_weight.data_ptr(), packed_weight.stride(0) * packed_weight.element_size(), scales.data_ptr(),
+            scales.stride(0), scales.stride(1), attn_out.data_ptr() if attn_out is not None else None,
+            out.data_ptr(), rows, _stream(out),
+        )
+        _lib.check(rc, "attention_combine_int4_matvec")
+        return out
+
     def split_single_token_gqa_attention(self, query, keys, values, out, heads, kv_heads, head_dim):
         """Split-KV attention (triton_kernels.py:5280-5363): the HIP kernel always splits
         the sequence into 64-token chunks."""

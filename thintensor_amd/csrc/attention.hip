@@ -564,7 +564,7 @@ __device__ __forceinline__ float ld_dev(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <typename T, typename SKT, int G, int CPW = 1>
+template <typename T, typename SKT, int G, int CPW = 1, bool COMBINE = true>
 __global__ __launch_bounds__(64 * G) void attn_kvchunk_kernel(AttnParams P, int* counters) {
   // CPW chunks per workgroup (1 or 2): with 2, both chunks' K and V pieces are requested
   // up front and the chunks are computed one after the other through the same LDS, which
@@ -678,6 +678,9 @@ __global__ __launch_bounds__(64 * G) void attn_kvchunk_kernel(AttnParams P, int*
     }
     st_dev(P.part_o + slot * D + lane, o);
   }
+  // without COMBINE the partials are the result: the kernel that consumes them runs after
+  // this one on the stream
+  if constexpr (!COMBINE) return;
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (threadIdx.x == 0)
@@ -814,6 +817,68 @@ constexpr int kAttnCounters = 1024;
 extern "C" int tt_attention_scratch_floats(int64_t heads, int64_t max_tokens, int64_t head_dim) {
   const int64_t chunks = (max_tokens + kChunk - 1) / kChunk;
   return (int)(kAttnCounters + heads * chunks * (2 + head_dim));
+}
+
+// Chunk partials only (contiguous head_dim-64 caches, whole-chunk capacity, no sinks):
+// the one-launch kernel without its arrival count and combine, for a consumer that
+// combines the partials itself (tt_attention_combine_int4_matvec).
+template <typename T, int G>
+static int launch_attn_partials(const AttnParams& P, hipStream_t st) {
+  const dim3 block(64 * G);
+  if ((int64_t)P.max_chunks * P.kv_heads > kAttnPairMinWorkgroups)
+    hipLaunchKernelGGL((attn_kvchunk_kernel<T, f16_t, G, 2, false>), dim3((unsigned)((P.max_chunks + 1) / 2), (unsigned)P.kv_heads),
+                       block, 0, st, P, nullptr);
+  else
+    hipLaunchKernelGGL((attn_kvchunk_kernel<T, f16_t, G, 1, false>), dim3((unsigned)P.max_chunks, (unsigned)P.kv_heads), block,
+                       0, st, P, nullptr);
+  return check_launch("gqa_attention_partials");
+}
+
+extern "C" int tt_single_token_gqa_attention_partials(const void* q, const void* keys, const void* values, int dtype,
+                                                      int64_t k_head, int64_t k_tok, int64_t v_head, int64_t v_tok,
+                                                      const int32_t* tokens_dev, int64_t tokens, int64_t max_tokens,
+                                                      int64_t heads, int64_t kv_heads, int64_t head_dim, float* scratch,
+                                                      int64_t scratch_floats, void* stream) {
+  const char* what = "single_token_gqa_attention_partials";
+  TT_REQUIRE(q && keys && values && scratch, "%s: null pointer", what);
+  TT_REQUIRE(heads > 0 && kv_heads > 0 && heads % kv_heads == 0, "%s: heads must be a multiple of kv_heads", what);
+  TT_REQUIRE(tokens_dev != nullptr || (tokens > 0 && tokens <= max_tokens), "%s: attention requires at least one KV token", what);
+  TT_REQUIRE(tokens_dev == nullptr || (tokens >= 0 && tokens <= 1), "%s: device token count offset must be 0 or 1", what);
+  TT_REQUIRE(max_tokens > 0 && kv_heads <= 65535, "%s: bad max_tokens / kv_heads", what);
+  const int64_t chunks = (max_tokens + kChunk - 1) / kChunk;
+  TT_REQUIRE(chunks <= 65535, "%s: sequence too long", what);
+  TT_REQUIRE(scratch_floats >= kAttnCounters + heads * chunks * (2 + head_dim), "%s: scratch too small", what);
+  const int64_t G = heads / kv_heads;
+  TT_UNSUPPORTED(head_dim == 64 && k_tok == 64 && v_tok == 64 && max_tokens % kChunk == 0 && aligned(keys, 16) &&
+                     aligned(values, 16) && k_head % 8 == 0 && v_head % 8 == 0 && (G == 1 || G == 2 || G == 4 || G == 8),
+                 "%s: needs contiguous head_dim-64 caches whose capacity is a multiple of %d tokens and 1, 2, 4 or 8 "
+                 "query heads per KV head", what, kChunk);
+  AttnParams P{};
+  P.q = q; P.keys = keys; P.values = values;
+  P.k_head = k_head; P.k_tok = k_tok; P.v_head = v_head; P.v_tok = v_tok;
+  P.sinks = nullptr; P.tokens_dev = tokens_dev; P.tokens = (int)tokens;
+  scratch += kAttnCounters;
+  P.part_m = scratch;
+  P.part_l = scratch + heads * chunks;
+  P.part_o = scratch + 2 * heads * chunks;
+  P.heads = (int)heads; P.kv_heads = (int)kv_heads; P.head_dim = (int)head_dim; P.max_chunks = (int)chunks;
+  P.max_tokens = (int)max_tokens;
+  P.scale = (float)(1.0 / __builtin_sqrt((double)head_dim));
+  P.out = nullptr;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  auto by_g = [&](auto t) -> int {
+    using T = decltype(t);
+    switch (G) {
+      case 1: return launch_attn_partials<T, 1>(P, st);
+      case 2: return launch_attn_partials<T, 2>(P, st);
+      case 4: return launch_attn_partials<T, 4>(P, st);
+      default: return launch_attn_partials<T, 8>(P, st);
+    }
+  };
+  if (dtype == TT_F16) return by_g(f16_t{});
+  if (dtype == TT_BF16) return by_g(bf16_t{});
+  set_error("%s: KV dtype must be fp16 or bf16", what);
+  return TT_ERR_INVALID;
 }
 
 extern "C" int tt_single_token_gqa_attention(const void* q, const void* keys, const void* values, int dtype,

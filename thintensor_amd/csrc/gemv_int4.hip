@@ -16,12 +16,28 @@ namespace {
 // later rounds are fetched one ahead.  Activation staging XM: 0 = one copy per
 // workgroup in LDS behind a barrier; 1 = each lane reads its chunk from global memory;
 // 2 = each wave stages the whole vector in its own LDS slice with coalesced loads
-// (no workgroup barrier; a wave's LDS accesses complete in order).
+// (no workgroup barrier; a wave's LDS accesses complete in order); 3 = the activation is
+// the combine of single-token attention chunk partials (CombineSrc), built in LDS by the
+// workgroup behind a barrier.
+//
+// Chunk partials of a head_dim-64 attention (the scratch layout of
+// tt_single_token_gqa_attention): per query head h and chunk c, the chunk maximum m,
+// the sum l of exp(s - m) and the 64 weighted sums o.
+struct CombineSrc {
+  const float* pm;
+  const float* pl;
+  const float* po;
+  const int32_t* tokens_dev;   // device token count (null: `tokens` is the count)
+  int tokens, max_tokens, max_chunks;
+  uint16_t* xout;              // optional: workgroup 0 writes the combined activation here
+};
+constexpr int kCombineChunks = 16;   // chunks whose partials are requested with the first weights
+
 template <typename XT, int LPR, int ROWS, int XM, int PFR>
 __global__ __launch_bounds__(256) void int4g128_kernel(const uint8_t* __restrict__ W, uint32_t w_row,
                                                        const f16_t* __restrict__ S, uint32_t s_row, uint32_t s_grp,
                                                        const uint16_t* __restrict__ x, XT* __restrict__ y, int rows,
-                                                       int cols) {
+                                                       int cols, CombineSrc C) {
   constexpr int L = 4;                       // 32-element chunks per group of 128
   constexpr int SUBS = 64 / LPR;
   constexpr int NVG = ROWS / L > 0 ? ROWS / L : 1;
@@ -58,6 +74,40 @@ __global__ __launch_bounds__(256) void int4g128_kernel(const uint8_t* __restrict
       xwidx[k] = idx < xn ? idx : xn - 1;
       xwreg[k] = reinterpret_cast<const uint4*>(x)[xwidx[k]];
     }
+  }
+  // XM 3: thread p builds piece p of the activation (head p / 8, dimensions 8 (p mod 8)
+  // .. +7; the host keeps cols <= 2048).  The partials of the first kCombineChunks chunks
+  // of the scratch (values past the active count are unused) and the token count are
+  // requested before the weights; the activation is rounded to XT.
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  constexpr int kCB = XM == 3 ? kCombineChunks : 1;
+  float cm[kCB], cl[kCB];
+  f32x4 co[kCB][2];
+  int ctok = 0;
+  const int cp = (int)threadIdx.x < xn ? (int)threadIdx.x : xn - 1;
+  const float* cpm = nullptr;
+  const float* cpl = nullptr;
+  const f32x4* cpo = nullptr;
+  if constexpr (XM == 3) {
+    const int h = cp >> 3;
+    cpm = C.pm + (int64_t)h * C.max_chunks;
+    cpl = C.pl + (int64_t)h * C.max_chunks;
+    cpo = reinterpret_cast<const f32x4*>(C.po + (int64_t)h * C.max_chunks * 64 + 8 * (cp & 7));
+    // chunks past the scratch are not requested (a uniform test on a kernel argument:
+    // the loads still go out in one batch); the active count never exceeds the scratch
+#pragma unroll
+    for (int u = 0; u < kCB; u++) {
+      if (u < C.max_chunks) {
+        cm[u] = cpm[u];
+        cl[u] = cpl[u];
+        co[u][0] = cpo[u * 16];
+        co[u][1] = cpo[u * 16 + 1];
+      } else {
+        cm[u] = cl[u] = 0.0f;
+        co[u][0] = co[u][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+    }
+    ctok = C.tokens_dev ? C.tokens_dev[0] + C.tokens : C.tokens;
   }
 
   // weights: row i of lane group `sub` is row0 + i * SUBS + sub (clamped to the last row)
@@ -123,6 +173,44 @@ __global__ __launch_bounds__(256) void int4g128_kernel(const uint8_t* __restrict
 #pragma unroll
     for (int k = 0; k < kXW; k++) xl[xwidx[k]] = xwreg[k];
     for (int idx = lane + 64 * kXW; idx < xn; idx += 64) xl[idx] = reinterpret_cast<const uint4*>(x)[idx];
+  } else if constexpr (XM == 3) {
+    // the combine of single_token_gqa_attention: M = the maximum of the active chunks'
+    // maxima, then in chunk order e = exp(m_c - M), den = fma(l_c, e, den),
+    // acc = fma(o_c, e, acc); the activation is acc / den rounded to fp16
+    const int T_act = min(ctok, C.max_tokens);
+    const int nc = T_act > 0 ? (T_act + 63) / 64 : 0;
+    float M = __builtin_bit_cast(float, 0xff800000u);
+#pragma unroll
+    for (int u = 0; u < kCB; u++)
+      if (u < nc) M = fmaxf(M, cm[u]);
+    for (int c = kCB; c < nc; c++) M = fmaxf(M, cpm[c]);
+    float den = 0.0f;
+    float acc[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) acc[k] = 0.0f;
+    auto fold = [&](float m, float lc, f32x4 o0, f32x4 o1) {
+      const float ec = exp_f32(m - M);
+      den = __builtin_fmaf(lc, ec, den);
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        acc[k] = __builtin_fmaf(o0[k], ec, acc[k]);
+        acc[4 + k] = __builtin_fmaf(o1[k], ec, acc[4 + k]);
+      }
+    };
+#pragma unroll
+    for (int u = 0; u < kCB; u++)
+      if (u < nc) fold(cm[u], cl[u], co[u][0], co[u][1]);
+    for (int c = kCB; c < nc; c++) fold(cpm[c], cpl[c], cpo[c * 16], cpo[c * 16 + 1]);
+    uint32_t pk[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+      pk[k] = bits16<XT>(acc[2 * k] / den) | (bits16<XT>(acc[2 * k + 1] / den) << 16);
+    const uint4 piece{pk[0], pk[1], pk[2], pk[3]};
+    if ((int)threadIdx.x < xn) {
+      reinterpret_cast<uint4*>(xs_lds)[threadIdx.x] = piece;
+      if (C.xout != nullptr && blockIdx.x == 0) reinterpret_cast<uint4*>(C.xout)[threadIdx.x] = piece;
+    }
+    lds_barrier();
   }
 
   float acc[NVG];
@@ -194,7 +282,7 @@ inline int int4g128_x_mode(int64_t rows, int64_t cols, int lpr) { return cols / 
 
 template <typename XT, int LPR>
 int launch_int4g128_lpr(int rpw, const void* W, int64_t w_row, const void* S, int64_t s_row, int64_t s_grp,
-                        const void* x, void* y, int rows, int cols, hipStream_t st) {
+                        const void* x, void* y, int rows, int cols, hipStream_t st, const CombineSrc* combine = nullptr) {
   const int per_wave = rpw * (64 / LPR);
   const int64_t waves = ((int64_t)rows + per_wave - 1) / per_wave;
   const dim3 grid((unsigned)((waves + 3) / 4));
@@ -202,8 +290,9 @@ int launch_int4g128_lpr(int rpw, const void* W, int64_t w_row, const void* S, in
   const auto* s = static_cast<const f16_t*>(S);
   const auto* xv = static_cast<const uint16_t*>(x);
   auto* yv = static_cast<XT*>(y);
-  const int xm = int4g128_x_mode(rows, cols, LPR);
+  const int xm = combine ? 3 : int4g128_x_mode(rows, cols, LPR);
   const size_t lds = xm == 1 ? 0 : (size_t)cols * 2 * (xm == 2 ? 4 : 1);
+  const CombineSrc cmb = combine ? *combine : CombineSrc{};
   const uint32_t wr = (uint32_t)w_row, sr = (uint32_t)s_row, sg = (uint32_t)s_grp;
   const int rounds = (cols / 32 + LPR - 1) / LPR;
   // several rounds per row and few rows per wave: four rounds in flight at a time
@@ -211,13 +300,14 @@ int launch_int4g128_lpr(int rpw, const void* W, int64_t w_row, const void* S, in
   do {                                                                                                        \
     if (rounds > 1 && R <= 2)                                                                                 \
       hipLaunchKernelGGL((int4g128_kernel<XT, LPR, R, M, 4>), grid, dim3(256), lds, st, w, wr, s, sr, sg, xv, yv, \
-                         rows, cols);                                                                         \
+                         rows, cols, cmb);                                                                    \
     else                                                                                                      \
       hipLaunchKernelGGL((int4g128_kernel<XT, LPR, R, M, 1>), grid, dim3(256), lds, st, w, wr, s, sr, sg, xv, yv, \
-                         rows, cols);                                                                         \
+                         rows, cols, cmb);                                                                    \
   } while (0)
-#define TT_INT4G_MODES(R) \
-  if (xm == 1) TT_INT4G_LAUNCH(R, 1); else if (xm == 2) TT_INT4G_LAUNCH(R, 2); else TT_INT4G_LAUNCH(R, 0);
+#define TT_INT4G_MODES(R)                                                                                  \
+  if (xm == 1) TT_INT4G_LAUNCH(R, 1); else if (xm == 2) TT_INT4G_LAUNCH(R, 2); else if (xm == 3) TT_INT4G_LAUNCH(R, 3); \
+  else TT_INT4G_LAUNCH(R, 0);
   if (rpw == 4) { TT_INT4G_MODES(4) }
   else if (rpw == 2) { TT_INT4G_MODES(2) }
   else { TT_INT4G_MODES(1) }
@@ -367,6 +457,51 @@ extern "C" int tt_multi_int4_scaled_matvec(int count, const void* const* packed,
   }
   if (scale_dtype == TT_F16) return launch_types<Fmt::kInt4Sym, SMode::kGroup, f16_t, 4>(x_dtype, out_dtype, Lg, lpr, P, 1, st, what);
   return launch_types<Fmt::kInt4Sym, SMode::kGroup, float, 4>(x_dtype, out_dtype, Lg, lpr, P, 1, st, what);
+}
+
+extern "C" int tt_attention_combine_int4_matvec(const float* scratch, int64_t scratch_floats, const int32_t* tokens_dev,
+                                                int64_t tokens, int64_t max_tokens, int64_t heads, int64_t head_dim,
+                                                int dtype, const void* packed, int64_t w_row_bytes, const void* scales,
+                                                int64_t s_row, int64_t s_group, void* attn_out, void* out, int64_t rows,
+                                                void* stream) {
+  const char* what = "attention_combine_int4_matvec";
+  TT_REQUIRE(scratch && packed && scales && out, "%s: null pointer", what);
+  TT_REQUIRE(dtype == TT_F16 || dtype == TT_BF16, "%s: activation dtype must be fp16 or bf16", what);
+  TT_REQUIRE(tokens_dev != nullptr || (tokens > 0 && tokens <= max_tokens), "%s: attention requires at least one KV token", what);
+  TT_REQUIRE(tokens_dev == nullptr || (tokens >= 0 && tokens <= 1), "%s: device token count offset must be 0 or 1", what);
+  TT_UNSUPPORTED(head_dim == 64 && heads > 0 && heads * head_dim <= 2048,
+                 "%s: combines head_dim-64 attention of at most 32 query heads", what);
+  TT_REQUIRE(max_tokens > 0 && max_tokens % 64 == 0, "%s: capacity must be a whole number of 64-token chunks", what);
+  const int64_t cols = heads * head_dim, chunks = max_tokens / 64;
+  TT_REQUIRE(scratch_floats >= 1024 + heads * chunks * (2 + head_dim), "%s: scratch too small", what);
+  TT_REQUIRE(rows > 0 && packed && aligned(packed, 16) && w_row_bytes % 16 == 0 && w_row_bytes >= cols / 2,
+             "%s: packed weights must be 16-byte aligned with a row stride >= cols/2 that is a multiple of 16", what);
+  TT_REQUIRE(attn_out == nullptr || aligned(attn_out, 16), "%s: attention output must be 16-byte aligned", what);
+  TT_REQUIRE(int4g128_fits(rows, w_row_bytes, s_row, s_group, cols) && s_row >= 0 && s_group >= 0,
+             "%s: operands too large for 32-bit offsets", what);
+  const int lpr = tt_gemv_lanes_per_row(cols / 32, 4);
+  TT_UNSUPPORTED(lpr > 0, "%s: no lane mapping for cols %lld", what, (long long)cols);
+  // the partials follow the 1024 arrival counters of the attention scratch
+  const float* part = scratch + 1024;
+  CombineSrc C{};
+  C.pm = part;
+  C.pl = part + heads * chunks;
+  C.po = part + 2 * heads * chunks;
+  C.tokens_dev = tokens_dev;
+  C.tokens = (int)tokens;
+  C.max_tokens = (int)max_tokens;
+  C.max_chunks = (int)chunks;
+  C.xout = static_cast<uint16_t*>(attn_out);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int rpw = int4g128_rows_per_wave(rows, cols, lpr);
+  auto go = [&](auto t) -> int {
+    using XT = decltype(t);
+    if (lpr == 64) return launch_int4g128_lpr<XT, 64>(rpw, packed, w_row_bytes, scales, s_row, s_group, nullptr, out, (int)rows, (int)cols, st, &C);
+    if (lpr == 32) return launch_int4g128_lpr<XT, 32>(rpw, packed, w_row_bytes, scales, s_row, s_group, nullptr, out, (int)rows, (int)cols, st, &C);
+    return launch_int4g128_lpr<XT, 16>(rpw, packed, w_row_bytes, scales, s_row, s_group, nullptr, out, (int)rows, (int)cols, st, &C);
+  };
+  if (dtype == TT_F16) return go(f16_t{});
+  return go(bf16_t{});
 }
 
 extern "C" int tt_int4_selected_matvec(const void* packed, int64_t w_expert_bytes, int64_t w_row_bytes,

@@ -251,12 +251,21 @@ class DenseDecoder(_GraphedDecoder):
         if not hasattr(self, "_head_desc"):
             self._build_fused()
         q = self.qkv[: s.q_dim]
+        # the o_proj GEMV combines the attention chunk partials itself (head_dim-64 caches
+        # of whole 64-token chunks, at most 32 query heads, 1/2/4/8 per KV head)
+        combine = (s.head_dim == 64 and s.heads <= 32 and s.group == 128 and s.heads // s.kv_heads in (1, 2, 4, 8)
+                   and int(w.k_cache[0].shape[1]) % 64 == 0 and w.k_cache[0].stride(1) == 64
+                   and w.v_cache[0].stride(1) == 64)
         for li, L in enumerate(w.layers):
             be.fused_gemv(self._qkv_desc[li])
-            be.single_token_gqa_attention(q, w.k_cache[li], w.v_cache[li], self.attn, s.heads, s.kv_heads, s.head_dim,
-                                          active_tokens=(self.position, 1))
-            be.int4_scaled_matvec(L.o[0], L.o[1], self.attn, self.attn_out, rows=s.hidden, cols=s.q_dim,
-                                  group_size=s.group)
+            if combine:
+                be.attention_then_int4_matvec(q, w.k_cache[li], w.v_cache[li], s.heads, s.kv_heads, s.head_dim,
+                                              L.o[0], L.o[1], self.attn_out, active_tokens=(self.position, 1))
+            else:
+                be.single_token_gqa_attention(q, w.k_cache[li], w.v_cache[li], self.attn, s.heads, s.kv_heads,
+                                              s.head_dim, active_tokens=(self.position, 1))
+                be.int4_scaled_matvec(L.o[0], L.o[1], self.attn, self.attn_out, rows=s.hidden, cols=s.q_dim,
+                                      group_size=s.group)
             be.fused_gemv(self._gu_desc[li])
             be.int4_scaled_matvec(L.down[0], L.down[1], self.act, self.mlp, rows=s.hidden, cols=s.intermediate,
                                   group_size=s.group)
