@@ -1175,6 +1175,8 @@ class HipDecodeBackend:
             raise ValueError(f"int4 packed weight {tuple(packed_weight.shape)} does not match rows={rows} cols={cols}")
         if scales.dtype != torch.float16 or tuple(scales.shape) != (rows, cols // 128):
             raise ValueError("o_proj scales must be fp16 [rows, cols / 128]")
+        if packed_weight.stride(1) != 1 or not out.is_contiguous() or not query.is_contiguous():
+            raise ValueError("o_proj weight rows, query and out must be contiguous")
         scratch = self._attention_scratch(heads, capacity, head_dim)
         if isinstance(tokens, torch.Tensor):
             if tokens.dtype != torch.int32:

@@ -809,10 +809,6 @@ static int launch_attn(const AttnParams& P, int sink_dtype, bool contiguous64, i
 
 using namespace tt;
 
-// Scratch: kAttnCounters arrival counters of the single-launch path (one per KV head,
-// at fixed offsets whatever the shape, left at zero by every call), then the chunk
-// partials (m, l, o) per query head.
-constexpr int kAttnCounters = 1024;
 
 extern "C" int tt_attention_scratch_floats(int64_t heads, int64_t max_tokens, int64_t head_dim) {
   const int64_t chunks = (max_tokens + kChunk - 1) / kChunk;

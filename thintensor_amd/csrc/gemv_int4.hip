@@ -473,7 +473,7 @@ extern "C" int tt_attention_combine_int4_matvec(const float* scratch, int64_t sc
                  "%s: combines head_dim-64 attention of at most 32 query heads", what);
   TT_REQUIRE(max_tokens > 0 && max_tokens % 64 == 0, "%s: capacity must be a whole number of 64-token chunks", what);
   const int64_t cols = heads * head_dim, chunks = max_tokens / 64;
-  TT_REQUIRE(scratch_floats >= 1024 + heads * chunks * (2 + head_dim), "%s: scratch too small", what);
+  TT_REQUIRE(scratch_floats >= kAttnCounters + heads * chunks * (2 + head_dim), "%s: scratch too small", what);
   TT_REQUIRE(rows > 0 && packed && aligned(packed, 16) && w_row_bytes % 16 == 0 && w_row_bytes >= cols / 2,
              "%s: packed weights must be 16-byte aligned with a row stride >= cols/2 that is a multiple of 16", what);
   TT_REQUIRE(attn_out == nullptr || aligned(attn_out, 16), "%s: attention output must be 16-byte aligned", what);
@@ -481,8 +481,8 @@ extern "C" int tt_attention_combine_int4_matvec(const float* scratch, int64_t sc
              "%s: operands too large for 32-bit offsets", what);
   const int lpr = tt_gemv_lanes_per_row(cols / 32, 4);
   TT_UNSUPPORTED(lpr > 0, "%s: no lane mapping for cols %lld", what, (long long)cols);
-  // the partials follow the 1024 arrival counters of the attention scratch
-  const float* part = scratch + 1024;
+  // the partials follow the arrival counters of the attention scratch
+  const float* part = scratch + kAttnCounters;
   CombineSrc C{};
   C.pm = part;
   C.pl = part + heads * chunks;

@@ -49,4 +49,9 @@ int dense_bias_rows_f16(const void* weight, int64_t w_row, const void* bias, con
 inline bool valid_act_dtype(int d) { return d == TT_F16 || d == TT_BF16; }
 inline bool valid_out_dtype(int d) { return d == TT_F16 || d == TT_BF16 || d == TT_F32; }
 
+// Attention scratch: kAttnCounters arrival counters of the single-launch path (one per
+// KV head, at fixed offsets whatever the shape, left at zero by every call), then the
+// chunk partials (m, l, o) per query head.
+constexpr int kAttnCounters = 1024;
+
 }  // namespace tt
