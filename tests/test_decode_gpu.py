@@ -139,6 +139,23 @@ def test_llama_1b_baseline_init_tokens(device):
     assert np.array_equal(_final_logits(dec).view(np.uint16), ref.last_logits.view(np.uint16))
 
 
+@pytest.mark.parametrize("graph", [True, False])
+def test_small_dense_combined_o_proj(device, graph):
+    """A capacity of whole 64-token chunks sends the fused step through the o_proj that
+    combines the attention partials itself; 64 tokens from 100 prior ones cross two chunk
+    boundaries.  Tokens and the last logits equal the oracle's bit for bit."""
+    s = SMALL_DENSE
+    w = make_dense(s, device=device, seed=3, capacity=192)
+    ref = DenseRef(w)
+    dec = DenseDecoder(_backend(device, s), w, fused=True)
+    start, pos = 11, s.prior_tokens
+    got = dec.generate(start, pos, s.max_new_tokens, use_graph=graph)
+    want = ref.generate(start, pos, s.max_new_tokens)
+    assert got == want
+    _, logits = ref.step(want[-2], pos + s.max_new_tokens - 1)
+    assert np.array_equal(_final_logits(dec).view(np.uint16), logits.view(np.uint16))
+
+
 @pytest.fixture(scope="module")
 def gptoss_case(device):
     s = GPT_OSS_20B
