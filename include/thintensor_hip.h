@@ -12,6 +12,9 @@
  *   - pointers are device pointers; sizes and strides are element counts unless the
  *     name ends in `_bytes`;
  *   - dtype codes: TT_F16, TT_BF16 (activations), TT_F32 (outputs / scales);
+ *   - expert_indices arrays of the selected-expert operators hold int32 or int64
+ *     ids (index_bytes 4 or 8), as the reference's kernels load whichever integer
+ *     tensor the runtime passes (triton_kernels.py:439, 886, 956, 1157, 1240);
  *   - return value: TT_OK, or a negative code with a message in tt_last_error().
  *
  * Numerics: binary32 accumulation with a fixed, documented reduction order (see
@@ -100,7 +103,7 @@ int tt_multi_matvec(int count, const void* const* weights, int w_dtype, const in
 int tt_mxfp4_selected_matvec(const void* blocks, int64_t b_expert_bytes, int64_t b_row_bytes,
                              const void* scales, int64_t s_expert, int64_t s_row,
                              const void* x, int x_dtype, int64_t x_slot,
-                             const int32_t* expert_indices, int64_t selected,
+                             const void* expert_indices, int index_bytes, int64_t selected,
                              void* out, int out_dtype, int64_t out_slot,
                              int64_t rows, int64_t cols, void* stream);
 
@@ -112,7 +115,7 @@ int tt_mxfp4_selected_matvec(const void* blocks, int64_t b_expert_bytes, int64_t
 int tt_mxfp_lowbit_selected_matvec(const void* packed, int64_t w_expert_bytes, int64_t w_row_bytes,
                                    const void* scales, int64_t s_expert, int64_t s_row, int bits,
                                    const void* x, int x_dtype, int64_t x_slot,
-                                   const int32_t* expert_indices, int64_t selected,
+                                   const void* expert_indices, int index_bytes, int64_t selected,
                                    void* out, int out_dtype, int64_t out_slot,
                                    int64_t rows, int64_t cols, void* stream);
 
@@ -131,7 +134,7 @@ int tt_mxfp_ternary_selected_matvec(const void* packed, int64_t w_expert_bytes, 
                                     int64_t w_total_bytes, const void* scales, int64_t s_expert,
                                     int64_t s_row, int64_t s_total_bytes, int64_t experts,
                                     const void* x, int x_dtype, int64_t x_slot,
-                                    const int32_t* expert_indices, int64_t selected,
+                                    const void* expert_indices, int index_bytes, int64_t selected,
                                     void* out, int out_dtype, int64_t out_slot,
                                     int64_t rows, int64_t cols, void* stream);
 
@@ -168,7 +171,7 @@ int tt_binary_residual_matvec(const void* packed_signs, int64_t bm, const void* 
 int tt_mxfp_lowbit_selected_swiglu(const void* packed, int64_t w_expert_bytes, int64_t w_row_bytes,
                                    const void* scales, int64_t s_expert, int64_t s_row, int bits,
                                    const void* x, int x_dtype, int64_t x_slot,
-                                   const int32_t* expert_indices, int64_t selected,
+                                   const void* expert_indices, int index_bytes, int64_t selected,
                                    const void* bias, int bias_dtype, int64_t bias_expert,
                                    float alpha, float limit,
                                    void* out, int out_dtype, int64_t out_slot,
@@ -180,7 +183,7 @@ int tt_mxfp_lowbit_selected_swiglu(const void* packed, int64_t w_expert_bytes, i
 int tt_mxfp_lowbit_weighted_down(const void* packed, int64_t w_expert_bytes, int64_t w_row_bytes,
                                  const void* scales, int64_t s_expert, int64_t s_row, int bits,
                                  const void* x, int x_dtype, int64_t x_slot,
-                                 const int32_t* expert_indices, const void* router_scores,
+                                 const void* expert_indices, int index_bytes, const void* router_scores,
                                  int score_dtype, int64_t selected,
                                  const void* bias, int bias_dtype, int64_t bias_expert,
                                  void* out, int out_dtype, int64_t rows, int64_t cols, void* stream);
@@ -201,7 +204,7 @@ int tt_matvec_bias_rows(const void* weight, int w_dtype, int64_t w_row, const vo
 int tt_mxfp_lowbit_selected_swiglu_tokens(const void* packed, int64_t w_expert_bytes, int64_t w_row_bytes,
                                           const void* scales, int64_t s_expert, int64_t s_row, int bits,
                                           const void* x, int x_dtype, int64_t x_token,
-                                          const int32_t* expert_indices, int64_t selected,
+                                          const void* expert_indices, int index_bytes, int64_t selected,
                                           const void* bias, int bias_dtype, int64_t bias_expert,
                                           float alpha, float limit, void* out, int out_dtype,
                                           int64_t out_slot, int64_t activation_rows, int64_t cols,
@@ -214,7 +217,7 @@ int tt_mxfp_lowbit_selected_swiglu_tokens(const void* packed, int64_t w_expert_b
 int tt_mxfp_lowbit_weighted_down_tokens(const void* packed, int64_t w_expert_bytes, int64_t w_row_bytes,
                                         const void* scales, int64_t s_expert, int64_t s_row, int bits,
                                         const void* x, int x_dtype, int64_t x_slot,
-                                        const int32_t* expert_indices, const void* router_scores,
+                                        const void* expert_indices, int index_bytes, const void* router_scores,
                                         int score_dtype, int64_t selected, const void* bias, int bias_dtype,
                                         int64_t bias_expert, void* out, int out_dtype, int64_t out_token,
                                         int64_t rows, int64_t cols, int64_t tokens, void* stream);
@@ -235,7 +238,7 @@ int tt_lowbit_affine_matvec(const void* packed, int64_t w_row_bytes, const void*
 int tt_int4_selected_matvec(const void* packed, int64_t w_expert_bytes, int64_t w_row_bytes,
                             const void* scales, int scale_dtype, int64_t s_expert, int64_t s_row,
                             int64_t s_group, const void* x, int x_dtype, int64_t x_slot,
-                            const int32_t* expert_indices, int64_t selected,
+                            const void* expert_indices, int index_bytes, int64_t selected,
                             void* out, int out_dtype, int64_t out_slot,
                             int64_t rows, int64_t cols, int64_t group_size, void* stream);
 
@@ -467,7 +470,10 @@ int tt_add_rms_norm_router_topk(const void* left, const void* right, void* resid
                                 int32_t* indices_out, void* scores_out, int score_dtype, int64_t tokens,
                                 void* workspace, int64_t workspace_bytes, void* stream);
 
-/* Top-k + softmax on given logits.  Replaces TritonDecodeBackend.moe_router_topk
+/* Top-k + softmax on given logits, any expert count up to 65536 (one wave up to 128
+ * experts, one workgroup above; above 128 experts top_k is at most 4096).  The
+ * runtime calls it exactly when the router has more than 128 rows
+ * (gpu_runtime.py:9474-9496).  Replaces TritonDecodeBackend.moe_router_topk
  * (triton_kernels.py:5803-5824; kernel :2821-2851). */
 int tt_moe_router_topk(const void* logits, int logits_dtype, int64_t experts, int64_t top_k, int renormalize,
                        int32_t* indices_out, void* scores_out, int score_dtype, void* stream);

@@ -597,7 +597,7 @@ int tto_attention(const void* q, const void* keys, const void* values, int dt, i
 static void topk_softmax(const float* lg, int E, int k, int renorm, int32_t* idx, float* score) {
   float maximum = -INFINITY;
   for (int e = 0; e < E; e++) maximum = fmaxf(maximum, lg[e]);
-  char taken[1024] = {0};
+  char* taken = (char*)calloc((size_t)E, 1);
   for (int s = 0; s < k; s++) {
     int bi = -1;
     float bv = 0.0f;
@@ -609,6 +609,7 @@ static void topk_softmax(const float* lg, int E, int k, int renorm, int32_t* idx
     idx[s] = bi;
     score[s] = bv;
   }
+  free(taken);
   float den = 0.0f;
   if (renorm) for (int s = 0; s < k; s++) den = den + tto_exp_f32(score[s] - maximum);
   else for (int e = 0; e < E; e++) den = den + tto_exp_f32(lg[e] - maximum);
@@ -634,10 +635,13 @@ int tto_router(const void* w, int wdt, int64_t w_row, const void* x, int xdt, in
 }
 
 int tto_topk(const void* logits, int ldt, int E, int k, int renorm, int32_t* idx, void* scores, int odt) {
-  float lg[1024], sc[1024];
+  float* lg = (float*)malloc(sizeof(float) * (size_t)E);
+  float* sc = (float*)malloc(sizeof(float) * (size_t)k);
   for (int e = 0; e < E; e++) lg[e] = act_get(logits, ldt, e);
   topk_softmax(lg, E, k, renorm, idx, sc);
   for (int s = 0; s < k; s++) act_put(scores, odt, s, sc[s]);
+  free(lg);
+  free(sc);
   return 0;
 }
 

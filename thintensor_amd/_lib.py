@@ -88,17 +88,18 @@ SIGNATURES: dict[str, list] = {
     "tt_qk_head_rmsnorm_rope_inplace": [_P, _P, _I, _P, _P, _I, _P, _P, _L, _L, _P, _L, _L, _L, _L, _F, _P],
     "tt_matvec": [_P, _I, _L, _P, _I, _P, _I, _L, _L, _P],
     "tt_multi_matvec": [_I, _PP, _I, _LP, _LP, _P, _I, _P, _I, _L, _P],
-    "tt_mxfp4_selected_matvec": [_P, _L, _L, _P, _L, _L, _P, _I, _L, _P, _L, _P, _I, _L, _L, _L, _P],
-    "tt_mxfp_lowbit_selected_matvec": [_P, _L, _L, _P, _L, _L, _I, _P, _I, _L, _P, _L, _P, _I, _L, _L, _L, _P],
+    "tt_mxfp4_selected_matvec": [_P, _L, _L, _P, _L, _L, _P, _I, _L, _P, _I, _L, _P, _I, _L, _L, _L, _P],
+    "tt_mxfp_lowbit_selected_matvec": [_P, _L, _L, _P, _L, _L, _I, _P, _I, _L, _P, _I, _L, _P, _I, _L, _L, _L, _P],
     "tt_sparse_residual_matvec": [_P, _I, _L, _L, _P, _I, _L, _L, _P, _I, _P, _I, _L, _L, _L, _P],
     "tt_binary_residual_matvec": [_P, _L, _P, _I, _L, _P, _I, _P, _I, _L, _L, _P],
-    "tt_mxfp_ternary_selected_matvec": [_P, _L, _L, _L, _P, _L, _L, _L, _L, _P, _I, _L, _P, _L, _P, _I, _L, _L, _L, _P],
-    "tt_mxfp_lowbit_selected_swiglu": [_P, _L, _L, _P, _L, _L, _I, _P, _I, _L, _P, _L, _P, _I, _L, _F, _F, _P, _I,
-                                       _L, _L, _L, _P],
-    "tt_mxfp_lowbit_weighted_down": [_P, _L, _L, _P, _L, _L, _I, _P, _I, _L, _P, _P, _I, _L, _P, _I, _L, _P, _I, _L,
-                                     _L, _P],
+    "tt_mxfp_ternary_selected_matvec": [_P, _L, _L, _L, _P, _L, _L, _L, _L, _P, _I, _L, _P, _I, _L, _P, _I, _L, _L,
+                                        _L, _P],
+    "tt_mxfp_lowbit_selected_swiglu": [_P, _L, _L, _P, _L, _L, _I, _P, _I, _L, _P, _I, _L, _P, _I, _L, _F, _F, _P,
+                                       _I, _L, _L, _L, _P],
+    "tt_mxfp_lowbit_weighted_down": [_P, _L, _L, _P, _L, _L, _I, _P, _I, _L, _P, _I, _P, _I, _L, _P, _I, _L, _P, _I,
+                                     _L, _L, _P],
     "tt_lowbit_affine_matvec": [_P, _L, _P, _L, _L, _I, _P, _I, _P, _I, _L, _L, _L, _P],
-    "tt_int4_selected_matvec": [_P, _L, _L, _P, _I, _L, _L, _L, _P, _I, _L, _P, _L, _P, _I, _L, _L, _L, _L, _P],
+    "tt_int4_selected_matvec": [_P, _L, _L, _P, _I, _L, _L, _L, _P, _I, _L, _P, _I, _L, _P, _I, _L, _L, _L, _L, _P],
     "tt_multi_matvec_bias": [_I, _PP, _I, _LP, _LP, _PP, _P, _I, _P, _I, _L, _P],
     "tt_record_token": [_P, _P, _P, _P, ctypes.c_int32, _P],
     "tt_record_tokens_advance": [_P, ctypes.c_int32, _P, _P, _P, _L, ctypes.c_int32, ctypes.c_int32, _P],
@@ -127,10 +128,10 @@ SIGNATURES: dict[str, list] = {
                                     _I, _L, _P, _L, _P],
     "tt_norm_router_workspace_bytes": [_L],
     "tt_matvec_bias_rows": [_P, _I, _L, _P, _P, _I, _L, _P, _I, _L, _L, _L, _L, _P],
-    "tt_mxfp_lowbit_selected_swiglu_tokens": [_P, _L, _L, _P, _L, _L, _I, _P, _I, _L, _P, _L, _P, _I, _L, _F, _F, _P,
-                                              _I, _L, _L, _L, _L, _P],
-    "tt_mxfp_lowbit_weighted_down_tokens": [_P, _L, _L, _P, _L, _L, _I, _P, _I, _L, _P, _P, _I, _L, _P, _I, _L, _P, _I,
-                                            _L, _L, _L, _L, _P],
+    "tt_mxfp_lowbit_selected_swiglu_tokens": [_P, _L, _L, _P, _L, _L, _I, _P, _I, _L, _P, _I, _L, _P, _I, _L, _F, _F,
+                                              _P, _I, _L, _L, _L, _L, _P],
+    "tt_mxfp_lowbit_weighted_down_tokens": [_P, _L, _L, _P, _L, _L, _I, _P, _I, _L, _P, _I, _P, _I, _L, _P, _I, _L,
+                                            _P, _I, _L, _L, _L, _L, _P],
     "tt_batched_workspace_floats": [_L, _L, _L],
     "tt_int4_batched_matvec": [_P, _L, _P, _L, _P, _L, _P, _L, _L, _L, _L, _L, _P, _L, _P],
     "tt_scaled_batched_matvec": [_P, _L, _P, _P, _L, _P, _L, _L, _L, _L, _P, _L, _P],

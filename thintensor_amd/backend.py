@@ -269,12 +269,12 @@ class HipDecodeBackend:
         stride_xe = self._selected_x_stride(x, selected, cols, "selected INT4")
         if tuple(out.shape) != (selected, rows):
             raise ValueError(f"selected INT4 output must be {(selected, rows)}, got {tuple(out.shape)}")
-        self._check_indices(expert_indices)
+        index_bytes = self._check_indices(expert_indices)
         _require_cuda(packed_weight, scales, x, out)
         rc = self.lib.tt_int4_selected_matvec(
             packed_weight.data_ptr(), packed_weight.stride(0), packed_weight.stride(1), scales.data_ptr(),
             _code(scales, "int4 scales"), scales.stride(0), scales.stride(1), scales.stride(2), x.data_ptr(),
-            _code(x, "int4_selected_matvec"), stride_xe, expert_indices.data_ptr(), selected, out.data_ptr(),
+            _code(x, "int4_selected_matvec"), stride_xe, expert_indices.data_ptr(), index_bytes, selected, out.data_ptr(),
             _code(out, "int4_selected_matvec"), out.stride(0), rows, cols, group_size, _stream(out),
         )
         _lib.check(rc, "int4_selected_matvec")
@@ -460,9 +460,21 @@ class HipDecodeBackend:
         raise ValueError(f"{what} input must be {(cols,)} or {(selected, cols)}, got {tuple(x.shape)}")
 
     @staticmethod
-    def _check_indices(expert_indices: torch.Tensor) -> None:
-        if expert_indices.dtype != torch.int32 or not expert_indices.is_contiguous():
-            raise ValueError("expert_indices must be a contiguous int32 device tensor")
+    def _check_indices(expert_indices: torch.Tensor) -> int:
+        """Byte width of a selected-expert index tensor.  The reference's kernels load
+        the ids in whatever integer type they are given (triton_kernels.py:439, 886, 956,
+        1157, 1240); the runtime passes int32 router output and, for dense low-bit
+        pages, a torch.long id (gpu_runtime.py:12069-12072).  Both are read as is."""
+        if expert_indices.dtype not in (torch.int32, torch.int64) or not expert_indices.is_contiguous():
+            raise ValueError("expert_indices must be a contiguous int32 or int64 device tensor")
+        return expert_indices.element_size()
+
+    @staticmethod
+    def _check_router_indices(indices_out: torch.Tensor) -> None:
+        # the router writes int32 ids, the dtype of the runtime's router buffer
+        # (gpu_runtime.py:5605-5607)
+        if indices_out.dtype != torch.int32 or not indices_out.is_contiguous():
+            raise ValueError("router indices_out must be a contiguous int32 device tensor")
 
     def mxfp4_selected_matvec(
         self,
@@ -488,11 +500,11 @@ class HipDecodeBackend:
             raise ValueError(f"MXFP4 output must be {(selected, rows)}, got {tuple(out.shape)}")
         if blocks.stride(3) != 1 or blocks.stride(2) != blocks.shape[3] or scales.stride(2) != 1:
             raise ValueError("MXFP4 blocks/scales must be contiguous within a row")
-        self._check_indices(expert_indices)
+        index_bytes = self._check_indices(expert_indices)
         _require_cuda(blocks, scales, x, out)
         rc = self.lib.tt_mxfp4_selected_matvec(
             blocks.data_ptr(), blocks.stride(0), blocks.stride(1), scales.data_ptr(), scales.stride(0),
-            scales.stride(1), x.data_ptr(), _code(x, "mxfp4_selected_matvec"), stride_xe, expert_indices.data_ptr(),
+            scales.stride(1), x.data_ptr(), _code(x, "mxfp4_selected_matvec"), stride_xe, expert_indices.data_ptr(), index_bytes,
             selected, out.data_ptr(), _code(out, "mxfp4_selected_matvec"), out.stride(0), rows, cols, _stream(out),
         )
         _lib.check(rc, "mxfp4_selected_matvec")
@@ -539,12 +551,12 @@ class HipDecodeBackend:
         stride_xe = self._selected_x_stride(x, selected, cols, "low-bit expert")
         if tuple(out.shape) != (selected, rows):
             raise ValueError(f"low-bit output must be {(selected, rows)}, got {tuple(out.shape)}")
-        self._check_indices(expert_indices)
+        index_bytes = self._check_indices(expert_indices)
         _require_cuda(packed_weight, scales, x, out)
         rc = self.lib.tt_mxfp_lowbit_selected_matvec(
             packed_weight.data_ptr(), packed_weight.stride(0), packed_weight.stride(1), scales.data_ptr(),
             scales.stride(0), scales.stride(1), bits, x.data_ptr(), _code(x, "mxfp_lowbit_selected_matvec"), stride_xe,
-            expert_indices.data_ptr(), selected, out.data_ptr(), _code(out, "mxfp_lowbit_selected_matvec"),
+            expert_indices.data_ptr(), index_bytes, selected, out.data_ptr(), _code(out, "mxfp_lowbit_selected_matvec"),
             out.stride(0), rows, cols, _stream(out),
         )
         _lib.check(rc, "mxfp_lowbit_selected_matvec")
@@ -657,12 +669,12 @@ class HipDecodeBackend:
             raise ValueError("ternary weights and scales must be uint8")
         if not packed_weight.is_contiguous() or not scales.is_contiguous() or out.stride(1) != 1:
             raise ValueError("ternary weights, scales and output rows must be contiguous")
-        self._check_indices(expert_indices)
+        index_bytes = self._check_indices(expert_indices)
         _require_cuda(packed_weight, scales, x, out)
         rc = self.lib.tt_mxfp_ternary_selected_matvec(
             packed_weight.data_ptr(), packed_weight.stride(0), packed_weight.stride(1), packed_weight.numel(),
             scales.data_ptr(), scales.stride(0), scales.stride(1), scales.numel(), experts, x.data_ptr(),
-            _code(x, "mxfp_ternary_selected_matvec"), stride_xe, expert_indices.data_ptr(), selected,
+            _code(x, "mxfp_ternary_selected_matvec"), stride_xe, expert_indices.data_ptr(), index_bytes, selected,
             out.data_ptr(), _code(out, "mxfp_ternary_selected_matvec"), out.stride(0), rows, cols, _stream(out),
         )
         _lib.check(rc, "mxfp_ternary_selected_matvec")
@@ -701,12 +713,12 @@ class HipDecodeBackend:
         if tuple(out.shape) != (selected, activation_rows):
             raise ValueError("fused SwiGLU output shape mismatch")
         stride_xe = self._selected_x_stride(x, selected, cols, "fused SwiGLU")
-        self._check_indices(expert_indices)
+        index_bytes = self._check_indices(expert_indices)
         _require_cuda(packed_weight, scales, x, out)
         rc = self.lib.tt_mxfp_lowbit_selected_swiglu(
             packed_weight.data_ptr(), packed_weight.stride(0), packed_weight.stride(1), scales.data_ptr(),
             scales.stride(0), scales.stride(1), bits, x.data_ptr(), _code(x, "swiglu"), stride_xe,
-            expert_indices.data_ptr(), selected, bias.data_ptr() if bias is not None else None,
+            expert_indices.data_ptr(), index_bytes, selected, bias.data_ptr() if bias is not None else None,
             _code(bias, "bias") if bias is not None else _lib.F32, bias.stride(0) if bias is not None else 0,
             float(alpha), float(limit), out.data_ptr(), _code(out, "swiglu"), out.stride(0), activation_rows, cols,
             _stream(out),
@@ -737,12 +749,12 @@ class HipDecodeBackend:
         selected = int(expert_indices.numel())
         if tuple(x.shape) != (selected, cols) or int(out.numel()) != rows:
             raise ValueError("fused weighted-down tensor shape mismatch")
-        self._check_indices(expert_indices)
+        index_bytes = self._check_indices(expert_indices)
         _require_cuda(packed_weight, scales, x, out, router_scores)
         rc = self.lib.tt_mxfp_lowbit_weighted_down(
             packed_weight.data_ptr(), packed_weight.stride(0), packed_weight.stride(1), scales.data_ptr(),
             scales.stride(0), scales.stride(1), bits, x.data_ptr(), _code(x, "weighted_down"), x.stride(0),
-            expert_indices.data_ptr(), router_scores.data_ptr(), _code(router_scores, "router scores"), selected,
+            expert_indices.data_ptr(), index_bytes, router_scores.data_ptr(), _code(router_scores, "router scores"), selected,
             bias.data_ptr() if bias is not None else None, _code(bias, "bias") if bias is not None else _lib.F32,
             bias.stride(0) if bias is not None else 0, out.data_ptr(), _code(out, "weighted_down"), rows, cols,
             _stream(out),
@@ -786,12 +798,12 @@ class HipDecodeBackend:
         tokens, selected = map(int, expert_indices.shape)
         if int(x.shape[1]) != cols or x.stride(1) != 1 or tuple(out.shape) != (tokens * selected, activation_rows):
             raise ValueError("batched SwiGLU shape mismatch")
-        self._check_indices(expert_indices)
+        index_bytes = self._check_indices(expert_indices)
         _require_cuda(packed_weight, scales, x, out)
         rc = self.lib.tt_mxfp_lowbit_selected_swiglu_tokens(
             packed_weight.data_ptr(), packed_weight.stride(0), packed_weight.stride(1), scales.data_ptr(),
             scales.stride(0), scales.stride(1), bits, x.data_ptr(), _code(x, "swiglu"), x.stride(0),
-            expert_indices.data_ptr(), selected, bias.data_ptr() if bias is not None else None,
+            expert_indices.data_ptr(), index_bytes, selected, bias.data_ptr() if bias is not None else None,
             _code(bias, "bias") if bias is not None else _lib.F32, bias.stride(0) if bias is not None else 0,
             float(alpha), float(limit), out.data_ptr(), _code(out, "swiglu"), out.stride(0), activation_rows, cols,
             tokens, _stream(out),
@@ -834,12 +846,12 @@ class HipDecodeBackend:
             raise ValueError("batched weighted-down shape mismatch")
         if not router_scores.is_contiguous() or out.stride(1) != 1:
             raise ValueError("batched weighted-down needs contiguous scores and output rows")
-        self._check_indices(expert_indices)
+        index_bytes = self._check_indices(expert_indices)
         _require_cuda(packed_weight, scales, x, out, router_scores)
         rc = self.lib.tt_mxfp_lowbit_weighted_down_tokens(
             packed_weight.data_ptr(), packed_weight.stride(0), packed_weight.stride(1), scales.data_ptr(),
             scales.stride(0), scales.stride(1), bits, x.data_ptr(), _code(x, "weighted_down"), x.stride(0),
-            expert_indices.data_ptr(), router_scores.data_ptr(), _code(router_scores, "router scores"), selected,
+            expert_indices.data_ptr(), index_bytes, router_scores.data_ptr(), _code(router_scores, "router scores"), selected,
             bias.data_ptr() if bias is not None else None, _code(bias, "bias") if bias is not None else _lib.F32,
             bias.stride(0) if bias is not None else 0, out.data_ptr(), _code(out, "weighted_down"), out.stride(0),
             rows, cols, tokens, _stream(out),
@@ -1100,6 +1112,30 @@ class HipDecodeBackend:
             self._attention_partials = torch.zeros(need, device=self.device, dtype=torch.float32)
         return self._attention_partials
 
+    @staticmethod
+    def _check_attention_operands(query, keys, values, out, heads: int, kv_heads: int, head_dim: int,
+                                  out_values: int) -> None:
+        """Operand checks of the attention kernels, which read the query in the cache
+        dtype and write their output in it: the reference leaves these to Triton's
+        pointer arithmetic, here a short query or KV tensor would be read past its end,
+        so the shapes are checked before anything is launched."""
+        if keys.ndim != 3 or values.ndim != 3:
+            raise ValueError("keys and values must be [kv_heads, capacity, head_dim]")
+        if query.dtype != keys.dtype or values.dtype != keys.dtype or out.dtype != keys.dtype:
+            raise ValueError("query, keys, values and out must share the cache dtype")
+        if not query.is_contiguous() or int(query.numel()) != heads * head_dim:
+            raise ValueError(f"query must be a contiguous tensor of heads * head_dim = {heads * head_dim} values")
+        if int(keys.shape[0]) < kv_heads or int(values.shape[0]) < kv_heads:
+            raise ValueError(f"keys and values must hold {kv_heads} KV heads")
+        if int(values.shape[1]) != int(keys.shape[1]):
+            raise ValueError("keys and values must have the same capacity")
+        if int(keys.shape[2]) < head_dim or int(values.shape[2]) < head_dim:
+            raise ValueError(f"keys and values must hold head_dim = {head_dim} values per token")
+        if keys.stride(2) != 1 or values.stride(2) != 1:
+            raise ValueError("keys and values must be contiguous along head_dim")
+        if not out.is_contiguous() or int(out.numel()) < out_values:
+            raise ValueError(f"out must be a contiguous tensor of at least {out_values} values")
+
     def single_token_gqa_attention(
         self,
         query: torch.Tensor,
@@ -1126,6 +1162,7 @@ class HipDecodeBackend:
         if head_dim > 256:
             raise ValueError("fused single-token attention supports head_dim <= 256")
         _require_cuda(query, keys, values, out)
+        self._check_attention_operands(query, keys, values, out, heads, kv_heads, head_dim, heads * head_dim)
         scratch = self._attention_scratch(heads, capacity, head_dim)
         if isinstance(tokens, torch.Tensor):
             if tokens.dtype != torch.int32:
@@ -1177,6 +1214,11 @@ class HipDecodeBackend:
             raise ValueError("o_proj scales must be fp16 [rows, cols / 128]")
         if packed_weight.stride(1) != 1 or not out.is_contiguous() or not query.is_contiguous():
             raise ValueError("o_proj weight rows, query and out must be contiguous")
+        self._check_attention_operands(query, keys, values, out, heads, kv_heads, head_dim, rows)
+        if attn_out is not None:
+            _require_cuda(attn_out)
+            if attn_out.dtype != keys.dtype or attn_out.numel() != cols or not attn_out.is_contiguous():
+                raise ValueError("attn_out must hold heads * head_dim values of the cache dtype")
         scratch = self._attention_scratch(heads, capacity, head_dim)
         if isinstance(tokens, torch.Tensor):
             if tokens.dtype != torch.int32:
@@ -1191,10 +1233,6 @@ class HipDecodeBackend:
             scratch.data_ptr(), scratch.numel(), _stream(out),
         )
         _lib.check(rc, "single_token_gqa_attention_partials")
-        if attn_out is not None:
-            _require_cuda(attn_out)
-            if attn_out.dtype != keys.dtype or attn_out.numel() != cols:
-                raise ValueError("attn_out must hold heads * head_dim values of the cache dtype")
         rc = self.lib.tt_attention_combine_int4_matvec(
             scratch.data_ptr(), scratch.numel(), tok_dev, tok, capacity, heads, head_dim, code,
             packed_weight.data_ptr(), packed_weight.stride(0) * packed_weight.element_size(), scales.data_ptr(),
@@ -1228,7 +1266,7 @@ class HipDecodeBackend:
             raise ValueError("fused router supports at most 128 experts")
         if bias is not None and int(bias.numel()) != experts:
             raise ValueError("router bias does not match expert count")
-        self._check_indices(indices_out)
+        self._check_router_indices(indices_out)
         _require_cuda(weight, hidden, indices_out, scores_out)
         rc = self.lib.tt_moe_router_matvec_topk(
             weight.data_ptr(), _code(weight, "router"), weight.stride(0), hidden.data_ptr(), _code(hidden, "router"),
@@ -1280,7 +1318,7 @@ class HipDecodeBackend:
             raise ValueError("fused router supports at most 128 experts")
         if bias is not None and int(bias.numel()) != experts:
             raise ValueError("router bias does not match expert count")
-        self._check_indices(indices_out)
+        self._check_router_indices(indices_out)
         _require_cuda(left, right, residual_out, norm_weight, norm_out, router_weight, indices_out, scores_out)
         ws = None
         if split:
@@ -1301,7 +1339,7 @@ class HipDecodeBackend:
     def moe_router_topk(self, logits: torch.Tensor, indices_out: torch.Tensor, scores_out: torch.Tensor, *,
                         renormalize: bool) -> tuple[torch.Tensor, torch.Tensor]:
         """(triton_kernels.py:5803-5824)"""
-        self._check_indices(indices_out)
+        self._check_router_indices(indices_out)
         _require_cuda(logits, indices_out, scores_out)
         rc = self.lib.tt_moe_router_topk(logits.data_ptr(), _code(logits, "logits"), int(logits.numel()),
                                          int(indices_out.numel()), int(bool(renormalize)), indices_out.data_ptr(),

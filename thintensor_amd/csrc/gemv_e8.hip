@@ -7,10 +7,12 @@ namespace {
 
 int selected_e8(const char* what, Fmt fmt, const void* packed, int64_t w_expert_bytes, int64_t w_row_bytes,
                 const void* scales, int64_t s_expert, int64_t s_row, const void* x, int x_dtype, int64_t x_slot,
-                const int32_t* experts, int64_t selected, void* out, int out_dtype, int64_t out_slot, int64_t rows,
+                const void* experts, int index_bytes, int64_t selected, void* out, int out_dtype, int64_t out_slot, int64_t rows,
                 int64_t cols, void* stream) {
   TT_REQUIRE(valid_act_dtype(x_dtype) && valid_out_dtype(out_dtype), "%s: bad dtype codes", what);
   TT_REQUIRE(selected >= 1 && selected <= 65535 && experts != nullptr, "%s: need 1..65535 selected experts", what);
+  int ishift;
+  TT_REQUIRE(index_shift(index_bytes, &ishift), "%s: expert indices must be int32 or int64", what);
   const int align = fmt == Fmt::kMxfp4 ? 16 : (fmt == Fmt::kQ2E8 ? 8 : 4);
   TT_REQUIRE(packed && aligned(packed, align) && w_row_bytes % align == 0 && w_expert_bytes % align == 0,
              "%s: packed weights must be %d-byte aligned", what, align);
@@ -26,6 +28,7 @@ int selected_e8(const char* what, Fmt fmt, const void* packed, int64_t w_expert_
   P.x = x;
   P.x_slot = x_slot;
   P.experts = experts;
+  P.ishift = ishift;
   P.w_expert = w_expert_bytes;
   P.s_expert = s_expert;
   P.out_slot = out_slot;
@@ -41,6 +44,7 @@ int selected_e8(const char* what, Fmt fmt, const void* packed, int64_t w_expert_
     L.x = x;
     L.out = out;
     L.experts = experts;
+    L.ishift = ishift;
     L.w_expert = w_expert_bytes;
     L.s_expert = s_expert;
     L.x_slot = x_slot;
@@ -262,17 +266,17 @@ int affine16_by_lpr(int lpr, const Aff16Params& A, hipStream_t st, const char* w
 
 extern "C" int tt_mxfp4_selected_matvec(const void* blocks, int64_t b_expert_bytes, int64_t b_row_bytes,
                                         const void* scales, int64_t s_expert, int64_t s_row, const void* x,
-                                        int x_dtype, int64_t x_slot, const int32_t* expert_indices, int64_t selected,
+                                        int x_dtype, int64_t x_slot, const void* expert_indices, int index_bytes, int64_t selected,
                                         void* out, int out_dtype, int64_t out_slot, int64_t rows, int64_t cols,
                                         void* stream) {
   return selected_e8("mxfp4_selected_matvec", Fmt::kMxfp4, blocks, b_expert_bytes, b_row_bytes, scales, s_expert,
-                     s_row, x, x_dtype, x_slot, expert_indices, selected, out, out_dtype, out_slot, rows, cols, stream);
+                     s_row, x, x_dtype, x_slot, expert_indices, index_bytes, selected, out, out_dtype, out_slot, rows, cols, stream);
 }
 
 extern "C" int tt_mxfp_lowbit_selected_matvec(const void* packed, int64_t w_expert_bytes, int64_t w_row_bytes,
                                               const void* scales, int64_t s_expert, int64_t s_row, int bits,
                                               const void* x, int x_dtype, int64_t x_slot,
-                                              const int32_t* expert_indices, int64_t selected, void* out,
+                                              const void* expert_indices, int index_bytes, int64_t selected, void* out,
                                               int out_dtype, int64_t out_slot, int64_t rows, int64_t cols,
                                               void* stream) {
   if (bits != 1 && bits != 2) {
@@ -280,7 +284,7 @@ extern "C" int tt_mxfp_lowbit_selected_matvec(const void* packed, int64_t w_expe
     return TT_ERR_INVALID;
   }
   return selected_e8("mxfp_lowbit_selected_matvec", bits == 2 ? Fmt::kQ2E8 : Fmt::kQ1E8, packed, w_expert_bytes,
-                     w_row_bytes, scales, s_expert, s_row, x, x_dtype, x_slot, expert_indices, selected, out,
+                     w_row_bytes, scales, s_expert, s_row, x, x_dtype, x_slot, expert_indices, index_bytes, selected, out,
                      out_dtype, out_slot, rows, cols, stream);
 }
 

@@ -96,7 +96,8 @@ struct GemvParams {
   int vtotal;              // virtual rows (segments padded to whole batches)
   const void* x;
   int64_t x_slot;          // activation elements between slots (0: shared vector)
-  const int32_t* experts;  // expert id per slot (nullptr: dense)
+  const void* experts;     // expert id per slot, int32 or int64 (nullptr: dense)
+  int ishift;              // log2 of the id size in 32-bit words (0: int32, 1: int64)
   int64_t w_expert;        // bytes between experts
   int64_t s_expert;        // scale elements between experts
   int64_t out_slot;        // output elements between slots
@@ -211,7 +212,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams P) {
   const int slot = blockIdx.y;
   int64_t woff = (int64_t)slot * P.w_slot, soff = 0;
   if (P.experts != nullptr) {
-    const int64_t e = P.experts[slot];
+    const int64_t e = load_expert(P.experts, P.ishift, slot);
     woff = e * P.w_expert;
     soff = e * P.s_expert;
   }

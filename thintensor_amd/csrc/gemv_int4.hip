@@ -507,13 +507,15 @@ extern "C" int tt_attention_combine_int4_matvec(const float* scratch, int64_t sc
 extern "C" int tt_int4_selected_matvec(const void* packed, int64_t w_expert_bytes, int64_t w_row_bytes,
                                        const void* scales, int scale_dtype, int64_t s_expert, int64_t s_row,
                                        int64_t s_group, const void* x, int x_dtype, int64_t x_slot,
-                                       const int32_t* expert_indices, int64_t selected, void* out, int out_dtype,
+                                       const void* expert_indices, int index_bytes, int64_t selected, void* out, int out_dtype,
                                        int64_t out_slot, int64_t rows, int64_t cols, int64_t group_size,
                                        void* stream) {
   const char* what = "int4_selected_matvec";
   TT_REQUIRE(valid_act_dtype(x_dtype) && valid_out_dtype(out_dtype), "%s: bad dtype codes", what);
   TT_REQUIRE(scale_dtype == TT_F16 || scale_dtype == TT_F32, "%s: scales must be fp16 or fp32", what);
   TT_REQUIRE(selected >= 1 && selected <= 65535 && expert_indices != nullptr, "%s: need 1..65535 selected experts", what);
+  int ishift;
+  TT_REQUIRE(index_shift(index_bytes, &ishift), "%s: expert indices must be int32 or int64", what);
   TT_REQUIRE(packed && aligned(packed, 16) && w_row_bytes % 16 == 0 && w_expert_bytes % 16 == 0,
              "%s: packed weights must be 16-byte aligned", what);
   TT_REQUIRE(x && aligned(x, 16) && (x_slot % 8) == 0, "%s: x must be 16-byte aligned (slot stride a multiple of 8)", what);
@@ -528,6 +530,7 @@ extern "C" int tt_int4_selected_matvec(const void* packed, int64_t w_expert_byte
   P.x = x;
   P.x_slot = x_slot;
   P.experts = expert_indices;
+  P.ishift = ishift;
   P.w_expert = w_expert_bytes;
   P.s_expert = s_expert;
   P.out_slot = out_slot;
@@ -543,6 +546,7 @@ extern "C" int tt_int4_selected_matvec(const void* packed, int64_t w_expert_byte
     Q.x = x;
     Q.out = out;
     Q.experts = expert_indices;
+    Q.ishift = ishift;
     Q.w_expert = w_expert_bytes;
     Q.s_expert = s_expert;
     Q.x_slot = x_slot;

@@ -23,12 +23,13 @@ struct LeanParams {
   const void* x;            // activations (slot 0)
   void* out;                // output (slot 0)
   const void* bias;         // optional, output dtype
-  const int32_t* experts;   // expert id per slot, nullptr: dense
+  const void* experts;      // expert id per slot (int32 or int64), nullptr: dense
   int64_t w_expert, s_expert, x_slot, out_slot;
   int64_t s_pair;           // affine: element offset of the second value of a pair
   uint32_t w_row;           // bytes between rows
   uint32_t s_row, s_grp;    // scale element strides
   int rows, cols, aff_zero;
+  int ishift;               // log2 of the expert id size in 32-bit words
 };
 
 template <Fmt F, SMode SM, typename XT, typename OT, typename ST, int LPR, int ROWS, int L, int XM, bool EXP,
@@ -57,7 +58,7 @@ __global__ __launch_bounds__(256) void lean_gemv_kernel(const LeanParams P) {
   const uint8_t* W = P.w;
   const ST* S = reinterpret_cast<const ST*>(P.s);
   if constexpr (EXP) {   // compile-time, so the argument loads stay in one scalar batch
-    const int64_t e = P.experts[slot];
+    const int64_t e = load_expert(P.experts, P.ishift, slot);
     W += e * P.w_expert;
     S += e * P.s_expert;
   }

@@ -18,7 +18,7 @@ struct SwigluParams {
   const uint8_t* w; int64_t w_expert, w_row;
   const uint8_t* s; int64_t s_expert, s_row;
   const void* x; int64_t x_slot;
-  const int32_t* experts;
+  const void* experts; int ishift;   // expert ids, int32 (ishift 0) or int64 (1)
   const void* bias; int64_t bias_expert;
   float alpha, limit;
   void* out; int64_t out_slot;
@@ -35,7 +35,7 @@ struct DownParams {
   const uint8_t* w; int64_t w_expert, w_row;
   const uint8_t* s; int64_t s_expert, s_row;
   const void* x; int64_t x_slot;
-  const int32_t* experts;
+  const void* experts; int ishift;   // expert ids, int32 (ishift 0) or int64 (1)
   const void* scores;
   const void* bias; int64_t bias_expert;
   void* out;

@@ -31,7 +31,7 @@ __global__ __launch_bounds__(256) void weighted_down_kernel(DownParams P) {
   const uint8_t* srow[RPW];
   int64_t e = 0;
   auto point = [&](int s) {
-    e = P.experts[(int64_t)blockIdx.y * P.slots + s];
+    e = load_expert(P.experts, P.ishift, (int64_t)blockIdx.y * P.slots + s);
 #pragma unroll
     for (int i = 0; i < RPW; i++) {
       wrow[i] = P.w + e * P.w_expert + (int64_t)row[i] * P.w_row;
@@ -125,7 +125,7 @@ __global__ __launch_bounds__(256) void down_lean_kernel(const DownParams P) {
 
   int64_t e[S];
 #pragma unroll
-  for (int s = 0; s < S; s++) e[s] = P.experts[tok * S + s];
+  for (int s = 0; s < S; s++) e[s] = load_expert(P.experts, P.ishift, (int64_t)tok * S + s);
   const uint8_t* wrow[S][ROWS];
   const uint8_t* srow[S][ROWS];
   bool rv[ROWS];
@@ -293,7 +293,7 @@ using namespace tt;
 static int weighted_down_impl(const void* packed, int64_t w_expert_bytes, int64_t w_row_bytes,
                                             const void* scales, int64_t s_expert, int64_t s_row, int bits,
                                             const void* x, int x_dtype, int64_t x_slot,
-                                            const int32_t* expert_indices, const void* router_scores,
+                                            const void* expert_indices, int index_bytes, const void* router_scores,
                                             int score_dtype, int64_t selected, const void* bias, int bias_dtype,
                                             int64_t bias_expert, void* out, int out_dtype, int64_t rows,
                                             int64_t cols, int64_t tokens, int64_t out_token, void* stream) {
@@ -311,9 +311,11 @@ static int weighted_down_impl(const void* packed, int64_t w_expert_bytes, int64_
   TT_REQUIRE(scales && x && aligned(x, 4) && x_slot % 2 == 0 && out && expert_indices && router_scores,
              "%s: null or misaligned pointer", what);
   TT_REQUIRE(valid_out_dtype(score_dtype), "%s: bad score dtype", what);
+  int ishift;
+  TT_REQUIRE(index_shift(index_bytes, &ishift), "%s: expert indices must be int32 or int64", what);
   if (bias) TT_REQUIRE(valid_out_dtype(bias_dtype), "%s: bad bias dtype", what);
   DownParams P{static_cast<const uint8_t*>(packed), w_expert_bytes, w_row_bytes,
-               static_cast<const uint8_t*>(scales), s_expert, s_row, x, x_slot, expert_indices, router_scores, bias,
+               static_cast<const uint8_t*>(scales), s_expert, s_row, x, x_slot, expert_indices, ishift, router_scores, bias,
                bias_expert, out, (int)rows, (int)cols, (int)selected, bias ? bias_dtype : TT_F32, score_dtype, out_token,
                (int)tokens};
   const int lpr = tt_gemv_lanes_per_row(cols / 32, 1);
@@ -329,23 +331,23 @@ static int weighted_down_impl(const void* packed, int64_t w_expert_bytes, int64_
 extern "C" int tt_mxfp_lowbit_weighted_down(const void* packed, int64_t w_expert_bytes, int64_t w_row_bytes,
                                             const void* scales, int64_t s_expert, int64_t s_row, int bits,
                                             const void* x, int x_dtype, int64_t x_slot,
-                                            const int32_t* expert_indices, const void* router_scores,
+                                            const void* expert_indices, int index_bytes, const void* router_scores,
                                             int score_dtype, int64_t selected, const void* bias, int bias_dtype,
                                             int64_t bias_expert, void* out, int out_dtype, int64_t rows,
                                             int64_t cols, void* stream) {
   return weighted_down_impl(packed, w_expert_bytes, w_row_bytes, scales, s_expert, s_row, bits, x, x_dtype, x_slot,
-                            expert_indices, router_scores, score_dtype, selected, bias, bias_dtype, bias_expert, out,
+                            expert_indices, index_bytes, router_scores, score_dtype, selected, bias, bias_dtype, bias_expert, out,
                             out_dtype, rows, cols, 1, 0, stream);
 }
 
 extern "C" int tt_mxfp_lowbit_weighted_down_tokens(const void* packed, int64_t w_expert_bytes, int64_t w_row_bytes,
                                                    const void* scales, int64_t s_expert, int64_t s_row, int bits,
                                                    const void* x, int x_dtype, int64_t x_slot,
-                                                   const int32_t* expert_indices, const void* router_scores,
+                                                   const void* expert_indices, int index_bytes, const void* router_scores,
                                                    int score_dtype, int64_t selected, const void* bias, int bias_dtype,
                                                    int64_t bias_expert, void* out, int out_dtype, int64_t out_token,
                                                    int64_t rows, int64_t cols, int64_t tokens, void* stream) {
   return weighted_down_impl(packed, w_expert_bytes, w_row_bytes, scales, s_expert, s_row, bits, x, x_dtype, x_slot,
-                            expert_indices, router_scores, score_dtype, selected, bias, bias_dtype, bias_expert, out,
+                            expert_indices, index_bytes, router_scores, score_dtype, selected, bias, bias_dtype, bias_expert, out,
                             out_dtype, rows, cols, tokens, out_token, stream);
 }

@@ -10,7 +10,7 @@ __global__ __launch_bounds__(256) void swiglu_kernel(SwigluParams P) {
   extern __shared__ uint32_t xs_lds[];
   constexpr int SUBS = 64 / LPR;
   const int slot = blockIdx.y;
-  const int64_t e = P.experts[slot];
+  const int64_t e = load_expert(P.experts, P.ishift, slot);
   const uint8_t* wexp = P.w + e * P.w_expert;
   const uint8_t* sexp = P.s + e * P.s_expert;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -101,7 +101,7 @@ __global__ __launch_bounds__(256) void swiglu_lean_kernel(const SwigluParams P) 
     xidx[k] = idx < xn ? idx : xn - 1;
     xreg[k] = xg[xidx[k]];
   }
-  const int64_t e = P.experts[slot];
+  const int64_t e = load_expert(P.experts, P.ishift, slot);
   const uint8_t* wexp = P.w + e * P.w_expert;
   const uint8_t* sexp = P.s + e * P.s_expert;
   const uint8_t* wrow[ROWS];
@@ -220,7 +220,7 @@ __global__ __launch_bounds__(256) void swiglu_lean_multi_kernel(const SwigluPara
     xidx[k] = idx < xn ? idx : xn - 1;
     xreg[k] = xg[xidx[k]];
   }
-  const int64_t e = P.experts[slot];
+  const int64_t e = load_expert(P.experts, P.ishift, slot);
   const uint8_t* wexp = P.w + e * P.w_expert;
   const uint8_t* sexp = P.s + e * P.s_expert;
   struct Round {
@@ -385,7 +385,7 @@ using namespace tt;
 static int selected_swiglu_impl(const void* packed, int64_t w_expert_bytes, int64_t w_row_bytes,
                                               const void* scales, int64_t s_expert, int64_t s_row, int bits,
                                               const void* x, int x_dtype, int64_t x_slot,
-                                              const int32_t* expert_indices, int64_t selected, const void* bias,
+                                              const void* expert_indices, int index_bytes, int64_t selected, const void* bias,
                                               int bias_dtype, int64_t bias_expert, float alpha, float limit,
                                               void* out, int out_dtype, int64_t out_slot, int64_t activation_rows,
                                               int64_t cols, int64_t tokens, void* stream) {
@@ -396,13 +396,15 @@ static int selected_swiglu_impl(const void* packed, int64_t w_expert_bytes, int6
   TT_REQUIRE(cols > 0 && cols % 32 == 0 && cols <= 32768, "%s: cols must be a multiple of 32 up to 32768", what);
   TT_REQUIRE(activation_rows > 0 && activation_rows < (1 << 29), "%s: bad activation rows", what);
   TT_REQUIRE(selected >= 1 && selected <= 65535 && expert_indices, "%s: need selected experts", what);
+  int ishift;
+  TT_REQUIRE(index_shift(index_bytes, &ishift), "%s: expert indices must be int32 or int64", what);
   const int align = bits == 4 ? 16 : (bits == 2 ? 8 : 4);
   TT_REQUIRE(packed && aligned(packed, align) && w_row_bytes % align == 0 && w_expert_bytes % align == 0,
              "%s: packed weights must be %d-byte aligned", what, align);
   TT_REQUIRE(scales && x && aligned(x, 4) && x_slot % 2 == 0 && out, "%s: null or misaligned pointer", what);
   if (bias) TT_REQUIRE(valid_out_dtype(bias_dtype), "%s: bad bias dtype", what);
   SwigluParams P{static_cast<const uint8_t*>(packed), w_expert_bytes, w_row_bytes,
-                 static_cast<const uint8_t*>(scales), s_expert, s_row, x, x_slot, expert_indices, bias, bias_expert,
+                 static_cast<const uint8_t*>(scales), s_expert, s_row, x, x_slot, expert_indices, ishift, bias, bias_expert,
                  alpha, limit, out, out_slot, (int)activation_rows, (int)cols, tokens > 1 ? (int)selected : 1};
   const int lpr = tt_gemv_lanes_per_row(cols / 32, 1);
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -419,24 +421,24 @@ static int selected_swiglu_impl(const void* packed, int64_t w_expert_bytes, int6
 extern "C" int tt_mxfp_lowbit_selected_swiglu(const void* packed, int64_t w_expert_bytes, int64_t w_row_bytes,
                                               const void* scales, int64_t s_expert, int64_t s_row, int bits,
                                               const void* x, int x_dtype, int64_t x_slot,
-                                              const int32_t* expert_indices, int64_t selected, const void* bias,
+                                              const void* expert_indices, int index_bytes, int64_t selected, const void* bias,
                                               int bias_dtype, int64_t bias_expert, float alpha, float limit,
                                               void* out, int out_dtype, int64_t out_slot, int64_t activation_rows,
                                               int64_t cols, void* stream) {
   return selected_swiglu_impl(packed, w_expert_bytes, w_row_bytes, scales, s_expert, s_row, bits, x, x_dtype, x_slot,
-                              expert_indices, selected, bias, bias_dtype, bias_expert, alpha, limit, out, out_dtype,
+                              expert_indices, index_bytes, selected, bias, bias_dtype, bias_expert, alpha, limit, out, out_dtype,
                               out_slot, activation_rows, cols, 1, stream);
 }
 
 extern "C" int tt_mxfp_lowbit_selected_swiglu_tokens(const void* packed, int64_t w_expert_bytes, int64_t w_row_bytes,
                                                      const void* scales, int64_t s_expert, int64_t s_row, int bits,
                                                      const void* x, int x_dtype, int64_t x_token,
-                                                     const int32_t* expert_indices, int64_t selected,
+                                                     const void* expert_indices, int index_bytes, int64_t selected,
                                                      const void* bias, int bias_dtype, int64_t bias_expert,
                                                      float alpha, float limit, void* out, int out_dtype,
                                                      int64_t out_slot, int64_t activation_rows, int64_t cols,
                                                      int64_t tokens, void* stream) {
   return selected_swiglu_impl(packed, w_expert_bytes, w_row_bytes, scales, s_expert, s_row, bits, x, x_dtype, x_token,
-                              expert_indices, selected, bias, bias_dtype, bias_expert, alpha, limit, out, out_dtype,
+                              expert_indices, index_bytes, selected, bias, bias_dtype, bias_expert, alpha, limit, out, out_dtype,
                               out_slot, activation_rows, cols, tokens, stream);
 }

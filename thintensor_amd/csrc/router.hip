@@ -517,6 +517,93 @@ __global__ __launch_bounds__(64) void topk_kernel(const void* logits_in, int E, 
   wave_topk<OT>(l0, l1, E, top_k, renorm != 0, idx_out, reinterpret_cast<OT*>(score_out));
 }
 
+// Top-k + softmax over 128 < E <= kTopkMaxExperts logits in one 256-thread workgroup:
+// the reference kernel has no expert cap (triton_kernels.py:2821-2851) and the runtime
+// calls it exactly when the router has more than 128 rows (gpu_runtime.py:9474-9496).
+// Same selection rule and summation order as wave_topk: slot s takes the first untaken
+// expert when its logit is NaN, otherwise the untaken expert of the largest non-NaN key
+// (lowest index among equal values); taken experts are bits of an LDS mask.  The logits
+// are re-read on every slot (cache hits after the first pass).  The denominator is summed
+// sequentially in slot order (renormalize) or in expert order by wave 0.
+constexpr int kTopkMaxExperts = 65536;
+constexpr int kTopkMaxSlots = 4096;
+
+template <typename LT, typename OT>
+__global__ __launch_bounds__(256) void topk_block_kernel(const void* logits_in, int E, int top_k, int renorm,
+                                                         int32_t* idx_out, void* score_out) {
+  __shared__ uint32_t taken[kTopkMaxExperts / 32];
+  __shared__ float sel_v[kTopkMaxSlots];
+  __shared__ uint64_t red_k[4];
+  __shared__ uint32_t red_f[4];
+  __shared__ float red_m[4];
+  const int t = threadIdx.x, lane = lane_id(), wave = t >> 6;
+  for (int i = t; i < (E + 31) / 32; i += 256) taken[i] = 0u;
+  float m = __builtin_bit_cast(float, 0xff800000u);
+  for (int e = t; e < E; e += 256) m = fmaxf(m, ldv<LT>(logits_in, e));
+  m = fmaxf(m, xor_partner<1>(m));
+  m = fmaxf(m, xor_partner<2>(m));
+  m = fmaxf(m, xor_partner<4>(m));
+  m = fmaxf(m, xor_partner<8>(m));
+  m = fmaxf(m, xor_partner<16>(m));
+  m = fmaxf(m, xor_partner<32>(m));
+  if (lane == 0) red_m[wave] = m;
+  __syncthreads();
+  m = fmaxf(fmaxf(red_m[0], red_m[1]), fmaxf(red_m[2], red_m[3]));
+  float den = 0.0f;
+  for (int s = 0; s < top_k; s++) {
+    uint64_t k = 0;
+    uint64_t f = 0;
+    for (int e = t; e < E; e += 256) {
+      if (taken[e >> 5] & (1u << (e & 31))) continue;
+      const uint64_t fe = 0xffffffffu - (uint32_t)e;
+      f = fe > f ? fe : f;
+      const float v = ldv<LT>(logits_in, e);
+      if (!__builtin_isnan(v)) {
+        const uint64_t key = topk_key(v, (uint32_t)e);
+        k = key > k ? key : k;
+      }
+    }
+    k = wave_max_u64(k);
+    f = wave_max_u64(f);
+    if (lane == 0) {
+      red_k[wave] = k;
+      red_f[wave] = (uint32_t)f;
+    }
+    __syncthreads();
+    k = red_k[0];
+    uint32_t fb = red_f[0];
+#pragma unroll
+    for (int w = 1; w < 4; w++) {
+      k = red_k[w] > k ? red_k[w] : k;
+      fb = red_f[w] > fb ? red_f[w] : fb;
+    }
+    const int first = (int)(0xffffffffu - fb);
+    const float fv = ldv<LT>(logits_in, first);
+    const int bi = __builtin_isnan(fv) ? first : (int)(0xffffffffu - (uint32_t)k);
+    const float bv = ldv<LT>(logits_in, bi);
+    if (renorm) den = den + exp_f32(bv - m);
+    if (t == 0) {
+      idx_out[s] = bi;
+      sel_v[s] = bv;
+      taken[bi >> 5] |= 1u << (bi & 31);
+    }
+    __syncthreads();
+  }
+  if (!renorm) {
+    if (wave == 0) {
+      for (int b = 0; b < E; b += 64) {
+        const float a = b + lane < E ? exp_f32(ldv<LT>(logits_in, b + lane) - m) : 0.0f;
+        const int n = E - b < 64 ? E - b : 64;
+        for (int j = 0; j < n; j++) den = den + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a), j));
+      }
+      if (lane == 0) red_m[0] = den;
+    }
+    __syncthreads();
+    den = red_m[0];
+  }
+  for (int s = t; s < top_k; s += 256) store<OT>(reinterpret_cast<OT*>(score_out) + s, exp_f32(sel_v[s] - m) / den);
+}
+
 template <typename Fn> static int dt3(int code, Fn&& f) {
   if (code == TT_F16) return f(f16_t{});
   if (code == TT_BF16) return f(bf16_t{});
@@ -566,14 +653,20 @@ extern "C" int tt_moe_router_matvec_topk(const void* weight, int w_dtype, int64_
 extern "C" int tt_moe_router_topk(const void* logits, int logits_dtype, int64_t experts, int64_t top_k, int renormalize,
                                   int32_t* indices_out, void* scores_out, int score_dtype, void* stream) {
   const char* what = "moe_router_topk";
-  TT_REQUIRE(experts > 0 && experts <= 128 && top_k > 0 && top_k <= experts, "%s: bad expert counts", what);
+  TT_REQUIRE(experts > 0 && top_k > 0 && top_k <= experts, "%s: bad expert counts", what);
+  TT_UNSUPPORTED(experts <= kTopkMaxExperts && (experts <= 128 || top_k <= kTopkMaxSlots),
+                 "%s: at most %d experts and, above 128 experts, %d slots", what, kTopkMaxExperts, kTopkMaxSlots);
   TT_REQUIRE(logits && indices_out && scores_out, "%s: null pointer", what);
   return dt3(logits_dtype, [&](auto lt) {
     using LT = decltype(lt);
     return dt3(score_dtype, [&](auto ot) {
       using OT = decltype(ot);
-      hipLaunchKernelGGL((topk_kernel<LT, OT>), dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream), logits,
-                         (int)experts, (int)top_k, renormalize, indices_out, scores_out);
+      if (experts <= 128)
+        hipLaunchKernelGGL((topk_kernel<LT, OT>), dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream), logits,
+                           (int)experts, (int)top_k, renormalize, indices_out, scores_out);
+      else
+        hipLaunchKernelGGL((topk_block_kernel<LT, OT>), dim3(1), dim3(256), 0, static_cast<hipStream_t>(stream),
+                           logits, (int)experts, (int)top_k, renormalize, indices_out, scores_out);
       return check_launch(what);
     });
   });

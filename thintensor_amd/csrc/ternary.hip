@@ -46,7 +46,8 @@ struct TernParams {
   const uint8_t* s;         // E8M0 [E, rows, G]
   const uint8_t* s_end;
   const void* x;            // [cols] or [selected, cols]
-  const int32_t* experts;
+  const void* experts;   // int32 (ishift 0) or int64 (ishift 1) ids
+  int ishift;
   void* out;                // [selected, out_slot]
   int64_t w_expert, w_row;  // bytes
   int64_t s_expert, s_row;  // bytes
@@ -90,7 +91,7 @@ __global__ __launch_bounds__(kThreads) void ternary_selected_kernel(TernParams P
   const int row0 = blockIdx.x * P.rpw;
   const int nrows = P.rows - row0 < P.rpw ? P.rows - row0 : P.rpw;
   OT* out = reinterpret_cast<OT*>(P.out) + (int64_t)slot * P.out_slot + row0;
-  const int64_t e = P.experts[slot];
+  const int64_t e = load_expert(P.experts, P.ishift, slot);
   if (e < 0 || e >= P.n_experts) {                      // uniform over the workgroup
     for (int r = threadIdx.x; r < nrows; r += kThreads) store(out + r, __builtin_nanf(""));
     return;
@@ -254,7 +255,7 @@ extern "C" int tt_mxfp_ternary_selected_matvec(const void* packed, int64_t w_exp
                                                int64_t w_total_bytes, const void* scales, int64_t s_expert,
                                                int64_t s_row, int64_t s_total_bytes, int64_t experts,
                                                const void* x, int x_dtype, int64_t x_slot,
-                                               const int32_t* expert_indices, int64_t selected, void* out,
+                                               const void* expert_indices, int index_bytes, int64_t selected, void* out,
                                                int out_dtype, int64_t out_slot, int64_t rows, int64_t cols,
                                                void* stream) {
   const char* what = "mxfp_ternary_selected_matvec";
@@ -263,6 +264,8 @@ extern "C" int tt_mxfp_ternary_selected_matvec(const void* packed, int64_t w_exp
   TT_UNSUPPORTED(cols <= kMaxCols, "%s: cols above %d are not supported", what, kMaxCols);
   TT_REQUIRE(rows > 0 && rows < (1 << 30) && experts >= 1, "%s: bad rows / experts", what);
   TT_REQUIRE(selected >= 1 && selected <= 65535 && expert_indices, "%s: need 1..65535 selected experts", what);
+  int ishift;
+  TT_REQUIRE(index_shift(index_bytes, &ishift), "%s: expert indices must be int32 or int64", what);
   const int64_t groups = cols / 32, tbytes = (cols + 4) / 5, mbytes = (groups * 3 + 7) / 8;
   TT_REQUIRE(w_row_bytes >= tbytes + mbytes && w_expert_bytes >= rows * w_row_bytes &&
                  w_total_bytes >= (experts - 1) * w_expert_bytes + rows * w_row_bytes,
@@ -282,6 +285,7 @@ extern "C" int tt_mxfp_ternary_selected_matvec(const void* packed, int64_t w_exp
   P.s_end = P.s + s_total_bytes;
   P.x = x;
   P.experts = expert_indices;
+  P.ishift = ishift;
   P.out = out;
   P.w_expert = w_expert_bytes;
   P.w_row = w_row_bytes;

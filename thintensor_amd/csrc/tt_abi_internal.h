@@ -46,6 +46,13 @@ inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintp
 int dense_bias_rows_f16(const void* weight, int64_t w_row, const void* bias, const void* x, int64_t x_row, void* out,
                         int64_t out_row, int64_t m, int64_t rows, int64_t cols, hipStream_t st);
 
+// Expert index arrays are int32 or int64 (index_bytes 4 or 8); the kernels take the
+// log2 of the size in 32-bit words.
+inline bool index_shift(int index_bytes, int* shift) {
+  *shift = index_bytes == 8 ? 1 : 0;
+  return index_bytes == 4 || index_bytes == 8;
+}
+
 inline bool valid_act_dtype(int d) { return d == TT_F16 || d == TT_BF16; }
 inline bool valid_out_dtype(int d) { return d == TT_F16 || d == TT_BF16 || d == TT_F32; }
 

@@ -173,6 +173,19 @@ __device__ __forceinline__ float pow2i(int e) {
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 
+// Expert id of slot s from an index array of int32 (ishift 0) or int64 (ishift 1)
+// elements, as the reference's kernels load whichever integer type they are given.
+// Both 32-bit words are requested at once from addresses that depend only on the
+// arguments (for int32 the second load repeats the first word, so nothing past the
+// array is read); an int64 id keeps its high word, so an out-of-range id stays out
+// of range.
+__device__ __forceinline__ int64_t load_expert(const void* p, int ishift, int64_t s) {
+  const int32_t* q = reinterpret_cast<const int32_t*>(p) + (s << ishift);
+  const uint32_t lo = (uint32_t)q[0];
+  const int32_t hi = q[ishift];
+  return ishift ? (int64_t)(((uint64_t)(uint32_t)hi << 32) | lo) : (int64_t)(int32_t)lo;
+}
+
 // Maximum of a 64-bit key over the wave (every lane gets the result).
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t k) {
 #define TT_MAXSTEP(M)                                                                                     \
