@@ -154,6 +154,7 @@ def table_entry(path, index):
     ("raw", "Uncompressed page model.norm.weight stored/raw sizes differ"),                  # :184-187
     ("before", "Page model.norm.weight offset starts before data_off"),                      # :174
     ("beyond", "Page model.norm.weight offset\\+size exceeds file size"),                    # :176
+    ("wrap", "Page model.norm.weight offset\\+size exceeds file size"),                      # no 2^64 wrap-around
     ("zero", "Page model.norm.weight has zero stored_size but nonzero raw_size"),            # :178
     ("empty_id", "Empty page id at page index 1"),                                           # :162
     ("data_off", "Page table ends at"),                                                      # :148-151
@@ -172,6 +173,8 @@ def test_page_table_checks(tmp_path, case, expect):
         corrupt(path, tail, u64(10))
     elif case == "beyond":
         corrupt(path, tail, u64(path.stat().st_size - 4))
+    elif case == "wrap":   # offset near 2^64 plus a small size: the sum would wrap in uint64
+        corrupt(path, tail, u64(2**64 - 8) + u64(16) + u64(16))
     elif case == "zero":
         corrupt(path, tail + 8, u64(0))
     elif case == "empty_id":

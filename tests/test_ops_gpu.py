@@ -400,6 +400,7 @@ def test_unrounded_argmax_matches_binary32_logits(backend, device, rows, cols):
     (16, 16, 1, 64),       # one token, one query head per KV head
     (32, 4, 130, 1024),    # eight query heads per KV head, most of the capacity unused
     (8, 2, 200, 256),      # four heads of 64 (cols 512: 16 lanes per row)
+    (32, 8, 8300, 8320),   # 130 chunks x 8 KV heads > 1024 workgroups: two chunks per workgroup, odd count on the 2nd call
 ])
 def test_attention_then_int4_matvec(backend, device, heads, kv_heads, tokens, cap):
     """o_proj that combines the attention chunk partials itself: the combined activation

@@ -211,7 +211,8 @@ extern "C" int tt_archive_parse_pages(tt_archive* a) {
     r.checksum_off = (int64_t)(pos + 28);
     pos += 60;
     if (r.offset < a->h.data_off) return fail("Page %s offset starts before data_off", id.c_str());
-    if (r.stored_size > size || r.offset + r.stored_size > size)
+    // offset + stored_size <= size, written so that no sum can wrap around 2^64
+    if (r.offset > size || r.stored_size > size - r.offset)
       return fail("Page %s offset+size exceeds file size", id.c_str());
     if (r.stored_size == 0 && r.raw_size != 0)
       return fail("Page %s has zero stored_size but nonzero raw_size", id.c_str());
@@ -236,7 +237,7 @@ extern "C" int tt_archive_check_overlaps(const tt_archive* a) {
   for (size_t k = 0; k + 1 < order.size(); k++) {
     const Record& r1 = a->pages[order[k]];
     const Record& r2 = a->pages[order[k + 1]];
-    if (r1.offset + r1.stored_size > r2.offset) {
+    if (r1.stored_size > r2.offset - r1.offset) {   // r2.offset >= r1.offset (sorted); no wrap
       const std::string n1(reinterpret_cast<const char*>(a->map + r1.id_off), r1.id_len);
       const std::string n2(reinterpret_cast<const char*>(a->map + r2.id_off), r2.id_len);
       return fail("Overlapping pages detected: %s overlaps with %s", n1.c_str(), n2.c_str());

@@ -11,10 +11,14 @@
 namespace tt {
 namespace {
 
+// The grid holds whole workgroups of four waves; waves at or past `waves` (the last
+// workgroup's padding) return at once, so out[] is written for wave < waves only.
 __global__ __launch_bounds__(256) void stream_read_kernel(const uint4* __restrict__ p, int64_t units,
-                                                          int units_per_wave, uint32_t* __restrict__ out) {
+                                                          int units_per_wave, int64_t waves,
+                                                          uint32_t* __restrict__ out) {
   const int lane = threadIdx.x & 63;
   const int64_t wave = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (wave >= waves) return;   // wave-uniform
   const int64_t base = wave * units_per_wave;
   uint32_t acc = 0;
   for (int u = 0; u < units_per_wave; u += 128) {
@@ -49,7 +53,7 @@ extern "C" int tt_stream_read(const void* data, int64_t bytes, int64_t bytes_per
   TT_REQUIRE(out_words >= waves, "%s: out needs %lld words", what, (long long)waves);
   const dim3 grid((unsigned)((waves + 3) / 4));
   hipLaunchKernelGGL(stream_read_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream),
-                     static_cast<const uint4*>(data), bytes / 16, (int)(bytes_per_wave / 16),
+                     static_cast<const uint4*>(data), bytes / 16, (int)(bytes_per_wave / 16), waves,
                      static_cast<uint32_t*>(out));
   return check_launch(what);
 }

@@ -682,7 +682,10 @@ extern "C" int tt_requantize_mxfp4_lowbit(const uint8_t* blocks, const uint8_t* 
   const char* what = "quantize_mxfp4_to_lowbit";
   TT_REQUIRE(blocks && scales && out && out_scales, "%s: null pointer", what);
   TT_REQUIRE(bits == 1 || bits == 2, "%s: packed MXFP4 expert precision must be Q1 or Q2", what);
-  TT_REQUIRE(n_groups > 0 && n_groups < (1ll << 36), "%s: bad group count", what);
+  TT_REQUIRE(n_groups > 0, "%s: bad group count", what);
+  // eight groups per 256-thread workgroup: 32 work-items per group, and a launch
+  // holds fewer than 2^32 work-items
+  TT_UNSUPPORTED(n_groups < (1ll << 27), "%s: at most 2^27 groups per call", what);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 grid((unsigned)((n_groups + 7) / 8));
   hipLaunchKernelGGL(lowbit_requant_kernel, grid, dim3(256), 0, st, blocks, scales, n_groups, bits, out, out_scales);
@@ -697,7 +700,7 @@ extern "C" int tt_quantize_dense_lowbit(const void* src, int src_dtype, int64_t 
   TT_REQUIRE(rows > 0 && cols > 0 && cols < (1 << 30) && src_row >= cols, "%s: bad shape", what);
   TT_REQUIRE(cols % 32 == 0, "%s: dense low-bit input width must be divisible by 32", what);
   const int64_t n = rows * (cols / 32);
-  TT_REQUIRE(n < (1ll << 36), "%s: too many groups", what);
+  TT_UNSUPPORTED(n < (1ll << 27), "%s: at most 2^27 groups per call (32 work-items each)", what);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 grid((unsigned)((n + 7) / 8));
   return by_src_dtype(src_dtype, what, [&](auto t) -> int {
