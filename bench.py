@@ -3,7 +3,9 @@
 Default run (N=1):
 
 * ``value``: bs=1 greedy decode tokens/s of the Llama-3.2-1B-shaped model (int4 g128
-  linear layers, fp16 embeddings/lm_head, fp16 KV cache with 512 prior tokens).  One
+  linear layers with codes q in [-7, 7], fp16 embeddings/lm_head, fp16 KV cache with
+  512 prior tokens), the model whose token stream the parity test pins; the
+  benchmark's own q in [-8, 7] init is timed beside it (same launches and bytes).  One
   "step" is one generated token: a replay of the HIP graph that holds the whole
   decode step (embedding -> 16 layers -> lm_head GEMV + greedy argmax -> token log).
   Warm-up steps decode from the 512-token prefix; the position is then reset to 512
@@ -319,7 +321,25 @@ def _time_decode(dec, start_token: int, position: int, warmup: int, steps: int) 
     return {"wall_s": wall, "event_s": e0.elapsed_time(e1) * 1e-3, "tokens": tokens}
 
 
-def dense_decode_phase(args) -> tuple[dict, object]:
+ORACLE_TOKENS = os.path.join(os.path.dirname(os.path.abspath(__file__)), "tests", "golden",
+                             "llama1b_centered_tokens.json")
+
+
+def _oracle_fixture_tokens(seed: int) -> list[int] | None:
+    """The oracle's greedy stream of the centred-code Llama-1B model (seed 0, start token
+    1 at position 512), committed as data by the parity test's fixture script."""
+    try:
+        with open(ORACLE_TOKENS) as f:
+            d = json.load(f)
+    except (OSError, ValueError):
+        return None
+    return [int(t) for t in d["tokens"]] if int(d.get("seed", -1)) == seed else None
+
+
+def dense_decode_phase(args, centered: bool = True) -> tuple[dict, object]:
+    """bs=1 decode of the Llama-1B-shaped model.  ``centered`` draws int4 codes q in
+    [-7, 7], the model whose 64-token stream the parity test pins against the oracle;
+    otherwise the benchmark's own q in [-8, 7] (finite for four layers only)."""
     import torch
 
     from thintensor_amd.backend import HipDecodeBackend
@@ -329,7 +349,7 @@ def dense_decode_phase(args) -> tuple[dict, object]:
     s = LLAMA_1B
     dev = torch.device("cuda:0")
     cap = s.prior_tokens + max(args.steps, args.warmup)
-    w = make_dense(s, device=dev, seed=args.seed, capacity=cap)
+    w = make_dense(s, device=dev, seed=args.seed, capacity=cap, centered_codes=centered)
     be = HipDecodeBackend(dev, torch.float16, s.hidden, s.q_dim, s.kv_dim, s.intermediate)
     dec = DenseDecoder(be, w, fused=not args.unfused)
     if args.steps > dec.history.numel():
@@ -402,7 +422,8 @@ def cpu_phase(args) -> tuple[dict, dict]:
     torch.set_num_threads(physical_cores())
     rows = gemv_rows(args.seed)
     s = LLAMA_1B
-    w = make_dense(s, device=torch.device("cuda:0"), seed=args.seed, capacity=s.prior_tokens + 64)
+    w = make_dense(s, device=torch.device("cuda:0"), seed=args.seed, capacity=s.prior_tokens + 64,
+                   centered_codes=True)
     dense = dense_decode_baseline(w, 1, budget_s=12.0, max_tokens=32)
     del w
     torch.cuda.empty_cache()
@@ -482,11 +503,19 @@ def main() -> int:
         print(json.dumps({"int4_gemv": r, "copy_calibration_bytes": src.numel() * 2}), flush=True)
         return 0
 
-    _log("dense decode (llama-3.2-1b-shaped)")
+    _log("dense decode (llama-3.2-1b-shaped, centred int4 codes)")
     torch.cuda.synchronize()
-    dense, be = dense_decode_phase(args)
+    dense, be = dense_decode_phase(args, centered=True)
     tok_s = args.steps / dense["wall_s"]
-    _log(f"dense decode: {tok_s:.1f} tok/s")
+    want = _oracle_fixture_tokens(args.seed)
+    n_cmp = min(len(want), args.steps) if want else 0
+    match = dense["tokens"][:n_cmp] == want[:n_cmp] if want else None
+    _log(f"dense decode: {tok_s:.1f} tok/s; first {n_cmp} tokens equal the oracle stream: {match}")
+    del be
+    torch.cuda.empty_cache()
+    _log("dense decode (llama-3.2-1b-shaped, benchmark init q in [-8, 7])")
+    dense_b, be = dense_decode_phase(args, centered=False)
+    _log(f"dense decode (benchmark init): {args.steps / dense_b['wall_s']:.1f} tok/s")
 
     _log("int4 g128 GEMV roofline (8192 x 2048, 64 rotated copies)")
     roof = int4_gemv_phase(be, 8192, 2048, 128, 64, args.seed)
@@ -564,9 +593,17 @@ def main() -> int:
         "decode_frac_of_hbm_peak": dense["bytes_per_token"] * tok_s / 1e9 / HBM_PEAK_GBS,
         "decode_event_tok_s": args.steps / dense["event_s"],
         "decode_tokens": dense["tokens"],
-        "decode_note": "benchmark init (int4 codes q in [-8, 7]): the fp16 residual overflows after four layers, "
-                       "so the stream is that of non-finite logits; the work per token does not depend on the "
-                       "values, and the 64-token parity test uses centered codes (q in [-7, 7]) of the same shapes",
+        "decode_tokens_match_oracle": match,
+        "decode_tokens_compared": n_cmp,
+        "decode_note": "int4 codes q in [-7, 7] (the clamp of the reference's _quantize_int4_rows), the model whose "
+                       "64-token stream the parity test pins against the oracle; decode_tokens_match_oracle "
+                       "compares the timed stream with that oracle stream (tests/golden/llama1b_centered_tokens.json)",
+        "baseline_init_decode": {
+            "workload": "same shapes, int4 codes q in [-8, 7] as the benchmark config states; the fp16 residual "
+                        "overflows after four layers, so its stream is that of non-finite logits",
+            "tok_s": args.steps / dense_b["wall_s"],
+            "event_tok_s": args.steps / dense_b["event_s"],
+        },
         "moe_decode": moe,
         "cpu_rows": cpu_rows,
         "extra": extra,

@@ -108,8 +108,21 @@ def llama_case(device):
     ref = DenseRef(w)
     margins: list[float] = []
     want = ref.generate(1, s.prior_tokens, 64, margins=margins)
-    print(f"llama-1b oracle stream: {len(set(want))} distinct of 64, min top-2 margin {min(margins):.4g}", flush=True)
+    print(f"llama-1b oracle stream: {len(set(want))} distinct of 64, min top-2 margin {min(margins):.4g}: {want}",
+          flush=True)
     return w, want, ref.last_logits, margins
+
+
+def test_llama_1b_oracle_stream_fixture(llama_case):
+    """The committed stream (tests/golden/llama1b_centered_tokens.json, which bench.py
+    compares its timed tokens with) is this oracle's stream."""
+    import json
+    from pathlib import Path
+
+    path = Path(__file__).with_name("golden") / "llama1b_centered_tokens.json"
+    d = json.loads(path.read_text())
+    assert d["seed"] == 0 and d["start_token"] == 1 and d["position"] == LLAMA_1B.prior_tokens
+    assert d["tokens"] == llama_case[1]
 
 
 @pytest.mark.parametrize("fused", [False, True])
