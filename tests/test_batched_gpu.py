@@ -68,18 +68,20 @@ def test_int4_batched_decode_shape_mfma(backend, device):
 
 
 @pytest.mark.parametrize("fmt,rows,cols,m", [
-    ("int4", 64, 256, 16),        # one unit: one workgroup, no shared block
-    ("int4", 100, 768, 20),       # six units over six workgroups: every block shared, ragged last block
-    ("int4", 4000, 2048, 48),     # one unit per workgroup: eight partial tiles per block
-    ("int4", 17920, 5120, 16),    # whole blocks inside a range and blocks shared at range ends
+    ("int4", 64, 256, 16),        # two K steps over four waves: two waves hold no columns; one row per tile
+    ("int4", 100, 768, 20),       # six K steps: waves take 1, 2, 1, 2 of them; ragged activation tile
+    ("int4", 4000, 2048, 48),     # one 16-row tile per workgroup
+    ("int4", 17920, 5120, 16),    # five tiles of 14 rows on each of 256 workgroups
+    ("int4", 40000, 1024, 64),    # six full tiles per workgroup, more workgroups than CUs
     ("fp8", 100, 768, 17),
-    ("fp8", 9000, 4096, 64),
+    ("fp8", 3001, 1024, 33),      # 12-row tiles, the last workgroup holding one row
+    ("fp8", 9000, 4096, 64),      # three tiles of 12 rows
 ])
-def test_batched_mfma_stream_k(backend, device, fmt, rows, cols, m):
-    """The MFMA path splits (64-row block, 256-column slice) units evenly over the
-    grid; blocks shared by several workgroups are summed from partial tiles.  Every
-    output row is checked against float64, and a second call with fewer activation
-    rows reuses the workspace."""
+def test_batched_mfma_blocks(backend, device, fmt, rows, cols, m):
+    """The MFMA path gives each workgroup a block of weight rows cut into tiles of up to
+    16 rows (padding rows computed and dropped) and splits K over its four waves, whose
+    partial tiles are summed in LDS.  Every output row is checked against float64, and
+    a second call with 16 activation rows follows on the same buffers."""
     g = rng(rows + cols + m)
     if fmt == "int4":
         packed, scales = _int4_case(g, rows, cols)

@@ -5,17 +5,12 @@
 //     activation row), so row m equals the single-row GEMV bit for bit (one int4 row
 //     goes to the single-row kernel itself);
 //   * from the threshold (int4 M >= 4, where the engine's per-row fma chains make it
-//     VALU-bound; fp8 M >= 16): MFMA, rows past M clamped to the last one.  The four
-//     waves of a workgroup own a 64-row block (16 rows each) and all M (<= 64, in
-//     tiles of 16) activation rows; per quantisation
-//     group of 128 columns each wave issues four v_mfma_f32_16x16x32_f16 with the
-//     dequantised weights as the A operand (int4: code times group scale, rounded
-//     to fp16; fp8: exact) and the activations (staged in LDS per 256-column slice)
-//     as the B operand; fp8's row scale multiplies the fp32 sum.  The (block, slice)
-//     units are split evenly over a grid of two workgroups per CU (stream-K), and
-//     blocks split between workgroups are summed in a fixed order by a second
-//     kernel.  MFMA sums products in a hardware-defined order, so this path matches
-//     the dequantise-then-matmul reference to the stated tolerance, not bit for bit.
+//     VALU-bound; fp8 M >= 16): MFMA (mfma_ksplit_kernel below): one workgroup per CU
+//     owns a block of weight rows for all M (<= 64) activation rows, its four waves
+//     split K, each reads its weight and activation fragments straight into MFMA
+//     operand registers, and the waves' fp32 tiles are summed in a fixed order at the
+//     end.  MFMA sums products in a hardware-defined order, so this path matches the
+//     dequantise-then-matmul reference to the stated tolerance, not bit for bit.
 //   * the M-row lm_head argmax runs the GEMV engine with eight activation rows per
 //     launch and one argmax key per (wave, row); a finishing kernel picks each row's
 //     token, as tt_matvec_argmax does for one row;
@@ -33,19 +28,24 @@ namespace {
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
-constexpr int kSlice = 256;   // columns of x staged in LDS per step (two int4 groups)
-constexpr int kMaxSlices = 8192 / kSlice;
-
-// LDS position (in 16-byte pieces) of activation row 16 t + i, columns 128 gs +
-// 32 g + 8 q + [0, 8) of a staged slice.  The B operand of (gs, q, t) is one read of
-// 64 consecutive pieces, lane 16 g + i taking piece i ^ (4 q + g) of its 16: any
-// group of lanes the LDS serves together reads distinct banks, and so do the 16
-// consecutive lanes of a store (one row, 16 pieces = 16 distinct (q, g)).
-__device__ __forceinline__ int x_piece(int t, int gs, int q, int g, int i) {
-  return ((t * (kSlice / 128) + gs) * 4 + q) * 64 + g * 16 + (i ^ (4 * q + g));
-}
-
 enum class WFmt : int { kInt4G128 = 0, kFp8Row = 1 };
+
+// Bytes of one weight row a lane reads per pipeline step and steps in flight per wave
+// of mfma_ksplit_kernel (measured on the MI355X: 32-byte reads and more steps in flight
+// gained nothing), and waves per SIMD of both MFMA kernels (two or four were slower).
+#define TT_KS_LB1 16   // one activation tile
+#define TT_KS_LB 16    // two or four activation tiles
+#define TT_KS_D1 2
+#define TT_KS_D 2
+#define TT_KS_WPE 1
+template <int MT> constexpr int ks_lane_bytes() { return MT == 1 ? TT_KS_LB1 : TT_KS_LB; }
+template <int MT> constexpr int ks_depth() { return MT == 1 ? TT_KS_D1 : TT_KS_D; }
+// K columns per pipeline step: a lane reads LB bytes of one weight row, a quarter of
+// the step's columns (int4: 2 LB columns, fp8: LB).
+template <WFmt W, int MT> constexpr int step_cols() {
+  return W == WFmt::kInt4G128 ? 8 * ks_lane_bytes<MT>() : 4 * ks_lane_bytes<MT>();
+}
+constexpr int kMaxNT = 6;     // 16-row tiles per workgroup
 
 struct MfmaParams {
   const uint8_t* w;
@@ -56,55 +56,31 @@ struct MfmaParams {
   int64_t x_row;
   uint16_t* out;        // fp16 [M, out_row]
   int64_t out_row;
-  float* ws;            // fp32 partial tiles [2 * grid][16 MT][64] of blocks shared by workgroups
   int m, n, k;
-  int spb;              // 256-column slices per 64-row block
-  int64_t units;        // blocks * spb
-  int grid;             // workgroups
-  int ws_row_scale;     // fold: multiply by the fp8 row scale
+  int rt;               // weight rows per 16-row MFMA tile (<= 16; rows past rt are padding)
+  int steps;            // K / step_cols
 };
 
-// Weights of one 128-column group for this lane: row n0 + lane % 16, columns
-// 128 g + 32 (lane / 16) + [0, 32).
+// A operand of MFMA q: 8 weights (one 32-bit word of int4 codes, two of fp8) as fp16.
+//   int4: (c - 8) * s rounded once to fp16 (the dequantised weight), in the order the
+//         nibble decode yields them: columns 0 4 1 5 2 6 3 7 of the word (the
+//         activations are permuted to the same order);
+//   fp8:  the exact fp16 value of each byte in column order (the row scale multiplies
+//         the fp32 sum).
 template <WFmt W>
-struct WChunk {
-  uint32_t w[W == WFmt::kInt4G128 ? 4 : 8];
-};
-
-// p: this lane's 32 columns of the group (int4: 16 bytes, fp8: 32 bytes).
-template <WFmt W>
-__device__ __forceinline__ WChunk<W> load_chunk(const uint8_t* p) {
-  WChunk<W> c;
-  if constexpr (W == WFmt::kInt4G128) {
-    const uint4 v = *reinterpret_cast<const uint4*>(p);
-    c.w[0] = v.x; c.w[1] = v.y; c.w[2] = v.z; c.w[3] = v.w;
-  } else {
-    const uint4 a = reinterpret_cast<const uint4*>(p)[0], b = reinterpret_cast<const uint4*>(p)[1];
-    c.w[0] = a.x; c.w[1] = a.y; c.w[2] = a.z; c.w[3] = a.w;
-    c.w[4] = b.x; c.w[5] = b.y; c.w[6] = b.z; c.w[7] = b.w;
-  }
-  return c;
-}
-
-// A operand of step q: the 8 weights of word q of this lane's 32 columns as fp16.
-//   int4: (c - 8) * s rounded once to fp16 (the dequantised weight), in the order
-//         the nibble decode yields them: k = 0, 4, 1, 5, 2, 6, 3, 7 of the word (the
-//         activations are staged in LDS in the same order, so the products pair up);
-//   fp8:  the exact fp16 value of each byte, natural order (row scale at the end).
-template <WFmt W>
-__device__ __forceinline__ h8 a_operand(const WChunk<W>& c, int q, h2 s2) {
+__device__ __forceinline__ h8 a_operand(const uint32_t* wd, int q, h2 s2) {
   h8 a;
   if constexpr (W == WFmt::kInt4G128) {
     h2 p0, p1, p2, p3;
-    nib_pairs(c.w[q], 8.0f, p0, p1, p2, p3);   // exact c - 8
+    nib_pairs(wd[q], 8.0f, p0, p1, p2, p3);   // exact c - 8
     p0 = p0 * s2; p1 = p1 * s2; p2 = p2 * s2; p3 = p3 * s2;
     a[0] = p0[0]; a[1] = p0[1]; a[2] = p1[0]; a[3] = p1[1];
     a[4] = p2[0]; a[5] = p2[1]; a[6] = p3[0]; a[7] = p3[1];
   } else {
 #pragma unroll
     for (int h = 0; h < 2; h++) {
-      const h2 lo = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(c.w[2 * q + h], 1.0f, false);
-      const h2 hi = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(c.w[2 * q + h], 1.0f, true);
+      const h2 lo = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(wd[2 * q + h], 1.0f, false);
+      const h2 hi = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(wd[2 * q + h], 1.0f, true);
       a[4 * h + 0] = lo[0]; a[4 * h + 1] = lo[1]; a[4 * h + 2] = hi[0]; a[4 * h + 3] = hi[1];
     }
   }
@@ -127,286 +103,433 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
-// Workgroups per CU (one wave per SIMD each) and pipeline depth (units in flight)
-// per activation tile count.  Two units in flight per workgroup already keep ~16 MB
-// of loads in flight over the chip; deeper pipelines only lengthen the start, when
-// every workgroup's first unit waits behind the whole initial burst (measured at
-// 17920 x 5120, M = 16: depth 8 -> 2 takes 28.0 -> 23.9 us).
-#ifndef TT_MFMA_TUNE
-template <int MT> constexpr int mfma_per_cu() { return 2; }
-template <bool I4, int MT> constexpr int mfma_depth() { return MT <= 3 ? 2 : (I4 ? 3 : 2); }
-#endif
-
-// Stream-K over (64-row block, 256-column slice) units: unit u is block u / spb,
-// slice u % spb; workgroup w owns units [w T / G, (w + 1) T / G) of T, so every
-// workgroup gets the same work (within one unit) whatever the block count, and the
-// grid is exactly the workgroups the chip holds at once.
-__device__ __host__ __forceinline__ int64_t unit_begin(int64_t w, int64_t units, int64_t grid) {
-  return w * units / grid;
-}
-// The workgroup whose range holds unit u.
-__device__ __forceinline__ int64_t unit_owner(int64_t u, int64_t units, int64_t grid) {
-  return ((u + 1) * grid - 1) / units;
-}
-
-template <WFmt W, int MT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(mfma_per_cu<MT>()))) void mfma_gemm_kernel(MfmaParams P) {
-  // Software pipeline of depth D units, held in registers:
-  //   * the weights (and int4 group scales) and the activations of unit i are both
-  //     requested D units before i computes (vector loads complete in issue order,
-  //     so a load issued later than another can never be waited for earlier: both
-  //     streams get the same lead);
-  //   * the activations of unit i + 1 go from registers to one of two LDS buffers at
-  //     the end of unit i;
-  //   * barriers order LDS only, so the global loads stay in flight across them;
-  //   * the pipeline runs on across block boundaries: at the last unit of a block
-  //     (or of the workgroup's range) the tile is written out and the accumulators
-  //     restart.  A block that lies inside one workgroup's range is stored as fp16;
-  //     a block shared by several workgroups leaves one fp32 partial tile per
-  //     workgroup, summed in workgroup order by mfma_fold_kernel.
-  // int4 weights enter the MFMA already scaled (fp16), so every product of a row
-  // accumulates into one fp32 tile; with a single activation tile the accumulation
-  // alternates between two tiles (summed at the end) to halve the dependency chain.
+// y[m][n] = sum_k W[n][k] x[m][k] on v_mfma_f32_16x16x32_f16, the weights as the A
+// operand (rows n) and the activations as the B operand (columns m).
+//
+//   * Workgroup b owns NT tiles of rt weight rows each (rows b NT rt ..), every
+//     activation row (MT tiles of 16) and the whole K axis; the host picks NT and rt so
+//     that the blocks cover N with one workgroup per CU (17920 rows on 256 CUs: five
+//     tiles of 14 rows).  Rows past rt in a tile are padding: their lanes load a
+//     duplicate of the tile's last row and their outputs are not stored.
+//   * The four waves split K: wave w takes steps [w S / 4, (w + 1) S / 4).  In a step,
+//     lane l reads LB bytes of weight row l % 16 of every tile (columns of quarter l / 16
+//     of the step) and the matching activation columns of row l % 16 of every
+//     activation tile, straight into MFMA operand registers: no LDS staging, and no
+//     operand is read twice inside the workgroup (the activations come from L2; every
+//     workgroup reads all of x once).  Each activation fragment feeds NT MFMAs and each
+//     dequantised weight fragment MT.
+//   * D steps of loads are in flight per wave (the weights and activations of step
+//     i + D requested right after step i computes; vector loads complete in issue
+//     order, so both streams get the same lead).
+//   * At the end the waves' fp32 tiles are summed through LDS in a fixed order,
+//     w0 + (w1 + (w2 + w3)), times the fp8 row scale, and stored as fp16: one launch,
+//     no workspace, and a result independent of timing.
+// MFMA sums products in a hardware-defined order, so this path matches the
+// dequantise-then-matmul reference to the stated tolerance, not bit for bit.
+template <WFmt W, int MT, int NT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TT_KS_WPE, TT_KS_WPE)))
+void mfma_ksplit_kernel(MfmaParams P) {
   constexpr bool kI4 = W == WFmt::kInt4G128;
-  constexpr int kAhead = mfma_depth<kI4, MT>();
-  constexpr int NA = MT == 1 ? 2 : 1;                  // accumulator tiles per activation tile
-  constexpr int XS = MT * 16 * kSlice;                 // halves per buffer
-  constexpr int XV = MT * 16 * kSlice / 8 / 256;       // 16-byte pieces per thread per slice
-  constexpr int GPS = kSlice / 128;                    // quantisation groups per slice
-  __shared__ __attribute__((aligned(16))) uint16_t xs[2 * XS];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int g = lane >> 4;
-  const int spb = P.spb;
-  const int64_t u0 = unit_begin(blockIdx.x, P.units, P.grid);
-  const int count = (int)(unit_begin(blockIdx.x + 1, P.units, P.grid) - u0);
-  const int first_block = (int)(u0 / spb);
-  // cursors: the unit computed (cb, cs) and the unit loaded next (lb, ls, li);
-  // loads past the range repeat its last unit, so every load is unconditional and
-  // the compiler keeps exact outstanding-load counts across the unrolled pipeline
-  int cb = first_block, cs = (int)(u0 - (int64_t)first_block * spb);
-  int lb = cb, ls = cs, li = 0;
-  // load pointers of the lane: weight row of block lb at slice ls (and its group
-  // scales); stepped by one slice per unit, recomputed at block changes
-  constexpr int kSliceBytes = kI4 ? kSlice / 2 : kSlice;
-  const int lane_col = (kI4 ? 16 : 32) * g;
-  const uint8_t* wp;
-  const uint16_t* sp;
-  auto row_ptrs = [&]() __attribute__((always_inline)) {
-    int row = lb * 64 + wave * 16 + (lane & 15);
+  constexpr int LB = ks_lane_bytes<MT>();
+  constexpr int D = ks_depth<MT>();
+  constexpr int kSC = step_cols<W, MT>();
+  constexpr int kLC = kSC / 4;             // columns per lane and step
+  constexpr int kNQ = kLC / 8;             // MFMAs per (tile, activation tile) and step
+  constexpr int kRB = kI4 ? kSC / 2 : kSC; // weight bytes per row and step
+  constexpr int kWV = LB / 16;             // 16-byte weight loads per tile and step
+  constexpr int kXV = kLC / 8;             // 16-byte activation loads per activation tile and step
+  static_assert(kRB == 4 * LB, "a lane reads a quarter of the step's row bytes");
+  __shared__ float red[NT * MT * 4 * 64];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int r = lane & 15, q4 = lane >> 4;
+  const int s0 = wave * P.steps / 4;
+  const int cnt = (wave + 1) * P.steps / 4 - s0;
+  const int rt = P.rt;
+  const int64_t row0 = (int64_t)blockIdx.x * NT * rt;
+
+  const uint8_t* wp[NT];
+  const uint16_t* sp[NT];
+#pragma unroll
+  for (int t = 0; t < NT; t++) {
+    int64_t row = row0 + t * rt + (r < rt ? r : rt - 1);
     row = row < P.n ? row : P.n - 1;
-    wp = P.w + (int64_t)row * P.w_row + ls * kSliceBytes + lane_col;
-    if constexpr (kI4) sp = static_cast<const uint16_t*>(P.s) + (int64_t)row * P.s_row + ls * GPS;
-  };
-  row_ptrs();
-  auto advance_load = [&]() __attribute__((always_inline)) {
-    if (li < count - 1) {
-      li++;
-      if (++ls == spb) {
-        ls = 0;
-        lb++;
-        row_ptrs();
-      } else {
-        wp += kSliceBytes;
-        if constexpr (kI4) sp += GPS;
-      }
-    }
-  };
-  // activation slot u: xq_even / xq_odd[(u / 2) * XV + v] (two arrays: smaller
-  // private arrays are the ones the compiler keeps in registers)
-  uint4 xq_even[(kAhead + 1) / 2 * XV], xq_odd[(kAhead + 1) / 2 * XV];
-  const uint16_t* xb[XV];                              // row min(r, m - 1), columns 8 c8 .. of slice 0
-#pragma unroll
-  for (int v = 0; v < XV; v++) {
-    const int i = threadIdx.x + 256 * v;
-    int r = i / (kSlice / 8);
-    const int c8 = i - r * (kSlice / 8);
-    r = r < P.m ? r : P.m - 1;
-    xb[v] = P.x + (int64_t)r * P.x_row + 8 * c8;
+    wp[t] = P.w + row * P.w_row + (int64_t)s0 * kRB + q4 * LB;
+    // int4: the lane's columns lie in group (step * kSC + q4 * kLC) / 128
+    if constexpr (kI4) sp[t] = static_cast<const uint16_t*>(P.s) + row * P.s_row + (s0 * kSC + q4 * kLC) / 128;
   }
-  auto load_x = [&](int sl, auto uc) __attribute__((always_inline)) {
-    constexpr int u = decltype(uc)::value;
+  const uint16_t* xp[MT];
 #pragma unroll
-    for (int v = 0; v < XV; v++) {
-      const uint4 t = *reinterpret_cast<const uint4*>(xb[v] + sl * kSlice);
-      if constexpr ((u & 1) == 0) xq_even[u / 2 * XV + v] = t;
-      else xq_odd[u / 2 * XV + v] = t;
-    }
-  };
-  auto store_x = [&](int buf, auto uc) __attribute__((always_inline)) {
-    constexpr int u = decltype(uc)::value;
+  for (int mt = 0; mt < MT; mt++) {
+    const int m = 16 * mt + r < P.m ? 16 * mt + r : P.m - 1;
+    xp[mt] = P.x + (int64_t)m * P.x_row + (int64_t)s0 * kSC + q4 * kLC;
+  }
+  // fp8: the row scales of the lane's output rows, requested first (clamped rows: every
+  // load unconditional, so none of them waits in the epilogue)
+  float rs[kI4 ? 1 : NT][4];
+  if constexpr (!kI4) {
 #pragma unroll
-    for (int v = 0; v < XV; v++) {
-      const int i = threadIdx.x + 256 * v;
-      const int r = i / (kSlice / 8), c8 = i - r * (kSlice / 8);
-      uint4 t = (u & 1) == 0 ? xq_even[u / 2 * XV + v] : xq_odd[u / 2 * XV + v];
-      if constexpr (kI4) t = nib_order(t);
-      const int cc = c8 & 15;
-      *reinterpret_cast<uint4*>(xs + buf * XS + 8 * x_piece(r >> 4, c8 >> 4, cc & 3, cc >> 2, r & 15)) = t;
-    }
-  };
-  WChunk<W> ring[kAhead][GPS];
-  uint32_t sring[kI4 ? kAhead : 1];                    // int4: the row's two group scales (fp16 pair)
-  auto load_unit = [&](auto uc) __attribute__((always_inline)) {
-    constexpr int u = decltype(uc)::value;
-#pragma unroll
-    for (int gs = 0; gs < GPS; gs++) ring[u][gs] = load_chunk<W>(wp + gs * (kSliceBytes / GPS));
-    if constexpr (kI4) sring[u] = *reinterpret_cast<const uint32_t*>(sp);
-    load_x(ls, uc);
-  };
-  f4 acc[NA][MT];
-#pragma unroll
-  for (int j = 0; j < NA; j++)
-#pragma unroll
-    for (int t = 0; t < MT; t++) acc[j][t] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
-  // prologue: units 0 .. kAhead - 1 in the order every step issues its loads (the
-  // wait for unit i + 1's activations is then as shallow in the first loop
-  // iteration as in later ones, and the first store waits for unit 0 only)
-  static_for<0, kAhead>([&](auto uc) __attribute__((always_inline)) {
-    load_unit(uc);
-    advance_load();
-  });
-  store_x(0, std::integral_constant<int, 0>{});
-  lds_barrier();
-
-  // lane holds output rows b * 64 + wave * 16 + 4 g + i of activation row 16 t + lane % 16
-  auto flush = [&](int b) __attribute__((always_inline)) {
-    if constexpr (NA == 2) {
+    for (int t = 0; t < NT; t++)
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        acc[0][0][i] = acc[0][0][i] + acc[1][0][i];
-        acc[1][0][i] = 0.0f;
+        int64_t row = row0 + t * rt + (4 * q4 + i < rt ? 4 * q4 + i : rt - 1);
+        row = row < P.n ? row : P.n - 1;
+        rs[t][i] = static_cast<const float*>(P.s)[row];
+      }
+  }
+
+  uint4 wr[D][NT][kWV];
+  uint16_t sr[D][NT];
+  uint4 xr[D][MT][kXV];
+  auto load = [&](auto uc, int i) __attribute__((always_inline)) {
+    constexpr int u = decltype(uc)::value;
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+#pragma unroll
+      for (int v = 0; v < kWV; v++) wr[u][t][v] = *reinterpret_cast<const uint4*>(wp[t] + (int64_t)i * kRB + 16 * v);
+      if constexpr (kI4) sr[u][t] = sp[t][i * kSC / 128];
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+      for (int v = 0; v < kXV; v++) xr[u][mt][v] = *reinterpret_cast<const uint4*>(xp[mt] + (int64_t)i * kSC + 8 * v);
+  };
+
+  f4 acc[NT][MT];
+#pragma unroll
+  for (int t = 0; t < NT; t++)
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) acc[t][mt] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
+
+  auto compute = [&](auto uc) __attribute__((always_inline)) {
+    constexpr int u = decltype(uc)::value;
+    h2 s2[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+      if constexpr (kI4) {
+        const _Float16 sv = __builtin_bit_cast(_Float16, sr[u][t]);
+        s2[t] = (h2){sv, sv};
+      } else {
+        s2[t] = (h2){};
       }
     }
-    const int64_t bu = (int64_t)b * spb;
-    const int r0 = b * 64 + wave * 16 + 4 * g;
-    if (bu >= u0 && bu + spb <= u0 + count) {
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int r = r0 + i;
-        if (r >= P.n) continue;
-        float rs = 1.0f;
-        if constexpr (W == WFmt::kFp8Row) rs = reinterpret_cast<const float*>(P.s)[r];
+    for (int q = 0; q < kNQ; q++) {
+      h8 b[MT];
 #pragma unroll
-        for (int t = 0; t < MT; t++) {
-          const int m = 16 * t + (lane & 15);
-          if (m < P.m) {
-            const float v = W == WFmt::kFp8Row ? acc[0][t][i] * rs : acc[0][t][i];
-            P.out[(int64_t)m * P.out_row + r] = f32_to_f16_bits(v);
+      for (int mt = 0; mt < MT; mt++) b[mt] = __builtin_bit_cast(h8, kI4 ? nib_order(xr[u][mt][q]) : xr[u][mt][q]);
+#pragma unroll
+      for (int t = 0; t < NT; t++) {
+        const uint32_t* wd = reinterpret_cast<const uint32_t*>(&wr[u][t][0]);
+        const h8 a = a_operand<W>(wd, q, s2[t]);
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) acc[t][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b[mt], acc[t][mt], 0, 0, 0);
+      }
+    }
+  };
+
+  // Every load in the pipeline is unconditional (steps past the range repeat the last
+  // one, a cache hit), so the outstanding-load count is the same on every path and
+  // each wait leaves the later steps' loads in flight.
+  if (cnt > 0) {
+    static_for<0, D>([&](auto uc) __attribute__((always_inline)) {
+      load(uc, decltype(uc)::value < cnt ? decltype(uc)::value : cnt - 1);
+    });
+    int i0 = 0;
+    for (; i0 + D <= cnt; i0 += D) {
+      static_for<0, D>([&](auto uc) __attribute__((always_inline)) {
+        compute(uc);
+        const int nxt = i0 + decltype(uc)::value + D;
+        load(uc, nxt < cnt ? nxt : cnt - 1);
+      });
+    }
+    static_for<0, D - 1>([&](auto uc) __attribute__((always_inline)) {
+      if (i0 + decltype(uc)::value < cnt) compute(uc);
+    });
+  }
+
+  // waves 3, 2, 1 leave running sums in LDS (the same lane and register positions in
+  // every wave hold the same output element); wave 0 adds its own and stores
+#pragma unroll
+  for (int w = 3; w >= 1; w--) {
+    if (wave == w) {
+#pragma unroll
+      for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            float* p = red + ((t * MT + mt) * 4 + i) * 64 + lane;
+            *p = w == 3 ? acc[t][mt][i] : acc[t][mt][i] + *p;
           }
-        }
+    }
+    __syncthreads();
+  }
+  if (wave != 0) return;
+  // lane holds rows 4 q4 + i of tile t, activation row 16 mt + r
+#pragma unroll
+  for (int t = 0; t < NT; t++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int tr = 4 * q4 + i;
+      const int64_t row = row0 + t * rt + tr;
+      if (tr >= rt || row >= P.n) continue;
+#pragma unroll
+      for (int mt = 0; mt < MT; mt++) {
+        const int m = 16 * mt + r;
+        if (m >= P.m) continue;
+        float v = acc[t][mt][i] + red[((t * MT + mt) * 4 + i) * 64 + lane];
+        if constexpr (!kI4) v = v * rs[t][i];
+        P.out[(int64_t)m * P.out_row + row] = f32_to_f16_bits(v);
       }
-    } else {
-      // partial tile [16 MT][64] in slot 2 w + (0: the range's first block, 1: its last)
-      float* tile = P.ws + (int64_t)(2 * blockIdx.x + (b == first_block ? 0 : 1)) * (16 * MT * 64);
-#pragma unroll
-      for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int t = 0; t < MT; t++) tile[(16 * t + (lane & 15)) * 64 + wave * 16 + 4 * g + i] = acc[0][t][i];
     }
-#pragma unroll
-    for (int t = 0; t < MT; t++) acc[0][t] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
-  };
-
-  auto step = [&](int i, auto uc) __attribute__((always_inline)) {
-    constexpr int u = decltype(uc)::value;
-    const uint16_t* xl = xs + (i & 1) * XS;
-    // this lane's row scales of the unit's two groups, as (s, s) pairs
-    h2 s2[GPS];
-    if constexpr (kI4) {
-      const h2 sp = __builtin_bit_cast(h2, sring[u]);
-#pragma unroll
-      for (int gs = 0; gs < GPS; gs++) s2[gs] = (h2){sp[gs], sp[gs]};
-    }
-    // B operands of a group are read from LDS together, the next group's while the
-    // current one's MFMAs run
-    h8 bb[GPS][4][MT];
-    auto read_b = [&](int gs) __attribute__((always_inline)) {
-#pragma unroll
-      for (int q = 0; q < 4; q++)
-#pragma unroll
-        for (int t = 0; t < MT; t++)
-          bb[gs][q][t] = *reinterpret_cast<const h8*>(xl + 8 * x_piece(t, gs, q, g, lane & 15));
-    };
-    read_b(0);
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int gs = 0; gs < GPS; gs++) {
-      if (gs + 1 < GPS) read_b(gs + 1);
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const h8 a = a_operand<W>(ring[u][gs], q, kI4 ? s2[gs] : (h2){});
-#pragma unroll
-        for (int t = 0; t < MT; t++) {
-          f4& d = acc[NA == 2 ? (q & 1) : 0][t];
-          d = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bb[gs][q][t], d, 0, 0, 0);
-        }
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    if (cs == spb - 1 || i == count - 1) flush(cb);
-    if (++cs == spb) { cs = 0; cb++; }
-    load_unit(uc);                                                   // slot u held unit i, stored a step ago
-    advance_load();
-    store_x((i + 1) & 1, std::integral_constant<int, (u + 1) % kAhead>{});  // unit i + 1
-    lds_barrier();
-  };
-  int i0 = 0;
-  for (; i0 + kAhead <= count; i0 += kAhead)
-    static_for<0, kAhead>([&](auto uc) __attribute__((always_inline)) { step(i0 + decltype(uc)::value, uc); });
-  // tail: fewer than kAhead units, still with static ring slots
-  static_for<0, kAhead - 1>([&](auto uc) __attribute__((always_inline)) {
-    if (i0 + decltype(uc)::value < count) step(i0 + decltype(uc)::value, uc);
-  });
 }
 
-// out[m][n] of the blocks that several workgroups share: the partial tiles summed in
-// workgroup order (((+0 + first) + second) + ...) [times the fp8 row scale], so the
-// result does not depend on which workgroup finished first.  Workgroup w of this
-// kernel takes the block holding unit_begin(w) when w is the first range boundary
-// inside that block.
-__global__ __launch_bounds__(256) void mfma_fold_kernel(MfmaParams P, int mp) {
-  const int64_t w = (int64_t)blockIdx.x + 1;
-  const int spb = P.spb;
-  const int64_t uw = unit_begin(w, P.units, P.grid);
-  const int64_t b = uw / spb, bu = b * spb;
-  if (uw == bu || unit_begin(w - 1, P.units, P.grid) > bu) return;
-  // partial tiles of the block in workgroup order: workgroups w - 1 .. last
-  __shared__ int slot[kMaxSlices + 1];
-  const int n_slots = (int)(unit_owner(bu + spb - 1, P.units, P.grid) - (w - 1) + 1);
-  if (threadIdx.x < n_slots) {
-    const int64_t o = w - 1 + threadIdx.x;
-    slot[threadIdx.x] = (int)(2 * o + (b == unit_begin(o, P.units, P.grid) / spb ? 0 : 1));
-  }
-  __syncthreads();
-  const float* rsc = P.ws_row_scale ? reinterpret_cast<const float*>(P.s) : nullptr;
-  // kE elements per thread and step with every partial of up to kJ slots requested before
-  // the first sum (one memory round trip per step instead of one per element and slot);
-  // slots past kJ (blocks shared by more workgroups) are added one at a time after them
-  constexpr int kE = 4, kJ = 4;
-  for (int e0 = threadIdx.x; e0 < mp * 64; e0 += 256 * kE) {
-    float p[kJ][kE];
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ u32x4 nib_order4(u32x4 v) {
+  return (u32x4){__builtin_amdgcn_perm(v[2], v[0], 0x05040100u), __builtin_amdgcn_perm(v[2], v[0], 0x07060302u),
+                 __builtin_amdgcn_perm(v[3], v[1], 0x05040100u), __builtin_amdgcn_perm(v[3], v[1], 0x07060302u)};
+}
+
+// ---------------------------------------------------------------- MFMA, LDS-staged operands
+// The same block / K-split decomposition as mfma_ksplit_kernel, with both operands
+// loaded coalesced and transposed through a per-wave LDS buffer instead of straight
+// into operand registers.  A direct load in MFMA layout gives the 16 lanes of a pass
+// 16 different rows, which the address unit serves one row at a time; here every quad
+// of lanes reads 64 contiguous bytes of one row into registers (D steps ahead), the
+// wave writes a step's pieces to its LDS buffer (swizzled so that the fragment reads
+// are free of bank conflicts, up to two-way for the int4 weights) and reads its MFMA
+// fragments back.  A wave's LDS reads and writes execute in order, so the buffer needs
+// no barrier; the waves share nothing until the final sum.
+//
+// A step covers 64 columns of K.  Per wave and step: the weight rows of the NT tiles
+// (int4: 32 bytes a row, fp8: 64) and 64 columns of every activation row; lane
+// (r = l % 16, q4 = l / 16) owns columns [16 q4, 16 q4 + 16) of the step, MFMA q of the
+// step (q = 0, 1) the eight columns 16 q4 + 8 q ..  Steps past a wave's range repeat its
+// last step, so every load is unconditional.
+// steps in flight per wave (one activation tile / more)
+#define TT_LDS_D1 3
+#define TT_LDS_D 2
+template <WFmt W, int MT, int NT> struct LdsGeom {
+  static constexpr bool kI4 = W == WFmt::kInt4G128;
+  static constexpr int kSC = 64;                        // K columns per step
+  static constexpr int kWRB = kI4 ? 32 : 64;            // weight bytes per row and step
+  static constexpr int kWP = NT * 16 * kWRB / 16;       // 16-byte weight pieces per step
+  static constexpr int kWI = (kWP + 63) / 64;           // weight loads per lane and step
+  static constexpr int kXI = 2 * MT;                    // activation loads per lane and step
+  static constexpr int kBuf = (kWI + kXI) * 1024;       // LDS bytes per wave
+  static constexpr int D = MT == 1 ? TT_LDS_D1 : TT_LDS_D;
+  static constexpr int kRed = NT * MT * 4 * 64 * 4;     // bytes of the cross-wave sum
+  static constexpr int kLds = (4 * kBuf > kRed ? 4 * kBuf : kRed);
+};
+
+template <WFmt W, int MT, int NT>
+__global__ __launch_bounds__(256) void mfma_lds_kernel(MfmaParams P) {
+  using G = LdsGeom<W, MT, NT>;
+  constexpr bool kI4 = G::kI4;
+  constexpr int D = G::D;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[G::kLds];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int r = lane & 15, q4 = lane >> 4;
+  const int s0 = wave * P.steps / 4;
+  const int cnt = (wave + 1) * P.steps / 4 - s0;
+  const int rt = P.rt;
+  const int64_t row0 = (int64_t)blockIdx.x * NT * rt;
+  // the wave's buffer as an LDS-space pointer: stores through it cannot alias the
+  // private arrays (a generic pointer would force them into scratch memory)
+  typedef __attribute__((address_space(3))) uint8_t lds_u8;
+  lds_u8* const buf = reinterpret_cast<lds_u8*>(reinterpret_cast<uintptr_t>(lds)) + wave * G::kBuf;
+
+  // ---- load sources (step 0 of the wave; + i * step bytes) and LDS destinations
+  // weights: piece f = v * 64 + lane of the step's block (rows of all tiles in order)
+  const uint8_t* wsrc[G::kWI];
+  int wdst[G::kWI];
 #pragma unroll
-    for (int j = 0; j < kJ; j++)
-#pragma unroll
-      for (int u = 0; u < kE; u++) {
-        const int e = e0 + 256 * u;
-        p[j][u] = (j < n_slots && e < mp * 64) ? P.ws[((int64_t)slot[j] * mp + (e >> 6)) * 64 + (e & 63)] : 0.0f;
-      }
-#pragma unroll
-    for (int u = 0; u < kE; u++) {
-      const int e = e0 + 256 * u;
-      const int mi = e >> 6, c = e & 63;
-      const int64_t r = b * 64 + c;
-      if (e >= mp * 64 || mi >= P.m || r >= P.n) continue;
-      float v = 0.0f;
-#pragma unroll
-      for (int j = 0; j < kJ; j++)
-        if (j < n_slots) v = v + p[j][u];
-      for (int j = kJ; j < n_slots; j++) v = v + P.ws[((int64_t)slot[j] * mp + mi) * 64 + c];
-      if (rsc) v = v * rsc[r];
-      P.out[(int64_t)mi * P.out_row + r] = f32_to_f16_bits(v);
+  for (int v = 0; v < G::kWI; v++) {
+    const int f0 = v * 64 + lane;
+    const int f = f0 < G::kWP ? f0 : G::kWP - 1;        // the last load's spare lanes repeat a piece
+    int R, c, pc;
+    if constexpr (kI4) {              // 32-byte rows: two pieces, swapped on row bit 2
+      R = f >> 1;
+      c = f & 1;
+      pc = c ^ ((R >> 2) & 1);
+    } else {                          // 64-byte rows: four pieces, xor-swizzled on row bits 1-2
+      R = f >> 2;
+      c = f & 3;
+      pc = c ^ ((R >> 1) & 3);
     }
+    const int t = R >> 4, rr = R & 15;
+    int64_t row = row0 + t * rt + (rr < rt ? rr : rt - 1);
+    row = row < P.n ? row : P.n - 1;
+    wsrc[v] = P.w + row * P.w_row + (int64_t)s0 * G::kWRB + 16 * c;
+    wdst[v] = R * G::kWRB + 16 * pc;
   }
+  // activations: load v = 2 mt + h covers rows 8 h .. 8 h + 7 of tile mt, eight 16-byte
+  // pieces a row, xor-swizzled on the row's low three bits
+  const uint16_t* xsrc[G::kXI];
+  int xdst[G::kXI];
+#pragma unroll
+  for (int v = 0; v < G::kXI; v++) {
+    const int mt = v >> 1;
+    const int rr = 8 * (v & 1) + (lane >> 3);
+    const int c = lane & 7;
+    const int m = 16 * mt + rr < P.m ? 16 * mt + rr : P.m - 1;
+    xsrc[v] = P.x + (int64_t)m * P.x_row + (int64_t)s0 * G::kSC + 8 * c;
+    xdst[v] = G::kWI * 1024 + mt * 2048 + rr * 128 + 16 * (c ^ (rr & 7));
+  }
+  // int4 group scale of the lane's row in every tile (group (s0 + i) / 2 at step i)
+  const uint16_t* sp[NT];
+#pragma unroll
+  for (int t = 0; t < NT; t++) {
+    int64_t row = row0 + t * rt + (r < rt ? r : rt - 1);
+    row = row < P.n ? row : P.n - 1;
+    if constexpr (kI4) sp[t] = static_cast<const uint16_t*>(P.s) + row * P.s_row;
+    else sp[t] = nullptr;
+  }
+  float rs[kI4 ? 1 : NT][4];
+  if constexpr (!kI4) {
+#pragma unroll
+    for (int t = 0; t < NT; t++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        int64_t row = row0 + t * rt + (4 * q4 + i < rt ? 4 * q4 + i : rt - 1);
+        row = row < P.n ? row : P.n - 1;
+        rs[t][i] = static_cast<const float*>(P.s)[row];
+      }
+  }
+
+  u32x4 wst[D][G::kWI], xst[D][G::kXI];
+  uint16_t sr[D][NT];
+  auto issue = [&](auto uc, int i) __attribute__((always_inline)) {
+    constexpr int u = decltype(uc)::value;
+#pragma unroll
+    for (int v = 0; v < G::kWI; v++) wst[u][v] = *reinterpret_cast<const u32x4*>(wsrc[v] + (int64_t)i * G::kWRB);
+#pragma unroll
+    for (int v = 0; v < G::kXI; v++) xst[u][v] = *reinterpret_cast<const u32x4*>(xsrc[v] + (int64_t)i * G::kSC);
+    if constexpr (kI4) {
+#pragma unroll
+      for (int t = 0; t < NT; t++) sr[u][t] = sp[t][(s0 + i) >> 1];
+    }
+  };
+
+  f4 acc[NT][MT];
+#pragma unroll
+  for (int t = 0; t < NT; t++)
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) acc[t][mt] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
+
+  // fragment offsets in the buffer
+  const int wfrag = kI4 ? r * 32 + 16 * ((q4 >> 1) ^ ((r >> 2) & 1)) + 8 * (q4 & 1)
+                        : r * 64 + 16 * (q4 ^ ((r >> 1) & 3));
+  const int xfrag0 = G::kWI * 1024 + r * 128 + 16 * ((2 * q4) ^ (r & 7));
+  const int xfrag1 = G::kWI * 1024 + r * 128 + 16 * ((2 * q4 + 1) ^ (r & 7));
+
+  auto compute = [&](auto uc) __attribute__((always_inline)) {
+    constexpr int u = decltype(uc)::value;
+#pragma unroll
+    for (int v = 0; v < G::kWI; v++) *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(buf + wdst[v]) = wst[u][v];
+#pragma unroll
+    for (int v = 0; v < G::kXI; v++) *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(buf + xdst[v]) = xst[u][v];
+    uint32_t wd[NT][4];
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+      if constexpr (kI4) {
+        const u32x2 v = *reinterpret_cast<const __attribute__((address_space(3))) u32x2*>(buf + t * 512 + wfrag);
+        wd[t][0] = v[0]; wd[t][1] = v[1]; wd[t][2] = 0; wd[t][3] = 0;
+      } else {
+        const u32x4 v = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(buf + t * 1024 + wfrag);
+        wd[t][0] = v[0]; wd[t][1] = v[1]; wd[t][2] = v[2]; wd[t][3] = v[3];
+      }
+    }
+    u32x4 xf[MT][2];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) {
+      xf[mt][0] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(buf + mt * 2048 + xfrag0);
+      xf[mt][1] = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(buf + mt * 2048 + xfrag1);
+    }
+    h2 s2[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+      if constexpr (kI4) {
+        const _Float16 sv = __builtin_bit_cast(_Float16, sr[u][t]);
+        s2[t] = (h2){sv, sv};
+      } else {
+        s2[t] = (h2){};
+      }
+    }
+    // every operand of the step is formed before the first MFMA: a VALU write to a
+    // register that an issued MFMA still reads waits for that MFMA, so operand
+    // registers are not reused inside the step
+    h8 bo[2][MT], ao[2][NT];
+#pragma unroll
+    for (int q = 0; q < 2; q++) {
+#pragma unroll
+      for (int mt = 0; mt < MT; mt++) bo[q][mt] = __builtin_bit_cast(h8, kI4 ? nib_order4(xf[mt][q]) : xf[mt][q]);
+#pragma unroll
+      for (int t = 0; t < NT; t++) ao[q][t] = a_operand<W>(wd[t], q, s2[t]);
+    }
+#pragma unroll
+    for (int q = 0; q < 2; q++)
+#pragma unroll
+      for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+          acc[t][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ao[q][t], bo[q][mt], acc[t][mt], 0, 0, 0);
+  };
+
+  if (cnt > 0) {
+    static_for<0, D>([&](auto uc) __attribute__((always_inline)) {
+      issue(uc, decltype(uc)::value < cnt ? decltype(uc)::value : cnt - 1);
+    });
+    int i0 = 0;
+    for (; i0 + D <= cnt; i0 += D) {
+      static_for<0, D>([&](auto uc) __attribute__((always_inline)) {
+        compute(uc);
+        const int nxt = i0 + decltype(uc)::value + D;
+        issue(uc, nxt < cnt ? nxt : cnt - 1);
+      });
+    }
+    static_for<0, D - 1>([&](auto uc) __attribute__((always_inline)) {
+      if (i0 + decltype(uc)::value < cnt) compute(uc);
+    });
+  }
+  __syncthreads();   // every wave is done with its buffer: the sum reuses the space
+
+  float* red = reinterpret_cast<float*>(lds);
+#pragma unroll
+  for (int w = 3; w >= 1; w--) {
+    if (wave == w) {
+#pragma unroll
+      for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            float* p = red + ((t * MT + mt) * 4 + i) * 64 + lane;
+            *p = w == 3 ? acc[t][mt][i] : acc[t][mt][i] + *p;
+          }
+    }
+    __syncthreads();
+  }
+  if (wave != 0) return;
+#pragma unroll
+  for (int t = 0; t < NT; t++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int tr = 4 * q4 + i;
+      const int64_t row = row0 + t * rt + tr;
+      if (tr >= rt || row >= P.n) continue;
+#pragma unroll
+      for (int mt = 0; mt < MT; mt++) {
+        const int m = 16 * mt + r;
+        if (m >= P.m) continue;
+        float v = acc[t][mt][i] + red[((t * MT + mt) * 4 + i) * 64 + lane];
+        if constexpr (!kI4) v = v * rs[t][i];
+        P.out[(int64_t)m * P.out_row + row] = f32_to_f16_bits(v);
+      }
+    }
 }
 
 inline int device_cus() {
@@ -420,41 +543,72 @@ inline int device_cus() {
   return cus[dev];
 }
 
-// Workgroups of the stream-K grid: the workgroups the chip holds at once, at most
-// one per unit.
-inline int64_t mfma_grid(int64_t units, int mt) {
-  static constexpr int per_cu[4] = {mfma_per_cu<1>(), mfma_per_cu<2>(), mfma_per_cu<3>(), mfma_per_cu<4>()};
-  return std::min<int64_t>((int64_t)per_cu[mt - 1] * device_cus(), units);
+// Tiles per workgroup (nt <= kMaxNT) and rows per tile (rt <= 16): the fewest rows per
+// workgroup that cover N with one workgroup per CU, cut into as few tiles as hold them.
+struct MfmaPlan {
+  int nt, rt;
+  int64_t blocks;
+};
+inline MfmaPlan mfma_plan(int64_t n, int cus) {
+  const int64_t per = (n + cus - 1) / cus;
+  MfmaPlan p;
+  p.nt = (int)std::min<int64_t>(kMaxNT, std::max<int64_t>(1, (per + 15) / 16));
+  p.rt = (int)std::min<int64_t>(16, (per + p.nt - 1) / p.nt);
+  p.blocks = (n + (int64_t)p.nt * p.rt - 1) / ((int64_t)p.nt * p.rt);
+  return p;
 }
 
-inline int64_t mfma_ws_floats(int64_t m, int64_t rows, int64_t cols) {
-  const int mt = (int)((m + 15) / 16);
-  const int64_t units = (rows + 63) / 64 * (cols / kSlice);
-  return 2 * mfma_grid(units, mt) * 16 * mt * 64;
+template <WFmt W, int MT, int NT>
+int launch_lds(const MfmaParams& P, const dim3& grid, hipStream_t st) {
+  hipLaunchKernelGGL((mfma_lds_kernel<W, MT, NT>), grid, dim3(256), 0, st, P);
+  return TT_OK;
+}
+
+// int4 with one activation tile runs the register-direct kernel (its per-step VALU
+// work, not the address unit, bounds it: 22.8 against 24.4 us at 17920 x 5120, M = 16);
+// everything else the LDS-staged one (int4 M = 64: 44.3 -> 40.8 us, fp8 M = 16 / 64:
+// 31.2 -> 26.7 / 47.7 -> 40.9 us).
+template <WFmt W, int MT> constexpr bool use_lds_kernel() { return !(W == WFmt::kInt4G128 && MT == 1); }
+
+template <WFmt W, int MT>
+int launch_mfma_mt(const MfmaParams& P, int nt, const dim3& grid, hipStream_t st) {
+  if constexpr (use_lds_kernel<W, MT>()) {
+    switch (nt) {
+      case 1: return launch_lds<W, MT, 1>(P, grid, st);
+      case 2: return launch_lds<W, MT, 2>(P, grid, st);
+      case 3: return launch_lds<W, MT, 3>(P, grid, st);
+      case 4: return launch_lds<W, MT, 4>(P, grid, st);
+      case 5: return launch_lds<W, MT, 5>(P, grid, st);
+      default: return launch_lds<W, MT, 6>(P, grid, st);
+    }
+  } else {
+    switch (nt) {
+      case 1: hipLaunchKernelGGL((mfma_ksplit_kernel<W, MT, 1>), grid, dim3(256), 0, st, P); break;
+      case 2: hipLaunchKernelGGL((mfma_ksplit_kernel<W, MT, 2>), grid, dim3(256), 0, st, P); break;
+      case 3: hipLaunchKernelGGL((mfma_ksplit_kernel<W, MT, 3>), grid, dim3(256), 0, st, P); break;
+      case 4: hipLaunchKernelGGL((mfma_ksplit_kernel<W, MT, 4>), grid, dim3(256), 0, st, P); break;
+      case 5: hipLaunchKernelGGL((mfma_ksplit_kernel<W, MT, 5>), grid, dim3(256), 0, st, P); break;
+      default: hipLaunchKernelGGL((mfma_ksplit_kernel<W, MT, 6>), grid, dim3(256), 0, st, P); break;
+    }
+  }
+  return TT_OK;
 }
 
 template <WFmt W>
-int launch_mfma(MfmaParams P, float* ws, int64_t ws_floats, hipStream_t st, const char* what) {
+int launch_mfma(MfmaParams P, hipStream_t st, const char* what) {
+  const MfmaPlan plan = mfma_plan(P.n, device_cus() * TT_KS_WPE);
   const int mt = (P.m + 15) / 16;
-  P.spb = P.k / kSlice;
-  P.units = (int64_t)((P.n + 63) / 64) * P.spb;
-  P.grid = (int)mfma_grid(P.units, mt);
-  TT_REQUIRE(P.spb >= 1 && P.units >= 1 && P.grid >= 1, "%s: bad MFMA grid", what);
-  TT_REQUIRE(ws != nullptr && ws_floats >= mfma_ws_floats(P.m, P.n, P.k),
-             "%s: workspace of tt_batched_workspace_floats(m, rows, cols) floats required on the MFMA path", what);
-  P.ws = ws;
-  P.ws_row_scale = W == WFmt::kFp8Row ? 1 : 0;
-  const dim3 grid((unsigned)P.grid);
-  switch (mt) {
-    case 1: hipLaunchKernelGGL((mfma_gemm_kernel<W, 1>), grid, dim3(256), 0, st, P); break;
-    case 2: hipLaunchKernelGGL((mfma_gemm_kernel<W, 2>), grid, dim3(256), 0, st, P); break;
-    case 3: hipLaunchKernelGGL((mfma_gemm_kernel<W, 3>), grid, dim3(256), 0, st, P); break;
-    default: hipLaunchKernelGGL((mfma_gemm_kernel<W, 4>), grid, dim3(256), 0, st, P); break;
-  }
-  int rc = check_launch(what);
-  if (rc || P.grid == 1) return rc;
-  hipLaunchKernelGGL(mfma_fold_kernel, dim3((unsigned)(P.grid - 1)), dim3(256), 0, st, P, 16 * mt);
-  return check_launch(what);
+  const int sc = mt == 1 ? (use_lds_kernel<W, 1>() ? 64 : step_cols<W, 1>()) : (use_lds_kernel<W, 4>() ? 64 : step_cols<W, 4>());
+  P.rt = plan.rt;
+  P.steps = P.k / sc;
+  TT_REQUIRE(P.steps >= 1 && P.steps * sc == P.k, "%s: K must be a multiple of %d on the MFMA path", what, sc);
+  TT_REQUIRE(plan.blocks >= 1 && plan.blocks < (1LL << 31), "%s: bad MFMA grid", what);
+  const dim3 grid((unsigned)plan.blocks);
+  int rc;
+  if (mt == 1) rc = launch_mfma_mt<W, 1>(P, plan.nt, grid, st);
+  else if (mt == 2) rc = launch_mfma_mt<W, 2>(P, plan.nt, grid, st);
+  else rc = launch_mfma_mt<W, 4>(P, plan.nt, grid, st);
+  return rc ? rc : check_launch(what);
 }
 
 // Up to four activation rows per GEMV launch, eight with M8 (the dense decode-step
@@ -568,9 +722,13 @@ int dense_bias_rows_f16(const void* weight, int64_t w_row, const void* bias, con
 constexpr int kInt4MfmaMin = 4;
 constexpr int kFp8MfmaMin = 16;
 
+// The MFMA path sums its partial tiles inside the workgroup: no workspace (the
+// workspace arguments of the batched entry points are accepted and unused).
 extern "C" int64_t tt_batched_workspace_floats(int64_t m, int64_t rows, int64_t cols) {
-  if (m < kInt4MfmaMin || m > 64 || rows <= 0 || cols < kSlice) return 0;
-  return mfma_ws_floats(m, rows, cols);
+  (void)m;
+  (void)rows;
+  (void)cols;
+  return 0;
 }
 
 extern "C" int tt_int4_batched_matvec(const void* packed, int64_t w_row_bytes, const void* scales, int64_t s_row,
@@ -587,12 +745,13 @@ extern "C" int tt_int4_batched_matvec(const void* packed, int64_t w_row_bytes, c
   TT_REQUIRE(scales && x && out && aligned(x, 16) && x_row % 8 == 0 && x_row >= cols && out_row >= rows,
              "%s: null or misaligned pointer / bad row strides", what);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  (void)workspace;
+  (void)workspace_floats;
   if (m >= kInt4MfmaMin) {
-    TT_REQUIRE(aligned(scales, 4) && s_row % 2 == 0, "%s: m >= 4 reads scale pairs: 4-byte aligned scales, even row stride",
-               what);
+    TT_REQUIRE(aligned(scales, 2) && s_row >= cols / 128, "%s: fp16 scales [rows, cols / 128] expected", what);
     MfmaParams P{static_cast<const uint8_t*>(packed), w_row_bytes, scales, s_row, static_cast<const uint16_t*>(x),
-                 x_row, static_cast<uint16_t*>(out), out_row, nullptr, (int)m, (int)rows, (int)cols};
-    return launch_mfma<WFmt::kInt4G128>(P, workspace, workspace_floats, st, what);
+                 x_row, static_cast<uint16_t*>(out), out_row, (int)m, (int)rows, (int)cols};
+    return launch_mfma<WFmt::kInt4G128>(P, st, what);
   }
   if (m == 1)   // one row: the single-row GEMV itself (its lean int4 kernel)
     return tt_int4_scaled_matvec(packed, w_row_bytes, scales, TT_F16, s_row, 1, 0, 0, x, TT_F16, out, TT_F16, rows, cols,
@@ -618,10 +777,12 @@ extern "C" int tt_scaled_batched_matvec(const void* weight, int64_t w_row_bytes,
   TT_REQUIRE(scales && x && out && aligned(x, 16) && x_row % 8 == 0 && x_row >= cols && out_row >= rows,
              "%s: null or misaligned pointer / bad row strides", what);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  (void)workspace;
+  (void)workspace_floats;
   if (m >= kFp8MfmaMin) {
     MfmaParams P{static_cast<const uint8_t*>(weight), w_row_bytes, scales, 1, static_cast<const uint16_t*>(x), x_row,
-                 static_cast<uint16_t*>(out), out_row, nullptr, (int)m, (int)rows, (int)cols};
-    return launch_mfma<WFmt::kFp8Row>(P, workspace, workspace_floats, st, what);
+                 static_cast<uint16_t*>(out), out_row, (int)m, (int)rows, (int)cols};
+    return launch_mfma<WFmt::kFp8Row>(P, st, what);
   }
   GemvParams P{};
   P.nseg = 1;
