@@ -38,7 +38,8 @@ extern "C" {
 #define TT_F16 0
 #define TT_BF16 1
 #define TT_F32 2
-#define TT_W_FP8 3   /* weight format code: float8_e4m3fn (tt_split_k_matvec) */
+#define TT_W_FP8 3   /* weight format code: float8_e4m3fn (scaled GEMVs, tt_split_k_matvec) */
+#define TT_W_INT8 4  /* weight format code: int8 (the same entry points) */
 
 /* Library version and last error (thread-local message of the last failing call). */
 int tt_version(void);
@@ -77,10 +78,11 @@ int tt_multi_int4_scaled_matvec(int count, const void* const* packed, const int6
                                 void* out, int out_dtype, int64_t cols, int64_t group_size,
                                 void* stream);
 
-/* y[n] = (sum_k w[n,k] x[k]) * s[n], w float8_e4m3fn [rows, cols], s fp32 or fp16 [rows].
- * Replaces TritonDecodeBackend.scaled_matvec for per-row scales
- * (triton_kernels.py:4452-4595; kernels :539-592, :2990-3019). */
-int tt_scaled_matvec(const void* weight, int64_t w_row_bytes, const void* scales, int scale_dtype,
+/* y[n] = (sum_k w[n,k] x[k]) * s[n], w [rows, cols] float8_e4m3fn (w_format TT_W_FP8) or
+ * int8 (TT_W_INT8), s fp32 or fp16 [rows].  Replaces TritonDecodeBackend.scaled_matvec
+ * for per-row scales (triton_kernels.py:4452-4595; kernels :539-592, :2990-3019, which
+ * read either byte format). */
+int tt_scaled_matvec(const void* weight, int w_format, int64_t w_row_bytes, const void* scales, int scale_dtype,
                      const void* x, int x_dtype, void* out, int out_dtype,
                      int64_t rows, int64_t cols, void* stream);
 
@@ -242,20 +244,20 @@ int tt_int4_selected_matvec(const void* packed, int64_t w_expert_bytes, int64_t 
                             void* out, int out_dtype, int64_t out_slot,
                             int64_t rows, int64_t cols, int64_t group_size, void* stream);
 
-/* fp8 GEMV with per-block scales: y[m] = sum_b s[m*s_row + b*s_block] * sum_{k in block b}
- * w[m,k] x[k], blocks of `block` columns (a power of two; the last may be partial; a
- * block as wide as the row is the per-row-scale GEMV).  Blocks of 32 to 2048 columns.
- * Replaces the block-scaled branch of TritonDecodeBackend.scaled_matvec
- * (triton_kernels.py:4465-4497; kernel :3113-3152). */
-int tt_block_scaled_matvec(const void* weight, int64_t w_row_bytes, const void* scales, int scale_dtype,
-                           int64_t s_row, int64_t s_block, int64_t block, const void* x, int x_dtype,
-                           void* out, int out_dtype, int64_t rows, int64_t cols, void* stream);
+/* fp8 / int8 GEMV with per-block scales: y[m] = sum_b s[m*s_row + b*s_block] *
+ * sum_{k in block b} w[m,k] x[k], blocks of `block` columns (a power of two; the last may
+ * be partial; a block as wide as the row is the per-row-scale GEMV).  Blocks of 32 to
+ * 2048 columns; w_format TT_W_FP8 or TT_W_INT8.  Replaces the block-scaled branch of
+ * TritonDecodeBackend.scaled_matvec (triton_kernels.py:4465-4497; kernel :3113-3152). */
+int tt_block_scaled_matvec(const void* weight, int w_format, int64_t w_row_bytes, const void* scales,
+                           int scale_dtype, int64_t s_row, int64_t s_block, int64_t block, const void* x,
+                           int x_dtype, void* out, int out_dtype, int64_t rows, int64_t cols, void* stream);
 
-/* One to three fp8 matrices with per-row scales (scale i of matrix j at
- * scales[j][i * s_stride[j]]) over one activation vector; outputs concatenated in
- * matrix order.  Replaces TritonDecodeBackend.multi_scaled_tensorcore_matvec
- * (triton_kernels.py:5119-5180; kernel :1958-2071). */
-int tt_multi_scaled_matvec(int count, const void* const* weights, const int64_t* w_row_bytes,
+/* One to three fp8 or int8 matrices (one w_format for all) with per-row scales (scale i
+ * of matrix j at scales[j][i * s_stride[j]]) over one activation vector; outputs
+ * concatenated in matrix order.  Replaces TritonDecodeBackend.multi_scaled_tensorcore_matvec
+ * (triton_kernels.py:5119-5180; kernel :1958-2071, IS_FP8 selecting the byte format). */
+int tt_multi_scaled_matvec(int count, const void* const* weights, int w_format, const int64_t* w_row_bytes,
                            const void* const* scales, int scale_dtype, const int64_t* s_stride,
                            const int64_t* rows, const void* x, int x_dtype, void* out, int out_dtype,
                            int64_t cols, void* stream);
@@ -263,21 +265,22 @@ int tt_multi_scaled_matvec(int count, const void* const* weights, const int64_t*
 /* Split-K GEMV: K cut into split_k (2, 4 or 8) slices of whole 32-column chunks; binary32
  * row sums of each slice go to partials[s * rows + m] (caller scratch of split_k * rows
  * floats), then y = ((0 + p_0) + p_1 + ...) * scale (scales nullable).  w_format TT_F16,
- * TT_BF16 or TT_W_FP8.  Replaces TritonDecodeBackend.split_k_matvec
+ * TT_BF16, TT_W_FP8 or TT_W_INT8.  Replaces TritonDecodeBackend.split_k_matvec
  * (triton_kernels.py:3773-3845; kernels :3023-3100). */
 int tt_split_k_matvec(const void* weight, int w_format, int64_t w_row_bytes, const void* scales, int scale_dtype,
                       const void* x, int x_dtype, void* out, int out_dtype, int64_t rows, int64_t cols,
                       int split_k, float* partials, int64_t partials_capacity, void* stream);
 
-/* Fused fp8 gate/up GEMV + SiLU: out[m] = silu(g) * u with g = bf16((W_g[m] . x) * s_g[m])
- * and u = bf16((W_u[m] . x) * s_u[m]) (bfloat16 rounding whatever the activation dtype).
- * Each dot product has the reduction order of tt_scaled_matvec.  Replaces
+/* Fused fp8 / int8 gate/up GEMV + SiLU: out[m] = silu(g) * u with
+ * g = bf16((W_g[m] . x) * s_g[m]) and u = bf16((W_u[m] . x) * s_u[m]) (bfloat16 rounding
+ * whatever the activation dtype); both matrices in w_format TT_W_FP8 or TT_W_INT8.  Each
+ * dot product has the reduction order of tt_scaled_matvec.  Replaces
  * TritonDecodeBackend.fused_scaled_gate_up_silu (triton_kernels.py:4346-4436; kernels
  * :3243-3350). */
 int tt_scaled_gate_up_silu(const void* gate_weight, int64_t wg_row_bytes, const void* gate_scales,
                            int64_t sg_stride, const void* up_weight, int64_t wu_row_bytes, const void* up_scales,
-                           int64_t su_stride, int scale_dtype, const void* x, int x_dtype, void* out,
-                           int out_dtype, int64_t rows, int64_t cols, void* stream);
+                           int64_t su_stride, int w_format, int scale_dtype, const void* x, int x_dtype,
+                           void* out, int out_dtype, int64_t rows, int64_t cols, void* stream);
 
 /* Greedy lm_head: logits = round(W x) (stored when `logits` is non-null), token =
  * first index of the maximum rounded logit (NaN counts as the maximum, +0 == -0),
@@ -640,12 +643,16 @@ int tt_stream_read(const void* data, int64_t bytes, int64_t bytes_per_wave, void
 
 /* Grouped INT4 (two codes per byte, even column in the low nibble) for group sizes
  * 32..512 (powers of two); importance [cols] (binary32 max(rms^2, 1e-8)) only with
- * TT_Q4_LSQ_AFFINE.  Replaces quantize_to_int4_cpu (gpu_runtime.py:91-304, without the
- * GPTQ covariance refinement) and ThinGpuCausalLMRuntime._quantize_int4_rows
- * (gpu_runtime.py:6609-6700). */
+ * TT_Q4_LSQ_AFFINE.  gptq_factors (nullable; TT_Q4_LSQ_AFFINE with groups of 32 only):
+ * device fp32 [groups, 32, 32], per group the upper Cholesky factor U of the inverse
+ * damped input covariance; after the affine fit two GPTQ passes requantize the group
+ * column by column, spreading each column's error (divided by U[c][c]) over the later
+ * columns along row c of U, with one refit of the line between the passes.  Replaces
+ * quantize_to_int4_cpu (gpu_runtime.py:91-304) and
+ * ThinGpuCausalLMRuntime._quantize_int4_rows (gpu_runtime.py:6609-6700). */
 int tt_quantize_int4(const void* src, int src_dtype, int64_t rows, int64_t cols, int64_t src_row,
-                     int64_t group_size, int mode, const float* importance, uint8_t* packed, void* scales,
-                     void* stream);
+                     int64_t group_size, int mode, const float* importance, const float* gptq_factors,
+                     uint8_t* packed, void* scales, void* stream);
 
 /* float8_e4m3fn rows with fp32 scales max(amax, 1e-12)/448 per row (block == 0, scales
  * [rows]) or per block of columns (scales [rows, ceil(cols/block)]).  via_bf16 rounds the

@@ -23,7 +23,7 @@ from . import build as _build
 from . import ref  # noqa: F401  (re-export)
 
 F16, BF16, F32 = 0, 1, 2
-FMT = dict(int4_sym=0, int4_aff=1, fp8=2, f16w=3, bf16w=4, mxfp4=5, q2e8=6, q1e8=7, q2aff=8, q1aff=9)
+FMT = dict(int4_sym=0, int4_aff=1, fp8=2, f16w=3, bf16w=4, mxfp4=5, q2e8=6, q1e8=7, q2aff=8, q1aff=9, int8=10)
 SMODE = dict(none=0, row=1, group=2, group_aff=3, block_e8=4)
 
 _P = ctypes.c_void_p
@@ -272,10 +272,10 @@ def split_k_gemv(fmt: str, w: np.ndarray, x: np.ndarray, split_k: int, scales=No
     """Split-K GEMV restated: slices of q = ceil(K/32/split_k) whole chunks (last one
     shorter or absent), each the single-matrix binary32 row sum of its width, added in
     slice order from +0, times the per-row scale, rounded once.  ``w`` is uint8
-    [rows, row_bytes] of dense fp16/bf16 or fp8 weights."""
+    [rows, row_bytes] of dense fp16/bf16, fp8 or int8 weights."""
     from .decode_ref import lanes
 
-    esz = 1 if fmt == "fp8" else 2
+    esz = 1 if fmt in ("fp8", "int8") else 2
     wb = np.ascontiguousarray(w).view(np.uint8).reshape(w.shape[0], -1)
     cols = x.shape[0]
     nchunks = cols // 32

@@ -164,11 +164,17 @@ def _affine_fit(g, q, w, present):
     return s, mn
 
 
-def int4_lsq_affine(x: np.ndarray, group_size: int, input_rms: np.ndarray | None = None):
+def int4_lsq_affine(x: np.ndarray, group_size: int, input_rms: np.ndarray | None = None,
+                    gptq_factors: np.ndarray | None = None):
     """quantize_to_int4_cpu with THINTENSOR_AFFINE_INT4=1 (gpu_runtime.py:155-236,
     cols divisible by the group): min/max line, two refits each followed by a
     requantization, then a final refit of (scale, minimum); codes in [0, 15];
-    optional column importance max(rms^2, 1e-8).  fp16 [scale, minimum] pairs."""
+    optional column importance max(rms^2, 1e-8).  With ``gptq_factors`` (binary32
+    [groups, 32, 32] upper factors U, groups of 32) two GPTQ passes follow
+    (:217-262): column c of each group is rounded on the current line from its
+    adjusted value, (value - code * scale - minimum) / U[c, c] is taken out of columns
+    c.. along U[c, c..] (product, then difference), and the line is refitted after the
+    first pass.  fp16 [scale, minimum] pairs."""
     rows, cols = x.shape
     assert cols % group_size == 0
     g, present = _groups(x, group_size)
@@ -184,6 +190,20 @@ def int4_lsq_affine(x: np.ndarray, group_size: int, input_rms: np.ndarray | None
         s, mn = _affine_fit(g, q, w, present)
         q = np.clip(np.rint(((g - mn[..., None]).astype(np.float32) / s[..., None]).astype(np.float32)), 0, 15).astype(np.float32)
     s, mn = _affine_fit(g, q, w, present)
+    if gptq_factors is not None:
+        assert group_size == 32
+        U = np.asarray(gptq_factors, dtype=np.float32)
+        for gptq_pass in range(2):
+            adj = g.copy()
+            for c in range(group_size):
+                cur = adj[:, :, c].copy()
+                code = np.clip(np.rint(((cur - mn).astype(np.float32) / s).astype(np.float32)), 0, 15).astype(np.float32)
+                q[:, :, c] = code
+                qv = ((code * s).astype(np.float32) + mn).astype(np.float32)
+                err = ((cur - qv).astype(np.float32) / U[None, :, c, c]).astype(np.float32)
+                adj[:, :, c:] = (adj[:, :, c:] - (err[..., None] * U[None, :, c, c:]).astype(np.float32)).astype(np.float32)
+            if gptq_pass == 0:
+                s, mn = _affine_fit(g, q, w, present)
     codes = q.astype(np.uint8).reshape(rows, cols)
     scales = np.stack([s, mn], axis=-1).astype(np.float16)
     return _pack_nibbles(codes), scales

@@ -124,14 +124,14 @@ float tto_exp_f32(float x) {
 
 enum {
   FMT_INT4_SYM = 0, FMT_INT4_AFF = 1, FMT_FP8 = 2, FMT_F16W = 3, FMT_BF16W = 4,
-  FMT_MXFP4 = 5, FMT_Q2E8 = 6, FMT_Q1E8 = 7, FMT_Q2AFF = 8, FMT_Q1AFF = 9
+  FMT_MXFP4 = 5, FMT_Q2E8 = 6, FMT_Q1E8 = 7, FMT_Q2AFF = 8, FMT_Q1AFF = 9, FMT_INT8 = 10
 };
 enum { SM_NONE = 0, SM_ROW = 1, SM_GROUP = 2, SM_GROUP_AFF = 3, SM_BLOCK_E8 = 4 };
 
 static int fmt_bytes(int fmt) {
   switch (fmt) {
     case FMT_INT4_SYM: case FMT_INT4_AFF: case FMT_MXFP4: return 16;
-    case FMT_FP8: return 32;
+    case FMT_FP8: case FMT_INT8: return 32;
     case FMT_F16W: case FMT_BF16W: return 64;
     case FMT_Q2E8: case FMT_Q2AFF: return 8;
     default: return 4;
@@ -169,6 +169,7 @@ static float chunk_weight(int fmt, const uint8_t* c, int e) {
     case FMT_Q1E8: return ((c[e >> 3] >> (e & 7)) & 1) ? 1.0f : -1.0f;
     case FMT_Q2AFF: return (float)((c[e >> 2] >> ((e & 3) * 2)) & 3);
     case FMT_Q1AFF: return (float)((c[e >> 3] >> (e & 7)) & 1);
+    case FMT_INT8: return (float)(int8_t)c[e];   /* triton_kernels.py:554-560: int8 rows .to(fp32) */
   }
   return 0.0f;
 }

@@ -7,7 +7,8 @@ data only; the GPU tests compare the HIP quantizers against it.
 
 Functions recorded (reference thinruntime/gpu_runtime.py):
   quantize_to_fp8_via_gpu            :40-88     (called with device=cpu)
-  quantize_to_int4_cpu               :91-304    (symmetric LSQ, affine refinement, importance)
+  quantize_to_int4_cpu               :91-304    (symmetric LSQ, affine refinement, importance,
+                                                  GPTQ passes with a calibration covariance)
   quantize_mxfp4_to_lowbit_cpu       :306-395
   quantize_dense_to_mxfp_lowbit_cpu  :398-491
   quantize_mxfp4_to_ternary_cpu      :494-583
@@ -99,7 +100,24 @@ def main(ref_root: str) -> None:
     src = _source(13, 12, 384)
     packed, scales = rt._quantize_int4_rows(src, group_size=128)
     put("int4_rows_affine", source=src, packed=packed, scales=scales, group_size=128)
+    # GPTQ passes (:130-150, :217-262): groups of 32, covariance of correlated calibration
+    # activations (neighbouring columns mixed so the factors have large off-diagonals)
+    src = _source(14, 12, 256)
+    g = torch.Generator().manual_seed(15)
+    calib = torch.randn(512, 256, generator=g)
+    calib = (calib + 0.6 * torch.roll(calib, 1, dims=1)) * (torch.rand(256, generator=g) * 2.0 + 0.1)
+    blocks = calib.reshape(512, 8, 32).permute(1, 2, 0)           # [groups, 32, samples]
+    cov = (blocks @ blocks.transpose(1, 2)) / 512.0
+    packed, scales = gr.quantize_to_int4_cpu(src, group_size=32, input_covariance32=cov)
+    put("int4_affine_gptq", source=src, packed=packed, scales=scales, group_size=32, covariance=cov)
+    rms = (torch.rand(256, generator=g) * 2.0 + 0.05)
+    packed, scales = gr.quantize_to_int4_cpu(src, group_size=32, input_rms=rms, input_covariance32=cov)
+    put("int4_affine_gptq_rms", source=src, packed=packed, scales=scales, group_size=32, covariance=cov,
+        input_rms=rms)
     os.environ["THINTENSOR_AFFINE_INT4"] = "0"
+    # the symmetric fit computes the factors but does not use them
+    packed, scales = gr.quantize_to_int4_cpu(src, group_size=32, input_covariance32=cov)
+    put("int4_lsq_gptq_unused", source=src, packed=packed, scales=scales, group_size=32, covariance=cov)
 
     # FP8 rows: per-row and per-block scales, direct fp32 -> e4m3 (:6551-6607)
     for name, (rows, cols, blk, dt) in {"fp8_rows": (16, 512, 0, torch.bfloat16),

@@ -42,6 +42,35 @@ def test_fp8_decoder_matches_torch():
     assert np.array_equal(t[ok].astype(np.float64), mine[ok])
 
 
+@pytest.mark.parametrize("smode", ["row", "group"])
+def test_int8_emulation_exact_on_integer_inputs(smode):
+    """int8 rows (the reference reads them with .to(fp32), triton_kernels.py:554-560):
+    integer activations and power-of-two scales make every partial sum exact, so the
+    binary32 restatement must equal the float64 closed form over torch's own int8
+    conversion; reading the bytes as unsigned (a plausible decode mistake) must not."""
+    from oracle.decode_ref import lanes
+
+    g = rng(11)
+    rows, cols, block = 40, 1024, 128
+    q = g.integers(-128, 128, size=(rows, cols), dtype=np.int8)
+    x = g.integers(-4, 5, size=cols).astype(np.float16)
+    w64 = torch.from_numpy(q).to(torch.float64).numpy()
+    if smode == "row":
+        s = (2.0 ** g.integers(-8, 0, size=rows)).astype(np.float32)
+        got = oracle.gemv("int8", "row", q.view(np.uint8), s, x, cols=cols, lpr=lanes(cols), s_row=1,
+                          odtype=oracle.F32)
+        scale = s[:, None].astype(np.float64)
+    else:
+        s = (2.0 ** g.integers(-8, 0, size=(rows, cols // block))).astype(np.float32)
+        L = block // 32
+        got = oracle.gemv("int8", "group", q.view(np.uint8), s, x, cols=cols, lpr=lanes(cols, L), L=L,
+                          s_row=cols // block, s_grp=1, odtype=oracle.F32)
+        scale = np.repeat(s.astype(np.float64), block, axis=1)
+    assert np.array_equal(got.astype(np.float64), ref.gemv64(w64 * scale, x))
+    unsigned = q.view(np.uint8).astype(np.float64)
+    assert not np.array_equal(got.astype(np.float64), ref.gemv64(unsigned * scale, x))
+
+
 def test_e2m1_and_lowbit_tables():
     # e2m1: value = (-1)^s * 2^(e-1) * (1 + m/2) for e > 0, m/2 for e == 0 (OCP MX v1.0)
     for code in range(16):

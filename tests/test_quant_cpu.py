@@ -48,6 +48,49 @@ def test_int4_affine_matches_reference(V, name, rms):
     assert same(p, V[name + ".packed"]) and same(s, V[name + ".scales"])
 
 
+def gptq_factors(V, name):
+    """The upper Cholesky factors of the damped inverse covariances, from the host-side
+    set-up the product uses (thintensor_amd.quantize.gptq_inverse_cholesky)."""
+    from thintensor_amd.quantize import gptq_inverse_cholesky
+
+    return gptq_inverse_cholesky(torch.from_numpy(V[name + ".covariance"])).numpy()
+
+
+@pytest.mark.parametrize("name,rms", [("int4_affine_gptq", False), ("int4_affine_gptq_rms", True)])
+def test_int4_affine_gptq_matches_reference(V, name, rms):
+    x = src(V, name)
+    U = gptq_factors(V, name)
+    p, s = Q.int4_lsq_affine(x, 32, V[name + ".input_rms"] if rms else None, gptq_factors=U)
+    assert same(p, V[name + ".packed"]) and same(s, V[name + ".scales"])
+    # the passes change the result (the vectors pin them, not just the plain affine fit)
+    p0, s0 = Q.int4_lsq_affine(x, 32, V[name + ".input_rms"] if rms else None)
+    assert not same(p0, V[name + ".packed"])
+    # planted mistake: the factor transposed (error spread down column c instead of along row c)
+    bad = np.ascontiguousarray(np.swapaxes(U, 1, 2))
+    pb, _ = Q.int4_lsq_affine(x, 32, V[name + ".input_rms"] if rms else None, gptq_factors=bad)
+    assert not same(pb, V[name + ".packed"])
+
+
+def test_int4_lsq_ignores_covariance(V):
+    """The symmetric fit computes the factors and leaves them unused (gpu_runtime.py:237-253)."""
+    name = "int4_lsq_gptq_unused"
+    p, s = Q.int4_lsq(src(V, name), 32)
+    assert same(p, V[name + ".packed"]) and same(s, V[name + ".scales"])
+
+
+def test_gptq_factors_properties(V):
+    """U is upper triangular with a positive diagonal and U^T U inverts the damped
+    covariance (float64 check of the host set-up)."""
+    cov = V["int4_affine_gptq.covariance"].astype(np.float64)
+    U = gptq_factors(V, "int4_affine_gptq").astype(np.float64)
+    assert np.all(np.tril(U, -1) == 0) and np.all(np.diagonal(U, axis1=1, axis2=2) > 0)
+    damp = np.maximum(np.diagonal(cov, axis1=1, axis2=2).mean(axis=1) * 0.01, 1e-6)
+    H = cov + damp[:, None, None] * np.eye(32)
+    # inv(H) = U^T U  <=>  U H U^T = I
+    eye = U @ H @ np.swapaxes(U, 1, 2)
+    assert np.max(np.abs(eye - np.eye(32))) < 1e-3
+
+
 @pytest.mark.parametrize("name,affine", [("int4_rows", False), ("int4_rows_ragged", False), ("int4_rows_affine", True)])
 def test_int4_rows_matches_reference(V, name, affine):
     p, s = Q.int4_rows(src(V, name), int(V[name + ".group_size"]), affine=affine)

@@ -80,6 +80,33 @@ def test_int4_affine_reference_vectors(V, affine_env):
     eq(s, V["int4_affine_rms.scales"], "affine+rms scales")
 
 
+@pytest.mark.parametrize("name,rms", [("int4_affine_gptq", False), ("int4_affine_gptq_rms", True)])
+def test_int4_affine_gptq_reference_vectors(V, affine_env, name, rms):
+    """GPTQ passes with a calibration covariance (gpu_runtime.py:130-150, :217-262)."""
+    affine_env(True)
+    cov = torch.from_numpy(V[name + ".covariance"])
+    kw = {"input_rms": torch.from_numpy(V[name + ".input_rms"])} if rms else {}
+    p, s = TQ.quantize_to_int4_cpu(src_t(V, name), group_size=32, input_covariance32=cov, **kw)
+    assert p.device.type == "cpu"
+    eq(p, V[name + ".packed"], name + " packed")
+    eq(s, V[name + ".scales"], name + " scales")
+
+
+def test_int4_gptq_covariance_contract(V, affine_env):
+    """The symmetric fit leaves the factors unused; group sizes other than 32 and
+    mismatched covariance shapes raise the reference's errors."""
+    affine_env(False)
+    name = "int4_lsq_gptq_unused"
+    cov = torch.from_numpy(V[name + ".covariance"])
+    p, s = TQ.quantize_to_int4_cpu(src_t(V, name), group_size=32, input_covariance32=cov)
+    eq(p, V[name + ".packed"], "symmetric packed")
+    eq(s, V[name + ".scales"], "symmetric scales")
+    with pytest.raises(ValueError, match="require INT4 group size 32"):
+        TQ.quantize_to_int4_cpu(src_t(V, name), group_size=64, input_covariance32=cov)
+    with pytest.raises(ValueError, match="covariance shape"):
+        TQ.quantize_to_int4_cpu(src_t(V, name), group_size=32, input_covariance32=cov[:4])
+
+
 @pytest.mark.parametrize("name,affine", [("int4_rows", False), ("int4_rows_ragged", False), ("int4_rows_affine", True)])
 def test_int4_rows_reference_vectors(V, affine_env, device, name, affine):
     affine_env(affine)
@@ -168,6 +195,25 @@ def test_int4_affine_matches_oracle(affine_env, with_rms):
     rms = (torch.rand(4096, generator=torch.Generator().manual_seed(6)) * 3 + 0.01) if with_rms else None
     p, s = TQ.quantize_to_int4_cpu(x, group_size=128, input_rms=rms)
     wp, ws = Q.int4_lsq_affine(f32(x), 128, rms.numpy() if with_rms else None)
+    eq(p, wp, "packed")
+    eq(s, ws.view(np.uint16), "scales")
+
+
+@pytest.mark.parametrize("with_rms", [False, True])
+def test_int4_affine_gptq_matches_oracle(affine_env, with_rms):
+    """GPTQ passes at a projection-sized width against the oracle, bit for bit."""
+    affine_env(True)
+    rows, cols = 96, 2048
+    x = seeded(8, rows, cols)
+    g = torch.Generator().manual_seed(9)
+    calib = torch.randn(256, cols, generator=g)
+    calib = calib + 0.5 * torch.roll(calib, 1, dims=1)
+    blocks = calib.reshape(256, cols // 32, 32).permute(1, 2, 0).contiguous()
+    cov = torch.matmul(blocks, blocks.transpose(1, 2).contiguous()) / 256.0
+    rms = (torch.rand(cols, generator=g) * 3 + 0.01) if with_rms else None
+    p, s = TQ.quantize_to_int4_cpu(x, group_size=32, input_rms=rms, input_covariance32=cov)
+    U = TQ.gptq_inverse_cholesky(cov).numpy()
+    wp, ws = Q.int4_lsq_affine(f32(x), 32, rms.numpy() if with_rms else None, gptq_factors=U)
     eq(p, wp, "packed")
     eq(s, ws.view(np.uint16), "scales")
 

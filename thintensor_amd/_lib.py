@@ -15,7 +15,8 @@ from pathlib import Path
 from . import build as _build
 
 F16, BF16, F32 = 0, 1, 2
-W_FP8 = 3   # weight format code of float8_e4m3fn (tt_split_k_matvec)
+W_FP8 = 3   # weight format code of float8_e4m3fn (scaled GEMVs, tt_split_k_matvec)
+W_INT8 = 4  # weight format code of int8 (the same entry points)
 Q4_LSQ, Q4_LSQ_AFFINE, Q4_ROWS, Q4_ROWS_AFFINE = 0, 1, 2, 3   # tt_quantize_int4 modes
 
 _P = ctypes.c_void_p
@@ -79,11 +80,11 @@ SIGNATURES: dict[str, list] = {
     "tt_gemv_lanes_per_row": [_L, _L],
     "tt_int4_scaled_matvec": [_P, _L, _P, _I, _L, _L, _L, _I, _P, _I, _P, _I, _L, _L, _L, _P],
     "tt_multi_int4_scaled_matvec": [_I, _PP, _LP, _PP, _I, _LP, _LP, _L, _I, _LP, _P, _I, _P, _I, _L, _L, _P],
-    "tt_scaled_matvec": [_P, _L, _P, _I, _P, _I, _P, _I, _L, _L, _P],
-    "tt_block_scaled_matvec": [_P, _L, _P, _I, _L, _L, _L, _P, _I, _P, _I, _L, _L, _P],
-    "tt_multi_scaled_matvec": [_I, _PP, _LP, _PP, _I, _LP, _LP, _P, _I, _P, _I, _L, _P],
+    "tt_scaled_matvec": [_P, _I, _L, _P, _I, _P, _I, _P, _I, _L, _L, _P],
+    "tt_block_scaled_matvec": [_P, _I, _L, _P, _I, _L, _L, _L, _P, _I, _P, _I, _L, _L, _P],
+    "tt_multi_scaled_matvec": [_I, _PP, _I, _LP, _PP, _I, _LP, _LP, _P, _I, _P, _I, _L, _P],
     "tt_split_k_matvec": [_P, _I, _L, _P, _I, _P, _I, _P, _I, _L, _L, _I, _P, _L, _P],
-    "tt_scaled_gate_up_silu": [_P, _L, _P, _L, _P, _L, _P, _L, _I, _P, _I, _P, _I, _L, _L, _P],
+    "tt_scaled_gate_up_silu": [_P, _L, _P, _L, _P, _L, _P, _L, _I, _I, _P, _I, _P, _I, _L, _L, _P],
     "tt_head_rms_norm": [_P, _I, _P, _I, _P, _L, _L, _F, _P],
     "tt_qk_head_rmsnorm_rope_inplace": [_P, _P, _I, _P, _P, _I, _P, _P, _L, _L, _P, _L, _L, _L, _L, _F, _P],
     "tt_matvec": [_P, _I, _L, _P, _I, _P, _I, _L, _L, _P],
@@ -142,7 +143,7 @@ SIGNATURES: dict[str, list] = {
     "tt_fused_lm_head_argmax": [_FGP, _P, _L, _P, _P, _P, _P, _P, ctypes.c_int32, _P],
     "tt_stream_read_waves": [_L, _L],
     "tt_stream_read": [_P, _L, _L, _P, _L, _P],
-    "tt_quantize_int4": [_P, _I, _L, _L, _L, _L, _I, _P, _P, _P, _P],
+    "tt_quantize_int4": [_P, _I, _L, _L, _L, _L, _I, _P, _P, _P, _P, _P],
     "tt_quantize_fp8_rows": [_P, _I, _L, _L, _L, _L, _I, _P, _P, _P],
     "tt_quantize_mxfp4_rows": [_P, _I, _L, _L, _L, _L, _P, _I, _P, _P, _P],
     "tt_requantize_mxfp4_lowbit": [_P, _P, _L, _I, _P, _P, _P],

@@ -33,6 +33,17 @@ def _code(t: torch.Tensor, what: str) -> int:
         raise ValueError(f"{what}: unsupported dtype {t.dtype}") from None
 
 
+# one-byte weight formats of the scaled GEMVs (the reference kernels convert either to fp32)
+_BYTE_WEIGHT_FORMATS = {torch.float8_e4m3fn: _lib.W_FP8, torch.int8: _lib.W_INT8}
+
+
+def _byte_weight_format(weight: torch.Tensor, what: str) -> int:
+    try:
+        return _BYTE_WEIGHT_FORMATS[weight.dtype]
+    except KeyError:
+        raise ValueError(f"{what} supports float8_e4m3fn and int8 weights, got {weight.dtype}") from None
+
+
 def _stream(t: torch.Tensor) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
 
@@ -292,10 +303,10 @@ class HipDecodeBackend:
         block_m: int | None = None,
         num_warps: int | None = None,
     ) -> torch.Tensor:
-        """y = (W_fp8 @ x) * s_row (triton_kernels.py:4452-4595, per-row scales)."""
+        """y = (W @ x) * s_row for float8_e4m3fn or int8 W (triton_kernels.py:4452-4595,
+        per-row or per-block scales; the kernels at :539-592 read either byte format)."""
         _require_cuda(weight, scales, x, out)
-        if weight.dtype != torch.float8_e4m3fn:
-            raise ValueError(f"scaled_matvec supports float8_e4m3fn weights on this backend, got {weight.dtype}")
+        wfmt = _byte_weight_format(weight, "scaled_matvec")
         rows, cols = int(weight.shape[0]), int(weight.shape[1])
         if scales.dim() == 2:
             # block-scaled branch (triton_kernels.py:4465-4497): blocks of
@@ -307,7 +318,7 @@ class HipDecodeBackend:
             block = 1 << max(0, (-(-cols // blocks) - 1).bit_length())
             _require_cuda(weight, scales, x, out)
             rc = self.lib.tt_block_scaled_matvec(
-                weight.data_ptr(), weight.stride(0), scales.data_ptr(), _code(scales, "fp8 scales"), scales.stride(0),
+                weight.data_ptr(), wfmt, weight.stride(0), scales.data_ptr(), _code(scales, "fp8 scales"), scales.stride(0),
                 scales.stride(1), block, x.data_ptr(), _code(x, "scaled_matvec"), out.data_ptr(),
                 _code(out, "scaled_matvec"), rows, cols, _stream(out),
             )
@@ -316,7 +327,7 @@ class HipDecodeBackend:
         if scales.numel() != rows or x.numel() != cols or out.numel() != rows or weight.stride(1) != 1:
             raise ValueError("scaled_matvec shape mismatch")
         rc = self.lib.tt_scaled_matvec(
-            weight.data_ptr(), weight.stride(0), scales.data_ptr(), _code(scales, "fp8 scales"), x.data_ptr(),
+            weight.data_ptr(), wfmt, weight.stride(0), scales.data_ptr(), _code(scales, "fp8 scales"), x.data_ptr(),
             _code(x, "scaled_matvec"), out.data_ptr(), _code(out, "scaled_matvec"), rows, cols, _stream(out),
         )
         _lib.check(rc, "scaled_matvec")
@@ -331,9 +342,8 @@ class HipDecodeBackend:
         x: torch.Tensor,
         out: torch.Tensor,
     ) -> torch.Tensor:
-        """Two or three fp8 matrices with per-row scales, outputs concatenated
-        (triton_kernels.py:5119-5180, kernel :1958-2071).  The reference's int8 weights are
-        not provided by this backend."""
+        """Two or three float8_e4m3fn or int8 matrices with per-row scales, outputs
+        concatenated (triton_kernels.py:5119-5180, kernel :1958-2071)."""
         if len(weights) not in {2, 3} or len(scales) != len(weights):
             raise ValueError("multi scaled tensor-core matvec supports two or three matrices")
         if cols % 256:
@@ -343,8 +353,6 @@ class HipDecodeBackend:
             raise ValueError("tensor-core matvec requires E4M3 or INT8 weights")
         if any(weight.dtype != dtype for weight in weights):
             raise ValueError("multi tensor-core weights must share one dtype")
-        if dtype == torch.int8:
-            raise ValueError("multi_scaled_tensorcore_matvec: int8 weights are not supported by the HIP backend")
         rows = tuple(int(r) for r in rows)[: len(weights)]
         if len(rows) != len(weights) or any(int(w.shape[0]) != r or int(w.shape[1]) != cols or w.stride(1) != 1
                                             for w, r in zip(weights, rows)):
@@ -355,7 +363,8 @@ class HipDecodeBackend:
             raise ValueError("multi scaled matvec scale/input/output mismatch")
         _require_cuda(*weights, *scales, x, out)
         rc = self.lib.tt_multi_scaled_matvec(
-            len(weights), _lib.ptr_array([w.data_ptr() for w in weights]), _lib.i64_array([w.stride(0) for w in weights]),
+            len(weights), _lib.ptr_array([w.data_ptr() for w in weights]),
+            _lib.W_INT8 if dtype == torch.int8 else _lib.W_FP8, _lib.i64_array([w.stride(0) for w in weights]),
             _lib.ptr_array([sc.data_ptr() for sc in scales]), _code(scales[0], "fp8 scales"),
             _lib.i64_array([sc.stride(0) for sc in scales]), _lib.i64_array(rows), x.data_ptr(),
             _code(x, "multi_scaled_tensorcore_matvec"), out.data_ptr(), _code(out, "multi_scaled_tensorcore_matvec"),
@@ -389,10 +398,10 @@ class HipDecodeBackend:
             fmt = _lib.F16
         elif weight.dtype == torch.bfloat16:
             fmt = _lib.BF16
-        elif weight.dtype == torch.float8_e4m3fn:
-            fmt = _lib.W_FP8
+        elif weight.dtype in _BYTE_WEIGHT_FORMATS:
+            fmt = _BYTE_WEIGHT_FORMATS[weight.dtype]
         else:
-            raise ValueError(f"split_k_matvec supports fp16, bf16 and float8_e4m3fn weights, got {weight.dtype}")
+            raise ValueError(f"split_k_matvec supports fp16, bf16, float8_e4m3fn and int8 weights, got {weight.dtype}")
         if weight.stride(1) != 1 or x.numel() != cols or out.numel() != rows or not out.is_contiguous():
             raise ValueError("split_k_matvec shape mismatch")
         count = split_k * rows
@@ -432,8 +441,9 @@ class HipDecodeBackend:
             raise ValueError("fused scaled gate/up matrices must have equal shapes")
         if gate_scales.numel() != rows or up_scales.numel() != rows:
             raise ValueError("fused scaled gate/up scales must match matrix rows")
-        if gate_weight.dtype != torch.float8_e4m3fn or up_weight.dtype != torch.float8_e4m3fn:
-            raise ValueError("fused_scaled_gate_up_silu supports float8_e4m3fn weights on this backend")
+        wfmt = _byte_weight_format(gate_weight, "fused_scaled_gate_up_silu")
+        if up_weight.dtype != gate_weight.dtype:
+            raise ValueError("fused scaled gate/up matrices must share a dtype")
         if gate_scales.dtype != up_scales.dtype:
             raise ValueError("fused scaled gate/up scales must share a dtype")
         if gate_weight.stride(1) != 1 or up_weight.stride(1) != 1 or x.numel() != cols or out.numel() != rows:
@@ -441,7 +451,7 @@ class HipDecodeBackend:
         _require_cuda(gate_weight, gate_scales, up_weight, up_scales, x, out)
         rc = self.lib.tt_scaled_gate_up_silu(
             gate_weight.data_ptr(), gate_weight.stride(0), gate_scales.data_ptr(), gate_scales.stride(0),
-            up_weight.data_ptr(), up_weight.stride(0), up_scales.data_ptr(), up_scales.stride(0),
+            up_weight.data_ptr(), up_weight.stride(0), up_scales.data_ptr(), up_scales.stride(0), wfmt,
             _code(gate_scales, "gate/up scales"), x.data_ptr(), _code(x, "fused_scaled_gate_up_silu"), out.data_ptr(),
             _code(out, "fused_scaled_gate_up_silu"), rows, cols, _stream(out),
         )

@@ -1,4 +1,4 @@
-// Fused per-row-scaled gate/up GEMV + SiLU for gfx950 (float8_e4m3fn weights):
+// Fused per-row-scaled gate/up GEMV + SiLU for gfx950 (float8_e4m3fn or int8 weights):
 //
 //   out[m] = silu(g) * u,  g = bf16((W_g[m] . x) * s_g[m]),  u = bf16((W_u[m] . x) * s_u[m])
 //
@@ -13,6 +13,8 @@
 // row sum).  After the reduction lane 0 of the group holds g and lane 1 holds u; one
 // cross-lane move brings u to lane 0, which stores the product.  The activation vector
 // is staged once per workgroup in LDS.
+#include <type_traits>
+
 #include "gemv_impl.h"
 
 namespace tt {
@@ -100,15 +102,17 @@ using namespace tt;
 
 extern "C" int tt_scaled_gate_up_silu(const void* gate_weight, int64_t wg_row_bytes, const void* gate_scales,
                                       int64_t sg_stride, const void* up_weight, int64_t wu_row_bytes,
-                                      const void* up_scales, int64_t su_stride, int scale_dtype, const void* x,
-                                      int x_dtype, void* out, int out_dtype, int64_t rows, int64_t cols,
-                                      void* stream) {
+                                      const void* up_scales, int64_t su_stride, int w_format, int scale_dtype,
+                                      const void* x, int x_dtype, void* out, int out_dtype, int64_t rows,
+                                      int64_t cols, void* stream) {
   const char* what = "fused_scaled_gate_up_silu";
+  TT_REQUIRE(w_format == TT_W_FP8 || w_format == TT_W_INT8, "%s: weights must be float8_e4m3fn or int8 (format %d)",
+             what, w_format);
   TT_REQUIRE(valid_act_dtype(x_dtype) && valid_out_dtype(out_dtype), "%s: bad dtype codes", what);
   TT_REQUIRE(scale_dtype == TT_F16 || scale_dtype == TT_F32, "%s: scales must be fp16 or fp32", what);
   TT_REQUIRE(gate_weight && up_weight && aligned(gate_weight, 16) && aligned(up_weight, 16) && wg_row_bytes % 16 == 0 &&
                  wu_row_bytes % 16 == 0 && wg_row_bytes >= cols && wu_row_bytes >= cols,
-             "%s: fp8 weights must be 16-byte aligned rows", what);
+             "%s: weights must be 16-byte aligned rows", what);
   TT_REQUIRE(gate_scales && up_scales && sg_stride >= 1 && su_stride >= 1, "%s: bad scales", what);
   TT_REQUIRE(x && aligned(x, 16) && out, "%s: null or misaligned pointer", what);
   TT_REQUIRE(rows > 0 && rows < (1 << 30), "%s: bad rows", what);
@@ -119,19 +123,24 @@ extern "C" int tt_scaled_gate_up_silu(const void* gate_weight, int64_t wg_row_by
   const int lpr = tt_gemv_lanes_per_row(cols / 32, 1);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const size_t lds = (size_t)cols * 2;
-  auto go = [&](auto xt, auto ot, auto sdt) -> int {
+  auto launch = [&](auto fmt, auto xt, auto ot, auto sdt) -> int {
+    constexpr Fmt F = decltype(fmt)::value;
     using XT = decltype(xt);
     using OT = decltype(ot);
     using ST = decltype(sdt);
     const int per_block = 4 * (64 / lpr);
     const dim3 grid((unsigned)((rows + per_block - 1) / per_block));
     switch (lpr) {
-      case 64: hipLaunchKernelGGL((gate_up_silu_kernel<Fmt::kFp8, XT, OT, ST, 64>), grid, dim3(256), lds, st, P); break;
-      case 32: hipLaunchKernelGGL((gate_up_silu_kernel<Fmt::kFp8, XT, OT, ST, 32>), grid, dim3(256), lds, st, P); break;
-      case 16: hipLaunchKernelGGL((gate_up_silu_kernel<Fmt::kFp8, XT, OT, ST, 16>), grid, dim3(256), lds, st, P); break;
+      case 64: hipLaunchKernelGGL((gate_up_silu_kernel<F, XT, OT, ST, 64>), grid, dim3(256), lds, st, P); break;
+      case 32: hipLaunchKernelGGL((gate_up_silu_kernel<F, XT, OT, ST, 32>), grid, dim3(256), lds, st, P); break;
+      case 16: hipLaunchKernelGGL((gate_up_silu_kernel<F, XT, OT, ST, 16>), grid, dim3(256), lds, st, P); break;
       default: set_error("%s: invalid lanes per row %d", what, lpr); return TT_ERR_INVALID;
     }
     return check_launch(what);
+  };
+  auto go = [&](auto xt, auto ot, auto sdt) -> int {
+    if (w_format == TT_W_INT8) return launch(std::integral_constant<Fmt, Fmt::kInt8>{}, xt, ot, sdt);
+    return launch(std::integral_constant<Fmt, Fmt::kFp8>{}, xt, ot, sdt);
   };
   auto by_scale = [&](auto xt, auto ot) { return scale_dtype == TT_F16 ? go(xt, ot, f16_t{}) : go(xt, ot, float{}); };
   if (x_dtype == TT_F16) {

@@ -5,15 +5,21 @@
 
 using namespace tt;
 
-// fp8 weights with one scale per row, scales s_stride elements apart.
-static int scaled_matvec_impl(const void* weight, int64_t w_row_bytes, const void* scales, int scale_dtype,
-                              int64_t s_stride, const void* x, int x_dtype, void* out, int out_dtype, int64_t rows,
-                              int64_t cols, void* stream) {
+// Byte-per-element weight formats of the scaled GEMVs: TT_W_FP8 (float8_e4m3fn) or
+// TT_W_INT8 (two's-complement int8); both decode exactly to binary32.
+static bool scaled_format_ok(int w_format) { return w_format == TT_W_FP8 || w_format == TT_W_INT8; }
+
+// fp8 or int8 weights with one scale per row, scales s_stride elements apart.
+template <Fmt F>
+static int scaled_matvec_fmt(const void* weight, int64_t w_row_bytes, const void* scales, int scale_dtype,
+                             int64_t s_stride, const void* x, int x_dtype, void* out, int out_dtype, int64_t rows,
+                             int64_t cols, void* stream) {
   const char* what = "scaled_matvec";
   TT_REQUIRE(s_stride >= 1 && s_stride < (1LL << 31), "%s: bad scale stride", what);
   TT_REQUIRE(valid_act_dtype(x_dtype) && valid_out_dtype(out_dtype), "%s: bad dtype codes", what);
   TT_REQUIRE(scale_dtype == TT_F16 || scale_dtype == TT_F32, "%s: scales must be fp16 or fp32", what);
-  TT_REQUIRE(weight && aligned(weight, 16) && w_row_bytes % 16 == 0 && w_row_bytes >= cols, "%s: fp8 weights must be 16-byte aligned rows", what);
+  TT_REQUIRE(weight && aligned(weight, 16) && w_row_bytes % 16 == 0 && w_row_bytes >= cols,
+             "%s: weights must be 16-byte aligned rows", what);
   TT_REQUIRE(x && aligned(x, 16) && scales && out, "%s: null or misaligned pointer", what);
   TT_REQUIRE(rows > 0 && rows < (1 << 30), "%s: bad rows", what);
   int L;
@@ -38,16 +44,28 @@ static int scaled_matvec_impl(const void* weight, int64_t w_row_bytes, const voi
     L.s_row = (uint32_t)s_stride;
     L.rows = (int)rows;
     L.cols = (int)cols;
-    return lean_launch<Fmt::kFp8, SMode::kRow, float, 1>(x_dtype, lpr, L, 1, st, what);
+    return lean_launch<F, SMode::kRow, float, 1>(x_dtype, lpr, L, 1, st, what);
   }
-  if (scale_dtype == TT_F16) return launch_types<Fmt::kFp8, SMode::kRow, f16_t, 4>(x_dtype, out_dtype, Lg, lpr, P, 1, st, what);
-  return launch_types<Fmt::kFp8, SMode::kRow, float, 4>(x_dtype, out_dtype, Lg, lpr, P, 1, st, what);
+  if (scale_dtype == TT_F16) return launch_types<F, SMode::kRow, f16_t, 4>(x_dtype, out_dtype, Lg, lpr, P, 1, st, what);
+  return launch_types<F, SMode::kRow, float, 4>(x_dtype, out_dtype, Lg, lpr, P, 1, st, what);
 }
 
-extern "C" int tt_scaled_matvec(const void* weight, int64_t w_row_bytes, const void* scales, int scale_dtype,
-                                const void* x, int x_dtype, void* out, int out_dtype, int64_t rows, int64_t cols,
-                                void* stream) {
-  return scaled_matvec_impl(weight, w_row_bytes, scales, scale_dtype, 1, x, x_dtype, out, out_dtype, rows, cols, stream);
+static int scaled_matvec_impl(const void* weight, int w_format, int64_t w_row_bytes, const void* scales,
+                              int scale_dtype, int64_t s_stride, const void* x, int x_dtype, void* out, int out_dtype,
+                              int64_t rows, int64_t cols, void* stream) {
+  TT_REQUIRE(scaled_format_ok(w_format), "scaled_matvec: weights must be float8_e4m3fn or int8 (format %d)", w_format);
+  if (w_format == TT_W_INT8)
+    return scaled_matvec_fmt<Fmt::kInt8>(weight, w_row_bytes, scales, scale_dtype, s_stride, x, x_dtype, out,
+                                         out_dtype, rows, cols, stream);
+  return scaled_matvec_fmt<Fmt::kFp8>(weight, w_row_bytes, scales, scale_dtype, s_stride, x, x_dtype, out, out_dtype,
+                                      rows, cols, stream);
+}
+
+extern "C" int tt_scaled_matvec(const void* weight, int w_format, int64_t w_row_bytes, const void* scales,
+                                int scale_dtype, const void* x, int x_dtype, void* out, int out_dtype, int64_t rows,
+                                int64_t cols, void* stream) {
+  return scaled_matvec_impl(weight, w_format, w_row_bytes, scales, scale_dtype, 1, x, x_dtype, out, out_dtype, rows,
+                            cols, stream);
 }
 
 extern "C" int tt_multi_matvec_bias(int count, const void* const* weights, int w_dtype, const int64_t* w_row,
@@ -280,14 +298,15 @@ extern "C" int tt_matvec_argmax_noalloc(const void* weight, int w_dtype, int64_t
 // :4465-4497).  A block is a group of block / 32 chunks in the group-scale reduction
 // order; a block as wide as the row is the per-row-scale GEMV.
 
-extern "C" int tt_block_scaled_matvec(const void* weight, int64_t w_row_bytes, const void* scales, int scale_dtype,
-                                      int64_t s_row, int64_t s_block, int64_t block, const void* x, int x_dtype,
-                                      void* out, int out_dtype, int64_t rows, int64_t cols, void* stream) {
+template <Fmt F>
+static int block_scaled_fmt(const void* weight, int w_format, int64_t w_row_bytes, const void* scales, int scale_dtype,
+                            int64_t s_row, int64_t s_block, int64_t block, const void* x, int x_dtype, void* out,
+                            int out_dtype, int64_t rows, int64_t cols, void* stream) {
   const char* what = "block_scaled_matvec";
   TT_REQUIRE(valid_act_dtype(x_dtype) && valid_out_dtype(out_dtype), "%s: bad dtype codes", what);
   TT_REQUIRE(scale_dtype == TT_F16 || scale_dtype == TT_F32, "%s: scales must be fp16 or fp32", what);
   TT_REQUIRE(weight && aligned(weight, 16) && w_row_bytes % 16 == 0 && w_row_bytes >= cols,
-             "%s: fp8 weights must be 16-byte aligned rows", what);
+             "%s: weights must be 16-byte aligned rows", what);
   TT_REQUIRE(x && aligned(x, 16) && scales && out, "%s: null or misaligned pointer", what);
   TT_REQUIRE(rows > 0 && rows < (1 << 30), "%s: bad rows", what);
   TT_REQUIRE(cols > 0 && cols % 32 == 0 && cols <= 32768, "%s: cols must be a positive multiple of 32 up to 32768",
@@ -295,8 +314,8 @@ extern "C" int tt_block_scaled_matvec(const void* weight, int64_t w_row_bytes, c
   TT_REQUIRE(block > 0 && (block & (block - 1)) == 0, "%s: the scale block must be a power of two", what);
   TT_REQUIRE(s_row >= (cols + block - 1) / block || block >= cols, "%s: scale rows too short", what);
   if (block >= cols)   // one block per row: the per-row-scale GEMV (s_row is the row stride)
-    return scaled_matvec_impl(weight, w_row_bytes, scales, scale_dtype, s_row, x, x_dtype, out, out_dtype, rows,
-                              cols, stream);
+    return scaled_matvec_impl(weight, w_format, w_row_bytes, scales, scale_dtype, s_row, x, x_dtype, out, out_dtype,
+                              rows, cols, stream);
   TT_UNSUPPORTED(block >= 32 && block <= 2048, "%s: scale blocks of %lld columns (32 to 2048 supported)", what,
                  (long long)block);
   const int L = (int)(block / 32);
@@ -315,7 +334,7 @@ extern "C" int tt_block_scaled_matvec(const void* weight, int64_t w_row_bytes, c
     Lp.s_grp = (uint32_t)s_block;
     Lp.rows = (int)rows;
     Lp.cols = (int)cols;
-    return lean_launch_group<Fmt::kFp8, SMode::kGroup, float>(L, x_dtype, lpr, Lp, 1, st, what);
+    return lean_launch_group<F, SMode::kGroup, float>(L, x_dtype, lpr, Lp, 1, st, what);
   }
   GemvParams P{};
   P.nseg = 1;
@@ -323,8 +342,21 @@ extern "C" int tt_block_scaled_matvec(const void* weight, int64_t w_row_bytes, c
   P.x = x;
   P.cols = (int)cols;
   if (scale_dtype == TT_F16)
-    return launch_types<Fmt::kFp8, SMode::kGroup, f16_t, 2>(x_dtype, out_dtype, L, lpr, P, 1, st, what);
-  return launch_types<Fmt::kFp8, SMode::kGroup, float, 2>(x_dtype, out_dtype, L, lpr, P, 1, st, what);
+    return launch_types<F, SMode::kGroup, f16_t, 2>(x_dtype, out_dtype, L, lpr, P, 1, st, what);
+  return launch_types<F, SMode::kGroup, float, 2>(x_dtype, out_dtype, L, lpr, P, 1, st, what);
+}
+
+extern "C" int tt_block_scaled_matvec(const void* weight, int w_format, int64_t w_row_bytes, const void* scales,
+                                      int scale_dtype, int64_t s_row, int64_t s_block, int64_t block, const void* x,
+                                      int x_dtype, void* out, int out_dtype, int64_t rows, int64_t cols,
+                                      void* stream) {
+  TT_REQUIRE(scaled_format_ok(w_format), "block_scaled_matvec: weights must be float8_e4m3fn or int8 (format %d)",
+             w_format);
+  if (w_format == TT_W_INT8)
+    return block_scaled_fmt<Fmt::kInt8>(weight, w_format, w_row_bytes, scales, scale_dtype, s_row, s_block, block, x,
+                                        x_dtype, out, out_dtype, rows, cols, stream);
+  return block_scaled_fmt<Fmt::kFp8>(weight, w_format, w_row_bytes, scales, scale_dtype, s_row, s_block, block, x,
+                                     x_dtype, out, out_dtype, rows, cols, stream);
 }
 
 // ------------------------------------------------------------------ several fp8 matrices
@@ -332,12 +364,13 @@ extern "C" int tt_block_scaled_matvec(const void* weight, int64_t w_row_bytes, c
 // Two or three fp8 matrices with per-row scales over one activation vector, outputs
 // concatenated in matrix order (triton_kernels.py:1958-2071, wrapper :5119-5180).  Each
 // row has the single-matrix reduction order.
-extern "C" int tt_multi_scaled_matvec(int count, const void* const* weights, const int64_t* w_row_bytes,
-                                      const void* const* scales, int scale_dtype, const int64_t* s_stride,
-                                      const int64_t* rows, const void* x, int x_dtype, void* out, int out_dtype,
-                                      int64_t cols, void* stream) {
+extern "C" int tt_multi_scaled_matvec(int count, const void* const* weights, int w_format,
+                                      const int64_t* w_row_bytes, const void* const* scales, int scale_dtype,
+                                      const int64_t* s_stride, const int64_t* rows, const void* x, int x_dtype,
+                                      void* out, int out_dtype, int64_t cols, void* stream) {
   const char* what = "multi_scaled_matvec";
   TT_REQUIRE(count >= 1 && count <= 3, "%s: supports one to three matrices", what);
+  TT_REQUIRE(scaled_format_ok(w_format), "%s: weights must be float8_e4m3fn or int8 (format %d)", what, w_format);
   TT_REQUIRE(valid_act_dtype(x_dtype) && valid_out_dtype(out_dtype), "%s: bad dtype codes", what);
   TT_REQUIRE(scale_dtype == TT_F16 || scale_dtype == TT_F32, "%s: scales must be fp16 or fp32", what);
   TT_REQUIRE(x && aligned(x, 16) && out && weights && scales && rows && w_row_bytes && s_stride,
@@ -353,7 +386,7 @@ extern "C" int tt_multi_scaled_matvec(int count, const void* const* weights, con
   for (int i = 0; i < count; i++) {
     TT_REQUIRE(rows[i] > 0 && weights[i] && scales[i], "%s: matrix %d is empty or null", what, i);
     TT_REQUIRE(aligned(weights[i], 16) && w_row_bytes[i] % 16 == 0 && w_row_bytes[i] >= cols,
-               "%s: fp8 weights must be 16-byte aligned rows", what);
+               "%s: weights must be 16-byte aligned rows", what);
     TT_REQUIRE(s_stride[i] >= 1, "%s: bad scale stride", what);
     P.seg[i] = Seg{static_cast<const uint8_t*>(weights[i]), w_row_bytes[i], scales[i], s_stride[i], 0,
                    static_cast<char*>(out) + acc_rows * osz, (int)rows[i]};
@@ -364,6 +397,11 @@ extern "C" int tt_multi_scaled_matvec(int count, const void* const* weights, con
   P.cols = (int)cols;
   const int lpr = tt_gemv_lanes_per_row(cols / 32, 1);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (w_format == TT_W_INT8) {
+    if (scale_dtype == TT_F16)
+      return launch_types<Fmt::kInt8, SMode::kRow, f16_t, 4>(x_dtype, out_dtype, 1, lpr, P, 1, st, what);
+    return launch_types<Fmt::kInt8, SMode::kRow, float, 4>(x_dtype, out_dtype, 1, lpr, P, 1, st, what);
+  }
   if (scale_dtype == TT_F16) return launch_types<Fmt::kFp8, SMode::kRow, f16_t, 4>(x_dtype, out_dtype, 1, lpr, P, 1, st, what);
   return launch_types<Fmt::kFp8, SMode::kRow, float, 4>(x_dtype, out_dtype, 1, lpr, P, 1, st, what);
 }
@@ -410,13 +448,14 @@ int split_k_partials(const void* weight, int64_t w_row_bytes, const void* x, int
 // may be shorter or empty); slice s writes its binary32 row sums to partials[s, :] in the
 // single-matrix reduction order of its width, then one kernel adds the slices in order
 // and applies the optional per-row scale.  w_format: TT_F16 / TT_BF16 dense, or
-// TT_W_FP8 (float8_e4m3fn, then `scales` are the per-row fp32/fp16 scales).
+// TT_W_FP8 / TT_W_INT8 (float8_e4m3fn / int8, then `scales` are the per-row fp32/fp16
+// scales).
 extern "C" int tt_split_k_matvec(const void* weight, int w_format, int64_t w_row_bytes, const void* scales,
                                  int scale_dtype, const void* x, int x_dtype, void* out, int out_dtype, int64_t rows,
                                  int64_t cols, int split_k, float* partials, int64_t partials_capacity, void* stream) {
   const char* what = "split_k_matvec";
   TT_REQUIRE(split_k == 2 || split_k == 4 || split_k == 8, "%s: split_k must be 2, 4, or 8", what);
-  TT_REQUIRE(w_format == TT_F16 || w_format == TT_BF16 || w_format == TT_W_FP8, "%s: bad weight format", what);
+  TT_REQUIRE(w_format == TT_F16 || w_format == TT_BF16 || scaled_format_ok(w_format), "%s: bad weight format", what);
   TT_REQUIRE(valid_act_dtype(x_dtype) && valid_out_dtype(out_dtype), "%s: bad dtype codes", what);
   TT_REQUIRE(scales == nullptr || scale_dtype == TT_F16 || scale_dtype == TT_F32, "%s: bad scale dtype", what);
   TT_REQUIRE(weight && aligned(weight, 16) && w_row_bytes % 16 == 0 && x && aligned(x, 16) && out && partials,
@@ -438,6 +477,9 @@ extern "C" int tt_split_k_matvec(const void* weight, int w_format, int64_t w_row
     if (w_format == TT_BF16)
       return split_k_partials<Fmt::kBF16W>(weight, w_row_bytes, x, x_dtype, partials, rows, col0, width, slots,
                                           width, slot0, st, what);
+    if (w_format == TT_W_INT8)
+      return split_k_partials<Fmt::kInt8>(weight, w_row_bytes, x, x_dtype, partials, rows, col0, width, slots, width,
+                                          slot0, st, what);
     return split_k_partials<Fmt::kFp8>(weight, w_row_bytes, x, x_dtype, partials, rows, col0, width, slots, width,
                                        slot0, st, what);
   };

@@ -4,7 +4,8 @@
 // Semantics follow the reference's torch quantizers (thinruntime/gpu_runtime.py):
 //   tt_quantize_int4             quantize_to_int4_cpu :91-304 (symmetric least-squares
 //                                refinement; affine line fit with optional column
-//                                importance) and _quantize_int4_rows :6609-6700
+//                                importance and GPTQ passes) and _quantize_int4_rows
+//                                :6609-6700
 //   tt_quantize_fp8_rows         _quantize_fp8_rows :6551-6607, quantize_to_fp8_via_gpu :40-88
 //   tt_quantize_mxfp4_rows       _quantize_mxfp4_rows :6702-6812 (Walsh-Hadamard blocks,
 //                                sign flips, binary-residual error)
@@ -130,6 +131,7 @@ struct Q4Params {
   const void* src;
   int64_t src_row;       // elements between rows
   const float* importance;   // [cols] column weights (affine least squares) or null
+  const float* gptq;     // [groups, 32, 32] upper Cholesky factors of the inverse Hessians, or null
   uint8_t* packed;       // [rows, cols / 2]
   void* scales;          // fp16 (LSQ modes) or fp32; [rows, groups] or [rows, groups, 2]
   int rows, cols, group, groups;
@@ -208,7 +210,8 @@ __global__ __launch_bounds__(256) void int4_quant_kernel(const Q4Params P) {
         for (int k = 0; k < EPL; k++) pw = pr[k] ? pw + (double)w[k] : pw;
         wsum = wave_sum64(pw);
       }
-      for (int it = 0; it < 3; it++) {
+      // (scale, minimum) of the line regressed on the current codes
+      auto fit = [&]() {
         double pq = 0.0, px = 0.0;
 #pragma unroll
         for (int k = 0; k < EPL; k++) {
@@ -241,9 +244,41 @@ __global__ __launch_bounds__(256) void int4_quant_kernel(const Q4Params P) {
         const float den = fmaxf(wave_sum64(pd), kTiny);
         s = fmaxf(num / den, kTiny);
         mn = x_mean - s * q_mean;
+      };
+      for (int it = 0; it < 3; it++) {
+        fit();
         if (it < 2) {
 #pragma unroll
           for (int k = 0; k < EPL; k++) codes[k] = clampf(__builtin_rintf((x[k] - mn) / s), 0.0f, 15.0f);
+        }
+      }
+      if constexpr (EPL == 1) {
+        if (P.gptq != nullptr) {
+          // GPTQ passes over the 32 columns of the group (gpu_runtime.py:217-262): column
+          // c is quantized on the current line, and its error divided by U[c][c] is taken
+          // out of columns c.. through row c of U.  Lane j < 32 owns column j and keeps
+          // column j of U; the line is refitted after the first pass only.
+          const float* U = P.gptq + (int64_t)g * 1024;
+          const int j = lane & 31;
+          float ucol[32];
+#pragma unroll
+          for (int c = 0; c < 32; c++) ucol[c] = U[c * 32 + j];
+          for (int pass = 0; pass < 2; pass++) {
+            float adj = x[0];
+            float code = 0.0f;
+#pragma unroll
+            for (int c = 0; c < 32; c++) {
+              const float cur = __builtin_bit_cast(
+                  float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, adj), c));
+              const float cq = clampf(__builtin_rintf((cur - mn) / s), 0.0f, 15.0f);
+              const float qv = cq * s + mn;   // product and sum rounded separately (no contraction)
+              const float err = (cur - qv) / U[c * 33];
+              code = lane == c ? cq : code;
+              adj = lane > c ? adj - err * ucol[c] : adj;
+            }
+            codes[0] = code;
+            if (pass == 0) fit();
+          }
         }
       }
     }
@@ -588,8 +623,8 @@ int by_src_dtype(int dtype, const char* what, F&& f) {
 using namespace tt;
 
 extern "C" int tt_quantize_int4(const void* src, int src_dtype, int64_t rows, int64_t cols, int64_t src_row,
-                                int64_t group_size, int mode, const float* importance, uint8_t* packed, void* scales,
-                                void* stream) {
+                                int64_t group_size, int mode, const float* importance, const float* gptq_factors,
+                                uint8_t* packed, void* scales, void* stream) {
   const char* what = "quantize_int4";
   TT_REQUIRE(src && packed && scales, "%s: null pointer", what);
   TT_REQUIRE(mode >= TT_Q4_LSQ && mode <= TT_Q4_ROWS_AFFINE, "%s: unknown mode %d", what, mode);
@@ -602,8 +637,10 @@ extern "C" int tt_quantize_int4(const void* src, int src_dtype, int64_t rows, in
              "%s: affine least-squares INT4 needs the width to be a multiple of the group", what);
   TT_REQUIRE(importance == nullptr || mode == TT_Q4_LSQ_AFFINE, "%s: column importance applies to the affine fit only",
              what);
+  TT_REQUIRE(gptq_factors == nullptr || (mode == TT_Q4_LSQ_AFFINE && group_size == 32),
+             "%s: GPTQ factors apply to the affine fit with groups of 32 only", what);
   const int groups = (int)((cols + group_size - 1) / group_size);
-  Q4Params P{src, src_row, importance, packed, scales, (int)rows, (int)cols, (int)group_size, groups};
+  Q4Params P{src, src_row, importance, gptq_factors, packed, scales, (int)rows, (int)cols, (int)group_size, groups};
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t waves = rows * groups;
   TT_REQUIRE((waves + 3) / 4 < (1ll << 31), "%s: too many groups", what);

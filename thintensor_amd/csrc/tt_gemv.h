@@ -30,6 +30,7 @@ enum class Fmt : int {
   kQ1E8 = 7,      // 1-bit codebook {-1,+1}, E8M0 scale per 32-element block
   kQ2Aff = 8,     // 2-bit code c in [0,3], w = (c - z) * s per group
   kQ1Aff = 9,     // 1-bit code c in {0,1}, w = (c - z) * s per group
+  kInt8 = 10,     // int8 rows, y = (sum w*x) * s_row (or per block)
 };
 
 template <Fmt F> struct FmtInfo;
@@ -43,6 +44,7 @@ template <> struct FmtInfo<Fmt::kQ2E8> { static constexpr int kBytes = 8; };
 template <> struct FmtInfo<Fmt::kQ1E8> { static constexpr int kBytes = 4; };
 template <> struct FmtInfo<Fmt::kQ2Aff> { static constexpr int kBytes = 8; };
 template <> struct FmtInfo<Fmt::kQ1Aff> { static constexpr int kBytes = 4; };
+template <> struct FmtInfo<Fmt::kInt8> { static constexpr int kBytes = 32; };
 
 template <int B> struct Raw { uint32_t w[B / 4]; };
 
@@ -98,6 +100,7 @@ __device__ __forceinline__ void nib_pairs(uint32_t w, float off, h2& a, h2& b, h
 // them through v_fma_mix without a conversion.
 template <Fmt F> struct WVal { using T = _Float16; };
 template <> struct WVal<Fmt::kFp8> { using T = float; };
+template <> struct WVal<Fmt::kInt8> { using T = float; };
 template <> struct WVal<Fmt::kBF16W> { using T = float; };
 
 template <Fmt F>
@@ -133,6 +136,13 @@ __device__ __forceinline__ void decode_chunk(const Raw<FmtInfo<F>::kBytes>& r, t
       auto lo = __builtin_amdgcn_cvt_pk_f32_fp8(r.w[i], false);
       auto hi = __builtin_amdgcn_cvt_pk_f32_fp8(r.w[i], true);
       wv[4 * i + 0] = lo[0]; wv[4 * i + 1] = lo[1]; wv[4 * i + 2] = hi[0]; wv[4 * i + 3] = hi[1];
+    }
+  } else if constexpr (F == Fmt::kInt8) {
+    // 32 bytes, byte e = element e as a two's-complement integer; int8 -> f32 is exact.
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+#pragma unroll
+      for (int b = 0; b < 4; b++) wv[4 * i + b] = (float)(int8_t)(r.w[i] >> (8 * b));
     }
   } else if constexpr (F == Fmt::kF16W) {
 #pragma unroll

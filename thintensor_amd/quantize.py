@@ -101,8 +101,8 @@ def quantize_to_int4_cpu(
     """gpu_runtime.py:91-304: grouped INT4 with fp16 scales.  Symmetric: amax/7, codes
     in [-8, 7], one least-squares refit of the scale.  With THINTENSOR_AFFINE_INT4=1
     (and rows < 65536): a min/max line refitted by (importance-weighted) least squares,
-    codes in [0, 15], [scale, minimum] pairs.  The GPTQ covariance refinement is not
-    implemented here."""
+    codes in [0, 15], [scale, minimum] pairs; with ``input_covariance32`` (groups of 32)
+    two GPTQ passes then requantize each group column by column (:217-262)."""
     rows, cols = int(source.shape[0]), int(source.shape[1])
     if cols % 2:
         raise ValueError("expert INT4 requires an even input width")
@@ -110,8 +110,6 @@ def quantize_to_int4_cpu(
         raise ValueError("expert INT4 group size must be a positive power of two")
     groups = (cols + group_size - 1) // group_size
     affine = os.environ.get("THINTENSOR_AFFINE_INT4", "0") == "1" and rows < 65536
-    if input_covariance32 is not None:
-        raise NotImplementedError("the HIP INT4 quantizer does not implement the GPTQ covariance refinement")
     dev = _device_of(source)
     importance = None
     if input_rms is not None:
@@ -120,12 +118,38 @@ def quantize_to_int4_cpu(
                 f"INT4 input RMS shape {tuple(input_rms.shape)} does not match the projection width {(cols,)}"
             )
         importance = input_rms.to(device=dev).float().square().clamp_min_(1e-8).contiguous()
+    factors = None
+    if input_covariance32 is not None:
+        if group_size != 32:
+            raise ValueError("GPTQ covariance blocks currently require INT4 group size 32")
+        if tuple(input_covariance32.shape) != (groups, 32, 32):
+            raise ValueError(
+                f"INT4 covariance shape {tuple(input_covariance32.shape)} does not match {(groups, 32, 32)}"
+            )
+        factors = gptq_inverse_cholesky(input_covariance32).to(device=dev).contiguous()
     if affine and cols % group_size:
         raise ValueError("affine INT4 needs the input width to be a multiple of the group size")
     mode = _lib.Q4_LSQ_AFFINE if affine else _lib.Q4_LSQ
+    # the reference computes the factors in both modes and uses them in the affine fit only
     packed, scales = _int4(_on_device(source, dev), group_size, groups, mode,
-                           importance if affine else None, torch.float16)
+                           importance if affine else None, torch.float16, factors if affine else None)
     return _back(packed, source), _back(scales, source)
+
+
+def gptq_inverse_cholesky(input_covariance32: torch.Tensor) -> torch.Tensor:
+    """Per 32-column group the upper Cholesky factor of the inverse of the damped input
+    covariance, in binary32 on the host as the reference computes it
+    (gpu_runtime.py:130-150): H = cov + max(mean(diag H) * p, 1e-6) I with p =
+    THINTENSOR_GPTQ_DAMP_PERCENT (default 0.01), U = cholesky(inv(H), upper=True).
+    A [groups, 32, 32] set of 32 x 32 factorizations: set-up for the GPU passes, which
+    read U."""
+    hessian = input_covariance32.detach().to(device="cpu", dtype=torch.float32).clone()
+    damp_percent = float(os.environ.get("THINTENSOR_GPTQ_DAMP_PERCENT", "0.01"))
+    if damp_percent <= 0:
+        raise ValueError("THINTENSOR_GPTQ_DAMP_PERCENT must be positive")
+    damp = hessian.diagonal(dim1=1, dim2=2).mean(dim=1).mul(damp_percent).clamp_min_(1e-6)
+    hessian.diagonal(dim1=1, dim2=2).add_(damp[:, None])
+    return torch.linalg.cholesky(torch.linalg.inv(hessian), upper=True)
 
 
 def quantize_int4_rows(
@@ -148,7 +172,7 @@ def quantize_int4_rows(
     return _back(packed, source), _back(scales, source)
 
 
-def _int4(src, group_size, groups, mode, importance, scale_dtype):
+def _int4(src, group_size, groups, mode, importance, scale_dtype, factors=None):
     rows, cols = int(src.shape[0]), int(src.shape[1])
     if group_size not in (32, 64, 128, 256, 512):
         raise ValueError(f"INT4 group size {group_size} is not supported by the HIP quantizer (32..512, powers of two)")
@@ -156,7 +180,8 @@ def _int4(src, group_size, groups, mode, importance, scale_dtype):
     pair = mode in (_lib.Q4_LSQ_AFFINE, _lib.Q4_ROWS_AFFINE)
     scales = torch.empty((rows, groups, 2) if pair else (rows, groups), device=src.device, dtype=scale_dtype)
     rc = _lib.load().tt_quantize_int4(src.data_ptr(), _SRC_CODE[src.dtype], rows, cols, cols, group_size, mode,
-                                      importance.data_ptr() if importance is not None else None, packed.data_ptr(),
+                                      importance.data_ptr() if importance is not None else None,
+                                      factors.data_ptr() if factors is not None else None, packed.data_ptr(),
                                       scales.data_ptr(), _stream(src.device))
     _lib.check(rc, "quantize_int4")
     return packed, scales
