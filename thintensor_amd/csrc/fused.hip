@@ -185,6 +185,9 @@ __global__ __launch_bounds__(256) void fused_lean_kernel(const LeanFused P) {
   Raw<B> wc[ROWS];
   f16_t sc[NS];
   fetch(0, wc, sc);   // in bounds for inactive waves too (rows clamped)
+  // nothing that consumes the prologue's loads may be scheduled above round 0's weight
+  // loads: its wait would hold the weight stream back by a memory round trip
+  __builtin_amdgcn_sched_barrier(0);
 
   // ---- activation vector into LDS
   if constexpr (PRO == Pro::kLoad) {
@@ -232,6 +235,26 @@ __global__ __launch_bounds__(256) void fused_lean_kernel(const LeanFused P) {
   }
   lds_barrier();
   if (!active) return;
+
+  // the row this lane stores and, for the RoPE segments, its cos / sin table entries:
+  // requested now so that they arrive during the dot products instead of costing the
+  // epilogue a memory round trip (a non-RoPE lane reads a weight byte pair instead, so
+  // the loads are unconditional)
+  const int frow = rs_row<ROWS>(l, log2c(ROWS), 0) * SUBS + sub;
+  const bool fstore = (l >> log2c(ROWS)) == 0;
+  const int fr = lr0 + frow;
+  const bool ok = fstore && fr < srows;
+  bool odd = false;
+  const int ph = kind == kSegCache || !paired ? fr : paired_row<SUBS>(fr < srows ? fr : srows - 1, kind, P.head_dim, odd);
+  const int64_t pos = (int64_t)__builtin_amdgcn_readfirstlane(pos_raw);
+  const bool rope = (kind == kSegRopeOut || kind == kSegRopeCache) && pos >= 0 && pos < P.table_rows;
+  const int hd = P.head_dim > 0 ? P.head_dim : 1;   // 0 for launches without RoPE segments
+  const int rope_j = (ph % hd) - (odd ? (hd >> 1) : 0);
+  const uint16_t* cos_p = rope ? reinterpret_cast<const uint16_t*>(P.cos) + pos * P.table_row + rope_j
+                               : reinterpret_cast<const uint16_t*>(wlo);
+  const uint16_t* sin_p = rope ? reinterpret_cast<const uint16_t*>(P.sin) + pos * P.table_row + rope_j
+                               : reinterpret_cast<const uint16_t*>(wlo);
+  const uint32_t cos_raw = *cos_p, sin_raw = *sin_p;
 
   float acc[NVG];
 #pragma unroll
@@ -281,10 +304,6 @@ __global__ __launch_bounds__(256) void fused_lean_kernel(const LeanFused P) {
   else reduce_range<ROWS, 1, LPR>(acc);
 
   // ---- epilogue on the row held by this lane (same as gemv_kernel's fused epilogues)
-  const int frow = rs_row<ROWS>(l, log2c(ROWS), 0) * SUBS + sub;
-  const bool fstore = (l >> log2c(ROWS)) == 0;
-  const int fr = lr0 + frow;
-  const bool ok = fstore && fr < srows;
   float v = acc[0];
   if (kind == kSegPlain) {
     if (ok) {
@@ -293,8 +312,6 @@ __global__ __launch_bounds__(256) void fused_lean_kernel(const LeanFused P) {
     }
     return;
   }
-  bool odd = false;
-  const int ph = kind == kSegCache ? fr : paired_row<SUBS>(fr < srows ? fr : srows - 1, kind, P.head_dim, odd);
   if (S.bias != nullptr && ok) v = round_to<XT>(v) + to_f32(reinterpret_cast<const XT*>(S.bias)[ph]);
   const float val = round_to<XT>(v);
   const float pv = xor_partner<ROWS / 2 < 1 ? 1 : ROWS / 2>(val);   // the other half of the pair
@@ -302,14 +319,11 @@ __global__ __launch_bounds__(256) void fused_lean_kernel(const LeanFused P) {
     if (ok && !odd) store<XT>(reinterpret_cast<XT*>(S.out) + tok * P.token_out + ph, silu_mul_val(val, pv));
     return;
   }
-  const int64_t pos = (int64_t)__builtin_amdgcn_readfirstlane(pos_raw);
   const int D = P.head_dim;
   float o = val;
-  if (kind != kSegCache && pos >= 0 && pos < P.table_rows) {
-    const int half = D >> 1;
-    const int j = (ph % D) - (odd ? half : 0);
-    const float c = ld<XT>(P.cos, pos * P.table_row + j);
-    const float sn = ld<XT>(P.sin, pos * P.table_row + j);
+  if (rope) {
+    const float c = lo_f32<XT>(cos_raw);
+    const float sn = lo_f32<XT>(sin_raw);
     float o1, o2;
     if (odd) rope_pair<XT>(pv, val, c, sn, o1, o2);
     else rope_pair<XT>(val, pv, c, sn, o1, o2);
@@ -398,8 +412,9 @@ int launch_lean_lpr(const tt_fused_gemv* d, hipStream_t st) {
   const int per_batch = rpw * (64 / LPR);
   const LeanFused P = lean_params(d, per_batch);
   const int64_t waves = P.vtotal / per_batch;
-  const dim3 grid((unsigned)((waves + 3) / 4), (unsigned)(d->tokens > 1 ? d->tokens : 1));
   const size_t lds = (size_t)d->cols * 2;
+  const unsigned ytok = (unsigned)(d->tokens > 1 ? d->tokens : 1);
+  const dim3 grid((unsigned)((waves + 3) / 4), ytok);
   if (d->count > 1) {
     if (rpw == 4) hipLaunchKernelGGL((fused_lean_kernel<F, XT, LPR, 4, PRO, true>), grid, dim3(256), lds, st, P);
     else hipLaunchKernelGGL((fused_lean_kernel<F, XT, LPR, 2, PRO, true>), grid, dim3(256), lds, st, P);

@@ -31,7 +31,8 @@ struct CombineSrc {
   int tokens, max_tokens, max_chunks;
   uint16_t* xout;              // optional: workgroup 0 writes the combined activation here
 };
-constexpr int kCombineChunks = 16;   // chunks whose partials are requested with the first weights
+constexpr int kCombineChunks = 12;   // chunks whose partials are requested with the first weights (48 loads: with
+                                     // the weights under the 63 loads a wave can have outstanding)
 
 template <typename XT, int LPR, int ROWS, int XM, int PFR>
 __global__ __launch_bounds__(256) void int4g128_kernel(const uint8_t* __restrict__ W, uint32_t w_row,
@@ -93,19 +94,17 @@ __global__ __launch_bounds__(256) void int4g128_kernel(const uint8_t* __restrict
     cpm = C.pm + (int64_t)h * C.max_chunks;
     cpl = C.pl + (int64_t)h * C.max_chunks;
     cpo = reinterpret_cast<const f32x4*>(C.po + (int64_t)h * C.max_chunks * 64 + 8 * (cp & 7));
-    // chunks past the scratch are not requested (a uniform test on a kernel argument:
-    // the loads still go out in one batch); the active count never exceeds the scratch
+    // chunks past the scratch re-read its last chunk (values unused: the active count
+    // never exceeds the scratch, which holds at least one chunk).  The loads are
+    // unconditional: a load under a branch leaves a copy at the join that waits for it,
+    // and that wait would hold back every later load by a memory round trip.
 #pragma unroll
     for (int u = 0; u < kCB; u++) {
-      if (u < C.max_chunks) {
-        cm[u] = cpm[u];
-        cl[u] = cpl[u];
-        co[u][0] = cpo[u * 16];
-        co[u][1] = cpo[u * 16 + 1];
-      } else {
-        cm[u] = cl[u] = 0.0f;
-        co[u][0] = co[u][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      }
+      const int uc = u < C.max_chunks ? u : C.max_chunks - 1;
+      cm[u] = cpm[uc];
+      cl[u] = cpl[uc];
+      co[u][0] = cpo[uc * 16];
+      co[u][1] = cpo[uc * 16 + 1];
     }
     ctok = C.tokens_dev ? C.tokens_dev[0] + C.tokens : C.tokens;
   }

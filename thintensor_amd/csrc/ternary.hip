@@ -11,10 +11,10 @@
 //   * E8M0 scales [E, rows, G] as a separate tensor: w = (digit - 1) * |w| * 2^(e - 127).
 //
 // Work split.  Five groups are exactly 32 digit bytes (lcm(5, 32) = 160 columns), so
-// the unit of work is an item = (row, 160-column chunk): 32 digit bytes, a 15-bit
-// field of magnitude selectors and five scale bytes.  A workgroup of 128 threads owns
-// `rpw` rows of one selected slot and hands its rpw * chunks items to its threads in
-// turn, two items' loads in flight per thread before either is used.  The slot's
+// the unit of work is an item = (two consecutive rows, 160-column chunk): per row 32
+// digit bytes, a 15-bit field of magnitude selectors and five scale bytes.  A workgroup
+// of 128 threads owns `rpw` rows of one selected slot and hands its items to its
+// threads in turn; every activation read from LDS feeds both rows' chains.  The slot's
 // activations are staged once per workgroup in LDS as fp32, together with the group
 // sums of x and a 256-entry table that expands a digit byte into its five digits as
 // bytes (read back with v_cvt_f32_ubyte).  Rows are not 4-byte aligned (row_bytes is
@@ -38,7 +38,13 @@ namespace {
 constexpr int kChunk = 160;                   // columns per item
 constexpr int kMaxCols = 8192;
 constexpr int kThreads = 128;
-constexpr int kBatch = 2;                     // items whose loads are in flight together
+// Measured at the gpt-oss expert shapes (gate/up 5760 x 2880, down 2880 x 2880, four
+// slots): two rows per item with one item's loads in flight (21.2 / 13.5 us) beat one row
+// per item with two (24.2 / 15.2 us), three (23.9 / 15.8 us), and four rows per item
+// (24.8 / 21.3 us: occupancy 2).  The activation reads from LDS are the main cost; an
+// item's reads feed every row of the item.
+constexpr int kRowsPerItem = 2;
+constexpr int kBatch = 1;                     // items whose loads are in flight together
 
 struct TernParams {
   const uint8_t* w;         // [E, rows, row_bytes]
@@ -72,15 +78,17 @@ __device__ __forceinline__ const uint8_t* align4(const uint8_t* a) {
 // |w| * 2 for selector m: {1, 2, 3, 4, 6, 8, 12, 0}.
 __device__ __forceinline__ float magnitude(uint32_t m) { return (float)((0x0C864321u >> (4 * m)) & 15u) * 0.5f; }
 
-struct Item {
+// One row's share of an item.
+struct ItemRow {
   uint32_t d[9];   // dwords covering the 32 digit bytes
   uint32_t m[3];   // dwords covering the selector field
   uint32_t s[3];   // dwords covering the five scale bytes
   uint32_t shd, shm, shs;
-  int mbit;
 };
 
-template <typename XT, typename OT>
+// RP rows per item: the item's activation reads from LDS feed the fma chains of RP
+// rows (each chain in the single-row order).
+template <typename XT, typename OT, int RP>
 __global__ __launch_bounds__(kThreads) void ternary_selected_kernel(TernParams P) {
   extern __shared__ __attribute__((aligned(16))) float smem[];
   float* xs = smem;                                     // chunks * 160 (zero past cols)
@@ -92,20 +100,32 @@ __global__ __launch_bounds__(kThreads) void ternary_selected_kernel(TernParams P
   const int nrows = P.rows - row0 < P.rpw ? P.rows - row0 : P.rpw;
   OT* out = reinterpret_cast<OT*>(P.out) + (int64_t)slot * P.out_slot + row0;
   const int64_t e = load_expert(P.experts, P.ishift, slot);
+  const XT* xv = reinterpret_cast<const XT*>(P.x) + (int64_t)slot * P.x_slot;
+  // 16-byte activation loads, four per thread in flight (cols is a multiple of 32 and
+  // the slot's row is 16-byte aligned), then zeros up to whole chunks.  The first four
+  // go out with the expert id, before the id is tested.
+  const int nvec = P.cols / 8;
+  uint4 t0[4];
+#pragma unroll
+  for (int u = 0; u < 4; u++) {
+    const int v = (int)threadIdx.x + u * kThreads < nvec ? (int)threadIdx.x + u * kThreads : nvec - 1;
+    t0[u] = reinterpret_cast<const uint4*>(xv)[v];
+  }
   if (e < 0 || e >= P.n_experts) {                      // uniform over the workgroup
     for (int r = threadIdx.x; r < nrows; r += kThreads) store(out + r, __builtin_nanf(""));
     return;
   }
-  const XT* xv = reinterpret_cast<const XT*>(P.x) + (int64_t)slot * P.x_slot;
-  // 16-byte activation loads, four per thread in flight (cols is a multiple of 32 and
-  // the slot's row is 16-byte aligned), then zeros up to whole chunks
-  const int nvec = P.cols / 8;
   for (int v0 = threadIdx.x; v0 < nvec; v0 += 4 * kThreads) {
     uint4 t[4];
+    if (v0 == (int)threadIdx.x) {
 #pragma unroll
-    for (int u = 0; u < 4; u++) {
-      const int v = v0 + u * kThreads < nvec ? v0 + u * kThreads : nvec - 1;
-      t[u] = reinterpret_cast<const uint4*>(xv)[v];
+      for (int u = 0; u < 4; u++) t[u] = t0[u];
+    } else {
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        const int v = v0 + u * kThreads < nvec ? v0 + u * kThreads : nvec - 1;
+        t[u] = reinterpret_cast<const uint4*>(xv)[v];
+      }
     }
 #pragma unroll
     for (int u = 0; u < 4; u++) {
@@ -144,77 +164,105 @@ __global__ __launch_bounds__(kThreads) void ternary_selected_kernel(TernParams P
   const uint8_t* slast = align4(P.s_end - 1);
   const uint8_t* wexp = P.w + e * P.w_expert;
   const uint8_t* sexp = P.s + e * P.s_expert;
-  const int items = nrows * P.chunks;
+  // items: (RP consecutive rows, chunk); the last item's missing rows read the last row
+  const int rgroups = (nrows + RP - 1) / RP;
+  const int items = rgroups * P.chunks;
   for (int base = threadIdx.x; base < items; base += kThreads * kBatch) {
-    Item it[kBatch];
+    ItemRow it[kBatch][RP];
+    int mbit[kBatch];
 #pragma unroll
     for (int u = 0; u < kBatch; u++) {
       int item = base + u * kThreads;
       item = item < items ? item : items - 1;
-      const int r = item / P.chunks, c = item - r * P.chunks;
-      const uint8_t* wrow = wexp + (int64_t)(row0 + r) * P.w_row;
-      const uint8_t* a = wrow + 32 * c;
-      const uint8_t* a4 = align4(a);
-      it[u].shd = (uint32_t)(a - a4);
+      const int rg = item / P.chunks, c = item - rg * P.chunks;
+      const int mb = 15 * c;
+      mbit[u] = mb & 7;
 #pragma unroll
-      for (int i = 0; i < 9; i++) it[u].d[i] = ld_u32(a4 + 4 * i, wlast);
-      const int mbit = 15 * c;
-      const uint8_t* ma = wrow + P.tbytes + (mbit >> 3);
-      const uint8_t* ma4 = align4(ma);
-      it[u].shm = (uint32_t)(ma - ma4);
-      it[u].mbit = mbit & 7;
+      for (int k = 0; k < RP; k++) {
+        const int r = RP * rg + k < nrows ? RP * rg + k : nrows - 1;
+        ItemRow& ir = it[u][k];
+        const uint8_t* wrow = wexp + (int64_t)(row0 + r) * P.w_row;
+        const uint8_t* a = wrow + 32 * c;
+        const uint8_t* a4 = align4(a);
+        ir.shd = (uint32_t)(a - a4);
 #pragma unroll
-      for (int i = 0; i < 3; i++) it[u].m[i] = ld_u32(ma4 + 4 * i, wlast);
-      const uint8_t* sa = sexp + (int64_t)(row0 + r) * P.s_row + 5 * c;
-      const uint8_t* sa4 = align4(sa);
-      it[u].shs = (uint32_t)(sa - sa4);
+        for (int i = 0; i < 9; i++) ir.d[i] = ld_u32(a4 + 4 * i, wlast);
+        const uint8_t* ma = wrow + P.tbytes + (mb >> 3);
+        const uint8_t* ma4 = align4(ma);
+        ir.shm = (uint32_t)(ma - ma4);
 #pragma unroll
-      for (int i = 0; i < 3; i++) it[u].s[i] = ld_u32(sa4 + 4 * i, slast);
+        for (int i = 0; i < 3; i++) ir.m[i] = ld_u32(ma4 + 4 * i, wlast);
+        const uint8_t* sa = sexp + (int64_t)(row0 + r) * P.s_row + 5 * c;
+        const uint8_t* sa4 = align4(sa);
+        ir.shs = (uint32_t)(sa - sa4);
+#pragma unroll
+        for (int i = 0; i < 3; i++) ir.s[i] = ld_u32(sa4 + 4 * i, slast);
+      }
     }
 #pragma unroll
     for (int u = 0; u < kBatch; u++) {
       const int item = base + u * kThreads;
       if (item >= items) break;
-      const int r = item / P.chunks, c = item - r * P.chunks;
+      const int rg = item / P.chunks, c = item - rg * P.chunks;
       const float* xc = xs + kChunk * c;
-      float A[5] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+      float A[RP][5];
+#pragma unroll
+      for (int k = 0; k < RP; k++)
+#pragma unroll
+        for (int g = 0; g < 5; g++) A[k][g] = 0.0f;
 #pragma unroll
       for (int wi = 0; wi < 8; wi++) {
-        const uint32_t word = __builtin_amdgcn_alignbyte(it[u].d[wi + 1], it[u].d[wi], it[u].shd);
+        uint32_t word[RP];
+#pragma unroll
+        for (int k = 0; k < RP; k++)
+          word[k] = __builtin_amdgcn_alignbyte(it[u][k].d[wi + 1], it[u][k].d[wi], it[u][k].shd);
 #pragma unroll
         for (int bi = 0; bi < 4; bi++) {
           const int b = 4 * wi + bi;
-          const uint2 ent = dlut[(word >> (8 * bi)) & 0xffu];
+          uint2 ent[RP];
+#pragma unroll
+          for (int k = 0; k < RP; k++) ent[k] = dlut[(word[k] >> (8 * bi)) & 0xffu];
 #pragma unroll
           for (int i = 0; i < 5; i++) {
             const int t = 5 * b + i;
-            const uint32_t src = i < 4 ? ent.x : ent.y;
-            const float dg = (float)((src >> (8 * (i & 3))) & 0xffu);
-            A[t / 32] = __builtin_fmaf(dg, xc[t], A[t / 32]);
+            const float xt = xc[t];
+#pragma unroll
+            for (int k = 0; k < RP; k++) {
+              const uint32_t src = i < 4 ? ent[k].x : ent[k].y;
+              const float dg = (float)((src >> (8 * (i & 3))) & 0xffu);
+              A[k][t / 32] = __builtin_fmaf(dg, xt, A[k][t / 32]);
+            }
           }
         }
         // finish each word's fma chains before the next word's table and activation
         // reads (bounds the registers that hold LDS results; without it the compiler
         // issues every read of the item first and keeps all 160 activations live)
-        asm volatile("" : "+v"(A[0]), "+v"(A[1]), "+v"(A[2]), "+v"(A[3]), "+v"(A[4])::"memory");
-      }
-      const uint32_t mlo = __builtin_amdgcn_alignbyte(it[u].m[1], it[u].m[0], it[u].shm);
-      const uint32_t mhi = __builtin_amdgcn_alignbyte(it[u].m[2], it[u].m[1], it[u].shm);
-      const uint32_t mfield = (uint32_t)((((uint64_t)mhi << 32) | mlo) >> it[u].mbit) & 0x7fffu;
-      const uint32_t slo = __builtin_amdgcn_alignbyte(it[u].s[1], it[u].s[0], it[u].shs);
-      const uint32_t shi = __builtin_amdgcn_alignbyte(it[u].s[2], it[u].s[1], it[u].shs);
-      float chunk = 0.0f;
 #pragma unroll
-      for (int g = 0; g < 5; g++) {
-        if (5 * c + g < P.groups) {
-          const uint32_t m = (mfield >> (3 * g)) & 7u;
-          const int ex = (int)(((g < 4 ? slo : shi) >> (8 * (g & 3))) & 0xffu);
-          const float v = magnitude(m) * pow2i(ex - 127);
-          const float p = A[g] - bsum[5 * c + g];
-          chunk = chunk + v * p;
-        }
+        for (int k = 0; k < RP; k++)
+          asm volatile("" : "+v"(A[k][0]), "+v"(A[k][1]), "+v"(A[k][2]), "+v"(A[k][3]), "+v"(A[k][4])::"memory");
       }
-      part[r * P.chunks + c] = chunk;
+#pragma unroll
+      for (int k = 0; k < RP; k++) {
+        if (RP * rg + k >= nrows) break;
+        const ItemRow& ir = it[u][k];
+        const uint32_t mlo = __builtin_amdgcn_alignbyte(ir.m[1], ir.m[0], ir.shm);
+        const uint32_t mhi = __builtin_amdgcn_alignbyte(ir.m[2], ir.m[1], ir.shm);
+        const uint32_t mfield = (uint32_t)((((uint64_t)mhi << 32) | mlo) >> mbit[u]) & 0x7fffu;
+        const uint32_t slo = __builtin_amdgcn_alignbyte(ir.s[1], ir.s[0], ir.shs);
+        const uint32_t shi = __builtin_amdgcn_alignbyte(ir.s[2], ir.s[1], ir.shs);
+        float chunk = 0.0f;
+#pragma unroll
+        for (int g = 0; g < 5; g++) {
+          if (5 * c + g < P.groups) {
+            const uint32_t m = (mfield >> (3 * g)) & 7u;
+            const int ex = (int)(((g < 4 ? slo : shi) >> (8 * (g & 3))) & 0xffu);
+            const float v = magnitude(m) * pow2i(ex - 127);
+            const float p = A[k][g] - bsum[5 * c + g];
+            chunk = chunk + v * p;
+          }
+        }
+        part[(RP * rg + k) * P.chunks + c] = chunk;
+      }
     }
   }
   __syncthreads();
@@ -238,10 +286,11 @@ size_t lds_bytes(int chunks, int rpw) {
 
 template <typename XT>
 int launch_out(int out_dtype, const TernParams& P, dim3 grid, size_t lds, hipStream_t st) {
+  constexpr int RP = kRowsPerItem;
   switch (out_dtype) {
-    case TT_F16: hipLaunchKernelGGL((ternary_selected_kernel<XT, f16_t>), grid, dim3(kThreads), lds, st, P); break;
-    case TT_BF16: hipLaunchKernelGGL((ternary_selected_kernel<XT, bf16_t>), grid, dim3(kThreads), lds, st, P); break;
-    default: hipLaunchKernelGGL((ternary_selected_kernel<XT, float>), grid, dim3(kThreads), lds, st, P); break;
+    case TT_F16: hipLaunchKernelGGL((ternary_selected_kernel<XT, f16_t, RP>), grid, dim3(kThreads), lds, st, P); break;
+    case TT_BF16: hipLaunchKernelGGL((ternary_selected_kernel<XT, bf16_t, RP>), grid, dim3(kThreads), lds, st, P); break;
+    default: hipLaunchKernelGGL((ternary_selected_kernel<XT, float, RP>), grid, dim3(kThreads), lds, st, P); break;
   }
   return check_launch("mxfp_ternary_selected_matvec");
 }
