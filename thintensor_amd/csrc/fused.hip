@@ -134,14 +134,35 @@ __global__ __launch_bounds__(256) void fused_lean_kernel(const LeanFused P) {
   const int lr0 = v0 - S.vbegin;
   const bool paired = kind == kSegRopeOut || kind == kSegRopeCache || kind == kSegSilu;
 
-  // physical row (and matrix) of segment-local virtual row v
-  auto phys = [&](int v, bool& up) -> int {
-    up = false;
-    if (!paired) return v;
-    bool odd;
-    const int ph = paired_row<SUBS>(v, kind, P.head_dim, odd);
-    up = odd && kind == kSegSilu;
-    return ph;
+  // Physical row (and matrix) of row vr (0 .. ROWS * SUBS - 1) of this wave's block, the
+  // mapping of paired_row: the block starts on a pair boundary (lr0 is a multiple of
+  // ROWS * SUBS), so its rows are a few shifts away from its first pair P0, and for the
+  // RoPE segments the block's pairs lie in one head (the host checks that half a head
+  // is a whole number of blocks), whose index and in-head offset are one scalar
+  // division per wave.  Rows past the segment read the block's first row, and a block
+  // past the segment reads row 0 (in bounds; the values are never used).
+  const int P0 = lr0 >> 1;
+  const int half = P.head_dim >> 1;
+  int h0 = 0, j0 = 0;
+  if (kind == kSegRopeOut || kind == kSegRopeCache) {
+    h0 = (int)((uint32_t)P0 / (uint32_t)half);
+    j0 = P0 - h0 * half;
+  }
+  const bool any_row = lr0 < srows;
+  const bool silu = kind == kSegSilu;
+  const int rope_base = h0 * P.head_dim + j0;   // row of the block's first pair (RoPE segments)
+  // (selects only, no branches: the row addressing stays a short straight run ahead of
+  // the first weight loads)
+  auto phys = [&](int vr, bool valid, bool& up, bool& odd) -> int {
+    vr = valid ? vr : 0;
+    const int blk = vr / (2 * SUBS), rem = vr % (2 * SUBS);   // SUBS is a power of two
+    const bool o = paired && rem >= SUBS;
+    const int poff = blk * SUBS + (o ? rem - SUBS : rem);
+    const int pr = silu ? P0 + poff : rope_base + poff + (o ? half : 0);
+    const int ph = paired ? pr : lr0 + vr;
+    odd = o;
+    up = o && silu && any_row;
+    return any_row ? ph : 0;
   };
   // both matrices' base pointers in scalar registers, so the per-lane choice between them
   // is a select and not a vector load of the chosen kernel argument
@@ -151,10 +172,10 @@ __global__ __launch_bounds__(256) void fused_lean_kernel(const LeanFused P) {
   bool rv[ROWS];
 #pragma unroll
   for (int i = 0; i < ROWS; i++) {
-    const int v = lr0 + i * SUBS + sub;
-    rv[i] = v < srows;
-    bool up;
-    const int ph = phys(rv[i] ? v : srows - 1, up);
+    const int vr = i * SUBS + sub;
+    rv[i] = lr0 + vr < srows;
+    bool up, odd;
+    const int ph = phys(vr, rv[i], up, odd);
     wrow[i] = (up ? whi : wlo) + (size_t)ph * S.w_row;
   }
   const f16_t* srow[NS];
@@ -164,10 +185,10 @@ __global__ __launch_bounds__(256) void fused_lean_kernel(const LeanFused P) {
     const f16_t* const shi = uniform_ptr(S.s2);
 #pragma unroll
     for (int k = 0; k < NS; k++) {
-      const int v = lr0 + rs_row<ROWS>(l, GLEV, k) * SUBS + sub;
-      sv[k] = v < srows;
-      bool up;
-      const int ph = phys(sv[k] ? v : srows - 1, up);
+      const int vr = rs_row<ROWS>(l, GLEV, k) * SUBS + sub;
+      sv[k] = lr0 + vr < srows;
+      bool up, odd;
+      const int ph = phys(vr, sv[k], up, odd);
       srow[k] = (up ? shi : slo) + (size_t)ph * S.s_row;
     }
   }
@@ -244,8 +265,8 @@ __global__ __launch_bounds__(256) void fused_lean_kernel(const LeanFused P) {
   const bool fstore = (l >> log2c(ROWS)) == 0;
   const int fr = lr0 + frow;
   const bool ok = fstore && fr < srows;
-  bool odd = false;
-  const int ph = kind == kSegCache || !paired ? fr : paired_row<SUBS>(fr < srows ? fr : srows - 1, kind, P.head_dim, odd);
+  bool odd = false, up_unused;
+  const int ph = phys(frow, fr < srows, up_unused, odd);
   const int64_t pos = (int64_t)__builtin_amdgcn_readfirstlane(pos_raw);
   const bool rope = (kind == kSegRopeOut || kind == kSegRopeCache) && pos >= 0 && pos < P.table_rows;
   const int hd = P.head_dim > 0 ? P.head_dim : 1;   // 0 for launches without RoPE segments
@@ -392,7 +413,9 @@ LeanFused lean_params(const tt_fused_gemv* d, int per_batch) {
 }
 
 // The lean kernel covers int4 g128 and dense segments whose operands fit 32-bit
-// offsets and whose activation vector fits the register-held prologue.
+// offsets and whose activation vector fits the register-held prologue.  With RoPE
+// segments half a head must hold whole wave blocks of pairs (at most 4 rows per wave
+// times 4 lane groups, i.e. 8 pairs): head_dim a multiple of 16.
 bool lean_fits(const tt_fused_gemv* d) {
   if (d->cols > 4096) return false;
   for (int i = 0; i < d->count; i++) {
@@ -400,6 +423,7 @@ bool lean_fits(const tt_fused_gemv* d) {
     const int64_t rows = g.rows;
     if (g.w_row_bytes >= ((int64_t)1 << 31) || rows * g.w_row_bytes >= ((int64_t)1 << 31)) return false;
     if (g.s_row >= ((int64_t)1 << 30)) return false;
+    if ((g.kind == TT_SEG_ROPE_OUT || g.kind == TT_SEG_ROPE_CACHE) && d->head_dim % 16 != 0) return false;
   }
   return true;
 }
