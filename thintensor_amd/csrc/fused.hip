@@ -360,10 +360,12 @@ __global__ __launch_bounds__(256) void fused_lean_kernel(const LeanFused P) {
   }
 }
 
-// Rows per wave of the lean fused kernel (paired segments need two).
+// Rows per wave of the lean fused kernel (paired segments need two).  Eight for the
+// largest launches (the 1B gate/up, 16384 virtual rows: 9.06 -> 8.69 us against four):
+// half the waves, each prologue shared by twice the rows.
 inline int fused_rows_per_wave(int64_t vrows, int lpr) {
   const int64_t groups = vrows * lpr / 64;
-  return groups >= 16384 ? 4 : 2;
+  return groups >= 16384 ? 8 : (groups >= 8192 ? 4 : 2);
 }
 
 LeanFused lean_params(const tt_fused_gemv* d, int per_batch) {
@@ -440,10 +442,12 @@ int launch_lean_lpr(const tt_fused_gemv* d, hipStream_t st) {
   const unsigned ytok = (unsigned)(d->tokens > 1 ? d->tokens : 1);
   const dim3 grid((unsigned)((waves + 3) / 4), ytok);
   if (d->count > 1) {
-    if (rpw == 4) hipLaunchKernelGGL((fused_lean_kernel<F, XT, LPR, 4, PRO, true>), grid, dim3(256), lds, st, P);
+    if (rpw == 8) hipLaunchKernelGGL((fused_lean_kernel<F, XT, LPR, 8, PRO, true>), grid, dim3(256), lds, st, P);
+    else if (rpw == 4) hipLaunchKernelGGL((fused_lean_kernel<F, XT, LPR, 4, PRO, true>), grid, dim3(256), lds, st, P);
     else hipLaunchKernelGGL((fused_lean_kernel<F, XT, LPR, 2, PRO, true>), grid, dim3(256), lds, st, P);
   } else {
-    if (rpw == 4) hipLaunchKernelGGL((fused_lean_kernel<F, XT, LPR, 4, PRO, false>), grid, dim3(256), lds, st, P);
+    if (rpw == 8) hipLaunchKernelGGL((fused_lean_kernel<F, XT, LPR, 8, PRO, false>), grid, dim3(256), lds, st, P);
+    else if (rpw == 4) hipLaunchKernelGGL((fused_lean_kernel<F, XT, LPR, 4, PRO, false>), grid, dim3(256), lds, st, P);
     else hipLaunchKernelGGL((fused_lean_kernel<F, XT, LPR, 2, PRO, false>), grid, dim3(256), lds, st, P);
   }
   return check_launch(kWhat);
