@@ -81,8 +81,9 @@ int selected_e8(const char* what, Fmt fmt, const void* packed, int64_t w_expert_
 // with one accumulator each; the first tree level over them is taken in
 // the lane and the rest over the row's Q = P / VP lanes, so the bits are those of the
 // contract.  Chunk x sums (sequential from +0) are computed once per workgroup; x sits
-// in LDS with 16-byte piece k of group g at slot 8g + (k xor g mod 8), so the row's
-// lanes, which read consecutive groups, spread over the banks.
+// in LDS with 16-byte piece k of group g at slot 9g + k: one pad piece per group puts
+// the row's lanes, which read consecutive groups, on distinct banks, and a lane's pieces
+// are immediate offsets from one address.
 struct Aff16Params {
   const uint8_t* w;
   const uint16_t* s;      // fp16 (scale, zero) pairs
@@ -149,22 +150,19 @@ __global__ __launch_bounds__(256) void affine16_kernel(const Aff16Params A) {
 #pragma unroll
   for (int k = 0; k < PF; k++) fetch(k, ring[k]);
 
-  // x into LDS (swizzled pieces), then the chunk sums
+  // x into LDS (padded pieces), then the chunk sums
   const int xn = A.cols >> 3;
   const uint4* xg = reinterpret_cast<const uint4*>(A.x);
-  for (int i = threadIdx.x; i < xn; i += 256) {
-    const int g = i >> 3, k = i & 7;
-    x_lds[8 * g + (k ^ (g & 7))] = xg[i];
-  }
+  for (int i = threadIdx.x; i < xn; i += 256) x_lds[9 * (i >> 3) + (i & 7)] = xg[i];
   __syncthreads();
-  float* xsum = reinterpret_cast<float*>(x_lds + xn);
+  float* xsum = reinterpret_cast<float*>(x_lds + xn + (A.cols >> 6));
   for (int c = threadIdx.x; c < (A.cols >> 5); c += 256) {
     const int g = c >> 1;
     float t = 0.0f;
 #pragma unroll
     for (int k4 = 0; k4 < 4; k4++) {
       const int k = 4 * (c & 1) + k4;
-      const uint4 v = x_lds[8 * g + (k ^ (g & 7))];
+      const uint4 v = x_lds[9 * g + k];
       const uint32_t wd[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
       for (int e = 0; e < 8; e++) t = t + ((e & 1) ? hi_f32<XT>(wd[e >> 1]) : lo_f32<XT>(wd[e >> 1]));
@@ -193,7 +191,7 @@ __global__ __launch_bounds__(256) void affine16_kernel(const Aff16Params A) {
 #pragma unroll
         for (int k4 = 0; k4 < 4; k4++) {
           const int k = 4 * h + k4;
-          const uint4 xv4 = x_lds[8 * gc + (k ^ (gc & 7))];
+          const uint4 xv4 = x_lds[9 * gc + k];
           xw[4 * k4] = xv4.x; xw[4 * k4 + 1] = xv4.y; xw[4 * k4 + 2] = xv4.z; xw[4 * k4 + 3] = xv4.w;
         }
         Raw<CB> raw[RPL];
@@ -235,19 +233,24 @@ __global__ __launch_bounds__(256) void affine16_kernel(const Aff16Params A) {
   }
 }
 
-// Measured at the cfg2 shapes: one group and one row per lane with two rounds in flight
-// was the fastest of {VP 1, 2} x {rows per lane 1, 2} x {2, 4 rounds in flight} for
-// both formats (q2 17920 x 5120 14.1 us, q1 5120 x 5120 6.6 us); the kernel is bound by
-// its VALU issue (v_fma_mix_f32 issues at half the rate of v_fma_f32 on this part).
-constexpr int kAffVP = 1, kAffRPL = 1, kAffPF = 2;
+// Measured at the cfg2 shapes: one group and one row per lane was the fastest of
+// {VP 1, 2} x {rows per lane 1, 2} for both formats.
+// Launches of several workgroups per CU request five rounds up front (17920 x 5120: q2
+// 14.26 -> 14.01 us, q1 12.81 -> 12.42 us); one-round launches keep two (five there:
+// q2 5120 x 5120 7.41 -> 7.70 us).
+constexpr int kAffVP = 1, kAffRPL = 1, kAffPF = 2, kAffPFBig = 5;
+constexpr int64_t kAffBigRows = 16384;
 
 template <int BITS, typename XT, int P, int VP, int RPL>
 int launch_affine16(const Aff16Params& A, hipStream_t st, const char* what) {
   constexpr int RPW = 64 / (P / VP) * RPL;
   const int64_t waves = ((int64_t)A.rows + RPW - 1) / RPW;
   const dim3 grid((unsigned)((waves + 3) / 4));
-  const size_t lds = (size_t)A.cols * 2 + (size_t)(A.cols / 32) * 4;
-  hipLaunchKernelGGL((affine16_kernel<BITS, XT, XT, P, VP, RPL, kAffPF>), grid, dim3(256), lds, st, A);
+  const size_t lds = (size_t)A.cols * 2 + (size_t)(A.cols / 64) * 16 + (size_t)(A.cols / 32) * 4;
+  if (A.rows >= kAffBigRows)
+    hipLaunchKernelGGL((affine16_kernel<BITS, XT, XT, P, VP, RPL, kAffPFBig>), grid, dim3(256), lds, st, A);
+  else
+    hipLaunchKernelGGL((affine16_kernel<BITS, XT, XT, P, VP, RPL, kAffPF>), grid, dim3(256), lds, st, A);
   return check_launch(what);
 }
 
