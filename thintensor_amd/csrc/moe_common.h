@@ -55,6 +55,21 @@ __device__ __forceinline__ float ld_typed(const void* p, int dtype, int64_t i) {
 }
 
 
+// ld_typed in two 16-bit halves requested without a branch on the dtype (both loads stay
+// inside the array for every dtype: a 16-bit array reads element i twice) and converted
+// where the value is used, so a kernel can request it long before it needs it.
+struct TypedBits { uint16_t lo, hi; };
+__device__ __forceinline__ TypedBits ld_typed_bits(const void* p, int dtype, int64_t i) {
+  const uint16_t* h = reinterpret_cast<const uint16_t*>(p);
+  const bool wide = dtype == TT_F32;
+  const int64_t k = wide ? 2 * i : i;
+  return TypedBits{h[k], h[wide ? k + 1 : k]};
+}
+__device__ __forceinline__ float typed_f32(TypedBits b, int dtype) {
+  if (dtype == TT_F32) return __builtin_bit_cast(float, (uint32_t)b.lo | ((uint32_t)b.hi << 16));
+  return dtype == TT_BF16 ? to_f32(bf16_t{b.lo}) : to_f32(f16_t{b.lo});
+}
+
 template <typename T> struct DT;
 template <> struct DT<f16_t> { static constexpr int code = TT_F16; };
 template <> struct DT<bf16_t> { static constexpr int code = TT_BF16; };

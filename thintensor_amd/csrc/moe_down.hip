@@ -227,7 +227,123 @@ __global__ __launch_bounds__(256) void down_lean_kernel(const DownParams P) {
   store<OT>(reinterpret_cast<OT*>(P.out) + (int64_t)tok * P.out_token + n, c);
 }
 
+constexpr int kDownSlotRounds = 4;   // rounds of a row per lane group (all in flight)
+constexpr int kDownSlotPieces = 6;   // 16-byte activation pieces per lane (cols <= 3072)
+
+// Weighted down with one wave per (row block, slot): wave s of a workgroup computes slot
+// s's values of the workgroup's SUBS rows (one row per lane group; down_lean_kernel's
+// lane mapping, chunk order, lane reduction and rounding).  Each wave stages its own
+// slot's activation in its own LDS region (no workgroup barrier before the dot
+// products) while every round of its weights, the bias and the router scores are in
+// flight.  The rounded row values meet in LDS and thread g folds row g's slots in slot
+// order: c = fma(v_s, score_s, c) from +0, the same bits as down_lean_kernel.  S times
+// the waves of down_lean_kernel for the same work, few registers per wave, so the whole
+// grid at the gpt-oss shape is resident at once: one memory phase, not two generations.
+template <Fmt F, typename XT, typename OT, typename RT, int LPR, int S>
+__global__ __launch_bounds__(64 * S) void down_slot_kernel(const DownParams P) {
+  constexpr int B = FmtInfo<F>::kBytes;
+  constexpr int SUBS = 64 / LPR;
+  constexpr int R = kDownSlotRounds;
+  extern __shared__ uint4 xs_pieces[];   // [S][cols / 8]
+  __shared__ float vals[S][SUBS];
+  const int lane = threadIdx.x & 63;
+  const int s = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int sub = lane / LPR, l = lane % LPR;
+  const int nchunks = P.cols >> 5;
+  const int xn = P.cols >> 3;
+  const int tok = blockIdx.y;
+  const int n = blockIdx.x * SUBS + sub;
+  const bool rv = n < P.rows;
+  const int ncl = rv ? n : P.rows - 1;
+  // this slot's activation pieces first (they do not wait for the expert id), clamped
+  const uint4* xg = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(P.x) +
+                                                   ((int64_t)tok * S + s) * P.x_slot);
+  // (native 4-vectors: an array of the uint4 struct type is kept in scratch memory)
+  typedef uint32_t piece_t __attribute__((ext_vector_type(4)));
+  const piece_t* xgp = reinterpret_cast<const piece_t*>(xg);
+  piece_t xr[kDownSlotPieces];
+#pragma unroll
+  for (int k = 0; k < kDownSlotPieces; k++) {
+    const int i = lane + 64 * k;
+    xr[k] = xgp[i < xn ? i : xn - 1];
+  }
+  const int64_t e = load_expert(P.experts, P.ishift, (int64_t)tok * S + s);
+  const uint8_t* wrow = P.w + e * P.w_expert + (int64_t)ncl * P.w_row;
+  const uint8_t* srow = P.s + e * P.s_expert + (int64_t)ncl * P.s_row;
+  // every round of the row (rounds past the last clamp to the last chunk: re-reads,
+  // results unused)
+  Raw<B> w[R];
+  uint8_t ex[R];
+#pragma unroll
+  for (int k = 0; k < R; k++) {
+    uint32_t j = (uint32_t)(k * LPR + l);
+    j = j < (uint32_t)nchunks ? j : (uint32_t)nchunks - 1;
+    w[k] = load_raw<B>(wrow + j * (uint32_t)B);
+    ex[k] = srow[j];
+  }
+  // the epilogue's bias and router scores (a null bias reads score 0 instead, unused)
+  const bool has_bias = P.bias != nullptr;
+  const TypedBits braw = ld_typed_bits(has_bias ? P.bias : P.scores, has_bias ? P.bias_dtype : P.score_dtype,
+                                       has_bias ? e * P.bias_expert + ncl : 0);
+  TypedBits sraw[S];
+#pragma unroll
+  for (int t = 0; t < S; t++) sraw[t] = ld_typed_bits(P.scores, P.score_dtype, (int64_t)tok * S + t);
+  __builtin_amdgcn_sched_barrier(0);
+  uint4* xl = xs_pieces + s * xn;
+#pragma unroll
+  for (int k = 0; k < kDownSlotPieces; k++) {
+    const int i = lane + 64 * k;
+    if (i < xn) reinterpret_cast<piece_t*>(xl)[i] = xr[k];
+  }
+  // the wave reads only its own pieces: its LDS operations run in order
+  __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0)
+  __builtin_amdgcn_wave_barrier();
+  float acc = 0.0f;
+  // every round is computed (a round past the last one adds +0): a round guarded by a
+  // branch had its loads sunk into the branch
+#pragma unroll
+  for (int k = 0; k < R; k++) {
+    const int j = k * LPR + l;
+    const bool cv = j < nchunks;
+    uint32_t xw[16];
+    const uint4* xp = xl + (cv ? j : 0) * 4;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const uint4 v = xp[q];
+      xw[4 * q] = v.x; xw[4 * q + 1] = v.y; xw[4 * q + 2] = v.z; xw[4 * q + 3] = v.w;
+    }
+    float p[1];
+    chunk_dot_rows<F, XT, 1>(&w[k], xw, p);
+    const float t = p[0] * pow2i((int)ex[k] - 127);
+    acc = acc + ((cv && rv) ? t : 0.0f);
+  }
+  reduce_range<1, 1, LPR>(&acc);
+  if (l == 0) {
+    float v = round_to<RT>(acc);
+    if (has_bias) v = round_to<RT>(v + typed_f32(braw, P.bias_dtype));
+    vals[s][sub] = v;
+  }
+  __syncthreads();
+  if (threadIdx.x < SUBS) {
+    const int nn = blockIdx.x * SUBS + (int)threadIdx.x;
+    if (nn < P.rows) {
+      float c = 0.0f;
+#pragma unroll
+      for (int t = 0; t < S; t++) c = __builtin_fmaf(vals[t][threadIdx.x], typed_f32(sraw[t], P.score_dtype), c);
+      store<OT>(reinterpret_cast<OT*>(P.out) + (int64_t)tok * P.out_token + nn, c);
+    }
+  }
+}
+
 // ------------------------------------------------------------------ dispatch
+
+template <Fmt F, typename XT, typename OT, typename RT, int LPR, int S>
+static int launch_down_slot(const DownParams& P, hipStream_t st) {
+  constexpr int SUBS = 64 / LPR;
+  hipLaunchKernelGGL((down_slot_kernel<F, XT, OT, RT, LPR, S>), dim3((unsigned)((P.rows + SUBS - 1) / SUBS), P.tokens),
+                     dim3(64 * S), (size_t)P.cols * 2 * S, st, P);
+  return check_launch("mxfp_lowbit_weighted_down");
+}
 
 template <Fmt F, typename XT, typename OT, typename RT, int LPR, int S>
 static int launch_down_lean(const DownParams& P, hipStream_t st) {
@@ -240,6 +356,14 @@ static int launch_down_lean(const DownParams& P, hipStream_t st) {
 
 template <Fmt F, typename XT, typename OT, typename RT, int LPR>
 static int launch_down_lean_s(const DownParams& P, hipStream_t st) {
+  if ((P.cols / 32 + LPR - 1) / LPR <= kDownSlotRounds && P.cols / 8 <= 64 * kDownSlotPieces) {
+    switch (P.slots) {
+      case 1: return launch_down_slot<F, XT, OT, RT, LPR, 1>(P, st);
+      case 2: return launch_down_slot<F, XT, OT, RT, LPR, 2>(P, st);
+      case 4: return launch_down_slot<F, XT, OT, RT, LPR, 4>(P, st);
+      default: return launch_down_slot<F, XT, OT, RT, LPR, 8>(P, st);
+    }
+  }
   switch (P.slots) {
     case 1: return launch_down_lean<F, XT, OT, RT, LPR, 1>(P, st);
     case 2: return launch_down_lean<F, XT, OT, RT, LPR, 2>(P, st);

@@ -308,6 +308,108 @@ __global__ __launch_bounds__(256) void swiglu_lean_multi_kernel(const SwigluPara
   }
 }
 
+constexpr int kSwigluSlotRounds = 4;   // rounds of a row per lane group (all in flight)
+constexpr int kSwigluSlotPieces = 4;   // 16-byte activation pieces per thread (cols <= 8192)
+
+// swiglu_lean_kernel (ROWS = 2) for rows of at most kSwigluSlotRounds rounds, with no
+// refill loop: the slot's activation pieces, then every round of the wave's gate/up
+// rows and their biases are requested before the first wait, and every round is
+// computed (a round past the last adds +0), so no load is sunk into a branch and the
+// wave needs few registers: at the gpt-oss shape the whole grid is resident at once.
+// Same chunk partition, fma order, reduction and epilogue as swiglu_lean_kernel.
+template <Fmt F, typename XT, typename OT, typename RT, typename BT, int LPR>
+__global__ __launch_bounds__(256) void swiglu_slot_kernel(const SwigluParams P) {
+  constexpr int ROWS = 2;
+  constexpr int B = FmtInfo<F>::kBytes;
+  constexpr int SUBS = 64 / LPR;
+  constexpr int R = kSwigluSlotRounds;
+  extern __shared__ uint32_t xs_lds[];
+  const int slot = blockIdx.y;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int sub = lane / LPR, l = lane % LPR;
+  const int nchunks = P.cols >> 5;
+  const int a = (int)(blockIdx.x * 4 + wave) * SUBS + sub;   // this lane group's activation row
+  const bool av = a < P.act_rows;
+  const int ac = av ? a : P.act_rows - 1;
+  // the slot's activations go to LDS (loads first, clamped indices; native 4-vectors:
+  // an array of the uint4 struct type is kept in scratch memory)
+  typedef uint32_t piece_t __attribute__((ext_vector_type(4)));
+  const int xn = P.cols >> 3;
+  const piece_t* xg = reinterpret_cast<const piece_t*>(reinterpret_cast<const uint16_t*>(P.x) +
+                                                       (int64_t)(slot / P.x_div) * P.x_slot);
+  piece_t xr[kSwigluSlotPieces];
+#pragma unroll
+  for (int k = 0; k < kSwigluSlotPieces; k++) {
+    const int i = (int)threadIdx.x + 256 * k;
+    xr[k] = xg[i < xn ? i : xn - 1];
+  }
+  const int64_t e = load_expert(P.experts, P.ishift, slot);
+  const uint8_t* w0 = P.w + e * P.w_expert + 2 * (int64_t)ac * P.w_row;
+  const uint8_t* s0 = P.s + e * P.s_expert + 2 * (int64_t)ac * P.s_row;
+  Raw<B> w[R][ROWS];
+  uint8_t ex[R][ROWS];
+#pragma unroll
+  for (int k = 0; k < R; k++) {
+    uint32_t j = (uint32_t)(k * LPR + l);
+    j = j < (uint32_t)nchunks ? j : (uint32_t)nchunks - 1;
+#pragma unroll
+    for (int i = 0; i < ROWS; i++) {
+      w[k][i] = load_raw<B>(w0 + i * P.w_row + j * (uint32_t)B);
+      ex[k][i] = s0[i * P.s_row + j];
+    }
+  }
+  // gate and up biases (a null bias reads the activation instead, unused)
+  const bool has_bias = P.bias != nullptr;
+  const int64_t bb = has_bias ? e * P.bias_expert + 2 * (int64_t)ac : 0;
+  const BT* bp = reinterpret_cast<const BT*>(has_bias ? P.bias : P.x);
+  const BT bg = bp[bb], bu = bp[has_bias ? bb + 1 : bb];
+  __builtin_amdgcn_sched_barrier(0);
+  piece_t* xl = reinterpret_cast<piece_t*>(xs_lds);
+#pragma unroll
+  for (int k = 0; k < kSwigluSlotPieces; k++) {
+    const int i = (int)threadIdx.x + 256 * k;
+    if (i < xn) xl[i] = xr[k];
+  }
+  lds_barrier();
+
+  float acc[ROWS] = {0.0f, 0.0f};
+#pragma unroll
+  for (int k = 0; k < R; k++) {
+    const int j = k * LPR + l;
+    const bool cv = j < nchunks;
+    uint32_t xw[16];
+    const uint4* xp = reinterpret_cast<const uint4*>(xs_lds + (cv ? j : 0) * 16);
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const uint4 v = xp[q];
+      xw[4 * q] = v.x; xw[4 * q + 1] = v.y; xw[4 * q + 2] = v.z; xw[4 * q + 3] = v.w;
+    }
+    float p[ROWS];
+    chunk_dot_rows<F, XT, ROWS>(w[k], xw, p);
+#pragma unroll
+    for (int i = 0; i < ROWS; i++) {
+      const float t = p[i] * pow2i((int)ex[k][i] - 127);
+      acc[i] = acc[i] + ((cv && av) ? t : 0.0f);
+    }
+  }
+  reduce_range<ROWS, 1, LPR>(acc);
+  const float v = acc[0];
+  const float pv = xor_partner<1>(v);   // the other row of the gate/up pair
+  if (l != 0 || !av) return;
+  float g = round_to<RT>(v);
+  float u = round_to<RT>(pv);
+  if (has_bias) {
+    g = round_to<RT>(g + to_f32(bg));
+    u = round_to<RT>(u + to_f32(bu));
+  }
+  g = fminf(g, P.limit);
+  u = fmaxf(fminf(u, P.limit), -P.limit);
+  const float num = (u + 1.0f) * g;
+  const float den = 1.0f + exp_f32(-g * P.alpha);
+  store<OT>(reinterpret_cast<OT*>(P.out) + (int64_t)slot * P.out_slot + a, num / den);
+}
+
 // ------------------------------------------------------------------ dispatch
 
 // Row blocks per workgroup of swiglu_lean_multi_kernel: 2 once the one-block grid would
@@ -329,6 +431,11 @@ static int launch_swiglu_lean(const SwigluParams& P, int slots, hipStream_t st) 
     const int64_t groups = ((nblocks + KB - 1) / KB + 7) / 8 * 8;
     hipLaunchKernelGGL((swiglu_lean_multi_kernel<F, XT, OT, RT, BT, LPR, KB>), dim3((unsigned)groups, slots), dim3(256),
                        (size_t)P.cols * 2, st, P, (int)nblocks);
+    return check_launch("mxfp_lowbit_selected_swiglu");
+  }
+  if (rounds <= kSwigluSlotRounds && P.cols / 8 <= 256 * kSwigluSlotPieces) {
+    hipLaunchKernelGGL((swiglu_slot_kernel<F, XT, OT, RT, BT, LPR>), dim3((unsigned)((waves + 3) / 4), slots),
+                       dim3(256), (size_t)P.cols * 2, st, P);
     return check_launch("mxfp_lowbit_selected_swiglu");
   }
   hipLaunchKernelGGL((swiglu_lean_kernel<F, XT, OT, RT, BT, LPR, 2>), dim3((unsigned)((waves + 3) / 4), slots),
