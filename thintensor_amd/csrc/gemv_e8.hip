@@ -95,7 +95,11 @@ struct Aff16Params {
 
 // RPL rows per lane (rows lane / Q and lane / Q + 64 / (Q * RPL) ... of the wave's block
 // share each activation read and give the lane RPL * 2 independent fma chains per group).
-template <int BITS, typename XT, typename OT, int P, int VP, int RPL, int PF>
+// ALL: the row's rounds all fit the PF-round ring (the host checks), so they are consumed
+// in one straight pass with no refill loop (a loop with conditional refills kept more
+// registers live, too many for the whole 17920-row grid to be resident at once).
+constexpr int kAffXPieces = 4;   // 16-byte activation pieces per thread requested up front
+template <int BITS, typename XT, typename OT, int P, int VP, int RPL, int PF, bool ALL>
 __global__ __launch_bounds__(256) void affine16_kernel(const Aff16Params A) {
   constexpr int Q = P / VP;                 // lanes per row
   constexpr int RG = 64 / Q;                // row groups per wave
@@ -146,14 +150,30 @@ __global__ __launch_bounds__(256) void affine16_kernel(const Aff16Params A) {
       }
     }
   };
+  // the activation pieces first (clamped; native 4-vectors: an array of the uint4
+  // struct type is kept in scratch memory), then the weight rounds
+  typedef uint32_t piece_t __attribute__((ext_vector_type(4)));
+  const int xn = A.cols >> 3;
+  const piece_t* xg = reinterpret_cast<const piece_t*>(A.x);
+  piece_t xr[kAffXPieces];
+#pragma unroll
+  for (int k = 0; k < kAffXPieces; k++) {
+    const int i = (int)threadIdx.x + 256 * k;
+    xr[k] = xg[i < xn ? i : xn - 1];
+  }
   Rnd ring[PF];
 #pragma unroll
   for (int k = 0; k < PF; k++) fetch(k, ring[k]);
+  __builtin_amdgcn_sched_barrier(0);
 
   // x into LDS (padded pieces), then the chunk sums
-  const int xn = A.cols >> 3;
-  const uint4* xg = reinterpret_cast<const uint4*>(A.x);
-  for (int i = threadIdx.x; i < xn; i += 256) x_lds[9 * (i >> 3) + (i & 7)] = xg[i];
+  piece_t* xl = reinterpret_cast<piece_t*>(x_lds);
+#pragma unroll
+  for (int k = 0; k < kAffXPieces; k++) {
+    const int i = (int)threadIdx.x + 256 * k;
+    if (i < xn) xl[9 * (i >> 3) + (i & 7)] = xr[k];
+  }
+  for (int i = (int)threadIdx.x + 256 * kAffXPieces; i < xn; i += 256) xl[9 * (i >> 3) + (i & 7)] = xg[i];
   __syncthreads();
   float* xsum = reinterpret_cast<float*>(x_lds + xn + (A.cols >> 6));
   for (int c = threadIdx.x; c < (A.cols >> 5); c += 256) {
@@ -215,12 +235,18 @@ __global__ __launch_bounds__(256) void affine16_kernel(const Aff16Params A) {
       }
     }
   };
-  for (int r0 = 0; r0 < rounds; r0 += PF) {
+  if constexpr (ALL) {
+    // rounds past the last re-read the last group and add +0
 #pragma unroll
-    for (int k = 0; k < PF; k++) {
-      if (r0 + k < rounds) {
-        consume(ring[k], r0 + k);
-        if (r0 + k + PF < rounds) fetch(r0 + k + PF, ring[k]);
+    for (int k = 0; k < PF; k++) consume(ring[k], k);
+  } else {
+    for (int r0 = 0; r0 < rounds; r0 += PF) {
+#pragma unroll
+      for (int k = 0; k < PF; k++) {
+        if (r0 + k < rounds) {
+          consume(ring[k], r0 + k);
+          if (r0 + k + PF < rounds) fetch(r0 + k + PF, ring[k]);
+        }
       }
     }
   }
@@ -247,10 +273,13 @@ int launch_affine16(const Aff16Params& A, hipStream_t st, const char* what) {
   const int64_t waves = ((int64_t)A.rows + RPW - 1) / RPW;
   const dim3 grid((unsigned)((waves + 3) / 4));
   const size_t lds = (size_t)A.cols * 2 + (size_t)(A.cols / 64) * 16 + (size_t)(A.cols / 32) * 4;
-  if (A.rows >= kAffBigRows)
-    hipLaunchKernelGGL((affine16_kernel<BITS, XT, XT, P, VP, RPL, kAffPFBig>), grid, dim3(256), lds, st, A);
+  const int rounds = (A.cols / 64 + P - 1) / P;
+  if (A.rows >= kAffBigRows && rounds <= kAffPFBig)
+    hipLaunchKernelGGL((affine16_kernel<BITS, XT, XT, P, VP, RPL, kAffPFBig, true>), grid, dim3(256), lds, st, A);
+  else if (A.rows >= kAffBigRows)
+    hipLaunchKernelGGL((affine16_kernel<BITS, XT, XT, P, VP, RPL, kAffPFBig, false>), grid, dim3(256), lds, st, A);
   else
-    hipLaunchKernelGGL((affine16_kernel<BITS, XT, XT, P, VP, RPL, kAffPF>), grid, dim3(256), lds, st, A);
+    hipLaunchKernelGGL((affine16_kernel<BITS, XT, XT, P, VP, RPL, kAffPF, false>), grid, dim3(256), lds, st, A);
   return check_launch(what);
 }
 
