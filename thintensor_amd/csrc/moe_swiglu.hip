@@ -256,10 +256,13 @@ __global__ __launch_bounds__(256) void swiglu_lean_multi_kernel(const SwigluPara
   for (int idx = threadIdx.x + 1024; idx < xn; idx += 256) xl[idx] = xg[idx];
   lds_barrier();
 
+  // every block's fetch and every round's arithmetic is unconditional (a block past the
+  // last reads clamped rows and stores nothing, a round past the last adds +0): a fetch
+  // or round under a branch had its loads sunk to their use
+  (void)nblocks;
 #pragma unroll
   for (int kb = 0; kb < KB; kb++) {
-    if ((int)blockIdx.x * KB + kb >= nblocks) break;   // uniform: past the last row block
-    if (kb + 1 < KB && (int)blockIdx.x * KB + kb + 1 < nblocks) fetch_block(kb + 1, d[(kb + 1) & 1]);
+    if (kb + 1 < KB) fetch_block(kb + 1, d[(kb + 1) & 1]);
     const Round* c = d[kb & 1];
     const int a = block_row(kb);
     const bool av = a < P.act_rows;
@@ -268,7 +271,7 @@ __global__ __launch_bounds__(256) void swiglu_lean_multi_kernel(const SwigluPara
     for (int i = 0; i < ROWS; i++) acc[i] = 0.0f;
 #pragma unroll
     for (int r = 0; r < R; r++) {
-      if (r < rounds) {
+      {
         const int j = r * LPR + l;
         const bool cv = j < nchunks;
         uint32_t xw[16];
