@@ -42,7 +42,11 @@ constexpr int kThreads = 128;
 // slots): two rows per item with one item's loads in flight (21.2 / 13.5 us) beat one row
 // per item with two (24.2 / 15.2 us), three (23.9 / 15.8 us), and four rows per item
 // (24.8 / 21.3 us: occupancy 2).  The activation reads from LDS are the main cost; an
-// item's reads feed every row of the item.
+// item's reads feed every row of the item.  One item per thread (rows per workgroup from
+// the chunk count, no item loop) took gate/up to 17.7 us (16 rows per workgroup made 144
+// items, a second loop pass with its own memory round trip for 16 threads) and down to
+// 13.1 us; requesting the items' words before the activation staging was slower (20.1 /
+// 14.5 us).
 constexpr int kRowsPerItem = 2;
 constexpr int kBatch = 1;                     // items whose loads are in flight together
 
@@ -159,7 +163,7 @@ __global__ __launch_bounds__(kThreads) void ternary_selected_kernel(TernParams P
     bsum[g] = b;
   }
   __syncthreads();
-
+  // this thread's item (the host keeps a workgroup's items within its threads)
   const uint8_t* wlast = align4(P.w_end - 1);
   const uint8_t* slast = align4(P.s_end - 1);
   const uint8_t* wexp = P.w + e * P.w_expert;
@@ -167,38 +171,40 @@ __global__ __launch_bounds__(kThreads) void ternary_selected_kernel(TernParams P
   // items: (RP consecutive rows, chunk); the last item's missing rows read the last row
   const int rgroups = (nrows + RP - 1) / RP;
   const int items = rgroups * P.chunks;
-  for (int base = threadIdx.x; base < items; base += kThreads * kBatch) {
-    ItemRow it[kBatch][RP];
-    int mbit[kBatch];
+  const int base = threadIdx.x;
+  ItemRow it[kBatch][RP];
+  int mbit[kBatch];
 #pragma unroll
-    for (int u = 0; u < kBatch; u++) {
-      int item = base + u * kThreads;
-      item = item < items ? item : items - 1;
-      const int rg = item / P.chunks, c = item - rg * P.chunks;
-      const int mb = 15 * c;
-      mbit[u] = mb & 7;
+  for (int u = 0; u < kBatch; u++) {
+    int item = base + u * kThreads;
+    item = item < items ? item : items - 1;
+    const int rg = item / P.chunks, c = item - rg * P.chunks;
+    const int mb = 15 * c;
+    mbit[u] = mb & 7;
 #pragma unroll
-      for (int k = 0; k < RP; k++) {
-        const int r = RP * rg + k < nrows ? RP * rg + k : nrows - 1;
-        ItemRow& ir = it[u][k];
-        const uint8_t* wrow = wexp + (int64_t)(row0 + r) * P.w_row;
-        const uint8_t* a = wrow + 32 * c;
-        const uint8_t* a4 = align4(a);
-        ir.shd = (uint32_t)(a - a4);
+    for (int k = 0; k < RP; k++) {
+      const int r = RP * rg + k < nrows ? RP * rg + k : nrows - 1;
+      ItemRow& ir = it[u][k];
+      const uint8_t* wrow = wexp + (int64_t)(row0 + r) * P.w_row;
+      const uint8_t* a = wrow + 32 * c;
+      const uint8_t* a4 = align4(a);
+      ir.shd = (uint32_t)(a - a4);
 #pragma unroll
-        for (int i = 0; i < 9; i++) ir.d[i] = ld_u32(a4 + 4 * i, wlast);
-        const uint8_t* ma = wrow + P.tbytes + (mb >> 3);
-        const uint8_t* ma4 = align4(ma);
-        ir.shm = (uint32_t)(ma - ma4);
+      for (int i = 0; i < 9; i++) ir.d[i] = ld_u32(a4 + 4 * i, wlast);
+      const uint8_t* ma = wrow + P.tbytes + (mb >> 3);
+      const uint8_t* ma4 = align4(ma);
+      ir.shm = (uint32_t)(ma - ma4);
 #pragma unroll
-        for (int i = 0; i < 3; i++) ir.m[i] = ld_u32(ma4 + 4 * i, wlast);
-        const uint8_t* sa = sexp + (int64_t)(row0 + r) * P.s_row + 5 * c;
-        const uint8_t* sa4 = align4(sa);
-        ir.shs = (uint32_t)(sa - sa4);
+      for (int i = 0; i < 3; i++) ir.m[i] = ld_u32(ma4 + 4 * i, wlast);
+      const uint8_t* sa = sexp + (int64_t)(row0 + r) * P.s_row + 5 * c;
+      const uint8_t* sa4 = align4(sa);
+      ir.shs = (uint32_t)(sa - sa4);
 #pragma unroll
-        for (int i = 0; i < 3; i++) ir.s[i] = ld_u32(sa4 + 4 * i, slast);
-      }
+      for (int i = 0; i < 3; i++) ir.s[i] = ld_u32(sa4 + 4 * i, slast);
     }
+  }
+
+  {
 #pragma unroll
     for (int u = 0; u < kBatch; u++) {
       const int item = base + u * kThreads;
@@ -273,9 +279,16 @@ __global__ __launch_bounds__(kThreads) void ternary_selected_kernel(TernParams P
   }
 }
 
-int rows_per_wg(int64_t rows, int64_t selected) {
-  int rpw = 32;
-  while (rpw > 8 && ((rows + rpw - 1) / rpw) * selected < 1024) rpw >>= 1;
+// Rows per workgroup: one thread per item (RP rows x one 160-column chunk), so a
+// workgroup's items fit its threads (the kernel takes item = thread); then fewer rows
+// while the grid is under 1024 workgroups (down to eight).
+int rows_per_wg(int64_t rows, int64_t selected, int chunks) {
+  int rpw = kRowsPerItem * (kThreads / chunks);
+  if (rpw > 32) rpw = 32;
+  while (rpw > 8 && ((rows + rpw - 1) / rpw) * selected < 1024) {
+    rpw = rpw / 2 / kRowsPerItem * kRowsPerItem;
+    if (rpw < 8) rpw = 8;
+  }
   return rpw;
 }
 
@@ -348,7 +361,9 @@ extern "C" int tt_mxfp_ternary_selected_matvec(const void* packed, int64_t w_exp
   P.tbytes = (int)tbytes;
   P.groups = (int)groups;
   P.chunks = (int)((cols + kChunk - 1) / kChunk);
-  P.rpw = rows_per_wg(rows, selected);
+  P.rpw = rows_per_wg(rows, selected, P.chunks);
+  TT_REQUIRE(P.rpw >= kRowsPerItem && (P.rpw + kRowsPerItem - 1) / kRowsPerItem * P.chunks <= kThreads,
+             "%s: a workgroup's items must fit its %d threads", what, kThreads);
   const size_t lds = lds_bytes(P.chunks, P.rpw);
   const dim3 grid((unsigned)((rows + P.rpw - 1) / P.rpw), (unsigned)selected);
   hipStream_t st = static_cast<hipStream_t>(stream);
