@@ -473,6 +473,37 @@ int tt_add_rms_norm_router_topk(const void* left, const void* right, void* resid
                                 int32_t* indices_out, void* scores_out, int score_dtype, int64_t tokens,
                                 void* workspace, int64_t workspace_bytes, void* stream);
 
+/* tt_add_rms_norm_router_topk without the top-k: residual_out and norm_out as there, and
+ * logits_out[t * experts + e] the router logit it ranks (bf16-rounded dot product, plus the
+ * bias rounded again), in one launch of ceil(experts / 4) workgroups per token with no
+ * arrival count.  The decode step's SwiGLU then runs the top-k on these logits
+ * (tt_mxfp_lowbit_selected_swiglu_router).  experts <= 32, hidden_size <= 4096.  Serves
+ * the same reference call pair as tt_add_rms_norm_router_topk (gpu_runtime.py:9465-9513). */
+int tt_add_rms_norm_router_logits(const void* left, const void* right, void* residual_out, int x_dtype,
+                                  const void* norm_weight, int norm_w_dtype, void* norm_out, int norm_dtype,
+                                  int64_t hidden_size, float eps, const void* weight, int w_dtype, int64_t w_row,
+                                  const void* bias, int bias_dtype, int64_t experts, float* logits_out,
+                                  int64_t tokens, void* stream);
+
+/* tt_mxfp_lowbit_selected_swiglu_tokens with the router's top-k folded in: router_logits
+ * [tokens, experts] fp32 as tt_add_rms_norm_router_logits writes them.  Every wave runs
+ * the top-k + softmax of its token (tt_moe_router_topk's selection and scores, bit for
+ * bit) and takes its slot's expert; slot t * selected + k is token t's k-th choice.  The
+ * slots' experts and scores (renormalized over the selected experts or not, score_dtype
+ * fp16/bf16/fp32) also go to indices_out / scores_out [tokens, selected] for the
+ * weighted-down.  experts <= 128, rows of at most four rounds of lanes and 8192 columns.
+ * Replaces the reference's moe_router_matvec_topk + mxfp_lowbit_selected_swiglu pair
+ * (triton_kernels.py:5826-5860, 4178-4235) as gpu_runtime.py:9465-9513 calls it. */
+int tt_mxfp_lowbit_selected_swiglu_router(const void* packed, int64_t w_expert_bytes, int64_t w_row_bytes,
+                                          const void* scales, int64_t s_expert, int64_t s_row, int bits,
+                                          const void* x, int x_dtype, int64_t x_token,
+                                          const float* router_logits, int64_t experts, int64_t selected,
+                                          int renormalize, int32_t* indices_out, void* scores_out,
+                                          int score_dtype, const void* bias, int bias_dtype,
+                                          int64_t bias_expert, float alpha, float limit, void* out,
+                                          int out_dtype, int64_t out_slot, int64_t activation_rows,
+                                          int64_t cols, int64_t tokens, void* stream);
+
 /* Top-k + softmax on given logits, any expert count up to 65536 (one wave up to 128
  * experts, one workgroup above; above 128 experts top_k is at most 4096).  The
  * runtime calls it exactly when the router has more than 128 rows

@@ -128,6 +128,9 @@ SIGNATURES: dict[str, list] = {
     "tt_add_rms_norm_router_topk": [_P, _P, _P, _I, _P, _I, _P, _I, _L, _F, _P, _I, _L, _P, _I, _L, _L, _I, _P, _P,
                                     _I, _L, _P, _L, _P],
     "tt_norm_router_workspace_bytes": [_L],
+    "tt_add_rms_norm_router_logits": [_P, _P, _P, _I, _P, _I, _P, _I, _L, _F, _P, _I, _L, _P, _I, _L, _P, _L, _P],
+    "tt_mxfp_lowbit_selected_swiglu_router": [_P, _L, _L, _P, _L, _L, _I, _P, _I, _L, _P, _L, _L, _I, _P, _P, _I,
+                                              _P, _I, _L, _F, _F, _P, _I, _L, _L, _L, _L, _P],
     "tt_matvec_bias_rows": [_P, _I, _L, _P, _P, _I, _L, _P, _I, _L, _L, _L, _L, _P],
     "tt_mxfp_lowbit_selected_swiglu_tokens": [_P, _L, _L, _P, _L, _L, _I, _P, _I, _L, _P, _I, _L, _P, _I, _L, _F, _F,
                                               _P, _I, _L, _L, _L, _L, _P],

@@ -1346,6 +1346,81 @@ class HipDecodeBackend:
         _lib.check(rc, "add_rms_norm_router_topk")
         return indices_out, scores_out
 
+    def add_rms_norm_router_logits(self, left: torch.Tensor, right: torch.Tensor, residual_out: torch.Tensor,
+                                   norm_weight: torch.Tensor, norm_out: torch.Tensor, eps: float,
+                                   router_weight: torch.Tensor, logits_out: torch.Tensor, *,
+                                   bias: torch.Tensor | None = None) -> torch.Tensor:
+        """``add_rms_norm_router_topk`` without the top-k: the same residual and norm
+        outputs, and logits_out [tokens, experts] fp32 holding the logits that operator
+        ranks.  ``mxfp_lowbit_selected_swiglu_router`` takes the top-k from them.  No
+        single reference operator (the pair at gpu_runtime.py:9465-9513)."""
+        experts, n = map(int, router_weight.shape)
+        tokens = int(left.numel()) // n if n else 0
+        if tokens < 1 or any(t.numel() != tokens * n for t in (left, right, residual_out, norm_out)) or \
+                int(norm_weight.numel()) != n:
+            raise ValueError("add_rms_norm_router_logits: vectors must be [tokens, hidden] matching the router weight")
+        if any(not t.is_contiguous() for t in (left, right, residual_out, norm_out, logits_out)):
+            raise ValueError("add_rms_norm_router_logits: vectors must be contiguous")
+        if right.dtype != left.dtype or residual_out.dtype != left.dtype:
+            raise ValueError("add_rms_norm: left, right and residual_out must share a dtype")
+        if logits_out.dtype != torch.float32 or int(logits_out.numel()) != tokens * experts:
+            raise ValueError("add_rms_norm_router_logits: logits_out must be float32 [tokens, experts]")
+        if bias is not None and int(bias.numel()) != experts:
+            raise ValueError("router bias does not match expert count")
+        _require_cuda(left, right, residual_out, norm_weight, norm_out, router_weight, logits_out)
+        rc = self.lib.tt_add_rms_norm_router_logits(
+            left.data_ptr(), right.data_ptr(), residual_out.data_ptr(), _code(left, "add_rms_norm"),
+            norm_weight.data_ptr(), _code(norm_weight, "add_rms_norm"), norm_out.data_ptr(),
+            _code(norm_out, "add_rms_norm"), n, float(eps), router_weight.data_ptr(), _code(router_weight, "router"),
+            router_weight.stride(0), bias.data_ptr() if bias is not None else None,
+            _code(bias, "bias") if bias is not None else _lib.F32, experts, logits_out.data_ptr(), tokens,
+            _stream(left),
+        )
+        _lib.check(rc, "add_rms_norm_router_logits")
+        return logits_out
+
+    def mxfp_lowbit_selected_swiglu_router(self, packed_weight: torch.Tensor, scales: torch.Tensor, x: torch.Tensor,
+                                           router_logits: torch.Tensor, indices_out: torch.Tensor,
+                                           scores_out: torch.Tensor, out: torch.Tensor, *, bits: int, alpha: float,
+                                           limit: float, renormalize: bool,
+                                           bias: torch.Tensor | None = None) -> torch.Tensor:
+        """``moe_router_topk`` + ``mxfp_lowbit_selected_swiglu`` in one launch: x [T, cols]
+        (or [cols]), router_logits [T, experts] float32, indices_out / scores_out
+        [T, k]; out [T * k, I].  Every wave takes its slot's expert from its own top-k
+        over the token's logits (the router's selection and scores, bit for bit) and the
+        slots' experts and scores are written for the weighted-down.  Replaces the pair
+        at gpu_runtime.py:9465-9513 (triton_kernels.py:5826-5860, 4178-4235)."""
+        if bits not in {1, 2, 4} or packed_weight.ndim != 4 or scales.ndim != 3:
+            raise ValueError("fused SwiGLU requires packed Q1, Q2 or MXFP4 experts")
+        activation_rows = int(packed_weight.shape[1]) // 2
+        cols = int(scales.shape[2] * 32)
+        lg = router_logits if router_logits.ndim == 2 else router_logits.reshape(1, -1)
+        tokens, experts = map(int, lg.shape)
+        if lg.dtype != torch.float32 or not lg.is_contiguous():
+            raise ValueError("router logits must be contiguous float32 [tokens, experts]")
+        if indices_out.dtype != torch.int32 or int(indices_out.numel()) % tokens or \
+                int(scores_out.numel()) != int(indices_out.numel()) or not indices_out.is_contiguous() or \
+                not scores_out.is_contiguous():
+            raise ValueError("indices/scores must be contiguous [tokens, top_k] (int32 indices)")
+        selected = int(indices_out.numel()) // tokens
+        xv = x if x.ndim == 2 else x.reshape(1, -1)
+        if int(xv.shape[0]) != tokens or int(xv.shape[1]) != cols or xv.stride(1) != 1:
+            raise ValueError("router SwiGLU takes x [T, cols]")
+        if tuple(out.shape) != (tokens * selected, activation_rows):
+            raise ValueError("router SwiGLU output shape mismatch")
+        _require_cuda(packed_weight, scales, x, lg, indices_out, scores_out, out)
+        rc = self.lib.tt_mxfp_lowbit_selected_swiglu_router(
+            packed_weight.data_ptr(), packed_weight.stride(0), packed_weight.stride(1), scales.data_ptr(),
+            scales.stride(0), scales.stride(1), bits, xv.data_ptr(), _code(xv, "swiglu"), xv.stride(0),
+            lg.data_ptr(), experts, selected, int(bool(renormalize)), indices_out.data_ptr(), scores_out.data_ptr(),
+            _code(scores_out, "scores"), bias.data_ptr() if bias is not None else None,
+            _code(bias, "bias") if bias is not None else _lib.F32, bias.stride(0) if bias is not None else 0,
+            float(alpha), float(limit), out.data_ptr(), _code(out, "swiglu"), out.stride(0), activation_rows, cols,
+            tokens, _stream(out),
+        )
+        _lib.check(rc, "mxfp_lowbit_selected_swiglu_router")
+        return out
+
     def moe_router_topk(self, logits: torch.Tensor, indices_out: torch.Tensor, scores_out: torch.Tensor, *,
                         renormalize: bool) -> tuple[torch.Tensor, torch.Tensor]:
         """(triton_kernels.py:5803-5824)"""

@@ -9,6 +9,7 @@
 #pragma once
 
 #include "gemv_impl.h"
+#include "tt_topk.h"
 
 #include <type_traits>
 
@@ -24,6 +25,13 @@ struct SwigluParams {
   void* out; int64_t out_slot;
   int act_rows, cols;
   int x_div;   // slots sharing one activation vector: slot s reads x + (s / x_div) * x_slot
+  // router logits [tokens, n_exp] (float) instead of expert ids: slot s is token s / top_k's
+  // (s % top_k)-th choice, and row block 0 writes each slot's expert and score to idx_out /
+  // score_out (score_dtype) for the weighted-down after it
+  const float* logits;
+  int n_exp, top_k, renorm, score_dtype;
+  int32_t* idx_out;
+  void* score_out;
 };
 
 template <typename BT> __device__ __forceinline__ float ld_bias(const void* b, int64_t i) {
@@ -68,6 +76,30 @@ __device__ __forceinline__ TypedBits ld_typed_bits(const void* p, int dtype, int
 __device__ __forceinline__ float typed_f32(TypedBits b, int dtype) {
   if (dtype == TT_F32) return __builtin_bit_cast(float, (uint32_t)b.lo | ((uint32_t)b.hi << 16));
   return dtype == TT_BF16 ? to_f32(bf16_t{b.lo}) : to_f32(f16_t{b.lo});
+}
+
+// Expert of SwiGLU slot `slot`: from the index list, or -- with router logits -- the
+// (slot % top_k)-th choice of this wave's own top-k over its token's logits
+// (wave_topk_lanes: the router's selection and scores, bit for bit).  With `publish` the
+// lane of that choice also writes the slot's expert and score.
+__device__ __forceinline__ int64_t swiglu_slot_expert(const SwigluParams& P, int slot, bool publish) {
+  if (P.logits == nullptr) return load_expert(P.experts, P.ishift, slot);
+  const int lane = lane_id();
+  const int tk = slot / P.top_k, k = slot - tk * P.top_k;
+  const float* lg = P.logits + (int64_t)tk * P.n_exp;
+  const float lg0 = lg[lane < P.n_exp ? lane : 0];
+  const float lg1 = lg[lane + 64 < P.n_exp ? lane + 64 : 0];
+  const TopkLanes r = wave_topk_lanes(lg0, lg1, P.n_exp, P.top_k, P.renorm != 0);
+  const int kl = k & 63;
+  const int e = __builtin_amdgcn_readlane(k < 64 ? r.idx0 : r.idx1, kl);
+  if (publish && lane == kl) {
+    P.idx_out[slot] = e;
+    const float sc = k < 64 ? r.score0 : r.score1;
+    if (P.score_dtype == TT_F32) reinterpret_cast<float*>(P.score_out)[slot] = sc;
+    else if (P.score_dtype == TT_BF16) store<bf16_t>(reinterpret_cast<bf16_t*>(P.score_out) + slot, sc);
+    else store<f16_t>(reinterpret_cast<f16_t*>(P.score_out) + slot, sc);
+  }
+  return e;
 }
 
 template <typename T> struct DT;

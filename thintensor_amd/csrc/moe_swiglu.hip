@@ -211,8 +211,10 @@ __global__ __launch_bounds__(256) void swiglu_lean_multi_kernel(const SwigluPara
   const int nchunks = P.cols >> 5;
   const int rounds = (nchunks + LPR - 1) / LPR;
   const int xn = P.cols >> 3;
-  const uint4* xg = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(P.x) + (int64_t)(slot / P.x_div) * P.x_slot);
-  uint4 xreg[4];
+  // (native 4-vectors: an array of the uint4 struct type is kept in scratch memory)
+  typedef uint32_t piece_t __attribute__((ext_vector_type(4)));
+  const piece_t* xg = reinterpret_cast<const piece_t*>(reinterpret_cast<const uint16_t*>(P.x) + (int64_t)(slot / P.x_div) * P.x_slot);
+  piece_t xreg[4];
   int xidx[4];
 #pragma unroll
   for (int k = 0; k < 4; k++) {
@@ -220,7 +222,7 @@ __global__ __launch_bounds__(256) void swiglu_lean_multi_kernel(const SwigluPara
     xidx[k] = idx < xn ? idx : xn - 1;
     xreg[k] = xg[xidx[k]];
   }
-  const int64_t e = load_expert(P.experts, P.ishift, slot);
+  const int64_t e = swiglu_slot_expert(P, slot, blockIdx.x == 0 && wave == 0);
   const uint8_t* wexp = P.w + e * P.w_expert;
   const uint8_t* sexp = P.s + e * P.s_expert;
   struct Round {
@@ -250,7 +252,7 @@ __global__ __launch_bounds__(256) void swiglu_lean_multi_kernel(const SwigluPara
   };
   Round d[2][R];
   fetch_block(0, d[0]);
-  uint4* xl = reinterpret_cast<uint4*>(xs_lds);
+  piece_t* xl = reinterpret_cast<piece_t*>(xs_lds);
 #pragma unroll
   for (int k = 0; k < 4; k++) xl[xidx[k]] = xreg[k];
   for (int idx = threadIdx.x + 1024; idx < xn; idx += 256) xl[idx] = xg[idx];
@@ -347,7 +349,7 @@ __global__ __launch_bounds__(256) void swiglu_slot_kernel(const SwigluParams P) 
     const int i = (int)threadIdx.x + 256 * k;
     xr[k] = xg[i < xn ? i : xn - 1];
   }
-  const int64_t e = load_expert(P.experts, P.ishift, slot);
+  const int64_t e = swiglu_slot_expert(P, slot, blockIdx.x == 0 && wave == 0);
   const uint8_t* w0 = P.w + e * P.w_expert + 2 * (int64_t)ac * P.w_row;
   const uint8_t* s0 = P.s + e * P.s_expert + 2 * (int64_t)ac * P.s_row;
   Raw<B> w[R][ROWS];
@@ -492,22 +494,46 @@ static int swiglu_dispatch(Fmt fmt, int out_dtype, int bias_dtype, const SwigluP
 
 using namespace tt;
 
+// Router-logits mode (logits != nullptr): slot s is token s / selected's (s % selected)-th
+// choice of the top-k over its n_exp logits, computed in the kernel; the slots' experts
+// and scores go to idx_out / score_out.
+struct SwigluRouter {
+  const float* logits;
+  int64_t n_exp;
+  int renorm;
+  int32_t* idx_out;
+  void* score_out;
+  int score_dtype;
+};
+
 static int selected_swiglu_impl(const void* packed, int64_t w_expert_bytes, int64_t w_row_bytes,
                                               const void* scales, int64_t s_expert, int64_t s_row, int bits,
                                               const void* x, int x_dtype, int64_t x_slot,
                                               const void* expert_indices, int index_bytes, int64_t selected, const void* bias,
                                               int bias_dtype, int64_t bias_expert, float alpha, float limit,
                                               void* out, int out_dtype, int64_t out_slot, int64_t activation_rows,
-                                              int64_t cols, int64_t tokens, void* stream) {
-  const char* what = "mxfp_lowbit_selected_swiglu";
+                                              int64_t cols, int64_t tokens, void* stream,
+                                              const SwigluRouter* router = nullptr) {
+  const char* what = router ? "mxfp_lowbit_selected_swiglu_router" : "mxfp_lowbit_selected_swiglu";
   TT_REQUIRE(tokens >= 1 && tokens * selected <= 65535, "%s: bad token count", what);
   TT_REQUIRE(bits == 1 || bits == 2 || bits == 4, "%s: fused SwiGLU requires packed Q1, Q2 or MXFP4 experts", what);
   TT_REQUIRE(valid_act_dtype(x_dtype) && valid_out_dtype(out_dtype), "%s: bad dtype codes", what);
   TT_REQUIRE(cols > 0 && cols % 32 == 0 && cols <= 32768, "%s: cols must be a multiple of 32 up to 32768", what);
   TT_REQUIRE(activation_rows > 0 && activation_rows < (1 << 29), "%s: bad activation rows", what);
-  TT_REQUIRE(selected >= 1 && selected <= 65535 && expert_indices, "%s: need selected experts", what);
-  int ishift;
-  TT_REQUIRE(index_shift(index_bytes, &ishift), "%s: expert indices must be int32 or int64", what);
+  int ishift = 0;
+  if (router) {
+    TT_REQUIRE(router->logits && router->idx_out && router->score_out && aligned(router->logits, 4),
+               "%s: null or misaligned router buffers", what);
+    TT_REQUIRE(router->n_exp >= 1 && router->n_exp <= 128 && selected >= 1 && selected <= router->n_exp,
+               "%s: need 1..128 experts and 1..experts selected", what);
+    TT_REQUIRE(valid_out_dtype(router->score_dtype), "%s: bad score dtype", what);
+    const int lpr0 = tt_gemv_lanes_per_row(cols / 32, 1);
+    TT_UNSUPPORTED(cols <= 8192 && (cols / 32 + lpr0 - 1) / lpr0 <= kSwigluSlotRounds,
+                   "%s: rows of at most %d rounds and 8192 columns", what, kSwigluSlotRounds);
+  } else {
+    TT_REQUIRE(selected >= 1 && selected <= 65535 && expert_indices, "%s: need selected experts", what);
+    TT_REQUIRE(index_shift(index_bytes, &ishift), "%s: expert indices must be int32 or int64", what);
+  }
   const int align = bits == 4 ? 16 : (bits == 2 ? 8 : 4);
   TT_REQUIRE(packed && aligned(packed, align) && w_row_bytes % align == 0 && w_expert_bytes % align == 0,
              "%s: packed weights must be %d-byte aligned", what, align);
@@ -516,6 +542,16 @@ static int selected_swiglu_impl(const void* packed, int64_t w_expert_bytes, int6
   SwigluParams P{static_cast<const uint8_t*>(packed), w_expert_bytes, w_row_bytes,
                  static_cast<const uint8_t*>(scales), s_expert, s_row, x, x_slot, expert_indices, ishift, bias, bias_expert,
                  alpha, limit, out, out_slot, (int)activation_rows, (int)cols, tokens > 1 ? (int)selected : 1};
+  if (router) {
+    P.x_div = (int)selected;   // slot s reads token s / selected's activation
+    P.logits = router->logits;
+    P.n_exp = (int)router->n_exp;
+    P.top_k = (int)selected;
+    P.renorm = router->renorm;
+    P.score_dtype = router->score_dtype;
+    P.idx_out = router->idx_out;
+    P.score_out = router->score_out;
+  }
   const int lpr = tt_gemv_lanes_per_row(cols / 32, 1);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const Fmt fmt = fmt_for_bits(bits);
@@ -551,4 +587,25 @@ extern "C" int tt_mxfp_lowbit_selected_swiglu_tokens(const void* packed, int64_t
   return selected_swiglu_impl(packed, w_expert_bytes, w_row_bytes, scales, s_expert, s_row, bits, x, x_dtype, x_token,
                               expert_indices, index_bytes, selected, bias, bias_dtype, bias_expert, alpha, limit, out, out_dtype,
                               out_slot, activation_rows, cols, tokens, stream);
+}
+
+// The decode step's SwiGLU with the router's top-k folded in: router_logits [tokens,
+// experts] as tt_add_rms_norm_router_logits writes them; every wave runs the top-k +
+// softmax of its token (the selection and scores of tt_moe_router_topk, bit for bit) and
+// takes its slot's expert; the slots' experts and scores (renormalized over the selected
+// experts or not) go to indices_out / scores_out [tokens, selected] for the weighted-down.
+// Rows of at most four rounds of lanes and 8192 columns.
+extern "C" int tt_mxfp_lowbit_selected_swiglu_router(const void* packed, int64_t w_expert_bytes, int64_t w_row_bytes,
+                                                     const void* scales, int64_t s_expert, int64_t s_row, int bits,
+                                                     const void* x, int x_dtype, int64_t x_token,
+                                                     const float* router_logits, int64_t experts, int64_t selected,
+                                                     int renormalize, int32_t* indices_out, void* scores_out,
+                                                     int score_dtype, const void* bias, int bias_dtype,
+                                                     int64_t bias_expert, float alpha, float limit, void* out,
+                                                     int out_dtype, int64_t out_slot, int64_t activation_rows,
+                                                     int64_t cols, int64_t tokens, void* stream) {
+  const SwigluRouter R{router_logits, experts, renormalize, indices_out, scores_out, score_dtype};
+  return selected_swiglu_impl(packed, w_expert_bytes, w_row_bytes, scales, s_expert, s_row, bits, x, x_dtype, x_token,
+                              nullptr, 4, selected, bias, bias_dtype, bias_expert, alpha, limit, out, out_dtype, out_slot,
+                              activation_rows, cols, tokens, stream, &R);
 }

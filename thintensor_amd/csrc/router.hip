@@ -12,6 +12,7 @@
 #include "tt_abi_internal.h"
 #include "tt_common.h"
 #include "tt_gemv.h"
+#include "tt_topk.h"
 
 #include <type_traits>
 
@@ -21,101 +22,20 @@ template <typename T> __device__ __forceinline__ float ldv(const void* p, int64_
   return to_f32(reinterpret_cast<const T*>(p)[i]);
 }
 
-// Ordered key of a router logit: larger value wins, equal values (+0 == -0) go to
-// the lowest expert index.  NaN never wins through the key (see wave_topk).
-__device__ __forceinline__ uint64_t topk_key(float v, uint32_t e) {
-  uint32_t b = __builtin_bit_cast(uint32_t, v);
-  if ((b & 0x7fffffffu) == 0) b = 0;
-  const uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-  return ((uint64_t)o << 32) | (uint64_t)(0xffffffffu - e);
-}
-
-__device__ __forceinline__ float lane_value(float a, float b, int i) {
-  return i < 64 ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a), i))
-                : __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, b), i - 64));
-}
-
-// Top-k + softmax over E <= 128 logits held by one wave (expert e in lane e % 64,
-// register e / 64).  Same result as scanning the experts in order for each slot:
-// the first untaken expert starts the scan and a later one replaces it only when
-// strictly greater -- so a NaN at the first untaken position is selected, any other
-// NaN never is, and equal values keep the lowest index.  The denominator is summed
-// sequentially in slot order (renormalize) or expert order, each term
-// exp(v - max) with max the NaN-ignoring maximum over all experts.
+// Top-k + softmax of one wave's logits (wave_topk_lanes), written out: slot s's expert
+// to idx_out[s] and its score to score_out[s].
 template <typename OT>
 __device__ void wave_topk(float lg0, float lg1, int E, int top_k, bool renorm, int32_t* idx_out, OT* score_out) {
   const int lane = lane_id();
-  const bool v0 = lane < E, v1 = lane + 64 < E;
-  float m = __builtin_bit_cast(float, 0xff800000u);
-  if (v0) m = fmaxf(m, lg0);
-  if (v1) m = fmaxf(m, lg1);
-  m = fmaxf(m, xor_partner<1>(m));
-  m = fmaxf(m, xor_partner<2>(m));
-  m = fmaxf(m, xor_partner<4>(m));
-  m = fmaxf(m, xor_partner<8>(m));
-  m = fmaxf(m, xor_partner<16>(m));
-  m = fmaxf(m, xor_partner<32>(m));
-  float sel0 = 0.0f, sel1 = 0.0f;
-  const bool any_nan = __builtin_amdgcn_ballot_w64((v0 && __builtin_isnan(lg0)) || (v1 && __builtin_isnan(lg1))) != 0;
-  if (E <= 64 && !any_nan) {
-    // Without NaNs the iterated selection is the order of the keys (value, then lowest
-    // index), so slot s is the expert with exactly s greater keys: every lane counts the
-    // keys above its own, independently of the others.
-    const uint64_t mine = topk_key(lg0, lane);
-    int rank = 0;
-    for (int f = 0; f < E; f++) {
-      const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)mine, f);
-      const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(mine >> 32), f);
-      rank += (((uint64_t)hi << 32) | lo) > mine ? 1 : 0;
-    }
-    __shared__ float sel_lds[64];
-    if (v0 && rank < top_k) {
-      idx_out[rank] = lane;
-      sel_lds[rank] = lg0;
-    }
-    __builtin_amdgcn_wave_barrier();
-    if (lane < top_k) sel0 = sel_lds[lane];
-  } else {
-  bool t0 = !v0, t1 = !v1;
-  for (int s = 0; s < top_k; s++) {
-    uint64_t k = 0, f = 0;
-    if (!t0) {
-      f = 0xffffffffu - (uint32_t)lane;
-      if (!__builtin_isnan(lg0)) k = topk_key(lg0, lane);
-    }
-    if (!t1) {
-      if (f == 0) f = 0xffffffffu - (uint32_t)(lane + 64);
-      if (!__builtin_isnan(lg1)) {
-        const uint64_t k1 = topk_key(lg1, lane + 64);
-        k = k1 > k ? k1 : k;
-      }
-    }
-    k = wave_max_u64(k);
-    f = wave_max_u64(f);
-    const int first = __builtin_amdgcn_readfirstlane((int)(0xffffffffu - (uint32_t)f));
-    const float fv = lane_value(lg0, lg1, first);
-    int bi = first;
-    if (!__builtin_isnan(fv)) bi = __builtin_amdgcn_readfirstlane((int)(0xffffffffu - (uint32_t)k));
-    const float bv = lane_value(lg0, lg1, bi);
-    if (lane == bi) t0 = true;
-    if (lane + 64 == bi) t1 = true;
-    if (lane == (s & 63)) {
-      if (s < 64) sel0 = bv;
-      else sel1 = bv;
-    }
-    if (lane == 0) idx_out[s] = bi;
+  const TopkLanes r = wave_topk_lanes(lg0, lg1, E, top_k, renorm);
+  if (lane < top_k) {
+    idx_out[lane] = r.idx0;
+    store<OT>(score_out + lane, r.score0);
   }
+  if (lane + 64 < top_k) {
+    idx_out[lane + 64] = r.idx1;
+    store<OT>(score_out + lane + 64, r.score1);
   }
-  const float e0 = exp_f32(sel0 - m), e1 = exp_f32(sel1 - m);
-  float den = 0.0f;
-  if (renorm) {
-    for (int s = 0; s < top_k; s++) den = den + lane_value(e0, e1, s);
-  } else {
-    const float a0 = exp_f32(lg0 - m), a1 = exp_f32(lg1 - m);
-    for (int e = 0; e < E; e++) den = den + lane_value(a0, a1, e);
-  }
-  if (lane < top_k) store<OT>(score_out + lane, e0 / den);
-  if (lane + 64 < top_k) store<OT>(score_out + lane + 64, e1 / den);
 }
 
 // Rows of E <= 32 experts with H <= 4096 (two rounds of 64 lanes): every wave requests
@@ -234,6 +154,7 @@ struct NormRouterParams {
   int64_t w_row;
   float eps;
   int H, E, top_k, renorm;
+  float* logits_out;   // split kernel only: when set, the logits [tokens, E] go here and the top-k is left to the caller
 };
 
 constexpr int kNormRouterExperts = 32;   // 16 waves x 2 experts
@@ -492,6 +413,11 @@ __global__ __launch_bounds__(256) void norm_router_split_kernel(const NormRouter
   }
   float v = round_bf16(xor_sum(acc, 1, 64));
   if (P.bias != nullptr) v = round_bf16(v + to_f32(braw));
+  if (P.logits_out != nullptr) {
+    // logits only: the kernel that consumes them runs the top-k (wave_topk_lanes) itself
+    if (e < P.E && lane == 0) P.logits_out[tok * P.E + e] = v;
+    return;
+  }
   if (e < P.E && lane == 0)
     __hip_atomic_store(reinterpret_cast<float*>(slot) + 32 + e, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -712,6 +638,7 @@ extern "C" int tt_add_rms_norm_router_topk(const void* left, const void* right, 
   P.left = left; P.right = right; P.residual_out = residual_out; P.norm_w = norm_weight; P.norm_out = norm_out;
   P.w = weight; P.bias = bias; P.idx_out = indices_out; P.score_out = scores_out; P.w_row = w_row; P.eps = eps;
   P.H = (int)hidden_size; P.E = (int)experts; P.top_k = (int)top_k; P.renorm = renormalize;
+  P.logits_out = nullptr;
   const int bdt = bias ? bias_dtype : TT_F32;
   return dt3(w_dtype, [&](auto wt) {
     using WT = decltype(wt);
@@ -737,6 +664,52 @@ extern "C" int tt_add_rms_norm_router_topk(const void* left, const void* right, 
             return check_launch(what);
           }
         });
+      });
+    });
+  });
+}
+
+// add_rms_norm + router logits, one launch of ceil(experts / 4) workgroups per token with
+// no finishing step: logits_out[t * experts + e] is the logit tt_add_rms_norm_router_topk
+// ranks (bf16-rounded dot, plus the bias rounded again); the decode step's SwiGLU kernel
+// runs the top-k on them (tt_mxfp_lowbit_selected_swiglu_router).
+extern "C" int tt_add_rms_norm_router_logits(const void* left, const void* right, void* residual_out, int x_dtype,
+                                             const void* norm_weight, int norm_w_dtype, void* norm_out, int norm_dtype,
+                                             int64_t hidden_size, float eps, const void* weight, int w_dtype,
+                                             int64_t w_row, const void* bias, int bias_dtype, int64_t experts,
+                                             float* logits_out, int64_t tokens, void* stream) {
+  const char* what = "add_rms_norm_router_logits";
+  TT_REQUIRE(tokens >= 1 && tokens <= 65535, "%s: bad token count", what);
+  TT_REQUIRE(left && right && residual_out && norm_weight && norm_out && weight && logits_out, "%s: null pointer", what);
+  TT_UNSUPPORTED(experts >= 1 && experts <= kNormRouterExperts && hidden_size > 0 && hidden_size <= 4096 &&
+                     hidden_size % 32 == 0,
+                 "%s: 1..%d experts and hidden sizes up to 4096 (multiples of 32)", what, kNormRouterExperts);
+  TT_REQUIRE(x_dtype != TT_F32 && norm_w_dtype == x_dtype && norm_dtype == x_dtype && (w_dtype == TT_F16 || w_dtype == TT_BF16),
+             "%s: fp16 or bf16 vectors of one dtype and an fp16 or bf16 router", what);
+  TT_REQUIRE(aligned(weight, 16) && w_row % 8 == 0 && w_row >= hidden_size && aligned(left, 16) && aligned(right, 16) &&
+                 aligned(residual_out, 16) && aligned(norm_weight, 16) && aligned(norm_out, 16) && aligned(logits_out, 4),
+             "%s: misaligned pointer or bad row stride", what);
+  NormRouterParams P;
+  P.left = left; P.right = right; P.residual_out = residual_out; P.norm_w = norm_weight; P.norm_out = norm_out;
+  P.w = weight; P.bias = bias; P.idx_out = nullptr; P.score_out = nullptr; P.w_row = w_row; P.eps = eps;
+  P.H = (int)hidden_size; P.E = (int)experts; P.top_k = 1; P.renorm = 0;
+  P.logits_out = logits_out;
+  const int bdt = bias ? bias_dtype : TT_F32;
+  if (bias) TT_REQUIRE(bias_dtype == TT_F16 || bias_dtype == TT_BF16 || bias_dtype == TT_F32, "%s: bad bias dtype", what);
+  return dt3(w_dtype, [&](auto wt) {
+    using WT = decltype(wt);
+    return dt3(x_dtype, [&](auto xt) {
+      using XT = decltype(xt);
+      return dt3(bdt, [&](auto bt) {
+        using BT = decltype(bt);
+        if constexpr (std::is_same_v<WT, float> || std::is_same_v<XT, float>) {
+          set_error("%s: unsupported dtypes", what);
+          return TT_ERR_UNSUPPORTED;
+        } else {
+          hipLaunchKernelGGL((norm_router_split_kernel<WT, XT, BT, float>), dim3((unsigned)((experts + 3) / 4),
+                             (unsigned)tokens), dim3(256), 0, static_cast<hipStream_t>(stream), P, nullptr);
+          return check_launch(what);
+        }
       });
     });
   });
