@@ -294,10 +294,18 @@ int launch_int4g128_lpr(int rpw, const void* W, int64_t w_row, const void* S, in
   const CombineSrc cmb = combine ? *combine : CombineSrc{};
   const uint32_t wr = (uint32_t)w_row, sr = (uint32_t)s_row, sg = (uint32_t)s_grp;
   const int rounds = (cols / 32 + LPR - 1) / LPR;
-  // several rounds per row and few rows per wave: four rounds in flight at a time
+  // several rounds per row and few rows per wave: rounds requested PFR at a time -- five
+  // rows of five rounds in one pass (17920 x 5120 at two rows per wave: 14.6 -> 13.1 us),
+  // two of the four rounds of a one-row wave (2048 x 8192: 5.39 -> 5.17 us), else four
 #define TT_INT4G_LAUNCH(R, M)                                                                                  \
   do {                                                                                                        \
-    if (rounds > 1 && R <= 2)                                                                                 \
+    if (rounds == 5 && R <= 2)                                                                                \
+      hipLaunchKernelGGL((int4g128_kernel<XT, LPR, R, M, 5>), grid, dim3(256), lds, st, w, wr, s, sr, sg, xv, yv, \
+                         rows, cols, cmb);                                                                    \
+    else if (rounds == 4 && R == 1)                                                                           \
+      hipLaunchKernelGGL((int4g128_kernel<XT, LPR, R, M, 2>), grid, dim3(256), lds, st, w, wr, s, sr, sg, xv, yv, \
+                         rows, cols, cmb);                                                                    \
+    else if (rounds > 1 && R <= 2)                                                                            \
       hipLaunchKernelGGL((int4g128_kernel<XT, LPR, R, M, 4>), grid, dim3(256), lds, st, w, wr, s, sr, sg, xv, yv, \
                          rows, cols, cmb);                                                                    \
     else                                                                                                      \
@@ -317,12 +325,18 @@ int launch_int4g128_lpr(int rpw, const void* W, int64_t w_row, const void* S, in
 
 // Rows per wave of the single-matrix path: enough waves to cover the chip several
 // times over before a wave takes more than one row.  Rows of several rounds take four
-// rows per wave from half the lane groups (17920 x 5120: 15.5 -> 14.5 us; single-round
-// rows of 8192 x 2048 are faster at two).
+// rows per wave from half the lane groups, except rows of five rounds, which take two
+// with all five rounds in flight (17920 x 5120: 15.5 us at one row, 14.6 at four, 13.1 at
+// two in one pass); rows of several rounds stay at one row per wave up to 2048 lane
+// groups (2048 x 8192: 5.43 -> 5.17 us); single-round rows of 8192 x 2048 are faster at
+// two.  Rows per wave never change the bits (the oracle's order has no such parameter).
 inline int int4g128_rows_per_wave(int64_t rows, int64_t cols, int lpr) {
   const int64_t groups = rows * lpr / 64;   // lane groups needed at one row each
-  const bool multi_round = cols / 32 > lpr;
+  const int64_t rounds = (cols / 32 + lpr - 1) / lpr;
+  const bool multi_round = rounds > 1;
+  if (multi_round && rounds == 5 && groups >= 8192) return 2;
   if (groups >= 16384 || (multi_round && groups >= 8192)) return 4;
+  if (multi_round && groups <= 2048) return 1;
   if (groups >= 2048) return 2;
   return 1;
 }
