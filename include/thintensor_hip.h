@@ -521,14 +521,12 @@ int tt_moe_router_topk(const void* logits, int logits_dtype, int64_t experts, in
  * to M rows.  Small M (int4: M < 4, fp8: M < 16) runs the GEMV engine on up to four
  * rows per launch (row m equals the single-row operator bit for bit); from there (up
  * to 64) an MFMA kernel runs whose fp32 sums follow the hardware's order (tolerance
- * parity).  cols must be a multiple of 256 up to 8192.  The MFMA path needs a
- * workspace of tt_batched_workspace_floats(m, rows, cols) floats (0 for m < 4): it splits the
- * (64-row block, 256-column slice) units evenly over one grid of the workgroups the
- * chip holds at once; a block shared by several workgroups leaves their fp32 partial
- * tiles in the workspace and a second kernel sums them in workgroup order, so the
- * result is the same from run to run.  Calls sharing one workspace must be ordered
- * (same stream).  int4 scales must be 4-byte aligned with an even row stride for
- * m >= 4 (the kernel reads the two group scales of a slice at once). */
+ * parity).  cols must be a multiple of 256 up to 8192.  The MFMA path is one launch
+ * with no workspace: one workgroup per CU owns a block of weight rows for every
+ * activation row, its four waves split K, and their fp32 tiles are summed in a fixed
+ * order inside the workgroup, so the result is the same from run to run.
+ * tt_batched_workspace_floats returns 0 and the workspace arguments are accepted and
+ * unused (kept for callers written against a workspace-taking build). */
 int64_t tt_batched_workspace_floats(int64_t m, int64_t rows, int64_t cols);
 int tt_int4_batched_matvec(const void* packed, int64_t w_row_bytes, const void* scales_f16, int64_t s_row,
                            const void* x, int64_t x_row, void* out, int64_t out_row, int64_t m, int64_t rows,
