@@ -110,7 +110,7 @@ def _fp8_case(g, rows, cols):
     return bits, scales
 
 
-@pytest.mark.parametrize("m", [2, 4, 16, 64])
+@pytest.mark.parametrize("m", [1, 2, 4, 16, 64])
 def test_fp8_batched(backend, device, m):
     g = rng(200 + m)
     rows, cols = 777, 5120

@@ -788,6 +788,8 @@ extern "C" int tt_scaled_batched_matvec(const void* weight, int64_t w_row_bytes,
                  static_cast<uint16_t*>(out), out_row, (int)m, (int)rows, (int)cols};
     return launch_mfma<WFmt::kFp8Row>(P, st, what);
   }
+  if (m == 1)   // one row: the single-row GEMV itself (its lean kernel; the same bits as a row of the engine)
+    return tt_scaled_matvec(weight, TT_W_FP8, w_row_bytes, scales, TT_F32, x, TT_F16, out, TT_F16, rows, cols, stream);
   GemvParams P{};
   P.nseg = 1;
   P.seg[0] = Seg{static_cast<const uint8_t*>(weight), w_row_bytes, scales, 1, 0, out, (int)rows};
