@@ -80,26 +80,38 @@ __device__ __forceinline__ float typed_f32(TypedBits b, int dtype) {
 
 // Expert of SwiGLU slot `slot`: from the index list, or -- with router logits -- the
 // (slot % top_k)-th choice of this wave's own top-k over its token's logits
-// (wave_topk_lanes: the router's selection and scores, bit for bit).  With `publish` the
-// lane of that choice also writes the slot's expert and score.
-__device__ __forceinline__ int64_t swiglu_slot_expert(const SwigluParams& P, int slot, bool publish) {
-  if (P.logits == nullptr) return load_expert(P.experts, P.ishift, slot);
+// (wave_topk_expert: the router's selection, bit for bit).  The token's logits stay in
+// lg0 / lg1 (expert e in lane e % 64 of lg(e / 64)) for swiglu_publish.
+struct SlotRoute {
+  int64_t e;
+  float lg0, lg1;
+};
+__device__ __forceinline__ SlotRoute swiglu_slot_route(const SwigluParams& P, int slot) {
+  if (P.logits == nullptr) return SlotRoute{load_expert(P.experts, P.ishift, slot), 0.0f, 0.0f};
   const int lane = lane_id();
   const int tk = slot / P.top_k, k = slot - tk * P.top_k;
   const float* lg = P.logits + (int64_t)tk * P.n_exp;
   const float lg0 = lg[lane < P.n_exp ? lane : 0];
   const float lg1 = lg[lane + 64 < P.n_exp ? lane + 64 : 0];
+  return SlotRoute{wave_topk_expert(lg0, lg1, P.n_exp, k), lg0, lg1};
+}
+
+// With router logits: the slot's expert id and router score (wave_topk_lanes, the
+// router's selection and softmax bit for bit) to idx_out / score_out.  One wave per slot
+// calls it, after its weight loads are issued, so the softmax is off every wave's path to
+// its first weight request.
+__device__ __forceinline__ void swiglu_publish(const SwigluParams& P, int slot, float lg0, float lg1) {
+  if (P.logits == nullptr) return;
+  const int lane = lane_id();
+  const int k = slot % P.top_k;
   const TopkLanes r = wave_topk_lanes(lg0, lg1, P.n_exp, P.top_k, P.renorm != 0);
-  const int kl = k & 63;
-  const int e = __builtin_amdgcn_readlane(k < 64 ? r.idx0 : r.idx1, kl);
-  if (publish && lane == kl) {
-    P.idx_out[slot] = e;
+  if (lane == (k & 63)) {
+    P.idx_out[slot] = k < 64 ? r.idx0 : r.idx1;
     const float sc = k < 64 ? r.score0 : r.score1;
     if (P.score_dtype == TT_F32) reinterpret_cast<float*>(P.score_out)[slot] = sc;
     else if (P.score_dtype == TT_BF16) store<bf16_t>(reinterpret_cast<bf16_t*>(P.score_out) + slot, sc);
     else store<f16_t>(reinterpret_cast<f16_t*>(P.score_out) + slot, sc);
   }
-  return e;
 }
 
 template <typename T> struct DT;

@@ -222,7 +222,8 @@ __global__ __launch_bounds__(256) void swiglu_lean_multi_kernel(const SwigluPara
     xidx[k] = idx < xn ? idx : xn - 1;
     xreg[k] = xg[xidx[k]];
   }
-  const int64_t e = swiglu_slot_expert(P, slot, blockIdx.x == 0 && wave == 0);
+  const SlotRoute route = swiglu_slot_route(P, slot);
+  const int64_t e = route.e;
   const uint8_t* wexp = P.w + e * P.w_expert;
   const uint8_t* sexp = P.s + e * P.s_expert;
   struct Round {
@@ -252,6 +253,7 @@ __global__ __launch_bounds__(256) void swiglu_lean_multi_kernel(const SwigluPara
   };
   Round d[2][R];
   fetch_block(0, d[0]);
+  if (blockIdx.x == 0 && wave == 0) swiglu_publish(P, slot, route.lg0, route.lg1);
   piece_t* xl = reinterpret_cast<piece_t*>(xs_lds);
 #pragma unroll
   for (int k = 0; k < 4; k++) xl[xidx[k]] = xreg[k];
@@ -349,7 +351,8 @@ __global__ __launch_bounds__(256) void swiglu_slot_kernel(const SwigluParams P) 
     const int i = (int)threadIdx.x + 256 * k;
     xr[k] = xg[i < xn ? i : xn - 1];
   }
-  const int64_t e = swiglu_slot_expert(P, slot, blockIdx.x == 0 && wave == 0);
+  const SlotRoute route = swiglu_slot_route(P, slot);
+  const int64_t e = route.e;
   const uint8_t* w0 = P.w + e * P.w_expert + 2 * (int64_t)ac * P.w_row;
   const uint8_t* s0 = P.s + e * P.s_expert + 2 * (int64_t)ac * P.s_row;
   Raw<B> w[R][ROWS];
@@ -370,6 +373,7 @@ __global__ __launch_bounds__(256) void swiglu_slot_kernel(const SwigluParams P) 
   const BT* bp = reinterpret_cast<const BT*>(has_bias ? P.bias : P.x);
   const BT bg = bp[bb], bu = bp[has_bias ? bb + 1 : bb];
   __builtin_amdgcn_sched_barrier(0);
+  if (blockIdx.x == 0 && wave == 0) swiglu_publish(P, slot, route.lg0, route.lg1);
   piece_t* xl = reinterpret_cast<piece_t*>(xs_lds);
 #pragma unroll
   for (int k = 0; k < kSwigluSlotPieces; k++) {

@@ -118,4 +118,49 @@ __device__ __forceinline__ TopkLanes wave_topk_lanes(float lg0, float lg1, int E
   return TopkLanes{id0, id1, e0 / den, e1 / den};
 }
 
+// Expert of slot k of wave_topk_lanes's selection (the same rule, so the same expert),
+// without the softmax: the rank pass when no logit is NaN and E <= 64, otherwise the
+// iterated scan stopped at slot k.
+__device__ __forceinline__ int wave_topk_expert(float lg0, float lg1, int E, int k) {
+  const int lane = lane_id();
+  const bool v0 = lane < E, v1 = lane + 64 < E;
+  const bool any_nan = __builtin_amdgcn_ballot_w64((v0 && __builtin_isnan(lg0)) || (v1 && __builtin_isnan(lg1))) != 0;
+  if (E <= 64 && !any_nan) {
+    const uint64_t mine = topk_key(lg0, lane);
+    int rank = 0;
+    for (int f = 0; f < E; f++) {
+      const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)mine, f);
+      const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(mine >> 32), f);
+      rank += (((uint64_t)hi << 32) | lo) > mine ? 1 : 0;
+    }
+    const uint64_t hit = __builtin_amdgcn_ballot_w64(v0 && rank == k);
+    return hit ? (int)__builtin_ctzll(hit) : 0;
+  }
+  bool t0 = !v0, t1 = !v1;
+  int bi = 0;
+  for (int s = 0; s <= k; s++) {
+    uint64_t key = 0, f = 0;
+    if (!t0) {
+      f = 0xffffffffu - (uint32_t)lane;
+      if (!__builtin_isnan(lg0)) key = topk_key(lg0, lane);
+    }
+    if (!t1) {
+      if (f == 0) f = 0xffffffffu - (uint32_t)(lane + 64);
+      if (!__builtin_isnan(lg1)) {
+        const uint64_t k1 = topk_key(lg1, lane + 64);
+        key = k1 > key ? k1 : key;
+      }
+    }
+    key = wave_max_u64(key);
+    f = wave_max_u64(f);
+    const int first = __builtin_amdgcn_readfirstlane((int)(0xffffffffu - (uint32_t)f));
+    const float fv = lane_value(lg0, lg1, first);
+    bi = first;
+    if (!__builtin_isnan(fv)) bi = __builtin_amdgcn_readfirstlane((int)(0xffffffffu - (uint32_t)key));
+    if (lane == bi) t0 = true;
+    if (lane + 64 == bi) t1 = true;
+  }
+  return bi;
+}
+
 }  // namespace tt
