@@ -58,12 +58,15 @@ def test_norm_router_logits(backend, device, tokens, E, H, bias):
 
 
 def _special_logits(g, tokens, E):
+    """Ties (values on a 0.5 grid); token t % 3 == 1 adds signed zeros and -inf, t % 3 == 2
+    also NaN (the scan without NaN and the NaN-aware scan are different code paths)."""
     lg = (np.round(g.standard_normal((tokens, E)) * 2) / 2).astype(np.float32)
     for t in range(tokens):
-        if t % 2:
+        if t % 3:
             lg[t, g.integers(0, E, size=max(1, E // 8))] = 0.0
             lg[t, g.integers(0, E, size=max(1, E // 8))] = -0.0
             lg[t, g.integers(0, E, size=max(1, E // 16))] = -np.inf
+        if t % 3 == 2:
             lg[t, g.integers(1, E, size=max(1, E // 16))] = np.nan
     return lg
 

@@ -119,22 +119,35 @@ __device__ __forceinline__ TopkLanes wave_topk_lanes(float lg0, float lg1, int E
 }
 
 // Expert of slot k of wave_topk_lanes's selection (the same rule, so the same expert),
-// without the softmax: the rank pass when no logit is NaN and E <= 64, otherwise the
-// iterated scan stopped at slot k.
+// without the softmax.  With no NaN logit and E <= 64 the keys (value, then lowest index)
+// are distinct and slot s holds the s-th largest, so k + 1 wave maxima over the untaken
+// keys find it: the maximum of the keys' value halves, then the lowest lane holding it (a
+// taken or invalid lane holds 0, below every valid value half: -inf orders as 0x007fffff).  Each SwiGLU wave calls
+// this before its first weight request: a rank pass over all E keys cost the gpt-oss
+// bs=1 decode ~4% (720 against 750 tok/s with the pass skipped in a timing copy).
+// Otherwise the iterated scan of wave_topk_lanes, stopped at slot k.
 __device__ __forceinline__ int wave_topk_expert(float lg0, float lg1, int E, int k) {
   const int lane = lane_id();
   const bool v0 = lane < E, v1 = lane + 64 < E;
   const bool any_nan = __builtin_amdgcn_ballot_w64((v0 && __builtin_isnan(lg0)) || (v1 && __builtin_isnan(lg1))) != 0;
   if (E <= 64 && !any_nan) {
-    const uint64_t mine = topk_key(lg0, lane);
-    int rank = 0;
-    for (int f = 0; f < E; f++) {
-      const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)mine, f);
-      const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(mine >> 32), f);
-      rank += (((uint64_t)hi << 32) | lo) > mine ? 1 : 0;
+    // the value half of the key (32-bit maxima), then the lowest index holding it
+    uint32_t mine = v0 ? (uint32_t)(topk_key(lg0, lane) >> 32) : 0u;
+    int e = 0;
+    for (int s = 0; s <= k; s++) {
+      uint32_t m = mine;
+      auto umax = [](uint32_t a, float b) { const uint32_t u = __builtin_bit_cast(uint32_t, b); return u > a ? u : a; };
+      m = umax(m, xor_partner<1>(__builtin_bit_cast(float, m)));
+      m = umax(m, xor_partner<2>(__builtin_bit_cast(float, m)));
+      m = umax(m, xor_partner<4>(__builtin_bit_cast(float, m)));
+      m = umax(m, xor_partner<8>(__builtin_bit_cast(float, m)));
+      m = umax(m, xor_partner<16>(__builtin_bit_cast(float, m)));
+      m = umax(m, xor_partner<32>(__builtin_bit_cast(float, m)));
+      const uint64_t hit = __builtin_amdgcn_ballot_w64(mine == m);
+      e = (int)__builtin_ctzll(hit);
+      if (lane == e) mine = 0u;
     }
-    const uint64_t hit = __builtin_amdgcn_ballot_w64(v0 && rank == k);
-    return hit ? (int)__builtin_ctzll(hit) : 0;
+    return e;
   }
   bool t0 = !v0, t1 = !v1;
   int bi = 0;
