@@ -51,11 +51,34 @@ __device__ __forceinline__ TopkLanes wave_topk_lanes(float lg0, float lg1, int E
   float sel0 = 0.0f, sel1 = 0.0f;
   int id0 = 0, id1 = 0;
   const bool any_nan = __builtin_amdgcn_ballot_w64((v0 && __builtin_isnan(lg0)) || (v1 && __builtin_isnan(lg1))) != 0;
-  if (E <= 64 && !any_nan) {
-    // Without NaNs the iterated selection is the order of the keys (value, then lowest
-    // index), so slot s is the expert with exactly s greater keys: every lane counts the
-    // keys above its own, independently of the others, and slot s finds its lane by a
-    // ballot.
+  if (E <= 64 && !any_nan && top_k <= 8) {
+    // Without NaNs the keys (value, then lowest index) are distinct and slot s holds the
+    // s-th largest: top_k wave maxima of the keys' value halves, each followed by a ballot
+    // for the lowest lane holding it (taken and invalid lanes hold 0, below every valid
+    // value half), as in wave_topk_expert.
+    uint32_t mk = v0 ? (uint32_t)(topk_key(lg0, lane) >> 32) : 0u;
+    auto umax = [](uint32_t a, float b) { const uint32_t u = __builtin_bit_cast(uint32_t, b); return u > a ? u : a; };
+    for (int s = 0; s < top_k; s++) {
+      uint32_t m = mk;
+      m = umax(m, xor_partner<1>(__builtin_bit_cast(float, m)));
+      m = umax(m, xor_partner<2>(__builtin_bit_cast(float, m)));
+      m = umax(m, xor_partner<4>(__builtin_bit_cast(float, m)));
+      m = umax(m, xor_partner<8>(__builtin_bit_cast(float, m)));
+      m = umax(m, xor_partner<16>(__builtin_bit_cast(float, m)));
+      m = umax(m, xor_partner<32>(__builtin_bit_cast(float, m)));
+      const uint64_t hit = __builtin_amdgcn_ballot_w64(mk == m);
+      const int e = (int)__builtin_ctzll(hit);
+      const float val = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lg0), e));
+      if (lane == s) {
+        sel0 = val;
+        id0 = e;
+      }
+      if (lane == e) mk = 0u;
+    }
+  } else if (E <= 64 && !any_nan) {
+    // Larger top_k: slot s is the expert with exactly s greater keys; every lane counts
+    // the keys above its own, independently of the others, and slot s finds its lane by
+    // a ballot.
     const uint64_t mine = topk_key(lg0, lane);
     int rank = 0;
     for (int f = 0; f < E; f++) {
