@@ -360,6 +360,332 @@ __global__ __launch_bounds__(256) void fused_lean_kernel(const LeanFused P) {
   }
 }
 
+// fused_lean_kernel for TOK tokens of a batched step per workgroup (a copy, so that the
+// one-token kernel's code stays as it is): every weight load feeds TOK tokens' dot
+// products, each in the one-token order (token t's activation at LDS slice t, its own
+// prologue and epilogue), so each token's outputs keep their bits.
+template <Fmt F, typename XT, int LPR, int ROWS, Pro PRO, bool MULTI, int TOK>
+__global__ __launch_bounds__(256) void fused_lean_tok_kernel(const LeanFused P) {
+  constexpr bool kInt4 = F == Fmt::kInt4Sym;
+  constexpr int B = FmtInfo<F>::kBytes;
+  constexpr int L = kInt4 ? 4 : 1;
+  constexpr int SUBS = 64 / LPR;
+  constexpr int NVG = kInt4 ? (ROWS / L > 0 ? ROWS / L : 1) : ROWS;
+  constexpr int NS = kInt4 ? NVG : 1;
+  constexpr int GLEV = kInt4 ? (log2c(L) < log2c(ROWS) ? log2c(L) : log2c(ROWS)) : 0;
+  static_assert(ROWS >= 2, "paired segments need two rows per wave");
+  extern __shared__ uint32_t xs_lds[];
+  const int lane = threadIdx.x & 63;
+  const int sub = lane / LPR;
+  const int l = lane % LPR;
+  const int cols = P.cols;
+  const int nchunks = cols >> 5;
+  const int rounds = (nchunks + LPR - 1) / LPR;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int v0 = (int)(blockIdx.x * 4 + wave) * (ROWS * SUBS);   // first virtual row (uniform)
+  const bool active = v0 < P.vtotal;
+  const int64_t tok0 = (int64_t)blockIdx.y * TOK;   // first token of the workgroup
+  // ---- the prologue's inputs are requested first -- before the row addressing, which
+  // is a few hundred scalar instructions for paired segments, and before round 0 of the
+  // weights, so that waiting for them never waits for the weight stream: one 16-byte
+  // piece of each vector per held piece (cols <= 4096, a multiple of 32; indices past the
+  // last piece repeat it)
+  __shared__ float red[4];
+  const int n = cols;
+  const int np = n >> 3;
+  uint4 qa[TOK][kNormPieces], qb[TOK][kNormPieces], qw[kNormPieces];
+  if constexpr (PRO != Pro::kLoad) {
+#pragma unroll
+    for (int ti = 0; ti < TOK; ti++) {
+      const int64_t tok = tok0 + ti;
+      const uint16_t* pa;
+      if constexpr (PRO == Pro::kEmbedNorm) {
+        int64_t t = P.token[tok];
+        t = t < 0 ? 0 : (t >= P.vocab ? P.vocab - 1 : t);
+        pa = reinterpret_cast<const uint16_t*>(P.embed) + t * P.embed_row;
+      } else {
+        pa = reinterpret_cast<const uint16_t*>(P.left) + tok * P.token_x;
+      }
+      const uint16_t* pb = reinterpret_cast<const uint16_t*>(P.right) + tok * P.token_x;
+#pragma unroll
+      for (int k = 0; k < kNormPieces; k++) {
+        const int pi = (int)threadIdx.x + 256 * k;
+        const int pc = pi < np ? pi : np - 1;
+        qa[ti][k] = reinterpret_cast<const uint4*>(pa)[pc];
+        if constexpr (PRO != Pro::kEmbedNorm) qb[ti][k] = reinterpret_cast<const uint4*>(pb)[pc];
+        if (ti == 0) qw[k] = reinterpret_cast<const uint4*>(P.norm_w)[pc];
+      }
+    }
+  }
+  // the token position of the RoPE / cache epilogues, requested with the prologue's
+  // inputs so that the epilogue's table reads are its only dependent round trip
+  const int32_t pos_raw = P.pos != nullptr ? P.pos[0] : 0;
+  __builtin_amdgcn_sched_barrier(0);
+  // MULTI: every segment's fields are read from the kernel arguments unconditionally and
+  // the wave's segment is selected afterwards (scalar selects), so the argument loads go
+  // out together instead of a second round trip behind the segment index; a
+  // one-segment launch reads segment 0 only (fewer argument loads, fewer scalar
+  // registers)
+  int si = 0;
+  if constexpr (MULTI) si = (P.nseg > 1 && v0 >= P.seg[1].vbegin ? 1 : 0) + (P.nseg > 2 && v0 >= P.seg[2].vbegin ? 1 : 0);
+  const LeanSeg S = MULTI ? pick_seg(P.seg[0], P.seg[1], P.seg[2], si) : P.seg[0];
+  const int kind = S.kind;
+  const int srows = S.rows;
+  const int lr0 = v0 - S.vbegin;
+  const bool paired = kind == kSegRopeOut || kind == kSegRopeCache || kind == kSegSilu;
+
+  // Physical row (and matrix) of row vr (0 .. ROWS * SUBS - 1) of this wave's block, the
+  // mapping of paired_row: the block starts on a pair boundary (lr0 is a multiple of
+  // ROWS * SUBS), so its rows are a few shifts away from its first pair P0, and for the
+  // RoPE segments the block's pairs lie in one head (the host checks that half a head
+  // is a whole number of blocks), whose index and in-head offset are one scalar
+  // division per wave.  Rows past the segment read the block's first row, and a block
+  // past the segment reads row 0 (in bounds; the values are never used).
+  const int P0 = lr0 >> 1;
+  const int half = P.head_dim >> 1;
+  int h0 = 0, j0 = 0;
+  if (kind == kSegRopeOut || kind == kSegRopeCache) {
+    h0 = (int)((uint32_t)P0 / (uint32_t)half);
+    j0 = P0 - h0 * half;
+  }
+  const bool any_row = lr0 < srows;
+  const bool silu = kind == kSegSilu;
+  const int rope_base = h0 * P.head_dim + j0;   // row of the block's first pair (RoPE segments)
+  // (selects only, no branches: the row addressing stays a short straight run ahead of
+  // the first weight loads)
+  auto phys = [&](int vr, bool valid, bool& up, bool& odd) -> int {
+    vr = valid ? vr : 0;
+    const int blk = vr / (2 * SUBS), rem = vr % (2 * SUBS);   // SUBS is a power of two
+    const bool o = paired && rem >= SUBS;
+    const int poff = blk * SUBS + (o ? rem - SUBS : rem);
+    const int pr = silu ? P0 + poff : rope_base + poff + (o ? half : 0);
+    const int ph = paired ? pr : lr0 + vr;
+    odd = o;
+    up = o && silu && any_row;
+    return any_row ? ph : 0;
+  };
+  // both matrices' base pointers in scalar registers, so the per-lane choice between them
+  // is a select and not a vector load of the chosen kernel argument
+  const uint8_t* const wlo = uniform_ptr(S.w);
+  const uint8_t* const whi = uniform_ptr(S.w2);
+  const uint8_t* wrow[ROWS];
+  bool rv[ROWS];
+#pragma unroll
+  for (int i = 0; i < ROWS; i++) {
+    const int vr = i * SUBS + sub;
+    rv[i] = lr0 + vr < srows;
+    bool up, odd;
+    const int ph = phys(vr, rv[i], up, odd);
+    wrow[i] = (up ? whi : wlo) + (size_t)ph * S.w_row;
+  }
+  const f16_t* srow[NS];
+  bool sv[NS];
+  if constexpr (kInt4) {
+    const f16_t* const slo = uniform_ptr(S.s);
+    const f16_t* const shi = uniform_ptr(S.s2);
+#pragma unroll
+    for (int k = 0; k < NS; k++) {
+      const int vr = rs_row<ROWS>(l, GLEV, k) * SUBS + sub;
+      sv[k] = lr0 + vr < srows;
+      bool up, odd;
+      const int ph = phys(vr, sv[k], up, odd);
+      srow[k] = (up ? shi : slo) + (size_t)ph * S.s_row;
+    }
+  }
+  auto fetch = [&](int r, Raw<B>* w, f16_t* sc) {
+    uint32_t j = (uint32_t)(r * LPR + l);
+    j = j < (uint32_t)nchunks ? j : (uint32_t)nchunks - 1;
+#pragma unroll
+    for (int i = 0; i < ROWS; i++) w[i] = load_raw<B>(wrow[i] + j * (uint32_t)B);
+    if constexpr (kInt4) {
+#pragma unroll
+      for (int k = 0; k < NS; k++) sc[k] = srow[k][j >> 2];
+    }
+  };
+  __builtin_amdgcn_sched_barrier(0);
+  Raw<B> wc[ROWS];
+  f16_t sc[NS];
+  fetch(0, wc, sc);   // in bounds for inactive waves too (rows clamped)
+  // nothing that consumes the prologue's loads may be scheduled above round 0's weight
+  // loads: its wait would hold the weight stream back by a memory round trip
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- activation vector into LDS
+  if constexpr (PRO == Pro::kLoad) {
+    const int xn = cols >> 3;
+#pragma unroll
+    for (int ti = 0; ti < TOK; ti++)
+      for (int idx = threadIdx.x; idx < xn; idx += 256)
+        reinterpret_cast<uint4*>(xs_lds)[ti * xn + idx] = reinterpret_cast<const uint4*>(
+            reinterpret_cast<const uint16_t*>(P.x) + (tok0 + ti) * P.token_x)[idx];
+  } else {
+    // RMSNorm of the residual stream in the piece partition, reduction order and
+    // rounding points of the standalone rms_norm / add_rms_norm kernels; workgroup 0
+    // stores the residual.
+    const bool writer = blockIdx.x == 0 && P.residual_out != nullptr;
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int ti = 0; ti < TOK; ti++) {
+      const int64_t tok = tok0 + ti;
+      float rr[kNormPieces][8];
+      float ss = 0.0f;
+#pragma unroll
+      for (int k = 0; k < kNormPieces; k++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          const float a = piece_f32<XT>(qa[ti][k], e);
+          float r;
+          if constexpr (PRO == Pro::kAddNorm) r = round_bf16(a + piece_f32<XT>(qb[ti][k], e));
+          else if constexpr (PRO == Pro::kAddRmsNorm) r = round_to<XT>(a + piece_f32<XT>(qb[ti][k], e));
+          else r = a;
+          rr[k][e] = r;
+          if (8 * (t + 256 * k) + e < n) ss = __builtin_fmaf(r, r, ss);
+        }
+      const float total = block_sum256(ss, red);
+      const float inv = 1.0f / __builtin_sqrtf(total / (float)n + P.eps);
+#pragma unroll
+      for (int k = 0; k < kNormPieces; k++) {
+        const int pi = t + 256 * k;
+        if (pi < np) {
+          float o[8];
+#pragma unroll
+          for (int e = 0; e < 8; e++) {
+            const float w = piece_f32<XT>(qw[k], e);
+            o[e] = PRO == Pro::kAddNorm ? (rr[k][e] * inv) * w : (rr[k][e] * inv) * (w + 0.0f);
+          }
+          if (writer)
+            reinterpret_cast<uint4*>(reinterpret_cast<XT*>(P.residual_out) + tok * P.token_x)[pi] = pack_piece<XT>(rr[k]);
+          reinterpret_cast<uint4*>(xs_lds)[ti * np + pi] = pack_piece<XT>(o);
+        }
+      }
+    }
+  }
+  lds_barrier();
+  if (!active) return;
+
+  // the row this lane stores and, for the RoPE segments, its cos / sin table entries:
+  // requested now so that they arrive during the dot products instead of costing the
+  // epilogue a memory round trip (a non-RoPE lane reads a weight byte pair instead, so
+  // the loads are unconditional)
+  const int frow = rs_row<ROWS>(l, log2c(ROWS), 0) * SUBS + sub;
+  const bool fstore = (l >> log2c(ROWS)) == 0;
+  const int fr = lr0 + frow;
+  const bool ok = fstore && fr < srows;
+  bool odd = false, up_unused;
+  const int ph = phys(frow, fr < srows, up_unused, odd);
+  const int64_t pos = (int64_t)__builtin_amdgcn_readfirstlane(pos_raw);
+  const bool rope = (kind == kSegRopeOut || kind == kSegRopeCache) && pos >= 0 && pos < P.table_rows;
+  const int hd = P.head_dim > 0 ? P.head_dim : 1;   // 0 for launches without RoPE segments
+  const int rope_j = (ph % hd) - (odd ? (hd >> 1) : 0);
+  const uint16_t* cos_p = rope ? reinterpret_cast<const uint16_t*>(P.cos) + pos * P.table_row + rope_j
+                               : reinterpret_cast<const uint16_t*>(wlo);
+  const uint16_t* sin_p = rope ? reinterpret_cast<const uint16_t*>(P.sin) + pos * P.table_row + rope_j
+                               : reinterpret_cast<const uint16_t*>(wlo);
+  const uint32_t cos_raw = *cos_p, sin_raw = *sin_p;
+
+  float acc_t[TOK][NVG];
+#pragma unroll
+  for (int ti = 0; ti < TOK; ti++)
+#pragma unroll
+    for (int k = 0; k < NVG; k++) acc_t[ti][k] = 0.0f;
+  int r = 0;
+  do {
+    Raw<B> wn[ROWS];
+    f16_t sn[NS];
+    const bool more = r + 1 < rounds;
+    if (more) fetch(r + 1, wn, sn);
+    const int j = r * LPR + l;
+    const bool cv = j < nchunks;
+#pragma unroll
+    for (int ti = 0; ti < TOK; ti++) {
+      float* acc = acc_t[ti];
+      uint32_t xw[16];
+      {
+        const uint4* xp = reinterpret_cast<const uint4*>(xs_lds + ti * (cols >> 1) + (cv ? j : 0) * 16);
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const uint4 v = xp[q];
+          xw[4 * q] = v.x; xw[4 * q + 1] = v.y; xw[4 * q + 2] = v.z; xw[4 * q + 3] = v.w;
+        }
+      }
+      float p[ROWS];
+      chunk_dot_rows<F, XT, ROWS>(wc, xw, p);
+#pragma unroll
+      for (int i = 0; i < ROWS; i++) p[i] = (cv && rv[i]) ? p[i] : 0.0f;
+      if constexpr (kInt4) {
+        reduce_range<ROWS, 1, L>(p);
+#pragma unroll
+        for (int k = 0; k < NVG; k++) {
+          const float t = p[k] * to_f32(sc[k]);
+          acc[k] = acc[k] + ((cv && sv[k]) ? t : 0.0f);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < ROWS; i++) acc[i] = acc[i] + p[i];
+      }
+    }
+    if (more) {
+#pragma unroll
+      for (int i = 0; i < ROWS; i++) wc[i] = wn[i];
+      if constexpr (kInt4) {
+#pragma unroll
+        for (int k = 0; k < NS; k++) sc[k] = sn[k];
+      }
+    }
+  } while (++r < rounds);
+#pragma unroll
+  for (int ti = 0; ti < TOK; ti++) {
+    if constexpr (kInt4) reduce_range<NVG, L, LPR>(acc_t[ti]);
+    else reduce_range<ROWS, 1, LPR>(acc_t[ti]);
+  }
+
+  // ---- epilogue on the row held by this lane, once per token of the workgroup
+  auto epilogue = [&](float v, int64_t tok) __attribute__((always_inline)) {
+  if (kind == kSegPlain) {
+    if (ok) {
+      if (S.bias != nullptr) v = round_to<XT>(v) + to_f32(reinterpret_cast<const XT*>(S.bias)[fr]);
+      store<XT>(reinterpret_cast<XT*>(S.out) + tok * P.token_out + fr, v);
+    }
+    return;
+  }
+  if (S.bias != nullptr && ok) v = round_to<XT>(v) + to_f32(reinterpret_cast<const XT*>(S.bias)[ph]);
+  const float val = round_to<XT>(v);
+  const float pv = xor_partner<ROWS / 2 < 1 ? 1 : ROWS / 2>(val);   // the other half of the pair
+  if (kind == kSegSilu) {
+    if (ok && !odd) store<XT>(reinterpret_cast<XT*>(S.out) + tok * P.token_out + ph, silu_mul_val(val, pv));
+    return;
+  }
+  const int D = P.head_dim;
+  float o = val;
+  if (rope) {
+    const float c = lo_f32<XT>(cos_raw);
+    const float sn = lo_f32<XT>(sin_raw);
+    float o1, o2;
+    if (odd) rope_pair<XT>(pv, val, c, sn, o1, o2);
+    else rope_pair<XT>(val, pv, c, sn, o1, o2);
+    o = odd ? o2 : o1;
+  }
+  if (ok) {
+    if (kind == kSegRopeOut) {
+      store<XT>(reinterpret_cast<XT*>(S.out) + tok * P.token_out + ph, o);
+    } else if (pos >= 0 && pos < P.capacity) {
+      const int64_t h = ph / D, d = ph - h * D;
+      store<XT>(reinterpret_cast<XT*>(S.out) + tok * P.token_cache + h * P.cache_head + pos * D + d, o);
+    }
+  }
+  };
+#pragma unroll
+  for (int ti = 0; ti < TOK; ti++) epilogue(acc_t[ti][0], tok0 + ti);
+}
+
+
+// Tokens per workgroup of the batched dense multi-matrix launch (gpt-oss QKV, eight
+// sequences): two measured 2,262 tok/s, four 2,249, eight 2,079 (VALU-bound) and one
+// 2,222 on one box.
+#ifndef TT_FUSED_TOK
+#define TT_FUSED_TOK 2
+#endif
+
 // Rows per wave of the lean fused kernel (paired segments need two).  Eight for the
 // largest launches (the 1B gate/up, 16384 virtual rows: 9.06 -> 8.69 us against four):
 // half the waves, each prologue shared by twice the rows.
@@ -441,6 +767,20 @@ int launch_lean_lpr(const tt_fused_gemv* d, hipStream_t st) {
   const size_t lds = (size_t)d->cols * 2;
   const unsigned ytok = (unsigned)(d->tokens > 1 ? d->tokens : 1);
   const dim3 grid((unsigned)((waves + 3) / 4), ytok);
+  // dense multi-matrix launches of a batched step (the gpt-oss QKV of eight sequences):
+  // TT_FUSED_TOK tokens per workgroup, so each weight row is streamed once per group of
+  // tokens instead of once per token
+  if constexpr (F != Fmt::kInt4Sym && LPR == 32) {
+    constexpr int TK = TT_FUSED_TOK;
+    if (TK > 1 && d->count > 1 && d->tokens >= TK && d->tokens % TK == 0) {
+      const dim3 gt((unsigned)((waves + 3) / 4), (unsigned)(d->tokens / TK));
+      const size_t ldst = (size_t)TK * d->cols * 2;
+      if (rpw == 8) hipLaunchKernelGGL((fused_lean_tok_kernel<F, XT, LPR, 8, PRO, true, TK>), gt, dim3(256), ldst, st, P);
+      else if (rpw == 4) hipLaunchKernelGGL((fused_lean_tok_kernel<F, XT, LPR, 4, PRO, true, TK>), gt, dim3(256), ldst, st, P);
+      else hipLaunchKernelGGL((fused_lean_tok_kernel<F, XT, LPR, 2, PRO, true, TK>), gt, dim3(256), ldst, st, P);
+      return check_launch(kWhat);
+    }
+  }
   if (d->count > 1) {
     if (rpw == 8) hipLaunchKernelGGL((fused_lean_kernel<F, XT, LPR, 8, PRO, true>), grid, dim3(256), lds, st, P);
     else if (rpw == 4) hipLaunchKernelGGL((fused_lean_kernel<F, XT, LPR, 4, PRO, true>), grid, dim3(256), lds, st, P);
